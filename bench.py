@@ -1,0 +1,202 @@
+"""Benchmark of the gfx950 render path: fwd and fwd+bwd frames/s on the BASELINE workload.
+
+A step is one forward + backward render of the workload (project -> rasterize -> MSE loss ->
+backward through rasterize and project), with all inputs resident in HBM. The default workload is
+config 2 (1,000,000 gaussians on 64 planes, one 1920x1080 camera).
+
+The JSON line carries:
+- value: forward+backward frames/s (whole job, one GPU); fwd_frames_per_s: forward only.
+- roofline: the dominant kernel's algorithmic work per launch / its average launch duration,
+  timed with HIP events on the launch stream inside the timed region (library stage timing).
+  Blend work is the reference loop's pair count from the CPU oracle (26 Pc + 16 Pr FLOPs
+  forward, 65 Qc + 16 Qr backward); sort+bin bytes are 12G + 32V + 76M + 16T.
+- cpu_baseline: the CPU oracle (the C restatement of the reference kernels, "port") timed on the
+  host on one full forward+backward frame of the same workload, OpenMP over `cores` threads.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--n", type=int, default=None, help="override the gaussian count")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=None)
+    ap.add_argument("--fwd-only", action="store_true")
+    return ap.parse_args()
+
+
+def oracle_leg(scene, threads):
+    """Time the CPU oracle on one full fwd+bwd frame; also returns the reference loop counts."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    O.set_threads(threads)
+    s = scene
+    q = np.roll(s.quats, -1, axis=-1)
+    B = s.B
+    vm = s.viewmats.reshape(-1, 4)
+    t0 = time.perf_counter()
+    xys, depths, radii, conics, nth, cum = O.project_fwd(
+        s.means, s.scales, q, vm, s.opacities, n=s.n, total=B * s.n, img_shape=s.img_shape,
+        f=s.f, c=s.c)
+    img, Ts, fidx, fstats, M = O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background,
+                                               xys, depths, radii, conics, cum, n=s.n, B=B,
+                                               img_shape=s.img_shape)
+    t1 = time.perf_counter()
+    H, W = s.img_shape
+    vout = (2.0 * (img.reshape(B, H, W, 3) - s.targets) / img.size).astype(np.float32)
+    g = O.rasterize_bwd(s.colors, s.opacities, s.opacities, s.background, xys, depths, radii,
+                        conics, cum, Ts, fidx, vout, n=s.n, B_out=B, B_geom=B,
+                        img_shape=s.img_shape)
+    O.project_bwd(s.means, s.scales, q, vm, radii, conics, g[2],
+                  np.zeros(B * s.n, np.float32), g[3], n=s.n, B=B, f=s.f)
+    t2 = time.perf_counter()
+    counts = dict(G=B * s.n, V=int((radii > 0).sum()), M=int(M), Pc=int(fstats[0]),
+                  Pr=int(fstats[1]), Qc=int(g[4][0]), Qr=int(g[4][1]))
+    return (t1 - t0), (t2 - t0), counts
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the path shards by camera across GPUs by design, but no multi-GPU run is built)",
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import splax_amd
+    from splax_amd import _lib
+    from splax_amd.scenes import make_scene
+
+    dev = torch.device("cuda:0")
+    scene = make_scene(args.config, n=args.n)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    params = [t(scene.means), t(scene.scales), t(scene.quats), t(scene.colors),
+              t(scene.opacities)]
+    for p in params:
+        p.requires_grad_(True)
+    B = scene.B
+    vm = t(scene.viewmats if B > 1 else scene.viewmats[0])
+    bg = t(scene.background)
+    target = t(scene.targets if B > 1 else scene.targets[0])
+    H, W = scene.img_shape
+
+    def forward():
+        img, _ = splax_amd.render(*params, viewmat=vm, background=bg, img_shape=(H, W),
+                                  f=scene.f, antialiased=scene.antialiased)
+        return img
+
+    def step():
+        for p in params:
+            p.grad = None
+        img = forward()
+        loss = ((img - target) ** 2).mean()
+        loss.backward()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # forward-only frames/s
+    with torch.no_grad():
+        for _ in range(2):
+            forward()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            forward()
+        torch.cuda.synchronize()
+        fwd_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    # timed fwd+bwd region with stage events on the launch stream
+    _lib.stage_times()  # reset
+    _lib.set_stage_timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    _lib.set_stage_timing(False)
+    stages = _lib.stage_times()
+
+    counts = None
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        cpu_fwd_s, cpu_s, counts = oracle_leg(scene, threads)
+        cpu = {"value": round(1.0 / cpu_s, 4), "unit": "frames/s", "cores": threads,
+               "kind": "port",
+               "sample": f"one full fwd+bwd frame of config {args.config} "
+                         f"({scene.n} gaussians, B={B}, {H}x{W}) by the C oracle; "
+                         f"fwd alone {cpu_fwd_s:.2f} s"}
+
+    per_stage = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in stages.items()}
+    stage_ms_per_step = {k: round(v[0] / args.steps, 4) for k, v in stages.items()}
+    roofline = None
+    if counts is not None:
+        G, V, M = counts["G"], counts["V"], counts["M"]
+        T = B * ((W + 15) // 16) * ((H + 15) // 16)
+        cands = {
+            "blend_bwd": ("valu", (65 * counts["Qc"] + 16 * counts["Qr"]) / 1e12, "TFLOP/s",
+                          FP32_PEAK_TFLOPS),
+            "blend_fwd": ("valu", (26 * counts["Pc"] + 16 * counts["Pr"]) / 1e12, "TFLOP/s",
+                          FP32_PEAK_TFLOPS),
+            "sort": ("hbm", 64 * M / 1e9, "GB/s", HBM_PEAK_GBS),
+            "project": ("hbm", (44 * scene.n + 40 * G) / 1e9, "GB/s", HBM_PEAK_GBS),
+        }
+        dom = max(cands, key=lambda k: per_stage.get(k, 0.0))
+        bound, work, unit, peak = cands[dom]
+        dur_s = per_stage[dom] / 1e3
+        achieved = work / dur_s if dur_s > 0 else 0.0
+        roofline = {"kernel": dom, "bound": bound, "achieved": round(achieved, 3),
+                    "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
+                    "traffic": None, "avg_launch_ms": round(per_stage[dom], 4),
+                    "work_per_launch": work * (1e12 if unit == "TFLOP/s" else 1e9)}
+
+    out = {
+        "metric": "fwd+bwd frames/sec @1M gaussians 1080p (fwd frames/sec alongside)",
+        "value": round(1e3 / ms, 3),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "fwd_frames_per_s": round(1e3 / fwd_ms, 3),
+        "fwd_ms": round(fwd_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy PCG64, BASELINE.json config distributions)",
+        "config": {"workload": f"config{args.config}", "gaussians": scene.n, "cameras": B,
+                   "img_shape": [H, W], "loss": "mse", "parallelism": "single-gpu"},
+        "stage_ms_per_step": stage_ms_per_step,
+        "counts": counts,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,125 @@
+/* C ABI of libsplat_hip.so — the MI355X (gfx950) gaussian-splat render path.
+ *
+ * Drop-in boundary for the four FFI callables of amacati/splax's render path plus its host-side
+ * sort/bin step and cache control. Plain pointers and sizes only; every device pointer is a
+ * gfx950 global-memory address, and all work is enqueued on `stream` (a hipStream_t; NULL is the
+ * default stream). Every entry point returns 0 on success or a nonzero status; the message of
+ * the last failure on the calling thread is splat_last_error().
+ *
+ * Batch convention (splax/_project/_kernels.py:58-75, splax/_rasterize/_kernels.py:56,408-418):
+ * operands arrive flattened into their leading dimension; an operand is batched when its row
+ * count exceeds num_gaussians (viewmat: exceeds 4 rows, transforms: exceeds num_transforms), and
+ * broadcast otherwise. Flat item idx = image * num_gaussians + gaussian.
+ *
+ * Quaternions are xyzw here (the public Python API takes wxyz and rolls them,
+ * splax/_project/_project.py:74-76). Matrices are row-major float32.
+ */
+#ifndef SPLAT_HIP_H
+#define SPLAT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* splat_stream_t; /* hipStream_t */
+
+/* Replaces _project_warp (splax/_project/_kernels.py:31-107, FFI callable :110-119): projection
+ * over total = B * num_gaussians items plus the global inclusive scan of the tile counts.
+ * Outputs (total rows each): xys [total,2], depths [total], radii [total] int32, conics [total,3],
+ * num_tiles_hit [total] int32, cum_tiles_hit [total] int32 (inclusive, global over the batch).
+ * transforms: (rows_transforms, 4, 4); transform_ids: [num_gaussians] (read only when
+ * has_transforms != 0). */
+int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
+                      const float* scales, int64_t rows_scales, const float* quats_xyzw,
+                      int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
+                      const float* opacities, int64_t rows_opac, const float* transforms,
+                      int64_t rows_transforms, const int32_t* transform_ids,
+                      int32_t num_gaussians, int32_t num_transforms, int32_t has_transforms,
+                      int64_t total, int32_t img_h, int32_t img_w, float fx, float fy, float cx,
+                      float cy, float glob_scale, float clip_thresh, float* xys, float* depths,
+                      int32_t* radii, float* conics, int32_t* num_tiles_hit,
+                      int32_t* cum_tiles_hit);
+
+/* Replaces _project_bwd_warp (splax/_project/_kernels.py:257-341, FFI callable :344-353).
+ * Outputs: v_mean3d [B*n,3], v_scale [B*n,3], v_quat [B*n,4] (xyzw), v_viewmat [4B,4],
+ * v_transforms [B*num_transforms,4,4] (may be NULL when has_transforms == 0). All outputs are
+ * fully written (no caller zeroing). */
+int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
+                      const float* scales, int64_t rows_scales, const float* quats_xyzw,
+                      int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
+                      const int32_t* radii, int64_t rows_radii, const float* conics,
+                      int64_t rows_conics, const float* v_xy, int64_t rows_vxy,
+                      const float* v_depth, int64_t rows_vdepth, const float* v_conic,
+                      int64_t rows_vconic, const float* transforms, int64_t rows_transforms,
+                      const int32_t* transform_ids, int32_t num_gaussians,
+                      int32_t num_transforms, int32_t has_transforms, int32_t B, float fx,
+                      float fy, float glob_scale, float* v_mean3d, float* v_scale,
+                      float* v_quat, float* v_viewmat, float* v_transforms);
+
+/* Replaces _rasterize_warp (splax/_rasterize/_kernels.py:37-87, FFI callable :90-99): sort_and_bin
+ * (one pinned device-to-host read of the intersection count) then the forward blend.
+ * Geometry inputs have B * num_gaussians rows; colors / opacities / map_opacities may be
+ * broadcast (rows == num_gaussians) or batched; background has 1 or B rows.
+ * Outputs: final_Ts [B*H, W], final_idx [B*H, W] int32, out_img [B*H, W, 3].
+ * num_intersects (may be NULL) receives M. */
+int splat_rasterize_fwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
+                        const float* opacities, int64_t rows_opac, const float* map_opacities,
+                        int64_t rows_map_opac, const float* background, int64_t rows_bg,
+                        const float* xys, const float* depths, const int32_t* radii,
+                        const float* conics, const int32_t* cum_tiles_hit,
+                        int32_t num_gaussians, int32_t B, int32_t img_h, int32_t img_w,
+                        float* final_Ts, int32_t* final_idx, float* out_img,
+                        int64_t* num_intersects);
+
+/* Replaces _rasterize_bwd_warp (splax/_rasterize/_kernels.py:386-500, FFI callable :503-512):
+ * recomputes sort_and_bin over the B_geom geometry images (deterministic, so it reproduces the
+ * forward order) and runs the backward blend over B_out output images. v_out_img has vout_rows
+ * rows of width W (B_out*H batched or H broadcast). Outputs (B_out * num_gaussians rows, fully
+ * written): v_colors [.,3], v_opacity [.], v_xy [.,2], v_conic [.,3]. */
+int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
+                        const float* opacities, int64_t rows_opac, const float* map_opacities,
+                        int64_t rows_map_opac, const float* background, int64_t rows_bg,
+                        const float* xys, const float* depths, const int32_t* radii,
+                        const float* conics, const int32_t* cum_tiles_hit,
+                        const float* final_Ts, const int32_t* final_idx, const float* v_out_img,
+                        int64_t vout_rows, int32_t num_gaussians, int32_t B_out, int32_t B_geom,
+                        int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
+                        float* v_xy, float* v_conic);
+
+/* Replaces sort_and_bin (splax/_rasterize/_sort/_sort.py:29-171), exposed for callers that keep
+ * the sorted lists: writes the M sorted packed keys and gaussian ids (capacity >= M required,
+ * else status 6 with *num_intersects = M) and the [B*num_tiles, 2] tile bins. */
+int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* depths,
+                       const int32_t* radii, const float* conics, const float* map_opacities,
+                       int64_t rows_map_opac, const int32_t* cum_tiles_hit,
+                       int32_t num_gaussians, int32_t B, int32_t img_h, int32_t img_w,
+                       int32_t* sorted_keys, int32_t* sorted_ids, int64_t capacity,
+                       int32_t* tile_bins, int64_t* num_intersects);
+
+/* Replaces clear_cache (splax/_cache.py:158-164): frees the per-device scratch. */
+void splat_clear_cache(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* splat_last_error(void);
+
+/* Stage timing with HIP events on the caller's stream (no counterpart in the reference; used by
+ * the benchmark). While enabled every stage launch is bracketed by events; get_stage_times waits
+ * for them and returns, per stage, the summed milliseconds and the number of calls, then resets.
+ * Stages: 0 project, 1 minmax, 2 emit, 3 sort, 4 bins, 5 blend_fwd, 6 blend_bwd, 7 project_bwd. */
+int splat_set_stage_timing(int enabled);
+int splat_get_stage_times(double* ms, int64_t* calls, int32_t n);
+
+/* Waits for the current device and returns (then clears) its device error word: 0 when every
+ * kernel ran within its invariants; bit 0 = a scan / sort look-back gave up waiting on a
+ * predecessor (its results are then invalid). No counterpart in the reference. */
+int splat_check_device(void);
+
+/* Library ABI version (bumped on any signature change). */
+int splat_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,254 @@
+"""numpy front end of the CPU oracle (test infrastructure only).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import this
+module, as the checker of the GPU library or as the timed CPU baseline. The product package
+(``splax_amd``) never imports it.
+
+Each wrapper mirrors one reference entry point of amacati/splax:
+- ``project_fwd``: ``_project_warp`` + ``_project_kernel``, splax/_project/_kernels.py:31-248
+- ``sort_and_bin``: splax/_rasterize/_sort/_sort.py:29-171
+- ``rasterize_fwd``: ``_rasterize_warp`` + ``_rasterize_kernel``, splax/_rasterize/_kernels.py:37-205
+- ``rasterize_bwd``: ``_rasterize_bwd_warp``, splax/_rasterize/_kernels.py:386-665,1212-1254
+- ``project_bwd``: ``_project_bwd_warp``, splax/_project/_kernels.py:257-664
+Arrays follow the reference's flattened batch convention (rows > n means batched).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            from oracle.build import build
+
+            build()
+        _lib = ctypes.CDLL(str(LIB_PATH))
+        _lib.oracle_logf.restype = ctypes.c_float
+        _lib.oracle_logf.argtypes = [ctypes.c_float]
+        _lib.oracle_expf.restype = ctypes.c_float
+        _lib.oracle_expf.argtypes = [ctypes.c_float]
+        for name in ("oracle_emit_keys", "oracle_sort_and_bin", "oracle_rasterize_fwd",
+                     "oracle_rasterize_bwd"):
+            getattr(_lib, name).restype = ctypes.c_int64
+    return _lib
+
+
+def _f(a: np.ndarray) -> ctypes.Array:
+    assert a.dtype == np.float32 and a.flags.c_contiguous, (a.dtype, a.flags)
+    return a.ctypes.data_as(_f32p)
+
+
+def _i(a: np.ndarray) -> ctypes.Array:
+    assert a.dtype == np.int32 and a.flags.c_contiguous, (a.dtype, a.flags)
+    return a.ctypes.data_as(_i32p)
+
+
+def _c32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def _ci32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int32))
+
+
+def _rows(a: np.ndarray, width: int) -> int:
+    return a.size // width
+
+
+def logf(x) -> np.ndarray:
+    x = _c32(x).ravel()
+    y = np.empty_like(x)
+    lib().oracle_logf_n(_f(x), _f(y), _i64(x.size))
+    return y
+
+
+def expf(x) -> np.ndarray:
+    x = _c32(x).ravel()
+    y = np.empty_like(x)
+    lib().oracle_expf_n(_f(x), _f(y), _i64(x.size))
+    return y
+
+
+def key_layout(B: int, H: int, W: int) -> tuple[dict, bool]:
+    out = np.zeros(6, np.int32)
+    ok = lib().oracle_key_layout(_i32(B), _i32(H), _i32(W), _i(out))
+    names = ("tile_bounds_x", "tile_bounds_y", "num_tiles", "tile_n_bits", "image_n_bits",
+             "depth_bits")
+    return dict(zip(names, (int(v) for v in out))), bool(ok)
+
+
+def project_fwd(means, scales, quats_xyzw, viewmat, opacities, *, n, total, img_shape, f, c,
+                glob_scale=1.0, clip_thresh=0.01, transforms=None, transform_ids=None,
+                num_transforms=None):
+    """Projection forward over ``total = B*n`` flat items; returns the six reference outputs.
+
+    ``transforms`` is (K, 4, 4) shared or (B*K, 4, 4) per image; ``num_transforms`` is K.
+    """
+    means, scales, quats, viewmat, opac = map(_c32, (means, scales, quats_xyzw, viewmat,
+                                                     opacities))
+    has_tf = transforms is not None
+    tf = _c32(transforms if has_tf else np.zeros((1, 4, 4)))
+    ids = _ci32(transform_ids if has_tf else np.full((1,), -1))
+    num_tf = int(num_transforms if num_transforms is not None else tf.size // 16)
+    H, W = img_shape
+    xys = np.empty((total, 2), np.float32)
+    depths = np.empty(total, np.float32)
+    radii = np.empty(total, np.int32)
+    conics = np.empty((total, 3), np.float32)
+    nth = np.empty(total, np.int32)
+    cum = np.empty(total, np.int32)
+    lib().oracle_project_fwd(
+        _f(means), _i64(_rows(means, 3)), _f(scales), _i64(_rows(scales, 3)), _f(quats),
+        _i64(_rows(quats, 4)), _f(viewmat), _i64(_rows(viewmat, 4)), _f(opac),
+        _i64(opac.size), _f(tf), _i64(_rows(tf, 16)), _i(ids), _i32(n), _i32(num_tf),
+        _i32(int(has_tf)), _i64(total), _i32(H), _i32(W), _f32(f[0]), _f32(f[1]), _f32(c[0]),
+        _f32(c[1]), _f32(glob_scale), _f32(clip_thresh), _f(xys), _f(depths), _i(radii),
+        _f(conics), _i(nth), _i(cum))
+    return xys, depths, radii, conics, nth, cum
+
+
+def emit_keys(xys, depths, radii, conics, map_opac, cum, *, n, B, img_shape):
+    """Unsorted keys/ids in emission order and the per-image depth range."""
+    xys, depths, conics, map_opac = map(_c32, (xys, depths, conics, map_opac))
+    radii, cum = _ci32(radii).ravel(), _ci32(cum).ravel()
+    M = int(cum[-1]) if cum.size else 0
+    keys = np.full(max(M, 1), -999, np.int32)
+    ids = np.full(max(M, 1), -1, np.int32)
+    mm = np.zeros(2 * B, np.float32)
+    H, W = img_shape
+    m = lib().oracle_emit_keys(_f(xys), _f(depths), _i(radii), _f(conics), _f(map_opac),
+                               _i64(map_opac.size), _i(cum), _i32(n), _i32(B), _i32(H),
+                               _i32(W), _i(keys), _i(ids), _i64(keys.size), _f(mm))
+    if m < 0:
+        raise ValueError(f"oracle emit_keys failed with code {m}")
+    return keys[:m], ids[:m], mm
+
+
+def sort_and_bin(xys, depths, radii, conics, map_opac, cum, *, n, B, img_shape):
+    """Sorted keys, sorted gaussian ids and (B*num_tiles, 2) tile bins."""
+    xys, depths, conics, map_opac = map(_c32, (xys, depths, conics, map_opac))
+    radii, cum = _ci32(radii).ravel(), _ci32(cum).ravel()
+    M = int(cum[-1]) if cum.size else 0
+    H, W = img_shape
+    lay, _ = key_layout(B, H, W)
+    keys = np.zeros(max(M, 1), np.int32)
+    ids = np.zeros(max(M, 1), np.int32)
+    bins = np.zeros((B * lay["num_tiles"], 2), np.int32)
+    m = lib().oracle_sort_and_bin(_f(xys), _f(depths), _i(radii), _f(conics), _f(map_opac),
+                                  _i64(map_opac.size), _i(cum), _i32(n), _i32(B), _i32(H),
+                                  _i32(W), _i(keys), _i(ids), _i64(keys.size), _i(bins))
+    if m < 0:
+        raise ValueError(f"oracle sort_and_bin failed with code {m}")
+    return keys[:m], ids[:m], bins
+
+
+def blend_fwd(colors, opacities, background, xys, conics, sorted_ids, tile_bins, *, B,
+              img_shape):
+    colors, opac, bg, xys, conics = map(_c32, (colors, opacities, background, xys, conics))
+    ids, bins = _ci32(sorted_ids), _ci32(tile_bins)
+    if ids.size == 0:
+        ids = np.zeros(1, np.int32)
+    H, W = img_shape
+    Ts = np.empty((B * H, W), np.float32)
+    fidx = np.empty((B * H, W), np.int32)
+    img = np.empty((B * H, W, 3), np.float32)
+    stats = np.zeros(2, np.int64)
+    lib().oracle_blend_fwd(_f(colors), _i64(_rows(colors, 3)), _f(opac), _i64(opac.size), _f(bg),
+                           _i64(_rows(bg, 3)), _f(xys), _f(conics), _i(ids), _i(bins), _i32(B),
+                           _i32(H), _i32(W), _f(Ts), _i(fidx), _f(img),
+                           stats.ctypes.data_as(_i64p))
+    return img, Ts, fidx, stats
+
+
+def rasterize_fwd(colors, opacities, map_opac, background, xys, depths, radii, conics, cum, *,
+                  n, B, img_shape):
+    """Returns (out_img (B*H, W, 3), final_Ts, final_idx, stats=[Pc, Pr], M)."""
+    colors, opac, mopac, bg, xys, depths, conics = map(
+        _c32, (colors, opacities, map_opac, background, xys, depths, conics))
+    radii, cum = _ci32(radii).ravel(), _ci32(cum).ravel()
+    H, W = img_shape
+    Ts = np.empty((B * H, W), np.float32)
+    fidx = np.empty((B * H, W), np.int32)
+    img = np.empty((B * H, W, 3), np.float32)
+    stats = np.zeros(2, np.int64)
+    m = lib().oracle_rasterize_fwd(
+        _f(colors), _i64(_rows(colors, 3)), _f(opac), _i64(opac.size), _f(mopac),
+        _i64(mopac.size), _f(bg), _i64(_rows(bg, 3)), _f(xys), _f(depths), _i(radii),
+        _f(conics), _i(cum), _i32(n), _i32(B), _i32(H), _i32(W), _f(Ts), _i(fidx), _f(img),
+        stats.ctypes.data_as(_i64p))
+    if m < 0:
+        raise ValueError(f"oracle rasterize_fwd failed with code {m}")
+    return img, Ts, fidx, stats, int(m)
+
+
+def rasterize_bwd(colors, opacities, map_opac, background, xys, depths, radii, conics, cum,
+                  final_Ts, final_idx, v_out, *, n, B_out, B_geom, img_shape):
+    """Returns (v_colors, v_opacity, v_xy, v_conic, stats=[Qc, Qr]) sized B_out*n."""
+    colors, opac, mopac, bg, xys, depths, conics, Ts, vout = map(
+        _c32, (colors, opacities, map_opac, background, xys, depths, conics, final_Ts, v_out))
+    radii, cum, fidx = _ci32(radii).ravel(), _ci32(cum).ravel(), _ci32(final_idx)
+    H, W = img_shape
+    nout = B_out * n
+    v_colors = np.empty((nout, 3), np.float32)
+    v_opac = np.empty(nout, np.float32)
+    v_xy = np.empty((nout, 2), np.float32)
+    v_conic = np.empty((nout, 3), np.float32)
+    stats = np.zeros(2, np.int64)
+    m = lib().oracle_rasterize_bwd(
+        _f(colors), _i64(_rows(colors, 3)), _f(opac), _i64(opac.size), _f(mopac),
+        _i64(mopac.size), _f(bg), _i64(_rows(bg, 3)), _f(xys), _f(depths), _i(radii),
+        _f(conics), _i(cum), _f(Ts), _i(fidx), _f(vout), _i64(vout.size // (3 * W)), _i32(n),
+        _i32(B_out), _i32(B_geom), _i32(H), _i32(W), _f(v_colors), _f(v_opac), _f(v_xy),
+        _f(v_conic), stats.ctypes.data_as(_i64p))
+    if m < 0:
+        raise ValueError(f"oracle rasterize_bwd failed with code {m}")
+    return v_colors, v_opac, v_xy, v_conic, stats
+
+
+def project_bwd(means, scales, quats_xyzw, viewmat, radii, conics, v_xy, v_depth, v_conic, *, n,
+                B, f, glob_scale=1.0, transforms=None, transform_ids=None, num_transforms=None):
+    """Returns (v_mean3d, v_scale, v_quat (xyzw), v_viewmat (B*4, 4), v_transforms)."""
+    means, scales, quats, viewmat, conics, v_xy, v_depth, v_conic = map(
+        _c32, (means, scales, quats_xyzw, viewmat, conics, v_xy, v_depth, v_conic))
+    radii = _ci32(radii).ravel()
+    has_tf = transforms is not None
+    tf = _c32(transforms if has_tf else np.zeros((1, 4, 4)))
+    ids = _ci32(transform_ids if has_tf else np.full((1,), -1))
+    K = int(num_transforms if num_transforms is not None else (tf.size // 16 if has_tf else 1))
+    total = B * n
+    v_mean = np.empty((total, 3), np.float32)
+    v_scale = np.empty((total, 3), np.float32)
+    v_quat = np.empty((total, 4), np.float32)
+    v_view = np.zeros((B * 4, 4), np.float32)
+    v_tf = np.zeros((B * K, 4, 4), np.float32)
+    lib().oracle_project_bwd(
+        _f(means), _i64(_rows(means, 3)), _f(scales), _i64(_rows(scales, 3)), _f(quats),
+        _i64(_rows(quats, 4)), _f(viewmat), _i64(_rows(viewmat, 4)), _i(radii), _i64(radii.size),
+        _f(conics), _i64(_rows(conics, 3)), _f(v_xy), _i64(_rows(v_xy, 2)), _f(v_depth),
+        _i64(v_depth.size), _f(v_conic), _i64(_rows(v_conic, 3)), _f(tf), _i64(_rows(tf, 16)),
+        _i(ids), _i32(n), _i32(K), _i32(int(has_tf)), _i32(B), _f32(f[0]), _f32(f[1]),
+        _f32(glob_scale), _f(v_mean), _f(v_scale), _f(v_quat), _f(v_view), _f(v_tf))
+    return v_mean, v_scale, v_quat, v_view, v_tf
+
+
+def set_threads(n: int) -> int:
+    """Set the oracle's OpenMP thread count; returns the count in effect."""
+    return int(lib().oracle_set_threads(ctypes.c_int(int(n))))

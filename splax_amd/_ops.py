@@ -1,0 +1,159 @@
+"""Tensor-level calls into the C ABI (no autograd).
+
+Each function takes flattened operands in the reference's FFI convention (leading dimension =
+rows; an operand is batched when its rows exceed ``n``), allocates the outputs with torch on the
+operands' device and enqueues the library call on torch's current stream of that device.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from splax_amd import _lib
+
+
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype != torch.float32:
+        raise ValueError(f"expected float32, got {t.dtype}")
+    return t.contiguous()
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+    return t.contiguous()
+
+
+def rows(t: torch.Tensor, width: int) -> int:
+    return t.numel() // width
+
+
+def project_fwd(means, scales, quats_xyzw, viewmat, opac, transforms, transform_ids, *, n,
+                total, num_transforms, has_transforms, img_shape, f, c, glob_scale, clip_thresh):
+    """_project_warp (splax/_project/_kernels.py:31-107) over ``total`` flat items."""
+    means, scales, quats, viewmat, opac = map(_f32, (means, scales, quats_xyzw, viewmat, opac))
+    transforms = _f32(transforms)
+    transform_ids = _i32(transform_ids)
+    dev = _lib.require_gpu(means, scales, quats, viewmat, opac, transforms, transform_ids)
+    H, W = img_shape
+    xys = torch.empty((total, 2), device=dev, dtype=torch.float32)
+    depths = torch.empty((total,), device=dev, dtype=torch.float32)
+    radii = torch.empty((total,), device=dev, dtype=torch.int32)
+    conics = torch.empty((total, 3), device=dev, dtype=torch.float32)
+    nth = torch.empty((total,), device=dev, dtype=torch.int32)
+    cum = torch.empty((total,), device=dev, dtype=torch.int32)
+    if total == 0:
+        return xys, depths, radii, conics, nth, cum
+    p = _lib.ptr
+    with torch.cuda.device(dev):
+        st = _lib.lib().splat_project_fwd(
+            _lib.stream_handle(dev), p(means), rows(means, 3), p(scales), rows(scales, 3),
+            p(quats), rows(quats, 4), p(viewmat), rows(viewmat, 4), p(opac), opac.numel(),
+            p(transforms), rows(transforms, 16), p(transform_ids), n, num_transforms,
+            int(has_transforms), total, H, W, f[0], f[1], c[0], c[1], glob_scale, clip_thresh,
+            p(xys), p(depths), p(radii), p(conics), p(nth), p(cum))
+    _lib.check(st, "project")
+    return xys, depths, radii, conics, nth, cum
+
+
+def project_bwd(means, scales, quats_xyzw, viewmat, radii, conics, v_xy, v_depth, v_conic,
+                transforms, transform_ids, *, n, B, num_transforms, has_transforms, f,
+                glob_scale):
+    """_project_bwd_warp (splax/_project/_kernels.py:257-341)."""
+    means, scales, quats, viewmat, conics = map(_f32, (means, scales, quats_xyzw, viewmat,
+                                                       conics))
+    v_xy, v_depth, v_conic, transforms = map(_f32, (v_xy, v_depth, v_conic, transforms))
+    radii, transform_ids = _i32(radii), _i32(transform_ids)
+    dev = _lib.require_gpu(means, scales, quats, viewmat, conics, v_xy, v_depth, v_conic)
+    total = B * n
+    v_mean = torch.empty((total, 3), device=dev, dtype=torch.float32)
+    v_scale = torch.empty((total, 3), device=dev, dtype=torch.float32)
+    v_quat = torch.empty((total, 4), device=dev, dtype=torch.float32)
+    v_view = torch.empty((B * 4, 4), device=dev, dtype=torch.float32)
+    K = num_transforms if has_transforms else 0
+    v_tf = torch.empty((max(B * K, 1), 4, 4), device=dev, dtype=torch.float32)
+    p = _lib.ptr
+    with torch.cuda.device(dev):
+        st = _lib.lib().splat_project_bwd(
+            _lib.stream_handle(dev), p(means), rows(means, 3), p(scales), rows(scales, 3),
+            p(quats), rows(quats, 4), p(viewmat), rows(viewmat, 4), p(radii), radii.numel(),
+            p(conics), rows(conics, 3), p(v_xy), rows(v_xy, 2), p(v_depth), v_depth.numel(),
+            p(v_conic), rows(v_conic, 3), p(transforms), rows(transforms, 16), p(transform_ids),
+            n, num_transforms, int(has_transforms), B, f[0], f[1], glob_scale, p(v_mean),
+            p(v_scale), p(v_quat), p(v_view), p(v_tf))
+    _lib.check(st, "project_bwd")
+    if not has_transforms:
+        v_tf.zero_()
+    return v_mean, v_scale, v_quat, v_view, v_tf
+
+
+def rasterize_fwd(colors, opac, map_opac, background, xys, depths, radii, conics, cum, *, n, B,
+                  img_shape):
+    """_rasterize_warp (splax/_rasterize/_kernels.py:37-87): sort_and_bin + forward blend."""
+    colors, opac, map_opac, background, xys, depths, conics = map(
+        _f32, (colors, opac, map_opac, background, xys, depths, conics))
+    radii, cum = _i32(radii), _i32(cum)
+    dev = _lib.require_gpu(colors, opac, map_opac, background, xys, depths, radii, conics, cum)
+    H, W = img_shape
+    Ts = torch.empty((B * H, W), device=dev, dtype=torch.float32)
+    fidx = torch.empty((B * H, W), device=dev, dtype=torch.int32)
+    img = torch.empty((B * H, W, 3), device=dev, dtype=torch.float32)
+    m = torch.zeros(1, dtype=torch.int64)
+    p = _lib.ptr
+    with torch.cuda.device(dev):
+        st = _lib.lib().splat_rasterize_fwd(
+            _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
+            p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys),
+            p(depths), p(radii), p(conics), p(cum), n, B, H, W, p(Ts), p(fidx), p(img),
+            m.data_ptr())
+    _lib.check(st, "rasterize")
+    return img, Ts, fidx, int(m.item())
+
+
+def rasterize_bwd(colors, opac, map_opac, background, xys, depths, radii, conics, cum, final_Ts,
+                  final_idx, v_out, *, n, B_out, B_geom, img_shape):
+    """_rasterize_bwd_warp (splax/_rasterize/_kernels.py:386-500)."""
+    colors, opac, map_opac, background, xys, depths, conics, final_Ts, v_out = map(
+        _f32, (colors, opac, map_opac, background, xys, depths, conics, final_Ts, v_out))
+    radii, cum, final_idx = _i32(radii), _i32(cum), _i32(final_idx)
+    dev = _lib.require_gpu(colors, opac, xys, conics, final_Ts, final_idx, v_out)
+    H, W = img_shape
+    nout = B_out * n
+    v_colors = torch.empty((nout, 3), device=dev, dtype=torch.float32)
+    v_opac = torch.empty((nout,), device=dev, dtype=torch.float32)
+    v_xy = torch.empty((nout, 2), device=dev, dtype=torch.float32)
+    v_conic = torch.empty((nout, 3), device=dev, dtype=torch.float32)
+    p = _lib.ptr
+    with torch.cuda.device(dev):
+        st = _lib.lib().splat_rasterize_bwd(
+            _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
+            p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys),
+            p(depths), p(radii), p(conics), p(cum), p(final_Ts), p(final_idx), p(v_out),
+            v_out.numel() // (3 * W), n, B_out, B_geom, H, W, p(v_colors), p(v_opac), p(v_xy),
+            p(v_conic))
+    _lib.check(st, "rasterize_bwd")
+    return v_colors, v_opac, v_xy, v_conic
+
+
+def sort_and_bin(xys, depths, radii, conics, map_opac, cum, *, n, B, img_shape, capacity=None):
+    """splax/_rasterize/_sort/_sort.py:29-171: sorted keys, sorted gaussian ids, tile bins."""
+    xys, depths, conics, map_opac = map(_f32, (xys, depths, conics, map_opac))
+    radii, cum = _i32(radii), _i32(cum)
+    dev = _lib.require_gpu(xys, depths, radii, conics, map_opac, cum)
+    H, W = img_shape
+    tiles = ((W + 15) // 16) * ((H + 15) // 16)
+    if capacity is None:
+        capacity = int(cum.reshape(-1)[-1].item()) if cum.numel() else 0
+    keys = torch.empty((max(capacity, 1),), device=dev, dtype=torch.int32)
+    ids = torch.empty((max(capacity, 1),), device=dev, dtype=torch.int32)
+    bins = torch.empty((B * tiles, 2), device=dev, dtype=torch.int32)
+    m = torch.zeros(1, dtype=torch.int64)
+    p = _lib.ptr
+    with torch.cuda.device(dev):
+        st = _lib.lib().splat_sort_and_bin(
+            _lib.stream_handle(dev), p(xys), p(depths), p(radii), p(conics), p(map_opac),
+            map_opac.numel(), p(cum), n, B, H, W, p(keys), p(ids), capacity, p(bins),
+            m.data_ptr())
+    _lib.check(st, "sort_and_bin")
+    M = int(m.item())
+    return keys[:M], ids[:M], bins

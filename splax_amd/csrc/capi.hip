@@ -1,0 +1,558 @@
+// C-ABI entry points of libsplat_hip.so, the per-device scratch cache and stage timing.
+//
+// Scratch follows splax/_cache.py:52-90 (grow-only, 1.25x headroom, freed by clear_cache) but is
+// owned by the library per device and guarded by a mutex (the reference leaned on Warp's FFI
+// callback lock, splax/_cache.py:99). The intersection count is read through one pinned
+// element and an event per device (splax/_cache.py:130-155). Calls from different host threads
+// on one device are serialized; calls that overlap on different streams of one device share the
+// scratch and must not run concurrently on the GPU.
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "../../include/splat_hip.h"
+#include "splat_common.hpp"
+#include "splat_internal.hpp"
+
+namespace splat {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+// ------------------------------------------------------------------ fills
+
+__global__ void fill_zero_f32_kernel(float* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0.0f;
+}
+__global__ void fill_zero_i32_kernel(int32_t* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+static unsigned fill_blocks(int64_t n) {
+    int64_t b = (n + 255) / 256;
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(b, 4096));
+}
+
+int fill_zero_f32(float* p, int64_t n, hipStream_t stream) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(fill_zero_f32_kernel, dim3(fill_blocks(n)), dim3(256), 0, stream, p, n);
+    return hipGetLastError() == hipSuccess ? 0 : fail(kErrLaunch, "fill launch failed");
+}
+int fill_zero_i32(int32_t* p, int64_t n, hipStream_t stream) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(fill_zero_i32_kernel, dim3(fill_blocks(n)), dim3(256), 0, stream, p, n);
+    return hipGetLastError() == hipSuccess ? 0 : fail(kErrLaunch, "fill launch failed");
+}
+
+// ------------------------------------------------------------------ scratch
+
+constexpr int kMaxDevices = 64;
+static DeviceScratch g_scratch[kMaxDevices];
+
+template <typename T>
+static int dev_alloc(T** p, int64_t count, bool zero) {
+    void* q = nullptr;
+    size_t bytes = (size_t)std::max<int64_t>(count, 1) * sizeof(T);
+    if (hipMalloc(&q, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(kErrAlloc, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+    }
+    if (zero && hipMemset(q, 0, bytes) != hipSuccess) return fail(kErrAlloc, "hipMemset failed");
+    *p = static_cast<T*>(q);
+    return 0;
+}
+template <typename T>
+static void dev_free(T** p) {
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+}
+
+int DeviceScratch::ensure_base() {
+    if (tickets) return 0;
+    int rc = dev_alloc(&tickets, kNumTickets, true);
+    if (!rc) rc = dev_alloc(&hist, 4 * 256, true);
+    if (!rc) rc = dev_alloc(&scan_status, 4096, true);
+    if (rc) return rc;
+    scan_status_cap = 4096;
+    void* h = nullptr;
+    if (hipHostMalloc(&h, sizeof(int32_t), hipHostMallocDefault) != hipSuccess)
+        return fail(kErrAlloc, "pinned readback allocation failed");
+    pinned_count = static_cast<int32_t*>(h);
+    if (hipEventCreateWithFlags(&count_event, hipEventDisableTiming) != hipSuccess)
+        return fail(kErrRuntime, "event creation failed");
+    return 0;
+}
+
+int DeviceScratch::grow_scan_status(int64_t blocks) {
+    if (blocks <= scan_status_cap) return 0;
+    (void)hipDeviceSynchronize();
+    dev_free(&scan_status);
+    int64_t cap = (int64_t)(blocks * 1.25) + 1;
+    int rc = dev_alloc(&scan_status, cap, true);
+    if (rc) {
+        scan_status_cap = 0;
+        return rc;
+    }
+    scan_status_cap = cap;
+    return 0;
+}
+
+int DeviceScratch::ensure_sort(int64_t M, int64_t bins, int32_t B) {
+    const int64_t sort_tile = 256 * 16;
+    const int64_t mm_blocks = 2 * (int64_t)B * 4096;  // generous partial capacity bound below
+    bool need_sync = true;
+    auto sync_once = [&]() {
+        if (need_sync) {
+            (void)hipDeviceSynchronize();
+            need_sync = false;
+        }
+    };
+    int rc = 0;
+    if (M > isect_cap) {
+        sync_once();
+        for (int k = 0; k < 2; ++k) {
+            dev_free(&keys[k]);
+            dev_free(&vals[k]);
+        }
+        isect_cap = 0;
+        int64_t cap = (int64_t)(M * 1.25) + 1;
+        for (int k = 0; k < 2 && !rc; ++k) {
+            rc = dev_alloc(&keys[k], cap, false);
+            if (!rc) rc = dev_alloc(&vals[k], cap, false);
+        }
+        if (rc) return rc;
+        isect_cap = cap;
+    }
+    const int64_t parts = (M + sort_tile - 1) / sort_tile;
+    if (parts * 256 > sort_status_cap) {
+        sync_once();
+        dev_free(&sort_status);
+        int64_t cap = (int64_t)(parts * 1.25 + 1) * 256;
+        rc = dev_alloc(&sort_status, cap, true);
+        if (rc) {
+            sort_status_cap = 0;
+            return rc;
+        }
+        sort_status_cap = cap;
+    }
+    if (2 * bins > bins_cap) {
+        sync_once();
+        dev_free(&tile_bins);
+        rc = dev_alloc(&tile_bins, 2 * bins, true);
+        if (rc) {
+            bins_cap = 0;
+            return rc;
+        }
+        bins_cap = 2 * bins;
+    }
+    if (2 * (int64_t)B > mm_cap) {
+        sync_once();
+        dev_free(&depth_mm);
+        rc = dev_alloc(&depth_mm, 2 * (int64_t)B, true);
+        if (rc) {
+            mm_cap = 0;
+            return rc;
+        }
+        mm_cap = 2 * (int64_t)B;
+    }
+    (void)mm_blocks;
+    return 0;
+}
+
+static int ensure_minmax_partials(DeviceScratch& sc, int64_t count) {
+    if (count <= sc.mm_partial_cap) return 0;
+    (void)hipDeviceSynchronize();
+    dev_free(&sc.mm_partial);
+    int64_t cap = (int64_t)(count * 1.25) + 2;
+    int rc = dev_alloc(&sc.mm_partial, cap, false);
+    if (rc) {
+        sc.mm_partial_cap = 0;
+        return rc;
+    }
+    sc.mm_partial_cap = cap;
+    return 0;
+}
+
+void DeviceScratch::release() {
+    if (!tickets && !keys[0] && !tile_bins) return;
+    (void)hipDeviceSynchronize();
+    for (int k = 0; k < 2; ++k) {
+        dev_free(&keys[k]);
+        dev_free(&vals[k]);
+    }
+    isect_cap = 0;
+    dev_free(&sort_status);
+    sort_status_cap = 0;
+    dev_free(&tile_bins);
+    bins_cap = 0;
+    dev_free(&depth_mm);
+    mm_cap = 0;
+    dev_free(&mm_partial);
+    mm_partial_cap = 0;
+    dev_free(&scan_status);
+    scan_status_cap = 0;
+    dev_free(&tickets);
+    dev_free(&hist);
+    if (pinned_count) (void)hipHostFree(pinned_count);
+    pinned_count = nullptr;
+    if (count_event) (void)hipEventDestroy(count_event);
+    count_event = nullptr;
+}
+
+DeviceScratch& scratch_for_current_device() {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev < 0 || dev >= kMaxDevices) dev = 0;
+    g_scratch[dev].device = dev;
+    return g_scratch[dev];
+}
+
+void release_all_scratch() {
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    for (int d = 0; d < kMaxDevices; ++d) {
+        DeviceScratch& sc = g_scratch[d];
+        std::lock_guard<std::mutex> lock(sc.mu);
+        if (sc.device < 0) continue;
+        if (hipSetDevice(d) != hipSuccess) continue;
+        sc.release();
+    }
+    (void)hipSetDevice(cur);
+}
+
+// ------------------------------------------------------------------ stage timing
+
+static std::mutex g_timing_mu;
+static bool g_timing = false;
+struct TimedSpan {
+    int stage;
+    hipEvent_t a, b;
+};
+static std::vector<TimedSpan> g_spans;
+static std::vector<hipEvent_t> g_event_pool;
+
+static hipEvent_t take_event() {
+    if (!g_event_pool.empty()) {
+        hipEvent_t e = g_event_pool.back();
+        g_event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    (void)hipEventCreate(&e);
+    return e;
+}
+
+StageTimer::StageTimer(hipStream_t s, int st) : stream(s), stage(st) {
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    if (!g_timing) return;
+    start = take_event();
+    (void)hipEventRecord(start, stream);
+}
+
+StageTimer::~StageTimer() {
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    if (!start) return;
+    hipEvent_t end = take_event();
+    (void)hipEventRecord(end, stream);
+    g_spans.push_back({stage, start, end});
+}
+
+}  // namespace splat
+
+using namespace splat;
+
+static double g_stage_ms[kNumStages];
+static int64_t g_stage_calls[kNumStages];
+
+extern "C" {
+
+int splat_abi_version(void) { return 1; }
+
+int splat_check_device(void) {
+    DeviceScratch& sc = scratch_for_current_device();
+    std::lock_guard<std::mutex> lock(sc.mu);
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    if (!sc.tickets) return 0;
+    uint32_t word = 0;
+    if (hipMemcpy(&word, sc.tickets + kDeviceError, sizeof(word), hipMemcpyDeviceToHost) !=
+        hipSuccess)
+        return -1;
+    if (word) {
+        uint32_t zero = 0;
+        (void)hipMemcpy(sc.tickets + kDeviceError, &zero, sizeof(zero), hipMemcpyHostToDevice);
+    }
+    return (int)word;
+}
+
+const char* splat_last_error(void) { return g_last_error.c_str(); }
+
+void splat_clear_cache(void) { release_all_scratch(); }
+
+int splat_set_stage_timing(int enabled) {
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    g_timing = enabled != 0;
+    return 0;
+}
+
+int splat_get_stage_times(double* ms, int64_t* calls, int32_t n) {
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    for (auto& s : g_spans) {
+        if (hipEventSynchronize(s.b) != hipSuccess) return fail(kErrRuntime, "event sync failed");
+        float t = 0.f;
+        (void)hipEventElapsedTime(&t, s.a, s.b);
+        g_stage_ms[s.stage] += t;
+        g_stage_calls[s.stage] += 1;
+        g_event_pool.push_back(s.a);
+        g_event_pool.push_back(s.b);
+    }
+    g_spans.clear();
+    for (int k = 0; k < n && k < kNumStages; ++k) {
+        if (ms) ms[k] = g_stage_ms[k];
+        if (calls) calls[k] = g_stage_calls[k];
+    }
+    for (int k = 0; k < kNumStages; ++k) {
+        g_stage_ms[k] = 0.0;
+        g_stage_calls[k] = 0;
+    }
+    return 0;
+}
+
+int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
+                      const float* scales, int64_t rows_scales, const float* quats_xyzw,
+                      int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
+                      const float* opacities, int64_t rows_opac, const float* transforms,
+                      int64_t rows_transforms, const int32_t* transform_ids,
+                      int32_t num_gaussians, int32_t num_transforms, int32_t has_transforms,
+                      int64_t total, int32_t img_h, int32_t img_w, float fx, float fy, float cx,
+                      float cy, float glob_scale, float clip_thresh, float* xys, float* depths,
+                      int32_t* radii, float* conics, int32_t* num_tiles_hit,
+                      int32_t* cum_tiles_hit) {
+    if (num_gaussians <= 0 || total < 0 || total % num_gaussians != 0 || img_h <= 0 ||
+        img_w <= 0)
+        return fail(kErrArgs, "project_fwd: invalid sizes");
+    if (rows_means < num_gaussians || rows_scales < num_gaussians ||
+        rows_quats < num_gaussians || rows_opac < num_gaussians || rows_viewmat < 4)
+        return fail(kErrArgs, "project_fwd: operand has fewer rows than num_gaussians");
+    if (has_transforms && (num_transforms <= 0 || !transforms || !transform_ids))
+        return fail(kErrArgs, "project_fwd: transforms requested but not given");
+    if (total >= ((int64_t)1 << 31))
+        return fail(kErrArgs, "project_fwd: more than 2^31 items");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    DeviceScratch& sc = scratch_for_current_device();
+    std::lock_guard<std::mutex> lock(sc.mu);
+    int rc = sc.ensure_base();
+    if (rc) return rc;
+    ProjectArgs a;
+    a.means = means3d; a.rows_means = rows_means;
+    a.scales = scales; a.rows_scales = rows_scales;
+    a.quats = quats_xyzw; a.rows_quats = rows_quats;
+    a.viewmat = viewmat; a.rows_viewmat = rows_viewmat;
+    a.opacities = opacities; a.rows_opac = rows_opac;
+    a.transforms = transforms; a.rows_transforms = has_transforms ? rows_transforms : 0;
+    a.transform_ids = transform_ids;
+    a.n = num_gaussians; a.num_transforms = has_transforms ? num_transforms : 1;
+    a.has_transforms = has_transforms;
+    a.total = total; a.img_h = img_h; a.img_w = img_w;
+    a.fx = fx; a.fy = fy; a.cx = cx; a.cy = cy;
+    a.glob_scale = glob_scale; a.clip_thresh = clip_thresh;
+    a.xys = xys; a.depths = depths; a.radii = radii; a.conics = conics;
+    a.num_tiles_hit = num_tiles_hit; a.cum_tiles_hit = cum_tiles_hit;
+    StageTimer tm(s, kStageProject);
+    rc = launch_project_fwd(a, sc, s);
+    if (rc && g_last_error.empty()) set_error("project_fwd launch failed");
+    return rc;
+}
+
+int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
+                      const float* scales, int64_t rows_scales, const float* quats_xyzw,
+                      int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
+                      const int32_t* radii, int64_t rows_radii, const float* conics,
+                      int64_t rows_conics, const float* v_xy, int64_t rows_vxy,
+                      const float* v_depth, int64_t rows_vdepth, const float* v_conic,
+                      int64_t rows_vconic, const float* transforms, int64_t rows_transforms,
+                      const int32_t* transform_ids, int32_t num_gaussians,
+                      int32_t num_transforms, int32_t has_transforms, int32_t B, float fx,
+                      float fy, float glob_scale, float* v_mean3d, float* v_scale,
+                      float* v_quat, float* v_viewmat, float* v_transforms) {
+    if (num_gaussians <= 0 || B <= 0) return fail(kErrArgs, "project_bwd: invalid sizes");
+    if (has_transforms && (num_transforms <= 0 || !transforms || !transform_ids || !v_transforms))
+        return fail(kErrArgs, "project_bwd: transforms requested but not given");
+    if ((int64_t)B * num_gaussians >= ((int64_t)1 << 31))
+        return fail(kErrArgs, "project_bwd: more than 2^31 items");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    ProjectBwdArgs a;
+    a.means = means3d; a.rows_means = rows_means;
+    a.scales = scales; a.rows_scales = rows_scales;
+    a.quats = quats_xyzw; a.rows_quats = rows_quats;
+    a.viewmat = viewmat; a.rows_viewmat = rows_viewmat;
+    a.radii = radii; a.rows_radii = rows_radii;
+    a.conics = conics; a.rows_conics = rows_conics;
+    a.v_xy = v_xy; a.rows_vxy = rows_vxy;
+    a.v_depth = v_depth; a.rows_vdepth = rows_vdepth;
+    a.v_conic = v_conic; a.rows_vconic = rows_vconic;
+    a.transforms = transforms; a.rows_transforms = has_transforms ? rows_transforms : 0;
+    a.transform_ids = transform_ids;
+    a.n = num_gaussians; a.num_transforms = has_transforms ? num_transforms : 0;
+    a.has_transforms = has_transforms; a.B = B;
+    a.fx = fx; a.fy = fy; a.glob_scale = glob_scale;
+    a.v_mean3d = v_mean3d; a.v_scale = v_scale; a.v_quat = v_quat;
+    a.v_viewmat = v_viewmat; a.v_transforms = has_transforms ? v_transforms : nullptr;
+    StageTimer tm(s, kStageProjectBwd);
+    int rc = launch_project_bwd(a, s);
+    if (rc && g_last_error.empty()) set_error("project_bwd launch failed");
+    return rc;
+}
+
+static int check_raster(const RasterInputs& in) {
+    if (in.n <= 0 || in.B_geom <= 0 || in.img_h <= 0 || in.img_w <= 0)
+        return fail(kErrArgs, "rasterize: invalid sizes");
+    if (in.rows_colors < in.n || in.rows_opac < in.n || in.rows_map_opac < in.n ||
+        in.rows_bg < 1)
+        return fail(kErrArgs, "rasterize: operand has fewer rows than num_gaussians");
+    if ((int64_t)in.B_geom * in.n >= ((int64_t)1 << 31))
+        return fail(kErrArgs, "rasterize: more than 2^31 items");
+    return 0;
+}
+
+int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* depths,
+                       const int32_t* radii, const float* conics, const float* map_opacities,
+                       int64_t rows_map_opac, const int32_t* cum_tiles_hit,
+                       int32_t num_gaussians, int32_t B, int32_t img_h, int32_t img_w,
+                       int32_t* sorted_keys, int32_t* sorted_ids, int64_t capacity,
+                       int32_t* tile_bins, int64_t* num_intersects) {
+    RasterInputs in{};
+    in.colors = nullptr; in.rows_colors = num_gaussians;
+    in.opac = nullptr; in.rows_opac = num_gaussians;
+    in.map_opac = map_opacities; in.rows_map_opac = rows_map_opac;
+    in.background = nullptr; in.rows_bg = 1;
+    in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
+    in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B;
+    in.img_h = img_h; in.img_w = img_w;
+    int rc = check_raster(in);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    DeviceScratch& sc = scratch_for_current_device();
+    std::lock_guard<std::mutex> lock(sc.mu);
+    rc = sc.ensure_base();
+    if (!rc) {
+        const int32_t bpi = (num_gaussians + 4095) / 4096;
+        rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * B);
+    }
+    if (rc) return rc;
+    int64_t M = 0;
+    KeyLayout L;
+    rc = run_sort_and_bin(in, sc, s, &M, &L);
+    if (num_intersects) *num_intersects = M;
+    if (rc) return rc;
+    if (M > capacity) return fail(kErrTooMany, "sort_and_bin: capacity below intersection count");
+    const int64_t nb = 2 * (int64_t)B * L.num_tiles;
+    if (hipMemcpyAsync(tile_bins, sc.tile_bins, nb * sizeof(int32_t), hipMemcpyDeviceToDevice,
+                       s) != hipSuccess)
+        return fail(kErrRuntime, "bins copy failed");
+    if (M > 0) {
+        if (hipMemcpyAsync(sorted_keys, sc.keys[0], M * sizeof(int32_t), hipMemcpyDeviceToDevice,
+                           s) != hipSuccess ||
+            hipMemcpyAsync(sorted_ids, sc.vals[0], M * sizeof(int32_t), hipMemcpyDeviceToDevice,
+                           s) != hipSuccess)
+            return fail(kErrRuntime, "sorted copy failed");
+    }
+    return 0;
+}
+
+int splat_rasterize_fwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
+                        const float* opacities, int64_t rows_opac, const float* map_opacities,
+                        int64_t rows_map_opac, const float* background, int64_t rows_bg,
+                        const float* xys, const float* depths, const int32_t* radii,
+                        const float* conics, const int32_t* cum_tiles_hit,
+                        int32_t num_gaussians, int32_t B, int32_t img_h, int32_t img_w,
+                        float* final_Ts, int32_t* final_idx, float* out_img,
+                        int64_t* num_intersects) {
+    RasterInputs in{};
+    in.colors = colors; in.rows_colors = rows_colors;
+    in.opac = opacities; in.rows_opac = rows_opac;
+    in.map_opac = map_opacities; in.rows_map_opac = rows_map_opac;
+    in.background = background; in.rows_bg = rows_bg;
+    in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
+    in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B;
+    in.img_h = img_h; in.img_w = img_w;
+    int rc = check_raster(in);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    DeviceScratch& sc = scratch_for_current_device();
+    std::lock_guard<std::mutex> lock(sc.mu);
+    rc = sc.ensure_base();
+    if (!rc) {
+        const int32_t bpi = (num_gaussians + 4095) / 4096;
+        rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * B);
+    }
+    if (rc) return rc;
+    int64_t M = 0;
+    KeyLayout L;
+    rc = run_sort_and_bin(in, sc, s, &M, &L);
+    if (num_intersects) *num_intersects = M;
+    if (rc) return rc;
+    StageTimer tm(s, kStageBlendFwd);
+    rc = launch_blend_fwd(in, L, sc.vals[0] ? sc.vals[0] : nullptr, sc.tile_bins, final_Ts,
+                          final_idx, out_img, s);
+    if (rc) return fail(rc, "blend_fwd launch failed");
+    return 0;
+}
+
+int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
+                        const float* opacities, int64_t rows_opac, const float* map_opacities,
+                        int64_t rows_map_opac, const float* background, int64_t rows_bg,
+                        const float* xys, const float* depths, const int32_t* radii,
+                        const float* conics, const int32_t* cum_tiles_hit,
+                        const float* final_Ts, const int32_t* final_idx, const float* v_out_img,
+                        int64_t vout_rows, int32_t num_gaussians, int32_t B_out, int32_t B_geom,
+                        int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
+                        float* v_xy, float* v_conic) {
+    RasterInputs in{};
+    in.colors = colors; in.rows_colors = rows_colors;
+    in.opac = opacities; in.rows_opac = rows_opac;
+    in.map_opac = map_opacities; in.rows_map_opac = rows_map_opac;
+    in.background = background; in.rows_bg = rows_bg;
+    in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
+    in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B_geom;
+    in.img_h = img_h; in.img_w = img_w;
+    int rc = check_raster(in);
+    if (rc) return rc;
+    if (B_out <= 0 || (B_geom > 1 && B_geom != B_out))
+        return fail(kErrArgs, "rasterize_bwd: B_geom must be 1 or equal to B_out");
+    if (vout_rows <= 0) return fail(kErrArgs, "rasterize_bwd: empty cotangent");
+    if ((int64_t)B_out * num_gaussians >= ((int64_t)1 << 31))
+        return fail(kErrArgs, "rasterize_bwd: more than 2^31 gradient rows");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    DeviceScratch& sc = scratch_for_current_device();
+    std::lock_guard<std::mutex> lock(sc.mu);
+    rc = sc.ensure_base();
+    if (!rc) {
+        const int32_t bpi = (num_gaussians + 4095) / 4096;
+        rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * B_geom);
+    }
+    if (rc) return rc;
+    int64_t M = 0;
+    KeyLayout L;
+    rc = run_sort_and_bin(in, sc, s, &M, &L);
+    if (rc) return rc;
+    BlendBwdArgs a;
+    a.final_Ts = final_Ts; a.final_idx = final_idx;
+    a.v_out = v_out_img; a.vout_rows = vout_rows; a.B_out = B_out;
+    a.v_colors = v_colors; a.v_opacity = v_opacity; a.v_xy = v_xy; a.v_conic = v_conic;
+    StageTimer tm(s, kStageBlendBwd);
+    rc = launch_blend_bwd(in, L, M > 0 ? sc.vals[0] : nullptr, sc.tile_bins, a, s);
+    if (rc) return fail(rc, "blend_bwd launch failed");
+    return 0;
+}
+
+}  // extern "C"

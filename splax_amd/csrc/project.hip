@@ -1,0 +1,535 @@
+// Projection forward (fused with the global inclusive scan of the tile counts) and projection
+// backward, gfx950.
+//
+// project_fwd: one thread per flat item (image b, gaussian g), restating _project_kernel
+// (splax/_project/_kernels.py:122-248). Each workgroup owns a contiguous chunk of items; after
+// counting tiles it scans its chunk in LDS and resolves its global prefix with a decoupled
+// look-back over the chunks before it, so cum_tiles_hit (the inclusive scan the reference gets
+// from a separate wp.utils.array_scan, splax/_project/_kernels.py:107) is written by the same
+// launch. Chunks are taken in ticket order (atomic counter), so every chunk a workgroup waits on
+// is already running.
+//
+// project_bwd: one thread per flat item, restating _project_bwd_kernel
+// (splax/_project/_kernels.py:356-484); the per-image viewmat gradient is reduced per wave with
+// DPP, then per workgroup in LDS, and added with one atomic per entry per workgroup.
+#include "splat_common.hpp"
+#include "splat_internal.hpp"
+
+namespace splat {
+
+struct ProjectParams {
+    const float* means; int64_t rows_means;
+    const float* scales; int64_t rows_scales;
+    const float* quats; int64_t rows_quats;
+    const float* viewmat; int64_t rows_viewmat;
+    const float* opac; int64_t rows_opac;
+    const float* transforms; int64_t rows_transforms;
+    const int32_t* transform_ids;
+    int32_t n, num_transforms, has_transforms;
+    int64_t total;
+    int32_t img_h, img_w;
+    float fx, fy, cx, cy, glob_scale, clip_thresh;
+    float* xys; float* depths; int32_t* radii; float* conics;
+    int32_t* num_tiles_hit; int32_t* cum_tiles_hit;
+    // scan state
+    uint64_t* status; uint32_t* ticket; uint32_t epoch; uint32_t* err;
+};
+
+constexpr int kProjThreads = 256;
+
+__device__ __forceinline__ bool apply_transform(const float* transforms, int32_t image_id,
+                                                int32_t num_transforms, bool sel_tf,
+                                                int32_t tf_id, float* mean, float* R_tf) {
+    R_tf[0] = 1.f; R_tf[1] = 0.f; R_tf[2] = 0.f;
+    R_tf[3] = 0.f; R_tf[4] = 1.f; R_tf[5] = 0.f;
+    R_tf[6] = 0.f; R_tf[7] = 0.f; R_tf[8] = 1.f;
+    // ids outside [0, num_transforms) are treated as static
+    if (tf_id < 0 || tf_id >= num_transforms) return false;
+    int64_t tf_idx = sel_tf ? (int64_t)image_id * num_transforms + tf_id : tf_id;
+    const float* m = transforms + tf_idx * 16;
+    float t[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        R_tf[3 * i] = m[4 * i];
+        R_tf[3 * i + 1] = m[4 * i + 1];
+        R_tf[3 * i + 2] = m[4 * i + 2];
+        t[i] = m[4 * i + 3];
+    }
+    float rm[3];
+    mat_vec(R_tf, mean, rm);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) mean[i] = rm[i] + t[i];
+    return true;
+}
+
+// _project_geom, splax/_project/_kernels.py:647-664
+__device__ __forceinline__ void project_geom(const float* mean, const float* q, const float* sc,
+                                             float glob_scale, const float* vm, const float* R_tf,
+                                             bool moved, float* W, float* p, float* M) {
+    float tr[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        W[3 * i] = vm[4 * i];
+        W[3 * i + 1] = vm[4 * i + 1];
+        W[3 * i + 2] = vm[4 * i + 2];
+        tr[i] = vm[4 * i + 3];
+    }
+    float wm[3];
+    mat_vec(W, mean, wm);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) p[i] = wm[i] + tr[i];
+    float R[9];
+    quat_to_rot(q[0], q[1], q[2], q[3], R);
+    float s[3] = {glob_scale * sc[0], glob_scale * sc[1], glob_scale * sc[2]};
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) M[3 * i + j] = R[3 * i + j] * s[j];
+    if (moved) {
+        float Mm[9];
+        mat_mul(R_tf, M, Mm);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) M[k] = Mm[k];
+    }
+}
+
+// Per-item projection; returns the tile count (0 when culled) and writes the item's outputs.
+__device__ __forceinline__ int32_t project_item(const ProjectParams& P, int64_t idx) {
+    const int32_t n = P.n;
+    const int32_t bid = (int32_t)(idx / n), gid = (int32_t)(idx - (int64_t)bid * n);
+    const int64_t m_idx = P.rows_means > n ? idx : gid;
+    const int64_t s_idx = P.rows_scales > n ? idx : gid;
+    const int64_t q_idx = P.rows_quats > n ? idx : gid;
+    const int64_t o_idx = P.rows_opac > n ? idx : gid;
+    const int64_t vb = (int64_t)(P.rows_viewmat > 4 ? bid : 0) * 4;
+
+    float2 xy = make_float2(0.f, 0.f);
+    float depth = 0.f;
+    int32_t radius = 0;
+    float con0 = 0.f, con1 = 0.f, con2 = 0.f;
+    int32_t count = 0;
+
+    float mean[3] = {P.means[3 * m_idx], P.means[3 * m_idx + 1], P.means[3 * m_idx + 2]};
+    int32_t tf_id = P.has_transforms ? P.transform_ids[gid] : -1;
+    float R_tf[9];
+    bool moved = apply_transform(P.transforms, bid, P.num_transforms,
+                                 P.rows_transforms > P.num_transforms, tf_id, mean, R_tf);
+    float W[9], p[3], M[9];
+    project_geom(mean, P.quats + 4 * q_idx, P.scales + 3 * s_idx, P.glob_scale,
+                 P.viewmat + vb * 4, R_tf, moved, W, p, M);
+    do {
+        if (p[2] <= P.clip_thresh) break;
+        float V[9];
+        mat_mul_nt(M, M, V);
+        const float tan_fovx = 0.5f * (float)P.img_w / P.fx;
+        const float tan_fovy = 0.5f * (float)P.img_h / P.fy;
+        const float lim_x = kFovClamp * tan_fovx;
+        const float lim_y = kFovClamp * tan_fovy;
+        float tz = p[2];
+        float tx = tz * minw(lim_x, maxw(-lim_x, p[0] / tz));
+        float ty = tz * minw(lim_y, maxw(-lim_y, p[1] / tz));
+        float rz = 1.0f / tz;
+        float rz2 = rz * rz;
+        float j00 = P.fx * rz, j02 = -P.fx * tx * rz2, j11 = P.fy * rz, j12 = -P.fy * ty * rz2;
+        float T0[3], T1[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            T0[j] = j00 * W[j] + j02 * W[6 + j];
+            T1[j] = j11 * W[3 + j] + j12 * W[6 + j];
+        }
+        float TV0[3], TV1[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            TV0[k] = (T0[0] * V[k] + T0[1] * V[3 + k]) + T0[2] * V[6 + k];
+            TV1[k] = (T1[0] * V[k] + T1[1] * V[3 + k]) + T1[2] * V[6 + k];
+        }
+        float c00 = (TV0[0] * T0[0] + TV0[1] * T0[1]) + TV0[2] * T0[2];
+        float c01 = (TV0[0] * T1[0] + TV0[1] * T1[1]) + TV0[2] * T1[2];
+        float c11 = (TV1[0] * T1[0] + TV1[1] * T1[1]) + TV1[2] * T1[2];
+        float cxx = c00 + kDilation, cxy = c01, cyy = c11 + kDilation;
+        float det = cxx * cyy - cxy * cxy;
+        if (det == 0.0f) break;
+        float inv_det = 1.0f / det;
+        float a = cyy * inv_det, b = -cxy * inv_det, c = cxx * inv_det;
+        float rw = 1.0f / (p[2] + kZEps);
+        float center_x = (p[0] * rw) * P.fx + P.cx;
+        float center_y = (p[1] * rw) * P.fy + P.cy;
+        float opac = P.opac[o_idx];
+        if (opac < kAlphaThresh) break;
+        float t = iso_level(opac);
+        float ext = sqrtf(t);
+        float radius_x = ceilf(ext * sqrtf(cxx));
+        float radius_y = ceilf(ext * sqrtf(cyy));
+        if (radius_x <= 0.0f && radius_y <= 0.0f) break;
+        if (center_x + radius_x <= 0.0f || center_x - radius_x >= (float)P.img_w ||
+            center_y + radius_y <= 0.0f || center_y - radius_y >= (float)P.img_h)
+            break;
+        const int32_t tb_x = (P.img_w + kBlockWidth - 1) / kBlockWidth;
+        const int32_t tb_y = (P.img_h + kBlockWidth - 1) / kBlockWidth;
+        Ellipse e = ellipse_init(a, b, c, t, center_x, center_y, tb_x, tb_y);
+        int32_t cnt = ellipse_tile_count(e);
+        if (cnt <= 0) break;
+        count = cnt;
+        depth = p[2];
+        radius = f2i(maxw(radius_x, radius_y));
+        xy = make_float2(center_x, center_y);
+        con0 = a;
+        con1 = b;
+        con2 = c;
+    } while (false);
+    reinterpret_cast<float2*>(P.xys)[idx] = xy;
+    P.depths[idx] = depth;
+    P.radii[idx] = radius;
+    P.conics[3 * idx] = con0;
+    P.conics[3 * idx + 1] = con1;
+    P.conics[3 * idx + 2] = con2;
+    P.num_tiles_hit[idx] = count;
+    return count;
+}
+
+// Items per thread of the fused projection + scan; one workgroup covers 256 * kProjItems items.
+constexpr int kProjItems = 4;
+
+__global__ void __launch_bounds__(kProjThreads) project_fwd_kernel(ProjectParams P) {
+    __shared__ uint32_t s_part;
+    __shared__ int32_t s_wave[kProjThreads / 64];
+    __shared__ int32_t s_prefix;
+    const int tid = threadIdx.x;
+    if (tid == 0) s_part = atomicAdd(P.ticket, 1u);
+    __syncthreads();
+    const uint32_t part = s_part;
+    if (tid == 0 && part == gridDim.x - 1) atomic_store_relaxed(P.ticket, 0u);
+    const int64_t base = (int64_t)part * (kProjThreads * kProjItems);
+    // Items are blocked per thread (thread t owns base + t*K .. +K-1) so the per-thread running
+    // sum plus one block scan gives the inclusive prefix.
+    int32_t cnt[kProjItems];
+    int32_t local = 0;
+#pragma unroll
+    for (int k = 0; k < kProjItems; ++k) {
+        int64_t idx = base + (int64_t)tid * kProjItems + k;
+        cnt[k] = idx < P.total ? project_item(P, idx) : 0;
+        local += cnt[k];
+    }
+    // block inclusive scan of `local`
+    const int lane = tid & 63, wave = tid >> 6;
+    int32_t incl = wave_inclusive_scan_i32(local, lane);
+    if (lane == 63) s_wave[wave] = incl;
+    __syncthreads();
+    int32_t wave_off = 0, block_total = 0;
+#pragma unroll
+    for (int w = 0; w < kProjThreads / 64; ++w) {
+        int32_t v = s_wave[w];
+        if (w < wave) wave_off += v;
+        block_total += v;
+    }
+    if (tid == 0)
+        s_prefix = lookback_single(P.status, part, (uint32_t)block_total, P.epoch, P.err);
+    __syncthreads();
+    int32_t run = s_prefix + wave_off + incl - local;
+#pragma unroll
+    for (int k = 0; k < kProjItems; ++k) {
+        int64_t idx = base + (int64_t)tid * kProjItems + k;
+        run += cnt[k];
+        if (idx < P.total) P.cum_tiles_hit[idx] = run;
+    }
+}
+
+// ------------------------------------------------------------------ projection backward
+
+struct ProjectBwdParams {
+    const float* means; int64_t rows_means;
+    const float* scales; int64_t rows_scales;
+    const float* quats; int64_t rows_quats;
+    const float* viewmat; int64_t rows_viewmat;
+    const int32_t* radii; int64_t rows_radii;
+    const float* conics; int64_t rows_conics;
+    const float* v_xy; int64_t rows_vxy;
+    const float* v_depth; int64_t rows_vdepth;
+    const float* v_conic; int64_t rows_vconic;
+    const float* transforms; int64_t rows_transforms;
+    const int32_t* transform_ids;
+    int32_t n, num_transforms, has_transforms, B, blocks_per_image;
+    float fx, fy, glob_scale;
+    float* v_mean3d; float* v_scale; float* v_quat; float* v_viewmat; float* v_transforms;
+};
+
+__global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdParams P) {
+    __shared__ float s_red[kProjThreads / 64][12];
+    __shared__ int32_t s_tf[2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int32_t n = P.n;
+    const int32_t image_id = blockIdx.x / P.blocks_per_image;
+    const int32_t local_block = blockIdx.x - image_id * P.blocks_per_image;
+    const int32_t gid = local_block * kProjThreads + tid;
+    const int64_t idx = (int64_t)image_id * n + gid;
+    float vR[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    float vt[3] = {0, 0, 0};
+    float vRtf[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    float vttf[3] = {0, 0, 0};
+    bool moved = false;
+    int32_t tf_id = -1;
+    const bool in_range = gid < n;
+    if (in_range && P.has_transforms) tf_id = P.transform_ids[gid];
+    if (in_range) {
+        float zero3[3] = {0.f, 0.f, 0.f};
+        float vmean_out[3] = {0.f, 0.f, 0.f}, vscale[3] = {0.f, 0.f, 0.f};
+        float vq[4] = {0.f, 0.f, 0.f, 0.f};
+        (void)zero3;
+        const int64_t r_idx = P.rows_radii > n ? idx : gid;
+        if (P.radii[r_idx] > 0) {
+            const int64_t m_idx = P.rows_means > n ? idx : gid;
+            const int64_t s_idx = P.rows_scales > n ? idx : gid;
+            const int64_t q_idx = P.rows_quats > n ? idx : gid;
+            const int64_t c_idx = P.rows_conics > n ? idx : gid;
+            const int64_t vx_idx = P.rows_vxy > n ? idx : gid;
+            const int64_t vd_idx = P.rows_vdepth > n ? idx : gid;
+            const int64_t vc_idx = P.rows_vconic > n ? idx : gid;
+            const int64_t vb = (int64_t)(P.rows_viewmat > 4 ? image_id : 0) * 4;
+            const float* mean_local = P.means + 3 * m_idx;
+            float ml[3] = {mean_local[0], mean_local[1], mean_local[2]};
+            float mean[3] = {ml[0], ml[1], ml[2]};
+            float R_tf[9];
+            moved = apply_transform(P.transforms, image_id, P.num_transforms,
+                                    P.rows_transforms > P.num_transforms, tf_id, mean, R_tf);
+            const float* q = P.quats + 4 * q_idx;
+            float qx = q[0], qy = q[1], qz = q[2], qw = q[3];
+            float qv[4] = {qx, qy, qz, qw};
+            const float* sc = P.scales + 3 * s_idx;
+            float scv[3] = {sc[0], sc[1], sc[2]};
+            float W[9], p[3], M[9];
+            project_geom(mean, qv, scv, P.glob_scale, P.viewmat + vb * 4, R_tf, moved, W, p, M);
+            float V[9];
+            mat_mul_nt(M, M, V);
+            float R[9];
+            quat_to_rot(qx, qy, qz, qw, R);
+            float s[3] = {P.glob_scale * scv[0], P.glob_scale * scv[1], P.glob_scale * scv[2]};
+            const float fx = P.fx, fy = P.fy;
+            float rz = 1.0f / p[2];
+            float rz2 = rz * rz;
+            float J[9] = {fx * rz, 0.0f, -fx * p[0] * rz2, 0.0f, fy * rz, -fy * p[1] * rz2,
+                          0.0f, 0.0f, 0.0f};
+            float T[9];
+            mat_mul(J, W, T);
+            const float* cn = P.conics + 3 * c_idx;
+            const float* vc = P.v_conic + 3 * vc_idx;
+            float X0 = cn[0], X1 = cn[1], X3 = cn[2];
+            float G0 = vc[0], G1 = 0.5f * vc[1], G3 = vc[2];
+            float XG0 = X0 * G0 + X1 * G1, XG1 = X0 * G1 + X1 * G3;
+            float XG2 = X1 * G0 + X3 * G1, XG3 = X1 * G1 + X3 * G3;
+            float S0 = XG0 * X0 + XG1 * X1, S1 = XG0 * X1 + XG1 * X3;
+            float S2 = XG2 * X0 + XG3 * X1, S3 = XG2 * X1 + XG3 * X3;
+            float vcov0 = -S0, vcov1 = -(S1 + S2), vcov2 = -S3;
+            // _proj_vjp, splax/_project/_kernels.py:487-533
+            float tx = p[0], ty = p[1], tz = p[2];
+            float prz = 1.0f / tz;
+            float prz2 = prz * prz;
+            float prz3 = prz2 * prz;
+            float rw = 1.0f / (tz + kZEps);
+            const float* vxy = P.v_xy + 2 * vx_idx;
+            float vpx = fx * vxy[0], vpy = fy * vxy[1];
+            float vvx = vpx * rw, vvy = vpy * rw;
+            float vvz = -(vpx * tx + vpy * ty) * rw * rw;
+            vvz = vvz + P.v_depth[vd_idx];
+            float v_cov[9] = {vcov0, 0.5f * vcov1, 0.0f, 0.5f * vcov1, vcov2, 0.0f,
+                              0.0f, 0.0f, 0.0f};
+            float tmp[9], v_V[9], v_T[9], v_J[9], two_vcov[9];
+            mat_mul_tn(T, v_cov, tmp);
+            mat_mul(tmp, T, v_V);
+#pragma unroll
+            for (int k = 0; k < 9; ++k) two_vcov[k] = 2.0f * v_cov[k];
+            mat_mul(two_vcov, T, tmp);
+            mat_mul(tmp, V, v_T);
+            mat_mul_nt(v_T, W, v_J);
+            float v_t_x = -fx * prz2 * v_J[2];
+            float v_t_y = -fy * prz2 * v_J[5];
+            float v_t_z = -fx * prz2 * v_J[0] + 2.0f * fx * tx * prz3 * v_J[2] -
+                          fy * prz2 * v_J[4] + 2.0f * fy * ty * prz3 * v_J[5];
+            float v_p[3] = {vvx + v_t_x, vvy + v_t_y, vvz + v_t_z};
+            float v_mean_world[3];
+            mat_t_vec(W, v_p, v_mean_world);
+            float vVs[9], v_M_world[9];
+#pragma unroll
+            for (int a = 0; a < 3; ++a)
+#pragma unroll
+                for (int b = 0; b < 3; ++b) vVs[3 * a + b] = v_V[3 * a + b] + v_V[3 * b + a];
+            mat_mul(vVs, M, v_M_world);
+            float v_M[9];
+            if (moved) {
+                mat_t_vec(R_tf, v_mean_world, vmean_out);
+                mat_mul_tn(R_tf, v_M_world, v_M);
+                float M_local[9], vmMl[9];
+                mat_mul_tn(R_tf, M, M_local);
+                mat_mul_nt(v_M_world, M_local, vmMl);
+#pragma unroll
+                for (int a = 0; a < 3; ++a)
+#pragma unroll
+                    for (int b = 0; b < 3; ++b)
+                        vRtf[3 * a + b] = v_mean_world[a] * ml[b] + vmMl[3 * a + b];
+#pragma unroll
+                for (int a = 0; a < 3; ++a) vttf[a] = v_mean_world[a];
+            } else {
+#pragma unroll
+                for (int a = 0; a < 3; ++a) vmean_out[a] = v_mean_world[a];
+#pragma unroll
+                for (int k = 0; k < 9; ++k) v_M[k] = v_M_world[k];
+            }
+            // _scale_vjp
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                vscale[j] = ((R[j] * v_M[j] + R[3 + j] * v_M[3 + j]) + R[6 + j] * v_M[6 + j]) *
+                            P.glob_scale;
+            // _quat_vjp (xyzw output)
+            float r[9];
+#pragma unroll
+            for (int a = 0; a < 3; ++a)
+#pragma unroll
+                for (int b = 0; b < 3; ++b) r[3 * a + b] = v_M[3 * a + b] * s[b];
+            float x = qx, y = qy, z = qz, w = qw;
+            vq[3] = 2.0f * ((x * (r[7] - r[5]) + y * (r[2] - r[6])) + z * (r[3] - r[1]));
+            vq[0] = 2.0f * (((-2.0f * x * (r[4] + r[8]) + y * (r[3] + r[1])) +
+                             z * (r[6] + r[2])) + w * (r[7] - r[5]));
+            vq[1] = 2.0f * (((x * (r[3] + r[1]) - 2.0f * y * (r[0] + r[8])) +
+                             z * (r[7] + r[5])) + w * (r[2] - r[6]));
+            vq[2] = 2.0f * (((x * (r[6] + r[2]) + y * (r[7] + r[5])) -
+                             2.0f * z * (r[0] + r[4])) + w * (r[3] - r[1]));
+            // _view_vjp: v_R = v_p (x) mean + J^T v_T, v_t = v_p
+            float JtvT[9];
+            mat_mul_tn(J, v_T, JtvT);
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+#pragma unroll
+                for (int b = 0; b < 3; ++b) vR[3 * a + b] = v_p[a] * mean[b] + JtvT[3 * a + b];
+                vt[a] = v_p[a];
+            }
+        }
+        P.v_mean3d[3 * idx] = vmean_out[0];
+        P.v_mean3d[3 * idx + 1] = vmean_out[1];
+        P.v_mean3d[3 * idx + 2] = vmean_out[2];
+        P.v_scale[3 * idx] = vscale[0];
+        P.v_scale[3 * idx + 1] = vscale[1];
+        P.v_scale[3 * idx + 2] = vscale[2];
+        reinterpret_cast<float4*>(P.v_quat)[idx] = make_float4(vq[0], vq[1], vq[2], vq[3]);
+    }
+    // viewmat gradient: wave DPP reduction, then across the 4 waves in LDS, one atomic per entry
+    float red[12];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+#pragma unroll
+        for (int b = 0; b < 3; ++b) red[4 * a + b] = vR[3 * a + b];
+        red[4 * a + 3] = vt[a];
+    }
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+        float v = wave_sum_to_lane63(red[k]);
+        if (lane == 63) s_red[wave][k] = v;
+    }
+    __syncthreads();
+    if (tid < 12) {
+        float v = ((s_red[0][tid] + s_red[1][tid]) + s_red[2][tid]) + s_red[3][tid];
+        atomicAdd(P.v_viewmat + (int64_t)image_id * 16 + tid, v);
+    }
+    // Transform gradient: uniform block -> block reduction; mixed -> per-thread atomics
+    // (splax/_project/_kernels.py:461-484).
+    if (P.has_transforms) {
+        int32_t id = in_range ? tf_id : -1;
+        int32_t tmin = block_min_i32(in_range ? tf_id : 2147483647, s_tf);
+        int32_t tmax = block_max_i32(in_range ? tf_id : (-2147483647 - 1), s_tf);
+        (void)id;
+        if (tmin == tmax && tmin >= 0) {
+            __syncthreads();
+            float rt[12];
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+#pragma unroll
+                for (int b = 0; b < 3; ++b) rt[4 * a + b] = vRtf[3 * a + b];
+                rt[4 * a + 3] = vttf[a];
+            }
+#pragma unroll
+            for (int k = 0; k < 12; ++k) {
+                float v = wave_sum_to_lane63(rt[k]);
+                if (lane == 63) s_red[wave][k] = v;
+            }
+            __syncthreads();
+            if (tid < 12) {
+                float v = ((s_red[0][tid] + s_red[1][tid]) + s_red[2][tid]) + s_red[3][tid];
+                int64_t slot = (int64_t)image_id * P.num_transforms + tmin;
+                atomicAdd(P.v_transforms + slot * 16 + tid, v);
+            }
+        } else if (moved && tmin != tmax) {
+            int64_t slot = (int64_t)image_id * P.num_transforms + tf_id;
+            float* dst = P.v_transforms + slot * 16;
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+#pragma unroll
+                for (int b = 0; b < 3; ++b) atomicAdd(dst + 4 * a + b, vRtf[3 * a + b]);
+                atomicAdd(dst + 4 * a + 3, vttf[a]);
+            }
+        }
+    }
+}
+
+int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stream) {
+    if (a.total <= 0) return 0;
+    const int64_t per_block = (int64_t)kProjThreads * kProjItems;
+    const int64_t blocks = (a.total + per_block - 1) / per_block;
+    if (blocks > (int64_t)sc.scan_status_cap) {
+        int rc = sc.grow_scan_status(blocks);
+        if (rc) return rc;
+    }
+    ProjectParams P;
+    P.means = a.means; P.rows_means = a.rows_means;
+    P.scales = a.scales; P.rows_scales = a.rows_scales;
+    P.quats = a.quats; P.rows_quats = a.rows_quats;
+    P.viewmat = a.viewmat; P.rows_viewmat = a.rows_viewmat;
+    P.opac = a.opacities; P.rows_opac = a.rows_opac;
+    P.transforms = a.transforms; P.rows_transforms = a.rows_transforms;
+    P.transform_ids = a.transform_ids;
+    P.n = a.n; P.num_transforms = a.num_transforms; P.has_transforms = a.has_transforms;
+    P.total = a.total; P.img_h = a.img_h; P.img_w = a.img_w;
+    P.fx = a.fx; P.fy = a.fy; P.cx = a.cx; P.cy = a.cy;
+    P.glob_scale = a.glob_scale; P.clip_thresh = a.clip_thresh;
+    P.xys = a.xys; P.depths = a.depths; P.radii = a.radii; P.conics = a.conics;
+    P.num_tiles_hit = a.num_tiles_hit; P.cum_tiles_hit = a.cum_tiles_hit;
+    P.status = sc.scan_status; P.ticket = sc.tickets + kTicketScan; P.epoch = sc.next_epoch();
+    P.err = sc.tickets + kDeviceError;
+    hipLaunchKernelGGL(project_fwd_kernel, dim3((unsigned)blocks), dim3(kProjThreads), 0, stream,
+                       P);
+    return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
+}
+
+int launch_project_bwd(const ProjectBwdArgs& a, hipStream_t stream) {
+    const int32_t blocks_per_image = (a.n + kProjThreads - 1) / kProjThreads;
+    // zero the reduction targets (per-item outputs are fully written by the kernel)
+    int64_t nview = (int64_t)a.B * 16;
+    int64_t ntf = (int64_t)a.B * a.num_transforms * 16;
+    int rc = fill_zero_f32(a.v_viewmat, nview, stream);
+    if (rc) return rc;
+    if (a.v_transforms && ntf > 0) {
+        rc = fill_zero_f32(a.v_transforms, ntf, stream);
+        if (rc) return rc;
+    }
+    if (a.n <= 0 || a.B <= 0) return 0;
+    ProjectBwdParams P;
+    P.means = a.means; P.rows_means = a.rows_means;
+    P.scales = a.scales; P.rows_scales = a.rows_scales;
+    P.quats = a.quats; P.rows_quats = a.rows_quats;
+    P.viewmat = a.viewmat; P.rows_viewmat = a.rows_viewmat;
+    P.radii = a.radii; P.rows_radii = a.rows_radii;
+    P.conics = a.conics; P.rows_conics = a.rows_conics;
+    P.v_xy = a.v_xy; P.rows_vxy = a.rows_vxy;
+    P.v_depth = a.v_depth; P.rows_vdepth = a.rows_vdepth;
+    P.v_conic = a.v_conic; P.rows_vconic = a.rows_vconic;
+    P.transforms = a.transforms; P.rows_transforms = a.rows_transforms;
+    P.transform_ids = a.transform_ids;
+    P.n = a.n; P.num_transforms = a.num_transforms; P.has_transforms = a.has_transforms;
+    P.B = a.B; P.blocks_per_image = blocks_per_image;
+    P.fx = a.fx; P.fy = a.fy; P.glob_scale = a.glob_scale;
+    P.v_mean3d = a.v_mean3d; P.v_scale = a.v_scale; P.v_quat = a.v_quat;
+    P.v_viewmat = a.v_viewmat; P.v_transforms = a.v_transforms;
+    int64_t blocks = (int64_t)a.B * blocks_per_image;
+    hipLaunchKernelGGL(project_bwd_kernel, dim3((unsigned)blocks), dim3(kProjThreads), 0, stream,
+                       P);
+    return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
+}
+
+}  // namespace splat

@@ -1,0 +1,483 @@
+// sort_and_bin on gfx950: per-image depth range, packed-key emission, a stable onesweep LSD radix
+// sort, and tile bin edges. Restates splax/_rasterize/_sort/_sort.py:29-171 and
+// splax/_rasterize/_sort/_kernels.py:28-153,214-241; the sort replaces warp-lang's
+// radix_sort_pairs (called at splax/_rasterize/_sort/_sort.py:136).
+//
+// Sort design: one global histogram launch counts all four 8-bit digits of every key; then each
+// of the four passes is a single launch in which a workgroup (4 wave64s) takes a 4096-key
+// partition by atomic ticket, ranks its keys stably with ballot-based digit matching per wave,
+// publishes its per-digit counts and resolves its global per-digit offsets by decoupled look-back
+// over the partitions before it, and scatters keys and values through LDS so that each digit's
+// run is written contiguously. Ranking follows position order (wave-striped items, lanes in order,
+// waves in order, partitions in ticket order), so the sort is stable: ties keep emission order,
+// which is the reference's (key, position) order.
+#include "splat_common.hpp"
+#include "splat_internal.hpp"
+
+namespace splat {
+
+// ------------------------------------------------------------------ depth range
+// _depth_minmax, splax/_rasterize/_sort/_kernels.py:38-73: per-image [dmin, dmax] over items with
+// radii > 0. Stage 1 writes one partial per workgroup; stage 2 (one workgroup per image) folds
+// them. Floats are mapped to order-preserving unsigned integers for the reductions.
+
+constexpr int kMmThreads = 256;
+constexpr int kMmItems = 16;
+
+__device__ __forceinline__ uint32_t f2ord(float f) {
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float ord2f(uint32_t u) {
+    return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+
+__global__ void __launch_bounds__(kMmThreads)
+minmax_partial_kernel(const float* depths, const int32_t* radii, int32_t n,
+                      int32_t blocks_per_image, uint32_t* partial) {
+    __shared__ uint32_t s_lo[kMmThreads / 64], s_hi[kMmThreads / 64];
+    const int image = blockIdx.y;
+    const int64_t base = (int64_t)image * n + (int64_t)blockIdx.x * (kMmThreads * kMmItems);
+    const int64_t end = (int64_t)image * n + n;
+    uint32_t lo = 0xffffffffu, hi = 0u;
+#pragma unroll
+    for (int k = 0; k < kMmItems; ++k) {
+        int64_t idx = base + (int64_t)k * kMmThreads + threadIdx.x;
+        if (idx < end && radii[idx] > 0) {
+            uint32_t o = f2ord(depths[idx]);
+            lo = o < lo ? o : lo;
+            hi = o > hi ? o : hi;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        uint32_t a = __shfl_xor(lo, off, 64), b = __shfl_xor(hi, off, 64);
+        lo = a < lo ? a : lo;
+        hi = b > hi ? b : hi;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        s_lo[wave] = lo;
+        s_hi[wave] = hi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kMmThreads / 64; ++w) {
+            lo = s_lo[w] < lo ? s_lo[w] : lo;
+            hi = s_hi[w] > hi ? s_hi[w] : hi;
+        }
+        int64_t slot = (int64_t)image * blocks_per_image + blockIdx.x;
+        partial[2 * slot] = lo;
+        partial[2 * slot + 1] = hi;
+    }
+}
+
+// Stage 2; also clears the sort's digit histogram (4 x 256) for the histogram launch.
+__global__ void __launch_bounds__(kMmThreads)
+minmax_final_kernel(const uint32_t* partial, int32_t blocks_per_image, float* mm,
+                    uint32_t* hist) {
+    __shared__ uint32_t s_lo[kMmThreads / 64], s_hi[kMmThreads / 64];
+    const int image = blockIdx.x;
+    if (image == 0)
+        for (int i = threadIdx.x; i < 4 * 256; i += kMmThreads) hist[i] = 0u;
+    uint32_t lo = 0xffffffffu, hi = 0u;
+    for (int b = threadIdx.x; b < blocks_per_image; b += kMmThreads) {
+        int64_t slot = (int64_t)image * blocks_per_image + b;
+        uint32_t a = partial[2 * slot], c = partial[2 * slot + 1];
+        lo = a < lo ? a : lo;
+        hi = c > hi ? c : hi;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        uint32_t a = __shfl_xor(lo, off, 64), c = __shfl_xor(hi, off, 64);
+        lo = a < lo ? a : lo;
+        hi = c > hi ? c : hi;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        s_lo[wave] = lo;
+        s_hi[wave] = hi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kMmThreads / 64; ++w) {
+            lo = s_lo[w] < lo ? s_lo[w] : lo;
+            hi = s_hi[w] > hi ? s_hi[w] : hi;
+        }
+        // no visible item: the reference's +-1e30 seeds remain (drange < 0 -> depth_q = 0)
+        mm[2 * image] = hi == 0u ? 1.0e30f : ord2f(lo);
+        mm[2 * image + 1] = hi == 0u ? -1.0e30f : ord2f(hi);
+    }
+}
+
+// ------------------------------------------------------------------ key emission
+// _map_intersects_32bit, splax/_rasterize/_sort/_kernels.py:76-153
+
+struct EmitParams {
+    const float* xys; const float* depths; const int32_t* radii; const float* conics;
+    const float* map_opac; int64_t rows_map_opac;
+    const int32_t* cum; const float* mm;
+    int32_t n; int64_t total; int64_t M;
+    int32_t tiles_x, tiles_y, tile_bits, depth_bits;
+    int32_t* keys; int32_t* vals;
+};
+
+__global__ void __launch_bounds__(256) emit_keys_kernel(EmitParams P) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= P.total) return;
+    if (P.radii[idx] <= 0) return;
+    const int32_t bid = (int32_t)(idx / P.n);
+    int64_t cur = idx > 0 ? P.cum[idx - 1] : 0;
+    // a consistent (radii, conics, cum) never leaves [0, M); inconsistent inputs stop here
+    if (cur < 0) return;
+    const float dmin = P.mm[2 * bid];
+    const float drange = P.mm[2 * bid + 1] - dmin;
+    const int32_t qmax = (1 << P.depth_bits) - 1;
+    const float maxq = (float)qmax;
+    int32_t dq = 0;
+    if (drange > 0.0f) {
+        float f = (P.depths[idx] - dmin) / drange;
+        dq = iminw(imaxw(f2i(f * maxq), 0), qmax);
+    }
+    const int32_t iid_enc = (int32_t)((uint32_t)bid << (P.depth_bits + P.tile_bits));
+    const float opac = P.map_opac[idx % P.rows_map_opac];
+    const float t = iso_level(opac);
+    const float2 c = reinterpret_cast<const float2*>(P.xys)[idx];
+    Ellipse e = ellipse_init(P.conics[3 * idx], P.conics[3 * idx + 1], P.conics[3 * idx + 2], t,
+                             c.x, c.y, P.tiles_x, P.tiles_y);
+    if (!e.valid) return;
+    float I0, I1;
+    ellipse_init_span(e, I0, I1);
+    for (int32_t u = e.rmin0; u < e.rmax0; ++u) {
+        int32_t mn, mx;
+        ellipse_column(e, u, I0, I1, mn, mx);
+        for (int32_t v = mn; v < mx; ++v) {
+            if (cur >= P.M) return;
+            int32_t tile_id = e.isY ? u * P.tiles_x + v : v * P.tiles_x + u;
+            P.keys[cur] = iid_enc | (tile_id << P.depth_bits) | dq;
+            P.vals[cur] = (int32_t)idx;
+            ++cur;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ digit histogram
+
+constexpr int kHistThreads = 256;
+
+__global__ void __launch_bounds__(kHistThreads)
+digit_hist_kernel(const int32_t* keys, int64_t M, uint32_t* hist, int32_t* bins, int64_t nbins2) {
+    __shared__ uint32_t s_h[kHistThreads / 64][4 * 256];
+    const int tid = threadIdx.x, wave = tid >> 6;
+    for (int i = tid; i < 4 * 256; i += kHistThreads)
+#pragma unroll
+        for (int w = 0; w < kHistThreads / 64; ++w) s_h[w][i] = 0u;
+    // tile bins start at (0, 0): the bin-edge launch writes only tiles that own intersections
+    for (int64_t i = (int64_t)blockIdx.x * kHistThreads + tid; i < nbins2;
+         i += (int64_t)gridDim.x * kHistThreads)
+        bins[i] = 0;
+    __syncthreads();
+    for (int64_t i = (int64_t)blockIdx.x * kHistThreads + tid; i < M;
+         i += (int64_t)gridDim.x * kHistThreads) {
+        uint32_t k = (uint32_t)keys[i];
+        atomicAdd(&s_h[wave][k & 255u], 1u);
+        atomicAdd(&s_h[wave][256 + ((k >> 8) & 255u)], 1u);
+        atomicAdd(&s_h[wave][512 + ((k >> 16) & 255u)], 1u);
+        atomicAdd(&s_h[wave][768 + (k >> 24)], 1u);
+    }
+    __syncthreads();
+    for (int i = tid; i < 4 * 256; i += kHistThreads) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int w = 0; w < kHistThreads / 64; ++w) v += s_h[w][i];
+        if (v) atomicAdd(hist + i, v);
+    }
+}
+
+// ------------------------------------------------------------------ onesweep pass
+
+constexpr int kSortThreads = 256;
+constexpr int kSortWaves = kSortThreads / 64;
+constexpr int kSortItems = 16;
+constexpr int kSortTile = kSortThreads * kSortItems;
+
+// Exclusive scan of one value per thread over a 256-thread workgroup.
+__device__ __forceinline__ uint32_t block_exclusive_scan_256(uint32_t v, uint32_t* s_tmp,
+                                                             uint32_t* total) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t incl = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        uint32_t o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
+    }
+    if (lane == 63) s_tmp[wave] = incl;
+    __syncthreads();
+    uint32_t off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) {
+        uint32_t x = s_tmp[w];
+        if (w < wave) off += x;
+        tot += x;
+    }
+    if (total) *total = tot;
+    __syncthreads();
+    return off + incl - v;
+}
+
+__global__ void __launch_bounds__(kSortThreads)
+onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
+                     int32_t* __restrict__ keys_out, int32_t* __restrict__ vals_out, int64_t M,
+                     int shift, const uint32_t* __restrict__ hist, uint64_t* status,
+                     uint32_t* ticket, uint32_t epoch, uint32_t* err) {
+    __shared__ uint32_t s_buf[kSortTile];
+    __shared__ uint32_t s_cnt[kSortWaves][256];
+    __shared__ uint32_t s_local_start[256];
+    __shared__ int64_t s_dest_base[256];
+    __shared__ uint32_t s_tmp[kSortWaves];
+    __shared__ uint32_t s_part;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) s_part = atomicAdd(ticket, 1u);
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) s_cnt[w][tid] = 0u;
+    __syncthreads();
+    const uint32_t part = s_part;
+    if (tid == 0 && part == gridDim.x - 1) atomic_store_relaxed(ticket, 0u);
+    const int64_t base = (int64_t)part * kSortTile;
+    const int64_t wbase = base + (int64_t)wave * (kSortItems * 64);
+
+    uint32_t key[kSortItems];
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+        int64_t pos = wbase + i * 64 + lane;
+        key[i] = pos < M ? (uint32_t)keys_in[pos] : 0xffffffffu;
+    }
+
+    // stable per-wave ranking: lanes with equal digits found by 8 ballots
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    uint32_t rank[kSortItems];
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+        const uint32_t d = (key[i] >> shift) & 255u;
+        uint64_t peers = ~0ull;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const bool bit = (d >> b) & 1u;
+            const uint64_t bal = __ballot(bit);
+            peers &= bit ? bal : ~bal;
+        }
+        const uint32_t below = (uint32_t)__popcll(peers & lt_mask);
+        const uint32_t old = s_cnt[wave][d];
+        rank[i] = old + below;
+        if (below == 0) s_cnt[wave][d] = old + (uint32_t)__popcll(peers);
+    }
+    __syncthreads();
+
+    // per digit (thread = digit): wave offsets, local digit starts, look-back
+    const uint32_t d = (uint32_t)tid;
+    uint32_t c[kSortWaves];
+    uint32_t tot = 0;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) {
+        c[w] = s_cnt[w][d];
+        tot += c[w];
+    }
+    uint32_t run = 0;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) {
+        s_cnt[w][d] = run;
+        run += c[w];
+    }
+    const uint32_t local_start = block_exclusive_scan_256(tot, s_tmp, nullptr);
+    const uint32_t global_start = block_exclusive_scan_256(hist[d], s_tmp, nullptr);
+    s_local_start[d] = local_start;
+    // decoupled look-back for digit d
+    uint64_t* st = status + d;
+    uint32_t prefix = 0;
+    if (part == 0) {
+        atomic_store_relaxed(st, status_word(epoch, true, tot));
+    } else {
+        atomic_store_relaxed(st + (int64_t)part * 256, status_word(epoch, false, tot));
+        int64_t j = (int64_t)part - 1;
+        while (j >= 0) {
+            uint64_t s = wait_status(st + j * 256, epoch, err);
+            prefix += (uint32_t)(s & 0x7fffffffull);
+            if (s & kInclusiveBit) break;
+            --j;
+        }
+        atomic_store_relaxed(st + (int64_t)part * 256, status_word(epoch, true, prefix + tot));
+    }
+    s_dest_base[d] = (int64_t)global_start + prefix - local_start;
+    __syncthreads();
+
+    // keys into LDS at their partition-sorted slot
+    uint32_t slot[kSortItems];
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+        const uint32_t dd = (key[i] >> shift) & 255u;
+        slot[i] = s_local_start[dd] + s_cnt[wave][dd] + rank[i];
+        s_buf[slot[i]] = key[i];
+    }
+    __syncthreads();
+    const int64_t valid = (M - base) < kSortTile ? (M - base) : kSortTile;
+    int64_t dest[kSortItems];
+#pragma unroll
+    for (int r = 0; r < kSortItems; ++r) {
+        const int j = r * kSortThreads + tid;
+        const uint32_t k = s_buf[j];
+        dest[r] = s_dest_base[(k >> shift) & 255u] + j;
+        if (j < valid) keys_out[dest[r]] = (int32_t)k;
+    }
+    __syncthreads();
+    // values through the same permutation
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+        int64_t pos = wbase + i * 64 + lane;
+        s_buf[slot[i]] = pos < M ? (uint32_t)vals_in[pos] : 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kSortItems; ++r) {
+        const int j = r * kSortThreads + tid;
+        if (j < valid) vals_out[dest[r]] = (int32_t)s_buf[j];
+    }
+}
+
+// ------------------------------------------------------------------ bin edges
+// _tile_bin_edges_32bit, splax/_rasterize/_sort/_kernels.py:214-241 (including its M == 1
+// behaviour: index 0 writes only the start, so a lone bin stays [0, 0)).
+
+__global__ void __launch_bounds__(256)
+bin_edges_kernel(const int32_t* keys, int64_t M, int32_t num_tiles, int32_t tile_bits,
+                 int32_t depth_bits, int32_t* bins) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= M) return;
+    const int32_t mask = (1 << tile_bits) - 1;
+    const int32_t key = keys[idx] >> depth_bits;
+    const int32_t cur = (key >> tile_bits) * num_tiles + (key & mask);
+    if (idx == 0) {
+        bins[2 * cur] = 0;
+        return;
+    }
+    if (idx == M - 1) bins[2 * cur + 1] = (int32_t)M;
+    const int32_t kp = keys[idx - 1] >> depth_bits;
+    const int32_t prev = (kp >> tile_bits) * num_tiles + (kp & mask);
+    if (prev != cur) {
+        bins[2 * prev + 1] = (int32_t)idx;
+        bins[2 * cur] = (int32_t)idx;
+    }
+}
+
+// ------------------------------------------------------------------ orchestration
+
+KeyLayout key_layout(int32_t B, int32_t img_h, int32_t img_w) {
+    KeyLayout L;
+    L.tiles_x = (img_w + kBlockWidth - 1) / kBlockWidth;
+    L.tiles_y = (img_h + kBlockWidth - 1) / kBlockWidth;
+    L.num_tiles = L.tiles_x * L.tiles_y;
+    auto bit_length = [](int64_t v) {
+        int b = 0;
+        while (v > 0) {
+            ++b;
+            v >>= 1;
+        }
+        return b;
+    };
+    L.tile_bits = bit_length((int64_t)L.num_tiles - 1);
+    L.image_bits = bit_length((int64_t)B - 1);
+    L.depth_bits = 31 - L.image_bits - L.tile_bits;
+    L.packed = L.depth_bits >= 16;
+    return L;
+}
+
+int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stream,
+                     int64_t* M_out, KeyLayout* lay_out) {
+    const int32_t B = in.B_geom;
+    const KeyLayout L = key_layout(B, in.img_h, in.img_w);
+    *lay_out = L;
+    if (!L.packed) {
+        return fail(kErrKeyOverflow,
+                    "intersection key does not pack into 32 bits: image_n_bits(" +
+                        std::to_string(L.image_bits) + ") + tile_n_bits(" +
+                        std::to_string(L.tile_bits) + ") leaves " + std::to_string(L.depth_bits) +
+                        " < 16 depth bits (batch B=" + std::to_string(B) +
+                        ", n_tiles=" + std::to_string(L.num_tiles) +
+                        "); the 64-bit key path is not built yet. Reduce batch size or resolution.");
+    }
+    const int64_t total = (int64_t)B * in.n;
+    const int64_t nbins = (int64_t)B * L.num_tiles;
+    int rc = sc.ensure_sort(0, nbins, B);
+    if (rc) return rc;
+    if (total <= 0) {
+        *M_out = 0;
+        return fill_zero_i32(sc.tile_bins, 2 * nbins, stream);
+    }
+    // The one device-to-host read: the intersection count. The copy is enqueued first; the depth
+    // range launches run while the host waits (splax/_rasterize/_sort/_sort.py:71-96).
+    if (hipMemcpyAsync(sc.pinned_count, in.cum + (total - 1), sizeof(int32_t),
+                       hipMemcpyDeviceToHost, stream) != hipSuccess ||
+        hipEventRecord(sc.count_event, stream) != hipSuccess)
+        return fail(kErrRuntime, "count readback enqueue failed");
+    const int32_t bpi = (int32_t)((in.n + kMmThreads * kMmItems - 1) / (kMmThreads * kMmItems));
+    if ((int64_t)bpi * B * 2 > sc.mm_partial_cap)
+        return fail(kErrRuntime, "depth-range partials not allocated");
+    {
+        StageTimer tm(stream, kStageMinmax);
+        hipLaunchKernelGGL(minmax_partial_kernel, dim3(bpi, B), dim3(kMmThreads), 0, stream,
+                           in.depths, in.radii, in.n, bpi, sc.mm_partial);
+        hipLaunchKernelGGL(minmax_final_kernel, dim3(B), dim3(kMmThreads), 0, stream,
+                           sc.mm_partial, bpi, sc.depth_mm, sc.hist);
+        if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "minmax launch failed");
+    }
+    if (hipEventSynchronize(sc.count_event) != hipSuccess)
+        return fail(kErrRuntime, "count readback failed");
+    const int64_t M = *sc.pinned_count;
+    if (M < 0) return fail(kErrTooMany, "intersection count overflowed int32");
+    *M_out = M;
+    rc = sc.ensure_sort(M, nbins, B);
+    if (rc) return rc;
+    if (M == 0) return fill_zero_i32(sc.tile_bins, 2 * nbins, stream);
+
+    {
+        StageTimer tm(stream, kStageEmit);
+        EmitParams E;
+        E.xys = in.xys; E.depths = in.depths; E.radii = in.radii; E.conics = in.conics;
+        E.map_opac = in.map_opac; E.rows_map_opac = in.rows_map_opac;
+        E.cum = in.cum; E.mm = sc.depth_mm; E.n = in.n; E.total = total; E.M = M;
+        E.tiles_x = L.tiles_x; E.tiles_y = L.tiles_y; E.tile_bits = L.tile_bits;
+        E.depth_bits = L.depth_bits; E.keys = sc.keys[0]; E.vals = sc.vals[0];
+        hipLaunchKernelGGL(emit_keys_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                           stream, E);
+        if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "emit launch failed");
+    }
+    {
+        StageTimer tm(stream, kStageSort);
+        int64_t hb = (M + kHistThreads * 16 - 1) / (kHistThreads * 16);
+        if (hb > 2048) hb = 2048;
+        if (hb < 1) hb = 1;
+        hipLaunchKernelGGL(digit_hist_kernel, dim3((unsigned)hb), dim3(kHistThreads), 0, stream,
+                           sc.keys[0], M, sc.hist, sc.tile_bins, 2 * nbins);
+        const int64_t parts = (M + kSortTile - 1) / kSortTile;
+        // passes 0..3 ping-pong 0 -> 1 -> 0 -> 1 -> 0 so the result lands back in buffer 0
+        for (int pass = 0; pass < 4; ++pass) {
+            const int src = pass & 1, dst = 1 - src;
+            hipLaunchKernelGGL(onesweep_pass_kernel, dim3((unsigned)parts), dim3(kSortThreads), 0,
+                               stream, sc.keys[src], sc.vals[src], sc.keys[dst], sc.vals[dst], M,
+                               8 * pass, sc.hist + 256 * pass, sc.sort_status,
+                               sc.tickets + kTicketSort + pass, sc.next_epoch(),
+                               sc.tickets + kDeviceError);
+        }
+        if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "sort launch failed");
+    }
+    {
+        StageTimer tm(stream, kStageBins);
+        hipLaunchKernelGGL(bin_edges_kernel, dim3((unsigned)((M + 255) / 256)), dim3(256), 0,
+                           stream, sc.keys[0], M, L.num_tiles, L.tile_bits, L.depth_bits,
+                           sc.tile_bins);
+        if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "bins launch failed");
+    }
+    return 0;
+}
+
+}  // namespace splat

@@ -1,0 +1,253 @@
+// Internal interfaces of the gfx950 splat library: argument bundles, the per-device scratch
+// cache, error codes and device-side scan / look-back helpers shared by the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace splat {
+
+// ------------------------------------------------------------------ error codes
+enum : int {
+    kOk = 0,
+    kErrArgs = 1,         // invalid shapes / arguments (reference raises ValueError)
+    kErrKeyOverflow = 2,  // image and tile ids do not fit the 32-bit key
+    kErrAlloc = 3,
+    kErrLaunch = 4,
+    kErrRuntime = 5,
+    kErrTooMany = 6,      // intersection count beyond the int32 / 2^31 range
+};
+
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+
+// ------------------------------------------------------------------ argument bundles
+struct ProjectArgs {
+    const float* means; int64_t rows_means;
+    const float* scales; int64_t rows_scales;
+    const float* quats; int64_t rows_quats;
+    const float* viewmat; int64_t rows_viewmat;
+    const float* opacities; int64_t rows_opac;
+    const float* transforms; int64_t rows_transforms;
+    const int32_t* transform_ids;
+    int32_t n, num_transforms, has_transforms;
+    int64_t total;
+    int32_t img_h, img_w;
+    float fx, fy, cx, cy, glob_scale, clip_thresh;
+    float* xys; float* depths; int32_t* radii; float* conics;
+    int32_t* num_tiles_hit; int32_t* cum_tiles_hit;
+};
+
+struct ProjectBwdArgs {
+    const float* means; int64_t rows_means;
+    const float* scales; int64_t rows_scales;
+    const float* quats; int64_t rows_quats;
+    const float* viewmat; int64_t rows_viewmat;
+    const int32_t* radii; int64_t rows_radii;
+    const float* conics; int64_t rows_conics;
+    const float* v_xy; int64_t rows_vxy;
+    const float* v_depth; int64_t rows_vdepth;
+    const float* v_conic; int64_t rows_vconic;
+    const float* transforms; int64_t rows_transforms;
+    const int32_t* transform_ids;
+    int32_t n, num_transforms, has_transforms, B;
+    float fx, fy, glob_scale;
+    float* v_mean3d; float* v_scale; float* v_quat; float* v_viewmat; float* v_transforms;
+};
+
+// Geometry of one sort_and_bin call (splax/_rasterize/_sort/_sort.py:51-60).
+struct KeyLayout {
+    int32_t tiles_x, tiles_y, num_tiles, tile_bits, image_bits, depth_bits;
+    bool packed;
+};
+KeyLayout key_layout(int32_t B, int32_t img_h, int32_t img_w);
+
+// Inputs of sort_and_bin and the blends.
+struct RasterInputs {
+    const float* colors; int64_t rows_colors;
+    const float* opac; int64_t rows_opac;
+    const float* map_opac; int64_t rows_map_opac;
+    const float* background; int64_t rows_bg;
+    const float* xys; const float* depths; const int32_t* radii; const float* conics;
+    const int32_t* cum;
+    int32_t n, B_geom, img_h, img_w;
+};
+
+// ------------------------------------------------------------------ tickets / scratch
+enum : int {
+    kTicketScan = 0,
+    kTicketSort = 40,    // + pass index (4)
+    kDeviceError = 63,   // device error word (bit flags, see kDevErr*)
+    kNumTickets = 64,
+};
+
+// Grow-only per-device scratch, the counterpart of splax/_cache.py:52-90. The intersection
+// buffers grow with 1.25x headroom; everything is freed by splat_clear_cache().
+struct DeviceScratch {
+    int device = -1;
+    std::mutex mu;
+    uint32_t epoch = 0;
+    // projection scan
+    uint64_t* scan_status = nullptr; int64_t scan_status_cap = 0;
+    uint32_t* tickets = nullptr;
+    // sort
+    int32_t* keys[2] = {nullptr, nullptr};
+    int32_t* vals[2] = {nullptr, nullptr};
+    int64_t isect_cap = 0;
+    uint64_t* sort_status = nullptr; int64_t sort_status_cap = 0;  // partitions * 256
+    uint32_t* hist = nullptr;                                       // 4 * 256
+    int32_t* tile_bins = nullptr; int64_t bins_cap = 0;             // (start, end) pairs
+    float* depth_mm = nullptr; int64_t mm_cap = 0;                  // 2 * B
+    uint32_t* mm_partial = nullptr; int64_t mm_partial_cap = 0;     // 2 * blocks
+    int32_t* pinned_count = nullptr;
+    hipEvent_t count_event = nullptr;
+
+    uint32_t next_epoch() {
+        ++epoch;
+        if (epoch == 0) epoch = 1;
+        return epoch;
+    }
+    int ensure_base();
+    int grow_scan_status(int64_t blocks);
+    int ensure_sort(int64_t M, int64_t bins, int32_t B);
+    void release();
+};
+
+DeviceScratch& scratch_for_current_device();
+void release_all_scratch();
+
+// ------------------------------------------------------------------ stage timing
+enum Stage : int {
+    kStageProject = 0,
+    kStageMinmax,
+    kStageEmit,
+    kStageSort,
+    kStageBins,
+    kStageBlendFwd,
+    kStageBlendBwd,
+    kStageProjectBwd,
+    kNumStages
+};
+struct StageTimer {
+    hipStream_t stream;
+    int stage;
+    hipEvent_t start = nullptr;
+    StageTimer(hipStream_t s, int st);
+    ~StageTimer();
+};
+
+// ------------------------------------------------------------------ launchers
+int fill_zero_f32(float* p, int64_t n, hipStream_t stream);
+int fill_zero_i32(int32_t* p, int64_t n, hipStream_t stream);
+int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stream);
+int launch_project_bwd(const ProjectBwdArgs& a, hipStream_t stream);
+
+// sort_and_bin: returns M (>= 0) in *M_out; sorted ids in sc.vals[0], keys in sc.keys[0],
+// tile bins in sc.tile_bins.
+int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stream,
+                     int64_t* M_out, KeyLayout* lay_out);
+
+int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
+                     const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,
+                     float* out_img, hipStream_t stream);
+
+struct BlendBwdArgs {
+    const float* final_Ts; const int32_t* final_idx;
+    const float* v_out; int64_t vout_rows;
+    int32_t B_out;
+    float* v_colors; float* v_opacity; float* v_xy; float* v_conic;
+};
+int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
+                     const int32_t* tile_bins, const BlendBwdArgs& a, hipStream_t stream);
+
+// ------------------------------------------------------------------ device helpers
+
+template <typename T>
+__device__ __forceinline__ void atomic_store_relaxed(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T atomic_load_relaxed(const T* p) {
+    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Status words of the decoupled look-back: bits 63..32 epoch of the launch that wrote them,
+// bit 31 set when the value is an inclusive prefix (else the chunk's own aggregate),
+// bits 30..0 the value. A word from another launch has a different epoch and reads as "not yet
+// published", so the arrays never need clearing between launches.
+constexpr uint64_t kInclusiveBit = 0x80000000ull;
+
+__device__ __forceinline__ uint64_t status_word(uint32_t epoch, bool inclusive, uint32_t v) {
+    return ((uint64_t)epoch << 32) | (inclusive ? kInclusiveBit : 0ull) | (uint64_t)v;
+}
+
+// Every spin-wait is bounded: a predecessor that has not published after this many polls means
+// a broken invariant (never expected); the waiter records it in the device error word and
+// proceeds, so the kernel always terminates. splat_check_device() reports the word.
+constexpr uint32_t kSpinLimit = 1u << 22;
+enum : uint32_t { kDevErrLookback = 1u };
+
+// Polls status[j] until it carries `epoch`; returns the word, or 0 on timeout (error recorded).
+__device__ __forceinline__ uint64_t wait_status(const uint64_t* p, uint32_t epoch, uint32_t* err) {
+    for (uint32_t spin = 0; spin < kSpinLimit; ++spin) {
+        uint64_t s = atomic_load_relaxed(p);
+        if ((uint32_t)(s >> 32) == epoch) return s;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    atomicOr(err, kDevErrLookback);
+    return kInclusiveBit;  // treat as an inclusive prefix of 0 so the walk ends
+}
+
+// Single-value decoupled look-back (one thread). Publishes this chunk's aggregate, walks back
+// to the nearest inclusive prefix and publishes its own; returns the exclusive prefix.
+__device__ __forceinline__ uint32_t lookback_single(uint64_t* status, uint32_t part, uint32_t agg,
+                                                    uint32_t epoch, uint32_t* err) {
+    if (part == 0) {
+        atomic_store_relaxed(status, status_word(epoch, true, agg));
+        return 0;
+    }
+    atomic_store_relaxed(status + part, status_word(epoch, false, agg));
+    uint32_t prefix = 0;
+    int64_t j = (int64_t)part - 1;
+    while (j >= 0) {
+        uint64_t s = wait_status(status + j, epoch, err);
+        prefix += (uint32_t)(s & 0x7fffffffull);
+        if (s & kInclusiveBit) break;
+        --j;
+    }
+    atomic_store_relaxed(status + part, status_word(epoch, true, prefix + agg));
+    return prefix;
+}
+
+__device__ __forceinline__ int32_t wave_inclusive_scan_i32(int32_t v, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        int32_t o = __shfl_up(v, off, 64);
+        if (lane >= off) v += o;
+    }
+    return v;
+}
+
+// Block-wide min / max of one int32 per thread; `tmp` is LDS of >= 2 ints. All threads call.
+__device__ __forceinline__ int32_t block_min_i32(int32_t v, int32_t* tmp) {
+    __syncthreads();
+    if (threadIdx.x == 0) tmp[0] = 2147483647;
+    __syncthreads();
+    atomicMin(tmp, v);
+    __syncthreads();
+    return tmp[0];
+}
+__device__ __forceinline__ int32_t block_max_i32(int32_t v, int32_t* tmp) {
+    __syncthreads();
+    if (threadIdx.x == 0) tmp[1] = (-2147483647 - 1);
+    __syncthreads();
+    atomicMax(tmp + 1, v);
+    __syncthreads();
+    return tmp[1];
+}
+
+}  // namespace splat

@@ -1,0 +1,241 @@
+"""GPU parity: the gfx950 library (through its C ABI) against the CPU oracle on identical inputs.
+
+Bars: projection outputs, intersection keys, sorted order, tile ranges,
+final_Ts / final_idx and the forward image are bit-exact (both sides follow one arithmetic
+contract); gradients that the GPU accumulates with float atomics are compared by relative
+Frobenius norm (< 1e-5) plus allclose(rtol=1e-4, atol=1e-6 * max|ref|); per-item projection
+gradients (no reduction) are bit-exact.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_bit_exact, random_scene, rel_fro
+from oracle import oracle as O
+from splax_amd import _ops
+from splax_amd.scenes import make_scene
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _device_healthy():
+    yield
+    from splax_amd import _lib
+
+    assert _lib.check_device() == 0, "a device-side invariant failed (look-back timeout)"
+
+
+def _t(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t if dtype is None else t.to(dtype)
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _project_both(means, scales, quats_wxyz, vm, opac, *, n, B, img_shape, f, c):
+    q = np.roll(quats_wxyz, -1, axis=-1)
+    ref = O.project_fwd(means, scales, q, vm, opac, n=n, total=B * n, img_shape=img_shape, f=f,
+                        c=c)
+    tf = torch.zeros((1, 4, 4), device="cuda")
+    ids = torch.full((1,), -1, device="cuda", dtype=torch.int32)
+    got = _ops.project_fwd(_t(means).reshape(-1, 3), _t(scales).reshape(-1, 3),
+                           _t(q).reshape(-1, 4), _t(vm).reshape(-1, 4), _t(opac).reshape(-1),
+                           tf, ids, n=n, total=B * n, num_transforms=1, has_transforms=False,
+                           img_shape=img_shape, f=f, c=c, glob_scale=1.0, clip_thresh=0.01)
+    torch.cuda.synchronize()
+    return ref, [_np(g) for g in got]
+
+
+CASES = {
+    "cfg0": lambda: make_scene(0),
+    "cfg1": lambda: make_scene(1),
+    "cfg2_50k": lambda: make_scene(2, n=50_000),
+}
+
+
+def _scene_arrays(name):
+    s = CASES[name]()
+    return s
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_project_fwd_bit_exact(name):
+    _case(f"project_fwd {name}")
+    s = _scene_arrays(name)
+    ref, got = _project_both(s.means, s.scales, s.quats, s.viewmats[0], s.opacities, n=s.n, B=1,
+                             img_shape=s.img_shape, f=s.f, c=s.c)
+    for label, r, g in zip(("xys", "depths", "radii", "conics", "num_tiles_hit", "cum"), ref,
+                           got):
+        assert_bit_exact(g.reshape(r.shape), r, f"{name}/{label}")
+    assert int(ref[5][-1]) > 0
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_sort_and_bin_bit_exact(name):
+    _case(f"sort_and_bin {name}")
+    s = _scene_arrays(name)
+    q = np.roll(s.quats, -1, axis=-1)
+    xys, depths, radii, conics, nth, cum = O.project_fwd(
+        s.means, s.scales, q, s.viewmats[0], s.opacities, n=s.n, total=s.n,
+        img_shape=s.img_shape, f=s.f, c=s.c)
+    rk, rid, rbins = O.sort_and_bin(xys, depths, radii, conics, s.opacities, cum, n=s.n, B=1,
+                                    img_shape=s.img_shape)
+    gk, gid, gbins = _ops.sort_and_bin(_t(xys), _t(depths), _t(radii), _t(conics),
+                                       _t(s.opacities).reshape(-1), _t(cum), n=s.n, B=1,
+                                       img_shape=s.img_shape)
+    torch.cuda.synchronize()
+    assert_bit_exact(_np(gk), rk, f"{name}/keys")
+    assert_bit_exact(_np(gid), rid, f"{name}/ids")
+    assert_bit_exact(_np(gbins), rbins, f"{name}/bins")
+
+
+def _raster_inputs(s):
+    q = np.roll(s.quats, -1, axis=-1)
+    proj = O.project_fwd(s.means, s.scales, q, s.viewmats[0], s.opacities, n=s.n, total=s.n,
+                         img_shape=s.img_shape, f=s.f, c=s.c)
+    return proj
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_rasterize_fwd_bit_exact(name):
+    _case(f"rasterize_fwd {name}")
+    s = _scene_arrays(name)
+    xys, depths, radii, conics, nth, cum = _raster_inputs(s)
+    rimg, rT, ridx, stats, M = O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background,
+                                               xys, depths, radii, conics, cum, n=s.n, B=1,
+                                               img_shape=s.img_shape)
+    gimg, gT, gidx, gM = _ops.rasterize_fwd(
+        _t(s.colors), _t(s.opacities).reshape(-1), _t(s.opacities).reshape(-1),
+        _t(s.background), _t(xys), _t(depths), _t(radii), _t(conics), _t(cum), n=s.n, B=1,
+        img_shape=s.img_shape)
+    torch.cuda.synchronize()
+    assert gM == M
+    assert_bit_exact(_np(gT), rT, f"{name}/final_Ts")
+    assert_bit_exact(_np(gidx), ridx, f"{name}/final_idx")
+    assert_bit_exact(_np(gimg), rimg, f"{name}/img")
+
+
+def _grad_compare(got, ref, label, rel_tol=1e-5):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    r = rel_fro(got, ref)
+    assert r < rel_tol, f"{label}: relative Frobenius error {r:.3e}"
+    scale = float(np.abs(ref).max()) + 1e-30
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-6 * scale, err_msg=label)
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_rasterize_bwd_matches_oracle(name):
+    _case(f"rasterize_bwd {name}")
+    s = _scene_arrays(name)
+    xys, depths, radii, conics, nth, cum = _raster_inputs(s)
+    rimg, rT, ridx, _, _ = O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background, xys,
+                                           depths, radii, conics, cum, n=s.n, B=1,
+                                           img_shape=s.img_shape)
+    H, W = s.img_shape
+    vout = (2.0 * (rimg.reshape(H, W, 3) - s.targets[0]) / rimg.size).astype(np.float32)
+    ref = O.rasterize_bwd(s.colors, s.opacities, s.opacities, s.background, xys, depths, radii,
+                          conics, cum, rT, ridx, vout, n=s.n, B_out=1, B_geom=1,
+                          img_shape=s.img_shape)
+    got = _ops.rasterize_bwd(_t(s.colors), _t(s.opacities).reshape(-1),
+                             _t(s.opacities).reshape(-1), _t(s.background), _t(xys), _t(depths),
+                             _t(radii), _t(conics), _t(cum), _t(rT), _t(ridx),
+                             _t(vout).reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
+                             img_shape=s.img_shape)
+    torch.cuda.synchronize()
+    for label, g, r in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), got, ref[:4]):
+        _grad_compare(_np(g).reshape(r.shape), r, f"{name}/{label}")
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_project_bwd_matches_oracle(name):
+    _case(f"project_bwd {name}")
+    s = _scene_arrays(name)
+    q = np.roll(s.quats, -1, axis=-1)
+    xys, depths, radii, conics, nth, cum = _raster_inputs(s)
+    rng = np.random.default_rng(5)
+    v_xy = rng.normal(size=(s.n, 2)).astype(np.float32)
+    v_depth = rng.normal(size=s.n).astype(np.float32)
+    v_conic = rng.normal(size=(s.n, 3)).astype(np.float32)
+    ref = O.project_bwd(s.means, s.scales, q, s.viewmats[0], radii, conics, v_xy, v_depth,
+                        v_conic, n=s.n, B=1, f=s.f)
+    tf = torch.zeros((1, 4, 4), device="cuda")
+    ids = torch.full((1,), -1, device="cuda", dtype=torch.int32)
+    got = _ops.project_bwd(_t(s.means), _t(s.scales), _t(q), _t(s.viewmats[0]), _t(radii),
+                           _t(conics), _t(v_xy), _t(v_depth), _t(v_conic), tf, ids, n=s.n, B=1,
+                           num_transforms=1, has_transforms=False, f=s.f, glob_scale=1.0)
+    torch.cuda.synchronize()
+    for label, g, r in zip(("v_mean3d", "v_scale", "v_quat"), got[:3], ref[:3]):
+        assert_bit_exact(_np(g).reshape(r.shape), r, f"{name}/{label}")
+    _grad_compare(_np(got[3]), ref[3], f"{name}/v_viewmat", rel_tol=1e-5)
+
+
+def test_batched_cameras_one_launch():
+    """Config-3-style orbit, B=16 cameras folded into the key (smaller N)."""
+    _case("batched B=16")
+    s = make_scene(3, n=40_000)
+    B, n = s.B, s.n
+    ref, got = _project_both(s.means, s.scales, s.quats, s.viewmats, s.opacities, n=n, B=B,
+                             img_shape=s.img_shape, f=s.f, c=s.c)
+    for label, r, g in zip(("xys", "depths", "radii", "conics", "nth", "cum"), ref, got):
+        assert_bit_exact(g.reshape(r.shape), r, f"batched/{label}")
+    xys, depths, radii, conics, nth, cum = ref
+    rk, rid, rbins = O.sort_and_bin(xys, depths, radii, conics, s.opacities, cum, n=n, B=B,
+                                    img_shape=s.img_shape)
+    gk, gid, gbins = _ops.sort_and_bin(_t(xys), _t(depths), _t(radii), _t(conics),
+                                       _t(s.opacities).reshape(-1), _t(cum), n=n, B=B,
+                                       img_shape=s.img_shape)
+    assert_bit_exact(_np(gk), rk, "batched/keys")
+    assert_bit_exact(_np(gid), rid, "batched/ids")
+    assert_bit_exact(_np(gbins), rbins, "batched/bins")
+    rimg, rT, ridx, _, _ = O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background, xys,
+                                           depths, radii, conics, cum, n=n, B=B,
+                                           img_shape=s.img_shape)
+    gimg, gT, gidx, _ = _ops.rasterize_fwd(
+        _t(s.colors), _t(s.opacities).reshape(-1), _t(s.opacities).reshape(-1),
+        _t(s.background), _t(xys), _t(depths), _t(radii), _t(conics), _t(cum), n=n, B=B,
+        img_shape=s.img_shape)
+    assert_bit_exact(_np(gimg), rimg, "batched/img")
+    assert_bit_exact(_np(gidx), ridx, "batched/final_idx")
+    H, W = s.img_shape
+    vout = (2.0 * (rimg.reshape(B, H, W, 3) - s.targets) / rimg.size).astype(np.float32)
+    ref_g = O.rasterize_bwd(s.colors, s.opacities, s.opacities, s.background, xys, depths, radii,
+                            conics, cum, rT, ridx, vout, n=n, B_out=B, B_geom=B,
+                            img_shape=s.img_shape)
+    got_g = _ops.rasterize_bwd(_t(s.colors), _t(s.opacities).reshape(-1),
+                               _t(s.opacities).reshape(-1), _t(s.background), _t(xys),
+                               _t(depths), _t(radii), _t(conics), _t(cum), _t(rT), _t(ridx),
+                               _t(vout).reshape(-1, 3), n=n, B_out=B, B_geom=B,
+                               img_shape=s.img_shape)
+    for label, g, r in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), got_g, ref_g[:4]):
+        _grad_compare(_np(g).reshape(r.shape), r, f"batched/{label}")
+
+
+@pytest.mark.parametrize("H,W", [(37, 53), (16, 16), (100, 33)])
+def test_ragged_images(H, W):
+    _case(f"ragged {H}x{W}")
+    sc = random_scene(3000, H, W, seed=H * W)
+    ref, got = _project_both(sc["means"], sc["scales"], sc["quats"], sc["vm"], sc["opac"],
+                             n=3000, B=1, img_shape=(H, W), f=sc["f"], c=sc["c"])
+    for label, r, g in zip(("xys", "depths", "radii", "conics", "nth", "cum"), ref, got):
+        assert_bit_exact(g.reshape(r.shape), r, f"ragged/{label}")
+    xys, depths, radii, conics, nth, cum = ref
+    rimg, rT, ridx, _, M = O.rasterize_fwd(sc["colors"], sc["opac"], sc["opac"], sc["bg"], xys,
+                                           depths, radii, conics, cum, n=3000, B=1,
+                                           img_shape=(H, W))
+    gimg, gT, gidx, gM = _ops.rasterize_fwd(
+        _t(sc["colors"]), _t(sc["opac"]).reshape(-1), _t(sc["opac"]).reshape(-1), _t(sc["bg"]),
+        _t(xys), _t(depths), _t(radii), _t(conics), _t(cum), n=3000, B=1, img_shape=(H, W))
+    assert gM == M
+    assert_bit_exact(_np(gimg), rimg, "ragged/img")
+    assert_bit_exact(_np(gidx), ridx, "ragged/final_idx")
