@@ -14,6 +14,33 @@ from splax_amd import _ops
 from splax_amd._project import resolve_batch
 
 
+def key_layout(B: int, H: int, W: int) -> dict:
+    """Fields of the packed 32-bit sort key (splax/_rasterize/_sort/_sort.py:51-60)."""
+    tx, ty = (W + 15) // 16, (H + 15) // 16
+    nt = tx * ty
+    tile_bits = (nt - 1).bit_length()
+    image_bits = (B - 1).bit_length()
+    depth_bits = 31 - image_bits - tile_bits
+    return {"tiles_x": tx, "tiles_y": ty, "num_tiles": nt, "tile_bits": tile_bits,
+            "image_bits": image_bits, "depth_bits": depth_bits, "packed": depth_bits >= 16}
+
+
+def check_key_fits(B: int, H: int, W: int) -> None:
+    """Raise like the reference when the batch / resolution cannot be keyed.
+
+    The reference falls back to a 64-bit key when fewer than 16 depth bits remain and raises
+    ValueError only when even that overflows (splax/_rasterize/_sort/_sort.py:61-66). The 64-bit
+    key path is not built here, so every non-packable layout raises.
+    """
+    lay = key_layout(B, H, W)
+    if not lay["packed"]:
+        raise ValueError(
+            f"intersection key does not pack into 32 bits: image_n_bits({lay['image_bits']}) + "
+            f"tile_n_bits({lay['tile_bits']}) leaves {lay['depth_bits']} < 16 depth bits "
+            f"(batch B={B}, n_tiles={lay['num_tiles']}); the 64-bit key path is not built yet. "
+            "Reduce batch size or resolution.")
+
+
 class _RasterizeFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, colors, opac, map_opac, background, xys, depths, radii, conics, cum,
@@ -79,6 +106,7 @@ def rasterize(colors: torch.Tensor, opacities: torch.Tensor, background: torch.T
             raise ValueError(f"{name} has {r} rows, expected {n} or {Bg * n}")
     if background.numel() not in (3, 3 * Bg):
         raise ValueError(f"background must have 3 or {3 * Bg} entries")
+    check_key_fits(Bg, int(H), int(W))
     img, _, _ = _RasterizeFn.apply(colors, opacities, map_opacities, background, xys, depths,
                                    radii, conics, cum_tiles_hit, (n, Bg, (int(H), int(W))))
     return img.reshape(Bg, H, W, 3) if batched else img.reshape(H, W, 3)

@@ -1,0 +1,245 @@
+"""GPU tests of the torch-facing API (splax_amd.render / project / rasterize with autograd).
+
+Mirrors the reference's API tests: render == oracle pipeline, gradients == the oracle's chained
+VJPs (tests/test_warp_grad.py), batched cameras == stacked single renders and summed shared
+gradients (tests/test_warp_batch.py, tests/test_warp_grad_batched.py), antialiased compensation
+(tests/test_antialiased.py), render_log, rigid transforms (tests/test_transforms.py), the
+broadcast-geometry backward (B_geom = 1 < B_out) and the empty / single-intersection edge cases.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import splax_amd
+from conftest import assert_bit_exact, random_scene, rel_fro
+from oracle import oracle as O
+from splax_amd import _lib, _ops
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _device_healthy():
+    yield
+    assert _lib.check_device() == 0
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _t(a, grad=False):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t.requires_grad_(True) if grad else t
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _oracle_render_and_grads(sc, n, w, opac_blend=None):
+    H, W = sc["img_shape"]
+    q = np.roll(sc["quats"], -1, axis=-1)
+    xys, depths, radii, conics, nth, cum = O.project_fwd(
+        sc["means"], sc["scales"], q, sc["vm"], sc["opac"], n=n, total=n, img_shape=(H, W),
+        f=sc["f"], c=sc["c"])
+    ob = sc["opac"] if opac_blend is None else opac_blend
+    img, Ts, fidx, _, _ = O.rasterize_fwd(sc["colors"], ob, sc["opac"], sc["bg"], xys, depths,
+                                          radii, conics, cum, n=n, B=1, img_shape=(H, W))
+    vc, vo, vxy, vcon, _ = O.rasterize_bwd(sc["colors"], ob, sc["opac"], sc["bg"], xys, depths,
+                                           radii, conics, cum, Ts, fidx, w.astype(np.float32),
+                                           n=n, B_out=1, B_geom=1, img_shape=(H, W))
+    vm_, vs_, vq_, vv_, _ = O.project_bwd(sc["means"], sc["scales"], q, sc["vm"], radii, conics,
+                                          vxy, np.zeros(n, np.float32), vcon, n=n, B=1, f=sc["f"])
+    return img.reshape(H, W, 3), dict(means=vm_, scales=vs_, quats=np.roll(vq_, 1, axis=-1),
+                                      colors=vc, opac=vo.reshape(-1, 1), viewmat=vv_)
+
+
+def test_render_and_grads_match_oracle():
+    _case("render + grads vs oracle")
+    n, H, W = 6000, 128, 160
+    sc = random_scene(n, H, W, seed=3)
+    w = np.random.default_rng(1).uniform(-1, 1, (H, W, 3)).astype(np.float32)
+    ref_img, ref_g = _oracle_render_and_grads(sc, n, w)
+    p = {k: _t(sc[k], grad=True) for k in ("means", "scales", "quats", "colors", "opac")}
+    vm = _t(sc["vm"], grad=True)
+    img, depth = splax_amd.render(p["means"], p["scales"], p["quats"], p["colors"], p["opac"],
+                                  viewmat=vm, background=_t(sc["bg"]), img_shape=(H, W),
+                                  f=sc["f"], c=sc["c"])
+    assert depth is None and img.shape == (H, W, 3)
+    assert_bit_exact(_np(img), ref_img, "render/img")
+    (img * _t(w)).sum().backward()
+    for k in ("means", "scales", "quats", "colors", "opac"):
+        r = rel_fro(_np(p[k].grad), ref_g[k])
+        assert r < 1e-5, f"{k}: relative Frobenius error {r:.2e}"
+    assert rel_fro(_np(vm.grad), ref_g["viewmat"]) < 1e-5
+    assert (_np(vm.grad)[3] == 0).all()
+
+
+def test_batched_cameras_equal_stacked():
+    _case("batched viewmats")
+    n, H, W = 4000, 96, 96
+    sc = random_scene(n, H, W, seed=8)
+    vms = np.stack([sc["vm"]] * 3)
+    vms[1, 0, 3] += 0.25
+    vms[2, 1, 3] -= 0.2
+    w = np.random.default_rng(2).uniform(-1, 1, (3, H, W, 3)).astype(np.float32)
+
+    def run(vm_np, w_np):
+        p = {k: _t(sc[k], grad=True) for k in ("means", "scales", "quats", "colors", "opac")}
+        img, _ = splax_amd.render(p["means"], p["scales"], p["quats"], p["colors"], p["opac"],
+                                  viewmat=_t(vm_np), background=_t(sc["bg"]), img_shape=(H, W),
+                                  f=sc["f"], c=sc["c"])
+        (img * _t(w_np)).sum().backward()
+        return _np(img), {k: _np(v.grad) for k, v in p.items()}
+
+    bimg, bg = run(vms, w)
+    assert bimg.shape == (3, H, W, 3)
+    singles = [run(vms[b], w[b]) for b in range(3)]
+    for b in range(3):
+        assert_bit_exact(bimg[b], singles[b][0], f"batched/img[{b}]")
+    for k in bg:
+        summed = sum(s[1][k].astype(np.float64) for s in singles)
+        r = rel_fro(bg[k], summed)
+        assert r < 1e-5, f"batched/{k}: {r:.2e}"
+
+
+def test_batched_viewmat_grads_per_pose():
+    _case("batched viewmat grads")
+    n, H, W = 3000, 64, 80
+    sc = random_scene(n, H, W, seed=9)
+    vms = np.stack([sc["vm"]] * 2)
+    vms[1, 0, 3] += 0.3
+    vm = _t(vms, grad=True)
+    args = [_t(sc[k]) for k in ("means", "scales", "quats", "colors", "opac")]
+    img, _ = splax_amd.render(*args, viewmat=vm, background=_t(sc["bg"]), img_shape=(H, W),
+                              f=sc["f"], c=sc["c"])
+    img.sum().backward()
+    g = _np(vm.grad)
+    for b in range(2):
+        v1 = _t(vms[b], grad=True)
+        i1, _ = splax_amd.render(*args, viewmat=v1, background=_t(sc["bg"]), img_shape=(H, W),
+                                 f=sc["f"], c=sc["c"])
+        i1.sum().backward()
+        assert rel_fro(g[b], _np(v1.grad)) < 1e-5
+
+
+def test_antialiased_matches_compensated_oracle():
+    _case("antialiased")
+    n, H, W = 3000, 96, 96
+    sc = random_scene(n, H, W, seed=4)
+    img_aa, _ = splax_amd.render(*[_t(sc[k]) for k in ("means", "scales", "quats", "colors",
+                                                        "opac")], viewmat=_t(sc["vm"]),
+                                 background=_t(sc["bg"]), img_shape=(H, W), f=sc["f"],
+                                 c=sc["c"], antialiased=True)
+    q = np.roll(sc["quats"], -1, axis=-1)
+    xys, depths, radii, conics, nth, cum = O.project_fwd(
+        sc["means"], sc["scales"], q, sc["vm"], sc["opac"], n=n, total=n, img_shape=(H, W),
+        f=sc["f"], c=sc["c"])
+    rho = _np(splax_amd.opacity_compensation(_t(conics), _t(radii)))
+    ob = (sc["opac"] * rho[:, None]).astype(np.float32)
+    ref, _, _, _, _ = O.rasterize_fwd(sc["colors"], ob, sc["opac"], sc["bg"], xys, depths, radii,
+                                      conics, cum, n=n, B=1, img_shape=(H, W))
+    assert_bit_exact(_np(img_aa), ref.reshape(H, W, 3), "antialiased/img")
+    plain, _ = splax_amd.render(*[_t(sc[k]) for k in ("means", "scales", "quats", "colors",
+                                                       "opac")], viewmat=_t(sc["vm"]),
+                                background=_t(sc["bg"]), img_shape=(H, W), f=sc["f"], c=sc["c"])
+    assert np.abs(_np(plain) - _np(img_aa)).max() > 1e-3
+
+
+def test_render_log_equals_render():
+    _case("render_log")
+    n, H, W = 2000, 64, 64
+    sc = random_scene(n, H, W, seed=12)
+    rng = np.random.default_rng(3)
+    log_s = np.log(sc["scales"])
+    logit_c = rng.normal(size=(n, 3)).astype(np.float32)
+    logit_o = rng.normal(size=(n, 1)).astype(np.float32)
+    quats = (sc["quats"] * 1.7).astype(np.float32)
+    cam = dict(viewmat=_t(sc["vm"]), background=_t(sc["bg"]), img_shape=(H, W), f=sc["f"],
+               c=sc["c"])
+    a, _ = splax_amd.render_log(_t(sc["means"]), _t(log_s), _t(quats), _t(logit_c), _t(logit_o),
+                                **cam)
+    tq = _t(quats)
+    b, _ = splax_amd.render(_t(sc["means"]), torch.exp(_t(log_s)),
+                            tq / (torch.linalg.norm(tq, dim=-1, keepdim=True) + 1e-8),
+                            torch.sigmoid(_t(logit_c)), torch.sigmoid(_t(logit_o)), **cam)
+    assert_bit_exact(_np(a), _np(b), "render_log")
+
+
+def test_rigid_transforms_forward_and_grads():
+    _case("transforms")
+    n, H, W = 2000, 80, 80
+    sc = random_scene(n, H, W, seed=21)
+    ang = 0.2
+    tf = np.eye(4, dtype=np.float32)
+    tf[:3, :3] = [[np.cos(ang), -np.sin(ang), 0], [np.sin(ang), np.cos(ang), 0], [0, 0, 1]]
+    tf[:3, 3] = [0.05, 0.1, -0.1]
+    tft = _t(tf[None], grad=True)
+    cam = dict(viewmat=_t(sc["vm"]), background=_t(sc["bg"]), img_shape=(H, W), f=sc["f"],
+               c=sc["c"])
+    args = [_t(sc[k]) for k in ("means", "scales", "quats", "colors", "opac")]
+    img, _ = splax_amd.render(*args, gaussian_transforms=tft, gaussian_slices=[(500, 1500)],
+                              **cam)
+    # identity transform == plain render, bit for bit
+    eye = _t(np.eye(4, dtype=np.float32)[None])
+    img_id, _ = splax_amd.render(*args, gaussian_transforms=eye, gaussian_slices=[(500, 1500)],
+                                 **cam)
+    plain, _ = splax_amd.render(*args, **cam)
+    assert_bit_exact(_np(img_id), _np(plain), "identity transform")
+    assert np.abs(_np(img) - _np(plain)).max() > 1e-3
+    img.sum().backward()
+    g = _np(tft.grad)
+    assert np.isfinite(g).all() and np.abs(g[0, :3]).max() > 0 and (g[0, 3] == 0).all()
+
+
+def test_broadcast_geometry_backward():
+    """B_geom = 1 < B_out (one render differentiated against B targets) through the C ABI."""
+    _case("broadcast geometry backward")
+    n, H, W = 3000, 64, 64
+    sc = random_scene(n, H, W, seed=30)
+    q = np.roll(sc["quats"], -1, axis=-1)
+    xys, depths, radii, conics, nth, cum = O.project_fwd(
+        sc["means"], sc["scales"], q, sc["vm"], sc["opac"], n=n, total=n, img_shape=(H, W),
+        f=sc["f"], c=sc["c"])
+    img, Ts, fidx, _, _ = O.rasterize_fwd(sc["colors"], sc["opac"], sc["opac"], sc["bg"], xys,
+                                          depths, radii, conics, cum, n=n, B=1, img_shape=(H, W))
+    B_out = 3
+    vout = np.random.default_rng(0).uniform(-1, 1, (B_out, H, W, 3)).astype(np.float32)
+    ref = O.rasterize_bwd(sc["colors"], sc["opac"], sc["opac"], sc["bg"], xys, depths, radii,
+                          conics, cum, Ts, fidx, vout, n=n, B_out=B_out, B_geom=1,
+                          img_shape=(H, W))
+    got = _ops.rasterize_bwd(_t(sc["colors"]), _t(sc["opac"]).reshape(-1),
+                             _t(sc["opac"]).reshape(-1), _t(sc["bg"]), _t(xys), _t(depths),
+                             _t(radii), _t(conics), _t(cum), _t(Ts), _t(fidx),
+                             _t(vout).reshape(-1, 3), n=n, B_out=B_out, B_geom=1,
+                             img_shape=(H, W))
+    for label, g, r in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), got, ref[:4]):
+        assert rel_fro(_np(g).reshape(r.shape), r) < 1e-5, label
+
+
+def test_empty_and_single_intersection():
+    _case("M == 0 and M == 1")
+    H = W = 48
+    bg = np.array([0.2, 0.4, 0.6], np.float32)
+    means = np.array([[0.0, 0.0, -3.0]], np.float32)  # behind the camera: M == 0
+    ones = dict(scales=np.full((1, 3), 0.02, np.float32),
+                quats=np.array([[1.0, 0, 0, 0]], np.float32),
+                colors=np.array([[1.0, 0, 0]], np.float32), opac=np.array([[0.9]], np.float32))
+    p = {k: _t(v, grad=True) for k, v in ones.items()}
+    mt = _t(means, grad=True)
+    img, _ = splax_amd.render(mt, p["scales"], p["quats"], p["colors"], p["opac"],
+                              viewmat=_t(np.eye(4, dtype=np.float32)), background=_t(bg),
+                              img_shape=(H, W), f=(40.0, 40.0))
+    np.testing.assert_array_equal(_np(img), np.broadcast_to(bg, (H, W, 3)))
+    img.sum().backward()
+    assert (_np(mt.grad) == 0).all() and (_np(p["colors"].grad) == 0).all()
+    # one small gaussian in one tile: the lone bin stays [0, 0) and nothing is drawn
+    img1, _ = splax_amd.render(_t(np.array([[0.0, 0.0, 4.0]], np.float32)), p["scales"],
+                               p["quats"], p["colors"], p["opac"],
+                               viewmat=_t(np.eye(4, dtype=np.float32)), background=_t(bg),
+                               img_shape=(H, W), f=(40.0, 40.0), c=(40.0, 40.0))
+    np.testing.assert_array_equal(_np(img1), np.broadcast_to(bg, (H, W, 3)))

@@ -239,3 +239,37 @@ def test_ragged_images(H, W):
     assert gM == M
     assert_bit_exact(_np(gimg), rimg, "ragged/img")
     assert_bit_exact(_np(gidx), ridx, "ragged/final_idx")
+
+
+def test_golden_fixture():
+    """The committed oracle fixture (tests/golden/tiny_render.npz) through the C ABI."""
+    from pathlib import Path
+
+    _case("golden fixture")
+    g = np.load(Path(__file__).resolve().parent / "golden" / "tiny_render.npz")
+    H, W = (int(v) for v in g["img_shape"])
+    n = g["means"].shape[0]
+    f, c = tuple(float(v) for v in g["f"]), tuple(float(v) for v in g["c"])
+    ref, got = _project_both(g["means"], g["scales"], g["quats_wxyz"], g["viewmat"], g["opac"],
+                             n=n, B=1, img_shape=(H, W), f=f, c=c)
+    for label, r, gg in zip(("xys", "depths", "radii", "conics", "num_tiles_hit", "cum"), ref,
+                            got):
+        assert_bit_exact(gg.reshape(r.shape), g[label], f"golden/{label}")
+    args = (_t(g["xys"]), _t(g["depths"]), _t(g["radii"]), _t(g["conics"]))
+    gk, gid, gbins = _ops.sort_and_bin(*args, _t(g["opac"]).reshape(-1), _t(g["cum"]), n=n, B=1,
+                                       img_shape=(H, W))
+    assert_bit_exact(_np(gk), g["keys"], "golden/keys")
+    assert_bit_exact(_np(gid), g["ids"], "golden/ids")
+    assert_bit_exact(_np(gbins), g["bins"], "golden/bins")
+    gimg, gT, gidx, _ = _ops.rasterize_fwd(_t(g["colors"]), _t(g["opac"]).reshape(-1),
+                                           _t(g["opac"]).reshape(-1), _t(g["bg"]), *args,
+                                           _t(g["cum"]), n=n, B=1, img_shape=(H, W))
+    assert_bit_exact(_np(gimg), g["img"], "golden/img")
+    assert_bit_exact(_np(gT), g["final_Ts"], "golden/final_Ts")
+    assert_bit_exact(_np(gidx), g["final_idx"], "golden/final_idx")
+    gg = _ops.rasterize_bwd(_t(g["colors"]), _t(g["opac"]).reshape(-1), _t(g["opac"]).reshape(-1),
+                            _t(g["bg"]), *args, _t(g["cum"]), _t(g["final_Ts"]),
+                            _t(g["final_idx"]), _t(g["v_out"]).reshape(-1, 3), n=n, B_out=1,
+                            B_geom=1, img_shape=(H, W))
+    for label, got_g in zip(("v_colors", "v_opac", "v_xy", "v_conic"), gg):
+        _grad_compare(_np(got_g).reshape(g[label].shape), g[label], f"golden/{label}")

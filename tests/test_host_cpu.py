@@ -1,0 +1,128 @@
+"""Host-side logic and the C-ABI library, without a GPU.
+
+- libsplat_hip.so loads and exports every entry point include/splat_hip.h declares, and the
+  Python binding covers all of them.
+- Argument validation mirrors the reference's ValueErrors (splax/_render.py:81-89,
+  splax/_project/_project.py:126-132, splax/_rasterize/_sort/_sort.py:61-66).
+- opacity_compensation closed form (splax/_project/_project.py:95-117), transform_ids, the
+  synthetic scene generators and look_at.
+- The product path refuses to run without a GPU (no CPU fallback).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import splax_amd
+from splax_amd import _lib
+from splax_amd._rasterize import check_key_fits, key_layout
+from splax_amd.scenes import make_scene
+from splax_amd.utils import look_at
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    text = (ROOT / "include" / "splat_hip.h").read_text()
+    return sorted(set(re.findall(r"\b(splat_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = _declared_symbols()
+    assert len(names) >= 10
+    handle = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in names:
+        assert hasattr(handle, name), f"{name} declared in include/splat_hip.h but not exported"
+    assert set(names) == set(_lib._SIGS), "Python binding and header disagree"
+    lib = _lib.lib()
+    assert lib.splat_abi_version() == 1
+    assert isinstance(lib.splat_last_error(), bytes)
+
+
+def test_no_cpu_fallback():
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    x = torch.zeros((4, 3))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        splax_amd.project(x, x + 0.1, torch.tensor([[1.0, 0, 0, 0]]).repeat(4, 1), torch.eye(4),
+                          opacities=torch.ones(4, 1), img_shape=(32, 32), f=(30.0, 30.0))
+
+
+def test_transform_ids_and_validation():
+    ids = splax_amd.transform_ids(10, [(2, 5), (7, 9)])
+    assert ids.tolist() == [-1, -1, 0, 0, 0, -1, -1, 1, 1, -1]
+    with pytest.raises(ValueError, match="outside"):
+        splax_amd.transform_ids(10, [(5, 12)])
+    with pytest.raises(ValueError, match="overlap"):
+        splax_amd.transform_ids(10, [(0, 5), (4, 6)])
+    x = torch.zeros((4, 3))
+    with pytest.raises(ValueError, match="passed together"):
+        splax_amd.render(x, x, torch.zeros(4, 4), x, torch.ones(4, 1), viewmat=torch.eye(4),
+                         background=torch.zeros(3), img_shape=(16, 16), f=(10.0, 10.0),
+                         gaussian_transforms=torch.zeros(1, 4, 4))
+    with pytest.raises(ValueError, match="does not match"):
+        splax_amd.render(x, x, torch.zeros(4, 4), x, torch.ones(4, 1), viewmat=torch.eye(4),
+                         background=torch.zeros(3), img_shape=(16, 16), f=(10.0, 10.0),
+                         gaussian_transforms=torch.zeros(2, 4, 4), gaussian_slices=[(0, 2)])
+
+
+def test_opacity_compensation_closed_form():
+    rng = np.random.default_rng(0)
+    a = rng.uniform(0.1, 2.0, 50)
+    c = rng.uniform(0.1, 2.0, 50)
+    b = rng.uniform(-0.5, 0.5, 50) * np.sqrt(a * c)
+    conics = torch.tensor(np.stack([a, b, c], -1))
+    radii = torch.tensor((np.arange(50) % 7 != 0).astype(np.int32))[:, None]
+    rho = splax_amd.opacity_compensation(conics, radii).numpy()
+    eps = 0.3
+    ref = np.sqrt(np.clip(1 - eps * (a + c) + eps ** 2 * (a * c - b * b), 0, 1))
+    ref[np.arange(50) % 7 == 0] = 1.0
+    np.testing.assert_allclose(rho, ref, rtol=1e-12)
+    # an isotropic screen gaussian of variance s2: conic = 1/(s2 + 0.3) -> rho = s2 / (s2 + 0.3)
+    s2 = 2.0
+    iso = torch.tensor([[1 / (s2 + 0.3), 0.0, 1 / (s2 + 0.3)]], dtype=torch.float64)
+    got = splax_amd.opacity_compensation(iso, torch.ones(1, 1)).item()
+    assert abs(got - s2 / (s2 + 0.3)) < 1e-12
+
+
+def test_key_layout_and_overflow_error():
+    assert key_layout(1, 1080, 1920)["depth_bits"] == 18
+    assert key_layout(16, 512, 512)["depth_bits"] == 17
+    assert key_layout(4, 1060, 1600)["packed"]
+    check_key_fits(4, 1060, 1600)
+    with pytest.raises(ValueError, match="64-bit key path"):
+        check_key_fits(8, 1080, 1920)
+
+
+def test_scenes_deterministic_and_shaped():
+    a = make_scene(0)
+    b = make_scene(0)
+    np.testing.assert_array_equal(a.means, b.means)
+    np.testing.assert_array_equal(a.targets, b.targets)
+    assert a.n == 10_000 and a.img_shape == (256, 256) and a.B == 1
+    assert np.allclose(np.linalg.norm(a.quats, axis=-1), 1.0, atol=1e-6)
+    assert (a.opacities > 0).all() and (a.opacities < 1).all()
+    s3 = make_scene(3, n=1000)
+    assert s3.B == 16 and s3.img_shape == (512, 512)
+    s2 = make_scene(2, n=2000)
+    assert s2.img_shape == (1080, 1920) and np.abs(s2.means).max() < 6
+
+
+def test_look_at_properties():
+    eyes = np.array([[0.5, 0.2, 4.0], [3.0, -2.0, 1.0]])
+    vm = look_at(eyes, np.zeros(3), up=(0, 0, 1))
+    for k in range(2):
+        R = vm[k, :3, :3].astype(np.float64)
+        np.testing.assert_allclose(R @ R.T, np.eye(3), atol=1e-6)
+        np.testing.assert_allclose(np.linalg.det(R), 1.0, atol=1e-6)
+        e = vm[k] @ np.r_[eyes[k], 1.0]
+        np.testing.assert_allclose(e[:3], 0.0, atol=1e-5)  # the eye is the camera origin
+        o = vm[k] @ np.array([0, 0, 0, 1.0])
+        np.testing.assert_allclose(o[:2], 0.0, atol=1e-5)  # the target lies on the +z axis
+        assert o[2] > 0

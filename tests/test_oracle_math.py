@@ -1,0 +1,89 @@
+"""Pins the oracle's fixed-sequence exp / log and the packed-key layout (CPU only).
+
+exp and log must be accurate to a couple of ulp (they replace the reference's fast-math
+wp.exp / wp.log, splax/_rasterize/_kernels.py:188 and splax/_project/_kernels.py:227); the
+float64 numpy functions are the truth. The key layout is checked against the closed form of
+splax/_rasterize/_sort/_sort.py:56-60 and the per-config table derived independently by hand.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+
+def _ulp_err(got: np.ndarray, truth64: np.ndarray) -> np.ndarray:
+    got = got.astype(np.float64)
+    ulp = np.spacing(np.abs(truth64).astype(np.float32)).astype(np.float64)
+    return np.abs(got - truth64) / ulp
+
+
+def test_logf_accuracy_sweep():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        np.float32(1.0) + np.arange(-2000, 2000, dtype=np.float32) * np.float32(2.0 ** -23),
+        rng.uniform(1.0, 255.0, 200_000).astype(np.float32),  # opac / (1/255) in projection
+        np.exp(rng.uniform(-80, 80, 200_000)).astype(np.float32),
+        np.array([1e-40, 1e-45, 3e-39, 1.17549435e-38, 2.0, 0.5, 255.0], np.float32),
+    ])
+    x = x[x > 0]
+    got = O.logf(x)
+    truth = np.log(x.astype(np.float64))
+    err = _ulp_err(got, truth)
+    nonzero = truth != 0
+    assert err[nonzero].max() <= 2.0, f"max ulp error {err[nonzero].max()}"
+    assert O.logf(np.float32(1.0))[0] == 0.0
+
+
+def test_expf_accuracy_sweep():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.uniform(-87.0, 88.0, 400_000),
+        rng.uniform(-6.0, 0.0, 400_000),  # the blend's range after the alpha cull
+        np.arange(-2000, 2000) * 2.0 ** -20,
+    ]).astype(np.float32)
+    got = O.expf(x)
+    truth = np.exp(x.astype(np.float64))
+    err = _ulp_err(got, truth)
+    assert err.max() <= 2.0, f"max ulp error {err.max()} at {x[np.argmax(err)]}"
+    assert O.expf(np.float32(0.0))[0] == 1.0
+    assert O.expf(np.float32(-0.0))[0] == 1.0
+
+
+def test_expf_special_values():
+    got = O.expf(np.array([np.nan, -1e9, -105.0, 100.0], np.float32))
+    assert got[0] == 0.0 and got[1] == 0.0 and got[2] == 0.0
+    assert np.isinf(got[3])
+    sub = O.expf(np.array([-100.0], np.float32))[0]
+    assert 0.0 < sub < 1e-40  # subnormal range is reached, never used for a blend decision
+
+
+def test_expf_monotone_on_blend_range():
+    x = np.sort(np.random.default_rng(2).uniform(-8.0, 0.0, 200_000).astype(np.float32))
+    y = O.expf(x)
+    assert np.all(np.diff(y.astype(np.float64)) >= 0.0)
+
+
+@pytest.mark.parametrize(
+    "B,H,W,tile_bits,image_bits,depth_bits,packed",
+    [
+        (1, 256, 256, 8, 0, 23, True),  # config 0: 16x16 tiles
+        (1, 800, 800, 12, 0, 19, True),  # config 1: 50x50
+        (1, 1080, 1920, 13, 0, 18, True),  # config 2: 120x68
+        (16, 512, 512, 10, 4, 17, True),  # config 3: 32x32, 16 cameras
+        (4, 1060, 1600, 13, 2, 16, True),  # config 4: 100x67, boundary case
+        (8, 1080, 1920, 13, 3, 15, False),  # B=8 at 1080p needs the 64-bit key
+        (1, 16, 16, 0, 0, 31, True),  # one tile
+    ],
+)
+def test_key_layout_table(B, H, W, tile_bits, image_bits, depth_bits, packed):
+    lay, ok = O.key_layout(B, H, W)
+    assert lay["tile_n_bits"] == tile_bits
+    assert lay["image_n_bits"] == image_bits
+    assert lay["depth_bits"] == depth_bits
+    assert ok == packed
+    nt = lay["num_tiles"]
+    assert nt == ((W + 15) // 16) * ((H + 15) // 16)
+    assert (nt - 1) < (1 << tile_bits) and (B - 1) < (1 << image_bits)
