@@ -88,6 +88,34 @@ int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows
                         int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
                         float* v_xy, float* v_conic);
 
+/* Forward that keeps the sorted intersection lists resident for the backward (no counterpart in
+ * the reference, whose backward re-sorts, splax/_rasterize/_kernels.py:422): the caller passes
+ * num_intersects = cum_tiles_hit[B*n-1] (so the library skips its own device-to-host read) and
+ * buffers sorted_ids [num_intersects] and tile_bins [B*num_tiles, 2], which receive exactly what
+ * splat_sort_and_bin would return. Other arguments and outputs as splat_rasterize_fwd. */
+int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t rows_colors,
+                             const float* opacities, int64_t rows_opac,
+                             const float* map_opacities, int64_t rows_map_opac,
+                             const float* background, int64_t rows_bg, const float* xys,
+                             const float* depths, const int32_t* radii, const float* conics,
+                             const int32_t* cum_tiles_hit, int32_t num_gaussians, int32_t B,
+                             int32_t img_h, int32_t img_w, int64_t num_intersects,
+                             float* final_Ts, int32_t* final_idx, float* out_img,
+                             int32_t* sorted_ids, int32_t* tile_bins);
+
+/* Backward over the sorted lists kept by splat_rasterize_fwd_keep (no re-sort). Arguments as
+ * splat_rasterize_bwd plus sorted_ids / tile_bins / num_intersects of the matching forward; the
+ * outputs equal splat_rasterize_bwd's up to float-atomic ordering. */
+int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64_t rows_colors,
+                               const float* opacities, int64_t rows_opac,
+                               const float* background, int64_t rows_bg, const float* xys,
+                               const float* conics, const int32_t* sorted_ids,
+                               const int32_t* tile_bins, int64_t num_intersects,
+                               const float* final_Ts, const int32_t* final_idx,
+                               const float* v_out_img, int64_t vout_rows, int32_t num_gaussians,
+                               int32_t B_out, int32_t B_geom, int32_t img_h, int32_t img_w,
+                               float* v_colors, float* v_opacity, float* v_xy, float* v_conic);
+
 /* Replaces sort_and_bin (splax/_rasterize/_sort/_sort.py:29-171), exposed for callers that keep
  * the sorted lists: writes the M sorted packed keys and gaussian ids (capacity >= M required,
  * else status 6 with *num_intersects = M) and the [B*num_tiles, 2] tile bins. */

@@ -110,6 +110,60 @@ def rasterize_fwd(colors, opac, map_opac, background, xys, depths, radii, conics
     return img, Ts, fidx, int(m.item())
 
 
+def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, conics, cum, *, n,
+                       B, img_shape):
+    """Forward that also returns the sorted gaussian ids and tile bins (kept for the backward).
+
+    The intersection count is read here (one device-to-host sync, the same one the reference
+    makes inside sort_and_bin) so the buffers can be sized before the launch.
+    """
+    colors, opac, map_opac, background, xys, depths, conics = map(
+        _f32, (colors, opac, map_opac, background, xys, depths, conics))
+    radii, cum = _i32(radii), _i32(cum)
+    dev = _lib.require_gpu(colors, opac, map_opac, background, xys, depths, radii, conics, cum)
+    H, W = img_shape
+    M = int(cum.reshape(-1)[-1].item()) if cum.numel() else 0
+    tiles = ((W + 15) // 16) * ((H + 15) // 16)
+    Ts = torch.empty((B * H, W), device=dev, dtype=torch.float32)
+    fidx = torch.empty((B * H, W), device=dev, dtype=torch.int32)
+    img = torch.empty((B * H, W, 3), device=dev, dtype=torch.float32)
+    ids = torch.empty((max(M, 1),), device=dev, dtype=torch.int32)
+    bins = torch.empty((B * tiles, 2), device=dev, dtype=torch.int32)
+    p = _lib.ptr
+    with torch.cuda.device(dev):
+        st = _lib.lib().splat_rasterize_fwd_keep(
+            _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
+            p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys),
+            p(depths), p(radii), p(conics), p(cum), n, B, H, W, M, p(Ts), p(fidx), p(img),
+            p(ids), p(bins))
+    _lib.check(st, "rasterize")
+    return img, Ts, fidx, ids, bins, M
+
+
+def rasterize_bwd_sorted(colors, opac, background, xys, conics, ids, bins, M, final_Ts,
+                         final_idx, v_out, *, n, B_out, B_geom, img_shape):
+    """Backward over the sorted lists of rasterize_fwd_keep (no re-sort)."""
+    colors, opac, background, xys, conics, final_Ts, v_out = map(
+        _f32, (colors, opac, background, xys, conics, final_Ts, v_out))
+    ids, bins, final_idx = _i32(ids), _i32(bins), _i32(final_idx)
+    dev = _lib.require_gpu(colors, opac, xys, conics, ids, bins, final_Ts, final_idx, v_out)
+    H, W = img_shape
+    nout = B_out * n
+    v_colors = torch.empty((nout, 3), device=dev, dtype=torch.float32)
+    v_opac = torch.empty((nout,), device=dev, dtype=torch.float32)
+    v_xy = torch.empty((nout, 2), device=dev, dtype=torch.float32)
+    v_conic = torch.empty((nout, 3), device=dev, dtype=torch.float32)
+    p = _lib.ptr
+    with torch.cuda.device(dev):
+        st = _lib.lib().splat_rasterize_bwd_sorted(
+            _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
+            p(background), rows(background, 3), p(xys), p(conics), p(ids), p(bins), M,
+            p(final_Ts), p(final_idx), p(v_out), v_out.numel() // (3 * W), n, B_out, B_geom, H, W,
+            p(v_colors), p(v_opac), p(v_xy), p(v_conic))
+    _lib.check(st, "rasterize_bwd")
+    return v_colors, v_opac, v_xy, v_conic
+
+
 def rasterize_bwd(colors, opac, map_opac, background, xys, depths, radii, conics, cum, final_Ts,
                   final_idx, v_out, *, n, B_out, B_geom, img_shape):
     """_rasterize_bwd_warp (splax/_rasterize/_kernels.py:386-500)."""

@@ -1,21 +1,24 @@
 // Forward and backward alpha blend on gfx950.
 //
 // One workgroup of 256 threads (four wave64s) per (image, 16x16 tile), as in the reference
-// (splax/_rasterize/_kernels.py:63-87,469-500). Each wave owns one 8x8 quadrant of the tile, so a
-// small gaussian touches few waves. Records of the tile's sorted range are staged in LDS in
-// batches of 256 (structure of arrays: every lane reads the same record, an LDS broadcast). While
-// staging, each record gets
+// (splax/_rasterize/_kernels.py:63-87,469-500). Each wave owns one 8x8 quadrant of the tile. The
+// tile's sorted range is staged in LDS in batches of 256 records (three float4 per record: every
+// lane of a wave reads the same record, an LDS broadcast). While staging, each record gets
 //   - sigma_max: a conservative bound (log(255 o) + 1e-3) above which o e^-sigma < 1/255, so a
 //     lane skips the exponential for pairs the reference rejects anyway, and
 //   - a 4-bit quadrant mask: the quadrants whose pixel centres can reach sigma <= sigma_max,
-//     from the ellipse's bounding box; a wave skips records outside its quadrant outright.
-// Both only remove pairs that the reference's `sigma < 0 or alpha < 1/255` test rejects, so the
-// per-pixel sequence of blended pairs (and every float operation on it) is the reference's.
+//     from the ellipse's bounding box;
+// and each wave then walks only the compacted, order-preserving list of records that reach its
+// quadrant. Both filters remove only pairs that the reference's `sigma < 0 or alpha < 1/255`
+// test rejects, so the per-pixel sequence of blended pairs (and every float operation on it) is
+// the reference's, and the forward image is bit-identical to the CPU oracle.
 //
-// Backward: the same staging walked back to front from the workgroup's largest final_idx. Per
-// record, the contributing lanes of a wave reduce their 9 gradient terms with DPP, one lane adds
-// them into the record's LDS accumulator, and after the batch each record issues at most 9 float
-// atomics to global memory (instead of 9 per contributing pixel).
+// Backward: the same staging walked back to front from the workgroup's largest final_idx. A
+// pixel's contribution to a record is nine floats; per record the contributing lanes of a wave
+// reduce them with a reduce-scatter (v_permlane32_swap, v_permlane16_swap, then DPP row shifts:
+// 28 VALU for nine values), add the totals into the record's LDS accumulator, and after each batch
+// every record issues at most nine float atomics to global memory. Events with few contributing
+// lanes skip the reduction and add their values straight into LDS.
 #include "splat_common.hpp"
 #include "splat_internal.hpp"
 
@@ -30,6 +33,7 @@ struct BlendCommon {
     const float* xys; const float* conics;
     const int32_t* ids; const int32_t* bins;
     int32_t img_h, img_w, tiles_x, num_tiles;
+    int64_t total;  // geometry rows (B_geom * n): ids outside [0, total) are ignored
 };
 
 // Pixel of thread `tid` in its tile: wave w = quadrant (w & 1, w >> 1), lane = 8x8 raster.
@@ -39,7 +43,7 @@ __device__ __forceinline__ void tile_pixel(int tid, int tile_x, int tile_y, int&
     j = tile_x * kBlockWidth + (wave & 1) * 8 + (lane & 7);
 }
 
-// Stage record `g` for the tile at (tile_x, tile_y); returns smax and the quadrant mask.
+// sigma_max and the quadrant mask of one record for the tile at (tile_x, tile_y).
 __device__ __forceinline__ void stage_bounds(float x, float y, float a, float b, float c, float o,
                                              int tile_x, int tile_y, float& smax,
                                              uint32_t& qmask) {
@@ -75,6 +79,76 @@ __device__ __forceinline__ void stage_bounds(float x, float y, float a, float b,
     }
 }
 
+// LDS record of one batch: r0 = (x, y, a, b), r1 = (c, o, sigma_max, quadrant mask bits),
+// r2 = (red, green, blue, gaussian id bits), plus per-quadrant compacted record lists.
+struct BatchLds {
+    float4 r0[kTile];
+    float4 r1[kTile];
+    float4 r2[kTile];
+    uint8_t list[4][kTile];
+    uint32_t cnt[4][4];  // [wave][quadrant]
+};
+
+// Stages record `src` of the sorted range into slot `tid` and builds the quadrant lists.
+// `live` is false for the clamped tail slots of the last batch (they reach no quadrant).
+// Returns, for the calling wave's quadrant, the list length. Contains two barriers.
+__device__ __forceinline__ int stage_batch(const BlendCommon& C, BatchLds& L, int32_t src,
+                                           bool live, int tile_x, int tile_y) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    int64_t g = C.ids[src];
+    uint32_t qm = 0u;
+    float4 r0 = make_float4(0.f, 0.f, 0.f, 0.f), r1 = r0, r2 = r0;
+    if (live && g >= 0 && g < C.total) {
+        const float2 xy = reinterpret_cast<const float2*>(C.xys)[g];
+        const float a = C.conics[3 * g], b = C.conics[3 * g + 1], c = C.conics[3 * g + 2];
+        const float o = C.opac[g % C.rows_opac];
+        const int64_t cg = g % C.rows_colors;
+        float smax;
+        stage_bounds(xy.x, xy.y, a, b, c, o, tile_x, tile_y, smax, qm);
+        r0 = make_float4(xy.x, xy.y, a, b);
+        r1 = make_float4(c, o, smax, __uint_as_float(qm));
+        r2 = make_float4(C.colors[3 * cg], C.colors[3 * cg + 1], C.colors[3 * cg + 2],
+                         __int_as_float((int32_t)g));
+    }
+    L.r0[tid] = r0;
+    L.r1[tid] = r1;
+    L.r2[tid] = r2;
+    uint64_t bal[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        bal[q] = __ballot((qm >> q) & 1u);
+        if (lane == 0) L.cnt[wave][q] = (uint32_t)__popcll(bal[q]);
+    }
+    __syncthreads();
+    const uint64_t lt = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if ((qm >> q) & 1u) {
+            uint32_t base = 0;
+            for (int w = 0; w < wave; ++w) base += L.cnt[w][q];
+            L.list[q][base + (uint32_t)__popcll(bal[q] & lt)] = (uint8_t)tid;
+        }
+    }
+    const int len = (int)(L.cnt[0][wave] + L.cnt[1][wave] + L.cnt[2][wave] + L.cnt[3][wave]);
+    __syncthreads();
+    return len;
+}
+
+// e^x for x in [-88, 0] (no range handling needed there); equal to det_expf on that domain.
+__device__ __forceinline__ float exp_core(float x) {
+    float kf = rintf(x * kLog2e);
+    float r = fmaf(kf, -kLn2Hi, x);
+    r = fmaf(kf, -kLn2Lo, r);
+    float p = fmaf(r, 0x1.a01a02p-13f, 0x1.6c16c2p-10f);
+    p = fmaf(r, p, 0x1.111112p-7f);
+    p = fmaf(r, p, 0x1.555556p-5f);
+    p = fmaf(r, p, 0x1.555556p-3f);
+    p = fmaf(r, p, 0.5f);
+    p = fmaf(r, p, 1.0f);
+    p = fmaf(r, p, 1.0f);
+    return ldexpf(p, (int)kf);
+}
+
 // ------------------------------------------------------------------ forward
 // _rasterize_kernel, splax/_rasterize/_kernels.py:102-205
 
@@ -84,10 +158,7 @@ struct BlendFwdParams {
 };
 
 __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
-    __shared__ float s_x[kTile], s_y[kTile], s_a[kTile], s_b[kTile], s_c[kTile], s_o[kTile];
-    __shared__ float s_smax[kTile], s_r[kTile], s_g[kTile], s_bl[kTile];
-    __shared__ uint32_t s_q[kTile];
-
+    __shared__ BatchLds L;
     const BlendCommon& C = P.c;
     const int tid = threadIdx.x, wave = tid >> 6;
     const int32_t tile_g = blockIdx.x;
@@ -105,47 +176,32 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
     float T = 1.0f;
     int32_t cur_idx = 0;
     float o0 = 0.f, o1 = 0.f, o2 = 0.f;
-    const uint32_t wbit = 1u << wave;
 
     for (int32_t bt = 0; bt < num_batches; ++bt) {
         // every pixel done -> stop; also the barrier before the LDS records are overwritten
         if (__syncthreads_count(done) >= kTile) break;
         const int32_t batch_start = range_start + bt * kTile;
-        {
-            const int32_t src = iminw(batch_start + tid, range_end - 1);
-            const int64_t g = C.ids[src];
-            const float2 xy = reinterpret_cast<const float2*>(C.xys)[g];
-            const float a = C.conics[3 * g], b = C.conics[3 * g + 1], c = C.conics[3 * g + 2];
-            const float o = C.opac[g % C.rows_opac];
-            const int64_t cg = g % C.rows_colors;
-            float smax;
-            uint32_t qm;
-            stage_bounds(xy.x, xy.y, a, b, c, o, tile_x, tile_y, smax, qm);
-            s_x[tid] = xy.x; s_y[tid] = xy.y;
-            s_a[tid] = a; s_b[tid] = b; s_c[tid] = c; s_o[tid] = o;
-            s_smax[tid] = smax; s_q[tid] = qm;
-            s_r[tid] = C.colors[3 * cg]; s_g[tid] = C.colors[3 * cg + 1];
-            s_bl[tid] = C.colors[3 * cg + 2];
-        }
-        __syncthreads();
-        const int32_t batch_size = iminw(kTile, range_end - batch_start);
+        const int32_t src = iminw(batch_start + tid, range_end - 1);
+        const int len = stage_batch(C, L, src, batch_start + tid < range_end, tile_x, tile_y);
         if (__ballot(!done) == 0ull) continue;
-        for (int32_t t = 0; t < batch_size; ++t) {
-            if (!(s_q[t] & wbit)) continue;
-            const float dx = s_x[t] - px, dy = s_y[t] - py;
-            const float sigma = 0.5f * (s_a[t] * dx * dx + s_c[t] * dy * dy) + s_b[t] * dx * dy;
-            if (done || sigma > s_smax[t] || sigma < 0.0f) continue;
-            const float alpha = minw(kAlphaMax, s_o[t] * det_expf(-sigma));
+        for (int k = 0; k < len; ++k) {
+            const int t = L.list[wave][k];
+            const float4 r0 = L.r0[t], r1 = L.r1[t];
+            const float dx = r0.x - px, dy = r0.y - py;
+            const float sigma = 0.5f * (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
+            if (done || !(sigma >= 0.0f && sigma <= r1.z)) continue;
+            const float alpha = minw(kAlphaMax, r1.y * exp_core(-sigma));
             if (alpha < kAlphaThresh) continue;
             const float next_T = T * (1.0f - alpha);
             if (next_T <= kTEps) {
                 done = true;
                 continue;
             }
+            const float4 r2 = L.r2[t];
             const float vis = alpha * T;
-            o0 = o0 + s_r[t] * vis;
-            o1 = o1 + s_g[t] * vis;
-            o2 = o2 + s_bl[t] * vis;
+            o0 = o0 + r2.x * vis;
+            o1 = o1 + r2.y * vis;
+            o2 = o2 + r2.z * vis;
             T = next_T;
             cur_idx = batch_start + t;
         }
@@ -162,19 +218,25 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
     }
 }
 
+static void fill_common(BlendCommon& c, const RasterInputs& in, const KeyLayout& lay,
+                        const int32_t* sorted_ids, const int32_t* tile_bins) {
+    c.colors = in.colors; c.rows_colors = in.rows_colors;
+    c.opac = in.opac; c.rows_opac = in.rows_opac;
+    c.background = in.background; c.rows_bg = in.rows_bg;
+    c.xys = in.xys; c.conics = in.conics;
+    c.ids = sorted_ids; c.bins = tile_bins;
+    c.img_h = in.img_h; c.img_w = in.img_w;
+    c.tiles_x = lay.tiles_x; c.num_tiles = lay.num_tiles;
+    c.total = (int64_t)in.B_geom * in.n;
+}
+
 int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,
                      float* out_img, hipStream_t stream) {
     const int64_t blocks = (int64_t)in.B_geom * lay.num_tiles;
     if (blocks <= 0) return 0;
     BlendFwdParams P;
-    P.c.colors = in.colors; P.c.rows_colors = in.rows_colors;
-    P.c.opac = in.opac; P.c.rows_opac = in.rows_opac;
-    P.c.background = in.background; P.c.rows_bg = in.rows_bg;
-    P.c.xys = in.xys; P.c.conics = in.conics;
-    P.c.ids = sorted_ids; P.c.bins = tile_bins;
-    P.c.img_h = in.img_h; P.c.img_w = in.img_w;
-    P.c.tiles_x = lay.tiles_x; P.c.num_tiles = lay.num_tiles;
+    fill_common(P.c, in, lay, sorted_ids, tile_bins);
     P.final_Ts = final_Ts; P.final_idx = final_idx; P.out_img = out_img;
     hipLaunchKernelGGL(blend_fwd_kernel, dim3((unsigned)blocks), dim3(kTile), 0, stream, P);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
@@ -192,12 +254,31 @@ struct BlendBwdParams {
     float* v_colors; float* v_opacity; float* v_xy; float* v_conic;
 };
 
+__device__ __forceinline__ float swap32_add(float a, float b) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                              false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap16_add(float a, float b) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                              false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float row_sum_to_lane15(float v) {
+    v = dpp_add<0x111, 0xf>(v);  // row_shr:1
+    v = dpp_add<0x112, 0xf>(v);  // row_shr:2
+    v = dpp_add<0x114, 0xf>(v);  // row_shr:4
+    v = dpp_add<0x118, 0xf>(v);  // row_shr:8
+    return v;
+}
+
+// Record accumulator slot k of batch record t ([t][9] layout: the four lanes that add at once
+// hit four different banks).
+#define ACC(t, k) acc[(t) * 9 + (k)]
+
 __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
-    __shared__ float s_x[kTile], s_y[kTile], s_a[kTile], s_b[kTile], s_c[kTile], s_o[kTile];
-    __shared__ float s_smax[kTile], s_r[kTile], s_g[kTile], s_bl[kTile];
-    __shared__ uint32_t s_q[kTile];
-    __shared__ int32_t s_id[kTile];
-    __shared__ float s_acc[9][kTile];
+    __shared__ BatchLds L;
+    __shared__ float acc[kTile * 9];
     __shared__ int32_t s_max;
 
     const BlendCommon& C = P.c;
@@ -216,23 +297,21 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     const float px = (float)j + 0.5f, py = (float)i + 0.5f;
     const bool inside = i < C.img_h && j < C.img_w;
     int32_t bin_final = range_start - 1;
-    float T = 1.0f, t_final = 1.0f;
-    float v0 = 0.f, v1 = 0.f, v2 = 0.f, bg0 = 0.f, bg1 = 0.f, bg2 = 0.f;
+    float T = 1.0f, v0 = 0.f, v1 = 0.f, v2 = 0.f, tfbg = 0.f;
     if (inside) {
         const int64_t frow = (int64_t)geom_image * C.img_h + i;
         bin_final = P.final_idx[frow * C.img_w + j];
-        t_final = P.final_Ts[frow * C.img_w + j];
+        const float t_final = P.final_Ts[frow * C.img_w + j];
         T = t_final;
         const int64_t vrow = ((int64_t)image_id * C.img_h + i) % P.vout_rows;
         const float* vo = P.v_out + 3 * (vrow * C.img_w + j);
         v0 = vo[0]; v1 = vo[1]; v2 = vo[2];
         const float* bg = C.background + 3 * (C.rows_bg > 1 ? image_id : 0);
-        bg0 = bg[0]; bg1 = bg[1]; bg2 = bg[2];
+        tfbg = t_final * ((bg[0] * v0 + bg[1] * v1) + bg[2] * v2);
     }
-    float buf0 = 0.f, buf1 = 0.f, buf2 = 0.f;
+    float bufv = 0.f;  // sum_k buffer_k * v_k of the reference's colour accumulator
     if (tid == 0) s_max = range_start - 1;
-#pragma unroll
-    for (int k = 0; k < 9; ++k) s_acc[k][tid] = 0.0f;
+    for (int k = tid; k < kTile * 9; k += kTile) acc[k] = 0.0f;
     __syncthreads();
     atomicMax(&s_max, bin_final);
     // wave-wide largest final index: a record above it has no contributing lane in this wave
@@ -246,113 +325,114 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     // a final_idx from the matching forward lies inside the tile's range; clamp anything else
     const int32_t start_idx = iminw(s_max, range_end - 1);
     const int32_t num_batches = (start_idx - range_start + kTile) / kTile;
-    const uint32_t wbit = 1u << wave;
+    const int row = lane >> 4;
 
     for (int32_t bt = 0; bt < num_batches; ++bt) {
         const int32_t batch_end = start_idx - bt * kTile;
-        {
-            const int32_t src = imaxw(batch_end - tid, range_start);
-            const int64_t g = C.ids[src];
-            const float2 xy = reinterpret_cast<const float2*>(C.xys)[g];
-            const float a = C.conics[3 * g], b = C.conics[3 * g + 1], c = C.conics[3 * g + 2];
-            const float o = C.opac[g % C.rows_opac];
-            const int64_t cg = g % C.rows_colors;
-            float smax;
-            uint32_t qm;
-            stage_bounds(xy.x, xy.y, a, b, c, o, tile_x, tile_y, smax, qm);
-            s_x[tid] = xy.x; s_y[tid] = xy.y;
-            s_a[tid] = a; s_b[tid] = b; s_c[tid] = c; s_o[tid] = o;
-            s_smax[tid] = smax; s_q[tid] = qm; s_id[tid] = (int32_t)g;
-            s_r[tid] = C.colors[3 * cg]; s_g[tid] = C.colors[3 * cg + 1];
-            s_bl[tid] = C.colors[3 * cg + 2];
-        }
-        __syncthreads();
-        const int32_t batch_size = iminw(kTile, batch_end - range_start + 1);
-        for (int32_t t = 0; t < batch_size; ++t) {
+        const int32_t src = imaxw(batch_end - tid, range_start);
+        const int len = stage_batch(C, L, src, batch_end - tid >= range_start, tile_x, tile_y);
+        for (int k = 0; k < len; ++k) {
+            const int t = L.list[wave][k];
             const int32_t idx = batch_end - t;
-            if (idx > wmax || !(s_q[t] & wbit)) continue;  // wave-uniform
-            const float dx = s_x[t] - px, dy = s_y[t] - py;
-            const float a = s_a[t], b = s_b[t], c = s_c[t];
-            const float sigma = 0.5f * (a * dx * dx + c * dy * dy) + b * dx * dy;
-            bool valid = idx <= bin_final && !(sigma > s_smax[t]) && sigma >= 0.0f;
+            if (idx > wmax) continue;  // wave-uniform
+            const float4 r0 = L.r0[t], r1 = L.r1[t];
+            const float dx = r0.x - px, dy = r0.y - py;
+            const float sigma = 0.5f * (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
+            bool valid = idx <= bin_final && sigma >= 0.0f && sigma <= r1.z;
+            if (__ballot(valid) == 0ull) continue;
+            float vis = 0.f, alpha = 0.f;
+            if (valid) {
+                vis = exp_core(-sigma);
+                alpha = minw(kAlphaMax, r1.y * vis);
+                valid = alpha >= kAlphaThresh;
+            }
+            const uint64_t vb = __ballot(valid);
+            if (vb == 0ull) continue;
             float g0 = 0.f, g1 = 0.f, g2 = 0.f, g3 = 0.f, g4 = 0.f, g5 = 0.f, g6 = 0.f, g7 = 0.f,
                   g8 = 0.f;
             if (valid) {
-                const float op = s_o[t];
-                const float vis = det_expf(-sigma);
-                const float alpha = minw(kAlphaMax, op * vis);
-                if (alpha < kAlphaThresh) {
-                    valid = false;
-                } else {
-                    const float cr = s_r[t], cgc = s_g[t], cb = s_bl[t];
-                    const float ra = 1.0f / (1.0f - alpha);
-                    T = T * ra;
-                    const float fac = alpha * T;
-                    float v_alpha = (cr * T - buf0 * ra) * v0;
-                    v_alpha += (cgc * T - buf1 * ra) * v1;
-                    v_alpha += (cb * T - buf2 * ra) * v2;
-                    v_alpha += -t_final * ra * bg0 * v0;
-                    v_alpha += -t_final * ra * bg1 * v1;
-                    v_alpha += -t_final * ra * bg2 * v2;
-                    buf0 = buf0 + cr * fac;
-                    buf1 = buf1 + cgc * fac;
-                    buf2 = buf2 + cb * fac;
-                    g0 = v0 * fac;
-                    g1 = v1 * fac;
-                    g2 = v2 * fac;
-                    if (op * vis <= kAlphaMax) {
-                        const float v_sigma = -op * vis * v_alpha;
-                        g3 = 0.5f * v_sigma * dx * dx;
-                        g4 = v_sigma * dx * dy;
-                        g5 = 0.5f * v_sigma * dy * dy;
-                        g6 = v_sigma * (a * dx + b * dy);
-                        g7 = v_sigma * (b * dx + c * dy);
-                        g8 = vis * v_alpha;
-                    }
+                const float4 r2 = L.r2[t];
+                const float d = 1.0f - alpha;
+                float ra = __builtin_amdgcn_rcpf(d);
+                ra = fmaf(ra, fmaf(-d, ra, 1.0f), ra);
+                T = T * ra;
+                const float fac = alpha * T;
+                const float cv = fmaf(r2.x, v0, fmaf(r2.y, v1, r2.z * v2));
+                const float v_alpha = fmaf(T, cv, -ra * (bufv + tfbg));
+                bufv = fmaf(cv, fac, bufv);
+                g0 = v0 * fac;
+                g1 = v1 * fac;
+                g2 = v2 * fac;
+                const float ov = r1.y * vis;
+                if (ov <= kAlphaMax) {
+                    const float vs = -ov * v_alpha;
+                    const float hx = vs * dx, hy = vs * dy;
+                    g3 = 0.5f * hx * dx;
+                    g4 = hx * dy;
+                    g5 = 0.5f * hy * dy;
+                    g6 = hx;
+                    g7 = hy;
+                    g8 = vis * v_alpha;
                 }
             }
-            if (__ballot(valid) == 0ull) continue;
-            const float r0 = wave_sum_to_lane63(g0), r1 = wave_sum_to_lane63(g1);
-            const float r2 = wave_sum_to_lane63(g2), r3 = wave_sum_to_lane63(g3);
-            const float r4 = wave_sum_to_lane63(g4), r5 = wave_sum_to_lane63(g5);
-            const float r6 = wave_sum_to_lane63(g6), r7 = wave_sum_to_lane63(g7);
-            const float r8 = wave_sum_to_lane63(g8);
-            if (lane == 63) {
-                atomicAdd(&s_acc[0][t], r0); atomicAdd(&s_acc[1][t], r1);
-                atomicAdd(&s_acc[2][t], r2); atomicAdd(&s_acc[3][t], r3);
-                atomicAdd(&s_acc[4][t], r4); atomicAdd(&s_acc[5][t], r5);
-                atomicAdd(&s_acc[6][t], r6); atomicAdd(&s_acc[7][t], r7);
-                atomicAdd(&s_acc[8][t], r8);
+            float* a = &ACC(t, 0);
+            if (__popcll(vb) <= 2) {
+                // few contributors: add straight into LDS (at most two lanes per address)
+                if (valid) {
+                    atomicAdd(a + 0, g0); atomicAdd(a + 1, g1); atomicAdd(a + 2, g2);
+                    atomicAdd(a + 3, g3); atomicAdd(a + 4, g4); atomicAdd(a + 5, g5);
+                    atomicAdd(a + 6, g6); atomicAdd(a + 7, g7); atomicAdd(a + 8, g8);
+                }
+                continue;
+            }
+            // reduce-scatter over the wave: after the swaps, row r of qa holds g0/g2/g1/g3 and
+            // of qb g4/g6/g5/g7 (rows 0..3), qc holds g8 in every row; row sums land in lane 15.
+            const float p01 = swap32_add(g0, g1), p23 = swap32_add(g2, g3);
+            const float p45 = swap32_add(g4, g5), p67 = swap32_add(g6, g7);
+            const float p8 = swap32_add(g8, g8);
+            float qa = swap16_add(p01, p23), qb = swap16_add(p45, p67), qc = swap16_add(p8, p8);
+            qa = row_sum_to_lane15(qa);
+            qb = row_sum_to_lane15(qb);
+            qc = row_sum_to_lane15(qc);
+            if ((lane & 15) == 15) {
+                const int ka = (row == 0) ? 0 : (row == 1) ? 2 : (row == 2) ? 1 : 3;
+                atomicAdd(a + ka, qa);
+                atomicAdd(a + 4 + ka, qb);
+                if (row == 0) atomicAdd(a + 8, qc);
             }
         }
         __syncthreads();
-        if (tid < batch_size) {
-            const int64_t og = og_base + s_id[tid];
-            float acc[9];
+        {
+            const float4 r0 = L.r0[tid], r1 = L.r1[tid], r2 = L.r2[tid];
+            float s[9];
 #pragma unroll
             for (int k = 0; k < 9; ++k) {
-                acc[k] = s_acc[k][tid];
-                s_acc[k][tid] = 0.0f;
+                s[k] = ACC(tid, k);
+                ACC(tid, k) = 0.0f;
             }
-            if (acc[0] != 0.f || acc[1] != 0.f || acc[2] != 0.f) {
-                atomicAdd(P.v_colors + 3 * og, acc[0]);
-                atomicAdd(P.v_colors + 3 * og + 1, acc[1]);
-                atomicAdd(P.v_colors + 3 * og + 2, acc[2]);
+            const int64_t og = og_base + __float_as_int(r2.w);
+            if (s[0] != 0.f || s[1] != 0.f || s[2] != 0.f) {
+                atomicAdd(P.v_colors + 3 * og, s[0]);
+                atomicAdd(P.v_colors + 3 * og + 1, s[1]);
+                atomicAdd(P.v_colors + 3 * og + 2, s[2]);
             }
-            if (acc[3] != 0.f || acc[4] != 0.f || acc[5] != 0.f) {
-                atomicAdd(P.v_conic + 3 * og, acc[3]);
-                atomicAdd(P.v_conic + 3 * og + 1, acc[4]);
-                atomicAdd(P.v_conic + 3 * og + 2, acc[5]);
+            if (s[3] != 0.f || s[4] != 0.f || s[5] != 0.f) {
+                atomicAdd(P.v_conic + 3 * og, s[3]);
+                atomicAdd(P.v_conic + 3 * og + 1, s[4]);
+                atomicAdd(P.v_conic + 3 * og + 2, s[5]);
             }
-            if (acc[6] != 0.f || acc[7] != 0.f) {
-                atomicAdd(P.v_xy + 2 * og, acc[6]);
-                atomicAdd(P.v_xy + 2 * og + 1, acc[7]);
+            if (s[6] != 0.f || s[7] != 0.f) {
+                // v_xy = sum v_sigma (a dx + b dy, b dx + c dy) with (a, b, c) fixed per record
+                atomicAdd(P.v_xy + 2 * og, r0.z * s[6] + r0.w * s[7]);
+                atomicAdd(P.v_xy + 2 * og + 1, r0.w * s[6] + r1.x * s[7]);
             }
-            if (acc[8] != 0.f) atomicAdd(P.v_opacity + og, acc[8]);
+            if (s[8] != 0.f) atomicAdd(P.v_opacity + og, s[8]);
         }
         __syncthreads();
     }
 }
+
+#undef ACC
 
 int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, const BlendBwdArgs& a, hipStream_t stream) {
@@ -365,13 +445,7 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
     const int64_t blocks = (int64_t)a.B_out * lay.num_tiles;
     if (blocks <= 0 || sorted_ids == nullptr) return 0;
     BlendBwdParams P;
-    P.c.colors = in.colors; P.c.rows_colors = in.rows_colors;
-    P.c.opac = in.opac; P.c.rows_opac = in.rows_opac;
-    P.c.background = in.background; P.c.rows_bg = in.rows_bg;
-    P.c.xys = in.xys; P.c.conics = in.conics;
-    P.c.ids = sorted_ids; P.c.bins = tile_bins;
-    P.c.img_h = in.img_h; P.c.img_w = in.img_w;
-    P.c.tiles_x = lay.tiles_x; P.c.num_tiles = lay.num_tiles;
+    fill_common(P.c, in, lay, sorted_ids, tile_bins);
     P.final_Ts = a.final_Ts; P.final_idx = a.final_idx;
     P.v_out = a.v_out; P.vout_rows = a.vout_rows;
     P.n = in.n; P.sel_geom = in.B_geom > 1;

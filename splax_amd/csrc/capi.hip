@@ -508,6 +508,89 @@ int splat_rasterize_fwd(splat_stream_t stream, const float* colors, int64_t rows
     return 0;
 }
 
+int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t rows_colors,
+                             const float* opacities, int64_t rows_opac,
+                             const float* map_opacities, int64_t rows_map_opac,
+                             const float* background, int64_t rows_bg, const float* xys,
+                             const float* depths, const int32_t* radii, const float* conics,
+                             const int32_t* cum_tiles_hit, int32_t num_gaussians, int32_t B,
+                             int32_t img_h, int32_t img_w, int64_t num_intersects,
+                             float* final_Ts, int32_t* final_idx, float* out_img,
+                             int32_t* sorted_ids, int32_t* tile_bins) {
+    RasterInputs in{};
+    in.colors = colors; in.rows_colors = rows_colors;
+    in.opac = opacities; in.rows_opac = rows_opac;
+    in.map_opac = map_opacities; in.rows_map_opac = rows_map_opac;
+    in.background = background; in.rows_bg = rows_bg;
+    in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
+    in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B;
+    in.img_h = img_h; in.img_w = img_w;
+    int rc = check_raster(in);
+    if (rc) return rc;
+    if (num_intersects < 0 || !tile_bins || (num_intersects > 0 && !sorted_ids))
+        return fail(kErrArgs, "rasterize_fwd_keep: missing sorted-list buffers");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    DeviceScratch& sc = scratch_for_current_device();
+    std::lock_guard<std::mutex> lock(sc.mu);
+    rc = sc.ensure_base();
+    if (!rc) {
+        const int32_t bpi = (num_gaussians + 4095) / 4096;
+        rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * B);
+    }
+    if (rc) return rc;
+    SortTargets tgt;
+    tgt.M_known = num_intersects;
+    tgt.ids = sorted_ids;
+    tgt.bins = tile_bins;
+    int64_t M = 0;
+    KeyLayout L;
+    rc = run_sort_and_bin(in, sc, s, &M, &L, &tgt);
+    if (rc) return rc;
+    StageTimer tm(s, kStageBlendFwd);
+    rc = launch_blend_fwd(in, L, M > 0 ? sorted_ids : nullptr, tile_bins, final_Ts, final_idx,
+                          out_img, s);
+    if (rc) return fail(rc, "blend_fwd launch failed");
+    return 0;
+}
+
+int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64_t rows_colors,
+                               const float* opacities, int64_t rows_opac,
+                               const float* background, int64_t rows_bg, const float* xys,
+                               const float* conics, const int32_t* sorted_ids,
+                               const int32_t* tile_bins, int64_t num_intersects,
+                               const float* final_Ts, const int32_t* final_idx,
+                               const float* v_out_img, int64_t vout_rows, int32_t num_gaussians,
+                               int32_t B_out, int32_t B_geom, int32_t img_h, int32_t img_w,
+                               float* v_colors, float* v_opacity, float* v_xy, float* v_conic) {
+    RasterInputs in{};
+    in.colors = colors; in.rows_colors = rows_colors;
+    in.opac = opacities; in.rows_opac = rows_opac;
+    in.map_opac = opacities; in.rows_map_opac = rows_opac;
+    in.background = background; in.rows_bg = rows_bg;
+    in.xys = xys; in.depths = nullptr; in.radii = nullptr; in.conics = conics;
+    in.cum = nullptr; in.n = num_gaussians; in.B_geom = B_geom;
+    in.img_h = img_h; in.img_w = img_w;
+    int rc = check_raster(in);
+    if (rc) return rc;
+    if (B_out <= 0 || (B_geom > 1 && B_geom != B_out))
+        return fail(kErrArgs, "rasterize_bwd_sorted: B_geom must be 1 or equal to B_out");
+    if (vout_rows <= 0 || num_intersects < 0 || !tile_bins)
+        return fail(kErrArgs, "rasterize_bwd_sorted: invalid cotangent or sorted lists");
+    if ((int64_t)B_out * num_gaussians >= ((int64_t)1 << 31))
+        return fail(kErrArgs, "rasterize_bwd_sorted: more than 2^31 gradient rows");
+    const KeyLayout L = key_layout(B_geom, img_h, img_w);
+    if (!L.packed) return fail(kErrKeyOverflow, "rasterize_bwd_sorted: key does not pack");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    BlendBwdArgs a;
+    a.final_Ts = final_Ts; a.final_idx = final_idx;
+    a.v_out = v_out_img; a.vout_rows = vout_rows; a.B_out = B_out;
+    a.v_colors = v_colors; a.v_opacity = v_opacity; a.v_xy = v_xy; a.v_conic = v_conic;
+    StageTimer tm(s, kStageBlendBwd);
+    rc = launch_blend_bwd(in, L, num_intersects > 0 ? sorted_ids : nullptr, tile_bins, a, s);
+    if (rc) return fail(rc, "blend_bwd launch failed");
+    return 0;
+}
+
 int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
                         const float* opacities, int64_t rows_opac, const float* map_opacities,
                         int64_t rows_map_opac, const float* background, int64_t rows_bg,

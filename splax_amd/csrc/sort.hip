@@ -350,12 +350,14 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
 
 __global__ void __launch_bounds__(256)
 bin_edges_kernel(const int32_t* keys, int64_t M, int32_t num_tiles, int32_t tile_bits,
-                 int32_t depth_bits, int32_t* bins) {
+                 int32_t depth_bits, int64_t nbins, int32_t* bins) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= M) return;
     const int32_t mask = (1 << tile_bits) - 1;
     const int32_t key = keys[idx] >> depth_bits;
     const int32_t cur = (key >> tile_bits) * num_tiles + (key & mask);
+    // keys emitted from consistent inputs always decode inside [0, nbins)
+    if (cur < 0 || cur >= nbins) return;
     if (idx == 0) {
         bins[2 * cur] = 0;
         return;
@@ -363,7 +365,7 @@ bin_edges_kernel(const int32_t* keys, int64_t M, int32_t num_tiles, int32_t tile
     if (idx == M - 1) bins[2 * cur + 1] = (int32_t)M;
     const int32_t kp = keys[idx - 1] >> depth_bits;
     const int32_t prev = (kp >> tile_bits) * num_tiles + (kp & mask);
-    if (prev != cur) {
+    if (prev != cur && prev >= 0 && prev < nbins) {
         bins[2 * prev + 1] = (int32_t)idx;
         bins[2 * cur] = (int32_t)idx;
     }
@@ -392,7 +394,7 @@ KeyLayout key_layout(int32_t B, int32_t img_h, int32_t img_w) {
 }
 
 int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stream,
-                     int64_t* M_out, KeyLayout* lay_out) {
+                     int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt) {
     const int32_t B = in.B_geom;
     const KeyLayout L = key_layout(B, in.img_h, in.img_w);
     *lay_out = L;
@@ -409,15 +411,18 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     const int64_t nbins = (int64_t)B * L.num_tiles;
     int rc = sc.ensure_sort(0, nbins, B);
     if (rc) return rc;
+    int32_t* bins = (tgt && tgt->bins) ? tgt->bins : sc.tile_bins;
+    const bool known = tgt && tgt->M_known >= 0;
     if (total <= 0) {
         *M_out = 0;
-        return fill_zero_i32(sc.tile_bins, 2 * nbins, stream);
+        return fill_zero_i32(bins, 2 * nbins, stream);
     }
-    // The one device-to-host read: the intersection count. The copy is enqueued first; the depth
-    // range launches run while the host waits (splax/_rasterize/_sort/_sort.py:71-96).
-    if (hipMemcpyAsync(sc.pinned_count, in.cum + (total - 1), sizeof(int32_t),
-                       hipMemcpyDeviceToHost, stream) != hipSuccess ||
-        hipEventRecord(sc.count_event, stream) != hipSuccess)
+    // The one device-to-host read: the intersection count (skipped when the caller supplies it).
+    // The copy is enqueued first; the depth range launches run while the host waits
+    // (splax/_rasterize/_sort/_sort.py:71-96).
+    if (!known && (hipMemcpyAsync(sc.pinned_count, in.cum + (total - 1), sizeof(int32_t),
+                                  hipMemcpyDeviceToHost, stream) != hipSuccess ||
+                   hipEventRecord(sc.count_event, stream) != hipSuccess))
         return fail(kErrRuntime, "count readback enqueue failed");
     const int32_t bpi = (int32_t)((in.n + kMmThreads * kMmItems - 1) / (kMmThreads * kMmItems));
     if ((int64_t)bpi * B * 2 > sc.mm_partial_cap)
@@ -430,14 +435,21 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
                            sc.mm_partial, bpi, sc.depth_mm, sc.hist);
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "minmax launch failed");
     }
-    if (hipEventSynchronize(sc.count_event) != hipSuccess)
-        return fail(kErrRuntime, "count readback failed");
-    const int64_t M = *sc.pinned_count;
+    int64_t M;
+    if (known) {
+        M = tgt->M_known;
+    } else {
+        if (hipEventSynchronize(sc.count_event) != hipSuccess)
+            return fail(kErrRuntime, "count readback failed");
+        M = *sc.pinned_count;
+    }
     if (M < 0) return fail(kErrTooMany, "intersection count overflowed int32");
+    if (M >= ((int64_t)1 << 31)) return fail(kErrTooMany, "more than 2^31 - 1 intersections");
     *M_out = M;
     rc = sc.ensure_sort(M, nbins, B);
     if (rc) return rc;
-    if (M == 0) return fill_zero_i32(sc.tile_bins, 2 * nbins, stream);
+    if (M == 0) return fill_zero_i32(bins, 2 * nbins, stream);
+    int32_t* ids_final = (tgt && tgt->ids) ? tgt->ids : sc.vals[0];
 
     {
         StageTimer tm(stream, kStageEmit);
@@ -457,13 +469,15 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         if (hb > 2048) hb = 2048;
         if (hb < 1) hb = 1;
         hipLaunchKernelGGL(digit_hist_kernel, dim3((unsigned)hb), dim3(kHistThreads), 0, stream,
-                           sc.keys[0], M, sc.hist, sc.tile_bins, 2 * nbins);
+                           sc.keys[0], M, sc.hist, bins, 2 * nbins);
         const int64_t parts = (M + kSortTile - 1) / kSortTile;
-        // passes 0..3 ping-pong 0 -> 1 -> 0 -> 1 -> 0 so the result lands back in buffer 0
+        // passes 0..3 ping-pong 0 -> 1 -> 0 -> 1 -> 0; the last pass writes the values straight
+        // into their final buffer (the caller's when it keeps the sorted lists)
         for (int pass = 0; pass < 4; ++pass) {
             const int src = pass & 1, dst = 1 - src;
+            int32_t* vdst = pass == 3 ? ids_final : sc.vals[dst];
             hipLaunchKernelGGL(onesweep_pass_kernel, dim3((unsigned)parts), dim3(kSortThreads), 0,
-                               stream, sc.keys[src], sc.vals[src], sc.keys[dst], sc.vals[dst], M,
+                               stream, sc.keys[src], sc.vals[src], sc.keys[dst], vdst, M,
                                8 * pass, sc.hist + 256 * pass, sc.sort_status,
                                sc.tickets + kTicketSort + pass, sc.next_epoch(),
                                sc.tickets + kDeviceError);
@@ -474,7 +488,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         StageTimer tm(stream, kStageBins);
         hipLaunchKernelGGL(bin_edges_kernel, dim3((unsigned)((M + 255) / 256)), dim3(256), 0,
                            stream, sc.keys[0], M, L.num_tiles, L.tile_bits, L.depth_bits,
-                           sc.tile_bins);
+                           nbins, bins);
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "bins launch failed");
     }
     return 0;

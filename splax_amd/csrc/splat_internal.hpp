@@ -146,10 +146,19 @@ int fill_zero_i32(int32_t* p, int64_t n, hipStream_t stream);
 int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stream);
 int launch_project_bwd(const ProjectBwdArgs& a, hipStream_t stream);
 
-// sort_and_bin: returns M (>= 0) in *M_out; sorted ids in sc.vals[0], keys in sc.keys[0],
-// tile bins in sc.tile_bins.
+// Optional caller-owned destinations of sort_and_bin: M_known >= 0 skips the count readback
+// (it must equal cum[B*n - 1]); ids / bins (when non-null) receive the sorted gaussian ids and
+// the tile bins instead of the library scratch.
+struct SortTargets {
+    int64_t M_known = -1;
+    int32_t* ids = nullptr;
+    int32_t* bins = nullptr;
+};
+
+// sort_and_bin: returns M (>= 0) in *M_out; sorted keys in sc.keys[0]; sorted ids in tgt->ids or
+// sc.vals[0]; tile bins in tgt->bins or sc.tile_bins.
 int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stream,
-                     int64_t* M_out, KeyLayout* lay_out);
+                     int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt = nullptr);
 
 int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,

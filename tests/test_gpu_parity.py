@@ -273,3 +273,33 @@ def test_golden_fixture():
                             B_geom=1, img_shape=(H, W))
     for label, got_g in zip(("v_colors", "v_opac", "v_xy", "v_conic"), gg):
         _grad_compare(_np(got_g).reshape(g[label].shape), g[label], f"golden/{label}")
+
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg2_50k"])
+def test_kept_sort_path_equals_resort_path(name):
+    """fwd_keep returns exactly sort_and_bin's lists; bwd_sorted equals the re-sorting backward."""
+    _case(f"keep/sorted path {name}")
+    s = _scene_arrays(name)
+    xys, depths, radii, conics, nth, cum = _raster_inputs(s)
+    o = _t(s.opacities).reshape(-1)
+    geo = (_t(xys), _t(depths), _t(radii), _t(conics), _t(cum))
+    img, Ts, fidx, ids, bins, M = _ops.rasterize_fwd_keep(_t(s.colors), o, o, _t(s.background),
+                                                          *geo, n=s.n, B=1, img_shape=s.img_shape)
+    rk, rid, rbins = O.sort_and_bin(xys, depths, radii, conics, s.opacities, cum, n=s.n, B=1,
+                                    img_shape=s.img_shape)
+    assert M == rid.size
+    assert_bit_exact(_np(ids)[:M], rid, f"{name}/kept ids")
+    assert_bit_exact(_np(bins), rbins, f"{name}/kept bins")
+    rimg, rT, ridx, _, _ = O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background, xys,
+                                           depths, radii, conics, cum, n=s.n, B=1,
+                                           img_shape=s.img_shape)
+    assert_bit_exact(_np(img), rimg, f"{name}/kept img")
+    H, W = s.img_shape
+    vout = _t((2.0 * (rimg.reshape(H, W, 3) - s.targets[0]) / rimg.size).astype(np.float32))
+    a = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[3], ids, bins, M,
+                                  Ts, fidx, vout.reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
+                                  img_shape=s.img_shape)
+    b = _ops.rasterize_bwd(_t(s.colors), o, o, _t(s.background), *geo, Ts, fidx,
+                           vout.reshape(-1, 3), n=s.n, B_out=1, B_geom=1, img_shape=s.img_shape)
+    for label, x, y in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), a, b):
+        _grad_compare(_np(x), _np(y), f"{name}/{label}")
