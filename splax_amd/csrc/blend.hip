@@ -134,6 +134,10 @@ __device__ __forceinline__ int stage_batch(const BlendCommon& C, BatchLds& L, in
     return len;
 }
 
+// Wave-uniform value as a scalar (the compiler cannot prove uniformity of values derived from
+// threadIdx.x / LDS on its own; scalar loop control avoids exec-mask branching).
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
 // e^x for x in [-88, 0] (no range handling needed there); equal to det_expf on that domain.
 __device__ __forceinline__ float exp_core(float x) {
     float kf = rintf(x * kLog2e);
@@ -182,10 +186,12 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
         if (__syncthreads_count(done) >= kTile) break;
         const int32_t batch_start = range_start + bt * kTile;
         const int32_t src = iminw(batch_start + tid, range_end - 1);
-        const int len = stage_batch(C, L, src, batch_start + tid < range_end, tile_x, tile_y);
+        const int len =
+            uniform(stage_batch(C, L, src, batch_start + tid < range_end, tile_x, tile_y));
         if (__ballot(!done) == 0ull) continue;
+        const uint8_t* list = L.list[uniform(wave)];
         for (int k = 0; k < len; ++k) {
-            const int t = L.list[wave][k];
+            const int t = uniform(list[k]);
             const float4 r0 = L.r0[t], r1 = L.r1[t];
             const float dx = r0.x - px, dy = r0.y - py;
             const float sigma = 0.5f * (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
@@ -321,6 +327,7 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
         int32_t o = __shfl_xor(wmax, off, 64);
         wmax = o > wmax ? o : wmax;
     }
+    wmax = uniform(wmax);
     __syncthreads();
     // a final_idx from the matching forward lies inside the tile's range; clamp anything else
     const int32_t start_idx = iminw(s_max, range_end - 1);
@@ -330,9 +337,11 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     for (int32_t bt = 0; bt < num_batches; ++bt) {
         const int32_t batch_end = start_idx - bt * kTile;
         const int32_t src = imaxw(batch_end - tid, range_start);
-        const int len = stage_batch(C, L, src, batch_end - tid >= range_start, tile_x, tile_y);
+        const int len =
+            uniform(stage_batch(C, L, src, batch_end - tid >= range_start, tile_x, tile_y));
+        const uint8_t* list = L.list[uniform(wave)];
         for (int k = 0; k < len; ++k) {
-            const int t = L.list[wave][k];
+            const int t = uniform(list[k]);
             const int32_t idx = batch_end - t;
             if (idx > wmax) continue;  // wave-uniform
             const float4 r0 = L.r0[t], r1 = L.r1[t];

@@ -108,7 +108,7 @@ int DeviceScratch::grow_scan_status(int64_t blocks) {
 }
 
 int DeviceScratch::ensure_sort(int64_t M, int64_t bins, int32_t B) {
-    const int64_t sort_tile = 256 * 16;
+    const int64_t sort_tile = 256 * 8;  // keys per onesweep partition (sort.hip kSortTile)
     const int64_t mm_blocks = 2 * (int64_t)B * 4096;  // generous partial capacity bound below
     bool need_sync = true;
     auto sync_once = [&]() {

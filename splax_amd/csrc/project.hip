@@ -6,8 +6,8 @@
 // counting tiles it scans its chunk in LDS and resolves its global prefix with a decoupled
 // look-back over the chunks before it, so cum_tiles_hit (the inclusive scan the reference gets
 // from a separate wp.utils.array_scan, splax/_project/_kernels.py:107) is written by the same
-// launch. Chunks are taken in ticket order (atomic counter), so every chunk a workgroup waits on
-// is already running.
+// launch. A chunk is its workgroup index and waits only on lower indices, which in-order
+// workgroup dispatch has already placed on the device; one wave polls 64 predecessors at a time.
 //
 // project_bwd: one thread per flat item, restating _project_bwd_kernel
 // (splax/_project/_kernels.py:356-484); the per-image viewmat gradient is reduced per wave with
@@ -32,7 +32,7 @@ struct ProjectParams {
     float* xys; float* depths; int32_t* radii; float* conics;
     int32_t* num_tiles_hit; int32_t* cum_tiles_hit;
     // scan state
-    uint64_t* status; uint32_t* ticket; uint32_t epoch; uint32_t* err;
+    uint64_t* status; uint32_t epoch; uint32_t* err;
 };
 
 constexpr int kProjThreads = 256;
@@ -188,17 +188,15 @@ __device__ __forceinline__ int32_t project_item(const ProjectParams& P, int64_t 
 }
 
 // Items per thread of the fused projection + scan; one workgroup covers 256 * kProjItems items.
-constexpr int kProjItems = 4;
+// One item per thread keeps the loads coalesced and gives the latency-bound projection the most
+// waves in flight.
+constexpr int kProjItems = 1;
 
 __global__ void __launch_bounds__(kProjThreads) project_fwd_kernel(ProjectParams P) {
-    __shared__ uint32_t s_part;
     __shared__ int32_t s_wave[kProjThreads / 64];
     __shared__ int32_t s_prefix;
     const int tid = threadIdx.x;
-    if (tid == 0) s_part = atomicAdd(P.ticket, 1u);
-    __syncthreads();
-    const uint32_t part = s_part;
-    if (tid == 0 && part == gridDim.x - 1) atomic_store_relaxed(P.ticket, 0u);
+    const uint32_t part = blockIdx.x;
     const int64_t base = (int64_t)part * (kProjThreads * kProjItems);
     // Items are blocked per thread (thread t owns base + t*K .. +K-1) so the per-thread running
     // sum plus one block scan gives the inclusive prefix.
@@ -222,8 +220,10 @@ __global__ void __launch_bounds__(kProjThreads) project_fwd_kernel(ProjectParams
         if (w < wave) wave_off += v;
         block_total += v;
     }
-    if (tid == 0)
-        s_prefix = lookback_single(P.status, part, (uint32_t)block_total, P.epoch, P.err);
+    if (wave == 0) {
+        const uint32_t pre = lookback_wave(P.status, part, (uint32_t)block_total, P.epoch, P.err);
+        if (lane == 0) s_prefix = (int32_t)pre;
+    }
     __syncthreads();
     int32_t run = s_prefix + wave_off + incl - local;
 #pragma unroll
@@ -276,7 +276,10 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
         float vq[4] = {0.f, 0.f, 0.f, 0.f};
         (void)zero3;
         const int64_t r_idx = P.rows_radii > n ? idx : gid;
-        if (P.radii[r_idx] > 0) {
+        // Every input is loaded and the math runs for culled items too (results discarded
+        // below): the loads then issue together instead of waiting on radii first.
+        const bool vis = P.radii[r_idx] > 0;
+        {
             const int64_t m_idx = P.rows_means > n ? idx : gid;
             const int64_t s_idx = P.rows_scales > n ? idx : gid;
             const int64_t q_idx = P.rows_quats > n ? idx : gid;
@@ -402,6 +405,15 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
                 vt[a] = v_p[a];
             }
         }
+        if (!vis) {  // culled items contribute nothing (splax/_project/_kernels.py:408)
+            moved = false;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) vR[k] = vRtf[k] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) vt[k] = vttf[k] = vmean_out[k] = vscale[k] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) vq[k] = 0.0f;
+        }
         P.v_mean3d[3 * idx] = vmean_out[0];
         P.v_mean3d[3 * idx + 1] = vmean_out[1];
         P.v_mean3d[3 * idx + 2] = vmean_out[2];
@@ -490,7 +502,7 @@ int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stre
     P.glob_scale = a.glob_scale; P.clip_thresh = a.clip_thresh;
     P.xys = a.xys; P.depths = a.depths; P.radii = a.radii; P.conics = a.conics;
     P.num_tiles_hit = a.num_tiles_hit; P.cum_tiles_hit = a.cum_tiles_hit;
-    P.status = sc.scan_status; P.ticket = sc.tickets + kTicketScan; P.epoch = sc.next_epoch();
+    P.status = sc.scan_status; P.epoch = sc.next_epoch();
     P.err = sc.tickets + kDeviceError;
     hipLaunchKernelGGL(project_fwd_kernel, dim3((unsigned)blocks), dim3(kProjThreads), 0, stream,
                        P);

@@ -4,12 +4,12 @@
 // radix_sort_pairs (called at splax/_rasterize/_sort/_sort.py:136).
 //
 // Sort design: one global histogram launch counts all four 8-bit digits of every key; then each
-// of the four passes is a single launch in which a workgroup (4 wave64s) takes a 4096-key
-// partition by atomic ticket, ranks its keys stably with ballot-based digit matching per wave,
+// of the four passes is a single launch in which a workgroup (4 wave64s) owns the 2048-key
+// partition of its workgroup index, ranks its keys stably with ballot-based digit matching per wave,
 // publishes its per-digit counts and resolves its global per-digit offsets by decoupled look-back
 // over the partitions before it, and scatters keys and values through LDS so that each digit's
 // run is written contiguously. Ranking follows position order (wave-striped items, lanes in order,
-// waves in order, partitions in ticket order), so the sort is stable: ties keep emission order,
+// waves in order, partitions in index order), so the sort is stable: ties keep emission order,
 // which is the reference's (key, position) order.
 #include "splat_common.hpp"
 #include "splat_internal.hpp"
@@ -164,9 +164,22 @@ __global__ void __launch_bounds__(256) emit_keys_kernel(EmitParams P) {
 // ------------------------------------------------------------------ digit histogram
 
 constexpr int kHistThreads = 256;
+// Workgroups of the histogram launch: each takes one contiguous chunk and adds its 4 x 256 counts
+// with one global atomic per non-zero bin. Same-address device-scope atomics serialise, so the
+// grid is kept small; 128 chunks still spread the read over half the CUs.
+constexpr int kHistBlocks = 128;
+constexpr int kHistChunkAlign = kHistThreads * 4;  // chunk starts stay 16-byte aligned
+
+__device__ __forceinline__ void hist_add(uint32_t* h, uint32_t k) {
+    atomicAdd(&h[k & 255u], 1u);
+    atomicAdd(&h[256 + ((k >> 8) & 255u)], 1u);
+    atomicAdd(&h[512 + ((k >> 16) & 255u)], 1u);
+    atomicAdd(&h[768 + (k >> 24)], 1u);
+}
 
 __global__ void __launch_bounds__(kHistThreads)
-digit_hist_kernel(const int32_t* keys, int64_t M, uint32_t* hist, int32_t* bins, int64_t nbins2) {
+digit_hist_kernel(const int32_t* keys, int64_t M, int64_t chunk, uint32_t* hist, int32_t* bins,
+                  int64_t nbins2) {
     __shared__ uint32_t s_h[kHistThreads / 64][4 * 256];
     const int tid = threadIdx.x, wave = tid >> 6;
     for (int i = tid; i < 4 * 256; i += kHistThreads)
@@ -177,20 +190,39 @@ digit_hist_kernel(const int32_t* keys, int64_t M, uint32_t* hist, int32_t* bins,
          i += (int64_t)gridDim.x * kHistThreads)
         bins[i] = 0;
     __syncthreads();
-    for (int64_t i = (int64_t)blockIdx.x * kHistThreads + tid; i < M;
-         i += (int64_t)gridDim.x * kHistThreads) {
-        uint32_t k = (uint32_t)keys[i];
-        atomicAdd(&s_h[wave][k & 255u], 1u);
-        atomicAdd(&s_h[wave][256 + ((k >> 8) & 255u)], 1u);
-        atomicAdd(&s_h[wave][512 + ((k >> 16) & 255u)], 1u);
-        atomicAdd(&s_h[wave][768 + (k >> 24)], 1u);
+    const int64_t lo = (int64_t)blockIdx.x * chunk;
+    const int64_t hi = lo + chunk < M ? lo + chunk : M;
+    uint32_t* h = s_h[wave];
+    // whole 16-byte groups, four in flight per thread
+    const int64_t nvec = hi > lo ? (hi - lo) >> 2 : 0;
+    const int4* kv = reinterpret_cast<const int4*>(keys + lo);
+    int64_t v = tid;
+    for (; v + 3 * kHistThreads < nvec; v += 4 * kHistThreads) {
+        int4 q[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) q[u] = kv[v + u * kHistThreads];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            hist_add(h, (uint32_t)q[u].x);
+            hist_add(h, (uint32_t)q[u].y);
+            hist_add(h, (uint32_t)q[u].z);
+            hist_add(h, (uint32_t)q[u].w);
+        }
     }
+    for (; v < nvec; v += kHistThreads) {
+        const int4 q = kv[v];
+        hist_add(h, (uint32_t)q.x);
+        hist_add(h, (uint32_t)q.y);
+        hist_add(h, (uint32_t)q.z);
+        hist_add(h, (uint32_t)q.w);
+    }
+    for (int64_t i = lo + 4 * nvec + tid; i < hi; i += kHistThreads) hist_add(h, (uint32_t)keys[i]);
     __syncthreads();
     for (int i = tid; i < 4 * 256; i += kHistThreads) {
-        uint32_t v = 0;
+        uint32_t c = 0;
 #pragma unroll
-        for (int w = 0; w < kHistThreads / 64; ++w) v += s_h[w][i];
-        if (v) atomicAdd(hist + i, v);
+        for (int w = 0; w < kHistThreads / 64; ++w) c += s_h[w][i];
+        if (c) atomicAdd(hist + i, c);
     }
 }
 
@@ -198,7 +230,7 @@ digit_hist_kernel(const int32_t* keys, int64_t M, uint32_t* hist, int32_t* bins,
 
 constexpr int kSortThreads = 256;
 constexpr int kSortWaves = kSortThreads / 64;
-constexpr int kSortItems = 16;
+constexpr int kSortItems = 8;
 constexpr int kSortTile = kSortThreads * kSortItems;
 
 // Exclusive scan of one value per thread over a 256-thread workgroup.
@@ -229,29 +261,29 @@ __global__ void __launch_bounds__(kSortThreads)
 onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
                      int32_t* __restrict__ keys_out, int32_t* __restrict__ vals_out, int64_t M,
                      int shift, const uint32_t* __restrict__ hist, uint64_t* status,
-                     uint32_t* ticket, uint32_t epoch, uint32_t* err) {
-    __shared__ uint32_t s_buf[kSortTile];
+                     uint32_t epoch, uint32_t* err) {
+    __shared__ uint32_t s_keys[kSortTile];
+    __shared__ uint32_t s_vals[kSortTile];
     __shared__ uint32_t s_cnt[kSortWaves][256];
     __shared__ uint32_t s_local_start[256];
-    __shared__ int64_t s_dest_base[256];
+    __shared__ int32_t s_dest_base[256];
     __shared__ uint32_t s_tmp[kSortWaves];
-    __shared__ uint32_t s_part;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) s_part = atomicAdd(ticket, 1u);
 #pragma unroll
     for (int w = 0; w < kSortWaves; ++w) s_cnt[w][tid] = 0u;
     __syncthreads();
-    const uint32_t part = s_part;
-    if (tid == 0 && part == gridDim.x - 1) atomic_store_relaxed(ticket, 0u);
+    const uint32_t part = blockIdx.x;
     const int64_t base = (int64_t)part * kSortTile;
     const int64_t wbase = base + (int64_t)wave * (kSortItems * 64);
 
-    uint32_t key[kSortItems];
+    // keys and values are both loaded up front so their latencies overlap
+    uint32_t key[kSortItems], val[kSortItems];
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
         int64_t pos = wbase + i * 64 + lane;
         key[i] = pos < M ? (uint32_t)keys_in[pos] : 0xffffffffu;
+        val[i] = pos < M ? (uint32_t)vals_in[pos] : 0u;
     }
 
     // stable per-wave ranking: lanes with equal digits found by 8 ballots
@@ -292,7 +324,10 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
     const uint32_t local_start = block_exclusive_scan_256(tot, s_tmp, nullptr);
     const uint32_t global_start = block_exclusive_scan_256(hist[d], s_tmp, nullptr);
     s_local_start[d] = local_start;
-    // decoupled look-back for digit d
+    // Decoupled look-back for digit d. Predecessors are polled four at a time (independent
+    // device-scope loads, one round trip per window) and folded nearest first until an inclusive
+    // prefix is found. Only lower workgroup indices are awaited, and in-order workgroup dispatch
+    // has placed them on the device already.
     uint64_t* st = status + d;
     uint32_t prefix = 0;
     if (part == 0) {
@@ -300,47 +335,58 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
     } else {
         atomic_store_relaxed(st + (int64_t)part * 256, status_word(epoch, false, tot));
         int64_t j = (int64_t)part - 1;
+        uint32_t spins = 0;
         while (j >= 0) {
-            uint64_t s = wait_status(st + j * 256, epoch, err);
-            prefix += (uint32_t)(s & 0x7fffffffull);
-            if (s & kInclusiveBit) break;
-            --j;
+            uint64_t w[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                w[k] = (j - k >= 0) ? atomic_load_relaxed(st + (j - k) * 256)
+                                    : status_word(epoch, true, 0u);
+            int consumed = 0;
+            bool found = false;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (found || consumed < k) continue;  // stop at the first gap or inclusive
+                if ((uint32_t)(w[k] >> 32) != epoch) continue;
+                prefix += (uint32_t)(w[k] & 0x7fffffffull);
+                consumed = k + 1;
+                found = (w[k] & kInclusiveBit) != 0;
+            }
+            if (found) break;
+            if (consumed == 0) {
+                if (++spins >= kSpinLimit) {
+                    atomicOr(err, kDevErrLookback);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            j -= consumed;
         }
         atomic_store_relaxed(st + (int64_t)part * 256, status_word(epoch, true, prefix + tot));
     }
-    s_dest_base[d] = (int64_t)global_start + prefix - local_start;
+    s_dest_base[d] = (int32_t)((int64_t)global_start + prefix - local_start);
     __syncthreads();
 
-    // keys into LDS at their partition-sorted slot
-    uint32_t slot[kSortItems];
+    // keys and values into LDS at their partition-sorted slot
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
         const uint32_t dd = (key[i] >> shift) & 255u;
-        slot[i] = s_local_start[dd] + s_cnt[wave][dd] + rank[i];
-        s_buf[slot[i]] = key[i];
+        const uint32_t slot = s_local_start[dd] + s_cnt[wave][dd] + rank[i];
+        s_keys[slot] = key[i];
+        s_vals[slot] = val[i];
     }
     __syncthreads();
+    // each digit's run is contiguous in the output: consecutive j write consecutive addresses
     const int64_t valid = (M - base) < kSortTile ? (M - base) : kSortTile;
-    int64_t dest[kSortItems];
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
         const int j = r * kSortThreads + tid;
-        const uint32_t k = s_buf[j];
-        dest[r] = s_dest_base[(k >> shift) & 255u] + j;
-        if (j < valid) keys_out[dest[r]] = (int32_t)k;
-    }
-    __syncthreads();
-    // values through the same permutation
-#pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
-        int64_t pos = wbase + i * 64 + lane;
-        s_buf[slot[i]] = pos < M ? (uint32_t)vals_in[pos] : 0u;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kSortItems; ++r) {
-        const int j = r * kSortThreads + tid;
-        if (j < valid) vals_out[dest[r]] = (int32_t)s_buf[j];
+        if (j < valid) {
+            const uint32_t k = s_keys[j];
+            const int64_t dest = (int64_t)s_dest_base[(k >> shift) & 255u] + j;
+            keys_out[dest] = (int32_t)k;
+            vals_out[dest] = (int32_t)s_vals[j];
+        }
     }
 }
 
@@ -465,11 +511,11 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     }
     {
         StageTimer tm(stream, kStageSort);
-        int64_t hb = (M + kHistThreads * 16 - 1) / (kHistThreads * 16);
-        if (hb > 2048) hb = 2048;
-        if (hb < 1) hb = 1;
+        int64_t chunk = (M + kHistBlocks - 1) / kHistBlocks;
+        chunk = (chunk + kHistChunkAlign - 1) / kHistChunkAlign * kHistChunkAlign;
+        const int64_t hb = (M + chunk - 1) / chunk;
         hipLaunchKernelGGL(digit_hist_kernel, dim3((unsigned)hb), dim3(kHistThreads), 0, stream,
-                           sc.keys[0], M, sc.hist, bins, 2 * nbins);
+                           sc.keys[0], M, chunk, sc.hist, bins, 2 * nbins);
         const int64_t parts = (M + kSortTile - 1) / kSortTile;
         // passes 0..3 ping-pong 0 -> 1 -> 0 -> 1 -> 0; the last pass writes the values straight
         // into their final buffer (the caller's when it keeps the sorted lists)
@@ -478,8 +524,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
             int32_t* vdst = pass == 3 ? ids_final : sc.vals[dst];
             hipLaunchKernelGGL(onesweep_pass_kernel, dim3((unsigned)parts), dim3(kSortThreads), 0,
                                stream, sc.keys[src], sc.vals[src], sc.keys[dst], vdst, M,
-                               8 * pass, sc.hist + 256 * pass, sc.sort_status,
-                               sc.tickets + kTicketSort + pass, sc.next_epoch(),
+                               8 * pass, sc.hist + 256 * pass, sc.sort_status, sc.next_epoch(),
                                sc.tickets + kDeviceError);
         }
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "sort launch failed");

@@ -77,11 +77,9 @@ struct RasterInputs {
     int32_t n, B_geom, img_h, img_w;
 };
 
-// ------------------------------------------------------------------ tickets / scratch
+// ------------------------------------------------------------------ device words / scratch
 enum : int {
-    kTicketScan = 0,
-    kTicketSort = 40,    // + pass index (4)
-    kDeviceError = 63,   // device error word (bit flags, see kDevErr*)
+    kDeviceError = 63,   // device error word in `tickets` (bit flags, see kDevErr*)
     kNumTickets = 64,
 };
 
@@ -200,35 +198,49 @@ __device__ __forceinline__ uint64_t status_word(uint32_t epoch, bool inclusive, 
 constexpr uint32_t kSpinLimit = 1u << 22;
 enum : uint32_t { kDevErrLookback = 1u };
 
-// Polls status[j] until it carries `epoch`; returns the word, or 0 on timeout (error recorded).
-__device__ __forceinline__ uint64_t wait_status(const uint64_t* p, uint32_t epoch, uint32_t* err) {
-    for (uint32_t spin = 0; spin < kSpinLimit; ++spin) {
-        uint64_t s = atomic_load_relaxed(p);
-        if ((uint32_t)(s >> 32) == epoch) return s;
-        __builtin_amdgcn_s_sleep(1);
-    }
-    atomicOr(err, kDevErrLookback);
-    return kInclusiveBit;  // treat as an inclusive prefix of 0 so the walk ends
-}
-
-// Single-value decoupled look-back (one thread). Publishes this chunk's aggregate, walks back
-// to the nearest inclusive prefix and publishes its own; returns the exclusive prefix.
-__device__ __forceinline__ uint32_t lookback_single(uint64_t* status, uint32_t part, uint32_t agg,
-                                                    uint32_t epoch, uint32_t* err) {
+// Single-value decoupled look-back run by one whole wave (all 64 lanes call it; the result is
+// wave-uniform). Publishes this chunk's aggregate, then polls 64 predecessors per round trip
+// (lane l reads chunk j - l): the run of published words nearest to the chunk is folded in, up to
+// and including the first inclusive prefix; a gap means a predecessor has not published yet, so
+// the wave waits and re-polls from the gap. Publishes its own inclusive prefix and returns the
+// exclusive one. Chunk indices are workgroup indices; a chunk only waits on lower indices, which
+// in-order workgroup dispatch has already placed on the device.
+__device__ __forceinline__ uint32_t lookback_wave(uint64_t* status, uint32_t part, uint32_t agg,
+                                                  uint32_t epoch, uint32_t* err) {
+    const int lane = threadIdx.x & 63;
     if (part == 0) {
-        atomic_store_relaxed(status, status_word(epoch, true, agg));
+        if (lane == 0) atomic_store_relaxed(status, status_word(epoch, true, agg));
         return 0;
     }
-    atomic_store_relaxed(status + part, status_word(epoch, false, agg));
-    uint32_t prefix = 0;
+    if (lane == 0) atomic_store_relaxed(status + part, status_word(epoch, false, agg));
+    uint32_t prefix = 0, spins = 0;
     int64_t j = (int64_t)part - 1;
-    while (j >= 0) {
-        uint64_t s = wait_status(status + j, epoch, err);
-        prefix += (uint32_t)(s & 0x7fffffffull);
-        if (s & kInclusiveBit) break;
-        --j;
+    for (;;) {
+        const int64_t q = j - lane;
+        // positions before chunk 0 read as an inclusive prefix of 0, so every walk ends there
+        const uint64_t w = q >= 0 ? atomic_load_relaxed(status + q) : status_word(epoch, true, 0u);
+        const bool valid = (uint32_t)(w >> 32) == epoch;
+        const uint64_t invalid = __ballot(!valid);
+        const uint64_t incl = __ballot(valid && (w & kInclusiveBit) != 0);
+        const int first_gap = invalid ? __builtin_ctzll(invalid) : 64;
+        const int first_incl = incl ? __builtin_ctzll(incl) : 64;
+        const bool done = first_incl < first_gap;
+        const int take = done ? first_incl + 1 : first_gap;  // lanes [0, take) are folded in
+        uint32_t v = lane < take ? (uint32_t)(w & 0x7fffffffull) : 0u;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        prefix += v;
+        if (done) break;
+        if (take == 0) {
+            if (++spins >= kSpinLimit) {
+                if (lane == 0) atomicOr(err, kDevErrLookback);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        j -= take;
     }
-    atomic_store_relaxed(status + part, status_word(epoch, true, prefix + agg));
+    if (lane == 0) atomic_store_relaxed(status + part, status_word(epoch, true, prefix + agg));
     return prefix;
 }
 
