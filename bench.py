@@ -40,7 +40,25 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=None)
     ap.add_argument("--fwd-only", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="end with three plain 256 MiB device copies (counter calibration for "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE runs)")
     return ap.parse_args()
+
+
+def profiled_traffic(kernel, config):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary, or None.
+
+    profiles/<kernel>_config<k>_hbm_traffic.md holds a line
+    `traffic_bytes_per_launch: <int>` (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the
+    counter's reading for a copy of known size)."""
+    path = ROOT / "profiles" / f"{kernel}_config{config}_hbm_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def oracle_leg(scene, threads):
@@ -170,11 +188,12 @@ def main():
         achieved = work / dur_s if dur_s > 0 else 0.0
         roofline = {"kernel": dom, "bound": bound, "achieved": round(achieved, 3),
                     "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
-                    "traffic": None, "avg_launch_ms": round(per_stage[dom], 4),
+                    "traffic": profiled_traffic(dom, args.config),
+                    "avg_launch_ms": round(per_stage[dom], 4),
                     "work_per_launch": work * (1e12 if unit == "TFLOP/s" else 1e9)}
 
     out = {
-        "metric": "fwd+bwd frames/sec @1M gaussians 1080p (fwd frames/sec alongside)",
+        "metric": "fwd and fwd+bwd frames/sec @1M gaussians 1080p; HBM GB/s & VALU % of peak",
         "value": round(1e3 / ms, 3),
         "unit": "frames/s",
         "n_gpus": 1,
@@ -195,7 +214,13 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(out))
+    print(json.dumps(out), flush=True)
+    if args.calibrate_copy:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
 
 
 if __name__ == "__main__":
