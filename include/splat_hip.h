@@ -77,7 +77,9 @@ int splat_rasterize_fwd(splat_stream_t stream, const float* colors, int64_t rows
  * recomputes sort_and_bin over the B_geom geometry images (deterministic, so it reproduces the
  * forward order) and runs the backward blend over B_out output images. v_out_img has vout_rows
  * rows of width W (B_out*H batched or H broadcast). Outputs (B_out * num_gaussians rows, fully
- * written): v_colors [.,3], v_opacity [.], v_xy [.,2], v_conic [.,3]. */
+ * written): v_colors [.,3], v_opacity [.], v_xy [.,2], v_conic [.,3]. No global float atomics:
+ * each intersection's sums are stored at its emission position and added per item in a fixed
+ * order. */
 int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
                         const float* opacities, int64_t rows_opac, const float* map_opacities,
                         int64_t rows_map_opac, const float* background, int64_t rows_bg,
@@ -91,8 +93,10 @@ int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows
 /* Forward that keeps the sorted intersection lists resident for the backward (no counterpart in
  * the reference, whose backward re-sorts, splax/_rasterize/_kernels.py:422): the caller passes
  * num_intersects = cum_tiles_hit[B*n-1] (so the library skips its own device-to-host read) and
- * buffers sorted_ids [num_intersects] and tile_bins [B*num_tiles, 2], which receive exactly what
- * splat_sort_and_bin would return. Other arguments and outputs as splat_rasterize_fwd. */
+ * buffers sorted_ids [num_intersects], sorted_pos [num_intersects] and tile_bins
+ * [B*num_tiles, 2]. sorted_ids and tile_bins receive exactly what splat_sort_and_bin returns;
+ * sorted_pos receives each sorted intersection's emission position (its index in the
+ * cum_tiles_hit-ordered emission sequence). Other arguments and outputs as splat_rasterize_fwd. */
 int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t rows_colors,
                              const float* opacities, int64_t rows_opac,
                              const float* map_opacities, int64_t rows_map_opac,
@@ -101,15 +105,17 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
                              const int32_t* cum_tiles_hit, int32_t num_gaussians, int32_t B,
                              int32_t img_h, int32_t img_w, int64_t num_intersects,
                              float* final_Ts, int32_t* final_idx, float* out_img,
-                             int32_t* sorted_ids, int32_t* tile_bins);
+                             int32_t* sorted_ids, int32_t* sorted_pos, int32_t* tile_bins);
 
 /* Backward over the sorted lists kept by splat_rasterize_fwd_keep (no re-sort). Arguments as
- * splat_rasterize_bwd plus sorted_ids / tile_bins / num_intersects of the matching forward; the
- * outputs equal splat_rasterize_bwd's up to float-atomic ordering. */
+ * splat_rasterize_bwd plus sorted_ids / sorted_pos / tile_bins / num_intersects of the matching
+ * forward; the outputs equal splat_rasterize_bwd's (same kernels; additions can differ in order
+ * only among a tile's four quadrant waves). */
 int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64_t rows_colors,
                                const float* opacities, int64_t rows_opac,
                                const float* background, int64_t rows_bg, const float* xys,
-                               const float* conics, const int32_t* sorted_ids,
+                               const float* conics, const int32_t* cum_tiles_hit,
+                               const int32_t* sorted_ids, const int32_t* sorted_pos,
                                const int32_t* tile_bins, int64_t num_intersects,
                                const float* final_Ts, const int32_t* final_idx,
                                const float* v_out_img, int64_t vout_rows, int32_t num_gaussians,

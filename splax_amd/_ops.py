@@ -112,7 +112,8 @@ def rasterize_fwd(colors, opac, map_opac, background, xys, depths, radii, conics
 
 def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, conics, cum, *, n,
                        B, img_shape):
-    """Forward that also returns the sorted gaussian ids and tile bins (kept for the backward).
+    """Forward that also returns the sorted gaussian ids, their emission positions and the tile
+    bins (kept for the backward).
 
     The intersection count is read here (one device-to-host sync, the same one the reference
     makes inside sort_and_bin) so the buffers can be sized before the launch.
@@ -128,6 +129,7 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
     fidx = torch.empty((B * H, W), device=dev, dtype=torch.int32)
     img = torch.empty((B * H, W, 3), device=dev, dtype=torch.float32)
     ids = torch.empty((max(M, 1),), device=dev, dtype=torch.int32)
+    pos = torch.empty((max(M, 1),), device=dev, dtype=torch.int32)
     bins = torch.empty((B * tiles, 2), device=dev, dtype=torch.int32)
     p = _lib.ptr
     with torch.cuda.device(dev):
@@ -135,18 +137,19 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
             _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
             p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys),
             p(depths), p(radii), p(conics), p(cum), n, B, H, W, M, p(Ts), p(fidx), p(img),
-            p(ids), p(bins))
+            p(ids), p(pos), p(bins))
     _lib.check(st, "rasterize")
-    return img, Ts, fidx, ids, bins, M
+    return img, Ts, fidx, ids, pos, bins, M
 
 
-def rasterize_bwd_sorted(colors, opac, background, xys, conics, ids, bins, M, final_Ts,
+def rasterize_bwd_sorted(colors, opac, background, xys, conics, cum, ids, pos, bins, M, final_Ts,
                          final_idx, v_out, *, n, B_out, B_geom, img_shape):
     """Backward over the sorted lists of rasterize_fwd_keep (no re-sort)."""
     colors, opac, background, xys, conics, final_Ts, v_out = map(
         _f32, (colors, opac, background, xys, conics, final_Ts, v_out))
-    ids, bins, final_idx = _i32(ids), _i32(bins), _i32(final_idx)
-    dev = _lib.require_gpu(colors, opac, xys, conics, ids, bins, final_Ts, final_idx, v_out)
+    cum, ids, pos, bins, final_idx = _i32(cum), _i32(ids), _i32(pos), _i32(bins), _i32(final_idx)
+    dev = _lib.require_gpu(colors, opac, xys, conics, cum, ids, pos, bins, final_Ts, final_idx,
+                           v_out)
     H, W = img_shape
     nout = B_out * n
     v_colors = torch.empty((nout, 3), device=dev, dtype=torch.float32)
@@ -157,7 +160,8 @@ def rasterize_bwd_sorted(colors, opac, background, xys, conics, ids, bins, M, fi
     with torch.cuda.device(dev):
         st = _lib.lib().splat_rasterize_bwd_sorted(
             _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
-            p(background), rows(background, 3), p(xys), p(conics), p(ids), p(bins), M,
+            p(background), rows(background, 3), p(xys), p(conics), p(cum), p(ids), p(pos),
+            p(bins), M,
             p(final_Ts), p(final_idx), p(v_out), v_out.numel() // (3 * W), n, B_out, B_geom, H, W,
             p(v_colors), p(v_opac), p(v_xy), p(v_conic))
     _lib.check(st, "rasterize_bwd")

@@ -48,11 +48,12 @@ class _RasterizeFn(torch.autograd.Function):
         n, B, img_shape = statics
         # The sorted lists stay resident for the backward (the reference re-sorts there,
         # splax/_rasterize/_kernels.py:422); the sort is deterministic, so both are identical.
-        img, Ts, fidx, ids, bins, M = _ops.rasterize_fwd_keep(
+        img, Ts, fidx, ids, pos, bins, M = _ops.rasterize_fwd_keep(
             colors.reshape(-1, 3), opac.reshape(-1), map_opac.reshape(-1),
             background.reshape(-1, 3), xys.reshape(-1, 2), depths.reshape(-1), radii.reshape(-1),
             conics.reshape(-1, 3), cum.reshape(-1), n=n, B=B, img_shape=img_shape)
-        ctx.save_for_backward(colors, opac, background, xys, conics, Ts, fidx, ids, bins)
+        ctx.save_for_backward(colors, opac, background, xys, conics, cum, Ts, fidx, ids, pos,
+                              bins)
         ctx.statics = statics
         ctx.num_intersects = M
         ctx.mark_non_differentiable(Ts, fidx)
@@ -60,14 +61,15 @@ class _RasterizeFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, v_img, _v_Ts, _v_idx):
-        colors, opac, background, xys, conics, Ts, fidx, ids, bins = ctx.saved_tensors
+        colors, opac, background, xys, conics, cum, Ts, fidx, ids, pos, bins = ctx.saved_tensors
         n, B, img_shape = ctx.statics
         if v_img is None:
             v_img = torch.zeros((B * img_shape[0], img_shape[1], 3), device=xys.device)
         v_colors, v_opac, v_xy, v_conic = _ops.rasterize_bwd_sorted(
             colors.reshape(-1, 3), opac.reshape(-1), background.reshape(-1, 3),
-            xys.reshape(-1, 2), conics.reshape(-1, 3), ids, bins, ctx.num_intersects, Ts, fidx,
-            v_img.reshape(-1, 3), n=n, B_out=B, B_geom=B, img_shape=img_shape)
+            xys.reshape(-1, 2), conics.reshape(-1, 3), cum.reshape(-1), ids, pos, bins,
+            ctx.num_intersects, Ts, fidx, v_img.reshape(-1, 3), n=n, B_out=B, B_geom=B,
+            img_shape=img_shape)
 
         def fold(g: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
             if like.numel() == g.numel():

@@ -16,9 +16,12 @@
 // Backward: the same staging walked back to front from the workgroup's largest final_idx. A
 // pixel's contribution to a record is nine floats; per record the contributing lanes of a wave
 // reduce them with a reduce-scatter (v_permlane32_swap, v_permlane16_swap, then DPP row shifts:
-// 28 VALU for nine values), add the totals into the record's LDS accumulator, and after each batch
-// every record issues at most nine float atomics to global memory. Events with few contributing
-// lanes skip the reduction and add their values straight into LDS.
+// 28 VALU for nine values) and add the totals into the record's LDS accumulator. Events with few
+// contributing lanes skip the reduction and add their values straight into LDS. After each batch
+// every record stores its nine sums (plain stores, no global atomics) at its emission position,
+// where all intersections of one item are contiguous; grad_gather_kernel then adds them per item
+// in a fixed order and writes the four gradient outputs. Only the LDS sums of one record over
+// the tile's four quadrant waves depend on the order in which the waves arrive.
 #include "splat_common.hpp"
 #include "splat_internal.hpp"
 
@@ -257,8 +260,17 @@ struct BlendBwdParams {
     const float* final_Ts; const int32_t* final_idx;
     const float* v_out; int64_t vout_rows;
     int32_t n; int32_t sel_geom;
-    float* v_colors; float* v_opacity; float* v_xy; float* v_conic;
+    const int32_t* pos; int64_t M;
+    float* rgrad;  // [images][M][9], images = 1 when geometry is batched, else B_out
 };
+
+// Nine partial sums of one intersection: v_colour (3), v_conic (3), the two sums
+// sum v_sigma * dx, sum v_sigma * dy (v_xy before the conic is applied), v_opacity.
+__device__ __forceinline__ void store_rgrad(float* rgrad, int64_t slot, const float* s) {
+    float* r = rgrad + slot * 9;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) r[k] = s[k];
+}
 
 __device__ __forceinline__ float swap32_add(float a, float b) {
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false,
@@ -293,7 +305,6 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     const int32_t image_id = tile_g / C.num_tiles;
     const int32_t tile_local = tile_g - image_id * C.num_tiles;
     const int32_t geom_image = P.sel_geom ? image_id : 0;
-    const int64_t og_base = P.sel_geom ? 0 : (int64_t)image_id * P.n;
     const int tile_x = tile_local % C.tiles_x, tile_y = tile_local / C.tiles_x;
     const int32_t gtile = geom_image * C.num_tiles + tile_local;
     const int32_t range_start = C.bins[2 * gtile], range_end = C.bins[2 * gtile + 1];
@@ -333,12 +344,22 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     const int32_t start_idx = iminw(s_max, range_end - 1);
     const int32_t num_batches = (start_idx - range_start + kTile) / kTile;
     const int row = lane >> 4;
+    const int64_t rg_off = P.sel_geom ? 0 : (int64_t)image_id * P.M;
+    {
+        // intersections above every final index of the tile contribute nothing
+        const float zero9[9] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int32_t jj = start_idx + 1 + tid; jj < range_end; jj += kTile) {
+            const int32_t e = P.pos[jj];
+            if (e >= 0 && e < P.M) store_rgrad(P.rgrad, rg_off + e, zero9);
+        }
+    }
 
     for (int32_t bt = 0; bt < num_batches; ++bt) {
         const int32_t batch_end = start_idx - bt * kTile;
         const int32_t src = imaxw(batch_end - tid, range_start);
-        const int len =
-            uniform(stage_batch(C, L, src, batch_end - tid >= range_start, tile_x, tile_y));
+        const bool live = batch_end - tid >= range_start;
+        const int32_t my_pos = live ? P.pos[src] : -1;  // emission position of slot tid
+        const int len = uniform(stage_batch(C, L, src, live, tile_x, tile_y));
         const uint8_t* list = L.list[uniform(wave)];
         for (int k = 0; k < len; ++k) {
             const int t = uniform(list[k]);
@@ -412,30 +433,13 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
         }
         __syncthreads();
         {
-            const float4 r0 = L.r0[tid], r1 = L.r1[tid], r2 = L.r2[tid];
             float s[9];
 #pragma unroll
             for (int k = 0; k < 9; ++k) {
                 s[k] = ACC(tid, k);
                 ACC(tid, k) = 0.0f;
             }
-            const int64_t og = og_base + __float_as_int(r2.w);
-            if (s[0] != 0.f || s[1] != 0.f || s[2] != 0.f) {
-                atomicAdd(P.v_colors + 3 * og, s[0]);
-                atomicAdd(P.v_colors + 3 * og + 1, s[1]);
-                atomicAdd(P.v_colors + 3 * og + 2, s[2]);
-            }
-            if (s[3] != 0.f || s[4] != 0.f || s[5] != 0.f) {
-                atomicAdd(P.v_conic + 3 * og, s[3]);
-                atomicAdd(P.v_conic + 3 * og + 1, s[4]);
-                atomicAdd(P.v_conic + 3 * og + 2, s[5]);
-            }
-            if (s[6] != 0.f || s[7] != 0.f) {
-                // v_xy = sum v_sigma (a dx + b dy, b dx + c dy) with (a, b, c) fixed per record
-                atomicAdd(P.v_xy + 2 * og, r0.z * s[6] + r0.w * s[7]);
-                atomicAdd(P.v_xy + 2 * og + 1, r0.w * s[6] + r1.x * s[7]);
-            }
-            if (s[8] != 0.f) atomicAdd(P.v_opacity + og, s[8]);
+            if (my_pos >= 0 && my_pos < P.M) store_rgrad(P.rgrad, rg_off + my_pos, s);
         }
         __syncthreads();
     }
@@ -443,23 +447,74 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
 
 #undef ACC
 
+// Per output item: sum of its intersections' partial gradients in emission order (fixed, so
+// deterministic), then v_xy = (a Sx + b Sy, b Sx + c Sy) with the item's conic (a, b, c), which
+// equals the reference's per-pair sum of v_sigma (a dx + b dy, b dx + c dy)
+// (splax/_rasterize/_kernels.py:1246-1250) up to rounding. Every output is written.
+struct GatherParams {
+    const int32_t* cum; const float* conics; const float* rgrad;
+    int64_t M; int64_t nout; int32_t n; int32_t sel_geom;
+    float* v_colors; float* v_opacity; float* v_xy; float* v_conic;
+};
+
+__global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
+    const int64_t og = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (og >= P.nout) return;
+    int64_t gi = og, off = 0;
+    if (!P.sel_geom) {
+        const int64_t b = og / P.n;
+        gi = og - b * P.n;
+        off = b * P.M;
+    }
+    int64_t lo = gi > 0 ? (int64_t)P.cum[gi - 1] : 0, hi = P.cum[gi];
+    lo = lo < 0 ? 0 : lo;
+    hi = hi > P.M ? P.M : hi;
+    float s[9] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int64_t e = lo; e < hi; ++e) {
+        const float* r = P.rgrad + (off + e) * 9;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) s[k] += r[k];
+    }
+    P.v_colors[3 * og] = s[0];
+    P.v_colors[3 * og + 1] = s[1];
+    P.v_colors[3 * og + 2] = s[2];
+    P.v_conic[3 * og] = s[3];
+    P.v_conic[3 * og + 1] = s[4];
+    P.v_conic[3 * og + 2] = s[5];
+    float vx = 0.f, vy = 0.f;
+    if (s[6] != 0.f || s[7] != 0.f) {
+        const float a = P.conics[3 * gi], b = P.conics[3 * gi + 1], c = P.conics[3 * gi + 2];
+        vx = a * s[6] + b * s[7];
+        vy = b * s[6] + c * s[7];
+    }
+    P.v_xy[2 * og] = vx;
+    P.v_xy[2 * og + 1] = vy;
+    P.v_opacity[og] = s[8];
+}
+
 int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, const BlendBwdArgs& a, hipStream_t stream) {
     const int64_t nout = (int64_t)a.B_out * in.n;
-    int rc = fill_zero_f32(a.v_colors, 3 * nout, stream);
-    if (!rc) rc = fill_zero_f32(a.v_opacity, nout, stream);
-    if (!rc) rc = fill_zero_f32(a.v_xy, 2 * nout, stream);
-    if (!rc) rc = fill_zero_f32(a.v_conic, 3 * nout, stream);
-    if (rc) return rc;
+    const int32_t sel_geom = in.B_geom > 1;
     const int64_t blocks = (int64_t)a.B_out * lay.num_tiles;
-    if (blocks <= 0 || sorted_ids == nullptr) return 0;
-    BlendBwdParams P;
-    fill_common(P.c, in, lay, sorted_ids, tile_bins);
-    P.final_Ts = a.final_Ts; P.final_idx = a.final_idx;
-    P.v_out = a.v_out; P.vout_rows = a.vout_rows;
-    P.n = in.n; P.sel_geom = in.B_geom > 1;
-    P.v_colors = a.v_colors; P.v_opacity = a.v_opacity; P.v_xy = a.v_xy; P.v_conic = a.v_conic;
-    hipLaunchKernelGGL(blend_bwd_kernel, dim3((unsigned)blocks), dim3(kTile), 0, stream, P);
+    if (blocks > 0 && sorted_ids != nullptr && a.M > 0) {
+        BlendBwdParams P;
+        fill_common(P.c, in, lay, sorted_ids, tile_bins);
+        P.final_Ts = a.final_Ts; P.final_idx = a.final_idx;
+        P.v_out = a.v_out; P.vout_rows = a.vout_rows;
+        P.n = in.n; P.sel_geom = sel_geom;
+        P.pos = a.sorted_pos; P.M = a.M; P.rgrad = a.rgrad;
+        hipLaunchKernelGGL(blend_bwd_kernel, dim3((unsigned)blocks), dim3(kTile), 0, stream, P);
+        if (hipGetLastError() != hipSuccess) return kErrLaunch;
+    }
+    if (nout <= 0) return 0;
+    GatherParams G;
+    G.cum = in.cum; G.conics = in.conics; G.rgrad = a.rgrad;
+    G.M = (sorted_ids != nullptr) ? a.M : 0;
+    G.nout = nout; G.n = in.n; G.sel_geom = sel_geom;
+    G.v_colors = a.v_colors; G.v_opacity = a.v_opacity; G.v_xy = a.v_xy; G.v_conic = a.v_conic;
+    hipLaunchKernelGGL(grad_gather_kernel, dim3((unsigned)((nout + 255) / 256)), dim3(256), 0,
+                       stream, G);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
 }
 

@@ -124,12 +124,16 @@ int DeviceScratch::ensure_sort(int64_t M, int64_t bins, int32_t B) {
             dev_free(&keys[k]);
             dev_free(&vals[k]);
         }
+        dev_free(&owner);
+        dev_free(&ids);
         isect_cap = 0;
         int64_t cap = (int64_t)(M * 1.25) + 1;
         for (int k = 0; k < 2 && !rc; ++k) {
             rc = dev_alloc(&keys[k], cap, false);
             if (!rc) rc = dev_alloc(&vals[k], cap, false);
         }
+        if (!rc) rc = dev_alloc(&owner, cap, false);
+        if (!rc) rc = dev_alloc(&ids, cap, false);
         if (rc) return rc;
         isect_cap = cap;
     }
@@ -169,6 +173,18 @@ int DeviceScratch::ensure_sort(int64_t M, int64_t bins, int32_t B) {
     return 0;
 }
 
+int DeviceScratch::ensure_rgrad(int64_t count) {
+    if (count <= rgrad_cap) return 0;
+    (void)hipDeviceSynchronize();
+    dev_free(&rgrad);
+    rgrad_cap = 0;
+    const int64_t cap = (int64_t)(count * 1.25) + 9;
+    int rc = dev_alloc(&rgrad, cap, false);
+    if (rc) return rc;
+    rgrad_cap = cap;
+    return 0;
+}
+
 static int ensure_minmax_partials(DeviceScratch& sc, int64_t count) {
     if (count <= sc.mm_partial_cap) return 0;
     (void)hipDeviceSynchronize();
@@ -190,7 +206,11 @@ void DeviceScratch::release() {
         dev_free(&keys[k]);
         dev_free(&vals[k]);
     }
+    dev_free(&owner);
+    dev_free(&ids);
     isect_cap = 0;
+    dev_free(&rgrad);
+    rgrad_cap = 0;
     dev_free(&sort_status);
     sort_status_cap = 0;
     dev_free(&tile_bins);
@@ -276,7 +296,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 1; }
+int splat_abi_version(void) { return 2; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();
@@ -462,7 +482,7 @@ int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* dep
     if (M > 0) {
         if (hipMemcpyAsync(sorted_keys, sc.keys[0], M * sizeof(int32_t), hipMemcpyDeviceToDevice,
                            s) != hipSuccess ||
-            hipMemcpyAsync(sorted_ids, sc.vals[0], M * sizeof(int32_t), hipMemcpyDeviceToDevice,
+            hipMemcpyAsync(sorted_ids, sc.ids, M * sizeof(int32_t), hipMemcpyDeviceToDevice,
                            s) != hipSuccess)
             return fail(kErrRuntime, "sorted copy failed");
     }
@@ -502,7 +522,7 @@ int splat_rasterize_fwd(splat_stream_t stream, const float* colors, int64_t rows
     if (num_intersects) *num_intersects = M;
     if (rc) return rc;
     StageTimer tm(s, kStageBlendFwd);
-    rc = launch_blend_fwd(in, L, sc.vals[0] ? sc.vals[0] : nullptr, sc.tile_bins, final_Ts,
+    rc = launch_blend_fwd(in, L, M > 0 ? sc.ids : nullptr, sc.tile_bins, final_Ts,
                           final_idx, out_img, s);
     if (rc) return fail(rc, "blend_fwd launch failed");
     return 0;
@@ -516,7 +536,7 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
                              const int32_t* cum_tiles_hit, int32_t num_gaussians, int32_t B,
                              int32_t img_h, int32_t img_w, int64_t num_intersects,
                              float* final_Ts, int32_t* final_idx, float* out_img,
-                             int32_t* sorted_ids, int32_t* tile_bins) {
+                             int32_t* sorted_ids, int32_t* sorted_pos, int32_t* tile_bins) {
     RasterInputs in{};
     in.colors = colors; in.rows_colors = rows_colors;
     in.opac = opacities; in.rows_opac = rows_opac;
@@ -527,7 +547,8 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
     in.img_h = img_h; in.img_w = img_w;
     int rc = check_raster(in);
     if (rc) return rc;
-    if (num_intersects < 0 || !tile_bins || (num_intersects > 0 && !sorted_ids))
+    if (num_intersects < 0 || !tile_bins ||
+        (num_intersects > 0 && (!sorted_ids || !sorted_pos)))
         return fail(kErrArgs, "rasterize_fwd_keep: missing sorted-list buffers");
     hipStream_t s = static_cast<hipStream_t>(stream);
     DeviceScratch& sc = scratch_for_current_device();
@@ -541,6 +562,7 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
     SortTargets tgt;
     tgt.M_known = num_intersects;
     tgt.ids = sorted_ids;
+    tgt.pos = sorted_pos;
     tgt.bins = tile_bins;
     int64_t M = 0;
     KeyLayout L;
@@ -556,7 +578,8 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
 int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64_t rows_colors,
                                const float* opacities, int64_t rows_opac,
                                const float* background, int64_t rows_bg, const float* xys,
-                               const float* conics, const int32_t* sorted_ids,
+                               const float* conics, const int32_t* cum_tiles_hit,
+                               const int32_t* sorted_ids, const int32_t* sorted_pos,
                                const int32_t* tile_bins, int64_t num_intersects,
                                const float* final_Ts, const int32_t* final_idx,
                                const float* v_out_img, int64_t vout_rows, int32_t num_gaussians,
@@ -568,22 +591,29 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
     in.map_opac = opacities; in.rows_map_opac = rows_opac;
     in.background = background; in.rows_bg = rows_bg;
     in.xys = xys; in.depths = nullptr; in.radii = nullptr; in.conics = conics;
-    in.cum = nullptr; in.n = num_gaussians; in.B_geom = B_geom;
+    in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B_geom;
     in.img_h = img_h; in.img_w = img_w;
     int rc = check_raster(in);
     if (rc) return rc;
     if (B_out <= 0 || (B_geom > 1 && B_geom != B_out))
         return fail(kErrArgs, "rasterize_bwd_sorted: B_geom must be 1 or equal to B_out");
-    if (vout_rows <= 0 || num_intersects < 0 || !tile_bins)
+    if (vout_rows <= 0 || num_intersects < 0 || !tile_bins || !cum_tiles_hit ||
+        (num_intersects > 0 && (!sorted_ids || !sorted_pos)))
         return fail(kErrArgs, "rasterize_bwd_sorted: invalid cotangent or sorted lists");
     if ((int64_t)B_out * num_gaussians >= ((int64_t)1 << 31))
         return fail(kErrArgs, "rasterize_bwd_sorted: more than 2^31 gradient rows");
     const KeyLayout L = key_layout(B_geom, img_h, img_w);
     if (!L.packed) return fail(kErrKeyOverflow, "rasterize_bwd_sorted: key does not pack");
     hipStream_t s = static_cast<hipStream_t>(stream);
+    DeviceScratch& sc = scratch_for_current_device();
+    std::lock_guard<std::mutex> lock(sc.mu);
+    const int64_t images = B_geom > 1 ? 1 : B_out;
+    rc = sc.ensure_rgrad(images * num_intersects * 9);
+    if (rc) return rc;
     BlendBwdArgs a;
     a.final_Ts = final_Ts; a.final_idx = final_idx;
     a.v_out = v_out_img; a.vout_rows = vout_rows; a.B_out = B_out;
+    a.sorted_pos = sorted_pos; a.M = num_intersects; a.rgrad = sc.rgrad;
     a.v_colors = v_colors; a.v_opacity = v_opacity; a.v_xy = v_xy; a.v_conic = v_conic;
     StageTimer tm(s, kStageBlendBwd);
     rc = launch_blend_bwd(in, L, num_intersects > 0 ? sorted_ids : nullptr, tile_bins, a, s);
@@ -628,12 +658,16 @@ int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows
     KeyLayout L;
     rc = run_sort_and_bin(in, sc, s, &M, &L);
     if (rc) return rc;
+    const int64_t images = B_geom > 1 ? 1 : B_out;
+    rc = sc.ensure_rgrad(images * M * 9);
+    if (rc) return rc;
     BlendBwdArgs a;
     a.final_Ts = final_Ts; a.final_idx = final_idx;
     a.v_out = v_out_img; a.vout_rows = vout_rows; a.B_out = B_out;
+    a.sorted_pos = sc.vals[0]; a.M = M; a.rgrad = sc.rgrad;
     a.v_colors = v_colors; a.v_opacity = v_opacity; a.v_xy = v_xy; a.v_conic = v_conic;
     StageTimer tm(s, kStageBlendBwd);
-    rc = launch_blend_bwd(in, L, M > 0 ? sc.vals[0] : nullptr, sc.tile_bins, a, s);
+    rc = launch_blend_bwd(in, L, M > 0 ? sc.ids : nullptr, sc.tile_bins, a, s);
     if (rc) return fail(rc, "blend_bwd launch failed");
     return 0;
 }

@@ -11,6 +11,12 @@
 // run is written contiguously. Ranking follows position order (wave-striped items, lanes in order,
 // waves in order, partitions in index order), so the sort is stable: ties keep emission order,
 // which is the reference's (key, position) order.
+//
+// The sorted values are emission positions rather than the reference's flat item ids: emission
+// records the owning item per position (`owner`), and the last pass writes both the sorted
+// positions and the sorted item ids (owner[position]). The item ids are exactly the reference's
+// sorted values; the positions let the backward blend store each intersection's gradient in
+// emission order, where every item's intersections are contiguous.
 #include "splat_common.hpp"
 #include "splat_internal.hpp"
 
@@ -119,7 +125,7 @@ struct EmitParams {
     const int32_t* cum; const float* mm;
     int32_t n; int64_t total; int64_t M;
     int32_t tiles_x, tiles_y, tile_bits, depth_bits;
-    int32_t* keys; int32_t* vals;
+    int32_t* keys; int32_t* owner;
 };
 
 __global__ void __launch_bounds__(256) emit_keys_kernel(EmitParams P) {
@@ -155,7 +161,7 @@ __global__ void __launch_bounds__(256) emit_keys_kernel(EmitParams P) {
             if (cur >= P.M) return;
             int32_t tile_id = e.isY ? u * P.tiles_x + v : v * P.tiles_x + u;
             P.keys[cur] = iid_enc | (tile_id << P.depth_bits) | dq;
-            P.vals[cur] = (int32_t)idx;
+            P.owner[cur] = (int32_t)idx;
             ++cur;
         }
     }
@@ -257,9 +263,13 @@ __device__ __forceinline__ uint32_t block_exclusive_scan_256(uint32_t v, uint32_
     return off + incl - v;
 }
 
+// Values are emission positions: the first pass generates them (vals_in == nullptr gives value
+// = position), later passes carry them. The last pass also writes, per sorted slot, the flat item
+// that emitted the key (ids_out[dest] = owner[value]), when owner is non-null.
 __global__ void __launch_bounds__(kSortThreads)
 onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
-                     int32_t* __restrict__ keys_out, int32_t* __restrict__ vals_out, int64_t M,
+                     int32_t* __restrict__ keys_out, int32_t* __restrict__ vals_out,
+                     const int32_t* __restrict__ owner, int32_t* __restrict__ ids_out, int64_t M,
                      int shift, const uint32_t* __restrict__ hist, uint64_t* status,
                      uint32_t epoch, uint32_t* err) {
     __shared__ uint32_t s_keys[kSortTile];
@@ -283,7 +293,7 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
     for (int i = 0; i < kSortItems; ++i) {
         int64_t pos = wbase + i * 64 + lane;
         key[i] = pos < M ? (uint32_t)keys_in[pos] : 0xffffffffu;
-        val[i] = pos < M ? (uint32_t)vals_in[pos] : 0u;
+        val[i] = pos < M ? (vals_in ? (uint32_t)vals_in[pos] : (uint32_t)pos) : 0u;
     }
 
     // stable per-wave ranking: lanes with equal digits found by 8 ballots
@@ -384,8 +394,10 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
         if (j < valid) {
             const uint32_t k = s_keys[j];
             const int64_t dest = (int64_t)s_dest_base[(k >> shift) & 255u] + j;
+            const uint32_t v = s_vals[j];
             keys_out[dest] = (int32_t)k;
-            vals_out[dest] = (int32_t)s_vals[j];
+            vals_out[dest] = (int32_t)v;
+            if (owner) ids_out[dest] = owner[v];
         }
     }
 }
@@ -495,7 +507,8 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     rc = sc.ensure_sort(M, nbins, B);
     if (rc) return rc;
     if (M == 0) return fill_zero_i32(bins, 2 * nbins, stream);
-    int32_t* ids_final = (tgt && tgt->ids) ? tgt->ids : sc.vals[0];
+    int32_t* ids_final = (tgt && tgt->ids) ? tgt->ids : sc.ids;
+    int32_t* pos_final = (tgt && tgt->pos) ? tgt->pos : sc.vals[0];
 
     {
         StageTimer tm(stream, kStageEmit);
@@ -504,7 +517,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         E.map_opac = in.map_opac; E.rows_map_opac = in.rows_map_opac;
         E.cum = in.cum; E.mm = sc.depth_mm; E.n = in.n; E.total = total; E.M = M;
         E.tiles_x = L.tiles_x; E.tiles_y = L.tiles_y; E.tile_bits = L.tile_bits;
-        E.depth_bits = L.depth_bits; E.keys = sc.keys[0]; E.vals = sc.vals[0];
+        E.depth_bits = L.depth_bits; E.keys = sc.keys[0]; E.owner = sc.owner;
         hipLaunchKernelGGL(emit_keys_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                            stream, E);
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "emit launch failed");
@@ -517,13 +530,16 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         hipLaunchKernelGGL(digit_hist_kernel, dim3((unsigned)hb), dim3(kHistThreads), 0, stream,
                            sc.keys[0], M, chunk, sc.hist, bins, 2 * nbins);
         const int64_t parts = (M + kSortTile - 1) / kSortTile;
-        // passes 0..3 ping-pong 0 -> 1 -> 0 -> 1 -> 0; the last pass writes the values straight
-        // into their final buffer (the caller's when it keeps the sorted lists)
+        // passes 0..3 ping-pong 0 -> 1 -> 0 -> 1 -> 0; the first pass generates the emission
+        // positions, the last writes them and the owning items straight into their final
+        // buffers (the caller's when it keeps the sorted lists)
         for (int pass = 0; pass < 4; ++pass) {
             const int src = pass & 1, dst = 1 - src;
-            int32_t* vdst = pass == 3 ? ids_final : sc.vals[dst];
+            const bool last = pass == 3;
             hipLaunchKernelGGL(onesweep_pass_kernel, dim3((unsigned)parts), dim3(kSortThreads), 0,
-                               stream, sc.keys[src], sc.vals[src], sc.keys[dst], vdst, M,
+                               stream, sc.keys[src], pass == 0 ? nullptr : sc.vals[src],
+                               sc.keys[dst], last ? pos_final : sc.vals[dst],
+                               last ? sc.owner : nullptr, last ? ids_final : nullptr, M,
                                8 * pass, sc.hist + 256 * pass, sc.sort_status, sc.next_epoch(),
                                sc.tickets + kDeviceError);
         }

@@ -94,8 +94,12 @@ struct DeviceScratch {
     uint32_t* tickets = nullptr;
     // sort
     int32_t* keys[2] = {nullptr, nullptr};
-    int32_t* vals[2] = {nullptr, nullptr};
+    int32_t* vals[2] = {nullptr, nullptr};  // emission positions (ping-pong)
+    int32_t* owner = nullptr;               // flat item of each emission position
+    int32_t* ids = nullptr;                 // sorted flat item ids
     int64_t isect_cap = 0;
+    // backward: nine partial gradient sums per (output image, intersection), emission order
+    float* rgrad = nullptr; int64_t rgrad_cap = 0;
     uint64_t* sort_status = nullptr; int64_t sort_status_cap = 0;  // partitions * 256
     uint32_t* hist = nullptr;                                       // 4 * 256
     int32_t* tile_bins = nullptr; int64_t bins_cap = 0;             // (start, end) pairs
@@ -112,6 +116,7 @@ struct DeviceScratch {
     int ensure_base();
     int grow_scan_status(int64_t blocks);
     int ensure_sort(int64_t M, int64_t bins, int32_t B);
+    int ensure_rgrad(int64_t count);
     void release();
 };
 
@@ -145,16 +150,18 @@ int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stre
 int launch_project_bwd(const ProjectBwdArgs& a, hipStream_t stream);
 
 // Optional caller-owned destinations of sort_and_bin: M_known >= 0 skips the count readback
-// (it must equal cum[B*n - 1]); ids / bins (when non-null) receive the sorted gaussian ids and
-// the tile bins instead of the library scratch.
+// (it must equal cum[B*n - 1]); ids / pos / bins (when non-null) receive the sorted gaussian ids,
+// the sorted emission positions and the tile bins instead of the library scratch.
 struct SortTargets {
     int64_t M_known = -1;
     int32_t* ids = nullptr;
+    int32_t* pos = nullptr;
     int32_t* bins = nullptr;
 };
 
 // sort_and_bin: returns M (>= 0) in *M_out; sorted keys in sc.keys[0]; sorted ids in tgt->ids or
-// sc.vals[0]; tile bins in tgt->bins or sc.tile_bins.
+// sc.ids; sorted emission positions in tgt->pos or sc.vals[0]; tile bins in tgt->bins or
+// sc.tile_bins.
 int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stream,
                      int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt = nullptr);
 
@@ -162,10 +169,14 @@ int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
                      const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,
                      float* out_img, hipStream_t stream);
 
+// Backward over sorted lists of M intersections: sorted_ids / sorted_pos / tile_bins as produced
+// by sort_and_bin; in.cum gives each item's emission range; rgrad is scratch of
+// B_out_eff * M * 9 floats (B_out_eff = 1 when geometry is batched, else B_out).
 struct BlendBwdArgs {
     const float* final_Ts; const int32_t* final_idx;
     const float* v_out; int64_t vout_rows;
     int32_t B_out;
+    const int32_t* sorted_pos; int64_t M; float* rgrad;
     float* v_colors; float* v_opacity; float* v_xy; float* v_conic;
 };
 int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,

@@ -277,29 +277,40 @@ def test_golden_fixture():
 
 @pytest.mark.parametrize("name", ["cfg1", "cfg2_50k"])
 def test_kept_sort_path_equals_resort_path(name):
-    """fwd_keep returns exactly sort_and_bin's lists; bwd_sorted equals the re-sorting backward."""
+    """fwd_keep returns exactly sort_and_bin's lists plus the emission positions (the stable
+    argsort of the emitted keys); bwd_sorted equals the re-sorting backward, and a repeated call,
+    up to the order in which a tile's four quadrant waves add into a record's LDS sums."""
     _case(f"keep/sorted path {name}")
     s = _scene_arrays(name)
     xys, depths, radii, conics, nth, cum = _raster_inputs(s)
     o = _t(s.opacities).reshape(-1)
     geo = (_t(xys), _t(depths), _t(radii), _t(conics), _t(cum))
-    img, Ts, fidx, ids, bins, M = _ops.rasterize_fwd_keep(_t(s.colors), o, o, _t(s.background),
-                                                          *geo, n=s.n, B=1, img_shape=s.img_shape)
+    img, Ts, fidx, ids, pos, bins, M = _ops.rasterize_fwd_keep(
+        _t(s.colors), o, o, _t(s.background), *geo, n=s.n, B=1, img_shape=s.img_shape)
     rk, rid, rbins = O.sort_and_bin(xys, depths, radii, conics, s.opacities, cum, n=s.n, B=1,
                                     img_shape=s.img_shape)
     assert M == rid.size
     assert_bit_exact(_np(ids)[:M], rid, f"{name}/kept ids")
     assert_bit_exact(_np(bins), rbins, f"{name}/kept bins")
+    ekeys, eids, _ = O.emit_keys(xys, depths, radii, conics, s.opacities, cum, n=s.n, B=1,
+                                 img_shape=s.img_shape)
+    want_pos = np.argsort(ekeys, kind="stable").astype(np.int32)
+    assert_bit_exact(_np(pos)[:M], want_pos, f"{name}/kept emission positions")
+    assert_bit_exact(eids[want_pos], rid, f"{name}/owner of each sorted position")
     rimg, rT, ridx, _, _ = O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background, xys,
                                            depths, radii, conics, cum, n=s.n, B=1,
                                            img_shape=s.img_shape)
     assert_bit_exact(_np(img), rimg, f"{name}/kept img")
     H, W = s.img_shape
     vout = _t((2.0 * (rimg.reshape(H, W, 3) - s.targets[0]) / rimg.size).astype(np.float32))
-    a = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[3], ids, bins, M,
-                                  Ts, fidx, vout.reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
-                                  img_shape=s.img_shape)
+    a = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[3], geo[4], ids,
+                                  pos, bins, M, Ts, fidx, vout.reshape(-1, 3), n=s.n, B_out=1,
+                                  B_geom=1, img_shape=s.img_shape)
     b = _ops.rasterize_bwd(_t(s.colors), o, o, _t(s.background), *geo, Ts, fidx,
                            vout.reshape(-1, 3), n=s.n, B_out=1, B_geom=1, img_shape=s.img_shape)
-    for label, x, y in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), a, b):
-        _grad_compare(_np(x), _np(y), f"{name}/{label}")
+    a2 = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[3], geo[4],
+                                   ids, pos, bins, M, Ts, fidx, vout.reshape(-1, 3), n=s.n,
+                                   B_out=1, B_geom=1, img_shape=s.img_shape)
+    for label, x, y, z in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), a, b, a2):
+        _grad_compare(_np(x), _np(y), f"{name}/{label} kept vs re-sorted")
+        _grad_compare(_np(x), _np(z), f"{name}/{label} repeat")
