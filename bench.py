@@ -7,7 +7,9 @@ config 2 (1,000,000 gaussians on 64 planes, one 1920x1080 camera, BASELINE.json 
 The JSON line carries:
 - value: forward+backward frames/s (whole job, one GPU); fwd_frames_per_s: forward only.
 - roofline: the dominant kernel's algorithmic work per launch / its average launch duration,
-  timed with HIP events on the launch stream inside the timed region (library stage timing).
+  timed with HIP events on the launch stream inside the timed region (library stage timing,
+  enabled for that stage only; a separate untimed pass with every stage bracketed gives
+  stage_ms_per_step and picks the dominant stage).
   Blend work is the reference loop's pair count from the CPU oracle (26 Pc + 16 Pr FLOPs
   forward, 65 Qc + 16 Qr backward); sort+bin bytes are 12G + 32V + 76M + 16T.
 - cpu_baseline: the CPU oracle (the C restatement of the reference kernels, "port") timed on the
@@ -129,7 +131,7 @@ def main():
         for p in params:
             p.grad = None
         img = forward()
-        loss = ((img - target) ** 2).mean()
+        loss = torch.nn.functional.mse_loss(img, target)
         loss.backward()
 
     for _ in range(args.warmup):
@@ -145,9 +147,21 @@ def main():
             forward()
         torch.cuda.synchronize()
         fwd_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    # timed fwd+bwd region with stage events on the launch stream
+    # per-stage breakdown (untimed pass: every stage bracketed by events)
     _lib.stage_times()  # reset
     _lib.set_stage_timing(True)
+    cal_steps = 3
+    for _ in range(cal_steps):
+        step()
+    torch.cuda.synchronize()
+    _lib.set_stage_timing(False)
+    cal = _lib.stage_times()
+    stage_ms_per_step = {k: round(v[0] / cal_steps, 4) for k, v in cal.items()}
+    roof_stages = ("blend_bwd", "blend_fwd", "sort", "project")
+    dom = max(roof_stages, key=lambda k: cal[k][0])
+    # timed fwd+bwd region; HIP events on the launch stream bracket only the dominant stage
+    _lib.stage_times()
+    _lib.set_stage_timing([dom])
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -169,7 +183,6 @@ def main():
                          f"fwd alone {cpu_fwd_s:.2f} s"}
 
     per_stage = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in stages.items()}
-    stage_ms_per_step = {k: round(v[0] / args.steps, 4) for k, v in stages.items()}
     roofline = None
     if counts is not None:
         G, V, M = counts["G"], counts["V"], counts["M"]
@@ -182,7 +195,6 @@ def main():
             "sort": ("hbm", 64 * M / 1e9, "GB/s", HBM_PEAK_GBS),
             "project": ("hbm", (44 * scene.n + 40 * G) / 1e9, "GB/s", HBM_PEAK_GBS),
         }
-        dom = max(cands, key=lambda k: per_stage.get(k, 0.0))
         bound, work, unit, peak = cands[dom]
         dur_s = per_stage[dom] / 1e3
         achieved = work / dur_s if dur_s > 0 else 0.0

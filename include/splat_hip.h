@@ -91,21 +91,22 @@ int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows
                         float* v_xy, float* v_conic);
 
 /* Forward that keeps the sorted intersection lists resident for the backward (no counterpart in
- * the reference, whose backward re-sorts, splax/_rasterize/_kernels.py:422): the caller passes
- * num_intersects = cum_tiles_hit[B*n-1] (so the library skips its own device-to-host read) and
- * buffers sorted_ids [num_intersects], sorted_pos [num_intersects] and tile_bins
- * [B*num_tiles, 2]. sorted_ids and tile_bins receive exactly what splat_sort_and_bin returns;
- * sorted_pos receives each sorted intersection's emission position (its index in the
- * cum_tiles_hit-ordered emission sequence). Other arguments and outputs as splat_rasterize_fwd. */
+ * the reference, whose backward re-sorts, splax/_rasterize/_kernels.py:422). The caller passes
+ * buffers sorted_ids [capacity], sorted_pos [capacity] and tile_bins [B*num_tiles, 2]; sorted_ids
+ * and tile_bins receive exactly what splat_sort_and_bin returns, sorted_pos each sorted
+ * intersection's emission position (its index in the cum_tiles_hit-ordered emission sequence).
+ * num_intersects receives M. When M > capacity the call returns status 6 after the count
+ * readback, with M reported and nothing written; the caller retries with larger buffers. Other
+ * arguments and outputs as splat_rasterize_fwd. */
 int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t rows_colors,
                              const float* opacities, int64_t rows_opac,
                              const float* map_opacities, int64_t rows_map_opac,
                              const float* background, int64_t rows_bg, const float* xys,
                              const float* depths, const int32_t* radii, const float* conics,
                              const int32_t* cum_tiles_hit, int32_t num_gaussians, int32_t B,
-                             int32_t img_h, int32_t img_w, int64_t num_intersects,
-                             float* final_Ts, int32_t* final_idx, float* out_img,
-                             int32_t* sorted_ids, int32_t* sorted_pos, int32_t* tile_bins);
+                             int32_t img_h, int32_t img_w, int64_t capacity, float* final_Ts,
+                             int32_t* final_idx, float* out_img, int32_t* sorted_ids,
+                             int32_t* sorted_pos, int32_t* tile_bins, int64_t* num_intersects);
 
 /* Backward over the sorted lists kept by splat_rasterize_fwd_keep (no re-sort). Arguments as
  * splat_rasterize_bwd plus sorted_ids / sorted_pos / tile_bins / num_intersects of the matching
@@ -139,10 +140,11 @@ void splat_clear_cache(void);
 const char* splat_last_error(void);
 
 /* Stage timing with HIP events on the caller's stream (no counterpart in the reference; used by
- * the benchmark). While enabled every stage launch is bracketed by events; get_stage_times waits
- * for them and returns, per stage, the summed milliseconds and the number of calls, then resets.
- * Stages: 0 project, 1 minmax, 2 emit, 3 sort, 4 bins, 5 blend_fwd, 6 blend_bwd, 7 project_bwd. */
-int splat_set_stage_timing(int enabled);
+ * the benchmark). Stages whose bit is set in stage_mask (0 turns timing off) are bracketed by
+ * events at every launch; get_stage_times waits for them and returns, per stage, the summed
+ * milliseconds and the number of calls, then resets. Stages: 0 project, 1 minmax, 2 emit,
+ * 3 sort, 4 bins, 5 blend_fwd, 6 blend_bwd, 7 project_bwd. */
+int splat_set_stage_timing(int stage_mask);
 int splat_get_stage_times(double* ms, int64_t* calls, int32_t n);
 
 /* Waits for the current device and returns (then clears) its device error word: 0 when every

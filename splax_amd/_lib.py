@@ -32,7 +32,7 @@ _SIGS = {
     "splat_rasterize_bwd": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_vp, _vp, _vp, _i64]
     + [_i32] * 5 + [_vp] * 4,
     "splat_rasterize_fwd_keep": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_i32] * 4 + [_i64]
-    + [_vp] * 6,
+    + [_vp] * 7,
     "splat_rasterize_bwd_sorted": [_vp] + [_vp, _i64] * 3 + [_vp] * 6 + [_i64]
     + [_vp, _vp, _vp, _i64] + [_i32] * 5 + [_vp] * 4,
     "splat_sort_and_bin": [_vp] + [_vp] * 4 + [_vp, _i64, _vp] + [_i32] * 4
@@ -113,8 +113,14 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def set_stage_timing(enabled: bool) -> None:
-    lib().splat_set_stage_timing(int(enabled))
+def set_stage_timing(stages=None) -> None:
+    """Bracket the named stages (all when True, none when False/empty) with HIP events."""
+    if stages is True:
+        stages = STAGES
+    mask = 0
+    for name in (stages or ()):
+        mask |= 1 << STAGES.index(name)
+    lib().splat_set_stage_timing(mask)
 
 
 def stage_times() -> dict[str, tuple[float, int]]:

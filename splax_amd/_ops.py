@@ -7,6 +7,8 @@ operands' device and enqueues the library call on torch's current stream of that
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from splax_amd import _lib
@@ -59,31 +61,34 @@ def project_fwd(means, scales, quats_xyzw, viewmat, opac, transforms, transform_
 def project_bwd(means, scales, quats_xyzw, viewmat, radii, conics, v_xy, v_depth, v_conic,
                 transforms, transform_ids, *, n, B, num_transforms, has_transforms, f,
                 glob_scale):
-    """_project_bwd_warp (splax/_project/_kernels.py:257-341)."""
+    """_project_bwd_warp (splax/_project/_kernels.py:257-341).
+
+    v_depth may be None (a zero depth cotangent); v_tf is None without transforms."""
     means, scales, quats, viewmat, conics = map(_f32, (means, scales, quats_xyzw, viewmat,
                                                        conics))
-    v_xy, v_depth, v_conic, transforms = map(_f32, (v_xy, v_depth, v_conic, transforms))
+    v_xy, v_conic, transforms = map(_f32, (v_xy, v_conic, transforms))
+    v_depth = None if v_depth is None else _f32(v_depth)
     radii, transform_ids = _i32(radii), _i32(transform_ids)
-    dev = _lib.require_gpu(means, scales, quats, viewmat, conics, v_xy, v_depth, v_conic)
+    dev = _lib.require_gpu(means, scales, quats, viewmat, conics, v_xy, v_conic)
     total = B * n
     v_mean = torch.empty((total, 3), device=dev, dtype=torch.float32)
     v_scale = torch.empty((total, 3), device=dev, dtype=torch.float32)
     v_quat = torch.empty((total, 4), device=dev, dtype=torch.float32)
     v_view = torch.empty((B * 4, 4), device=dev, dtype=torch.float32)
-    K = num_transforms if has_transforms else 0
-    v_tf = torch.empty((max(B * K, 1), 4, 4), device=dev, dtype=torch.float32)
+    v_tf = None
+    if has_transforms:
+        v_tf = torch.empty((B * num_transforms, 4, 4), device=dev, dtype=torch.float32)
     p = _lib.ptr
     with torch.cuda.device(dev):
         st = _lib.lib().splat_project_bwd(
             _lib.stream_handle(dev), p(means), rows(means, 3), p(scales), rows(scales, 3),
             p(quats), rows(quats, 4), p(viewmat), rows(viewmat, 4), p(radii), radii.numel(),
-            p(conics), rows(conics, 3), p(v_xy), rows(v_xy, 2), p(v_depth), v_depth.numel(),
-            p(v_conic), rows(v_conic, 3), p(transforms), rows(transforms, 16), p(transform_ids),
-            n, num_transforms, int(has_transforms), B, f[0], f[1], glob_scale, p(v_mean),
-            p(v_scale), p(v_quat), p(v_view), p(v_tf))
+            p(conics), rows(conics, 3), p(v_xy), rows(v_xy, 2), p(v_depth),
+            0 if v_depth is None else v_depth.numel(), p(v_conic), rows(v_conic, 3),
+            p(transforms), rows(transforms, 16), p(transform_ids), n, num_transforms,
+            int(has_transforms), B, f[0], f[1], glob_scale, p(v_mean), p(v_scale), p(v_quat),
+            p(v_view), p(v_tf))
     _lib.check(st, "project_bwd")
-    if not has_transforms:
-        v_tf.zero_()
     return v_mean, v_scale, v_quat, v_view, v_tf
 
 
@@ -110,35 +115,51 @@ def rasterize_fwd(colors, opac, map_opac, background, xys, depths, radii, conics
     return img, Ts, fidx, int(m.item())
 
 
+_KEEP_CAPACITY: dict = {}  # per device: capacity estimate for the kept sorted lists
+
+
 def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, conics, cum, *, n,
                        B, img_shape):
     """Forward that also returns the sorted gaussian ids, their emission positions and the tile
     bins (kept for the backward).
 
-    The intersection count is read here (one device-to-host sync, the same one the reference
-    makes inside sort_and_bin) so the buffers can be sized before the launch.
+    The buffers are sized from a per-device estimate (1.25x the largest count seen), so the host
+    does not wait for the intersection count before launching: the library reads it itself while
+    its first kernels run, and reports status 6 with the count when the buffers are too small, in
+    which case they are reallocated and the call repeated.
     """
     colors, opac, map_opac, background, xys, depths, conics = map(
         _f32, (colors, opac, map_opac, background, xys, depths, conics))
     radii, cum = _i32(radii), _i32(cum)
     dev = _lib.require_gpu(colors, opac, map_opac, background, xys, depths, radii, conics, cum)
     H, W = img_shape
-    M = int(cum.reshape(-1)[-1].item()) if cum.numel() else 0
     tiles = ((W + 15) // 16) * ((H + 15) // 16)
     Ts = torch.empty((B * H, W), device=dev, dtype=torch.float32)
     fidx = torch.empty((B * H, W), device=dev, dtype=torch.int32)
     img = torch.empty((B * H, W, 3), device=dev, dtype=torch.float32)
-    ids = torch.empty((max(M, 1),), device=dev, dtype=torch.int32)
-    pos = torch.empty((max(M, 1),), device=dev, dtype=torch.int32)
     bins = torch.empty((B * tiles, 2), device=dev, dtype=torch.int32)
+    key = str(dev)
+    cap = _KEEP_CAPACITY.get(key, 0)
+    m = ctypes.c_int64(0)
     p = _lib.ptr
-    with torch.cuda.device(dev):
-        st = _lib.lib().splat_rasterize_fwd_keep(
-            _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
-            p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys),
-            p(depths), p(radii), p(conics), p(cum), n, B, H, W, M, p(Ts), p(fidx), p(img),
-            p(ids), p(pos), p(bins))
+    for _ in range(2):
+        ids = torch.empty((max(cap, 1),), device=dev, dtype=torch.int32)
+        pos = torch.empty((max(cap, 1),), device=dev, dtype=torch.int32)
+        with torch.cuda.device(dev):
+            st = _lib.lib().splat_rasterize_fwd_keep(
+                _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
+                p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys),
+                p(depths), p(radii), p(conics), p(cum), n, B, H, W, cap, p(Ts), p(fidx), p(img),
+                p(ids), p(pos), p(bins), ctypes.byref(m))
+        if st == _lib.ERR_TOO_MANY and m.value > cap:
+            cap = int(m.value * 1.25) + 1
+            _KEEP_CAPACITY[key] = cap
+            continue
+        break
     _lib.check(st, "rasterize")
+    M = int(m.value)
+    if M > _KEEP_CAPACITY.get(key, 0):
+        _KEEP_CAPACITY[key] = int(M * 1.25) + 1
     return img, Ts, fidx, ids, pos, bins, M
 
 

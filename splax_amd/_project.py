@@ -59,6 +59,7 @@ class _ProjectFn(torch.autograd.Function):
                               conics)
         ctx.statics = statics
         ctx.mark_non_differentiable(radii, nth, cum)
+        ctx.set_materialize_grads(False)  # unused outputs arrive as None, not zero tensors
         return xys, depths, radii, conics, nth, cum
 
     @staticmethod
@@ -68,20 +69,20 @@ class _ProjectFn(torch.autograd.Function):
         z = torch.zeros_like
         v_xys = z(radii, dtype=torch.float32).unsqueeze(-1).expand(-1, 2) if v_xys is None \
             else v_xys
-        v_depths = z(radii, dtype=torch.float32) if v_depths is None else v_depths
         v_conics = z(radii, dtype=torch.float32).unsqueeze(-1).expand(-1, 3) if v_conics is None \
             else v_conics
         v_mean, v_scale, v_quat, v_view, v_tf = _ops.project_bwd(
             _flat(means, 3), _flat(scales, 3), _flat(quats, 4), viewmat.reshape(-1, 4), radii,
-            conics, v_xys.reshape(-1, 2), v_depths.reshape(-1), v_conics.reshape(-1, 3),
+            conics, v_xys.reshape(-1, 2), None if v_depths is None else v_depths.reshape(-1),
+            v_conics.reshape(-1, 3),
             transforms.reshape(-1, 4, 4), tf_ids.reshape(-1), n=n, B=B, num_transforms=K,
             has_transforms=has_tf, f=f, glob_scale=glob_scale)
 
         def fold(g: torch.Tensor, like: torch.Tensor, width: int) -> torch.Tensor:
+            if g.numel() == like.numel():  # one image, or a batched operand
+                return g.reshape(like.shape)
             g = g.reshape(B, n, width) if width > 1 else g.reshape(B, n)
-            if like.ndim == (2 if width > 1 else 1):  # shared operand: sum over the batch
-                g = g.sum(0)
-            return g.reshape(like.shape)
+            return g.sum(0).reshape(like.shape)  # shared operand: sum over the batch
 
         g_means = fold(v_mean, means, 3) if ctx.needs_input_grad[0] else None
         g_scales = fold(v_scale, scales, 3) if ctx.needs_input_grad[1] else None
@@ -95,6 +96,19 @@ class _ProjectFn(torch.autograd.Function):
             g_tf = v_tf.reshape(B, K, 4, 4)
             g_tf = g_tf.reshape(transforms.shape) if transforms.ndim == 4 else g_tf.sum(0)
         return g_means, g_scales, g_quats, g_view, None, g_tf, None, None
+
+
+_NO_TF: dict = {}
+
+
+def _no_transforms(dev: torch.device):
+    """The reference's dummy (1, 4, 4) transforms and (1,) ids of -1 (splax/_project/_project.py:71-73),
+    made once per device."""
+    key = str(dev)
+    if key not in _NO_TF:
+        _NO_TF[key] = (torch.zeros((1, 4, 4), device=dev, dtype=torch.float32),
+                       torch.full((1,), -1, device=dev, dtype=torch.int32))
+    return _NO_TF[key]
 
 
 def project(mean3ds: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor,
@@ -120,8 +134,7 @@ def project(mean3ds: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor,
         raise ValueError("gaussian_transforms and transform_ids must be passed together")
     dev = mean3ds.device
     if not has_tf:
-        gaussian_transforms = torch.zeros((1, 4, 4), device=dev, dtype=torch.float32)
-        transform_ids = torch.full((1,), -1, device=dev, dtype=torch.int32)
+        gaussian_transforms, transform_ids = _no_transforms(dev)
         K = 1
     else:
         K = int(gaussian_transforms.shape[-3])

@@ -57,6 +57,7 @@ class _RasterizeFn(torch.autograd.Function):
         ctx.statics = statics
         ctx.num_intersects = M
         ctx.mark_non_differentiable(Ts, fidx)
+        ctx.set_materialize_grads(False)  # no zero tensors for the unused Ts / fidx grads
         return img, Ts, fidx
 
     @staticmethod

@@ -54,6 +54,12 @@ int fill_zero_i32(int32_t* p, int64_t n, hipStream_t stream) {
     return hipGetLastError() == hipSuccess ? 0 : fail(kErrLaunch, "fill launch failed");
 }
 
+// An operand is shared (rows == per) or batched (rows == per * B); the kernels index it as such,
+// so any other row count would read outside it (splax/_project/_kernels.py:70-75).
+static bool rows_match(int64_t rows, int64_t per, int64_t B) {
+    return rows == per || rows == per * B;
+}
+
 // ------------------------------------------------------------------ scratch
 
 constexpr int kMaxDevices = 64;
@@ -123,17 +129,15 @@ int DeviceScratch::ensure_sort(int64_t M, int64_t bins, int32_t B) {
         for (int k = 0; k < 2; ++k) {
             dev_free(&keys[k]);
             dev_free(&vals[k]);
+            dev_free(&gids[k]);
         }
-        dev_free(&owner);
-        dev_free(&ids);
         isect_cap = 0;
         int64_t cap = (int64_t)(M * 1.25) + 1;
         for (int k = 0; k < 2 && !rc; ++k) {
             rc = dev_alloc(&keys[k], cap, false);
             if (!rc) rc = dev_alloc(&vals[k], cap, false);
+            if (!rc) rc = dev_alloc(&gids[k], cap, false);
         }
-        if (!rc) rc = dev_alloc(&owner, cap, false);
-        if (!rc) rc = dev_alloc(&ids, cap, false);
         if (rc) return rc;
         isect_cap = cap;
     }
@@ -205,9 +209,8 @@ void DeviceScratch::release() {
     for (int k = 0; k < 2; ++k) {
         dev_free(&keys[k]);
         dev_free(&vals[k]);
+        dev_free(&gids[k]);
     }
-    dev_free(&owner);
-    dev_free(&ids);
     isect_cap = 0;
     dev_free(&rgrad);
     rgrad_cap = 0;
@@ -253,7 +256,7 @@ void release_all_scratch() {
 // ------------------------------------------------------------------ stage timing
 
 static std::mutex g_timing_mu;
-static bool g_timing = false;
+static uint32_t g_timing_mask = 0;  // bit s set: stage s is bracketed by events
 struct TimedSpan {
     int stage;
     hipEvent_t a, b;
@@ -274,7 +277,7 @@ static hipEvent_t take_event() {
 
 StageTimer::StageTimer(hipStream_t s, int st) : stream(s), stage(st) {
     std::lock_guard<std::mutex> lock(g_timing_mu);
-    if (!g_timing) return;
+    if (!((g_timing_mask >> st) & 1u)) return;
     start = take_event();
     (void)hipEventRecord(start, stream);
 }
@@ -318,9 +321,9 @@ const char* splat_last_error(void) { return g_last_error.c_str(); }
 
 void splat_clear_cache(void) { release_all_scratch(); }
 
-int splat_set_stage_timing(int enabled) {
+int splat_set_stage_timing(int stage_mask) {
     std::lock_guard<std::mutex> lock(g_timing_mu);
-    g_timing = enabled != 0;
+    g_timing_mask = (uint32_t)stage_mask & ((1u << kNumStages) - 1u);
     return 0;
 }
 
@@ -360,11 +363,16 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
     if (num_gaussians <= 0 || total < 0 || total % num_gaussians != 0 || img_h <= 0 ||
         img_w <= 0)
         return fail(kErrArgs, "project_fwd: invalid sizes");
-    if (rows_means < num_gaussians || rows_scales < num_gaussians ||
-        rows_quats < num_gaussians || rows_opac < num_gaussians || rows_viewmat < 4)
-        return fail(kErrArgs, "project_fwd: operand has fewer rows than num_gaussians");
-    if (has_transforms && (num_transforms <= 0 || !transforms || !transform_ids))
-        return fail(kErrArgs, "project_fwd: transforms requested but not given");
+    const int64_t B = total / num_gaussians;
+    if (!rows_match(rows_means, num_gaussians, B) || !rows_match(rows_scales, num_gaussians, B) ||
+        !rows_match(rows_quats, num_gaussians, B) || !rows_match(rows_opac, num_gaussians, B) ||
+        !rows_match(rows_viewmat, 4, B))
+        return fail(kErrArgs, "project_fwd: operand rows must be num_gaussians (shared) or "
+                              "B * num_gaussians (batched); viewmat 4 or 4 * B");
+    if (has_transforms && (num_transforms <= 0 || !transforms || !transform_ids ||
+                           !rows_match(rows_transforms, num_transforms, B)))
+        return fail(kErrArgs, "project_fwd: transforms requested but not given (or rows not "
+                              "num_transforms / B * num_transforms)");
     if (total >= ((int64_t)1 << 31))
         return fail(kErrArgs, "project_fwd: more than 2^31 items");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -405,7 +413,15 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
                       float fy, float glob_scale, float* v_mean3d, float* v_scale,
                       float* v_quat, float* v_viewmat, float* v_transforms) {
     if (num_gaussians <= 0 || B <= 0) return fail(kErrArgs, "project_bwd: invalid sizes");
-    if (has_transforms && (num_transforms <= 0 || !transforms || !transform_ids || !v_transforms))
+    if (!rows_match(rows_means, num_gaussians, B) || !rows_match(rows_scales, num_gaussians, B) ||
+        !rows_match(rows_quats, num_gaussians, B) || !rows_match(rows_viewmat, 4, B) ||
+        !rows_match(rows_radii, num_gaussians, B) || !rows_match(rows_conics, num_gaussians, B) ||
+        !rows_match(rows_vxy, num_gaussians, B) || !rows_match(rows_vconic, num_gaussians, B) ||
+        (v_depth && !rows_match(rows_vdepth, num_gaussians, B)))
+        return fail(kErrArgs, "project_bwd: operand rows must be num_gaussians (shared) or "
+                              "B * num_gaussians (batched); viewmat 4 or 4 * B");
+    if (has_transforms && (num_transforms <= 0 || !transforms || !transform_ids ||
+                           !v_transforms || !rows_match(rows_transforms, num_transforms, B)))
         return fail(kErrArgs, "project_bwd: transforms requested but not given");
     if ((int64_t)B * num_gaussians >= ((int64_t)1 << 31))
         return fail(kErrArgs, "project_bwd: more than 2^31 items");
@@ -433,12 +449,15 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
     return rc;
 }
 
-static int check_raster(const RasterInputs& in) {
+static int check_raster(const RasterInputs& in, int32_t B_out) {
     if (in.n <= 0 || in.B_geom <= 0 || in.img_h <= 0 || in.img_w <= 0)
         return fail(kErrArgs, "rasterize: invalid sizes");
     if (in.rows_colors < in.n || in.rows_opac < in.n || in.rows_map_opac < in.n ||
         in.rows_bg < 1)
         return fail(kErrArgs, "rasterize: operand has fewer rows than num_gaussians");
+    // the background is indexed per output image when it has more than one row
+    if (in.rows_bg > 1 && in.rows_bg < B_out)
+        return fail(kErrArgs, "rasterize: background needs 1 or B rows");
     if ((int64_t)in.B_geom * in.n >= ((int64_t)1 << 31))
         return fail(kErrArgs, "rasterize: more than 2^31 items");
     return 0;
@@ -458,7 +477,7 @@ int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* dep
     in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
     in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B;
     in.img_h = img_h; in.img_w = img_w;
-    int rc = check_raster(in);
+    int rc = check_raster(in, B);
     if (rc) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     DeviceScratch& sc = scratch_for_current_device();
@@ -482,7 +501,7 @@ int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* dep
     if (M > 0) {
         if (hipMemcpyAsync(sorted_keys, sc.keys[0], M * sizeof(int32_t), hipMemcpyDeviceToDevice,
                            s) != hipSuccess ||
-            hipMemcpyAsync(sorted_ids, sc.ids, M * sizeof(int32_t), hipMemcpyDeviceToDevice,
+            hipMemcpyAsync(sorted_ids, sc.gids[0], M * sizeof(int32_t), hipMemcpyDeviceToDevice,
                            s) != hipSuccess)
             return fail(kErrRuntime, "sorted copy failed");
     }
@@ -505,7 +524,7 @@ int splat_rasterize_fwd(splat_stream_t stream, const float* colors, int64_t rows
     in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
     in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B;
     in.img_h = img_h; in.img_w = img_w;
-    int rc = check_raster(in);
+    int rc = check_raster(in, B);
     if (rc) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     DeviceScratch& sc = scratch_for_current_device();
@@ -522,7 +541,7 @@ int splat_rasterize_fwd(splat_stream_t stream, const float* colors, int64_t rows
     if (num_intersects) *num_intersects = M;
     if (rc) return rc;
     StageTimer tm(s, kStageBlendFwd);
-    rc = launch_blend_fwd(in, L, M > 0 ? sc.ids : nullptr, sc.tile_bins, final_Ts,
+    rc = launch_blend_fwd(in, L, M > 0 ? sc.gids[0] : nullptr, sc.tile_bins, final_Ts,
                           final_idx, out_img, s);
     if (rc) return fail(rc, "blend_fwd launch failed");
     return 0;
@@ -534,9 +553,9 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
                              const float* background, int64_t rows_bg, const float* xys,
                              const float* depths, const int32_t* radii, const float* conics,
                              const int32_t* cum_tiles_hit, int32_t num_gaussians, int32_t B,
-                             int32_t img_h, int32_t img_w, int64_t num_intersects,
-                             float* final_Ts, int32_t* final_idx, float* out_img,
-                             int32_t* sorted_ids, int32_t* sorted_pos, int32_t* tile_bins) {
+                             int32_t img_h, int32_t img_w, int64_t capacity, float* final_Ts,
+                             int32_t* final_idx, float* out_img, int32_t* sorted_ids,
+                             int32_t* sorted_pos, int32_t* tile_bins, int64_t* num_intersects) {
     RasterInputs in{};
     in.colors = colors; in.rows_colors = rows_colors;
     in.opac = opacities; in.rows_opac = rows_opac;
@@ -545,10 +564,9 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
     in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
     in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B;
     in.img_h = img_h; in.img_w = img_w;
-    int rc = check_raster(in);
+    int rc = check_raster(in, B);
     if (rc) return rc;
-    if (num_intersects < 0 || !tile_bins ||
-        (num_intersects > 0 && (!sorted_ids || !sorted_pos)))
+    if (capacity < 0 || !tile_bins || (capacity > 0 && (!sorted_ids || !sorted_pos)))
         return fail(kErrArgs, "rasterize_fwd_keep: missing sorted-list buffers");
     hipStream_t s = static_cast<hipStream_t>(stream);
     DeviceScratch& sc = scratch_for_current_device();
@@ -560,13 +578,14 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
     }
     if (rc) return rc;
     SortTargets tgt;
-    tgt.M_known = num_intersects;
+    tgt.capacity = capacity;
     tgt.ids = sorted_ids;
     tgt.pos = sorted_pos;
     tgt.bins = tile_bins;
     int64_t M = 0;
     KeyLayout L;
     rc = run_sort_and_bin(in, sc, s, &M, &L, &tgt);
+    if (num_intersects) *num_intersects = M;
     if (rc) return rc;
     StageTimer tm(s, kStageBlendFwd);
     rc = launch_blend_fwd(in, L, M > 0 ? sorted_ids : nullptr, tile_bins, final_Ts, final_idx,
@@ -593,7 +612,7 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
     in.xys = xys; in.depths = nullptr; in.radii = nullptr; in.conics = conics;
     in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B_geom;
     in.img_h = img_h; in.img_w = img_w;
-    int rc = check_raster(in);
+    int rc = check_raster(in, B_out);
     if (rc) return rc;
     if (B_out <= 0 || (B_geom > 1 && B_geom != B_out))
         return fail(kErrArgs, "rasterize_bwd_sorted: B_geom must be 1 or equal to B_out");
@@ -638,7 +657,7 @@ int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows
     in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
     in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B_geom;
     in.img_h = img_h; in.img_w = img_w;
-    int rc = check_raster(in);
+    int rc = check_raster(in, B_out);
     if (rc) return rc;
     if (B_out <= 0 || (B_geom > 1 && B_geom != B_out))
         return fail(kErrArgs, "rasterize_bwd: B_geom must be 1 or equal to B_out");
@@ -667,7 +686,7 @@ int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows
     a.sorted_pos = sc.vals[0]; a.M = M; a.rgrad = sc.rgrad;
     a.v_colors = v_colors; a.v_opacity = v_opacity; a.v_xy = v_xy; a.v_conic = v_conic;
     StageTimer tm(s, kStageBlendBwd);
-    rc = launch_blend_bwd(in, L, M > 0 ? sc.ids : nullptr, sc.tile_bins, a, s);
+    rc = launch_blend_bwd(in, L, M > 0 ? sc.gids[0] : nullptr, sc.tile_bins, a, s);
     if (rc) return fail(rc, "blend_bwd launch failed");
     return 0;
 }

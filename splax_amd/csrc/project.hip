@@ -332,7 +332,7 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
             float vpx = fx * vxy[0], vpy = fy * vxy[1];
             float vvx = vpx * rw, vvy = vpy * rw;
             float vvz = -(vpx * tx + vpy * ty) * rw * rw;
-            vvz = vvz + P.v_depth[vd_idx];
+            vvz = vvz + (P.v_depth ? P.v_depth[vd_idx] : 0.0f);  // NULL: zero cotangent
             float v_cov[9] = {vcov0, 0.5f * vcov1, 0.0f, 0.5f * vcov1, vcov2, 0.0f,
                               0.0f, 0.0f, 0.0f};
             float tmp[9], v_V[9], v_T[9], v_J[9], two_vcov[9];

@@ -12,11 +12,9 @@
 // waves in order, partitions in index order), so the sort is stable: ties keep emission order,
 // which is the reference's (key, position) order.
 //
-// The sorted values are emission positions rather than the reference's flat item ids: emission
-// records the owning item per position (`owner`), and the last pass writes both the sorted
-// positions and the sorted item ids (owner[position]). The item ids are exactly the reference's
-// sorted values; the positions let the backward blend store each intersection's gradient in
-// emission order, where every item's intersections are contiguous.
+// Each key carries two values: the reference's value (the flat item id) and the key's emission
+// position. The positions let the backward blend store each intersection's gradient in emission
+// order, where every item's intersections are contiguous.
 #include "splat_common.hpp"
 #include "splat_internal.hpp"
 
@@ -263,17 +261,18 @@ __device__ __forceinline__ uint32_t block_exclusive_scan_256(uint32_t v, uint32_
     return off + incl - v;
 }
 
-// Values are emission positions: the first pass generates them (vals_in == nullptr gives value
-// = position), later passes carry them. The last pass also writes, per sorted slot, the flat item
-// that emitted the key (ids_out[dest] = owner[value]), when owner is non-null.
+// Two values travel with each key: its emission position and the flat item that emitted it.
+// The first pass generates the positions (vals_in == nullptr gives value = position) and reads
+// the items in emission order, so no pass gathers at random.
 __global__ void __launch_bounds__(kSortThreads)
 onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
-                     int32_t* __restrict__ keys_out, int32_t* __restrict__ vals_out,
-                     const int32_t* __restrict__ owner, int32_t* __restrict__ ids_out, int64_t M,
+                     const int32_t* __restrict__ ids_in, int32_t* __restrict__ keys_out,
+                     int32_t* __restrict__ vals_out, int32_t* __restrict__ ids_out, int64_t M,
                      int shift, const uint32_t* __restrict__ hist, uint64_t* status,
                      uint32_t epoch, uint32_t* err) {
     __shared__ uint32_t s_keys[kSortTile];
     __shared__ uint32_t s_vals[kSortTile];
+    __shared__ uint32_t s_ids[kSortTile];
     __shared__ uint32_t s_cnt[kSortWaves][256];
     __shared__ uint32_t s_local_start[256];
     __shared__ int32_t s_dest_base[256];
@@ -287,13 +286,14 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
     const int64_t base = (int64_t)part * kSortTile;
     const int64_t wbase = base + (int64_t)wave * (kSortItems * 64);
 
-    // keys and values are both loaded up front so their latencies overlap
-    uint32_t key[kSortItems], val[kSortItems];
+    // keys and values are all loaded up front so their latencies overlap
+    uint32_t key[kSortItems], val[kSortItems], gid[kSortItems];
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
         int64_t pos = wbase + i * 64 + lane;
         key[i] = pos < M ? (uint32_t)keys_in[pos] : 0xffffffffu;
         val[i] = pos < M ? (vals_in ? (uint32_t)vals_in[pos] : (uint32_t)pos) : 0u;
+        gid[i] = pos < M ? (uint32_t)ids_in[pos] : 0u;
     }
 
     // stable per-wave ranking: lanes with equal digits found by 8 ballots
@@ -384,6 +384,7 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
         const uint32_t slot = s_local_start[dd] + s_cnt[wave][dd] + rank[i];
         s_keys[slot] = key[i];
         s_vals[slot] = val[i];
+        s_ids[slot] = gid[i];
     }
     __syncthreads();
     // each digit's run is contiguous in the output: consecutive j write consecutive addresses
@@ -394,10 +395,9 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
         if (j < valid) {
             const uint32_t k = s_keys[j];
             const int64_t dest = (int64_t)s_dest_base[(k >> shift) & 255u] + j;
-            const uint32_t v = s_vals[j];
             keys_out[dest] = (int32_t)k;
-            vals_out[dest] = (int32_t)v;
-            if (owner) ids_out[dest] = owner[v];
+            vals_out[dest] = (int32_t)s_vals[j];
+            ids_out[dest] = (int32_t)s_ids[j];
         }
     }
 }
@@ -504,10 +504,13 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     if (M < 0) return fail(kErrTooMany, "intersection count overflowed int32");
     if (M >= ((int64_t)1 << 31)) return fail(kErrTooMany, "more than 2^31 - 1 intersections");
     *M_out = M;
+    if (tgt && tgt->capacity >= 0 && M > tgt->capacity)
+        return fail(kErrTooMany, "sorted-list buffers hold " + std::to_string(tgt->capacity) +
+                                     " intersections, " + std::to_string(M) + " needed");
     rc = sc.ensure_sort(M, nbins, B);
     if (rc) return rc;
     if (M == 0) return fill_zero_i32(bins, 2 * nbins, stream);
-    int32_t* ids_final = (tgt && tgt->ids) ? tgt->ids : sc.ids;
+    int32_t* ids_final = (tgt && tgt->ids) ? tgt->ids : sc.gids[0];
     int32_t* pos_final = (tgt && tgt->pos) ? tgt->pos : sc.vals[0];
 
     {
@@ -517,7 +520,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         E.map_opac = in.map_opac; E.rows_map_opac = in.rows_map_opac;
         E.cum = in.cum; E.mm = sc.depth_mm; E.n = in.n; E.total = total; E.M = M;
         E.tiles_x = L.tiles_x; E.tiles_y = L.tiles_y; E.tile_bits = L.tile_bits;
-        E.depth_bits = L.depth_bits; E.keys = sc.keys[0]; E.owner = sc.owner;
+        E.depth_bits = L.depth_bits; E.keys = sc.keys[0]; E.owner = sc.gids[0];
         hipLaunchKernelGGL(emit_keys_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                            stream, E);
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "emit launch failed");
@@ -531,16 +534,16 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
                            sc.keys[0], M, chunk, sc.hist, bins, 2 * nbins);
         const int64_t parts = (M + kSortTile - 1) / kSortTile;
         // passes 0..3 ping-pong 0 -> 1 -> 0 -> 1 -> 0; the first pass generates the emission
-        // positions, the last writes them and the owning items straight into their final
-        // buffers (the caller's when it keeps the sorted lists)
+        // positions, the last writes positions and items straight into their final buffers
+        // (the caller's when it keeps the sorted lists)
         for (int pass = 0; pass < 4; ++pass) {
             const int src = pass & 1, dst = 1 - src;
             const bool last = pass == 3;
             hipLaunchKernelGGL(onesweep_pass_kernel, dim3((unsigned)parts), dim3(kSortThreads), 0,
                                stream, sc.keys[src], pass == 0 ? nullptr : sc.vals[src],
-                               sc.keys[dst], last ? pos_final : sc.vals[dst],
-                               last ? sc.owner : nullptr, last ? ids_final : nullptr, M,
-                               8 * pass, sc.hist + 256 * pass, sc.sort_status, sc.next_epoch(),
+                               sc.gids[src], sc.keys[dst], last ? pos_final : sc.vals[dst],
+                               last ? ids_final : sc.gids[dst], M, 8 * pass,
+                               sc.hist + 256 * pass, sc.sort_status, sc.next_epoch(),
                                sc.tickets + kDeviceError);
         }
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "sort launch failed");

@@ -95,8 +95,7 @@ struct DeviceScratch {
     // sort
     int32_t* keys[2] = {nullptr, nullptr};
     int32_t* vals[2] = {nullptr, nullptr};  // emission positions (ping-pong)
-    int32_t* owner = nullptr;               // flat item of each emission position
-    int32_t* ids = nullptr;                 // sorted flat item ids
+    int32_t* gids[2] = {nullptr, nullptr};  // flat item ids (ping-pong; [0] ends sorted)
     int64_t isect_cap = 0;
     // backward: nine partial gradient sums per (output image, intersection), emission order
     float* rgrad = nullptr; int64_t rgrad_cap = 0;
@@ -151,16 +150,19 @@ int launch_project_bwd(const ProjectBwdArgs& a, hipStream_t stream);
 
 // Optional caller-owned destinations of sort_and_bin: M_known >= 0 skips the count readback
 // (it must equal cum[B*n - 1]); ids / pos / bins (when non-null) receive the sorted gaussian ids,
-// the sorted emission positions and the tile bins instead of the library scratch.
+// the sorted emission positions and the tile bins instead of the library scratch. With
+// capacity >= 0, an M above it stops the call with kErrTooMany (M is still reported) before
+// anything is written to ids / pos / bins.
 struct SortTargets {
     int64_t M_known = -1;
+    int64_t capacity = -1;
     int32_t* ids = nullptr;
     int32_t* pos = nullptr;
     int32_t* bins = nullptr;
 };
 
 // sort_and_bin: returns M (>= 0) in *M_out; sorted keys in sc.keys[0]; sorted ids in tgt->ids or
-// sc.ids; sorted emission positions in tgt->pos or sc.vals[0]; tile bins in tgt->bins or
+// sc.gids[0]; sorted emission positions in tgt->pos or sc.vals[0]; tile bins in tgt->bins or
 // sc.tile_bins.
 int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stream,
                      int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt = nullptr);

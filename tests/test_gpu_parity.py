@@ -178,6 +178,16 @@ def test_project_bwd_matches_oracle(name):
     for label, g, r in zip(("v_mean3d", "v_scale", "v_quat"), got[:3], ref[:3]):
         assert_bit_exact(_np(g).reshape(r.shape), r, f"{name}/{label}")
     _grad_compare(_np(got[3]), ref[3], f"{name}/v_viewmat", rel_tol=1e-5)
+    # a NULL depth cotangent is a zero one, bit for bit
+    zero = _ops.project_bwd(_t(s.means), _t(s.scales), _t(q), _t(s.viewmats[0]), _t(radii),
+                            _t(conics), _t(v_xy), torch.zeros(s.n, device="cuda"), _t(v_conic),
+                            tf, ids, n=s.n, B=1, num_transforms=1, has_transforms=False, f=s.f,
+                            glob_scale=1.0)
+    none = _ops.project_bwd(_t(s.means), _t(s.scales), _t(q), _t(s.viewmats[0]), _t(radii),
+                            _t(conics), _t(v_xy), None, _t(v_conic), tf, ids, n=s.n, B=1,
+                            num_transforms=1, has_transforms=False, f=s.f, glob_scale=1.0)
+    for label, a, b in zip(("v_mean3d", "v_scale", "v_quat"), zero[:3], none[:3]):
+        assert_bit_exact(_np(b), _np(a), f"{name}/{label} null v_depth")
 
 
 def test_batched_cameras_one_launch():

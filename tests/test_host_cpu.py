@@ -126,3 +126,29 @@ def test_look_at_properties():
         o = vm[k] @ np.array([0, 0, 0, 1.0])
         np.testing.assert_allclose(o[:2], 0.0, atol=1e-5)  # the target lies on the +z axis
         assert o[2] > 0
+
+
+def test_abi_rejects_rows_that_are_neither_shared_nor_batched():
+    """Operands must have n (shared) or B*n (batched) rows; the C ABI rejects anything else
+    with status 1 before touching the device (so this runs without a GPU)."""
+    import ctypes
+
+    lib = _lib.lib()
+    lib.splat_last_error.restype = ctypes.c_char_p
+    f = ctypes.c_float
+    n, total = 10, 30  # B = 3
+    null = None
+
+    def fwd(rows_means, rows_view):
+        return lib.splat_project_fwd(null, null, rows_means, null, n, null, n, null, rows_view,
+                                     null, n, null, 1, null, n, 1, 0, total, 16, 16, f(10.0),
+                                     f(10.0), f(8.0), f(8.0), f(1.0), f(0.01), null, null, null,
+                                     null, null, null)
+
+    assert fwd(20, 4) == 1  # between n and B*n
+    assert b"rows" in lib.splat_last_error()
+    assert fwd(5, 4) == 1   # fewer than n
+    assert fwd(n, 8) == 1   # viewmat neither 4 nor 4B
+    rc = lib.splat_rasterize_fwd(null, null, n, null, n, null, n, null, 2, null, null, null,
+                                 null, null, n, 3, 16, 16, null, null, null, null)
+    assert rc == 1 and b"background" in lib.splat_last_error()
