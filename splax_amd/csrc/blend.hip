@@ -16,8 +16,7 @@
 // Backward: the same staging walked back to front from the workgroup's largest final_idx. A
 // pixel's contribution to a record is nine floats; per record the contributing lanes of a wave
 // reduce them with a reduce-scatter (v_permlane32_swap, v_permlane16_swap, then DPP row shifts:
-// 28 VALU for nine values) and add the totals into the record's LDS accumulator. Events with few
-// contributing lanes skip the reduction and add their values straight into LDS. After each batch
+// 28 VALU for nine values) and add the totals into the record's LDS accumulator. After each batch
 // every record stores its nine sums (plain stores, no global atomics) at its emission position,
 // where all intersections of one item are contiguous; grad_gather_kernel then adds them per item
 // in a fixed order and writes the four gradient outputs. Only the LDS sums of one record over
@@ -282,11 +281,12 @@ __device__ __forceinline__ float swap16_add(float a, float b) {
                                               false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
-__device__ __forceinline__ float row_sum_to_lane15(float v) {
+// Lanes 7 and 15 of each 16-lane row end with the sums of the row's lower and upper halves;
+// both add into LDS (a two-lane collision there costs less than one more DPP step).
+__device__ __forceinline__ float row_halves_to_lanes_7_15(float v) {
     v = dpp_add<0x111, 0xf>(v);  // row_shr:1
     v = dpp_add<0x112, 0xf>(v);  // row_shr:2
     v = dpp_add<0x114, 0xf>(v);  // row_shr:4
-    v = dpp_add<0x118, 0xf>(v);  // row_shr:8
     return v;
 }
 
@@ -368,63 +368,45 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             const float4 r0 = L.r0[t], r1 = L.r1[t];
             const float dx = r0.x - px, dy = r0.y - py;
             const float sigma = 0.5f * (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
-            bool valid = idx <= bin_final && sigma >= 0.0f && sigma <= r1.z;
-            if (__ballot(valid) == 0ull) continue;
-            float vis = 0.f, alpha = 0.f;
-            if (valid) {
-                vis = exp_core(-sigma);
-                alpha = minw(kAlphaMax, r1.y * vis);
-                valid = alpha >= kAlphaThresh;
-            }
-            const uint64_t vb = __ballot(valid);
-            if (vb == 0ull) continue;
-            float g0 = 0.f, g1 = 0.f, g2 = 0.f, g3 = 0.f, g4 = 0.f, g5 = 0.f, g6 = 0.f, g7 = 0.f,
-                  g8 = 0.f;
-            if (valid) {
-                const float4 r2 = L.r2[t];
-                const float d = 1.0f - alpha;
-                float ra = __builtin_amdgcn_rcpf(d);
-                ra = fmaf(ra, fmaf(-d, ra, 1.0f), ra);
-                T = T * ra;
-                const float fac = alpha * T;
-                const float cv = fmaf(r2.x, v0, fmaf(r2.y, v1, r2.z * v2));
-                const float v_alpha = fmaf(T, cv, -ra * (bufv + tfbg));
-                bufv = fmaf(cv, fac, bufv);
-                g0 = v0 * fac;
-                g1 = v1 * fac;
-                g2 = v2 * fac;
-                const float ov = r1.y * vis;
-                if (ov <= kAlphaMax) {
-                    const float vs = -ov * v_alpha;
-                    const float hx = vs * dx, hy = vs * dy;
-                    g3 = 0.5f * hx * dx;
-                    g4 = hx * dy;
-                    g5 = 0.5f * hy * dy;
-                    g6 = hx;
-                    g7 = hy;
-                    g8 = vis * v_alpha;
-                }
-            }
+            // bitwise: no short-circuit branch around the sigma_max read
+            const bool in_range = (idx <= bin_final) & (sigma >= 0.0f) & (sigma <= r1.z);
+            if (__builtin_amdgcn_ballot_w64(in_range) == 0ull) continue;
+            // Every lane computes and the lanes outside the accepted set are masked by selects
+            // (an exec-masked instruction costs the same issue slot), so the wave reduction
+            // below always sees exact zeros there and no branch is needed.
+            const float vis = exp_core(-sigma);
+            const float alpha = minw(kAlphaMax, r1.y * vis);
+            const bool valid = in_range && alpha >= kAlphaThresh;
+            const float4 r2 = L.r2[t];
+            const float d = 1.0f - alpha;
+            float ra = __builtin_amdgcn_rcpf(d);
+            ra = fmaf(ra, fmaf(-d, ra, 1.0f), ra);
+            const float Tn = T * ra;
+            T = valid ? Tn : T;
+            const float fac = valid ? alpha * Tn : 0.0f;
+            const float cv = fmaf(r2.x, v0, fmaf(r2.y, v1, r2.z * v2));
+            const float v_alpha = fmaf(Tn, cv, -ra * (bufv + tfbg));
+            bufv = fmaf(cv, fac, bufv);
+            const float ov = r1.y * vis;
+            const bool geo = valid && ov <= kAlphaMax;
+            const float vs = geo ? -ov * v_alpha : 0.0f;
+            const float hx = vs * dx, hy = vs * dy;
+            const float g0 = v0 * fac, g1 = v1 * fac, g2 = v2 * fac;
+            const float g3 = 0.5f * hx * dx, g4 = hx * dy, g5 = 0.5f * hy * dy;
+            const float g6 = hx, g7 = hy;
+            const float g8 = geo ? vis * v_alpha : 0.0f;
             float* a = &ACC(t, 0);
-            if (__popcll(vb) <= 2) {
-                // few contributors: add straight into LDS (at most two lanes per address)
-                if (valid) {
-                    atomicAdd(a + 0, g0); atomicAdd(a + 1, g1); atomicAdd(a + 2, g2);
-                    atomicAdd(a + 3, g3); atomicAdd(a + 4, g4); atomicAdd(a + 5, g5);
-                    atomicAdd(a + 6, g6); atomicAdd(a + 7, g7); atomicAdd(a + 8, g8);
-                }
-                continue;
-            }
             // reduce-scatter over the wave: after the swaps, row r of qa holds g0/g2/g1/g3 and
-            // of qb g4/g6/g5/g7 (rows 0..3), qc holds g8 in every row; row sums land in lane 15.
+            // of qb g4/g6/g5/g7 (rows 0..3), qc holds g8 in every row; the half-row sums land
+            // in lanes 7 and 15.
             const float p01 = swap32_add(g0, g1), p23 = swap32_add(g2, g3);
             const float p45 = swap32_add(g4, g5), p67 = swap32_add(g6, g7);
             const float p8 = swap32_add(g8, g8);
             float qa = swap16_add(p01, p23), qb = swap16_add(p45, p67), qc = swap16_add(p8, p8);
-            qa = row_sum_to_lane15(qa);
-            qb = row_sum_to_lane15(qb);
-            qc = row_sum_to_lane15(qc);
-            if ((lane & 15) == 15) {
+            qa = row_halves_to_lanes_7_15(qa);
+            qb = row_halves_to_lanes_7_15(qb);
+            qc = row_halves_to_lanes_7_15(qc);
+            if ((lane & 7) == 7) {
                 const int ka = (row == 0) ? 0 : (row == 1) ? 2 : (row == 2) ? 1 : 3;
                 atomicAdd(a + ka, qa);
                 atomicAdd(a + 4 + ka, qb);

@@ -3,7 +3,7 @@
 Bars: projection outputs, intersection keys, sorted order, tile ranges,
 final_Ts / final_idx and the forward image are bit-exact (both sides follow one arithmetic
 contract); gradients that the GPU accumulates with float atomics are compared by relative
-Frobenius norm (< 1e-5) plus allclose(rtol=1e-4, atol=1e-6 * max|ref|); per-item projection
+Frobenius norm (< 1e-5) plus allclose(rtol=1e-4, atol=1e-5 * max|ref|); per-item projection
 gradients (no reduction) are bit-exact.
 """
 
@@ -126,12 +126,16 @@ def test_rasterize_fwd_bit_exact(name):
 
 
 def _grad_compare(got, ref, label, rel_tol=1e-5):
+    """Float-sum comparison: relative Frobenius error below rel_tol over the whole array, and per
+    element |got - ref| <= 1e-4 |ref| + 1e-5 max|ref|. The absolute floor covers elements that are
+    sums of terms cancelling to a small fraction of the array's scale (v_xy near a gaussian's
+    centre), whose last bits depend on the summation order."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     r = rel_fro(got, ref)
     assert r < rel_tol, f"{label}: relative Frobenius error {r:.3e}"
     scale = float(np.abs(ref).max()) + 1e-30
-    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-6 * scale, err_msg=label)
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5 * scale, err_msg=label)
 
 
 @pytest.mark.parametrize("name", list(CASES))
