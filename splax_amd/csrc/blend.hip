@@ -193,11 +193,14 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
         if (__ballot(!done) == 0ull) continue;
         const uint8_t* list = L.list[uniform(wave)];
         for (int k = 0; k < len; ++k) {
+            // the wave stops walking its list once all of its pixels are done
+            if (__builtin_amdgcn_ballot_w64(!done) == 0ull) break;
             const int t = uniform(list[k]);
             const float4 r0 = L.r0[t], r1 = L.r1[t];
             const float dx = r0.x - px, dy = r0.y - py;
             const float sigma = 0.5f * (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
-            if (done || !(sigma >= 0.0f && sigma <= r1.z)) continue;
+            // bitwise: no short-circuit branch around the sigma_max read (NaN sigma fails both)
+            if (!((!done) & (sigma >= 0.0f) & (sigma <= r1.z))) continue;
             const float alpha = minw(kAlphaMax, r1.y * exp_core(-sigma));
             if (alpha < kAlphaThresh) continue;
             const float next_T = T * (1.0f - alpha);
@@ -406,6 +409,9 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             qa = row_halves_to_lanes_7_15(qa);
             qb = row_halves_to_lanes_7_15(qb);
             qc = row_halves_to_lanes_7_15(qc);
+            // Empty uses keep the last DPP adds in this block: sunk into the branch below they
+            // would no longer fuse with their DPP moves (two extra VALU each).
+            asm volatile("" ::"v"(qa), "v"(qb), "v"(qc));
             if ((lane & 7) == 7) {
                 const int ka = (row == 0) ? 0 : (row == 1) ? 2 : (row == 2) ? 1 : 3;
                 atomicAdd(a + ka, qa);
