@@ -73,6 +73,19 @@ int splat_rasterize_fwd(splat_stream_t stream, const float* colors, int64_t rows
                         float* final_Ts, int32_t* final_idx, float* out_img,
                         int64_t* num_intersects);
 
+/* Replaces _rasterize_depth_warp (splax/_rasterize/_kernels.py:208-262, FFI callable :265-274):
+ * splat_rasterize_fwd plus the expected-depth channel out_depth [B*H, W] = sum of depths[g] times
+ * the colour blend's weights (no background term); the image, final_Ts and final_idx equal
+ * splat_rasterize_fwd's bit for bit. */
+int splat_rasterize_depth_fwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
+                              const float* opacities, int64_t rows_opac,
+                              const float* map_opacities, int64_t rows_map_opac,
+                              const float* background, int64_t rows_bg, const float* xys,
+                              const float* depths, const int32_t* radii, const float* conics,
+                              const int32_t* cum_tiles_hit, int32_t num_gaussians, int32_t B,
+                              int32_t img_h, int32_t img_w, float* final_Ts, int32_t* final_idx,
+                              float* out_img, float* out_depth, int64_t* num_intersects);
+
 /* Replaces _rasterize_bwd_warp (splax/_rasterize/_kernels.py:386-500, FFI callable :503-512):
  * recomputes sort_and_bin over the B_geom geometry images (deterministic, so it reproduces the
  * forward order) and runs the backward blend over B_out output images. v_out_img has vout_rows
@@ -90,13 +103,30 @@ int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows
                         int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
                         float* v_xy, float* v_conic);
 
+/* Replaces _rasterize_bwd_depth_warp (splax/_rasterize/_kernels.py:797-914, FFI callable
+ * :917-926): splat_rasterize_bwd with the depth channel's cotangent v_out_depth
+ * (vdepth_rows rows of width W, B_out*H batched or H broadcast) and the extra output v_depths
+ * [B_out*num_gaussians] (the cotangent of the projection's depths). */
+int splat_rasterize_depth_bwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
+                              const float* opacities, int64_t rows_opac,
+                              const float* map_opacities, int64_t rows_map_opac,
+                              const float* background, int64_t rows_bg, const float* xys,
+                              const float* depths, const int32_t* radii, const float* conics,
+                              const int32_t* cum_tiles_hit, const float* final_Ts,
+                              const int32_t* final_idx, const float* v_out_img,
+                              int64_t vout_rows, const float* v_out_depth, int64_t vdepth_rows,
+                              int32_t num_gaussians, int32_t B_out, int32_t B_geom,
+                              int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
+                              float* v_xy, float* v_conic, float* v_depths);
+
 /* Forward that keeps the sorted intersection lists resident for the backward (no counterpart in
  * the reference, whose backward re-sorts, splax/_rasterize/_kernels.py:422). The caller passes
  * buffers sorted_ids [capacity], sorted_pos [capacity] and tile_bins [B*num_tiles, 2]; sorted_ids
  * and tile_bins receive exactly what splat_sort_and_bin returns, sorted_pos each sorted
  * intersection's emission position (its index in the cum_tiles_hit-ordered emission sequence).
  * num_intersects receives M. When M > capacity the call returns status 6 after the count
- * readback, with M reported and nothing written; the caller retries with larger buffers. Other
+ * readback, with M reported and nothing written; the caller retries with larger buffers.
+ * out_depth (may be NULL) selects the depth channel as in splat_rasterize_depth_fwd. Other
  * arguments and outputs as splat_rasterize_fwd. */
 int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t rows_colors,
                              const float* opacities, int64_t rows_opac,
@@ -105,23 +135,27 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
                              const float* depths, const int32_t* radii, const float* conics,
                              const int32_t* cum_tiles_hit, int32_t num_gaussians, int32_t B,
                              int32_t img_h, int32_t img_w, int64_t capacity, float* final_Ts,
-                             int32_t* final_idx, float* out_img, int32_t* sorted_ids,
-                             int32_t* sorted_pos, int32_t* tile_bins, int64_t* num_intersects);
+                             int32_t* final_idx, float* out_img, float* out_depth,
+                             int32_t* sorted_ids, int32_t* sorted_pos, int32_t* tile_bins,
+                             int64_t* num_intersects);
 
 /* Backward over the sorted lists kept by splat_rasterize_fwd_keep (no re-sort). Arguments as
  * splat_rasterize_bwd plus sorted_ids / sorted_pos / tile_bins / num_intersects of the matching
  * forward; the outputs equal splat_rasterize_bwd's (same kernels; additions can differ in order
- * only among a tile's four quadrant waves). */
+ * only among a tile's four quadrant waves). v_depths (may be NULL) selects the depth channel as
+ * in splat_rasterize_depth_bwd (then depths and v_out_depth are read). */
 int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64_t rows_colors,
                                const float* opacities, int64_t rows_opac,
                                const float* background, int64_t rows_bg, const float* xys,
-                               const float* conics, const int32_t* cum_tiles_hit,
-                               const int32_t* sorted_ids, const int32_t* sorted_pos,
-                               const int32_t* tile_bins, int64_t num_intersects,
-                               const float* final_Ts, const int32_t* final_idx,
-                               const float* v_out_img, int64_t vout_rows, int32_t num_gaussians,
-                               int32_t B_out, int32_t B_geom, int32_t img_h, int32_t img_w,
-                               float* v_colors, float* v_opacity, float* v_xy, float* v_conic);
+                               const float* depths, const float* conics,
+                               const int32_t* cum_tiles_hit, const int32_t* sorted_ids,
+                               const int32_t* sorted_pos, const int32_t* tile_bins,
+                               int64_t num_intersects, const float* final_Ts,
+                               const int32_t* final_idx, const float* v_out_img,
+                               int64_t vout_rows, const float* v_out_depth, int64_t vdepth_rows,
+                               int32_t num_gaussians, int32_t B_out, int32_t B_geom,
+                               int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
+                               float* v_xy, float* v_conic, float* v_depths);
 
 /* Replaces sort_and_bin (splax/_rasterize/_sort/_sort.py:29-171), exposed for callers that keep
  * the sorted lists: writes the M sorted packed keys and gaussian ids (capacity >= M required,

@@ -161,7 +161,8 @@ def sort_and_bin(xys, depths, radii, conics, map_opac, cum, *, n, B, img_shape):
 
 
 def blend_fwd(colors, opacities, background, xys, conics, sorted_ids, tile_bins, *, B,
-              img_shape):
+              img_shape, depths=None):
+    """Returns (img, Ts, fidx, stats) and, when depths is given, the expected depth (B*H, W)."""
     colors, opac, bg, xys, conics = map(_c32, (colors, opacities, background, xys, conics))
     ids, bins = _ci32(sorted_ids), _ci32(tile_bins)
     if ids.size == 0:
@@ -171,16 +172,22 @@ def blend_fwd(colors, opacities, background, xys, conics, sorted_ids, tile_bins,
     fidx = np.empty((B * H, W), np.int32)
     img = np.empty((B * H, W, 3), np.float32)
     stats = np.zeros(2, np.int64)
+    dep = None if depths is None else _c32(depths)
+    out_depth = None if depths is None else np.empty((B * H, W), np.float32)
     lib().oracle_blend_fwd(_f(colors), _i64(_rows(colors, 3)), _f(opac), _i64(opac.size), _f(bg),
                            _i64(_rows(bg, 3)), _f(xys), _f(conics), _i(ids), _i(bins), _i32(B),
                            _i32(H), _i32(W), _f(Ts), _i(fidx), _f(img),
-                           stats.ctypes.data_as(_i64p))
-    return img, Ts, fidx, stats
+                           stats.ctypes.data_as(_i64p), None if dep is None else _f(dep),
+                           None if out_depth is None else _f(out_depth))
+    if depths is None:
+        return img, Ts, fidx, stats
+    return img, Ts, fidx, stats, out_depth
 
 
 def rasterize_fwd(colors, opacities, map_opac, background, xys, depths, radii, conics, cum, *,
-                  n, B, img_shape):
-    """Returns (out_img (B*H, W, 3), final_Ts, final_idx, stats=[Pc, Pr], M)."""
+                  n, B, img_shape, render_depth=False):
+    """Returns (out_img (B*H, W, 3), final_Ts, final_idx, stats=[Pc, Pr], M), plus the expected
+    depth (B*H, W) last when render_depth."""
     colors, opac, mopac, bg, xys, depths, conics = map(
         _c32, (colors, opacities, map_opac, background, xys, depths, conics))
     radii, cum = _ci32(radii).ravel(), _ci32(cum).ravel()
@@ -189,19 +196,23 @@ def rasterize_fwd(colors, opacities, map_opac, background, xys, depths, radii, c
     fidx = np.empty((B * H, W), np.int32)
     img = np.empty((B * H, W, 3), np.float32)
     stats = np.zeros(2, np.int64)
+    out_depth = np.empty((B * H, W), np.float32) if render_depth else None
     m = lib().oracle_rasterize_fwd(
         _f(colors), _i64(_rows(colors, 3)), _f(opac), _i64(opac.size), _f(mopac),
         _i64(mopac.size), _f(bg), _i64(_rows(bg, 3)), _f(xys), _f(depths), _i(radii),
         _f(conics), _i(cum), _i32(n), _i32(B), _i32(H), _i32(W), _f(Ts), _i(fidx), _f(img),
-        stats.ctypes.data_as(_i64p))
+        stats.ctypes.data_as(_i64p), None if out_depth is None else _f(out_depth))
     if m < 0:
         raise ValueError(f"oracle rasterize_fwd failed with code {m}")
+    if render_depth:
+        return img, Ts, fidx, stats, int(m), out_depth
     return img, Ts, fidx, stats, int(m)
 
 
 def rasterize_bwd(colors, opacities, map_opac, background, xys, depths, radii, conics, cum,
-                  final_Ts, final_idx, v_out, *, n, B_out, B_geom, img_shape):
-    """Returns (v_colors, v_opacity, v_xy, v_conic, stats=[Qc, Qr]) sized B_out*n."""
+                  final_Ts, final_idx, v_out, *, n, B_out, B_geom, img_shape, v_out_depth=None):
+    """Returns (v_colors, v_opacity, v_xy, v_conic, stats=[Qc, Qr]) sized B_out*n; with
+    v_out_depth (the depth channel's cotangent) also v_depths, last."""
     colors, opac, mopac, bg, xys, depths, conics, Ts, vout = map(
         _c32, (colors, opacities, map_opac, background, xys, depths, conics, final_Ts, v_out))
     radii, cum, fidx = _ci32(radii).ravel(), _ci32(cum).ravel(), _ci32(final_idx)
@@ -212,15 +223,20 @@ def rasterize_bwd(colors, opacities, map_opac, background, xys, depths, radii, c
     v_xy = np.empty((nout, 2), np.float32)
     v_conic = np.empty((nout, 3), np.float32)
     stats = np.zeros(2, np.int64)
+    vd = None if v_out_depth is None else _c32(v_out_depth)
+    v_depths = None if vd is None else np.empty(nout, np.float32)
     m = lib().oracle_rasterize_bwd(
         _f(colors), _i64(_rows(colors, 3)), _f(opac), _i64(opac.size), _f(mopac),
         _i64(mopac.size), _f(bg), _i64(_rows(bg, 3)), _f(xys), _f(depths), _i(radii),
         _f(conics), _i(cum), _f(Ts), _i(fidx), _f(vout), _i64(vout.size // (3 * W)), _i32(n),
         _i32(B_out), _i32(B_geom), _i32(H), _i32(W), _f(v_colors), _f(v_opac), _f(v_xy),
-        _f(v_conic), stats.ctypes.data_as(_i64p))
+        _f(v_conic), stats.ctypes.data_as(_i64p), None if vd is None else _f(vd),
+        _i64(0 if vd is None else vd.size // W), None if v_depths is None else _f(v_depths))
     if m < 0:
         raise ValueError(f"oracle rasterize_bwd failed with code {m}")
-    return v_colors, v_opac, v_xy, v_conic, stats
+    if vd is None:
+        return v_colors, v_opac, v_xy, v_conic, stats
+    return v_colors, v_opac, v_xy, v_conic, stats, v_depths
 
 
 def project_bwd(means, scales, quats_xyzw, viewmat, radii, conics, v_xy, v_depth, v_conic, *, n,

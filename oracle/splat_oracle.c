@@ -603,13 +603,16 @@ int64_t oracle_sort_and_bin(const float* xys, const float* depths, const int32_t
 /* ---------------------------------------------------------------- forward blend
  * _rasterize_kernel, splax/_rasterize/_kernels.py:102-205. Per pixel the blend walks the tile's
  * sorted range front to back; the block-wide batching and early-exit vote of the reference do not
- * change any pixel's result, so the oracle walks each pixel's range directly. */
+ * change any pixel's result, so the oracle walks each pixel's range directly. With out_depth the
+ * walk also accumulates the expected depth, _rasterize_depth_kernel (:277-383): depth[g] times the
+ * same blend weight, no background term. */
 
 void oracle_blend_fwd(const float* colors, int64_t rows_colors, const float* opacities,
                       int64_t rows_opac, const float* background, int64_t rows_bg,
                       const float* xys, const float* conics, const int32_t* sorted_ids,
                       const int32_t* tile_bins, int32_t B, int32_t img_h, int32_t img_w,
-                      float* final_Ts, int32_t* final_idx, float* out_img, int64_t* stats) {
+                      float* final_Ts, int32_t* final_idx, float* out_img, int64_t* stats,
+                      const float* depths, float* out_depth) {
     const int32_t tbx = (img_w + BLOCK_WIDTH - 1) / BLOCK_WIDTH;
     const int32_t tby = (img_h + BLOCK_WIDTH - 1) / BLOCK_WIDTH;
     const int32_t num_tiles = tbx * tby;
@@ -627,7 +630,7 @@ void oracle_blend_fwd(const float* colors, int64_t rows_colors, const float* opa
                 float px = (float)j + 0.5f, py = (float)i + 0.5f;
                 float T = 1.0f;
                 int32_t cur_idx = 0;
-                float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f;
+                float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, od = 0.0f;
                 for (int32_t k = start; k < end; ++k) {
                     int64_t g = sorted_ids[k];
                     float dx = xys[2 * g] - px, dy = xys[2 * g + 1] - py;
@@ -650,6 +653,7 @@ void oracle_blend_fwd(const float* colors, int64_t rows_colors, const float* opa
                     o0 = o0 + c[0] * vis;
                     o1 = o1 + c[1] * vis;
                     o2 = o2 + c[2] * vis;
+                    if (out_depth) od = od + depths[g] * vis;
                     T = next_T;
                     cur_idx = k;
                 }
@@ -660,6 +664,7 @@ void oracle_blend_fwd(const float* colors, int64_t rows_colors, const float* opa
                 out_img[3 * pix] = o0 + T * bg[0];
                 out_img[3 * pix + 1] = o1 + T * bg[1];
                 out_img[3 * pix + 2] = o2 + T * bg[2];
+                if (out_depth) out_depth[pix] = od;
             }
         }
     }
@@ -675,7 +680,7 @@ int64_t oracle_rasterize_fwd(const float* colors, int64_t rows_colors, const flo
                              const float* depths, const int32_t* radii, const float* conics,
                              const int32_t* cum, int32_t n, int32_t B, int32_t img_h,
                              int32_t img_w, float* final_Ts, int32_t* final_idx, float* out_img,
-                             int64_t* stats) {
+                             int64_t* stats, float* out_depth) {
     int32_t L[6];
     if (!oracle_key_layout(B, img_h, img_w, L)) return -2;
     const int64_t total = (int64_t)B * n;
@@ -687,7 +692,8 @@ int64_t oracle_rasterize_fwd(const float* colors, int64_t rows_colors, const flo
                                     B, img_h, img_w, keys, ids, M, bins);
     if (m >= 0)
         oracle_blend_fwd(colors, rows_colors, opacities, rows_opac, background, rows_bg, xys,
-                         conics, ids, bins, B, img_h, img_w, final_Ts, final_idx, out_img, stats);
+                         conics, ids, bins, B, img_h, img_w, final_Ts, final_idx, out_img, stats,
+                         depths, out_depth);
     free(keys);
     free(ids);
     free(bins);
@@ -698,7 +704,10 @@ int64_t oracle_rasterize_fwd(const float* colors, int64_t rows_colors, const flo
  * _rasterize_bwd_warp + _rasterize_bwd_kernel, splax/_rasterize/_kernels.py:386-500,530-665, with
  * _blend_color_vjp (:1212-1254). Per pixel the walk visits sorted indices bin_final down to
  * range_start, exactly the pairs the staged and aggregated reference kernels visit. Gradients are
- * accumulated in double here (the reference's float atomics have no fixed order). */
+ * accumulated in double here (the reference's float atomics have no fixed order). With v_depths,
+ * the depth-channel backward _rasterize_bwd_depth_warp / _kernel (:797-1080) with
+ * _blend_depth_vjp (:1257-1302): the depth term joins v_alpha after the colour terms, its own
+ * accumulator dbuffer, and v_depth = v_out_depth * fac per pair. */
 
 int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const float* opacities,
                              int64_t rows_opac, const float* map_opac, int64_t rows_map_opac,
@@ -707,7 +716,10 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
                              const int32_t* cum, const float* final_Ts, const int32_t* final_idx,
                              const float* v_out_img, int64_t vout_rows, int32_t n, int32_t B_out,
                              int32_t B_geom, int32_t img_h, int32_t img_w, float* v_colors,
-                             float* v_opacity, float* v_xy, float* v_conic, int64_t* stats) {
+                             float* v_opacity, float* v_xy, float* v_conic, int64_t* stats,
+                             const float* v_out_depth, int64_t vdepth_rows, float* v_depths) {
+    const int with_depth = v_depths != NULL;
+    const int NG = with_depth ? 10 : 9;
     int32_t L[6];
     if (!oracle_key_layout(B_geom, img_h, img_w, L)) return -2;
     const int32_t tbx = L[0], num_tiles = L[2];
@@ -719,7 +731,7 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
     int64_t m = oracle_sort_and_bin(xys, depths, radii, conics, map_opac, rows_map_opac, cum, n,
                                     B_geom, img_h, img_w, keys, ids, M, bins);
     const int64_t nout = (int64_t)B_out * n;
-    double* acc = (double*)calloc((size_t)(nout > 0 ? nout : 1) * 9, sizeof(double));
+    double* acc = (double*)calloc((size_t)(nout > 0 ? nout : 1) * NG, sizeof(double));
     const int sel_geom = B_geom > 1, sel_bg = rows_bg > 1;
     int64_t qc = 0, qr = 0;
     if (m > 0) {
@@ -742,8 +754,12 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
                     float T = t_final;
                     const float* vo = v_out_img + 3 * ((((int64_t)image * img_h + i) % vout_rows) *
                                                            img_w + j);
+                    const float vd =
+                        with_depth ? v_out_depth[(((int64_t)image * img_h + i) % vdepth_rows) *
+                                                     img_w + j]
+                                   : 0.0f;
                     float px = (float)j + 0.5f, py = (float)i + 0.5f;
-                    float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
+                    float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, db = 0.0f;
                     for (int32_t k = bin_final; k >= start; --k) {
                         int64_t g = ids[k];
                         float dx = xys[2 * g] - px, dy = xys[2 * g + 1] - py;
@@ -770,15 +786,25 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
                         float v_alpha = (col[0] * T - b0 * ra) * vo[0];
                         v_alpha += (col[1] * T - b1 * ra) * vo[1];
                         v_alpha += (col[2] * T - b2 * ra) * vo[2];
+                        float dep = 0.0f;
+                        if (with_depth) {
+                            dep = depths[g];
+                            v_alpha += (dep * T - db * ra) * vd;
+                        }
                         v_alpha += -t_final * ra * bg[0] * vo[0];
                         v_alpha += -t_final * ra * bg[1] * vo[1];
                         v_alpha += -t_final * ra * bg[2] * vo[2];
                         b0 = b0 + col[0] * fac;
                         b1 = b1 + col[1] * fac;
                         b2 = b2 + col[2] * fac;
-                        double* o = acc + 9 * (og_base + g);
+                        if (with_depth) db = db + dep * fac;
+                        double* o = acc + NG * (og_base + g);
                         float gr[9] = {vo[0] * fac, vo[1] * fac, vo[2] * fac, 0, 0, 0, 0, 0, 0};
                         int ng = 3;
+                        if (with_depth) {
+#pragma omp atomic
+                            o[9] += (double)(vd * fac);
+                        }
                         if (op * vis <= ALPHA_MAX) {
                             float v_sigma = -op * vis * v_alpha;
                             gr[3] = 0.5f * v_sigma * dx * dx;
@@ -799,7 +825,8 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
         }
     }
     for (int64_t g = 0; g < nout; ++g) {
-        const double* o = acc + 9 * g;
+        const double* o = acc + NG * g;
+        if (with_depth) v_depths[g] = (float)o[9];
         v_colors[3 * g] = (float)o[0];
         v_colors[3 * g + 1] = (float)o[1];
         v_colors[3 * g + 2] = (float)o[2];

@@ -53,12 +53,14 @@ int64_t oracle_sort_and_bin(const float* xys, const float* depths, const int32_t
                             int32_t img_w, int32_t* sorted_keys, int32_t* sorted_ids,
                             int64_t cap, int32_t* tile_bins);
 
-/* Forward blend over given sorted ids and tile bins. stats (may be NULL): [Pc, Pr]. */
+/* Forward blend over given sorted ids and tile bins. stats (may be NULL): [Pc, Pr]. With a
+ * non-NULL out_depth [B*H*W], also the expected depth from depths [B*n] (depth channel). */
 void oracle_blend_fwd(const float* colors, int64_t rows_colors, const float* opacities,
                       int64_t rows_opac, const float* background, int64_t rows_bg,
                       const float* xys, const float* conics, const int32_t* sorted_ids,
                       const int32_t* tile_bins, int32_t B, int32_t img_h, int32_t img_w,
-                      float* final_Ts, int32_t* final_idx, float* out_img, int64_t* stats);
+                      float* final_Ts, int32_t* final_idx, float* out_img, int64_t* stats,
+                      const float* depths, float* out_depth);
 
 /* rasterize forward = sort_and_bin + blend. Returns M or a negative code. */
 int64_t oracle_rasterize_fwd(const float* colors, int64_t rows_colors, const float* opacities,
@@ -67,9 +69,11 @@ int64_t oracle_rasterize_fwd(const float* colors, int64_t rows_colors, const flo
                              const float* depths, const int32_t* radii, const float* conics,
                              const int32_t* cum, int32_t n, int32_t B, int32_t img_h,
                              int32_t img_w, float* final_Ts, int32_t* final_idx,
-                             float* out_img, int64_t* stats);
+                             float* out_img, int64_t* stats, float* out_depth);
 
-/* rasterize backward (recomputes the sort). stats (may be NULL): [Qc, Qr]. */
+/* rasterize backward (recomputes the sort). stats (may be NULL): [Qc, Qr]. With a non-NULL
+ * v_depths [B_out*n], the depth-channel backward with cotangent v_out_depth (vdepth_rows rows of
+ * width W). */
 int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const float* opacities,
                              int64_t rows_opac, const float* map_opac, int64_t rows_map_opac,
                              const float* background, int64_t rows_bg, const float* xys,
@@ -77,7 +81,8 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
                              const int32_t* cum, const float* final_Ts, const int32_t* final_idx,
                              const float* v_out, int64_t vout_rows, int32_t n, int32_t B_out,
                              int32_t B_geom, int32_t img_h, int32_t img_w, float* v_colors,
-                             float* v_opacity, float* v_xy, float* v_conic, int64_t* stats);
+                             float* v_opacity, float* v_xy, float* v_conic, int64_t* stats,
+                             const float* v_out_depth, int64_t vdepth_rows, float* v_depths);
 
 int oracle_project_bwd(const float* means3d, int64_t rows_means, const float* scales,
                        int64_t rows_scales, const float* quats_xyzw, int64_t rows_quats,

@@ -93,8 +93,9 @@ def project_bwd(means, scales, quats_xyzw, viewmat, radii, conics, v_xy, v_depth
 
 
 def rasterize_fwd(colors, opac, map_opac, background, xys, depths, radii, conics, cum, *, n, B,
-                  img_shape):
-    """_rasterize_warp (splax/_rasterize/_kernels.py:37-87): sort_and_bin + forward blend."""
+                  img_shape, render_depth=False):
+    """_rasterize_warp (splax/_rasterize/_kernels.py:37-87): sort_and_bin + forward blend; with
+    render_depth, _rasterize_depth_warp (:208-262), whose expected depth (B*H, W) comes last."""
     colors, opac, map_opac, background, xys, depths, conics = map(
         _f32, (colors, opac, map_opac, background, xys, depths, conics))
     radii, cum = _i32(radii), _i32(cum)
@@ -103,25 +104,30 @@ def rasterize_fwd(colors, opac, map_opac, background, xys, depths, radii, conics
     Ts = torch.empty((B * H, W), device=dev, dtype=torch.float32)
     fidx = torch.empty((B * H, W), device=dev, dtype=torch.int32)
     img = torch.empty((B * H, W, 3), device=dev, dtype=torch.float32)
-    m = torch.zeros(1, dtype=torch.int64)
+    depth = torch.empty((B * H, W), device=dev, dtype=torch.float32) if render_depth else None
+    m = ctypes.c_int64(0)
     p = _lib.ptr
+    args = (_lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
+            p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys), p(depths),
+            p(radii), p(conics), p(cum), n, B, H, W, p(Ts), p(fidx), p(img))
     with torch.cuda.device(dev):
-        st = _lib.lib().splat_rasterize_fwd(
-            _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
-            p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys),
-            p(depths), p(radii), p(conics), p(cum), n, B, H, W, p(Ts), p(fidx), p(img),
-            m.data_ptr())
+        if render_depth:
+            st = _lib.lib().splat_rasterize_depth_fwd(*args, p(depth), ctypes.byref(m))
+        else:
+            st = _lib.lib().splat_rasterize_fwd(*args, ctypes.byref(m))
     _lib.check(st, "rasterize")
-    return img, Ts, fidx, int(m.item())
+    if render_depth:
+        return img, Ts, fidx, int(m.value), depth
+    return img, Ts, fidx, int(m.value)
 
 
 _KEEP_CAPACITY: dict = {}  # per device: capacity estimate for the kept sorted lists
 
 
 def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, conics, cum, *, n,
-                       B, img_shape):
+                       B, img_shape, render_depth=False):
     """Forward that also returns the sorted gaussian ids, their emission positions and the tile
-    bins (kept for the backward).
+    bins (kept for the backward); returns (img, Ts, fidx, ids, pos, bins, M, depth or None).
 
     The buffers are sized from a per-device estimate (1.25x the largest count seen), so the host
     does not wait for the intersection count before launching: the library reads it itself while
@@ -137,6 +143,7 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
     Ts = torch.empty((B * H, W), device=dev, dtype=torch.float32)
     fidx = torch.empty((B * H, W), device=dev, dtype=torch.int32)
     img = torch.empty((B * H, W, 3), device=dev, dtype=torch.float32)
+    depth = torch.empty((B * H, W), device=dev, dtype=torch.float32) if render_depth else None
     bins = torch.empty((B * tiles, 2), device=dev, dtype=torch.int32)
     key = str(dev)
     cap = _KEEP_CAPACITY.get(key, 0)
@@ -150,7 +157,7 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
                 _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
                 p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys),
                 p(depths), p(radii), p(conics), p(cum), n, B, H, W, cap, p(Ts), p(fidx), p(img),
-                p(ids), p(pos), p(bins), ctypes.byref(m))
+                p(depth), p(ids), p(pos), p(bins), ctypes.byref(m))
         if st == _lib.ERR_TOO_MANY and m.value > cap:
             cap = int(m.value * 1.25) + 1
             _KEEP_CAPACITY[key] = cap
@@ -160,58 +167,69 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
     M = int(m.value)
     if M > _KEEP_CAPACITY.get(key, 0):
         _KEEP_CAPACITY[key] = int(M * 1.25) + 1
-    return img, Ts, fidx, ids, pos, bins, M
+    return img, Ts, fidx, ids, pos, bins, M, depth
 
 
-def rasterize_bwd_sorted(colors, opac, background, xys, conics, cum, ids, pos, bins, M, final_Ts,
-                         final_idx, v_out, *, n, B_out, B_geom, img_shape):
-    """Backward over the sorted lists of rasterize_fwd_keep (no re-sort)."""
-    colors, opac, background, xys, conics, final_Ts, v_out = map(
-        _f32, (colors, opac, background, xys, conics, final_Ts, v_out))
+def _bwd_outputs(nout, dev, with_depth):
+    f = lambda *shape: torch.empty(shape, device=dev, dtype=torch.float32)  # noqa: E731
+    return f(nout, 3), f(nout), f(nout, 2), f(nout, 3), (f(nout) if with_depth else None)
+
+
+def rasterize_bwd_sorted(colors, opac, background, xys, depths, conics, cum, ids, pos, bins, M,
+                         final_Ts, final_idx, v_out, *, n, B_out, B_geom, img_shape,
+                         v_out_depth=None):
+    """Backward over the sorted lists of rasterize_fwd_keep (no re-sort); with v_out_depth also
+    the depth channel's v_depths (last)."""
+    colors, opac, background, xys, depths, conics, final_Ts, v_out = map(
+        _f32, (colors, opac, background, xys, depths, conics, final_Ts, v_out))
     cum, ids, pos, bins, final_idx = _i32(cum), _i32(ids), _i32(pos), _i32(bins), _i32(final_idx)
+    vd = None if v_out_depth is None else _f32(v_out_depth)
     dev = _lib.require_gpu(colors, opac, xys, conics, cum, ids, pos, bins, final_Ts, final_idx,
                            v_out)
     H, W = img_shape
-    nout = B_out * n
-    v_colors = torch.empty((nout, 3), device=dev, dtype=torch.float32)
-    v_opac = torch.empty((nout,), device=dev, dtype=torch.float32)
-    v_xy = torch.empty((nout, 2), device=dev, dtype=torch.float32)
-    v_conic = torch.empty((nout, 3), device=dev, dtype=torch.float32)
+    v_colors, v_opac, v_xy, v_conic, v_depths = _bwd_outputs(B_out * n, dev, vd is not None)
     p = _lib.ptr
     with torch.cuda.device(dev):
         st = _lib.lib().splat_rasterize_bwd_sorted(
             _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
-            p(background), rows(background, 3), p(xys), p(conics), p(cum), p(ids), p(pos),
-            p(bins), M,
-            p(final_Ts), p(final_idx), p(v_out), v_out.numel() // (3 * W), n, B_out, B_geom, H, W,
-            p(v_colors), p(v_opac), p(v_xy), p(v_conic))
+            p(background), rows(background, 3), p(xys), p(depths), p(conics), p(cum), p(ids),
+            p(pos), p(bins), M, p(final_Ts), p(final_idx), p(v_out), v_out.numel() // (3 * W),
+            p(vd), 0 if vd is None else vd.numel() // W, n, B_out, B_geom, H, W, p(v_colors),
+            p(v_opac), p(v_xy), p(v_conic), p(v_depths))
     _lib.check(st, "rasterize_bwd")
-    return v_colors, v_opac, v_xy, v_conic
+    if vd is None:
+        return v_colors, v_opac, v_xy, v_conic
+    return v_colors, v_opac, v_xy, v_conic, v_depths
 
 
 def rasterize_bwd(colors, opac, map_opac, background, xys, depths, radii, conics, cum, final_Ts,
-                  final_idx, v_out, *, n, B_out, B_geom, img_shape):
-    """_rasterize_bwd_warp (splax/_rasterize/_kernels.py:386-500)."""
+                  final_idx, v_out, *, n, B_out, B_geom, img_shape, v_out_depth=None):
+    """_rasterize_bwd_warp (splax/_rasterize/_kernels.py:386-500); with v_out_depth,
+    _rasterize_bwd_depth_warp (:797-914), whose v_depths comes last."""
     colors, opac, map_opac, background, xys, depths, conics, final_Ts, v_out = map(
         _f32, (colors, opac, map_opac, background, xys, depths, conics, final_Ts, v_out))
     radii, cum, final_idx = _i32(radii), _i32(cum), _i32(final_idx)
+    vd = None if v_out_depth is None else _f32(v_out_depth)
     dev = _lib.require_gpu(colors, opac, xys, conics, final_Ts, final_idx, v_out)
     H, W = img_shape
-    nout = B_out * n
-    v_colors = torch.empty((nout, 3), device=dev, dtype=torch.float32)
-    v_opac = torch.empty((nout,), device=dev, dtype=torch.float32)
-    v_xy = torch.empty((nout, 2), device=dev, dtype=torch.float32)
-    v_conic = torch.empty((nout, 3), device=dev, dtype=torch.float32)
+    v_colors, v_opac, v_xy, v_conic, v_depths = _bwd_outputs(B_out * n, dev, vd is not None)
     p = _lib.ptr
+    args = (_lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
+            p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys), p(depths),
+            p(radii), p(conics), p(cum), p(final_Ts), p(final_idx), p(v_out),
+            v_out.numel() // (3 * W))
     with torch.cuda.device(dev):
-        st = _lib.lib().splat_rasterize_bwd(
-            _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
-            p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys),
-            p(depths), p(radii), p(conics), p(cum), p(final_Ts), p(final_idx), p(v_out),
-            v_out.numel() // (3 * W), n, B_out, B_geom, H, W, p(v_colors), p(v_opac), p(v_xy),
-            p(v_conic))
+        if vd is None:
+            st = _lib.lib().splat_rasterize_bwd(*args, n, B_out, B_geom, H, W, p(v_colors),
+                                                p(v_opac), p(v_xy), p(v_conic))
+        else:
+            st = _lib.lib().splat_rasterize_depth_bwd(*args, p(vd), vd.numel() // W, n, B_out,
+                                                      B_geom, H, W, p(v_colors), p(v_opac),
+                                                      p(v_xy), p(v_conic), p(v_depths))
     _lib.check(st, "rasterize_bwd")
-    return v_colors, v_opac, v_xy, v_conic
+    if vd is None:
+        return v_colors, v_opac, v_xy, v_conic
+    return v_colors, v_opac, v_xy, v_conic, v_depths
 
 
 def sort_and_bin(xys, depths, radii, conics, map_opac, cum, *, n, B, img_shape, capacity=None):

@@ -1,9 +1,10 @@
 """Differentiable rasterization stage (torch).
 
-Mirrors splax/_rasterize/_rasterize.py:24-234: ``rasterize`` blends projected gaussians into an
-image; ``_RasterizeFn`` is the counterpart of the ``jax.custom_vjp`` ``_rasterize`` whose forward
-keeps final_Ts / final_idx as residuals and whose backward recomputes the (deterministic) sort
-inside the library. Differentiable w.r.t. colors, opacities, xys and conics.
+Mirrors splax/_rasterize/_rasterize.py:24-360: ``rasterize`` blends projected gaussians into an
+image and ``rasterize_depth`` adds the expected-depth map; ``_RasterizeFn`` is the counterpart of
+the ``jax.custom_vjp`` rules ``_rasterize`` / ``_rasterize_depth``, whose forward keeps final_Ts /
+final_idx (here also the sorted lists) as residuals. Differentiable w.r.t. colors, opacities, xys
+and conics, and on the depth path also depths.
 """
 
 from __future__ import annotations
@@ -45,53 +46,58 @@ class _RasterizeFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, colors, opac, map_opac, background, xys, depths, radii, conics, cum,
                 statics):
-        n, B, img_shape = statics
+        n, B, img_shape, render_depth = statics
         # The sorted lists stay resident for the backward (the reference re-sorts there,
         # splax/_rasterize/_kernels.py:422); the sort is deterministic, so both are identical.
-        img, Ts, fidx, ids, pos, bins, M = _ops.rasterize_fwd_keep(
+        img, Ts, fidx, ids, pos, bins, M, depth = _ops.rasterize_fwd_keep(
             colors.reshape(-1, 3), opac.reshape(-1), map_opac.reshape(-1),
             background.reshape(-1, 3), xys.reshape(-1, 2), depths.reshape(-1), radii.reshape(-1),
-            conics.reshape(-1, 3), cum.reshape(-1), n=n, B=B, img_shape=img_shape)
-        ctx.save_for_backward(colors, opac, background, xys, conics, cum, Ts, fidx, ids, pos,
-                              bins)
+            conics.reshape(-1, 3), cum.reshape(-1), n=n, B=B, img_shape=img_shape,
+            render_depth=render_depth)
+        ctx.save_for_backward(colors, opac, background, xys, depths, conics, cum, Ts, fidx, ids,
+                              pos, bins)
         ctx.statics = statics
         ctx.num_intersects = M
-        ctx.mark_non_differentiable(Ts, fidx)
         ctx.set_materialize_grads(False)  # no zero tensors for the unused Ts / fidx grads
-        return img, Ts, fidx
+        if depth is None:
+            depth = Ts.new_zeros(())  # placeholder output of the colour-only path
+            ctx.mark_non_differentiable(Ts, fidx, depth)  # one call: it replaces the set
+        else:
+            ctx.mark_non_differentiable(Ts, fidx)
+        return img, depth, Ts, fidx
 
     @staticmethod
-    def backward(ctx, v_img, _v_Ts, _v_idx):
-        colors, opac, background, xys, conics, cum, Ts, fidx, ids, pos, bins = ctx.saved_tensors
-        n, B, img_shape = ctx.statics
+    def backward(ctx, v_img, v_depth, _v_Ts, _v_idx):
+        colors, opac, background, xys, depths, conics, cum, Ts, fidx, ids, pos, bins = \
+            ctx.saved_tensors
+        n, B, img_shape, render_depth = ctx.statics
+        H, W = img_shape
         if v_img is None:
-            v_img = torch.zeros((B * img_shape[0], img_shape[1], 3), device=xys.device)
-        v_colors, v_opac, v_xy, v_conic = _ops.rasterize_bwd_sorted(
+            v_img = torch.zeros((B * H, W, 3), device=xys.device)
+        if render_depth and v_depth is None:
+            v_depth = torch.zeros((B * H, W), device=xys.device)
+        grads = _ops.rasterize_bwd_sorted(
             colors.reshape(-1, 3), opac.reshape(-1), background.reshape(-1, 3),
-            xys.reshape(-1, 2), conics.reshape(-1, 3), cum.reshape(-1), ids, pos, bins,
-            ctx.num_intersects, Ts, fidx, v_img.reshape(-1, 3), n=n, B_out=B, B_geom=B,
-            img_shape=img_shape)
+            xys.reshape(-1, 2), depths.reshape(-1), conics.reshape(-1, 3), cum.reshape(-1), ids,
+            pos, bins, ctx.num_intersects, Ts, fidx, v_img.reshape(-1, 3), n=n, B_out=B,
+            B_geom=B, img_shape=img_shape,
+            v_out_depth=v_depth.reshape(-1, W) if render_depth else None)
+        v_colors, v_opac, v_xy, v_conic = grads[:4]
 
         def fold(g: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
             if like.numel() == g.numel():
                 return g.reshape(like.shape)
             return g.reshape(B, -1).sum(0).reshape(like.shape)  # shared over the batch
 
-        return (fold(v_colors, colors), fold(v_opac, opac), None, None, fold(v_xy, xys), None,
-                None, fold(v_conic, conics), None, None)
+        # the depths cotangent exists only on the depth path
+        # (splax/_rasterize/_rasterize.py:231 vs :357)
+        v_depths = fold(grads[4], depths) if render_depth else None
+        return (fold(v_colors, colors), fold(v_opac, opac), None, None, fold(v_xy, xys),
+                v_depths, None, fold(v_conic, conics), None, None)
 
 
-def rasterize(colors: torch.Tensor, opacities: torch.Tensor, background: torch.Tensor,
-              xys: torch.Tensor, depths: torch.Tensor, radii: torch.Tensor, conics: torch.Tensor,
-              cum_tiles_hit: torch.Tensor, *, img_shape: tuple[int, int],
-              map_opacities: torch.Tensor | None = None) -> torch.Tensor:
-    """Blend projected gaussians into an (H, W, 3) image (splax/_rasterize/_rasterize.py:24-60).
-
-    Geometry (xys, depths, radii, conics, cum_tiles_hit) with a leading batch dimension B renders
-    B images in one launch and returns (B, H, W, 3); colors / opacities may be shared (N, ...) or
-    per image (B, N, ...), background (3,) or (B, 3). map_opacities (default: opacities) drive the
-    tile intersection only and carry no gradient.
-    """
+def _rasterize_checked(colors, opacities, background, xys, depths, radii, conics, cum_tiles_hit,
+                       img_shape, map_opacities, render_depth):
     n = int(colors.shape[-2])
     H, W = img_shape
     if map_opacities is None:
@@ -109,12 +115,42 @@ def rasterize(colors: torch.Tensor, opacities: torch.Tensor, background: torch.T
             raise ValueError(f"{name} has {r} rows, expected {n} or {Bg * n}")
     if background.numel() not in (3, 3 * Bg):
         raise ValueError(f"background must have 3 or {3 * Bg} entries")
+    if depths.numel() != Bg * n:
+        raise ValueError(f"depths has {depths.numel()} entries, expected {Bg * n}")
     check_key_fits(Bg, int(H), int(W))
-    img, _, _ = _RasterizeFn.apply(colors, opacities, map_opacities, background, xys, depths,
-                                   radii, conics, cum_tiles_hit, (n, Bg, (int(H), int(W))))
-    return img.reshape(Bg, H, W, 3) if batched else img.reshape(H, W, 3)
+    img, depth, _, _ = _RasterizeFn.apply(colors, opacities, map_opacities, background, xys,
+                                          depths, radii, conics, cum_tiles_hit,
+                                          (n, Bg, (int(H), int(W)), render_depth))
+    img = img.reshape(Bg, H, W, 3) if batched else img.reshape(H, W, 3)
+    if not render_depth:
+        return img, None
+    return img, (depth.reshape(Bg, H, W) if batched else depth.reshape(H, W))
 
 
-def rasterize_depth(*args, **kwargs):
-    """Expected-depth twin of rasterize (splax/_rasterize/_rasterize.py:63-99): not built yet."""
-    raise NotImplementedError("rasterize_depth (the expected-depth channel) is not built yet")
+def rasterize(colors: torch.Tensor, opacities: torch.Tensor, background: torch.Tensor,
+              xys: torch.Tensor, depths: torch.Tensor, radii: torch.Tensor, conics: torch.Tensor,
+              cum_tiles_hit: torch.Tensor, *, img_shape: tuple[int, int],
+              map_opacities: torch.Tensor | None = None) -> torch.Tensor:
+    """Blend projected gaussians into an (H, W, 3) image (splax/_rasterize/_rasterize.py:24-60).
+
+    Geometry (xys, depths, radii, conics, cum_tiles_hit) with a leading batch dimension B renders
+    B images in one launch and returns (B, H, W, 3); colors / opacities may be shared (N, ...) or
+    per image (B, N, ...), background (3,) or (B, 3). map_opacities (default: opacities) drive the
+    tile intersection only and carry no gradient.
+    """
+    return _rasterize_checked(colors, opacities, background, xys, depths, radii, conics,
+                              cum_tiles_hit, img_shape, map_opacities, False)[0]
+
+
+def rasterize_depth(colors: torch.Tensor, opacities: torch.Tensor, background: torch.Tensor,
+                    xys: torch.Tensor, depths: torch.Tensor, radii: torch.Tensor,
+                    conics: torch.Tensor, cum_tiles_hit: torch.Tensor, *,
+                    img_shape: tuple[int, int], map_opacities: torch.Tensor | None = None):
+    """rasterize plus the alpha-blended expected depth map (splax/_rasterize/_rasterize.py:63-99).
+
+    Returns (image (H, W, 3), depth (H, W)), batched as rasterize. The depth uses the colour
+    blend's weights and no background term; the image is bit-for-bit rasterize's. Gradients flow
+    to depths as well (splax/_rasterize/_rasterize.py:316-357).
+    """
+    return _rasterize_checked(colors, opacities, background, xys, depths, radii, conics,
+                              cum_tiles_hit, img_shape, map_opacities, True)

@@ -33,6 +33,7 @@ struct BlendCommon {
     const float* opac; int64_t rows_opac;
     const float* background; int64_t rows_bg;
     const float* xys; const float* conics;
+    const float* depths;  // per geometry item; non-null only when the depth channel is rendered
     const int32_t* ids; const int32_t* bins;
     int32_t img_h, img_w, tiles_x, num_tiles;
     int64_t total;  // geometry rows (B_geom * n): ids outside [0, total) are ignored
@@ -82,7 +83,7 @@ __device__ __forceinline__ void stage_bounds(float x, float y, float a, float b,
 }
 
 // LDS record of one batch: r0 = (x, y, a, b), r1 = (c, o, sigma_max, quadrant mask bits),
-// r2 = (red, green, blue, gaussian id bits), plus per-quadrant compacted record lists.
+// r2 = (red, green, blue, depth or 0), plus per-quadrant compacted record lists.
 struct BatchLds {
     float4 r0[kTile];
     float4 r1[kTile];
@@ -110,7 +111,7 @@ __device__ __forceinline__ int stage_batch(const BlendCommon& C, BatchLds& L, in
         r0 = make_float4(xy.x, xy.y, a, b);
         r1 = make_float4(c, o, smax, __uint_as_float(qm));
         r2 = make_float4(C.colors[3 * cg], C.colors[3 * cg + 1], C.colors[3 * cg + 2],
-                         __int_as_float((int32_t)g));
+                         C.depths ? C.depths[g] : 0.0f);
     }
     L.r0[tid] = r0;
     L.r1[tid] = r1;
@@ -161,8 +162,12 @@ __device__ __forceinline__ float exp_core(float x) {
 struct BlendFwdParams {
     BlendCommon c;
     float* final_Ts; int32_t* final_idx; float* out_img;
+    float* out_depth;  // kDepth: expected depth per pixel
 };
 
+// kDepth adds the expected-depth channel of _rasterize_depth_kernel
+// (splax/_rasterize/_kernels.py:277-383): depth times the same blend weight, no background term.
+template <bool kDepth>
 __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
     __shared__ BatchLds L;
     const BlendCommon& C = P.c;
@@ -181,7 +186,7 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
     const int32_t num_batches = (range_end - range_start + kTile - 1) / kTile;
     float T = 1.0f;
     int32_t cur_idx = 0;
-    float o0 = 0.f, o1 = 0.f, o2 = 0.f;
+    float o0 = 0.f, o1 = 0.f, o2 = 0.f, od = 0.f;
 
     for (int32_t bt = 0; bt < num_batches; ++bt) {
         // every pixel done -> stop; also the barrier before the LDS records are overwritten
@@ -213,6 +218,7 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
             o0 = o0 + r2.x * vis;
             o1 = o1 + r2.y * vis;
             o2 = o2 + r2.z * vis;
+            if constexpr (kDepth) od = od + r2.w * vis;
             T = next_T;
             cur_idx = batch_start + t;
         }
@@ -226,6 +232,7 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
         P.out_img[3 * pix] = o0 + T * bg[0];
         P.out_img[3 * pix + 1] = o1 + T * bg[1];
         P.out_img[3 * pix + 2] = o2 + T * bg[2];
+        if constexpr (kDepth) P.out_depth[pix] = od;
     }
 }
 
@@ -235,6 +242,7 @@ static void fill_common(BlendCommon& c, const RasterInputs& in, const KeyLayout&
     c.opac = in.opac; c.rows_opac = in.rows_opac;
     c.background = in.background; c.rows_bg = in.rows_bg;
     c.xys = in.xys; c.conics = in.conics;
+    c.depths = nullptr;
     c.ids = sorted_ids; c.bins = tile_bins;
     c.img_h = in.img_h; c.img_w = in.img_w;
     c.tiles_x = lay.tiles_x; c.num_tiles = lay.num_tiles;
@@ -243,13 +251,20 @@ static void fill_common(BlendCommon& c, const RasterInputs& in, const KeyLayout&
 
 int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,
-                     float* out_img, hipStream_t stream) {
+                     float* out_img, float* out_depth, hipStream_t stream) {
     const int64_t blocks = (int64_t)in.B_geom * lay.num_tiles;
     if (blocks <= 0) return 0;
     BlendFwdParams P;
     fill_common(P.c, in, lay, sorted_ids, tile_bins);
+    P.c.depths = out_depth ? in.depths : nullptr;
     P.final_Ts = final_Ts; P.final_idx = final_idx; P.out_img = out_img;
-    hipLaunchKernelGGL(blend_fwd_kernel, dim3((unsigned)blocks), dim3(kTile), 0, stream, P);
+    P.out_depth = out_depth;
+    if (out_depth)
+        hipLaunchKernelGGL(blend_fwd_kernel<true>, dim3((unsigned)blocks), dim3(kTile), 0, stream,
+                           P);
+    else
+        hipLaunchKernelGGL(blend_fwd_kernel<false>, dim3((unsigned)blocks), dim3(kTile), 0, stream,
+                           P);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
 }
 
@@ -263,15 +278,18 @@ struct BlendBwdParams {
     const float* v_out; int64_t vout_rows;
     int32_t n; int32_t sel_geom;
     const int32_t* pos; int64_t M;
-    float* rgrad;  // [images][M][9], images = 1 when geometry is batched, else B_out
+    const float* v_out_depth; int64_t vdepth_rows;  // kDepth
+    float* rgrad;  // [images][M][NG], images = 1 when geometry is batched, else B_out
 };
 
-// Nine partial sums of one intersection: v_colour (3), v_conic (3), the two sums
-// sum v_sigma * dx, sum v_sigma * dy (v_xy before the conic is applied), v_opacity.
+// Partial sums of one intersection: v_colour (3), v_conic (3), the two sums sum v_sigma * dx,
+// sum v_sigma * dy (v_xy before the conic is applied), v_opacity, and with the depth channel
+// v_depth (NG = 10).
+template <int NG>
 __device__ __forceinline__ void store_rgrad(float* rgrad, int64_t slot, const float* s) {
-    float* r = rgrad + slot * 9;
+    float* r = rgrad + slot * NG;
 #pragma unroll
-    for (int k = 0; k < 9; ++k) r[k] = s[k];
+    for (int k = 0; k < NG; ++k) r[k] = s[k];
 }
 
 __device__ __forceinline__ float swap32_add(float a, float b) {
@@ -293,13 +311,18 @@ __device__ __forceinline__ float row_halves_to_lanes_7_15(float v) {
     return v;
 }
 
-// Record accumulator slot k of batch record t ([t][9] layout: the four lanes that add at once
-// hit four different banks).
-#define ACC(t, k) acc[(t) * 9 + (k)]
+// Record accumulator slot k of batch record t ([t][NG] layout: the lanes that add at once hit
+// different banks).
+#define ACC(t, k) acc[(t) * NG + (k)]
 
+// kDepth adds the depth channel of _rasterize_bwd_depth_kernel / _blend_depth_vjp
+// (splax/_rasterize/_kernels.py:935-1080,1257-1302): the record's depth joins the colour dot
+// product (v_alpha and the accumulator), and v_depth = v_out_depth * fac is a tenth sum.
+template <bool kDepth>
 __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
+    constexpr int NG = kDepth ? 10 : 9;
     __shared__ BatchLds L;
-    __shared__ float acc[kTile * 9];
+    __shared__ float acc[kTile * NG];
     __shared__ int32_t s_max;
 
     const BlendCommon& C = P.c;
@@ -317,7 +340,7 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     const float px = (float)j + 0.5f, py = (float)i + 0.5f;
     const bool inside = i < C.img_h && j < C.img_w;
     int32_t bin_final = range_start - 1;
-    float T = 1.0f, v0 = 0.f, v1 = 0.f, v2 = 0.f, tfbg = 0.f;
+    float T = 1.0f, v0 = 0.f, v1 = 0.f, v2 = 0.f, tfbg = 0.f, vd = 0.f;
     if (inside) {
         const int64_t frow = (int64_t)geom_image * C.img_h + i;
         bin_final = P.final_idx[frow * C.img_w + j];
@@ -328,10 +351,12 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
         v0 = vo[0]; v1 = vo[1]; v2 = vo[2];
         const float* bg = C.background + 3 * (C.rows_bg > 1 ? image_id : 0);
         tfbg = t_final * ((bg[0] * v0 + bg[1] * v1) + bg[2] * v2);
+        if constexpr (kDepth)
+            vd = P.v_out_depth[(((int64_t)image_id * C.img_h + i) % P.vdepth_rows) * C.img_w + j];
     }
     float bufv = 0.f;  // sum_k buffer_k * v_k of the reference's colour accumulator
     if (tid == 0) s_max = range_start - 1;
-    for (int k = tid; k < kTile * 9; k += kTile) acc[k] = 0.0f;
+    for (int k = tid; k < kTile * NG; k += kTile) acc[k] = 0.0f;
     __syncthreads();
     atomicMax(&s_max, bin_final);
     // wave-wide largest final index: a record above it has no contributing lane in this wave
@@ -350,10 +375,12 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     const int64_t rg_off = P.sel_geom ? 0 : (int64_t)image_id * P.M;
     {
         // intersections above every final index of the tile contribute nothing
-        const float zero9[9] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float zeros[NG];
+#pragma unroll
+        for (int k = 0; k < NG; ++k) zeros[k] = 0.0f;
         for (int32_t jj = start_idx + 1 + tid; jj < range_end; jj += kTile) {
             const int32_t e = P.pos[jj];
-            if (e >= 0 && e < P.M) store_rgrad(P.rgrad, rg_off + e, zero9);
+            if (e >= 0 && e < P.M) store_rgrad<NG>(P.rgrad, rg_off + e, zeros);
         }
     }
 
@@ -387,7 +414,8 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             const float Tn = T * ra;
             T = valid ? Tn : T;
             const float fac = valid ? alpha * Tn : 0.0f;
-            const float cv = fmaf(r2.x, v0, fmaf(r2.y, v1, r2.z * v2));
+            float cv = fmaf(r2.x, v0, fmaf(r2.y, v1, r2.z * v2));
+            if constexpr (kDepth) cv = fmaf(r2.w, vd, cv);  // depth as a fourth channel
             const float v_alpha = fmaf(Tn, cv, -ra * (bufv + tfbg));
             bufv = fmaf(cv, fac, bufv);
             const float ov = r1.y * vis;
@@ -398,13 +426,15 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             const float g3 = 0.5f * hx * dx, g4 = hx * dy, g5 = 0.5f * hy * dy;
             const float g6 = hx, g7 = hy;
             const float g8 = geo ? vis * v_alpha : 0.0f;
+            const float g9 = kDepth ? vd * fac : 0.0f;
             float* a = &ACC(t, 0);
             // reduce-scatter over the wave: after the swaps, row r of qa holds g0/g2/g1/g3 and
             // of qb g4/g6/g5/g7 (rows 0..3), qc holds g8 in every row; the half-row sums land
             // in lanes 7 and 15.
             const float p01 = swap32_add(g0, g1), p23 = swap32_add(g2, g3);
             const float p45 = swap32_add(g4, g5), p67 = swap32_add(g6, g7);
-            const float p8 = swap32_add(g8, g8);
+            // depth: g8 and g9 share the first swap (rows 0-1 then carry g8, rows 2-3 g9)
+            const float p8 = kDepth ? swap32_add(g8, g9) : swap32_add(g8, g8);
             float qa = swap16_add(p01, p23), qb = swap16_add(p45, p67), qc = swap16_add(p8, p8);
             qa = row_halves_to_lanes_7_15(qa);
             qb = row_halves_to_lanes_7_15(qb);
@@ -417,17 +447,18 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
                 atomicAdd(a + ka, qa);
                 atomicAdd(a + 4 + ka, qb);
                 if (row == 0) atomicAdd(a + 8, qc);
+                if (kDepth && row == 2) atomicAdd(a + 9, qc);
             }
         }
         __syncthreads();
         {
-            float s[9];
+            float s[NG];
 #pragma unroll
-            for (int k = 0; k < 9; ++k) {
+            for (int k = 0; k < NG; ++k) {
                 s[k] = ACC(tid, k);
                 ACC(tid, k) = 0.0f;
             }
-            if (my_pos >= 0 && my_pos < P.M) store_rgrad(P.rgrad, rg_off + my_pos, s);
+            if (my_pos >= 0 && my_pos < P.M) store_rgrad<NG>(P.rgrad, rg_off + my_pos, s);
         }
         __syncthreads();
     }
@@ -443,8 +474,10 @@ struct GatherParams {
     const int32_t* cum; const float* conics; const float* rgrad;
     int64_t M; int64_t nout; int32_t n; int32_t sel_geom;
     float* v_colors; float* v_opacity; float* v_xy; float* v_conic;
+    float* v_depths;  // NG == 10
 };
 
+template <int NG>
 __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
     const int64_t og = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (og >= P.nout) return;
@@ -457,11 +490,13 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
     int64_t lo = gi > 0 ? (int64_t)P.cum[gi - 1] : 0, hi = P.cum[gi];
     lo = lo < 0 ? 0 : lo;
     hi = hi > P.M ? P.M : hi;
-    float s[9] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int64_t e = lo; e < hi; ++e) {
-        const float* r = P.rgrad + (off + e) * 9;
+    float s[NG];
 #pragma unroll
-        for (int k = 0; k < 9; ++k) s[k] += r[k];
+    for (int k = 0; k < NG; ++k) s[k] = 0.0f;
+    for (int64_t e = lo; e < hi; ++e) {
+        const float* r = P.rgrad + (off + e) * NG;
+#pragma unroll
+        for (int k = 0; k < NG; ++k) s[k] += r[k];
     }
     P.v_colors[3 * og] = s[0];
     P.v_colors[3 * og + 1] = s[1];
@@ -478,6 +513,7 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
     P.v_xy[2 * og] = vx;
     P.v_xy[2 * og + 1] = vy;
     P.v_opacity[og] = s[8];
+    if constexpr (NG == 10) P.v_depths[og] = s[9];
 }
 
 int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
@@ -485,14 +521,23 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
     const int64_t nout = (int64_t)a.B_out * in.n;
     const int32_t sel_geom = in.B_geom > 1;
     const int64_t blocks = (int64_t)a.B_out * lay.num_tiles;
+    const bool depth = a.v_depths != nullptr;
     if (blocks > 0 && sorted_ids != nullptr && a.M > 0) {
         BlendBwdParams P;
         fill_common(P.c, in, lay, sorted_ids, tile_bins);
+        P.c.depths = depth ? in.depths : nullptr;
         P.final_Ts = a.final_Ts; P.final_idx = a.final_idx;
         P.v_out = a.v_out; P.vout_rows = a.vout_rows;
         P.n = in.n; P.sel_geom = sel_geom;
-        P.pos = a.sorted_pos; P.M = a.M; P.rgrad = a.rgrad;
-        hipLaunchKernelGGL(blend_bwd_kernel, dim3((unsigned)blocks), dim3(kTile), 0, stream, P);
+        P.pos = a.sorted_pos; P.M = a.M;
+        P.v_out_depth = a.v_out_depth; P.vdepth_rows = a.vdepth_rows;
+        P.rgrad = a.rgrad;
+        if (depth)
+            hipLaunchKernelGGL(blend_bwd_kernel<true>, dim3((unsigned)blocks), dim3(kTile), 0,
+                               stream, P);
+        else
+            hipLaunchKernelGGL(blend_bwd_kernel<false>, dim3((unsigned)blocks), dim3(kTile), 0,
+                               stream, P);
         if (hipGetLastError() != hipSuccess) return kErrLaunch;
     }
     if (nout <= 0) return 0;
@@ -501,8 +546,12 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
     G.M = (sorted_ids != nullptr) ? a.M : 0;
     G.nout = nout; G.n = in.n; G.sel_geom = sel_geom;
     G.v_colors = a.v_colors; G.v_opacity = a.v_opacity; G.v_xy = a.v_xy; G.v_conic = a.v_conic;
-    hipLaunchKernelGGL(grad_gather_kernel, dim3((unsigned)((nout + 255) / 256)), dim3(256), 0,
-                       stream, G);
+    G.v_depths = a.v_depths;
+    const dim3 grid((unsigned)((nout + 255) / 256));
+    if (depth)
+        hipLaunchKernelGGL(grad_gather_kernel<10>, grid, dim3(256), 0, stream, G);
+    else
+        hipLaunchKernelGGL(grad_gather_kernel<9>, grid, dim3(256), 0, stream, G);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
 }
 

@@ -299,7 +299,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 2; }
+int splat_abi_version(void) { return 3; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();
@@ -508,6 +508,124 @@ int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* dep
     return 0;
 }
 
+static RasterInputs raster_inputs(const float* colors, int64_t rows_colors,
+                                  const float* opacities, int64_t rows_opac,
+                                  const float* map_opacities, int64_t rows_map_opac,
+                                  const float* background, int64_t rows_bg, const float* xys,
+                                  const float* depths, const int32_t* radii, const float* conics,
+                                  const int32_t* cum, int32_t n, int32_t B_geom, int32_t img_h,
+                                  int32_t img_w) {
+    RasterInputs in{};
+    in.colors = colors; in.rows_colors = rows_colors;
+    in.opac = opacities; in.rows_opac = rows_opac;
+    in.map_opac = map_opacities; in.rows_map_opac = rows_map_opac;
+    in.background = background; in.rows_bg = rows_bg;
+    in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
+    in.cum = cum; in.n = n; in.B_geom = B_geom;
+    in.img_h = img_h; in.img_w = img_w;
+    return in;
+}
+
+// Forward: sort_and_bin into the library scratch or the caller's kept lists (tgt), then the
+// blend; out_depth non-null adds the expected-depth channel.
+static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortTargets* tgt,
+                              float* final_Ts, int32_t* final_idx, float* out_img,
+                              float* out_depth, int64_t* num_intersects) {
+    int rc = check_raster(in, in.B_geom);
+    if (rc) return rc;
+    if (out_depth && !in.depths) return fail(kErrArgs, "rasterize: depth channel needs depths");
+    DeviceScratch& sc = scratch_for_current_device();
+    std::lock_guard<std::mutex> lock(sc.mu);
+    rc = sc.ensure_base();
+    if (!rc) {
+        const int32_t bpi = (in.n + 4095) / 4096;
+        rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * in.B_geom);
+    }
+    if (rc) return rc;
+    int64_t M = 0;
+    KeyLayout L;
+    rc = run_sort_and_bin(in, sc, s, &M, &L, tgt);
+    if (num_intersects) *num_intersects = M;
+    if (rc) return rc;
+    const int32_t* ids = (tgt && tgt->ids) ? tgt->ids : sc.gids[0];
+    const int32_t* bins = (tgt && tgt->bins) ? tgt->bins : sc.tile_bins;
+    StageTimer tm(s, kStageBlendFwd);
+    rc = launch_blend_fwd(in, L, M > 0 ? ids : nullptr, bins, final_Ts, final_idx, out_img,
+                          out_depth, s);
+    if (rc) return fail(rc, "blend_fwd launch failed");
+    return 0;
+}
+
+// Sorted lists kept from the forward (splat_rasterize_fwd_keep).
+struct KeptLists {
+    const int32_t* ids; const int32_t* pos; const int32_t* bins; int64_t M;
+};
+
+// Backward over kept sorted lists or, with kept == nullptr, over a fresh sort_and_bin.
+// v_depths non-null selects the depth channel.
+static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptLists* kept,
+                              const BlendBwdArgs& args) {
+    int rc = check_raster(in, args.B_out);
+    if (rc) return rc;
+    if (args.B_out <= 0 || (in.B_geom > 1 && in.B_geom != args.B_out))
+        return fail(kErrArgs, "rasterize_bwd: B_geom must be 1 or equal to B_out");
+    if (args.vout_rows <= 0 || !in.cum) return fail(kErrArgs, "rasterize_bwd: empty cotangent");
+    if (args.v_depths && (!in.depths || !args.v_out_depth || args.vdepth_rows <= 0))
+        return fail(kErrArgs, "rasterize_bwd: depth channel needs depths and v_out_depth");
+    if ((int64_t)args.B_out * in.n >= ((int64_t)1 << 31))
+        return fail(kErrArgs, "rasterize_bwd: more than 2^31 gradient rows");
+    DeviceScratch& sc = scratch_for_current_device();
+    std::lock_guard<std::mutex> lock(sc.mu);
+    rc = sc.ensure_base();
+    if (rc) return rc;
+    KeyLayout L;
+    const int32_t* ids = nullptr;
+    const int32_t* pos = nullptr;
+    const int32_t* bins = nullptr;
+    int64_t M = 0;
+    if (kept) {
+        L = key_layout(in.B_geom, in.img_h, in.img_w);
+        if (!L.packed) return fail(kErrKeyOverflow, "rasterize_bwd: key does not pack");
+        ids = kept->ids;
+        pos = kept->pos;
+        bins = kept->bins;
+        M = kept->M;
+    } else {
+        const int32_t bpi = (in.n + 4095) / 4096;
+        rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * in.B_geom);
+        if (rc) return rc;
+        rc = run_sort_and_bin(in, sc, s, &M, &L);
+        if (rc) return rc;
+        ids = sc.gids[0];
+        pos = sc.vals[0];
+        bins = sc.tile_bins;
+    }
+    const int64_t images = in.B_geom > 1 ? 1 : args.B_out;
+    rc = sc.ensure_rgrad(images * M * (args.v_depths ? 10 : 9));
+    if (rc) return rc;
+    BlendBwdArgs a = args;
+    a.sorted_pos = pos;
+    a.M = M;
+    a.rgrad = sc.rgrad;
+    StageTimer tm(s, kStageBlendBwd);
+    rc = launch_blend_bwd(in, L, M > 0 ? ids : nullptr, bins, a, s);
+    if (rc) return fail(rc, "blend_bwd launch failed");
+    return 0;
+}
+
+static BlendBwdArgs bwd_args(const float* final_Ts, const int32_t* final_idx,
+                             const float* v_out_img, int64_t vout_rows, int32_t B_out,
+                             float* v_colors, float* v_opacity, float* v_xy, float* v_conic,
+                             const float* v_out_depth, int64_t vdepth_rows, float* v_depths) {
+    BlendBwdArgs a;
+    a.final_Ts = final_Ts; a.final_idx = final_idx;
+    a.v_out = v_out_img; a.vout_rows = vout_rows; a.B_out = B_out;
+    a.sorted_pos = nullptr; a.M = 0; a.rgrad = nullptr;
+    a.v_colors = v_colors; a.v_opacity = v_opacity; a.v_xy = v_xy; a.v_conic = v_conic;
+    a.v_out_depth = v_out_depth; a.vdepth_rows = vdepth_rows; a.v_depths = v_depths;
+    return a;
+}
+
 int splat_rasterize_fwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
                         const float* opacities, int64_t rows_opac, const float* map_opacities,
                         int64_t rows_map_opac, const float* background, int64_t rows_bg,
@@ -516,35 +634,29 @@ int splat_rasterize_fwd(splat_stream_t stream, const float* colors, int64_t rows
                         int32_t num_gaussians, int32_t B, int32_t img_h, int32_t img_w,
                         float* final_Ts, int32_t* final_idx, float* out_img,
                         int64_t* num_intersects) {
-    RasterInputs in{};
-    in.colors = colors; in.rows_colors = rows_colors;
-    in.opac = opacities; in.rows_opac = rows_opac;
-    in.map_opac = map_opacities; in.rows_map_opac = rows_map_opac;
-    in.background = background; in.rows_bg = rows_bg;
-    in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
-    in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B;
-    in.img_h = img_h; in.img_w = img_w;
-    int rc = check_raster(in, B);
-    if (rc) return rc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    DeviceScratch& sc = scratch_for_current_device();
-    std::lock_guard<std::mutex> lock(sc.mu);
-    rc = sc.ensure_base();
-    if (!rc) {
-        const int32_t bpi = (num_gaussians + 4095) / 4096;
-        rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * B);
-    }
-    if (rc) return rc;
-    int64_t M = 0;
-    KeyLayout L;
-    rc = run_sort_and_bin(in, sc, s, &M, &L);
-    if (num_intersects) *num_intersects = M;
-    if (rc) return rc;
-    StageTimer tm(s, kStageBlendFwd);
-    rc = launch_blend_fwd(in, L, M > 0 ? sc.gids[0] : nullptr, sc.tile_bins, final_Ts,
-                          final_idx, out_img, s);
-    if (rc) return fail(rc, "blend_fwd launch failed");
-    return 0;
+    const RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac,
+                                          map_opacities, rows_map_opac, background, rows_bg, xys,
+                                          depths, radii, conics, cum_tiles_hit, num_gaussians, B,
+                                          img_h, img_w);
+    return rasterize_fwd_impl(static_cast<hipStream_t>(stream), in, nullptr, final_Ts,
+                              final_idx, out_img, nullptr, num_intersects);
+}
+
+int splat_rasterize_depth_fwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
+                              const float* opacities, int64_t rows_opac,
+                              const float* map_opacities, int64_t rows_map_opac,
+                              const float* background, int64_t rows_bg, const float* xys,
+                              const float* depths, const int32_t* radii, const float* conics,
+                              const int32_t* cum_tiles_hit, int32_t num_gaussians, int32_t B,
+                              int32_t img_h, int32_t img_w, float* final_Ts, int32_t* final_idx,
+                              float* out_img, float* out_depth, int64_t* num_intersects) {
+    if (!out_depth) return fail(kErrArgs, "rasterize_depth_fwd: out_depth missing");
+    const RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac,
+                                          map_opacities, rows_map_opac, background, rows_bg, xys,
+                                          depths, radii, conics, cum_tiles_hit, num_gaussians, B,
+                                          img_h, img_w);
+    return rasterize_fwd_impl(static_cast<hipStream_t>(stream), in, nullptr, final_Ts,
+                              final_idx, out_img, out_depth, num_intersects);
 }
 
 int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t rows_colors,
@@ -554,90 +666,47 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
                              const float* depths, const int32_t* radii, const float* conics,
                              const int32_t* cum_tiles_hit, int32_t num_gaussians, int32_t B,
                              int32_t img_h, int32_t img_w, int64_t capacity, float* final_Ts,
-                             int32_t* final_idx, float* out_img, int32_t* sorted_ids,
-                             int32_t* sorted_pos, int32_t* tile_bins, int64_t* num_intersects) {
-    RasterInputs in{};
-    in.colors = colors; in.rows_colors = rows_colors;
-    in.opac = opacities; in.rows_opac = rows_opac;
-    in.map_opac = map_opacities; in.rows_map_opac = rows_map_opac;
-    in.background = background; in.rows_bg = rows_bg;
-    in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
-    in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B;
-    in.img_h = img_h; in.img_w = img_w;
-    int rc = check_raster(in, B);
-    if (rc) return rc;
+                             int32_t* final_idx, float* out_img, float* out_depth,
+                             int32_t* sorted_ids, int32_t* sorted_pos, int32_t* tile_bins,
+                             int64_t* num_intersects) {
     if (capacity < 0 || !tile_bins || (capacity > 0 && (!sorted_ids || !sorted_pos)))
         return fail(kErrArgs, "rasterize_fwd_keep: missing sorted-list buffers");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    DeviceScratch& sc = scratch_for_current_device();
-    std::lock_guard<std::mutex> lock(sc.mu);
-    rc = sc.ensure_base();
-    if (!rc) {
-        const int32_t bpi = (num_gaussians + 4095) / 4096;
-        rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * B);
-    }
-    if (rc) return rc;
+    const RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac,
+                                          map_opacities, rows_map_opac, background, rows_bg, xys,
+                                          depths, radii, conics, cum_tiles_hit, num_gaussians, B,
+                                          img_h, img_w);
     SortTargets tgt;
     tgt.capacity = capacity;
     tgt.ids = sorted_ids;
     tgt.pos = sorted_pos;
     tgt.bins = tile_bins;
-    int64_t M = 0;
-    KeyLayout L;
-    rc = run_sort_and_bin(in, sc, s, &M, &L, &tgt);
-    if (num_intersects) *num_intersects = M;
-    if (rc) return rc;
-    StageTimer tm(s, kStageBlendFwd);
-    rc = launch_blend_fwd(in, L, M > 0 ? sorted_ids : nullptr, tile_bins, final_Ts, final_idx,
-                          out_img, s);
-    if (rc) return fail(rc, "blend_fwd launch failed");
-    return 0;
+    return rasterize_fwd_impl(static_cast<hipStream_t>(stream), in, &tgt, final_Ts, final_idx,
+                              out_img, out_depth, num_intersects);
 }
 
 int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64_t rows_colors,
                                const float* opacities, int64_t rows_opac,
                                const float* background, int64_t rows_bg, const float* xys,
-                               const float* conics, const int32_t* cum_tiles_hit,
-                               const int32_t* sorted_ids, const int32_t* sorted_pos,
-                               const int32_t* tile_bins, int64_t num_intersects,
-                               const float* final_Ts, const int32_t* final_idx,
-                               const float* v_out_img, int64_t vout_rows, int32_t num_gaussians,
-                               int32_t B_out, int32_t B_geom, int32_t img_h, int32_t img_w,
-                               float* v_colors, float* v_opacity, float* v_xy, float* v_conic) {
-    RasterInputs in{};
-    in.colors = colors; in.rows_colors = rows_colors;
-    in.opac = opacities; in.rows_opac = rows_opac;
-    in.map_opac = opacities; in.rows_map_opac = rows_opac;
-    in.background = background; in.rows_bg = rows_bg;
-    in.xys = xys; in.depths = nullptr; in.radii = nullptr; in.conics = conics;
-    in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B_geom;
-    in.img_h = img_h; in.img_w = img_w;
-    int rc = check_raster(in, B_out);
-    if (rc) return rc;
-    if (B_out <= 0 || (B_geom > 1 && B_geom != B_out))
-        return fail(kErrArgs, "rasterize_bwd_sorted: B_geom must be 1 or equal to B_out");
-    if (vout_rows <= 0 || num_intersects < 0 || !tile_bins || !cum_tiles_hit ||
+                               const float* depths, const float* conics,
+                               const int32_t* cum_tiles_hit, const int32_t* sorted_ids,
+                               const int32_t* sorted_pos, const int32_t* tile_bins,
+                               int64_t num_intersects, const float* final_Ts,
+                               const int32_t* final_idx, const float* v_out_img,
+                               int64_t vout_rows, const float* v_out_depth, int64_t vdepth_rows,
+                               int32_t num_gaussians, int32_t B_out, int32_t B_geom,
+                               int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
+                               float* v_xy, float* v_conic, float* v_depths) {
+    if (num_intersects < 0 || !tile_bins ||
         (num_intersects > 0 && (!sorted_ids || !sorted_pos)))
-        return fail(kErrArgs, "rasterize_bwd_sorted: invalid cotangent or sorted lists");
-    if ((int64_t)B_out * num_gaussians >= ((int64_t)1 << 31))
-        return fail(kErrArgs, "rasterize_bwd_sorted: more than 2^31 gradient rows");
-    const KeyLayout L = key_layout(B_geom, img_h, img_w);
-    if (!L.packed) return fail(kErrKeyOverflow, "rasterize_bwd_sorted: key does not pack");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    DeviceScratch& sc = scratch_for_current_device();
-    std::lock_guard<std::mutex> lock(sc.mu);
-    const int64_t images = B_geom > 1 ? 1 : B_out;
-    rc = sc.ensure_rgrad(images * num_intersects * 9);
-    if (rc) return rc;
-    BlendBwdArgs a;
-    a.final_Ts = final_Ts; a.final_idx = final_idx;
-    a.v_out = v_out_img; a.vout_rows = vout_rows; a.B_out = B_out;
-    a.sorted_pos = sorted_pos; a.M = num_intersects; a.rgrad = sc.rgrad;
-    a.v_colors = v_colors; a.v_opacity = v_opacity; a.v_xy = v_xy; a.v_conic = v_conic;
-    StageTimer tm(s, kStageBlendBwd);
-    rc = launch_blend_bwd(in, L, num_intersects > 0 ? sorted_ids : nullptr, tile_bins, a, s);
-    if (rc) return fail(rc, "blend_bwd launch failed");
-    return 0;
+        return fail(kErrArgs, "rasterize_bwd_sorted: invalid sorted lists");
+    const RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac, opacities,
+                                          rows_opac, background, rows_bg, xys, depths, nullptr,
+                                          conics, cum_tiles_hit, num_gaussians, B_geom, img_h,
+                                          img_w);
+    const BlendBwdArgs a = bwd_args(final_Ts, final_idx, v_out_img, vout_rows, B_out, v_colors,
+                                    v_opacity, v_xy, v_conic, v_out_depth, vdepth_rows, v_depths);
+    const KeptLists kept{sorted_ids, sorted_pos, tile_bins, num_intersects};
+    return rasterize_bwd_impl(static_cast<hipStream_t>(stream), in, &kept, a);
 }
 
 int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
@@ -649,46 +718,34 @@ int splat_rasterize_bwd(splat_stream_t stream, const float* colors, int64_t rows
                         int64_t vout_rows, int32_t num_gaussians, int32_t B_out, int32_t B_geom,
                         int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
                         float* v_xy, float* v_conic) {
-    RasterInputs in{};
-    in.colors = colors; in.rows_colors = rows_colors;
-    in.opac = opacities; in.rows_opac = rows_opac;
-    in.map_opac = map_opacities; in.rows_map_opac = rows_map_opac;
-    in.background = background; in.rows_bg = rows_bg;
-    in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
-    in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B_geom;
-    in.img_h = img_h; in.img_w = img_w;
-    int rc = check_raster(in, B_out);
-    if (rc) return rc;
-    if (B_out <= 0 || (B_geom > 1 && B_geom != B_out))
-        return fail(kErrArgs, "rasterize_bwd: B_geom must be 1 or equal to B_out");
-    if (vout_rows <= 0) return fail(kErrArgs, "rasterize_bwd: empty cotangent");
-    if ((int64_t)B_out * num_gaussians >= ((int64_t)1 << 31))
-        return fail(kErrArgs, "rasterize_bwd: more than 2^31 gradient rows");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    DeviceScratch& sc = scratch_for_current_device();
-    std::lock_guard<std::mutex> lock(sc.mu);
-    rc = sc.ensure_base();
-    if (!rc) {
-        const int32_t bpi = (num_gaussians + 4095) / 4096;
-        rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * B_geom);
-    }
-    if (rc) return rc;
-    int64_t M = 0;
-    KeyLayout L;
-    rc = run_sort_and_bin(in, sc, s, &M, &L);
-    if (rc) return rc;
-    const int64_t images = B_geom > 1 ? 1 : B_out;
-    rc = sc.ensure_rgrad(images * M * 9);
-    if (rc) return rc;
-    BlendBwdArgs a;
-    a.final_Ts = final_Ts; a.final_idx = final_idx;
-    a.v_out = v_out_img; a.vout_rows = vout_rows; a.B_out = B_out;
-    a.sorted_pos = sc.vals[0]; a.M = M; a.rgrad = sc.rgrad;
-    a.v_colors = v_colors; a.v_opacity = v_opacity; a.v_xy = v_xy; a.v_conic = v_conic;
-    StageTimer tm(s, kStageBlendBwd);
-    rc = launch_blend_bwd(in, L, M > 0 ? sc.gids[0] : nullptr, sc.tile_bins, a, s);
-    if (rc) return fail(rc, "blend_bwd launch failed");
-    return 0;
+    const RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac,
+                                          map_opacities, rows_map_opac, background, rows_bg, xys,
+                                          depths, radii, conics, cum_tiles_hit, num_gaussians,
+                                          B_geom, img_h, img_w);
+    const BlendBwdArgs a = bwd_args(final_Ts, final_idx, v_out_img, vout_rows, B_out, v_colors,
+                                    v_opacity, v_xy, v_conic, nullptr, 0, nullptr);
+    return rasterize_bwd_impl(static_cast<hipStream_t>(stream), in, nullptr, a);
+}
+
+int splat_rasterize_depth_bwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
+                              const float* opacities, int64_t rows_opac,
+                              const float* map_opacities, int64_t rows_map_opac,
+                              const float* background, int64_t rows_bg, const float* xys,
+                              const float* depths, const int32_t* radii, const float* conics,
+                              const int32_t* cum_tiles_hit, const float* final_Ts,
+                              const int32_t* final_idx, const float* v_out_img,
+                              int64_t vout_rows, const float* v_out_depth, int64_t vdepth_rows,
+                              int32_t num_gaussians, int32_t B_out, int32_t B_geom,
+                              int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
+                              float* v_xy, float* v_conic, float* v_depths) {
+    if (!v_depths) return fail(kErrArgs, "rasterize_depth_bwd: v_depths missing");
+    const RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac,
+                                          map_opacities, rows_map_opac, background, rows_bg, xys,
+                                          depths, radii, conics, cum_tiles_hit, num_gaussians,
+                                          B_geom, img_h, img_w);
+    const BlendBwdArgs a = bwd_args(final_Ts, final_idx, v_out_img, vout_rows, B_out, v_colors,
+                                    v_opacity, v_xy, v_conic, v_out_depth, vdepth_rows, v_depths);
+    return rasterize_bwd_impl(static_cast<hipStream_t>(stream), in, nullptr, a);
 }
 
 }  // extern "C"

@@ -167,19 +167,22 @@ struct SortTargets {
 int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stream,
                      int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt = nullptr);
 
+// out_depth non-null: also the expected-depth channel (in.depths per geometry item).
 int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,
-                     float* out_img, hipStream_t stream);
+                     float* out_img, float* out_depth, hipStream_t stream);
 
 // Backward over sorted lists of M intersections: sorted_ids / sorted_pos / tile_bins as produced
 // by sort_and_bin; in.cum gives each item's emission range; rgrad is scratch of
-// B_out_eff * M * 9 floats (B_out_eff = 1 when geometry is batched, else B_out).
+// B_out_eff * M * NG floats (B_out_eff = 1 when geometry is batched, else B_out; NG = 9, or 10
+// with the depth channel). v_depths non-null selects the depth channel (in.depths, v_out_depth).
 struct BlendBwdArgs {
     const float* final_Ts; const int32_t* final_idx;
     const float* v_out; int64_t vout_rows;
     int32_t B_out;
     const int32_t* sorted_pos; int64_t M; float* rgrad;
     float* v_colors; float* v_opacity; float* v_xy; float* v_conic;
+    const float* v_out_depth = nullptr; int64_t vdepth_rows = 0; float* v_depths = nullptr;
 };
 int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, const BlendBwdArgs& a, hipStream_t stream);

@@ -243,3 +243,76 @@ def test_empty_and_single_intersection():
                                viewmat=_t(np.eye(4, dtype=np.float32)), background=_t(bg),
                                img_shape=(H, W), f=(40.0, 40.0), c=(40.0, 40.0))
     np.testing.assert_array_equal(_np(img1), np.broadcast_to(bg, (H, W, 3)))
+
+
+def test_render_depth_and_grads_match_oracle():
+    """render(render_depth=True) (splax/_render.py:112-114): image bit-exact with the plain
+    render, expected depth bit-exact with the oracle, and the gradients of a mixed colour + depth
+    loss through project -> rasterize_depth (v_depths feeding the projection's depth cotangent)."""
+    _case("render_depth + grads vs oracle")
+    n, H, W = 6000, 128, 160
+    sc = random_scene(n, H, W, seed=5)
+    rng = np.random.default_rng(6)
+    w = rng.uniform(-1, 1, (H, W, 3)).astype(np.float32)
+    wd = rng.uniform(-1, 1, (H, W)).astype(np.float32)
+    q = np.roll(sc["quats"], -1, axis=-1)
+    xys, depths, radii, conics, nth, cum = O.project_fwd(
+        sc["means"], sc["scales"], q, sc["vm"], sc["opac"], n=n, total=n, img_shape=(H, W),
+        f=sc["f"], c=sc["c"])
+    img, Ts, fidx, _, _, dimg = O.rasterize_fwd(sc["colors"], sc["opac"], sc["opac"], sc["bg"],
+                                                xys, depths, radii, conics, cum, n=n, B=1,
+                                                img_shape=(H, W), render_depth=True)
+    vc, vo, vxy, vcon, _, vdep = O.rasterize_bwd(
+        sc["colors"], sc["opac"], sc["opac"], sc["bg"], xys, depths, radii, conics, cum, Ts, fidx,
+        w, n=n, B_out=1, B_geom=1, img_shape=(H, W), v_out_depth=wd)
+    vm_, vs_, vq_, vv_, _ = O.project_bwd(sc["means"], sc["scales"], q, sc["vm"], radii, conics,
+                                          vxy, vdep, vcon, n=n, B=1, f=sc["f"])
+    ref = dict(means=vm_, scales=vs_, quats=np.roll(vq_, 1, axis=-1), colors=vc,
+               opac=vo.reshape(-1, 1))
+    p = {k: _t(sc[k], grad=True) for k in ("means", "scales", "quats", "colors", "opac")}
+    vm = _t(sc["vm"], grad=True)
+    common = dict(viewmat=vm, background=_t(sc["bg"]), img_shape=(H, W), f=sc["f"], c=sc["c"])
+    gimg, gdep = splax_amd.render(p["means"], p["scales"], p["quats"], p["colors"], p["opac"],
+                                  render_depth=True, **common)
+    assert gdep.shape == (H, W)
+    plain, _ = splax_amd.render(*[v.detach() for v in p.values()], **common)
+    assert_bit_exact(_np(gimg), _np(plain), "render_depth/img vs plain render")
+    assert_bit_exact(_np(gimg), img.reshape(H, W, 3), "render_depth/img")
+    assert_bit_exact(_np(gdep), dimg.reshape(H, W), "render_depth/depth")
+    ((gimg * _t(w)).sum() + (gdep * _t(wd)).sum()).backward()
+    for k in ("means", "scales", "quats", "colors", "opac"):
+        r = rel_fro(_np(p[k].grad), ref[k])
+        assert r < 1e-5, f"{k}: relative Frobenius error {r:.2e}"
+    assert rel_fro(_np(vm.grad), vv_) < 1e-5
+
+
+def test_render_depth_batched_equals_sequential():
+    """Batched cameras on the depth path equal the per-camera renders (image and depth bit for
+    bit, gradients summed), as the reference's tests/test_depth_reg.py:194-229."""
+    _case("render_depth batched")
+    n, H, W = 2000, 64, 64
+    sc = random_scene(n, H, W, seed=12)
+    vms = np.stack([sc["vm"]] * 3)
+    vms[1, 0, 3] += 0.2
+    vms[2, 2, 3] += 0.3
+    wd = np.random.default_rng(3).uniform(0, 1, (3, H, W)).astype(np.float32)
+
+    def run(vm_np, wd_np):
+        p = {k: _t(sc[k], grad=True) for k in ("means", "scales", "quats", "colors", "opac")}
+        img, dep = splax_amd.render(p["means"], p["scales"], p["quats"], p["colors"], p["opac"],
+                                    viewmat=_t(vm_np), background=_t(sc["bg"]), img_shape=(H, W),
+                                    f=sc["f"], c=sc["c"], render_depth=True)
+        (dep * _t(wd_np)).sum().backward()
+        return _np(img), _np(dep), {k: _np(v.grad) for k, v in p.items()}
+
+    bimg, bdep, bg = run(vms, wd)
+    assert bdep.shape == (3, H, W)
+    singles = [run(vms[b], wd[b]) for b in range(3)]
+    for b in range(3):
+        assert_bit_exact(bimg[b], singles[b][0], f"batched depth/img[{b}]")
+        assert_bit_exact(bdep[b], singles[b][1], f"batched depth/depth[{b}]")
+    assert float(np.abs(bg["colors"]).max()) == 0.0  # a depth-only loss: no colour gradient
+    for k in ("means", "scales", "quats", "opac"):
+        summed = sum(s[2][k].astype(np.float64) for s in singles)
+        r = rel_fro(bg[k], summed)
+        assert r < 1e-5, f"batched depth/{k}: {r:.2e}"

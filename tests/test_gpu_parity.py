@@ -299,7 +299,7 @@ def test_kept_sort_path_equals_resort_path(name):
     xys, depths, radii, conics, nth, cum = _raster_inputs(s)
     o = _t(s.opacities).reshape(-1)
     geo = (_t(xys), _t(depths), _t(radii), _t(conics), _t(cum))
-    img, Ts, fidx, ids, pos, bins, M = _ops.rasterize_fwd_keep(
+    img, Ts, fidx, ids, pos, bins, M, _ = _ops.rasterize_fwd_keep(
         _t(s.colors), o, o, _t(s.background), *geo, n=s.n, B=1, img_shape=s.img_shape)
     rk, rid, rbins = O.sort_and_bin(xys, depths, radii, conics, s.opacities, cum, n=s.n, B=1,
                                     img_shape=s.img_shape)
@@ -317,14 +317,77 @@ def test_kept_sort_path_equals_resort_path(name):
     assert_bit_exact(_np(img), rimg, f"{name}/kept img")
     H, W = s.img_shape
     vout = _t((2.0 * (rimg.reshape(H, W, 3) - s.targets[0]) / rimg.size).astype(np.float32))
-    a = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[3], geo[4], ids,
-                                  pos, bins, M, Ts, fidx, vout.reshape(-1, 3), n=s.n, B_out=1,
-                                  B_geom=1, img_shape=s.img_shape)
+    a = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[1], geo[3],
+                                  geo[4], ids, pos, bins, M, Ts, fidx, vout.reshape(-1, 3),
+                                  n=s.n, B_out=1, B_geom=1, img_shape=s.img_shape)
     b = _ops.rasterize_bwd(_t(s.colors), o, o, _t(s.background), *geo, Ts, fidx,
                            vout.reshape(-1, 3), n=s.n, B_out=1, B_geom=1, img_shape=s.img_shape)
-    a2 = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[3], geo[4],
-                                   ids, pos, bins, M, Ts, fidx, vout.reshape(-1, 3), n=s.n,
-                                   B_out=1, B_geom=1, img_shape=s.img_shape)
+    a2 = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[1], geo[3],
+                                   geo[4], ids, pos, bins, M, Ts, fidx, vout.reshape(-1, 3),
+                                   n=s.n, B_out=1, B_geom=1, img_shape=s.img_shape)
     for label, x, y, z in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), a, b, a2):
         _grad_compare(_np(x), _np(y), f"{name}/{label} kept vs re-sorted")
         _grad_compare(_np(x), _np(z), f"{name}/{label} repeat")
+
+
+# ---------------------------------------------------------------- depth channel
+
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg2_50k"])
+def test_rasterize_depth_fwd_bit_exact(name):
+    """The depth path (splax/_rasterize/_kernels.py:208-383): expected depth bit-exact against
+    the oracle, image / final_Ts / final_idx identical to the colour-only path."""
+    _case(f"rasterize_depth_fwd {name}")
+    s = _scene_arrays(name)
+    xys, depths, radii, conics, nth, cum = _raster_inputs(s)
+    ref = O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background, xys, depths, radii,
+                          conics, cum, n=s.n, B=1, img_shape=s.img_shape, render_depth=True)
+    args = (_t(s.colors), _t(s.opacities).reshape(-1), _t(s.opacities).reshape(-1),
+            _t(s.background), _t(xys), _t(depths), _t(radii), _t(conics), _t(cum))
+    gimg, gT, gidx, gM, gdep = _ops.rasterize_fwd(*args, n=s.n, B=1, img_shape=s.img_shape,
+                                                   render_depth=True)
+    pimg, pT, pidx, _ = _ops.rasterize_fwd(*args, n=s.n, B=1, img_shape=s.img_shape)
+    kimg, kT, kidx, _, _, _, kM, kdep = _ops.rasterize_fwd_keep(
+        *args, n=s.n, B=1, img_shape=s.img_shape, render_depth=True)
+    torch.cuda.synchronize()
+    assert gM == ref[4] == kM
+    assert_bit_exact(_np(gdep), ref[5], f"{name}/depth")
+    assert_bit_exact(_np(kdep), ref[5], f"{name}/kept-path depth")
+    assert_bit_exact(_np(gimg), _np(pimg), f"{name}/image vs colour-only path")
+    assert_bit_exact(_np(gT), _np(pT), f"{name}/final_Ts vs colour-only path")
+    assert_bit_exact(_np(gidx), ref[2], f"{name}/final_idx")
+
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg2_50k"])
+def test_rasterize_depth_bwd_matches_oracle(name):
+    _case(f"rasterize_depth_bwd {name}")
+    s = _scene_arrays(name)
+    xys, depths, radii, conics, nth, cum = _raster_inputs(s)
+    rimg, rT, ridx, _, _, rdep = O.rasterize_fwd(
+        s.colors, s.opacities, s.opacities, s.background, xys, depths, radii, conics, cum, n=s.n,
+        B=1, img_shape=s.img_shape, render_depth=True)
+    H, W = s.img_shape
+    rng = np.random.default_rng(17)
+    vout = (2.0 * (rimg.reshape(H, W, 3) - s.targets[0]) / rimg.size).astype(np.float32)
+    vd = (rng.uniform(-1, 1, (H, W)) / (H * W)).astype(np.float32)
+    ref = O.rasterize_bwd(s.colors, s.opacities, s.opacities, s.background, xys, depths, radii,
+                          conics, cum, rT, ridx, vout, n=s.n, B_out=1, B_geom=1,
+                          img_shape=s.img_shape, v_out_depth=vd)
+    o = _t(s.opacities).reshape(-1)
+    geo = (_t(xys), _t(depths), _t(radii), _t(conics), _t(cum))
+    got = _ops.rasterize_bwd(_t(s.colors), o, o, _t(s.background), *geo, _t(rT), _t(ridx),
+                             _t(vout).reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
+                             img_shape=s.img_shape, v_out_depth=_t(vd))
+    _, Ts, fidx, ids, pos, bins, M, _ = _ops.rasterize_fwd_keep(
+        _t(s.colors), o, o, _t(s.background), *geo, n=s.n, B=1, img_shape=s.img_shape,
+        render_depth=True)
+    kept = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[1], geo[3],
+                                     geo[4], ids, pos, bins, M, Ts, fidx,
+                                     _t(vout).reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
+                                     img_shape=s.img_shape, v_out_depth=_t(vd))
+    torch.cuda.synchronize()
+    labels = ("v_colors", "v_opacity", "v_xy", "v_conic", "v_depths")
+    refs = (*ref[:4], ref[5])
+    for label, g, k, r in zip(labels, got, kept, refs):
+        _grad_compare(_np(g).reshape(r.shape), r, f"{name}/{label}")
+        _grad_compare(_np(k).reshape(r.shape), r, f"{name}/{label} (kept lists)")

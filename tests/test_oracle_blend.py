@@ -133,3 +133,60 @@ def test_front_gaussian_occludes():
     expect = np.array([a0, 0.0, (1 - a0) * a1])  # red in front of blue, black background
     np.testing.assert_allclose(img.reshape(H, W, 3)[8, 8], expect, atol=1e-6)
     np.testing.assert_allclose(Ts.reshape(H, W)[8, 8], (1 - a0) * (1 - a1), atol=1e-6)
+
+
+# ---------------------------------------------------------------- depth channel
+# _rasterize_depth_kernel (splax/_rasterize/_kernels.py:277-383): the expected depth uses the
+# colour blend's weights and adds no background term.
+
+
+def test_depth_single_gaussian_equals_z_times_coverage():
+    """One gaussian: depth = z * A exactly, A the accumulated alpha (unit colour over black), as
+    the reference's tests/test_depth_reg.py:75-107; empty pixels are 0."""
+    H = W = 64
+    means = np.array([[0.1, -0.05, 0.0]], np.float32)
+    scales = np.full((1, 3), 0.12, np.float32)
+    quats = np.array([[0.0, 0.0, 0.0, 1.0]], np.float32)
+    opac = np.array([[0.9]], np.float32)
+    vm = np.array([[1, 0, 0, 0], [0, 1, 0, 0], [0, 0, 1, 4.0], [0, 0, 0, 1]], np.float32)
+    f, c = (float(H), float(H)), (W // 2, H // 2)
+    xys, depths, radii, conics, nth, cum = O.project_fwd(means, scales, quats, vm, opac, n=1,
+                                                         total=1, img_shape=(H, W), f=f, c=c)
+    black = np.zeros(3, np.float32)
+    A = O.rasterize_fwd(np.ones((1, 3), np.float32), opac, opac, black, xys, depths, radii,
+                        conics, cum, n=1, B=1, img_shape=(H, W))[0][..., 0]
+    out = O.rasterize_fwd(np.full((1, 3), 0.5, np.float32), opac, opac, black, xys, depths,
+                          radii, conics, cum, n=1, B=1, img_shape=(H, W), render_depth=True)
+    D = out[5]
+    z = np.float32(4.0)
+    assert depths[0] == z
+    np.testing.assert_array_equal(D, z * A)  # the same weight times z, in float32
+    assert D[0, 0] == 0.0 and A[0, 0] == 0.0
+    assert D.max() > 0.5 * z
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_depth_path_keeps_image_and_matches_brute_force(seed):
+    """The depth path's image is bit-for-bit the plain one (tests/test_depth_reg.py:110-118),
+    and its depth equals a float64 brute-force blend of the depths."""
+    n, H, W = 300, 48, 64
+    sc = random_scene(n, H, W, seed=seed, scale_range=(0.02, 0.1), mean_scale=0.6,
+                      opac_range=(0.2, 0.95))
+    proj, (img, Ts, fidx, stats, M), (sk, sid, bins) = _pipeline(sc, n)
+    xys, depths, radii, conics, nth, cum = proj
+    dimg_out = O.rasterize_fwd(sc["colors"], sc["opac"], sc["opac"], sc["bg"], xys, depths, radii,
+                               conics, cum, n=n, B=1, img_shape=(H, W), render_depth=True)
+    np.testing.assert_array_equal(dimg_out[0], img)
+    np.testing.assert_array_equal(dimg_out[1], Ts)
+    np.testing.assert_array_equal(dimg_out[2], fidx)
+    lay, _ = O.key_layout(1, H, W)
+    order = _front_to_back(sk, sid, lay["depth_bits"])
+    mem = tile_members(sk, sid, order, img_shape=(H, W), depth_bits=lay["depth_bits"],
+                       tile_bits=lay["tile_n_bits"])
+    t = lambda a: torch.from_numpy(np.asarray(a, np.float64))  # noqa: E731
+    _, _, _, rdep = blend_ref(t(xys), t(conics), t(sc["opac"][:, 0]), t(sc["colors"]),
+                              t(sc["bg"]), order, torch.from_numpy(mem), img_shape=(H, W),
+                              depths=t(depths).reshape(-1))
+    err = np.abs(dimg_out[5].reshape(H, W) - rdep.numpy())
+    assert err.max() < 1e-5 * max(1.0, float(np.abs(depths).max())), err.max()
+    assert float(np.abs(dimg_out[5]).max()) > 0.0

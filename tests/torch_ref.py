@@ -58,13 +58,16 @@ def project_ref(means, scales, quats_wxyz, viewmat, *, f, c, img_shape, glob_sca
     return xys, tz, conics, cov
 
 
-def blend_ref(xys, conics, opac, colors, bg, order, members, *, img_shape, keep=None):
+def blend_ref(xys, conics, opac, colors, bg, order, members, *, img_shape, keep=None,
+              depths=None):
     """Dense front-to-back blend of the gaussians `order` (front first) into (H, W, 3).
 
     members[k] is a (H, W) bool mask of the pixels whose tile lists gaussian order[k] (the tile
     assignment, fixed by the sort). keep (optional, (K, H, W) bool) overrides the per-pair
     accept decision (e.g. the oracle's float32 decisions) so gradients follow the same pairs.
-    Returns (img, T_final, accepted (K, H, W)).
+    Returns (img, T_final, accepted (K, H, W)); with depths (per gaussian) also the expected
+    depth (H, W): depth times the same blend weights, no background term
+    (splax/_rasterize/_kernels.py:370-372).
     """
     H, W = img_shape
     jj, ii = torch.meshgrid(torch.arange(W, dtype=F64), torch.arange(H, dtype=F64),
@@ -72,6 +75,7 @@ def blend_ref(xys, conics, opac, colors, bg, order, members, *, img_shape, keep=
     px, py = jj + 0.5, ii + 0.5
     T = torch.ones((H, W), dtype=F64)
     out = torch.zeros((H, W, 3), dtype=F64)
+    dout = torch.zeros((H, W), dtype=F64)
     done = torch.zeros((H, W), dtype=torch.bool)
     acc = []
     for k, g in enumerate(order):
@@ -91,9 +95,14 @@ def blend_ref(xys, conics, opac, colors, bg, order, members, *, img_shape, keep=
         acc.append(ok)
         okf = ok.to(F64)
         out = out + (colors[g] * (alpha * T * okf)[..., None])
+        if depths is not None:
+            dout = dout + depths[g] * (alpha * T * okf)
         T = T * (1 - alpha * okf)
     img = out + T[..., None] * bg
-    return img, T, torch.stack(acc) if acc else torch.zeros((0, H, W), dtype=torch.bool)
+    accepted = torch.stack(acc) if acc else torch.zeros((0, H, W), dtype=torch.bool)
+    if depths is not None:
+        return img, T, accepted, dout
+    return img, T, accepted
 
 
 def tile_members(keys: np.ndarray, ids: np.ndarray, order: np.ndarray, *, img_shape,
