@@ -158,14 +158,21 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
                                float* v_xy, float* v_conic, float* v_depths);
 
 /* Replaces sort_and_bin (splax/_rasterize/_sort/_sort.py:29-171), exposed for callers that keep
- * the sorted lists: writes the M sorted packed keys and gaussian ids (capacity >= M required,
- * else status 6 with *num_intersects = M) and the [B*num_tiles, 2] tile bins. */
+ * the sorted lists: writes the M sorted keys (as int64: the packed 32-bit key widened, or the
+ * 64-bit key (image << (32 + tile_bits)) | (tile << 32) | raw float depth bits when fewer than 16
+ * depth bits remain, _sort.py:56-66,143-170) and gaussian ids (capacity >= M required, else
+ * status 6 with *num_intersects = M), and the [B*num_tiles, 2] tile bins. Status 2 when even the
+ * 64-bit key overflows (image + tile bits above 32). */
 int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* depths,
                        const int32_t* radii, const float* conics, const float* map_opacities,
                        int64_t rows_map_opac, const int32_t* cum_tiles_hit,
                        int32_t num_gaussians, int32_t B, int32_t img_h, int32_t img_w,
-                       int32_t* sorted_keys, int32_t* sorted_ids, int64_t capacity,
+                       int64_t* sorted_keys, int32_t* sorted_ids, int64_t capacity,
                        int32_t* tile_bins, int64_t* num_intersects);
+
+/* Replaces the _use_32bit_keys switch (splax/_rasterize/_sort/_sort.py:23-26), which the
+ * reference's tests patch: force != 0 makes every sort take the 64-bit key (process-wide). */
+int splat_set_wide_keys(int force);
 
 /* Replaces clear_cache (splax/_cache.py:158-164): frees the per-device scratch. */
 void splat_clear_cache(void);

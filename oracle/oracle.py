@@ -46,7 +46,7 @@ def lib() -> ctypes.CDLL:
         _lib.oracle_expf.restype = ctypes.c_float
         _lib.oracle_expf.argtypes = [ctypes.c_float]
         for name in ("oracle_emit_keys", "oracle_sort_and_bin", "oracle_rasterize_fwd",
-                     "oracle_rasterize_bwd"):
+                     "oracle_rasterize_bwd", "oracle_emit_keys_wide", "oracle_sort_and_bin_wide"):
             getattr(_lib, name).restype = ctypes.c_int64
     return _lib
 
@@ -95,6 +95,16 @@ def key_layout(B: int, H: int, W: int) -> tuple[dict, bool]:
     return dict(zip(names, (int(v) for v in out))), bool(ok)
 
 
+def set_wide_keys(force: bool) -> None:
+    """Force the 64-bit key for every layout (as the reference's tests patch _use_32bit_keys)."""
+    lib().oracle_set_wide_keys(ctypes.c_int(int(bool(force))))
+
+
+def key_mode(B: int, H: int, W: int) -> int:
+    """0: packed 32-bit key, 1: 64-bit key, -2: even the 64-bit key overflows."""
+    return int(lib().oracle_key_mode(_i32(B), _i32(H), _i32(W)))
+
+
 def project_fwd(means, scales, quats_xyzw, viewmat, opacities, *, n, total, img_shape, f, c,
                 glob_scale=1.0, clip_thresh=0.01, transforms=None, transform_ids=None,
                 num_transforms=None):
@@ -126,17 +136,25 @@ def project_fwd(means, scales, quats_xyzw, viewmat, opacities, *, n, total, img_
 
 
 def emit_keys(xys, depths, radii, conics, map_opac, cum, *, n, B, img_shape):
-    """Unsorted keys/ids in emission order and the per-image depth range."""
+    """Unsorted keys/ids in emission order and the per-image depth range (packed key), or
+    int64 keys and ids (64-bit key; the depth range is then unused and returned as zeros)."""
     xys, depths, conics, map_opac = map(_c32, (xys, depths, conics, map_opac))
     radii, cum = _ci32(radii).ravel(), _ci32(cum).ravel()
     M = int(cum[-1]) if cum.size else 0
-    keys = np.full(max(M, 1), -999, np.int32)
     ids = np.full(max(M, 1), -1, np.int32)
     mm = np.zeros(2 * B, np.float32)
     H, W = img_shape
-    m = lib().oracle_emit_keys(_f(xys), _f(depths), _i(radii), _f(conics), _f(map_opac),
-                               _i64(map_opac.size), _i(cum), _i32(n), _i32(B), _i32(H),
-                               _i32(W), _i(keys), _i(ids), _i64(keys.size), _f(mm))
+    if key_mode(B, H, W) == 1:
+        keys = np.full(max(M, 1), -999, np.int64)
+        m = lib().oracle_emit_keys_wide(_f(xys), _f(depths), _i(radii), _f(conics), _f(map_opac),
+                                        _i64(map_opac.size), _i(cum), _i32(n), _i32(B), _i32(H),
+                                        _i32(W), keys.ctypes.data_as(_i64p), _i(ids),
+                                        _i64(keys.size))
+    else:
+        keys = np.full(max(M, 1), -999, np.int32)
+        m = lib().oracle_emit_keys(_f(xys), _f(depths), _i(radii), _f(conics), _f(map_opac),
+                                   _i64(map_opac.size), _i(cum), _i32(n), _i32(B), _i32(H),
+                                   _i32(W), _i(keys), _i(ids), _i64(keys.size), _f(mm))
     if m < 0:
         raise ValueError(f"oracle emit_keys failed with code {m}")
     return keys[:m], ids[:m], mm
@@ -149,12 +167,14 @@ def sort_and_bin(xys, depths, radii, conics, map_opac, cum, *, n, B, img_shape):
     M = int(cum[-1]) if cum.size else 0
     H, W = img_shape
     lay, _ = key_layout(B, H, W)
-    keys = np.zeros(max(M, 1), np.int32)
+    wide = key_mode(B, H, W) == 1
+    keys = np.zeros(max(M, 1), np.int64 if wide else np.int32)
     ids = np.zeros(max(M, 1), np.int32)
     bins = np.zeros((B * lay["num_tiles"], 2), np.int32)
-    m = lib().oracle_sort_and_bin(_f(xys), _f(depths), _i(radii), _f(conics), _f(map_opac),
-                                  _i64(map_opac.size), _i(cum), _i32(n), _i32(B), _i32(H),
-                                  _i32(W), _i(keys), _i(ids), _i64(keys.size), _i(bins))
+    fn = lib().oracle_sort_and_bin_wide if wide else lib().oracle_sort_and_bin
+    kp = keys.ctypes.data_as(_i64p) if wide else _i(keys)
+    m = fn(_f(xys), _f(depths), _i(radii), _f(conics), _f(map_opac), _i64(map_opac.size),
+           _i(cum), _i32(n), _i32(B), _i32(H), _i32(W), kp, _i(ids), _i64(keys.size), _i(bins))
     if m < 0:
         raise ValueError(f"oracle sort_and_bin failed with code {m}")
     return keys[:m], ids[:m], bins

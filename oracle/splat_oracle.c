@@ -319,6 +319,21 @@ int oracle_key_layout(int32_t B, int32_t img_h, int32_t img_w, int32_t* out) {
     return out[5] >= 16;
 }
 
+/* _use_32bit_keys, splax/_rasterize/_sort/_sort.py:23-26 (which the reference's tests patch to
+ * force the 64-bit key): with the switch set, every layout takes the 64-bit key. */
+static int g_force_wide = 0;
+void oracle_set_wide_keys(int force) { g_force_wide = force != 0; }
+
+/* 0: packed 32-bit key; 1: 64-bit key; -2: even the 64-bit key overflows (image + tile bits
+ * above 32, splax/_rasterize/_sort/_sort.py:61-66). */
+int oracle_key_mode(int32_t B, int32_t img_h, int32_t img_w) {
+    int32_t L[6];
+    int packed = oracle_key_layout(B, img_h, img_w, L);
+    if (packed && !g_force_wide) return 0;
+    if (L[3] + L[4] > 32) return -2;
+    return 1;
+}
+
 /* ---------------------------------------------------------------- projection forward
  * _project_kernel, splax/_project/_kernels.py:122-248, with _apply_transform (:627-644) and
  * _project_geom (:647-664); the inclusive scan of splax/_project/_kernels.py:107. */
@@ -583,6 +598,134 @@ static void tile_bin_edges(const int32_t* sorted_keys, int64_t M, int32_t num_ti
     }
 }
 
+/* _map_intersects_64bit, splax/_rasterize/_sort/_kernels.py:156-211: the same tile walk, key
+ * (image << (32 + tile_bits)) | (tile << 32) | the depth's raw float bits (int32, widened with
+ * sign extension; a visible item's depth is positive, so its bits order like the value). */
+int64_t oracle_emit_keys_wide(const float* xys, const float* depths, const int32_t* radii,
+                              const float* conics, const float* map_opac, int64_t rows_map_opac,
+                              const int32_t* cum, int32_t n, int32_t B, int32_t img_h,
+                              int32_t img_w, int64_t* keys, int32_t* ids, int64_t cap) {
+    int32_t L[6];
+    oracle_key_layout(B, img_h, img_w, L);
+    const int32_t tbx = L[0], tby = L[1], tile_bits = L[3];
+    if (L[3] + L[4] > 32) return -2;
+    const int64_t total = (int64_t)B * n;
+    const int64_t M = total > 0 ? cum[total - 1] : 0;
+    if (M > cap) return -3;
+#pragma omp parallel for schedule(dynamic, 4096)
+    for (int64_t idx = 0; idx < total; ++idx) {
+        if (radii[idx] <= 0) continue;
+        int32_t bid = (int32_t)(idx / n);
+        int64_t cur = idx > 0 ? cum[idx - 1] : 0;
+        int32_t dbits;
+        memcpy(&dbits, depths + idx, sizeof(dbits));
+        const int64_t depth_id = (int64_t)dbits;
+        const int64_t iid_enc = (int64_t)((uint64_t)bid << (32 + tile_bits));
+        float opac = map_opac[idx % rows_map_opac];
+        float t = iso_level(opac);
+        Ellipse e;
+        ellipse_init(conics[3 * idx], conics[3 * idx + 1], conics[3 * idx + 2], t, xys[2 * idx],
+                     xys[2 * idx + 1], tbx, tby, &e);
+        if (!e.valid) continue;
+        float I[2];
+        ellipse_init_span(&e, I);
+        for (int32_t u = e.rect_min[0]; u < e.rect_max[0]; ++u) {
+            int32_t mn, mx;
+            ellipse_column(&e, u, I, &mn, &mx);
+            for (int32_t v = mn; v < mx; ++v) {
+                int64_t tile_id = e.isY ? (int64_t)u * tbx + v : (int64_t)v * tbx + u;
+                keys[cur] = iid_enc | (int64_t)((uint64_t)tile_id << 32) | depth_id;
+                ids[cur] = (int32_t)idx;
+                ++cur;
+            }
+        }
+    }
+    return M;
+}
+
+/* Stable ascending LSD radix sort of 64-bit keys (as unsigned, i.e. by (image, tile, depth))
+ * with int32 values; bytes on which every key agrees are skipped. */
+static void radix_sort_pairs64(int64_t* keys, int32_t* vals, int64_t m) {
+    if (m <= 1) return;
+    uint64_t all_or = 0, all_and = ~0ull;
+    for (int64_t i = 0; i < m; ++i) {
+        all_or |= (uint64_t)keys[i];
+        all_and &= (uint64_t)keys[i];
+    }
+    const uint64_t varying = all_or ^ all_and;
+    int64_t* k2 = (int64_t*)malloc(sizeof(int64_t) * (size_t)m);
+    int32_t* v2 = (int32_t*)malloc(sizeof(int32_t) * (size_t)m);
+    int64_t *ks = keys, *kd = k2;
+    int32_t *vs = vals, *vd = v2;
+    for (int pass = 0; pass < 8; ++pass) {
+        const int sh = 8 * pass;
+        if (!((varying >> sh) & 255u)) continue;
+        int64_t cnt[257];
+        memset(cnt, 0, sizeof(cnt));
+        for (int64_t i = 0; i < m; ++i) cnt[(((uint64_t)ks[i]) >> sh & 255u) + 1]++;
+        for (int d = 0; d < 256; ++d) cnt[d + 1] += cnt[d];
+        for (int64_t i = 0; i < m; ++i) {
+            int64_t dst = cnt[((uint64_t)ks[i]) >> sh & 255u]++;
+            kd[dst] = ks[i];
+            vd[dst] = vs[i];
+        }
+        int64_t* tk = ks; ks = kd; kd = tk;
+        int32_t* tv = vs; vs = vd; vd = tv;
+    }
+    if (ks != keys) {
+        memcpy(keys, ks, sizeof(int64_t) * (size_t)m);
+        memcpy(vals, vs, sizeof(int32_t) * (size_t)m);
+    }
+    free(k2);
+    free(v2);
+}
+
+/* _tile_bin_edges_64bit, splax/_rasterize/_sort/_kernels.py:244-269 (same M == 1 behaviour). */
+static void tile_bin_edges64(const int64_t* sorted_keys, int64_t M, int32_t num_tiles,
+                             int32_t tile_bits, int32_t* bins) {
+    const int64_t mask = ((int64_t)1 << tile_bits) - 1;
+    for (int64_t idx = 0; idx < M; ++idx) {
+        int64_t key = (int64_t)((uint64_t)sorted_keys[idx] >> 32);
+        int32_t cur = (int32_t)(key >> tile_bits) * num_tiles + (int32_t)(key & mask);
+        if (idx == 0) {
+            bins[2 * cur] = 0;
+            continue;
+        }
+        if (idx == M - 1) bins[2 * cur + 1] = (int32_t)M;
+        int64_t kp = (int64_t)((uint64_t)sorted_keys[idx - 1] >> 32);
+        int32_t prev = (int32_t)(kp >> tile_bits) * num_tiles + (int32_t)(kp & mask);
+        if (prev != cur) {
+            bins[2 * prev + 1] = (int32_t)idx;
+            bins[2 * cur] = (int32_t)idx;
+        }
+    }
+}
+
+/* sort_and_bin, 64-bit key path (splax/_rasterize/_sort/_sort.py:143-170) */
+int64_t oracle_sort_and_bin_wide(const float* xys, const float* depths, const int32_t* radii,
+                                 const float* conics, const float* map_opac,
+                                 int64_t rows_map_opac, const int32_t* cum, int32_t n, int32_t B,
+                                 int32_t img_h, int32_t img_w, int64_t* sorted_keys,
+                                 int32_t* sorted_ids, int64_t cap, int32_t* tile_bins) {
+    int32_t L[6];
+    oracle_key_layout(B, img_h, img_w, L);
+    if (L[3] + L[4] > 32) return -2;
+    memset(tile_bins, 0, sizeof(int32_t) * 2 * (size_t)B * (size_t)L[2]);
+    int64_t M = oracle_emit_keys_wide(xys, depths, radii, conics, map_opac, rows_map_opac, cum,
+                                      n, B, img_h, img_w, sorted_keys, sorted_ids, cap);
+    if (M <= 0) return M;
+    radix_sort_pairs64(sorted_keys, sorted_ids, M);
+    tile_bin_edges64(sorted_keys, M, L[2], L[3], tile_bins);
+    return M;
+}
+
+/* Sorted ids and bins through whichever key the layout takes (ids [cap], bins [B*tiles*2]). */
+static int64_t sort_ids_and_bins(const float* xys, const float* depths, const int32_t* radii,
+                                 const float* conics, const float* map_opac,
+                                 int64_t rows_map_opac, const int32_t* cum, int32_t n, int32_t B,
+                                 int32_t img_h, int32_t img_w, int32_t* ids, int64_t cap,
+                                 int32_t* bins);
+
 /* sort_and_bin, splax/_rasterize/_sort/_sort.py:29-171 (packed 32-bit key path) */
 int64_t oracle_sort_and_bin(const float* xys, const float* depths, const int32_t* radii,
                             const float* conics, const float* map_opac, int64_t rows_map_opac,
@@ -590,13 +733,35 @@ int64_t oracle_sort_and_bin(const float* xys, const float* depths, const int32_t
                             int32_t img_w, int32_t* sorted_keys, int32_t* sorted_ids,
                             int64_t cap, int32_t* tile_bins) {
     int32_t L[6];
-    if (!oracle_key_layout(B, img_h, img_w, L)) return -2;
+    if (!oracle_key_layout(B, img_h, img_w, L) || g_force_wide) return -2;
     memset(tile_bins, 0, sizeof(int32_t) * 2 * (size_t)B * (size_t)L[2]);
     int64_t M = oracle_emit_keys(xys, depths, radii, conics, map_opac, rows_map_opac, cum, n, B,
                                  img_h, img_w, sorted_keys, sorted_ids, cap, NULL);
     if (M <= 0) return M;
     radix_sort_pairs(sorted_keys, sorted_ids, M);
     tile_bin_edges(sorted_keys, M, L[2], L[3], L[5], tile_bins);
+    return M;
+}
+
+static int64_t sort_ids_and_bins(const float* xys, const float* depths, const int32_t* radii,
+                                 const float* conics, const float* map_opac,
+                                 int64_t rows_map_opac, const int32_t* cum, int32_t n, int32_t B,
+                                 int32_t img_h, int32_t img_w, int32_t* ids, int64_t cap,
+                                 int32_t* bins) {
+    const int mode = oracle_key_mode(B, img_h, img_w);
+    if (mode < 0) return mode;
+    const size_t m = (size_t)(cap > 0 ? cap : 1);
+    if (mode == 0) {
+        int32_t* keys = (int32_t*)malloc(sizeof(int32_t) * m);
+        int64_t M = oracle_sort_and_bin(xys, depths, radii, conics, map_opac, rows_map_opac, cum,
+                                        n, B, img_h, img_w, keys, ids, cap, bins);
+        free(keys);
+        return M;
+    }
+    int64_t* keys = (int64_t*)malloc(sizeof(int64_t) * m);
+    int64_t M = oracle_sort_and_bin_wide(xys, depths, radii, conics, map_opac, rows_map_opac,
+                                         cum, n, B, img_h, img_w, keys, ids, cap, bins);
+    free(keys);
     return M;
 }
 
@@ -682,19 +847,17 @@ int64_t oracle_rasterize_fwd(const float* colors, int64_t rows_colors, const flo
                              int32_t img_w, float* final_Ts, int32_t* final_idx, float* out_img,
                              int64_t* stats, float* out_depth) {
     int32_t L[6];
-    if (!oracle_key_layout(B, img_h, img_w, L)) return -2;
+    oracle_key_layout(B, img_h, img_w, L);
     const int64_t total = (int64_t)B * n;
     const int64_t M = total > 0 ? cum[total - 1] : 0;
-    int32_t* keys = (int32_t*)malloc(sizeof(int32_t) * (size_t)(M > 0 ? M : 1));
     int32_t* ids = (int32_t*)malloc(sizeof(int32_t) * (size_t)(M > 0 ? M : 1));
     int32_t* bins = (int32_t*)malloc(sizeof(int32_t) * 2 * (size_t)B * (size_t)L[2]);
-    int64_t m = oracle_sort_and_bin(xys, depths, radii, conics, map_opac, rows_map_opac, cum, n,
-                                    B, img_h, img_w, keys, ids, M, bins);
+    int64_t m = sort_ids_and_bins(xys, depths, radii, conics, map_opac, rows_map_opac, cum, n, B,
+                                  img_h, img_w, ids, M, bins);
     if (m >= 0)
         oracle_blend_fwd(colors, rows_colors, opacities, rows_opac, background, rows_bg, xys,
                          conics, ids, bins, B, img_h, img_w, final_Ts, final_idx, out_img, stats,
                          depths, out_depth);
-    free(keys);
     free(ids);
     free(bins);
     return m;
@@ -721,15 +884,14 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
     const int with_depth = v_depths != NULL;
     const int NG = with_depth ? 10 : 9;
     int32_t L[6];
-    if (!oracle_key_layout(B_geom, img_h, img_w, L)) return -2;
+    oracle_key_layout(B_geom, img_h, img_w, L);
     const int32_t tbx = L[0], num_tiles = L[2];
     const int64_t total = (int64_t)B_geom * n;
     const int64_t M = total > 0 ? cum[total - 1] : 0;
-    int32_t* keys = (int32_t*)malloc(sizeof(int32_t) * (size_t)(M > 0 ? M : 1));
     int32_t* ids = (int32_t*)malloc(sizeof(int32_t) * (size_t)(M > 0 ? M : 1));
     int32_t* bins = (int32_t*)malloc(sizeof(int32_t) * 2 * (size_t)B_geom * (size_t)num_tiles);
-    int64_t m = oracle_sort_and_bin(xys, depths, radii, conics, map_opac, rows_map_opac, cum, n,
-                                    B_geom, img_h, img_w, keys, ids, M, bins);
+    int64_t m = sort_ids_and_bins(xys, depths, radii, conics, map_opac, rows_map_opac, cum, n,
+                                  B_geom, img_h, img_w, ids, M, bins);
     const int64_t nout = (int64_t)B_out * n;
     double* acc = (double*)calloc((size_t)(nout > 0 ? nout : 1) * NG, sizeof(double));
     const int sel_geom = B_geom > 1, sel_bg = rows_bg > 1;
@@ -842,7 +1004,6 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
         stats[1] = qr;
     }
     free(acc);
-    free(keys);
     free(ids);
     free(bins);
     return m;

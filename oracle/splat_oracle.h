@@ -39,6 +39,23 @@ int oracle_project_fwd(const float* means3d, int64_t rows_means, const float* sc
                        float clip_thresh, float* xys, float* depths, int32_t* radii,
                        float* conics, int32_t* num_tiles_hit, int32_t* cum_tiles_hit);
 
+/* Force the 64-bit key for every layout (the reference's tests patch _use_32bit_keys,
+ * splax/_rasterize/_sort/_sort.py:23-26, the same way). */
+void oracle_set_wide_keys(int force);
+/* 0: packed 32-bit key; 1: 64-bit key; -2: image + tile bits above 32 (overflow). */
+int oracle_key_mode(int32_t B, int32_t img_h, int32_t img_w);
+
+/* 64-bit key path of sort_and_bin: emission-order keys, and sorted keys / ids / bins. */
+int64_t oracle_emit_keys_wide(const float* xys, const float* depths, const int32_t* radii,
+                              const float* conics, const float* map_opac, int64_t rows_map_opac,
+                              const int32_t* cum, int32_t n, int32_t B, int32_t img_h,
+                              int32_t img_w, int64_t* keys, int32_t* ids, int64_t cap);
+int64_t oracle_sort_and_bin_wide(const float* xys, const float* depths, const int32_t* radii,
+                                 const float* conics, const float* map_opac,
+                                 int64_t rows_map_opac, const int32_t* cum, int32_t n, int32_t B,
+                                 int32_t img_h, int32_t img_w, int64_t* sorted_keys,
+                                 int32_t* sorted_ids, int64_t cap, int32_t* tile_bins);
+
 /* Emission order (unsorted) keys and ids, exactly num_tiles_hit per visible item at cum[idx-1].
  * Returns the number of emitted keys, or a negative code (-2: key does not pack). */
 int64_t oracle_emit_keys(const float* xys, const float* depths, const int32_t* radii,

@@ -40,6 +40,7 @@ _SIGS = {
     + [_vp, _vp, _vp, _i64] + [_vp, _i64] + [_i32] * 5 + [_vp] * 5,
     "splat_sort_and_bin": [_vp] + [_vp] * 4 + [_vp, _i64, _vp] + [_i32] * 4
     + [_vp, _vp, _i64, _vp, _vp],
+    "splat_set_wide_keys": [_i32],
     "splat_clear_cache": [],
     "splat_last_error": [],
     "splat_set_stage_timing": [_i32],
@@ -132,6 +133,12 @@ def stage_times() -> dict[str, tuple[float, int]]:
     calls = (ctypes.c_int64 * len(STAGES))()
     check(lib().splat_get_stage_times(ms, calls, len(STAGES)), "stage_times")
     return {s: (ms[i], calls[i]) for i, s in enumerate(STAGES)}
+
+
+def set_wide_keys(force: bool) -> None:
+    """Make every sort take the 64-bit key (the reference's tests patch _use_32bit_keys,
+    splax/_rasterize/_sort/_sort.py:23-26, the same way)."""
+    lib().splat_set_wide_keys(int(bool(force)))
 
 
 def check_device() -> int:

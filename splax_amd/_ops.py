@@ -233,7 +233,8 @@ def rasterize_bwd(colors, opac, map_opac, background, xys, depths, radii, conics
 
 
 def sort_and_bin(xys, depths, radii, conics, map_opac, cum, *, n, B, img_shape, capacity=None):
-    """splax/_rasterize/_sort/_sort.py:29-171: sorted keys, sorted gaussian ids, tile bins."""
+    """splax/_rasterize/_sort/_sort.py:29-171: sorted keys (int64; packed keys widened), sorted
+    gaussian ids, tile bins."""
     xys, depths, conics, map_opac = map(_f32, (xys, depths, conics, map_opac))
     radii, cum = _i32(radii), _i32(cum)
     dev = _lib.require_gpu(xys, depths, radii, conics, map_opac, cum)
@@ -241,7 +242,7 @@ def sort_and_bin(xys, depths, radii, conics, map_opac, cum, *, n, B, img_shape, 
     tiles = ((W + 15) // 16) * ((H + 15) // 16)
     if capacity is None:
         capacity = int(cum.reshape(-1)[-1].item()) if cum.numel() else 0
-    keys = torch.empty((max(capacity, 1),), device=dev, dtype=torch.int32)
+    keys = torch.empty((max(capacity, 1),), device=dev, dtype=torch.int64)
     ids = torch.empty((max(capacity, 1),), device=dev, dtype=torch.int32)
     bins = torch.empty((B * tiles, 2), device=dev, dtype=torch.int32)
     m = torch.zeros(1, dtype=torch.int64)

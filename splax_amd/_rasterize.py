@@ -16,30 +16,30 @@ from splax_amd._project import resolve_batch
 
 
 def key_layout(B: int, H: int, W: int) -> dict:
-    """Fields of the packed 32-bit sort key (splax/_rasterize/_sort/_sort.py:51-60)."""
+    """Fields of the sort key (splax/_rasterize/_sort/_sort.py:51-66): the packed 32-bit key when
+    at least 16 depth bits remain, else the 64-bit key, which overflows past 32 image + tile bits.
+    """
     tx, ty = (W + 15) // 16, (H + 15) // 16
     nt = tx * ty
     tile_bits = (nt - 1).bit_length()
     image_bits = (B - 1).bit_length()
     depth_bits = 31 - image_bits - tile_bits
+    packed = depth_bits >= 16
     return {"tiles_x": tx, "tiles_y": ty, "num_tiles": nt, "tile_bits": tile_bits,
-            "image_bits": image_bits, "depth_bits": depth_bits, "packed": depth_bits >= 16}
+            "image_bits": image_bits, "depth_bits": depth_bits, "packed": packed,
+            "overflow": not packed and image_bits + tile_bits > 32}
 
 
 def check_key_fits(B: int, H: int, W: int) -> None:
-    """Raise like the reference when the batch / resolution cannot be keyed.
-
-    The reference falls back to a 64-bit key when fewer than 16 depth bits remain and raises
-    ValueError only when even that overflows (splax/_rasterize/_sort/_sort.py:61-66). The 64-bit
-    key path is not built here, so every non-packable layout raises.
-    """
+    """Raise like the reference when even the 64-bit key cannot hold the image and tile ids
+    (splax/_rasterize/_sort/_sort.py:61-66)."""
     lay = key_layout(B, H, W)
-    if not lay["packed"]:
+    if lay["overflow"]:
+        upper = lay["image_bits"] + lay["tile_bits"]
         raise ValueError(
-            f"intersection key does not pack into 32 bits: image_n_bits({lay['image_bits']}) + "
-            f"tile_n_bits({lay['tile_bits']}) leaves {lay['depth_bits']} < 16 depth bits "
-            f"(batch B={B}, n_tiles={lay['num_tiles']}); the 64-bit key path is not built yet. "
-            "Reduce batch size or resolution.")
+            f"batched intersection key overflow: image_n_bits({lay['image_bits']}) + "
+            f"tile_n_bits({lay['tile_bits']}) = {upper} > 32 (batch B={B}, "
+            f"n_tiles={lay['num_tiles']}). Reduce batch size or resolution.")
 
 
 class _RasterizeFn(torch.autograd.Function):

@@ -38,6 +38,12 @@ __global__ void fill_zero_i32_kernel(int32_t* p, int64_t n) {
         p[i] = 0;
 }
 
+__global__ void widen_i32_kernel(const int32_t* a, int64_t* b, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        b[i] = a[i];
+}
+
 static unsigned fill_blocks(int64_t n) {
     int64_t b = (n + 255) / 256;
     return (unsigned)std::max<int64_t>(1, std::min<int64_t>(b, 4096));
@@ -86,7 +92,7 @@ static void dev_free(T** p) {
 int DeviceScratch::ensure_base() {
     if (tickets) return 0;
     int rc = dev_alloc(&tickets, kNumTickets, true);
-    if (!rc) rc = dev_alloc(&hist, 4 * 256, true);
+    if (!rc) rc = dev_alloc(&hist, kMaxPasses * 256, true);
     if (!rc) rc = dev_alloc(&scan_status, 4096, true);
     if (rc) return rc;
     scan_status_cap = 4096;
@@ -113,7 +119,7 @@ int DeviceScratch::grow_scan_status(int64_t blocks) {
     return 0;
 }
 
-int DeviceScratch::ensure_sort(int64_t M, int64_t bins, int32_t B) {
+int DeviceScratch::ensure_sort(int64_t M, int64_t bins, int32_t B, bool wide) {
     const int64_t sort_tile = 256 * 8;  // keys per onesweep partition (sort.hip kSortTile)
     const int64_t mm_blocks = 2 * (int64_t)B * 4096;  // generous partial capacity bound below
     bool need_sync = true;
@@ -140,6 +146,15 @@ int DeviceScratch::ensure_sort(int64_t M, int64_t bins, int32_t B) {
         }
         if (rc) return rc;
         isect_cap = cap;
+    }
+    if (wide && M > wide_cap) {
+        sync_once();
+        for (int k = 0; k < 2; ++k) dev_free(&wkeys[k]);
+        wide_cap = 0;
+        const int64_t cap = (int64_t)(M * 1.25) + 1;
+        for (int k = 0; k < 2 && !rc; ++k) rc = dev_alloc(&wkeys[k], cap, false);
+        if (rc) return rc;
+        wide_cap = cap;
     }
     const int64_t parts = (M + sort_tile - 1) / sort_tile;
     if (parts * 256 > sort_status_cap) {
@@ -210,8 +225,10 @@ void DeviceScratch::release() {
         dev_free(&keys[k]);
         dev_free(&vals[k]);
         dev_free(&gids[k]);
+        dev_free(&wkeys[k]);
     }
     isect_cap = 0;
+    wide_cap = 0;
     dev_free(&rgrad);
     rgrad_cap = 0;
     dev_free(&sort_status);
@@ -299,7 +316,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 3; }
+int splat_abi_version(void) { return 4; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();
@@ -463,11 +480,16 @@ static int check_raster(const RasterInputs& in, int32_t B_out) {
     return 0;
 }
 
+int splat_set_wide_keys(int force) {
+    set_force_wide_keys(force != 0);
+    return 0;
+}
+
 int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* depths,
                        const int32_t* radii, const float* conics, const float* map_opacities,
                        int64_t rows_map_opac, const int32_t* cum_tiles_hit,
                        int32_t num_gaussians, int32_t B, int32_t img_h, int32_t img_w,
-                       int32_t* sorted_keys, int32_t* sorted_ids, int64_t capacity,
+                       int64_t* sorted_keys, int32_t* sorted_ids, int64_t capacity,
                        int32_t* tile_bins, int64_t* num_intersects) {
     RasterInputs in{};
     in.colors = nullptr; in.rows_colors = num_gaussians;
@@ -490,19 +512,27 @@ int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* dep
     if (rc) return rc;
     int64_t M = 0;
     KeyLayout L;
-    rc = run_sort_and_bin(in, sc, s, &M, &L);
+    SortOutputs o;
+    rc = run_sort_and_bin(in, sc, s, &M, &L, nullptr, &o);
     if (num_intersects) *num_intersects = M;
     if (rc) return rc;
     if (M > capacity) return fail(kErrTooMany, "sort_and_bin: capacity below intersection count");
     const int64_t nb = 2 * (int64_t)B * L.num_tiles;
-    if (hipMemcpyAsync(tile_bins, sc.tile_bins, nb * sizeof(int32_t), hipMemcpyDeviceToDevice,
-                       s) != hipSuccess)
+    if (hipMemcpyAsync(tile_bins, o.bins, nb * sizeof(int32_t), hipMemcpyDeviceToDevice, s) !=
+        hipSuccess)
         return fail(kErrRuntime, "bins copy failed");
     if (M > 0) {
-        if (hipMemcpyAsync(sorted_keys, sc.keys[0], M * sizeof(int32_t), hipMemcpyDeviceToDevice,
-                           s) != hipSuccess ||
-            hipMemcpyAsync(sorted_ids, sc.gids[0], M * sizeof(int32_t), hipMemcpyDeviceToDevice,
-                           s) != hipSuccess)
+        if (o.wide) {
+            if (hipMemcpyAsync(sorted_keys, o.keys, M * sizeof(int64_t), hipMemcpyDeviceToDevice,
+                               s) != hipSuccess)
+                return fail(kErrRuntime, "sorted copy failed");
+        } else {
+            hipLaunchKernelGGL(widen_i32_kernel, dim3(fill_blocks(M)), dim3(256), 0, s,
+                               static_cast<const int32_t*>(o.keys), sorted_keys, M);
+            if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "key copy failed");
+        }
+        if (hipMemcpyAsync(sorted_ids, o.ids, M * sizeof(int32_t), hipMemcpyDeviceToDevice, s) !=
+            hipSuccess)
             return fail(kErrRuntime, "sorted copy failed");
     }
     return 0;
@@ -544,11 +574,12 @@ static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortT
     if (rc) return rc;
     int64_t M = 0;
     KeyLayout L;
-    rc = run_sort_and_bin(in, sc, s, &M, &L, tgt);
+    SortOutputs o;
+    rc = run_sort_and_bin(in, sc, s, &M, &L, tgt, &o);
     if (num_intersects) *num_intersects = M;
     if (rc) return rc;
-    const int32_t* ids = (tgt && tgt->ids) ? tgt->ids : sc.gids[0];
-    const int32_t* bins = (tgt && tgt->bins) ? tgt->bins : sc.tile_bins;
+    const int32_t* ids = o.ids;
+    const int32_t* bins = o.bins;
     StageTimer tm(s, kStageBlendFwd);
     rc = launch_blend_fwd(in, L, M > 0 ? ids : nullptr, bins, final_Ts, final_idx, out_img,
                           out_depth, s);
@@ -585,7 +616,7 @@ static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptL
     int64_t M = 0;
     if (kept) {
         L = key_layout(in.B_geom, in.img_h, in.img_w);
-        if (!L.packed) return fail(kErrKeyOverflow, "rasterize_bwd: key does not pack");
+        if (L.overflow) return fail(kErrKeyOverflow, "rasterize_bwd: intersection key overflow");
         ids = kept->ids;
         pos = kept->pos;
         bins = kept->bins;
@@ -594,11 +625,12 @@ static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptL
         const int32_t bpi = (in.n + 4095) / 4096;
         rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * in.B_geom);
         if (rc) return rc;
-        rc = run_sort_and_bin(in, sc, s, &M, &L);
+        SortOutputs o;
+        rc = run_sort_and_bin(in, sc, s, &M, &L, nullptr, &o);
         if (rc) return rc;
-        ids = sc.gids[0];
-        pos = sc.vals[0];
-        bins = sc.tile_bins;
+        ids = o.ids;
+        pos = o.pos;
+        bins = o.bins;
     }
     const int64_t images = in.B_geom > 1 ? 1 : args.B_out;
     rc = sc.ensure_rgrad(images * M * (args.v_depths ? 10 : 9));

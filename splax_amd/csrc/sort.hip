@@ -123,9 +123,13 @@ struct EmitParams {
     const int32_t* cum; const float* mm;
     int32_t n; int64_t total; int64_t M;
     int32_t tiles_x, tiles_y, tile_bits, depth_bits;
-    int32_t* keys; int32_t* owner;
+    void* keys; int32_t* owner;
 };
 
+// kWide: the 64-bit key of _map_intersects_64bit (splax/_rasterize/_sort/_kernels.py:156-211),
+// (image << (32 + tile_bits)) | (tile << 32) | the depth's raw float bits (int32, widened with
+// sign extension). Otherwise the packed key image | tile | quantized depth.
+template <bool kWide>
 __global__ void __launch_bounds__(256) emit_keys_kernel(EmitParams P) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= P.total) return;
@@ -134,16 +138,22 @@ __global__ void __launch_bounds__(256) emit_keys_kernel(EmitParams P) {
     int64_t cur = idx > 0 ? P.cum[idx - 1] : 0;
     // a consistent (radii, conics, cum) never leaves [0, M); inconsistent inputs stop here
     if (cur < 0) return;
-    const float dmin = P.mm[2 * bid];
-    const float drange = P.mm[2 * bid + 1] - dmin;
-    const int32_t qmax = (1 << P.depth_bits) - 1;
-    const float maxq = (float)qmax;
-    int32_t dq = 0;
-    if (drange > 0.0f) {
-        float f = (P.depths[idx] - dmin) / drange;
-        dq = iminw(imaxw(f2i(f * maxq), 0), qmax);
+    int32_t dq = 0, iid_enc = 0;
+    uint64_t wide_base = 0;
+    if constexpr (kWide) {
+        const int64_t depth_id = (int64_t)__float_as_int(P.depths[idx]);
+        wide_base = ((uint64_t)(uint32_t)bid << (32 + P.tile_bits)) | (uint64_t)depth_id;
+    } else {
+        const float dmin = P.mm[2 * bid];
+        const float drange = P.mm[2 * bid + 1] - dmin;
+        const int32_t qmax = (1 << P.depth_bits) - 1;
+        const float maxq = (float)qmax;
+        if (drange > 0.0f) {
+            float f = (P.depths[idx] - dmin) / drange;
+            dq = iminw(imaxw(f2i(f * maxq), 0), qmax);
+        }
+        iid_enc = (int32_t)((uint32_t)bid << (P.depth_bits + P.tile_bits));
     }
-    const int32_t iid_enc = (int32_t)((uint32_t)bid << (P.depth_bits + P.tile_bits));
     const float opac = P.map_opac[idx % P.rows_map_opac];
     const float t = iso_level(opac);
     const float2 c = reinterpret_cast<const float2*>(P.xys)[idx];
@@ -158,7 +168,11 @@ __global__ void __launch_bounds__(256) emit_keys_kernel(EmitParams P) {
         for (int32_t v = mn; v < mx; ++v) {
             if (cur >= P.M) return;
             int32_t tile_id = e.isY ? u * P.tiles_x + v : v * P.tiles_x + u;
-            P.keys[cur] = iid_enc | (tile_id << P.depth_bits) | dq;
+            if constexpr (kWide)
+                static_cast<uint64_t*>(P.keys)[cur] =
+                    wide_base | ((uint64_t)(uint32_t)tile_id << 32);
+            else
+                static_cast<int32_t*>(P.keys)[cur] = iid_enc | (tile_id << P.depth_bits) | dq;
             P.owner[cur] = (int32_t)idx;
             ++cur;
         }
@@ -168,25 +182,32 @@ __global__ void __launch_bounds__(256) emit_keys_kernel(EmitParams P) {
 // ------------------------------------------------------------------ digit histogram
 
 constexpr int kHistThreads = 256;
-// Workgroups of the histogram launch: each takes one contiguous chunk and adds its 4 x 256 counts
-// with one global atomic per non-zero bin. Same-address device-scope atomics serialise, so the
-// grid is kept small; 128 chunks still spread the read over half the CUs.
+// Workgroups of the histogram launch: each takes one contiguous chunk and adds its per-pass
+// 256-bin counts with one global atomic per non-zero bin. Same-address device-scope atomics
+// serialise, so the grid is kept small; 128 chunks still spread the read over half the CUs.
 constexpr int kHistBlocks = 128;
 constexpr int kHistChunkAlign = kHistThreads * 4;  // chunk starts stay 16-byte aligned
 
-__device__ __forceinline__ void hist_add(uint32_t* h, uint32_t k) {
-    atomicAdd(&h[k & 255u], 1u);
-    atomicAdd(&h[256 + ((k >> 8) & 255u)], 1u);
-    atomicAdd(&h[512 + ((k >> 16) & 255u)], 1u);
-    atomicAdd(&h[768 + (k >> 24)], 1u);
+// The digits a sort visits: 8-bit digits at these shifts (packed key: 0, 8, 16, 24).
+struct PassShifts {
+    int32_t n;
+    int32_t shift[kMaxPasses];
+};
+
+template <typename K, int kPasses>
+__device__ __forceinline__ void hist_add(uint32_t* h, K k, const PassShifts& ps) {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p)
+        if (p < ps.n) atomicAdd(&h[p * 256 + (uint32_t)((k >> ps.shift[p]) & 255u)], 1u);
 }
 
+template <typename K, int kPasses>
 __global__ void __launch_bounds__(kHistThreads)
-digit_hist_kernel(const int32_t* keys, int64_t M, int64_t chunk, uint32_t* hist, int32_t* bins,
-                  int64_t nbins2) {
-    __shared__ uint32_t s_h[kHistThreads / 64][4 * 256];
+digit_hist_kernel(const K* keys, int64_t M, int64_t chunk, PassShifts ps, uint32_t* hist,
+                  int32_t* bins, int64_t nbins2) {
+    __shared__ uint32_t s_h[kHistThreads / 64][kPasses * 256];
     const int tid = threadIdx.x, wave = tid >> 6;
-    for (int i = tid; i < 4 * 256; i += kHistThreads)
+    for (int i = tid; i < kPasses * 256; i += kHistThreads)
 #pragma unroll
         for (int w = 0; w < kHistThreads / 64; ++w) s_h[w][i] = 0u;
     // tile bins start at (0, 0): the bin-edge launch writes only tiles that own intersections
@@ -198,31 +219,31 @@ digit_hist_kernel(const int32_t* keys, int64_t M, int64_t chunk, uint32_t* hist,
     const int64_t hi = lo + chunk < M ? lo + chunk : M;
     uint32_t* h = s_h[wave];
     // whole 16-byte groups, four in flight per thread
-    const int64_t nvec = hi > lo ? (hi - lo) >> 2 : 0;
-    const int4* kv = reinterpret_cast<const int4*>(keys + lo);
+    constexpr int kPer = 16 / sizeof(K);
+    const int64_t nvec = hi > lo ? (hi - lo) / kPer : 0;
+    const uint4* kv = reinterpret_cast<const uint4*>(keys + lo);
     int64_t v = tid;
     for (; v + 3 * kHistThreads < nvec; v += 4 * kHistThreads) {
-        int4 q[4];
+        uint4 q[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) q[u] = kv[v + u * kHistThreads];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            hist_add(h, (uint32_t)q[u].x);
-            hist_add(h, (uint32_t)q[u].y);
-            hist_add(h, (uint32_t)q[u].z);
-            hist_add(h, (uint32_t)q[u].w);
+            const K* e = reinterpret_cast<const K*>(&q[u]);
+#pragma unroll
+            for (int x = 0; x < kPer; ++x) hist_add<K, kPasses>(h, e[x], ps);
         }
     }
     for (; v < nvec; v += kHistThreads) {
-        const int4 q = kv[v];
-        hist_add(h, (uint32_t)q.x);
-        hist_add(h, (uint32_t)q.y);
-        hist_add(h, (uint32_t)q.z);
-        hist_add(h, (uint32_t)q.w);
+        const uint4 q = kv[v];
+        const K* e = reinterpret_cast<const K*>(&q);
+#pragma unroll
+        for (int x = 0; x < kPer; ++x) hist_add<K, kPasses>(h, e[x], ps);
     }
-    for (int64_t i = lo + 4 * nvec + tid; i < hi; i += kHistThreads) hist_add(h, (uint32_t)keys[i]);
+    for (int64_t i = lo + kPer * nvec + tid; i < hi; i += kHistThreads)
+        hist_add<K, kPasses>(h, keys[i], ps);
     __syncthreads();
-    for (int i = tid; i < 4 * 256; i += kHistThreads) {
+    for (int i = tid; i < kPasses * 256; i += kHistThreads) {
         uint32_t c = 0;
 #pragma unroll
         for (int w = 0; w < kHistThreads / 64; ++w) c += s_h[w][i];
@@ -263,14 +284,16 @@ __device__ __forceinline__ uint32_t block_exclusive_scan_256(uint32_t v, uint32_
 
 // Two values travel with each key: its emission position and the flat item that emitted it.
 // The first pass generates the positions (vals_in == nullptr gives value = position) and reads
-// the items in emission order, so no pass gathers at random.
+// the items in emission order, so no pass gathers at random. K is the key word (uint32_t for the
+// packed key, uint64_t for the 64-bit key, ordered as unsigned).
+template <typename K>
 __global__ void __launch_bounds__(kSortThreads)
-onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
-                     const int32_t* __restrict__ ids_in, int32_t* __restrict__ keys_out,
+onesweep_pass_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
+                     const int32_t* __restrict__ ids_in, K* __restrict__ keys_out,
                      int32_t* __restrict__ vals_out, int32_t* __restrict__ ids_out, int64_t M,
                      int shift, const uint32_t* __restrict__ hist, uint64_t* status,
                      uint32_t epoch, uint32_t* err) {
-    __shared__ uint32_t s_keys[kSortTile];
+    __shared__ K s_keys[kSortTile];
     __shared__ uint32_t s_vals[kSortTile];
     __shared__ uint32_t s_ids[kSortTile];
     __shared__ uint32_t s_cnt[kSortWaves][256];
@@ -287,11 +310,12 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
     const int64_t wbase = base + (int64_t)wave * (kSortItems * 64);
 
     // keys and values are all loaded up front so their latencies overlap
-    uint32_t key[kSortItems], val[kSortItems], gid[kSortItems];
+    K key[kSortItems];
+    uint32_t val[kSortItems], gid[kSortItems];
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
         int64_t pos = wbase + i * 64 + lane;
-        key[i] = pos < M ? (uint32_t)keys_in[pos] : 0xffffffffu;
+        key[i] = pos < M ? keys_in[pos] : ~(K)0;
         val[i] = pos < M ? (vals_in ? (uint32_t)vals_in[pos] : (uint32_t)pos) : 0u;
         gid[i] = pos < M ? (uint32_t)ids_in[pos] : 0u;
     }
@@ -301,7 +325,7 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
     uint32_t rank[kSortItems];
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
-        const uint32_t d = (key[i] >> shift) & 255u;
+        const uint32_t d = (uint32_t)(key[i] >> shift) & 255u;
         uint64_t peers = ~0ull;
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
@@ -380,7 +404,7 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
     // keys and values into LDS at their partition-sorted slot
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
-        const uint32_t dd = (key[i] >> shift) & 255u;
+        const uint32_t dd = (uint32_t)(key[i] >> shift) & 255u;
         const uint32_t slot = s_local_start[dd] + s_cnt[wave][dd] + rank[i];
         s_keys[slot] = key[i];
         s_vals[slot] = val[i];
@@ -393,9 +417,9 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
     for (int r = 0; r < kSortItems; ++r) {
         const int j = r * kSortThreads + tid;
         if (j < valid) {
-            const uint32_t k = s_keys[j];
-            const int64_t dest = (int64_t)s_dest_base[(k >> shift) & 255u] + j;
-            keys_out[dest] = (int32_t)k;
+            const K k = s_keys[j];
+            const int64_t dest = (int64_t)s_dest_base[(uint32_t)(k >> shift) & 255u] + j;
+            keys_out[dest] = k;
             vals_out[dest] = (int32_t)s_vals[j];
             ids_out[dest] = (int32_t)s_ids[j];
         }
@@ -406,14 +430,29 @@ onesweep_pass_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restr
 // _tile_bin_edges_32bit, splax/_rasterize/_sort/_kernels.py:214-241 (including its M == 1
 // behaviour: index 0 writes only the start, so a lone bin stays [0, 0)).
 
+// kWide: _tile_bin_edges_64bit (splax/_rasterize/_sort/_kernels.py:244-269), the (image, tile)
+// field read from the high word.
+template <bool kWide>
+__device__ __forceinline__ int32_t key_bin(const void* keys, int64_t i, int32_t num_tiles,
+                                           int32_t tile_bits, int32_t depth_bits) {
+    if constexpr (kWide) {
+        const uint64_t k = static_cast<const uint64_t*>(keys)[i] >> 32;
+        const uint64_t mask = ((uint64_t)1 << tile_bits) - 1;
+        return (int32_t)(k >> tile_bits) * num_tiles + (int32_t)(k & mask);
+    } else {
+        const int32_t mask = (1 << tile_bits) - 1;
+        const int32_t k = static_cast<const int32_t*>(keys)[i] >> depth_bits;
+        return (k >> tile_bits) * num_tiles + (k & mask);
+    }
+}
+
+template <bool kWide>
 __global__ void __launch_bounds__(256)
-bin_edges_kernel(const int32_t* keys, int64_t M, int32_t num_tiles, int32_t tile_bits,
+bin_edges_kernel(const void* keys, int64_t M, int32_t num_tiles, int32_t tile_bits,
                  int32_t depth_bits, int64_t nbins, int32_t* bins) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= M) return;
-    const int32_t mask = (1 << tile_bits) - 1;
-    const int32_t key = keys[idx] >> depth_bits;
-    const int32_t cur = (key >> tile_bits) * num_tiles + (key & mask);
+    const int32_t cur = key_bin<kWide>(keys, idx, num_tiles, tile_bits, depth_bits);
     // keys emitted from consistent inputs always decode inside [0, nbins)
     if (cur < 0 || cur >= nbins) return;
     if (idx == 0) {
@@ -421,8 +460,7 @@ bin_edges_kernel(const int32_t* keys, int64_t M, int32_t num_tiles, int32_t tile
         return;
     }
     if (idx == M - 1) bins[2 * cur + 1] = (int32_t)M;
-    const int32_t kp = keys[idx - 1] >> depth_bits;
-    const int32_t prev = (kp >> tile_bits) * num_tiles + (kp & mask);
+    const int32_t prev = key_bin<kWide>(keys, idx - 1, num_tiles, tile_bits, depth_bits);
     if (prev != cur && prev >= 0 && prev < nbins) {
         bins[2 * prev + 1] = (int32_t)idx;
         bins[2 * cur] = (int32_t)idx;
@@ -430,6 +468,11 @@ bin_edges_kernel(const int32_t* keys, int64_t M, int32_t num_tiles, int32_t tile
 }
 
 // ------------------------------------------------------------------ orchestration
+
+// _use_32bit_keys (splax/_rasterize/_sort/_sort.py:23-26), which the reference's tests patch to
+// force the 64-bit key; here a process-wide switch (splat_set_wide_keys).
+static bool g_force_wide = false;
+void set_force_wide_keys(bool force) { g_force_wide = force; }
 
 KeyLayout key_layout(int32_t B, int32_t img_h, int32_t img_w) {
     KeyLayout L;
@@ -447,29 +490,44 @@ KeyLayout key_layout(int32_t B, int32_t img_h, int32_t img_w) {
     L.tile_bits = bit_length((int64_t)L.num_tiles - 1);
     L.image_bits = bit_length((int64_t)B - 1);
     L.depth_bits = 31 - L.image_bits - L.tile_bits;
-    L.packed = L.depth_bits >= 16;
+    L.packed = L.depth_bits >= 16 && !g_force_wide;
+    L.overflow = !L.packed && L.image_bits + L.tile_bits > 32;
     return L;
 }
 
 int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stream,
-                     int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt) {
+                     int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt,
+                     SortOutputs* out) {
     const int32_t B = in.B_geom;
     const KeyLayout L = key_layout(B, in.img_h, in.img_w);
     *lay_out = L;
-    if (!L.packed) {
+    if (L.overflow) {
         return fail(kErrKeyOverflow,
-                    "intersection key does not pack into 32 bits: image_n_bits(" +
+                    "batched intersection key overflow: image_n_bits(" +
                         std::to_string(L.image_bits) + ") + tile_n_bits(" +
-                        std::to_string(L.tile_bits) + ") leaves " + std::to_string(L.depth_bits) +
-                        " < 16 depth bits (batch B=" + std::to_string(B) +
-                        ", n_tiles=" + std::to_string(L.num_tiles) +
-                        "); the 64-bit key path is not built yet. Reduce batch size or resolution.");
+                        std::to_string(L.tile_bits) + ") = " +
+                        std::to_string(L.image_bits + L.tile_bits) + " > 32 (batch B=" +
+                        std::to_string(B) + ", n_tiles=" + std::to_string(L.num_tiles) +
+                        "). Reduce batch size or resolution.");
     }
+    const bool wide = !L.packed;
+    // the sort's digits: four bytes of the (quantized or raw float) depth, then for the 64-bit
+    // key the bytes of the (image, tile) field above bit 32
+    PassShifts ps;
+    ps.n = 0;
+    for (int b = 0; b < 4; ++b) ps.shift[ps.n++] = 8 * b;
+    if (wide)
+        for (int b = 0; b < (L.image_bits + L.tile_bits + 7) / 8; ++b) ps.shift[ps.n++] = 32 + 8 * b;
+    const int last_dst = ((ps.n - 1) & 1) ? 0 : 1;  // buffer the last pass writes
     const int64_t total = (int64_t)B * in.n;
     const int64_t nbins = (int64_t)B * L.num_tiles;
-    int rc = sc.ensure_sort(0, nbins, B);
+    int rc = sc.ensure_sort(0, nbins, B, wide);
     if (rc) return rc;
     int32_t* bins = (tgt && tgt->bins) ? tgt->bins : sc.tile_bins;
+    SortOutputs o;
+    o.bins = bins;
+    o.wide = wide;
+    if (out) *out = o;
     const bool known = tgt && tgt->M_known >= 0;
     if (total <= 0) {
         *M_out = 0;
@@ -482,10 +540,15 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
                                   hipMemcpyDeviceToHost, stream) != hipSuccess ||
                    hipEventRecord(sc.count_event, stream) != hipSuccess))
         return fail(kErrRuntime, "count readback enqueue failed");
-    const int32_t bpi = (int32_t)((in.n + kMmThreads * kMmItems - 1) / (kMmThreads * kMmItems));
-    if ((int64_t)bpi * B * 2 > sc.mm_partial_cap)
-        return fail(kErrRuntime, "depth-range partials not allocated");
-    {
+    if (wide) {
+        // the 64-bit key carries the raw depth: no depth range, only the histogram to clear
+        rc = fill_zero_i32(reinterpret_cast<int32_t*>(sc.hist), kMaxPasses * 256, stream);
+        if (rc) return rc;
+    } else {
+        const int32_t bpi =
+            (int32_t)((in.n + kMmThreads * kMmItems - 1) / (kMmThreads * kMmItems));
+        if ((int64_t)bpi * B * 2 > sc.mm_partial_cap)
+            return fail(kErrRuntime, "depth-range partials not allocated");
         StageTimer tm(stream, kStageMinmax);
         hipLaunchKernelGGL(minmax_partial_kernel, dim3(bpi, B), dim3(kMmThreads), 0, stream,
                            in.depths, in.radii, in.n, bpi, sc.mm_partial);
@@ -507,11 +570,17 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     if (tgt && tgt->capacity >= 0 && M > tgt->capacity)
         return fail(kErrTooMany, "sorted-list buffers hold " + std::to_string(tgt->capacity) +
                                      " intersections, " + std::to_string(M) + " needed");
-    rc = sc.ensure_sort(M, nbins, B);
+    rc = sc.ensure_sort(M, nbins, B, wide);
     if (rc) return rc;
     if (M == 0) return fill_zero_i32(bins, 2 * nbins, stream);
-    int32_t* ids_final = (tgt && tgt->ids) ? tgt->ids : sc.gids[0];
-    int32_t* pos_final = (tgt && tgt->pos) ? tgt->pos : sc.vals[0];
+    int32_t* ids_final = (tgt && tgt->ids) ? tgt->ids : sc.gids[last_dst];
+    int32_t* pos_final = (tgt && tgt->pos) ? tgt->pos : sc.vals[last_dst];
+    void* kbuf[2] = {wide ? (void*)sc.wkeys[0] : (void*)sc.keys[0],
+                     wide ? (void*)sc.wkeys[1] : (void*)sc.keys[1]};
+    o.keys = kbuf[last_dst];
+    o.ids = ids_final;
+    o.pos = pos_final;
+    if (out) *out = o;
 
     {
         StageTimer tm(stream, kStageEmit);
@@ -520,9 +589,12 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         E.map_opac = in.map_opac; E.rows_map_opac = in.rows_map_opac;
         E.cum = in.cum; E.mm = sc.depth_mm; E.n = in.n; E.total = total; E.M = M;
         E.tiles_x = L.tiles_x; E.tiles_y = L.tiles_y; E.tile_bits = L.tile_bits;
-        E.depth_bits = L.depth_bits; E.keys = sc.keys[0]; E.owner = sc.gids[0];
-        hipLaunchKernelGGL(emit_keys_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                           stream, E);
+        E.depth_bits = L.depth_bits; E.keys = kbuf[0]; E.owner = sc.gids[0];
+        const dim3 grid((unsigned)((total + 255) / 256));
+        if (wide)
+            hipLaunchKernelGGL(emit_keys_kernel<true>, grid, dim3(256), 0, stream, E);
+        else
+            hipLaunchKernelGGL(emit_keys_kernel<false>, grid, dim3(256), 0, stream, E);
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "emit launch failed");
     }
     {
@@ -530,29 +602,50 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         int64_t chunk = (M + kHistBlocks - 1) / kHistBlocks;
         chunk = (chunk + kHistChunkAlign - 1) / kHistChunkAlign * kHistChunkAlign;
         const int64_t hb = (M + chunk - 1) / chunk;
-        hipLaunchKernelGGL(digit_hist_kernel, dim3((unsigned)hb), dim3(kHistThreads), 0, stream,
-                           sc.keys[0], M, chunk, sc.hist, bins, 2 * nbins);
+        if (wide)
+            hipLaunchKernelGGL((digit_hist_kernel<uint64_t, kMaxPasses>), dim3((unsigned)hb),
+                               dim3(kHistThreads), 0, stream, sc.wkeys[0], M, chunk, ps,
+                               sc.hist, bins, 2 * nbins);
+        else
+            hipLaunchKernelGGL((digit_hist_kernel<uint32_t, 4>), dim3((unsigned)hb),
+                               dim3(kHistThreads), 0, stream,
+                               reinterpret_cast<const uint32_t*>(sc.keys[0]), M, chunk, ps,
+                               sc.hist, bins, 2 * nbins);
         const int64_t parts = (M + kSortTile - 1) / kSortTile;
-        // passes 0..3 ping-pong 0 -> 1 -> 0 -> 1 -> 0; the first pass generates the emission
-        // positions, the last writes positions and items straight into their final buffers
-        // (the caller's when it keeps the sorted lists)
-        for (int pass = 0; pass < 4; ++pass) {
+        // passes ping-pong 0 -> 1 -> 0 ...; the first pass generates the emission positions,
+        // the last writes positions and items straight into their final buffers (the caller's
+        // when it keeps the sorted lists)
+        for (int pass = 0; pass < ps.n; ++pass) {
             const int src = pass & 1, dst = 1 - src;
-            const bool last = pass == 3;
-            hipLaunchKernelGGL(onesweep_pass_kernel, dim3((unsigned)parts), dim3(kSortThreads), 0,
-                               stream, sc.keys[src], pass == 0 ? nullptr : sc.vals[src],
-                               sc.gids[src], sc.keys[dst], last ? pos_final : sc.vals[dst],
-                               last ? ids_final : sc.gids[dst], M, 8 * pass,
-                               sc.hist + 256 * pass, sc.sort_status, sc.next_epoch(),
-                               sc.tickets + kDeviceError);
+            const bool last = pass == ps.n - 1;
+            const int32_t* vin = pass == 0 ? nullptr : sc.vals[src];
+            int32_t* vout = last ? pos_final : sc.vals[dst];
+            int32_t* iout = last ? ids_final : sc.gids[dst];
+            if (wide)
+                hipLaunchKernelGGL(onesweep_pass_kernel<uint64_t>, dim3((unsigned)parts),
+                                   dim3(kSortThreads), 0, stream, sc.wkeys[src], vin,
+                                   sc.gids[src], sc.wkeys[dst], vout, iout, M, ps.shift[pass],
+                                   sc.hist + 256 * pass, sc.sort_status, sc.next_epoch(),
+                                   sc.tickets + kDeviceError);
+            else
+                hipLaunchKernelGGL(onesweep_pass_kernel<uint32_t>, dim3((unsigned)parts),
+                                   dim3(kSortThreads), 0, stream,
+                                   reinterpret_cast<const uint32_t*>(sc.keys[src]), vin,
+                                   sc.gids[src], reinterpret_cast<uint32_t*>(sc.keys[dst]), vout,
+                                   iout, M, ps.shift[pass], sc.hist + 256 * pass,
+                                   sc.sort_status, sc.next_epoch(), sc.tickets + kDeviceError);
         }
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "sort launch failed");
     }
     {
         StageTimer tm(stream, kStageBins);
-        hipLaunchKernelGGL(bin_edges_kernel, dim3((unsigned)((M + 255) / 256)), dim3(256), 0,
-                           stream, sc.keys[0], M, L.num_tiles, L.tile_bits, L.depth_bits,
-                           nbins, bins);
+        const dim3 grid((unsigned)((M + 255) / 256));
+        if (wide)
+            hipLaunchKernelGGL(bin_edges_kernel<true>, grid, dim3(256), 0, stream, o.keys, M,
+                               L.num_tiles, L.tile_bits, L.depth_bits, nbins, bins);
+        else
+            hipLaunchKernelGGL(bin_edges_kernel<false>, grid, dim3(256), 0, stream, o.keys, M,
+                               L.num_tiles, L.tile_bits, L.depth_bits, nbins, bins);
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "bins launch failed");
     }
     return 0;

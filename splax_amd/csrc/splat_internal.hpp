@@ -60,11 +60,18 @@ struct ProjectBwdArgs {
 };
 
 // Geometry of one sort_and_bin call (splax/_rasterize/_sort/_sort.py:51-60).
+// packed: the 32-bit key (at least 16 depth bits left); otherwise the 64-bit key, which
+// overflows when image + tile bits exceed 32 (splax/_rasterize/_sort/_sort.py:56-66).
 struct KeyLayout {
     int32_t tiles_x, tiles_y, num_tiles, tile_bits, image_bits, depth_bits;
-    bool packed;
+    bool packed, overflow;
 };
 KeyLayout key_layout(int32_t B, int32_t img_h, int32_t img_w);
+// Force the 64-bit key for every layout (the reference's tests patch _use_32bit_keys).
+void set_force_wide_keys(bool force);
+
+// Digit passes of the sort: at most 8 bytes of a 64-bit key.
+constexpr int kMaxPasses = 8;
 
 // Inputs of sort_and_bin and the blends.
 struct RasterInputs {
@@ -93,14 +100,16 @@ struct DeviceScratch {
     uint64_t* scan_status = nullptr; int64_t scan_status_cap = 0;
     uint32_t* tickets = nullptr;
     // sort
-    int32_t* keys[2] = {nullptr, nullptr};
+    int32_t* keys[2] = {nullptr, nullptr};   // packed 32-bit keys (ping-pong)
+    uint64_t* wkeys[2] = {nullptr, nullptr};  // 64-bit keys (ping-pong), allocated on first use
+    int64_t wide_cap = 0;
     int32_t* vals[2] = {nullptr, nullptr};  // emission positions (ping-pong)
     int32_t* gids[2] = {nullptr, nullptr};  // flat item ids (ping-pong; [0] ends sorted)
     int64_t isect_cap = 0;
     // backward: nine partial gradient sums per (output image, intersection), emission order
     float* rgrad = nullptr; int64_t rgrad_cap = 0;
     uint64_t* sort_status = nullptr; int64_t sort_status_cap = 0;  // partitions * 256
-    uint32_t* hist = nullptr;                                       // 4 * 256
+    uint32_t* hist = nullptr;                                       // kMaxPasses * 256
     int32_t* tile_bins = nullptr; int64_t bins_cap = 0;             // (start, end) pairs
     float* depth_mm = nullptr; int64_t mm_cap = 0;                  // 2 * B
     uint32_t* mm_partial = nullptr; int64_t mm_partial_cap = 0;     // 2 * blocks
@@ -114,7 +123,7 @@ struct DeviceScratch {
     }
     int ensure_base();
     int grow_scan_status(int64_t blocks);
-    int ensure_sort(int64_t M, int64_t bins, int32_t B);
+    int ensure_sort(int64_t M, int64_t bins, int32_t B, bool wide);
     int ensure_rgrad(int64_t count);
     void release();
 };
@@ -161,11 +170,20 @@ struct SortTargets {
     int32_t* bins = nullptr;
 };
 
-// sort_and_bin: returns M (>= 0) in *M_out; sorted keys in sc.keys[0]; sorted ids in tgt->ids or
-// sc.gids[0]; sorted emission positions in tgt->pos or sc.vals[0]; tile bins in tgt->bins or
-// sc.tile_bins.
+// Where sort_and_bin left its results: sorted keys (int32 when packed, uint64 when wide), ids,
+// emission positions (tgt's buffers when given) and bins.
+struct SortOutputs {
+    const void* keys = nullptr;
+    bool wide = false;
+    const int32_t* ids = nullptr;
+    const int32_t* pos = nullptr;
+    const int32_t* bins = nullptr;
+};
+
+// sort_and_bin: returns M (>= 0) in *M_out and the result locations in *out.
 int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stream,
-                     int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt = nullptr);
+                     int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt,
+                     SortOutputs* out);
 
 // out_depth non-null: also the expected-depth channel (in.depths per geometry item).
 int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,

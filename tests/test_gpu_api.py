@@ -316,3 +316,27 @@ def test_render_depth_batched_equals_sequential():
         summed = sum(s[2][k].astype(np.float64) for s in singles)
         r = rel_fro(bg[k], summed)
         assert r < 1e-5, f"batched depth/{k}: {r:.2e}"
+
+
+def test_wide_keys_batch_equals_stack_bit_exact():
+    """With the 64-bit key each image's (tile, depth) order does not depend on B, so a batched
+    render equals the per-camera renders bit for bit (the reference's tests/test_warp_batch.py
+    forces the 64-bit key for exactly this, :45-56)."""
+    _case("wide keys batch == stack")
+    from splax_amd import _lib
+
+    n, H, W = 3000, 96, 96
+    sc = random_scene(n, H, W, seed=14)
+    vms = np.stack([sc["vm"]] * 3)
+    vms[1, 0, 3] += 0.2
+    vms[2, 1, 3] -= 0.2
+    args = [_t(sc[k]) for k in ("means", "scales", "quats", "colors", "opac")]
+    common = dict(background=_t(sc["bg"]), img_shape=(H, W), f=sc["f"], c=sc["c"])
+    _lib.set_wide_keys(True)
+    try:
+        bimg, _ = splax_amd.render(*args, viewmat=_t(vms), **common)
+        singles = [splax_amd.render(*args, viewmat=_t(vms[b]), **common)[0] for b in range(3)]
+    finally:
+        _lib.set_wide_keys(False)
+    for b in range(3):
+        assert_bit_exact(_np(bimg[b]), _np(singles[b]), f"wide batch/img[{b}]")

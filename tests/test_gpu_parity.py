@@ -391,3 +391,87 @@ def test_rasterize_depth_bwd_matches_oracle(name):
     for label, g, k, r in zip(labels, got, kept, refs):
         _grad_compare(_np(g).reshape(r.shape), r, f"{name}/{label}")
         _grad_compare(_np(k).reshape(r.shape), r, f"{name}/{label} (kept lists)")
+
+
+# ---------------------------------------------------------------- 64-bit key path
+
+
+@pytest.fixture
+def wide_keys():
+    from splax_amd import _lib
+
+    _lib.set_wide_keys(True)
+    O.set_wide_keys(True)
+    yield
+    _lib.set_wide_keys(False)
+    O.set_wide_keys(False)
+
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg2_50k"])
+def test_wide_keys_sort_render_and_grads(name, wide_keys):
+    """The 64-bit key (splax/_rasterize/_sort/_sort.py:143-170) forced, as the reference's tests
+    do: keys / ids / bins and the forward bit-exact against the oracle, gradients in
+    tolerance."""
+    _case(f"wide keys {name}")
+    s = _scene_arrays(name)
+    xys, depths, radii, conics, nth, cum = _raster_inputs(s)
+    rk, rid, rbins = O.sort_and_bin(xys, depths, radii, conics, s.opacities, cum, n=s.n, B=1,
+                                    img_shape=s.img_shape)
+    assert rk.dtype == np.int64
+    gk, gid, gbins = _ops.sort_and_bin(_t(xys), _t(depths), _t(radii), _t(conics),
+                                       _t(s.opacities).reshape(-1), _t(cum), n=s.n, B=1,
+                                       img_shape=s.img_shape)
+    torch.cuda.synchronize()
+    assert_bit_exact(_np(gk), rk, f"{name}/wide keys")
+    assert_bit_exact(_np(gid), rid, f"{name}/wide ids")
+    assert_bit_exact(_np(gbins), rbins, f"{name}/wide bins")
+    rimg, rT, ridx, _, M = O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background, xys,
+                                           depths, radii, conics, cum, n=s.n, B=1,
+                                           img_shape=s.img_shape)
+    o = _t(s.opacities).reshape(-1)
+    geo = (_t(xys), _t(depths), _t(radii), _t(conics), _t(cum))
+    gimg, gT, gidx, gM = _ops.rasterize_fwd(_t(s.colors), o, o, _t(s.background), *geo, n=s.n,
+                                            B=1, img_shape=s.img_shape)
+    torch.cuda.synchronize()
+    assert gM == M
+    assert_bit_exact(_np(gimg), rimg, f"{name}/wide img")
+    assert_bit_exact(_np(gidx), ridx, f"{name}/wide final_idx")
+    H, W = s.img_shape
+    vout = (2.0 * (rimg.reshape(H, W, 3) - s.targets[0]) / rimg.size).astype(np.float32)
+    ref = O.rasterize_bwd(s.colors, s.opacities, s.opacities, s.background, xys, depths, radii,
+                          conics, cum, rT, ridx, vout, n=s.n, B_out=1, B_geom=1,
+                          img_shape=s.img_shape)
+    got = _ops.rasterize_bwd(_t(s.colors), o, o, _t(s.background), *geo, _t(rT), _t(ridx),
+                             _t(vout).reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
+                             img_shape=s.img_shape)
+    for label, g, r in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), got, ref[:4]):
+        _grad_compare(_np(g).reshape(r.shape), r, f"{name}/wide {label}")
+
+
+def test_wide_key_fallback_eight_cameras_1080p():
+    """B=8 at 1920x1080 leaves 15 depth bits: the sort falls back to the 64-bit key by itself
+    (the reference's tests/test_warp_rasterize.py:321-359) and matches the oracle bit for bit."""
+    _case("wide key fallback B=8 1080p")
+    s = make_scene(2, n=20_000)
+    B, n = 8, s.n
+    from splax_amd.utils import look_at
+
+    ang = np.linspace(0, 2 * np.pi, B, endpoint=False)
+    eyes = np.stack([8 * np.sin(ang), 0.5 * np.cos(3 * ang), 8 * np.cos(ang)], -1)
+    vms = look_at(eyes, np.zeros(3), up=(0, 1, 0)).astype(np.float32)
+    assert O.key_mode(B, *s.img_shape) == 1
+    q = np.roll(s.quats, -1, axis=-1)
+    proj = O.project_fwd(s.means, s.scales, q, vms.reshape(-1, 4), s.opacities, n=n, total=B * n,
+                         img_shape=s.img_shape, f=s.f, c=s.c)
+    xys, depths, radii, conics, nth, cum = proj
+    rimg, rT, ridx, _, M = O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background, xys,
+                                           depths, radii, conics, cum, n=n, B=B,
+                                           img_shape=s.img_shape)
+    o = _t(s.opacities).reshape(-1)
+    gimg, gT, gidx, gM = _ops.rasterize_fwd(_t(s.colors), o, o, _t(s.background), _t(xys),
+                                            _t(depths), _t(radii), _t(conics), _t(cum), n=n, B=B,
+                                            img_shape=s.img_shape)
+    torch.cuda.synchronize()
+    assert gM == M > 0
+    assert_bit_exact(_np(gimg), rimg, "B=8 1080p/img")
+    assert_bit_exact(_np(gidx), ridx, "B=8 1080p/final_idx")

@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(handle, name), f"{name} declared in include/splat_hip.h but not exported"
     assert set(names) == set(_lib._SIGS), "Python binding and header disagree"
     lib = _lib.lib()
-    assert lib.splat_abi_version() == 3
+    assert lib.splat_abi_version() == 4
     assert isinstance(lib.splat_last_error(), bytes)
 
 
@@ -96,8 +96,11 @@ def test_key_layout_and_overflow_error():
     assert key_layout(16, 512, 512)["depth_bits"] == 17
     assert key_layout(4, 1060, 1600)["packed"]
     check_key_fits(4, 1060, 1600)
-    with pytest.raises(ValueError, match="64-bit key path"):
-        check_key_fits(8, 1080, 1920)
+    lay = key_layout(8, 1080, 1920)  # 15 depth bits: the 64-bit key, which fits
+    assert not lay["packed"] and not lay["overflow"]
+    check_key_fits(8, 1080, 1920)
+    with pytest.raises(ValueError, match="key overflow"):
+        check_key_fits(1 << 20, 1080, 1920)  # 20 image + 13 tile bits
 
 
 def test_scenes_deterministic_and_shaped():

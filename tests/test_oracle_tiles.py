@@ -160,3 +160,98 @@ def test_single_intersection_bin_quirk():
     sk, sid, bins = O.sort_and_bin(xys, depths, radii, conics, opac, cum, n=1, B=1,
                                    img_shape=(H, W))
     assert (bins == 0).all()
+
+
+# ---------------------------------------------------------------- 64-bit key path
+# splax/_rasterize/_sort/_sort.py:23-26,56-66,143-170 and _sort/_kernels.py:156-211,244-269.
+
+
+@pytest.fixture
+def wide_keys():
+    O.set_wide_keys(True)
+    yield
+    O.set_wide_keys(False)
+
+
+def test_key_mode_fallback_and_overflow():
+    """B=1 at 1080p packs (18 depth bits); B=8 leaves 15 < 16 and falls back to the 64-bit key
+    (the reference's tests/test_warp_rasterize.py:321-359); image + tile bits above 32 overflow."""
+    assert O.key_mode(1, 1080, 1920) == 0
+    assert O.key_mode(8, 1080, 1920) == 1
+    assert O.key_mode(16, 512, 512) == 0  # config 3: 17 depth bits
+    assert O.key_mode(1 << 20, 1080, 1920) == -2  # 20 image + 13 tile bits
+    O.set_wide_keys(True)
+    try:
+        assert O.key_mode(1, 1080, 1920) == 1
+    finally:
+        O.set_wide_keys(False)
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_wide_keys_fields_sort_and_bins(B, wide_keys):
+    sc = random_scene(6000, 144, 176, seed=10 + B)
+    n = 6000
+    vms = np.stack([sc["vm"]] * B)
+    for b in range(B):
+        vms[b, 0, 3] += 0.1 * b
+    xys, depths, radii, conics, nth, cum = _project(sc, B=B, vms=vms)
+    H, W = sc["img_shape"]
+    lay, _ = O.key_layout(B, H, W)
+    ek, eid, _ = O.emit_keys(xys, depths, radii, conics, sc["opac"], cum, n=n, B=B,
+                             img_shape=(H, W))
+    assert ek.dtype == np.int64 and ek.size == int(cum[-1])
+    # fields: image and tile above bit 32, the float depth's bits below
+    hi = (ek.view(np.uint64) >> np.uint64(32)).astype(np.int64)
+    tb = lay["tile_n_bits"]
+    np.testing.assert_array_equal(hi >> tb, eid // n)
+    np.testing.assert_array_equal((ek & 0xFFFFFFFF).astype(np.uint32),
+                                  depths.ravel()[eid].view(np.uint32))
+    sk, sid, bins = O.sort_and_bin(xys, depths, radii, conics, sc["opac"], cum, n=n, B=B,
+                                   img_shape=(H, W))
+    order = np.lexsort((eid, ek.view(np.uint64)))  # (key as unsigned, flat index)
+    np.testing.assert_array_equal(sk, ek[order])
+    np.testing.assert_array_equal(sid, eid[order])
+    # within a tile, the order is by exact depth
+    ref = _bins_closed_form(hi[order], B, lay["num_tiles"], 0, tb)
+    np.testing.assert_array_equal(bins, ref)
+
+
+def test_wide_and_packed_renders_agree():
+    """The 64-bit key orders by exact depth, the packed key by quantized depth; the images
+    agree within the reference's bound (tests/test_warp_rasterize.py:280-318: max abs < 0.05,
+    PSNR > 65 dB)."""
+    sc = random_scene(20000, 128, 128, seed=21, scale_range=(0.01, 0.05))
+    n = 20000
+    xys, depths, radii, conics, nth, cum = _project(sc)
+    H, W = sc["img_shape"]
+    args = (sc["colors"], sc["opac"], sc["opac"], np.ones(3, np.float32), xys, depths, radii,
+            conics, cum)
+    packed = O.rasterize_fwd(*args, n=n, B=1, img_shape=(H, W))[0]
+    O.set_wide_keys(True)
+    try:
+        wide = O.rasterize_fwd(*args, n=n, B=1, img_shape=(H, W))[0]
+    finally:
+        O.set_wide_keys(False)
+    d = np.abs(packed.astype(np.float64) - wide)
+    mse = float((d ** 2).mean())
+    psnr = 99.0 if mse == 0 else -10 * np.log10(mse)
+    assert d.max() < 0.05 and psnr > 65, (d.max(), psnr)
+
+
+def test_wide_batch_equals_stack_bit_exact(wide_keys):
+    """With the 64-bit key each image's (tile, depth) order does not depend on B, so a batched
+    render equals the per-image renders bit for bit (tests/test_warp_batch.py:45-56)."""
+    sc = random_scene(3000, 96, 96, seed=5)
+    n, B = 3000, 3
+    vms = np.stack([sc["vm"]] * B)
+    vms[1, 0, 3] += 0.2
+    vms[2, 1, 3] -= 0.15
+    H, W = sc["img_shape"]
+    xys, depths, radii, conics, nth, cum = _project(sc, B=B, vms=vms)
+    bimg = O.rasterize_fwd(sc["colors"], sc["opac"], sc["opac"], sc["bg"], xys, depths, radii,
+                           conics, cum, n=n, B=B, img_shape=(H, W))[0].reshape(B, H, W, 3)
+    for b in range(B):
+        p = _project(sc, B=1, vms=vms[b:b + 1])
+        img = O.rasterize_fwd(sc["colors"], sc["opac"], sc["opac"], sc["bg"], *p[:4], p[5],
+                              n=n, B=1, img_shape=(H, W))[0].reshape(H, W, 3)
+        np.testing.assert_array_equal(bimg[b], img)
