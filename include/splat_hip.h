@@ -126,8 +126,10 @@ int splat_rasterize_depth_bwd(splat_stream_t stream, const float* colors, int64_
  * intersection's emission position (its index in the cum_tiles_hit-ordered emission sequence).
  * num_intersects receives M. When M > capacity the call returns status 6 after the count
  * readback, with M reported and nothing written; the caller retries with larger buffers.
- * out_depth (may be NULL) selects the depth channel as in splat_rasterize_depth_fwd. Other
- * arguments and outputs as splat_rasterize_fwd. */
+ * out_depth (may be NULL) selects the depth channel as in splat_rasterize_depth_fwd. records
+ * (may be NULL) receives the packed blend record of every geometry item, 16 floats per item
+ * ([B*num_gaussians, 16], 16-byte aligned), for splat_rasterize_bwd_sorted; it is written only
+ * when M > 0. Other arguments and outputs as splat_rasterize_fwd. */
 int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t rows_colors,
                              const float* opacities, int64_t rows_opac,
                              const float* map_opacities, int64_t rows_map_opac,
@@ -137,20 +139,23 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
                              int32_t img_h, int32_t img_w, int64_t capacity, float* final_Ts,
                              int32_t* final_idx, float* out_img, float* out_depth,
                              int32_t* sorted_ids, int32_t* sorted_pos, int32_t* tile_bins,
-                             int64_t* num_intersects);
+                             float* records, int64_t* num_intersects);
 
 /* Backward over the sorted lists kept by splat_rasterize_fwd_keep (no re-sort). Arguments as
- * splat_rasterize_bwd plus sorted_ids / sorted_pos / tile_bins / num_intersects of the matching
- * forward; the outputs equal splat_rasterize_bwd's (same kernels; additions can differ in order
- * only among a tile's four quadrant waves). v_depths (may be NULL) selects the depth channel as
- * in splat_rasterize_depth_bwd (then depths and v_out_depth are read). */
+ * splat_rasterize_bwd plus sorted_ids / sorted_pos / tile_bins / records / num_intersects of
+ * the matching forward (records may be NULL: the backward then packs them again from its
+ * inputs, which must be the forward's); the outputs equal splat_rasterize_bwd's (same kernels;
+ * additions can differ in order only among a tile's four quadrant waves). v_depths (may be NULL)
+ * selects the depth channel as in splat_rasterize_depth_bwd (then depths and v_out_depth are
+ * read). */
 int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64_t rows_colors,
                                const float* opacities, int64_t rows_opac,
                                const float* background, int64_t rows_bg, const float* xys,
                                const float* depths, const float* conics,
                                const int32_t* cum_tiles_hit, const int32_t* sorted_ids,
                                const int32_t* sorted_pos, const int32_t* tile_bins,
-                               int64_t num_intersects, const float* final_Ts,
+                               const float* records, int64_t num_intersects,
+                               const float* final_Ts,
                                const int32_t* final_idx, const float* v_out_img,
                                int64_t vout_rows, const float* v_out_depth, int64_t vdepth_rows,
                                int32_t num_gaussians, int32_t B_out, int32_t B_geom,

@@ -8,6 +8,7 @@ operands' device and enqueues the library call on torch's current stream of that
 from __future__ import annotations
 
 import ctypes
+from typing import NamedTuple, Optional
 
 import torch
 
@@ -124,10 +125,21 @@ def rasterize_fwd(colors, opac, map_opac, background, xys, depths, radii, conics
 _KEEP_CAPACITY: dict = {}  # per device: capacity estimate for the kept sorted lists
 
 
+class KeptSort(NamedTuple):
+    """What rasterize_fwd_keep leaves for rasterize_bwd_sorted: the sorted gaussian ids, their
+    emission positions, the tile bins, the intersection count and the packed blend records
+    ([B*n, 16], or None to have the backward pack them again)."""
+    ids: torch.Tensor
+    pos: torch.Tensor
+    bins: torch.Tensor
+    M: int
+    records: Optional[torch.Tensor]
+
+
 def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, conics, cum, *, n,
                        B, img_shape, render_depth=False):
-    """Forward that also returns the sorted gaussian ids, their emission positions and the tile
-    bins (kept for the backward); returns (img, Ts, fidx, ids, pos, bins, M, depth or None).
+    """Forward that also keeps the sorted lists and packed records for the backward; returns
+    (img, Ts, fidx, KeptSort, depth or None).
 
     The buffers are sized from a per-device estimate (1.25x the largest count seen), so the host
     does not wait for the intersection count before launching: the library reads it itself while
@@ -145,6 +157,7 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
     img = torch.empty((B * H, W, 3), device=dev, dtype=torch.float32)
     depth = torch.empty((B * H, W), device=dev, dtype=torch.float32) if render_depth else None
     bins = torch.empty((B * tiles, 2), device=dev, dtype=torch.int32)
+    recs = torch.empty((xys.shape[0], 16), device=dev, dtype=torch.float32)
     key = str(dev)
     cap = _KEEP_CAPACITY.get(key, 0)
     m = ctypes.c_int64(0)
@@ -157,7 +170,7 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
                 _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
                 p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys),
                 p(depths), p(radii), p(conics), p(cum), n, B, H, W, cap, p(Ts), p(fidx), p(img),
-                p(depth), p(ids), p(pos), p(bins), ctypes.byref(m))
+                p(depth), p(ids), p(pos), p(bins), p(recs), ctypes.byref(m))
         if st == _lib.ERR_TOO_MANY and m.value > cap:
             cap = int(m.value * 1.25) + 1
             _KEEP_CAPACITY[key] = cap
@@ -167,7 +180,7 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
     M = int(m.value)
     if M > _KEEP_CAPACITY.get(key, 0):
         _KEEP_CAPACITY[key] = int(M * 1.25) + 1
-    return img, Ts, fidx, ids, pos, bins, M, depth
+    return img, Ts, fidx, KeptSort(ids, pos, bins, M, recs), depth
 
 
 def _bwd_outputs(nout, dev, with_depth):
@@ -175,14 +188,18 @@ def _bwd_outputs(nout, dev, with_depth):
     return f(nout, 3), f(nout), f(nout, 2), f(nout, 3), (f(nout) if with_depth else None)
 
 
-def rasterize_bwd_sorted(colors, opac, background, xys, depths, conics, cum, ids, pos, bins, M,
+def rasterize_bwd_sorted(colors, opac, background, xys, depths, conics, cum, kept: KeptSort,
                          final_Ts, final_idx, v_out, *, n, B_out, B_geom, img_shape,
                          v_out_depth=None):
-    """Backward over the sorted lists of rasterize_fwd_keep (no re-sort); with v_out_depth also
-    the depth channel's v_depths (last)."""
+    """Backward over the sorted lists (and records) of rasterize_fwd_keep for the same inputs
+    (no re-sort); with v_out_depth also the depth channel's v_depths (last)."""
     colors, opac, background, xys, depths, conics, final_Ts, v_out = map(
         _f32, (colors, opac, background, xys, depths, conics, final_Ts, v_out))
-    cum, ids, pos, bins, final_idx = _i32(cum), _i32(ids), _i32(pos), _i32(bins), _i32(final_idx)
+    ids, pos, bins, M = _i32(kept.ids), _i32(kept.pos), _i32(kept.bins), kept.M
+    recs = None if kept.records is None else _f32(kept.records)
+    if recs is not None and recs.shape != (xys.shape[0], 16):
+        raise ValueError(f"records must be [{xys.shape[0]}, 16], got {tuple(recs.shape)}")
+    cum, final_idx = _i32(cum), _i32(final_idx)
     vd = None if v_out_depth is None else _f32(v_out_depth)
     dev = _lib.require_gpu(colors, opac, xys, conics, cum, ids, pos, bins, final_Ts, final_idx,
                            v_out)
@@ -193,7 +210,8 @@ def rasterize_bwd_sorted(colors, opac, background, xys, depths, conics, cum, ids
         st = _lib.lib().splat_rasterize_bwd_sorted(
             _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
             p(background), rows(background, 3), p(xys), p(depths), p(conics), p(cum), p(ids),
-            p(pos), p(bins), M, p(final_Ts), p(final_idx), p(v_out), v_out.numel() // (3 * W),
+            p(pos), p(bins), p(recs), M, p(final_Ts), p(final_idx), p(v_out),
+            v_out.numel() // (3 * W),
             p(vd), 0 if vd is None else vd.numel() // W, n, B_out, B_geom, H, W, p(v_colors),
             p(v_opac), p(v_xy), p(v_conic), p(v_depths))
     _lib.check(st, "rasterize_bwd")

@@ -49,15 +49,15 @@ class _RasterizeFn(torch.autograd.Function):
         n, B, img_shape, render_depth = statics
         # The sorted lists stay resident for the backward (the reference re-sorts there,
         # splax/_rasterize/_kernels.py:422); the sort is deterministic, so both are identical.
-        img, Ts, fidx, ids, pos, bins, M, depth = _ops.rasterize_fwd_keep(
+        img, Ts, fidx, kept, depth = _ops.rasterize_fwd_keep(
             colors.reshape(-1, 3), opac.reshape(-1), map_opac.reshape(-1),
             background.reshape(-1, 3), xys.reshape(-1, 2), depths.reshape(-1), radii.reshape(-1),
             conics.reshape(-1, 3), cum.reshape(-1), n=n, B=B, img_shape=img_shape,
             render_depth=render_depth)
-        ctx.save_for_backward(colors, opac, background, xys, depths, conics, cum, Ts, fidx, ids,
-                              pos, bins)
+        ctx.save_for_backward(colors, opac, background, xys, depths, conics, cum, Ts, fidx,
+                              kept.ids, kept.pos, kept.bins, kept.records)
         ctx.statics = statics
-        ctx.num_intersects = M
+        ctx.num_intersects = kept.M
         ctx.set_materialize_grads(False)  # no zero tensors for the unused Ts / fidx grads
         if depth is None:
             depth = Ts.new_zeros(())  # placeholder output of the colour-only path
@@ -68,7 +68,7 @@ class _RasterizeFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, v_img, v_depth, _v_Ts, _v_idx):
-        colors, opac, background, xys, depths, conics, cum, Ts, fidx, ids, pos, bins = \
+        colors, opac, background, xys, depths, conics, cum, Ts, fidx, ids, pos, bins, recs = \
             ctx.saved_tensors
         n, B, img_shape, render_depth = ctx.statics
         H, W = img_shape
@@ -78,8 +78,9 @@ class _RasterizeFn(torch.autograd.Function):
             v_depth = torch.zeros((B * H, W), device=xys.device)
         grads = _ops.rasterize_bwd_sorted(
             colors.reshape(-1, 3), opac.reshape(-1), background.reshape(-1, 3),
-            xys.reshape(-1, 2), depths.reshape(-1), conics.reshape(-1, 3), cum.reshape(-1), ids,
-            pos, bins, ctx.num_intersects, Ts, fidx, v_img.reshape(-1, 3), n=n, B_out=B,
+            xys.reshape(-1, 2), depths.reshape(-1), conics.reshape(-1, 3), cum.reshape(-1),
+            _ops.KeptSort(ids, pos, bins, ctx.num_intersects, recs), Ts, fidx,
+            v_img.reshape(-1, 3), n=n, B_out=B,
             B_geom=B, img_shape=img_shape,
             v_out_depth=v_depth.reshape(-1, W) if render_depth else None)
         v_colors, v_opac, v_xy, v_conic = grads[:4]

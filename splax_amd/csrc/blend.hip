@@ -29,11 +29,8 @@ namespace splat {
 constexpr int kTile = 256;
 
 struct BlendCommon {
-    const float* colors; int64_t rows_colors;
-    const float* opac; int64_t rows_opac;
     const float* background; int64_t rows_bg;
-    const float* xys; const float* conics;
-    const float* depths;  // per geometry item; non-null only when the depth channel is rendered
+    const float4* recs;  // packed records, four float4 per geometry item (pack_records_kernel)
     const int32_t* ids; const int32_t* bins;
     int32_t img_h, img_w, tiles_x, num_tiles;
     int64_t total;  // geometry rows (B_geom * n): ids outside [0, total) are ignored
@@ -46,40 +43,91 @@ __device__ __forceinline__ void tile_pixel(int tid, int tile_x, int tile_y, int&
     j = tile_x * kBlockWidth + (wave & 1) * 8 + (lane & 7);
 }
 
-// sigma_max and the quadrant mask of one record for the tile at (tile_x, tile_y).
-__device__ __forceinline__ void stage_bounds(float x, float y, float a, float b, float c, float o,
-                                             int tile_x, int tile_y, float& smax,
-                                             uint32_t& qmask) {
-    if (o > 0.0f) {
-        smax = __logf(o * 255.0f) + 1e-3f;
-    } else {
-        smax = (o != o) ? __builtin_inff() : -__builtin_inff();
-    }
-    qmask = 0xfu;
-    if (!(smax >= 0.0f)) {  // every pixel rejected (NaN smax only for NaN opacity: keep all)
-        if (smax == smax) qmask = 0u;
-        return;
-    }
-    // Points beyond k times the bounding box of {sigma <= smax} have exact sigma >= k^2 smax.
-    // The evaluated sigma differs from the exact one by at most ~6e-7 * cond(Q) relative (Q the
-    // conic), so with cond(Q) <= (a + c)^2 / det < 1e4 and k = 1.01 every point outside the box
-    // evaluates above smax. Worse-conditioned conics keep all four quadrants.
-    const float det = a * c - b * b;
-    const float tr = a + c;
-    const float ex2 = 2.0f * smax * c / det, ey2 = 2.0f * smax * a / det;
-    if (a > 0.0f && c > 0.0f && det > 0.0f && tr * tr < 1e4f * det && ex2 < 1e30f &&
-        ey2 < 1e30f) {
-        const float ex = sqrtf(ex2) * 1.01f + 0.01f, ey = sqrtf(ey2) * 1.01f + 0.01f;
-        qmask = 0u;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float x0 = (float)(tile_x * kBlockWidth + (q & 1) * 8) + 0.5f;
-            const float y0 = (float)(tile_y * kBlockWidth + (q >> 1) * 8) + 0.5f;
-            const bool hit = (x + ex >= x0) && (x - ex <= x0 + 7.0f) && (y + ey >= y0) &&
-                             (y - ey <= y0 + 7.0f);
-            qmask |= hit ? (1u << q) : 0u;
+// Packed record of one geometry item, 64 bytes (one aligned segment per staged intersection):
+//   r0 = (x, y, a, b), r1 = (c, o, sigma_max, 0), r2 = (red, green, blue, depth),
+//   r3 = (ex, ey, cull mode, 0).
+// They depend only on the rasterizer's inputs, so a forward's records serve its backward.
+// sigma_max = log(255 o) + 1e-3 bounds sigma where o e^-sigma can still reach 1/255. The cull mode
+// says whether the tile-independent box (+-ex, +-ey) around the centre holds every pixel centre
+// with sigma <= sigma_max (kCullBox), or no pixel can pass (kCullNone: sigma_max < 0), or the box
+// cannot be trusted and every quadrant is kept (kCullKeep).
+enum : uint32_t { kCullBox = 0u, kCullKeep = 1u, kCullNone = 2u };
+
+struct PackParams {
+    const float* colors; int64_t rows_colors;
+    const float* opac; int64_t rows_opac;
+    const float* xys; const float* conics; const float* depths;
+    int64_t total;
+    float4* recs;
+};
+
+// One thread per item computes its record; the block's records leave through LDS so that
+// consecutive lanes store consecutive float4s.
+__global__ void __launch_bounds__(256) pack_records_kernel(PackParams P) {
+    __shared__ float4 s_rec[4 * 256];
+    const int64_t base = (int64_t)blockIdx.x * 256;
+    const int64_t g = base + threadIdx.x;
+    if (g < P.total) {
+        const float2 xy = reinterpret_cast<const float2*>(P.xys)[g];
+        const float a = P.conics[3 * g], b = P.conics[3 * g + 1], c = P.conics[3 * g + 2];
+        const float o = P.opac[g % P.rows_opac];
+        const int64_t cg = g % P.rows_colors;
+        float smax;
+        if (o > 0.0f) {
+            smax = __logf(o * 255.0f) + 1e-3f;
+        } else {
+            smax = (o != o) ? __builtin_inff() : -__builtin_inff();
         }
+        uint32_t mode = kCullKeep;
+        float ex = 0.0f, ey = 0.0f;
+        if (!(smax >= 0.0f)) {
+            mode = kCullNone;  // every pixel rejected
+        } else {
+            // Points beyond k times the bounding box of {sigma <= smax} have exact
+            // sigma >= k^2 smax. The evaluated sigma differs from the exact one by at most
+            // ~6e-7 * cond(Q) relative (Q the conic), so with cond(Q) <= (a + c)^2 / det < 1e4
+            // and k = 1.01 every point outside the box evaluates above smax.
+            // Worse-conditioned conics keep all four quadrants.
+            const float det = a * c - b * b;
+            const float tr = a + c;
+            const float ex2 = 2.0f * smax * c / det, ey2 = 2.0f * smax * a / det;
+            if (a > 0.0f && c > 0.0f && det > 0.0f && tr * tr < 1e4f * det && ex2 < 1e30f &&
+                ey2 < 1e30f) {
+                ex = sqrtf(ex2) * 1.01f + 0.01f;
+                ey = sqrtf(ey2) * 1.01f + 0.01f;
+                mode = kCullBox;
+            }
+        }
+        float4* r = s_rec + 4 * threadIdx.x;
+        r[0] = make_float4(xy.x, xy.y, a, b);
+        r[1] = make_float4(c, o, smax, 0.0f);
+        r[2] = make_float4(P.colors[3 * cg], P.colors[3 * cg + 1], P.colors[3 * cg + 2],
+                           P.depths ? P.depths[g] : 0.0f);
+        r[3] = make_float4(ex, ey, __uint_as_float(mode), 0.0f);
     }
+    __syncthreads();
+    const int64_t left = P.total - base;
+    const int count = 4 * (int)(left < 256 ? left : 256);
+    float4* dst = P.recs + 4 * base;
+    for (int k = threadIdx.x; k < count; k += 256) dst[k] = s_rec[k];
+}
+
+// Quadrants of the tile at (tile_x, tile_y) whose pixel centres a packed record can reach.
+__device__ __forceinline__ uint32_t quadrant_mask(const float4& r0, const float4& r3,
+                                                  int tile_x, int tile_y) {
+    const uint32_t mode = __float_as_uint(r3.z);
+    if (mode == kCullNone) return 0u;
+    if (mode != kCullBox) return 0xfu;
+    uint32_t qmask = 0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float x0 = (float)(tile_x * kBlockWidth + (q & 1) * 8) + 0.5f;
+        const float y0 = (float)(tile_y * kBlockWidth + (q >> 1) * 8) + 0.5f;
+        const bool hit = (r0.x + r3.x >= x0) && (r0.x - r3.x <= x0 + 7.0f) &&
+                         (r0.y + r3.y >= y0) && (r0.y - r3.y <= y0 + 7.0f);
+        qmask |= hit ? (1u << q) : 0u;
+    }
+    return qmask;
 }
 
 // LDS record of one batch: r0 = (x, y, a, b), r1 = (c, o, sigma_max, quadrant mask bits),
@@ -102,16 +150,12 @@ __device__ __forceinline__ int stage_batch(const BlendCommon& C, BatchLds& L, in
     uint32_t qm = 0u;
     float4 r0 = make_float4(0.f, 0.f, 0.f, 0.f), r1 = r0, r2 = r0;
     if (live && g >= 0 && g < C.total) {
-        const float2 xy = reinterpret_cast<const float2*>(C.xys)[g];
-        const float a = C.conics[3 * g], b = C.conics[3 * g + 1], c = C.conics[3 * g + 2];
-        const float o = C.opac[g % C.rows_opac];
-        const int64_t cg = g % C.rows_colors;
-        float smax;
-        stage_bounds(xy.x, xy.y, a, b, c, o, tile_x, tile_y, smax, qm);
-        r0 = make_float4(xy.x, xy.y, a, b);
-        r1 = make_float4(c, o, smax, __uint_as_float(qm));
-        r2 = make_float4(C.colors[3 * cg], C.colors[3 * cg + 1], C.colors[3 * cg + 2],
-                         C.depths ? C.depths[g] : 0.0f);
+        const float4* rec = C.recs + 4 * g;
+        r0 = rec[0];
+        r1 = rec[1];
+        r2 = rec[2];
+        qm = quadrant_mask(r0, rec[3], tile_x, tile_y);
+        r1.w = __uint_as_float(qm);
     }
     L.r0[tid] = r0;
     L.r1[tid] = r1;
@@ -236,13 +280,24 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
     }
 }
 
+// Packs the records of the in.B_geom * in.n geometry items into recs.
+int launch_pack_records(const RasterInputs& in, float4* recs, hipStream_t stream) {
+    PackParams K;
+    K.colors = in.colors; K.rows_colors = in.rows_colors;
+    K.opac = in.opac; K.rows_opac = in.rows_opac;
+    K.xys = in.xys; K.conics = in.conics; K.depths = in.depths;
+    K.total = (int64_t)in.B_geom * in.n;
+    K.recs = recs;
+    if (K.total <= 0) return 0;
+    hipLaunchKernelGGL(pack_records_kernel, dim3((unsigned)((K.total + 255) / 256)), dim3(256),
+                       0, stream, K);
+    return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
+}
+
 static void fill_common(BlendCommon& c, const RasterInputs& in, const KeyLayout& lay,
                         const int32_t* sorted_ids, const int32_t* tile_bins) {
-    c.colors = in.colors; c.rows_colors = in.rows_colors;
-    c.opac = in.opac; c.rows_opac = in.rows_opac;
     c.background = in.background; c.rows_bg = in.rows_bg;
-    c.xys = in.xys; c.conics = in.conics;
-    c.depths = nullptr;
+    c.recs = nullptr;
     c.ids = sorted_ids; c.bins = tile_bins;
     c.img_h = in.img_h; c.img_w = in.img_w;
     c.tiles_x = lay.tiles_x; c.num_tiles = lay.num_tiles;
@@ -251,12 +306,13 @@ static void fill_common(BlendCommon& c, const RasterInputs& in, const KeyLayout&
 
 int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,
-                     float* out_img, float* out_depth, hipStream_t stream) {
+                     float* out_img, float* out_depth, const float4* recs,
+                     hipStream_t stream) {
     const int64_t blocks = (int64_t)in.B_geom * lay.num_tiles;
     if (blocks <= 0) return 0;
     BlendFwdParams P;
     fill_common(P.c, in, lay, sorted_ids, tile_bins);
-    P.c.depths = out_depth ? in.depths : nullptr;
+    P.c.recs = recs;
     P.final_Ts = final_Ts; P.final_idx = final_idx; P.out_img = out_img;
     P.out_depth = out_depth;
     if (out_depth)
@@ -525,7 +581,7 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
     if (blocks > 0 && sorted_ids != nullptr && a.M > 0) {
         BlendBwdParams P;
         fill_common(P.c, in, lay, sorted_ids, tile_bins);
-        P.c.depths = depth ? in.depths : nullptr;
+        P.c.recs = a.recs;
         P.final_Ts = a.final_Ts; P.final_idx = a.final_idx;
         P.v_out = a.v_out; P.vout_rows = a.vout_rows;
         P.n = in.n; P.sel_geom = sel_geom;

@@ -204,6 +204,18 @@ int DeviceScratch::ensure_rgrad(int64_t count) {
     return 0;
 }
 
+int DeviceScratch::ensure_recs(int64_t items) {
+    if (items <= recs_cap) return 0;
+    (void)hipDeviceSynchronize();
+    dev_free(&recs);
+    recs_cap = 0;
+    const int64_t cap = (int64_t)(items * 1.25) + 1;
+    int rc = dev_alloc(&recs, 4 * cap, false);
+    if (rc) return rc;
+    recs_cap = cap;
+    return 0;
+}
+
 static int ensure_minmax_partials(DeviceScratch& sc, int64_t count) {
     if (count <= sc.mm_partial_cap) return 0;
     (void)hipDeviceSynchronize();
@@ -231,6 +243,8 @@ void DeviceScratch::release() {
     wide_cap = 0;
     dev_free(&rgrad);
     rgrad_cap = 0;
+    dev_free(&recs);
+    recs_cap = 0;
     dev_free(&sort_status);
     sort_status_cap = 0;
     dev_free(&tile_bins);
@@ -316,7 +330,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 4; }
+int splat_abi_version(void) { return 5; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();
@@ -558,9 +572,11 @@ static RasterInputs raster_inputs(const float* colors, int64_t rows_colors,
 
 // Forward: sort_and_bin into the library scratch or the caller's kept lists (tgt), then the
 // blend; out_depth non-null adds the expected-depth channel.
+// records: caller buffer for the packed blend records (kept for the backward), or null for
+// library scratch.
 static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortTargets* tgt,
                               float* final_Ts, int32_t* final_idx, float* out_img,
-                              float* out_depth, int64_t* num_intersects) {
+                              float* out_depth, float* records, int64_t* num_intersects) {
     int rc = check_raster(in, in.B_geom);
     if (rc) return rc;
     if (out_depth && !in.depths) return fail(kErrArgs, "rasterize: depth channel needs depths");
@@ -580,16 +596,26 @@ static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortT
     if (rc) return rc;
     const int32_t* ids = o.ids;
     const int32_t* bins = o.bins;
+    float4* recs = reinterpret_cast<float4*>(records);
+    if (!recs) {
+        rc = sc.ensure_recs((int64_t)in.B_geom * in.n);
+        if (rc) return rc;
+        recs = sc.recs;
+    }
     StageTimer tm(s, kStageBlendFwd);
-    rc = launch_blend_fwd(in, L, M > 0 ? ids : nullptr, bins, final_Ts, final_idx, out_img,
-                          out_depth, s);
+    if (M > 0) rc = launch_pack_records(in, recs, s);
+    if (!rc)
+        rc = launch_blend_fwd(in, L, M > 0 ? ids : nullptr, bins, final_Ts, final_idx, out_img,
+                              out_depth, recs, s);
     if (rc) return fail(rc, "blend_fwd launch failed");
     return 0;
 }
 
-// Sorted lists kept from the forward (splat_rasterize_fwd_keep).
+// Sorted lists (and, when non-null, the packed records) kept from the forward
+// (splat_rasterize_fwd_keep).
 struct KeptLists {
     const int32_t* ids; const int32_t* pos; const int32_t* bins; int64_t M;
+    const float* records;
 };
 
 // Backward over kept sorted lists or, with kept == nullptr, over a fresh sort_and_bin.
@@ -633,13 +659,21 @@ static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptL
         bins = o.bins;
     }
     const int64_t images = in.B_geom > 1 ? 1 : args.B_out;
+    const float4* recs = kept ? reinterpret_cast<const float4*>(kept->records) : nullptr;
     rc = sc.ensure_rgrad(images * M * (args.v_depths ? 10 : 9));
+    if (!rc && !recs && M > 0) rc = sc.ensure_recs((int64_t)in.B_geom * in.n);
     if (rc) return rc;
     BlendBwdArgs a = args;
     a.sorted_pos = pos;
     a.M = M;
     a.rgrad = sc.rgrad;
     StageTimer tm(s, kStageBlendBwd);
+    if (!recs && M > 0) {
+        rc = launch_pack_records(in, sc.recs, s);
+        if (rc) return fail(rc, "pack_records launch failed");
+        recs = sc.recs;
+    }
+    a.recs = recs;
     rc = launch_blend_bwd(in, L, M > 0 ? ids : nullptr, bins, a, s);
     if (rc) return fail(rc, "blend_bwd launch failed");
     return 0;
@@ -671,7 +705,7 @@ int splat_rasterize_fwd(splat_stream_t stream, const float* colors, int64_t rows
                                           depths, radii, conics, cum_tiles_hit, num_gaussians, B,
                                           img_h, img_w);
     return rasterize_fwd_impl(static_cast<hipStream_t>(stream), in, nullptr, final_Ts,
-                              final_idx, out_img, nullptr, num_intersects);
+                              final_idx, out_img, nullptr, nullptr, num_intersects);
 }
 
 int splat_rasterize_depth_fwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
@@ -688,7 +722,7 @@ int splat_rasterize_depth_fwd(splat_stream_t stream, const float* colors, int64_
                                           depths, radii, conics, cum_tiles_hit, num_gaussians, B,
                                           img_h, img_w);
     return rasterize_fwd_impl(static_cast<hipStream_t>(stream), in, nullptr, final_Ts,
-                              final_idx, out_img, out_depth, num_intersects);
+                              final_idx, out_img, out_depth, nullptr, num_intersects);
 }
 
 int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t rows_colors,
@@ -700,7 +734,7 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
                              int32_t img_h, int32_t img_w, int64_t capacity, float* final_Ts,
                              int32_t* final_idx, float* out_img, float* out_depth,
                              int32_t* sorted_ids, int32_t* sorted_pos, int32_t* tile_bins,
-                             int64_t* num_intersects) {
+                             float* records, int64_t* num_intersects) {
     if (capacity < 0 || !tile_bins || (capacity > 0 && (!sorted_ids || !sorted_pos)))
         return fail(kErrArgs, "rasterize_fwd_keep: missing sorted-list buffers");
     const RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac,
@@ -713,7 +747,7 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
     tgt.pos = sorted_pos;
     tgt.bins = tile_bins;
     return rasterize_fwd_impl(static_cast<hipStream_t>(stream), in, &tgt, final_Ts, final_idx,
-                              out_img, out_depth, num_intersects);
+                              out_img, out_depth, records, num_intersects);
 }
 
 int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64_t rows_colors,
@@ -722,7 +756,8 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
                                const float* depths, const float* conics,
                                const int32_t* cum_tiles_hit, const int32_t* sorted_ids,
                                const int32_t* sorted_pos, const int32_t* tile_bins,
-                               int64_t num_intersects, const float* final_Ts,
+                               const float* records, int64_t num_intersects,
+                               const float* final_Ts,
                                const int32_t* final_idx, const float* v_out_img,
                                int64_t vout_rows, const float* v_out_depth, int64_t vdepth_rows,
                                int32_t num_gaussians, int32_t B_out, int32_t B_geom,
@@ -737,7 +772,7 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
                                           img_w);
     const BlendBwdArgs a = bwd_args(final_Ts, final_idx, v_out_img, vout_rows, B_out, v_colors,
                                     v_opacity, v_xy, v_conic, v_out_depth, vdepth_rows, v_depths);
-    const KeptLists kept{sorted_ids, sorted_pos, tile_bins, num_intersects};
+    const KeptLists kept{sorted_ids, sorted_pos, tile_bins, num_intersects, records};
     return rasterize_bwd_impl(static_cast<hipStream_t>(stream), in, &kept, a);
 }
 

@@ -108,6 +108,8 @@ struct DeviceScratch {
     int64_t isect_cap = 0;
     // backward: nine partial gradient sums per (output image, intersection), emission order
     float* rgrad = nullptr; int64_t rgrad_cap = 0;
+    // blends: packed per-item records (4 float4 each)
+    float4* recs = nullptr; int64_t recs_cap = 0;
     uint64_t* sort_status = nullptr; int64_t sort_status_cap = 0;  // partitions * 256
     uint32_t* hist = nullptr;                                       // kMaxPasses * 256
     int32_t* tile_bins = nullptr; int64_t bins_cap = 0;             // (start, end) pairs
@@ -125,6 +127,7 @@ struct DeviceScratch {
     int grow_scan_status(int64_t blocks);
     int ensure_sort(int64_t M, int64_t bins, int32_t B, bool wide);
     int ensure_rgrad(int64_t count);
+    int ensure_recs(int64_t items);
     void release();
 };
 
@@ -185,10 +188,14 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
                      int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt,
                      SortOutputs* out);
 
-// out_depth non-null: also the expected-depth channel (in.depths per geometry item).
+// Writes the packed blend record (4 float4) of each of the in.B_geom * in.n geometry items.
+int launch_pack_records(const RasterInputs& in, float4* recs, hipStream_t stream);
+
+// out_depth non-null: also the expected-depth channel (in.depths per geometry item). recs holds
+// the records written by launch_pack_records for the same inputs.
 int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,
-                     float* out_img, float* out_depth, hipStream_t stream);
+                     float* out_img, float* out_depth, const float4* recs, hipStream_t stream);
 
 // Backward over sorted lists of M intersections: sorted_ids / sorted_pos / tile_bins as produced
 // by sort_and_bin; in.cum gives each item's emission range; rgrad is scratch of
@@ -201,6 +208,7 @@ struct BlendBwdArgs {
     const int32_t* sorted_pos; int64_t M; float* rgrad;
     float* v_colors; float* v_opacity; float* v_xy; float* v_conic;
     const float* v_out_depth = nullptr; int64_t vdepth_rows = 0; float* v_depths = nullptr;
+    const float4* recs = nullptr;  // launch_pack_records output for the same inputs
 };
 int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, const BlendBwdArgs& a, hipStream_t stream);

@@ -299,8 +299,9 @@ def test_kept_sort_path_equals_resort_path(name):
     xys, depths, radii, conics, nth, cum = _raster_inputs(s)
     o = _t(s.opacities).reshape(-1)
     geo = (_t(xys), _t(depths), _t(radii), _t(conics), _t(cum))
-    img, Ts, fidx, ids, pos, bins, M, _ = _ops.rasterize_fwd_keep(
+    img, Ts, fidx, kept, _ = _ops.rasterize_fwd_keep(
         _t(s.colors), o, o, _t(s.background), *geo, n=s.n, B=1, img_shape=s.img_shape)
+    ids, pos, bins, M, recs = kept
     rk, rid, rbins = O.sort_and_bin(xys, depths, radii, conics, s.opacities, cum, n=s.n, B=1,
                                     img_shape=s.img_shape)
     assert M == rid.size
@@ -318,16 +319,31 @@ def test_kept_sort_path_equals_resort_path(name):
     H, W = s.img_shape
     vout = _t((2.0 * (rimg.reshape(H, W, 3) - s.targets[0]) / rimg.size).astype(np.float32))
     a = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[1], geo[3],
-                                  geo[4], ids, pos, bins, M, Ts, fidx, vout.reshape(-1, 3),
+                                  geo[4], kept, Ts, fidx, vout.reshape(-1, 3),
                                   n=s.n, B_out=1, B_geom=1, img_shape=s.img_shape)
     b = _ops.rasterize_bwd(_t(s.colors), o, o, _t(s.background), *geo, Ts, fidx,
                            vout.reshape(-1, 3), n=s.n, B_out=1, B_geom=1, img_shape=s.img_shape)
     a2 = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[1], geo[3],
-                                   geo[4], ids, pos, bins, M, Ts, fidx, vout.reshape(-1, 3),
-                                   n=s.n, B_out=1, B_geom=1, img_shape=s.img_shape)
+                                   geo[4], kept._replace(records=None), Ts, fidx,
+                                   vout.reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
+                                   img_shape=s.img_shape)
     for label, x, y, z in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), a, b, a2):
         _grad_compare(_np(x), _np(y), f"{name}/{label} kept vs re-sorted")
-        _grad_compare(_np(x), _np(z), f"{name}/{label} repeat")
+        _grad_compare(_np(x), _np(z), f"{name}/{label} repacked records")
+    # packed record layout: (x, y, a, b), (c, o, sigma_max, 0), (r, g, b, depth), (ex, ey, mode, 0)
+    r = _np(recs)
+    flat = lambda x: np.ascontiguousarray(x).reshape(-1)  # noqa: E731
+    cn = np.asarray(conics).reshape(-1, 3)
+    assert_bit_exact(flat(r[:, 0:2]), flat(xys), f"{name}/record xy")
+    assert_bit_exact(flat(r[:, 2:4]), flat(cn[:, 0:2]), f"{name}/record a, b")
+    assert_bit_exact(r[:, 4], cn[:, 2], f"{name}/record c")
+    assert_bit_exact(r[:, 5], flat(s.opacities), f"{name}/record opacity")
+    assert_bit_exact(flat(r[:, 8:11]), flat(s.colors), f"{name}/record colour")
+    assert_bit_exact(r[:, 11], flat(depths), f"{name}/record depth")
+    mode = r[:, 14].view(np.uint32)
+    assert set(np.unique(mode)) <= {0, 1, 2}
+    box = mode == 0
+    assert np.all(r[box, 12] > 0) and np.all(r[box, 13] > 0)
 
 
 # ---------------------------------------------------------------- depth channel
@@ -347,8 +363,9 @@ def test_rasterize_depth_fwd_bit_exact(name):
     gimg, gT, gidx, gM, gdep = _ops.rasterize_fwd(*args, n=s.n, B=1, img_shape=s.img_shape,
                                                    render_depth=True)
     pimg, pT, pidx, _ = _ops.rasterize_fwd(*args, n=s.n, B=1, img_shape=s.img_shape)
-    kimg, kT, kidx, _, _, _, kM, kdep = _ops.rasterize_fwd_keep(
+    kimg, kT, kidx, kkept, kdep = _ops.rasterize_fwd_keep(
         *args, n=s.n, B=1, img_shape=s.img_shape, render_depth=True)
+    kM = kkept.M
     torch.cuda.synchronize()
     assert gM == ref[4] == kM
     assert_bit_exact(_np(gdep), ref[5], f"{name}/depth")
@@ -378,11 +395,11 @@ def test_rasterize_depth_bwd_matches_oracle(name):
     got = _ops.rasterize_bwd(_t(s.colors), o, o, _t(s.background), *geo, _t(rT), _t(ridx),
                              _t(vout).reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
                              img_shape=s.img_shape, v_out_depth=_t(vd))
-    _, Ts, fidx, ids, pos, bins, M, _ = _ops.rasterize_fwd_keep(
+    _, Ts, fidx, kept_lists, _ = _ops.rasterize_fwd_keep(
         _t(s.colors), o, o, _t(s.background), *geo, n=s.n, B=1, img_shape=s.img_shape,
         render_depth=True)
     kept = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[1], geo[3],
-                                     geo[4], ids, pos, bins, M, Ts, fidx,
+                                     geo[4], kept_lists, Ts, fidx,
                                      _t(vout).reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
                                      img_shape=s.img_shape, v_out_depth=_t(vd))
     torch.cuda.synchronize()
