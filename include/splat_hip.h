@@ -179,6 +179,54 @@ int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* dep
  * reference's tests patch: force != 0 makes every sort take the 64-bit key (process-wide). */
 int splat_set_wide_keys(int force);
 
+/* ---------------------------------------------------------------- training step
+ * The config-4 training step around the render: the per-parameter Adam of the trainers and the
+ * MCMC relocation of splax.mcmc. All arrays are contiguous float32 device buffers, updated in
+ * place. */
+
+/* One Adam parameter group: params, grads, first and second moments (size elements each) and
+ * its learning rate at this step (schedules are evaluated by the caller at the pre-increment
+ * count, as optax's scale_by_schedule does). */
+typedef struct splat_adam_group {
+    float* params;
+    const float* grads;
+    float* mu;
+    float* nu;
+    int64_t size;
+    double lr;
+} splat_adam_group;
+
+/* Replaces optax.adam per group under optax.multi_transform (scripts/train_lego.py:203-211;
+ * optax 0.2.8 scale_by_adam + scale_by_learning_rate + apply_updates): one launch for up to 8
+ * groups. count is the incremented step count (1 on the first update); the bias corrections
+ * 1 - b^count are formed in double and rounded to float32. */
+int splat_adam_step(splat_stream_t stream, const splat_adam_group* groups, int32_t num_groups,
+                    double b1, double b2, double eps, double eps_root, int64_t count);
+
+/* Replaces _reset_opt_state (scripts/train_lego.py:136-146): zeroes mu and nu of every row
+ * whose reset[row] != 0; each group's size must be a multiple of num_rows (its row width). */
+int splat_adam_reset_rows(splat_stream_t stream, const splat_adam_group* groups,
+                          int32_t num_groups, const uint8_t* reset, int64_t num_rows);
+
+/* Replaces splax.mcmc.relocate (splax/mcmc.py:74-131) in place on the [N,3] means3d, [N,3]
+ * log_scales, [N,4] quats (wxyz, copied as is), [N,3] logit_colors and [N] logit_opacities.
+ * n_max is the binomial table size of make_binoms (splax/mcmc.py:29-41), at most 62. The
+ * source draw uses Philox4x32-10 keyed by seed (the reference uses a JAX PRNG key), with
+ * probability exactly proportional to opacity among the alive gaussians. source (may be NULL)
+ * receives the reference's `source` (drawn source for dead rows, the row itself otherwise);
+ * reset (may be NULL) the rows whose optimizer moments the caller should zero. */
+int splat_mcmc_relocate(splat_stream_t stream, float* means3d, float* log_scales, float* quats,
+                        float* logit_colors, float* logit_opacities, int64_t num_gaussians,
+                        int32_t n_max, float min_opacity, uint64_t seed, int32_t* source,
+                        uint8_t* reset);
+
+/* Replaces splax.mcmc.compute_relocation (splax/mcmc.py:44-71): opacities [n], scales [n,3],
+ * ratios [n] (rounded, clipped to [1, n_max]) -> new_opacities [n], new_scales [n,3]. Evaluated
+ * in double with exact binomial coefficients. */
+int splat_mcmc_compute_relocation(splat_stream_t stream, const float* opacities,
+                                  const float* scales, const float* ratios, int64_t n,
+                                  int32_t n_max, float* new_opacities, float* new_scales);
+
 /* Replaces clear_cache (splax/_cache.py:158-164): frees the per-device scratch. */
 void splat_clear_cache(void);
 

@@ -1,0 +1,170 @@
+"""CPU restatement of the training-step operations (test infrastructure only).
+
+Only ``tests/`` and ``bench.py``'s ``cpu_baseline`` leg import this module, as the checker of
+the GPU library; the product package never does.
+
+- ``adam_step``: optax 0.2.8 ``adam`` (a dependency of the reference's trainers, pinned in
+  pixi.lock, not vendored in the reference) as called at scripts/train_lego.py:203-211:
+  ``scale_by_adam`` (mu = (1-b1) g + b1 mu, nu = (1-b2) g^2 + b2 nu, bias corrections
+  1 - b^count at the incremented count, u = mu_hat / (sqrt(nu_hat + eps_root) + eps)), then
+  ``scale_by_learning_rate`` (u * -lr) and ``apply_updates`` (p + u), in float32.
+- ``reset_rows``: _reset_opt_state, scripts/train_lego.py:136-146.
+- ``philox4x32_10``: the counter-based generator of Salmon et al., "Parallel random numbers:
+  as easy as 1, 2, 3" (SC'11), 10 rounds, as the library's relocation draw uses it.
+- ``compute_relocation``: splax/mcmc.py:44-71 in double with exact binomials.
+- ``relocate``: splax/mcmc.py:74-131 with the library's exact draw (integer weights
+  opacity * 2^32, inclusive uint64 prefix, u = floor(r * total / 2^64) from a Philox draw at
+  counter (i, 0, tag, 0), first index whose prefix exceeds u).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from oracle import oracle as O
+
+PHILOX_M = (0xD2511F53, 0xCD9E8D57)
+PHILOX_W = (0x9E3779B9, 0xBB67AE85)
+RELOCATE_TAG = 0x4D434D43
+_M32 = np.uint64(0xFFFFFFFF)
+
+
+# ---------------------------------------------------------------- Adam
+
+def adam_step(p, g, mu, nu, *, lr, count, b1=0.9, b2=0.999, eps=1e-8, eps_root=0.0):
+    """One optax adam update of one parameter group; returns new (p, mu, nu) as float32."""
+    f = np.float32
+    p, g, mu, nu = (np.asarray(a, np.float32) for a in (p, g, mu, nu))
+    c1, c2 = f(1.0 - b1), f(1.0 - b2)  # Python-float constants, rounded once to float32
+    bc1 = f(1.0 - math.pow(b1, count))
+    bc2 = f(1.0 - math.pow(b2, count))
+    mu = c1 * g + f(b1) * mu
+    nu = c2 * (g * g) + f(b2) * nu
+    u = (mu / bc1) / (np.sqrt(nu / bc2 + f(eps_root)) + f(eps))
+    p = p + f(-lr) * u
+    return p.astype(np.float32), mu.astype(np.float32), nu.astype(np.float32)
+
+
+def reset_rows(mu, nu, reset):
+    """Zero the moment rows flagged in reset (leading axis = rows)."""
+    keep = ~np.asarray(reset, bool)
+    shape = (-1,) + (1,) * (np.ndim(mu) - 1)
+    return mu * keep.reshape(shape), nu * keep.reshape(shape)
+
+
+# ---------------------------------------------------------------- Philox4x32-10
+
+def philox4x32_10(ctr, key):
+    """ctr: four uint32 arrays (or scalars), key: two uint32 -> four uint32 arrays."""
+    c = [np.asarray(x, np.uint64) & _M32 for x in ctr]
+    k0, k1 = int(key[0]) & 0xFFFFFFFF, int(key[1]) & 0xFFFFFFFF
+    for r in range(10):
+        if r:
+            k0 = (k0 + PHILOX_W[0]) & 0xFFFFFFFF
+            k1 = (k1 + PHILOX_W[1]) & 0xFFFFFFFF
+        p0 = np.uint64(PHILOX_M[0]) * c[0]
+        p1 = np.uint64(PHILOX_M[1]) * c[2]
+        c = [(p1 >> np.uint64(32)) ^ c[1] ^ np.uint64(k0), p1 & _M32,
+             (p0 >> np.uint64(32)) ^ c[3] ^ np.uint64(k1), p0 & _M32]
+    return [x.astype(np.uint32) for x in c]
+
+
+def mulhi64(r: np.ndarray, t: int) -> np.ndarray:
+    """floor(r * t / 2^64) for uint64 r and 0 <= t < 2^64, exactly."""
+    r = np.asarray(r, np.uint64)
+    rh, rl = r >> np.uint64(32), r & _M32
+    th, tl = np.uint64(t >> 32), np.uint64(t & 0xFFFFFFFF)
+    ll, lh, hl = rl * tl, rl * th, rh * tl
+    mid = (ll >> np.uint64(32)) + (lh & _M32) + (hl & _M32)
+    return rh * th + (lh >> np.uint64(32)) + (hl >> np.uint64(32)) + (mid >> np.uint64(32))
+
+
+# ---------------------------------------------------------------- relocation
+
+def sigmoid(x) -> np.ndarray:
+    """1 / (1 + e^-x) in float32 with the library's fixed-sequence exp."""
+    x = np.asarray(x, np.float32)
+    return (np.float32(1.0) / (np.float32(1.0) + O.expf(-x))).astype(np.float32)
+
+
+def relocation_values(o: float, r: int) -> tuple[float, float]:
+    """(new opacity, scale factor) for one source of multiplicity r (splax/mcmc.py:44-71).
+    IEEE double throughout: an opacity too small to change 1 - o gives o / 0 = inf, as in the
+    reference's float32 evaluation."""
+    no = 1.0 - (1.0 - o) ** (1.0 / r)
+    denom, pw = 0.0, 1.0
+    for k in range(r):
+        pw = pw * no
+        term = float(math.comb(r, k + 1)) * pw / math.sqrt(k + 1)
+        denom = denom - term if k & 1 else denom + term
+    with np.errstate(divide="ignore", invalid="ignore"):
+        coeff = float(np.float64(o) / np.float64(denom))
+    return no, coeff
+
+
+def compute_relocation(opacities, scales, ratios, n_max: int):
+    """splax/mcmc.py:44-71 -> (new_opac [n] f32, new_scales [n,3] f32)."""
+    opac = np.asarray(opacities, np.float32).reshape(-1)
+    sc = np.asarray(scales, np.float32).reshape(-1, 3)
+    rr = np.rint(np.asarray(ratios, np.float32).reshape(-1))
+    new_o = np.empty_like(opac)
+    new_s = np.empty_like(sc)
+    for i in range(opac.size):
+        r = 1 if not rr[i] >= 1 else (n_max if rr[i] >= n_max else int(rr[i]))
+        no, coeff = relocation_values(float(opac[i]), r)
+        new_o[i] = np.float32(no)
+        with np.errstate(invalid="ignore", over="ignore"):
+            new_s[i] = (coeff * sc[i].astype(np.float64)).astype(np.float32)
+    return new_o, new_s
+
+
+def relocate(seed: int, means, log_scales, quats, logit_colors, logit_opacities, n_max: int,
+             min_opacity: float = 0.005):
+    """splax/mcmc.py:74-131 with the library's draw; returns (means, log_scales, quats,
+    logit_colors, logit_opacities, source int32, reset bool) as new arrays."""
+    means = np.array(means, np.float32).reshape(-1, 3)
+    log_scales = np.array(log_scales, np.float32).reshape(-1, 3)
+    quats = np.array(quats, np.float32).reshape(-1, 4)
+    colors = np.array(logit_colors, np.float32).reshape(-1, 3)
+    logit = np.array(logit_opacities, np.float32).reshape(-1)
+    n = logit.size
+    mo = np.float32(min_opacity)
+    opac = sigmoid(logit)
+    dead = opac <= mo
+    w = np.where(dead, np.uint64(0), (opac * np.float32(2.0**32)).astype(np.uint64))
+    cdf = np.cumsum(w, dtype=np.uint64)
+    total = int(cdf[-1]) if n else 0
+    idx = np.arange(n, dtype=np.int64)
+    src = idx.copy()
+    d = np.nonzero(dead)[0]
+    if d.size:
+        if total == 0:
+            src[d] = 0
+        else:
+            c = philox4x32_10((d & 0xFFFFFFFF, d >> 32, np.full(d.size, RELOCATE_TAG),
+                               np.zeros(d.size)), (seed & 0xFFFFFFFF, seed >> 32))
+            r = (c[0].astype(np.uint64) << np.uint64(32)) | c[1].astype(np.uint64)
+            u = mulhi64(r, total)
+            src[d] = np.searchsorted(cdf, u, side="right")
+    counts = np.bincount(src[d], minlength=n).astype(np.int64)
+    reset = dead | (counts > 0)
+    newv = {}
+    lo_clip, hi_clip = float(mo), 1.0 - 2.0**-23
+    for s in np.nonzero(counts)[0]:
+        r = min(int(counts[s]) + 1, n_max)
+        no, coeff = relocation_values(float(opac[s]), r)
+        no = min(max(no, lo_clip), hi_clip)
+        sc = O.expf(log_scales[s]).astype(np.float64)
+        with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+            newv[s] = (np.float32(np.log(no / (1.0 - no))),
+                       np.log(coeff * sc).astype(np.float32))
+    out_means, out_ls, out_q, out_c, out_l = (a.copy() for a in (means, log_scales, quats,
+                                                                   colors, logit))
+    for i in np.nonzero(reset)[0]:
+        s = int(src[i]) if dead[i] else int(i)
+        if dead[i]:
+            out_means[i], out_q[i], out_c[i] = means[s], quats[s], colors[s]
+        out_l[i], out_ls[i] = newv[s]
+    return out_means, out_ls, out_q, out_c, out_l, src.astype(np.int32), reset

@@ -21,6 +21,15 @@ _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
 _f32 = ctypes.c_float
+_f64 = ctypes.c_double
+_u64 = ctypes.c_uint64
+
+
+class AdamGroup(ctypes.Structure):
+    """splat_adam_group (include/splat_hip.h)."""
+    _fields_ = [("params", _vp), ("grads", _vp), ("mu", _vp), ("nu", _vp), ("size", _i64),
+                ("lr", _f64)]
+
 
 # name -> argtypes, in the order of include/splat_hip.h
 _SIGS = {
@@ -41,6 +50,10 @@ _SIGS = {
     "splat_sort_and_bin": [_vp] + [_vp] * 4 + [_vp, _i64, _vp] + [_i32] * 4
     + [_vp, _vp, _i64, _vp, _vp],
     "splat_set_wide_keys": [_i32],
+    "splat_adam_step": [_vp, _vp, _i32, _f64, _f64, _f64, _f64, _i64],
+    "splat_adam_reset_rows": [_vp, _vp, _i32, _vp, _i64],
+    "splat_mcmc_relocate": [_vp] + [_vp] * 5 + [_i64, _i32, _f32, _u64, _vp, _vp],
+    "splat_mcmc_compute_relocation": [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp],
     "splat_clear_cache": [],
     "splat_last_error": [],
     "splat_set_stage_timing": [_i32],

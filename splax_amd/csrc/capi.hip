@@ -330,7 +330,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 5; }
+int splat_abi_version(void) { return 6; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();
@@ -350,7 +350,10 @@ int splat_check_device(void) {
 
 const char* splat_last_error(void) { return g_last_error.c_str(); }
 
-void splat_clear_cache(void) { release_all_scratch(); }
+void splat_clear_cache(void) {
+    release_all_scratch();
+    release_train_scratch();
+}
 
 int splat_set_stage_timing(int stage_mask) {
     std::lock_guard<std::mutex> lock(g_timing_mu);

@@ -155,6 +155,9 @@ struct StageTimer {
 };
 
 // ------------------------------------------------------------------ launchers
+// Frees the relocation scratch of every device (train.hip).
+void release_train_scratch();
+
 int fill_zero_f32(float* p, int64_t n, hipStream_t stream);
 int fill_zero_i32(int32_t* p, int64_t n, hipStream_t stream);
 int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stream);

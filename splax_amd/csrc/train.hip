@@ -1,0 +1,524 @@
+// Training-step kernels of the gfx950 splat library:
+//   - the fused multi-tensor Adam update, optax 0.2.8 `adam` (scale_by_adam followed by
+//     scale_by_learning_rate, then apply_updates) as the trainers configure it per parameter
+//     group (scripts/train_lego.py:203-211), and the moment reset of relocated rows
+//     (scripts/train_lego.py:136-146);
+//   - the fixed-budget MCMC relocation, splax/mcmc.py:29-131.
+//
+// Adam arithmetic per element (float32, no contraction): mu = c1 g + b1 mu; nu = c2 (g g) + b2 nu;
+// u = (mu / bc1) / (sqrt(nu / bc2 + eps_root) + eps); p = p + (-lr) u, with c1 = f32(1 - b1),
+// c2 = f32(1 - b2) formed in double as Python does for optax's weakly typed constants, and the
+// bias corrections bc = f32(1 - b^count) formed in double on the host.
+//
+// Relocation (splax/mcmc.py:74-131). A gaussian is dead when sigmoid(logit) <= min_opacity, with
+// sigmoid(x) = 1 / (1 + det_expf(-x)). Every dead gaussian draws a source among the alive ones
+// with probability proportional to opacity (splax/mcmc.py:107-109). The draw is exact and
+// reproducible: the weights are the integers opacity * 2^32 (exact for opacities >= 2^-8), their
+// inclusive prefix is an order-free uint64 scan, and a dead gaussian i takes 64 bits r from
+// Philox4x32-10 (Salmon et al., SC'11) at counter (i, tag) under the caller's 64-bit seed,
+// u = floor(r * total / 2^64), and the first index whose prefix exceeds u. The relocation values
+// (compute_relocation, splax/mcmc.py:44-71, after gsplat's relocation kernel) are evaluated in
+// double with exact binomial coefficients and rounded to float32 once.
+#include <mutex>
+#include <string>
+
+#include "../../include/splat_hip.h"
+#include "splat_common.hpp"
+#include "splat_internal.hpp"
+
+namespace splat {
+
+// ------------------------------------------------------------------ Adam
+
+constexpr int kAdamMaxGroups = 8;
+constexpr int kAdamChunk = 2048;  // elements per workgroup (8 per thread)
+
+struct AdamGroupDev {
+    float* p; const float* g; float* mu; float* nu;
+    int64_t size;
+    float neg_lr;
+};
+
+struct AdamParams {
+    AdamGroupDev grp[kAdamMaxGroups];
+    int64_t block_start[kAdamMaxGroups + 1];  // first workgroup of each group
+    int n_groups;
+    float b1, c1, b2, c2, eps, eps_root, bc1, bc2;
+};
+
+__global__ void __launch_bounds__(256) adam_step_kernel(AdamParams P) {
+    const int64_t b = blockIdx.x;
+    int gi = 0;
+    while (gi + 1 < P.n_groups && b >= P.block_start[gi + 1]) ++gi;  // uniform per workgroup
+    const AdamGroupDev G = P.grp[gi];
+    const int64_t base = (b - P.block_start[gi]) * kAdamChunk;
+#pragma unroll
+    for (int j = 0; j < kAdamChunk / 256; ++j) {
+        const int64_t i = base + j * 256 + threadIdx.x;
+        if (i >= G.size) break;
+        const float g = G.g[i];
+        float m = G.mu[i], v = G.nu[i];
+        m = P.c1 * g + P.b1 * m;
+        v = P.c2 * (g * g) + P.b2 * v;
+        const float mh = m / P.bc1;
+        const float vh = v / P.bc2;
+        const float u = mh / (sqrtf(vh + P.eps_root) + P.eps);
+        G.mu[i] = m;
+        G.nu[i] = v;
+        G.p[i] = G.p[i] + G.neg_lr * u;
+    }
+}
+
+struct ResetParams {
+    float* mu[kAdamMaxGroups];
+    float* nu[kAdamMaxGroups];
+    int32_t width[kAdamMaxGroups];
+    int n_groups;
+    const uint8_t* reset;
+    int64_t rows;
+};
+
+__global__ void __launch_bounds__(256) adam_reset_rows_kernel(ResetParams P) {
+    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r >= P.rows || !P.reset[r]) return;
+    // x * keep, as the reference does: a negative moment becomes -0 and NaN stays NaN
+    for (int g = 0; g < P.n_groups; ++g) {
+        const int32_t w = P.width[g];
+        for (int k = 0; k < w; ++k) {
+            P.mu[g][r * w + k] = P.mu[g][r * w + k] * 0.0f;
+            P.nu[g][r * w + k] = P.nu[g][r * w + k] * 0.0f;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ Philox4x32-10
+
+constexpr uint32_t kPhiloxM0 = 0xD2511F53u, kPhiloxM1 = 0xCD9E8D57u;
+constexpr uint32_t kPhiloxW0 = 0x9E3779B9u, kPhiloxW1 = 0xBB67AE85u;
+constexpr uint32_t kRelocateTag = 0x4d434d43u;  // counter word 2 of the relocation draws
+
+__device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        if (r > 0) {
+            k0 += kPhiloxW0;
+            k1 += kPhiloxW1;
+        }
+        const uint64_t p0 = (uint64_t)kPhiloxM0 * c[0];
+        const uint64_t p1 = (uint64_t)kPhiloxM1 * c[2];
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0;
+        const uint32_t n1 = (uint32_t)p1;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
+        const uint32_t n3 = (uint32_t)p0;
+        c[0] = n0; c[1] = n1; c[2] = n2; c[3] = n3;
+    }
+}
+
+// ------------------------------------------------------------------ relocation
+
+constexpr int kRelocChunk = 4096;  // weights per workgroup of the scan (16 per thread)
+constexpr int kMaxBinomRows = 62;  // C(r, k) * (r - k) stays below 2^64 for r <= 62
+
+__device__ __forceinline__ float reloc_sigmoid(float x) { return 1.0f / (1.0f + det_expf(-x)); }
+
+// splax/mcmc.py:104 (sigmoid never yields NaN here: det_expf maps NaN to 0).
+__device__ __forceinline__ bool reloc_dead(float logit, float min_opacity) {
+    return reloc_sigmoid(logit) <= min_opacity;
+}
+
+__device__ __forceinline__ uint64_t reloc_weight(float logit, float min_opacity) {
+    const float o = reloc_sigmoid(logit);
+    if (o <= min_opacity) return 0ull;
+    return (uint64_t)(o * 0x1p32f);
+}
+
+// compute_relocation for one row (splax/mcmc.py:44-71): new opacity 1 - (1 - o)^(1/r) and the
+// scale factor o / sum_{k<r} C(r, k+1) (-1)^k (k+1)^(-1/2) new^(k+1). The reference's
+// cumsum(binoms)[r-1, k] equals C(r, k+1).
+__device__ __forceinline__ void relocation_values(double o, int r, double& no, double& coeff) {
+    no = 1.0 - pow(1.0 - o, 1.0 / (double)r);
+    double denom = 0.0, pw = 1.0;
+    uint64_t binom = 1;  // C(r, k) before the update, C(r, k+1) after
+    for (int k = 0; k < r; ++k) {
+        binom = binom * (uint64_t)(r - k) / (uint64_t)(k + 1);
+        pw = pw * no;
+        const double term = (double)binom * pw / sqrt((double)(k + 1));
+        denom = (k & 1) ? denom - term : denom + term;
+    }
+    coeff = o / denom;
+}
+
+struct RelocParams {
+    float* means; float* log_scales; float* quats; float* colors; float* logit_opac;
+    int64_t n;
+    int32_t n_max;
+    float min_opacity;
+    uint32_t seed_lo, seed_hi;
+    uint64_t* cdf;       // [n] inclusive prefix of the weights
+    uint64_t* partials;  // [blocks + 1] exclusive prefix per scan workgroup, then the total
+    int32_t* counts;     // [n] dead gaussians that drew each source
+    int32_t* src;        // [n] dead: drawn source; alive: itself
+    float4* newv;        // [n] (logit, log_scale x3) of rows with counts > 0
+    int32_t* source_out; // optional [n]
+    uint8_t* reset_out;  // optional [n]
+    int64_t blocks;
+};
+
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* s_wave) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) s_wave[wave] = v;
+    __syncthreads();
+    const uint64_t t = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
+    __syncthreads();
+    return t;
+}
+
+// Workgroup sums of the weights; also clears the draw counts of the chunk.
+__global__ void __launch_bounds__(256) reloc_partials_kernel(RelocParams P) {
+    __shared__ uint64_t s_wave[4];
+    const int64_t base = (int64_t)blockIdx.x * kRelocChunk;
+    uint64_t acc = 0;
+#pragma unroll
+    for (int j = 0; j < kRelocChunk / 256; ++j) {
+        const int64_t i = base + j * 256 + threadIdx.x;
+        if (i < P.n) {
+            acc += reloc_weight(P.logit_opac[i], P.min_opacity);
+            P.counts[i] = 0;
+        }
+    }
+    const uint64_t t = block_sum_u64(acc, s_wave);
+    if (threadIdx.x == 0) P.partials[blockIdx.x] = t;
+}
+
+// One workgroup: exclusive scan of the workgroup sums, total in partials[blocks].
+__global__ void __launch_bounds__(256) reloc_scan_partials_kernel(RelocParams P) {
+    __shared__ uint64_t s[256];
+    uint64_t carry = 0;
+    for (int64_t c0 = 0; c0 < P.blocks; c0 += 256) {
+        const int64_t i = c0 + threadIdx.x;
+        const uint64_t v = i < P.blocks ? P.partials[i] : 0ull;
+        s[threadIdx.x] = v;
+        __syncthreads();
+        for (int off = 1; off < 256; off <<= 1) {  // Hillis-Steele inclusive scan
+            const uint64_t add = threadIdx.x >= (unsigned)off ? s[threadIdx.x - off] : 0ull;
+            __syncthreads();
+            s[threadIdx.x] += add;
+            __syncthreads();
+        }
+        if (i < P.blocks) P.partials[i] = carry + s[threadIdx.x] - v;
+        carry += s[255];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) P.partials[P.blocks] = carry;
+}
+
+// Inclusive prefix of the weights: each thread owns 16 consecutive weights.
+__global__ void __launch_bounds__(256) reloc_cdf_kernel(RelocParams P) {
+    __shared__ uint64_t s[256];
+    const int64_t base = (int64_t)blockIdx.x * kRelocChunk + 16 * threadIdx.x;
+    uint64_t w[16];
+    uint64_t own = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int64_t i = base + k;
+        w[k] = i < P.n ? reloc_weight(P.logit_opac[i], P.min_opacity) : 0ull;
+        own += w[k];
+    }
+    s[threadIdx.x] = own;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+        const uint64_t add = threadIdx.x >= (unsigned)off ? s[threadIdx.x - off] : 0ull;
+        __syncthreads();
+        s[threadIdx.x] += add;
+        __syncthreads();
+    }
+    uint64_t run = P.partials[blockIdx.x] + s[threadIdx.x] - own;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int64_t i = base + k;
+        run += w[k];
+        if (i < P.n) P.cdf[i] = run;
+    }
+}
+
+// Draws the source of every dead gaussian (splax/mcmc.py:107-111) and counts the draws.
+__global__ void __launch_bounds__(256) reloc_sample_kernel(RelocParams P) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= P.n) return;
+    if (!reloc_dead(P.logit_opac[i], P.min_opacity)) {
+        P.src[i] = (int32_t)i;
+        return;
+    }
+    const uint64_t total = P.partials[P.blocks];
+    int64_t s = 0;  // nothing alive: every logit is -inf and the reference's argmax gives 0
+    if (total > 0) {
+        uint32_t c[4] = {(uint32_t)i, (uint32_t)((uint64_t)i >> 32), kRelocateTag, 0u};
+        philox4x32_10(c, P.seed_lo, P.seed_hi);
+        const uint64_t r = ((uint64_t)c[0] << 32) | c[1];
+        const uint64_t u = __umul64hi(r, total);
+        int64_t lo = 0, hi = P.n - 1;  // first index with cdf > u; cdf[n-1] = total > u
+        while (lo < hi) {
+            const int64_t mid = (lo + hi) >> 1;
+            if (P.cdf[mid] > u) hi = mid; else lo = mid + 1;
+        }
+        s = lo;
+    }
+    P.src[i] = (int32_t)s;
+    atomicAdd(&P.counts[s], 1);
+}
+
+// New (logit, log scales) of every drawn source, from its unmodified row.
+__global__ void __launch_bounds__(256) reloc_values_kernel(RelocParams P) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= P.n) return;
+    const int32_t cnt = P.counts[i];
+    if (cnt <= 0) return;
+    const int r = cnt + 1 < P.n_max ? cnt + 1 : P.n_max;  // ratio, clipped to [1, n_max]
+    const double o = (double)reloc_sigmoid(P.logit_opac[i]);
+    double no, coeff;
+    relocation_values(o, r, no, coeff);
+    const double lo_clip = (double)P.min_opacity, hi_clip = 1.0 - 0x1p-23;
+    no = no < lo_clip ? lo_clip : no;
+    no = no > hi_clip ? hi_clip : no;
+    float4 v;
+    v.x = (float)log(no / (1.0 - no));
+    v.y = (float)log(coeff * (double)det_expf(P.log_scales[3 * i]));
+    v.z = (float)log(coeff * (double)det_expf(P.log_scales[3 * i + 1]));
+    v.w = (float)log(coeff * (double)det_expf(P.log_scales[3 * i + 2]));
+    P.newv[i] = v;
+}
+
+// Writes the relocated rows (splax/mcmc.py:119-131). Dead rows copy mean, quaternion and colour
+// of their source, which is alive and keeps those, and take the source's new values.
+__global__ void __launch_bounds__(256) reloc_apply_kernel(RelocParams P) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= P.n) return;
+    const int32_t s = P.src[i];
+    const bool dead = reloc_dead(P.logit_opac[i], P.min_opacity);  // own row, read before writing
+    const bool reset = dead || P.counts[i] > 0;
+    if (dead) {
+        const float m0 = P.means[3 * s], m1 = P.means[3 * s + 1], m2 = P.means[3 * s + 2];
+        const float q0 = P.quats[4 * s], q1 = P.quats[4 * s + 1], q2 = P.quats[4 * s + 2],
+                    q3 = P.quats[4 * s + 3];
+        const float c0 = P.colors[3 * s], c1 = P.colors[3 * s + 1], c2 = P.colors[3 * s + 2];
+        P.means[3 * i] = m0; P.means[3 * i + 1] = m1; P.means[3 * i + 2] = m2;
+        P.quats[4 * i] = q0; P.quats[4 * i + 1] = q1; P.quats[4 * i + 2] = q2;
+        P.quats[4 * i + 3] = q3;
+        P.colors[3 * i] = c0; P.colors[3 * i + 1] = c1; P.colors[3 * i + 2] = c2;
+    }
+    if (reset) {
+        const float4 v = P.newv[dead ? s : (int32_t)i];
+        P.logit_opac[i] = v.x;
+        P.log_scales[3 * i] = v.y;
+        P.log_scales[3 * i + 1] = v.z;
+        P.log_scales[3 * i + 2] = v.w;
+    }
+    if (P.source_out) P.source_out[i] = s;
+    if (P.reset_out) P.reset_out[i] = reset ? 1 : 0;
+}
+
+struct ComputeRelocParams {
+    const float* opac; const float* scales; const float* ratios;
+    int64_t n;
+    int32_t n_max;
+    float* new_opac; float* new_scales;
+};
+
+// compute_relocation alone (splax/mcmc.py:44-71): ratio rounded and clipped to [1, n_max].
+__global__ void __launch_bounds__(256) compute_relocation_kernel(ComputeRelocParams P) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= P.n) return;
+    const float rf = rintf(P.ratios[i]);
+    int r = rf >= (float)P.n_max ? P.n_max : (rf >= 1.0f ? (int)rf : 1);
+    double no, coeff;
+    relocation_values((double)P.opac[i], r, no, coeff);
+    P.new_opac[i] = (float)no;
+    for (int k = 0; k < 3; ++k) P.new_scales[3 * i + k] = (float)(coeff * (double)P.scales[3 * i + k]);
+}
+
+// ------------------------------------------------------------------ scratch
+
+struct RelocScratch {
+    std::mutex mu;
+    int64_t cap = 0;
+    uint64_t* cdf = nullptr;
+    uint64_t* partials = nullptr;
+    int32_t* counts = nullptr;
+    int32_t* src = nullptr;
+    float4* newv = nullptr;
+
+    void release() {
+        if (cap) (void)hipDeviceSynchronize();
+        (void)hipFree(cdf); (void)hipFree(partials); (void)hipFree(counts);
+        (void)hipFree(src); (void)hipFree(newv);
+        cdf = nullptr; partials = nullptr; counts = nullptr; src = nullptr; newv = nullptr;
+        cap = 0;
+    }
+    int ensure(int64_t n) {
+        if (n <= cap) return 0;
+        release();
+        const int64_t c = (int64_t)(n * 1.25) + 1;
+        const int64_t nb = (c + kRelocChunk - 1) / kRelocChunk + 1;
+        if (hipMalloc((void**)&cdf, c * sizeof(uint64_t)) != hipSuccess ||
+            hipMalloc((void**)&partials, nb * sizeof(uint64_t)) != hipSuccess ||
+            hipMalloc((void**)&counts, c * sizeof(int32_t)) != hipSuccess ||
+            hipMalloc((void**)&src, c * sizeof(int32_t)) != hipSuccess ||
+            hipMalloc((void**)&newv, c * sizeof(float4)) != hipSuccess) {
+            release();
+            return fail(kErrAlloc, "relocate: scratch allocation failed");
+        }
+        cap = c;
+        return 0;
+    }
+};
+
+constexpr int kRelocMaxDevices = 64;
+static RelocScratch g_reloc[kRelocMaxDevices];
+
+void release_train_scratch() {
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return;
+    for (int d = 0; d < kRelocMaxDevices; ++d) {
+        std::lock_guard<std::mutex> lock(g_reloc[d].mu);
+        if (!g_reloc[d].cap) continue;
+        if (hipSetDevice(d) != hipSuccess) continue;
+        g_reloc[d].release();
+    }
+    (void)hipSetDevice(cur);
+}
+
+static unsigned grid_for(int64_t n, int64_t per) { return (unsigned)((n + per - 1) / per); }
+
+static int launched(const char* what) {
+    return hipGetLastError() == hipSuccess ? 0 : fail(kErrLaunch, std::string(what) + " launch failed");
+}
+
+}  // namespace splat
+
+using namespace splat;
+
+extern "C" {
+
+int splat_adam_step(splat_stream_t stream, const splat_adam_group* groups, int32_t num_groups,
+                    double b1, double b2, double eps, double eps_root, int64_t count) {
+    if (num_groups < 0 || num_groups > kAdamMaxGroups || (num_groups > 0 && !groups))
+        return fail(kErrArgs, "adam_step: between 0 and 8 parameter groups");
+    if (count < 1) return fail(kErrArgs, "adam_step: count (the incremented step) must be >= 1");
+    AdamParams P;
+    P.n_groups = num_groups;
+    int64_t blocks = 0;
+    for (int g = 0; g < num_groups; ++g) {
+        const splat_adam_group& s = groups[g];
+        if (s.size < 0 || (s.size > 0 && (!s.params || !s.grads || !s.mu || !s.nu)))
+            return fail(kErrArgs, "adam_step: group " + std::to_string(g) + " has no buffers");
+        P.grp[g] = AdamGroupDev{s.params, s.grads, s.mu, s.nu, s.size, (float)(-s.lr)};
+        P.block_start[g] = blocks;
+        blocks += (s.size + kAdamChunk - 1) / kAdamChunk;
+    }
+    P.block_start[num_groups] = blocks;
+    P.b1 = (float)b1;
+    P.c1 = (float)(1.0 - b1);
+    P.b2 = (float)b2;
+    P.c2 = (float)(1.0 - b2);
+    P.eps = (float)eps;
+    P.eps_root = (float)eps_root;
+    P.bc1 = (float)(1.0 - pow(b1, (double)count));
+    P.bc2 = (float)(1.0 - pow(b2, (double)count));
+    if (blocks == 0) return 0;
+    if (blocks > 0x7fffffff) return fail(kErrArgs, "adam_step: too many elements");
+    hipLaunchKernelGGL(adam_step_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), P);
+    return launched("adam_step");
+}
+
+int splat_adam_reset_rows(splat_stream_t stream, const splat_adam_group* groups,
+                          int32_t num_groups, const uint8_t* reset, int64_t num_rows) {
+    if (num_groups < 0 || num_groups > kAdamMaxGroups || (num_groups > 0 && !groups))
+        return fail(kErrArgs, "adam_reset_rows: between 0 and 8 parameter groups");
+    if (num_rows < 0 || (num_rows > 0 && !reset))
+        return fail(kErrArgs, "adam_reset_rows: missing reset mask");
+    ResetParams P;
+    P.n_groups = num_groups;
+    P.reset = reset;
+    P.rows = num_rows;
+    for (int g = 0; g < num_groups; ++g) {
+        const splat_adam_group& s = groups[g];
+        if (num_rows == 0) break;
+        if (s.size % num_rows != 0 || (s.size > 0 && (!s.mu || !s.nu)))
+            return fail(kErrArgs, "adam_reset_rows: group " + std::to_string(g) +
+                                      " is not a whole number of rows");
+        P.mu[g] = s.mu;
+        P.nu[g] = s.nu;
+        P.width[g] = (int32_t)(s.size / num_rows);
+    }
+    if (num_rows == 0 || num_groups == 0) return 0;
+    hipLaunchKernelGGL(adam_reset_rows_kernel, dim3(grid_for(num_rows, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), P);
+    return launched("adam_reset_rows");
+}
+
+int splat_mcmc_relocate(splat_stream_t stream, float* means3d, float* log_scales, float* quats,
+                        float* logit_colors, float* logit_opacities, int64_t num_gaussians,
+                        int32_t n_max, float min_opacity, uint64_t seed, int32_t* source,
+                        uint8_t* reset) {
+    if (num_gaussians < 0 || num_gaussians > 0x7fffffff)
+        return fail(kErrArgs, "relocate: gaussian count outside [0, 2^31)");
+    if (n_max < 1 || n_max > kMaxBinomRows)
+        return fail(kErrArgs, "relocate: binomial table size must be in [1, 62]");
+    if (num_gaussians == 0) return 0;
+    if (!means3d || !log_scales || !quats || !logit_colors || !logit_opacities)
+        return fail(kErrArgs, "relocate: missing parameter arrays");
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kRelocMaxDevices)
+        return fail(kErrRuntime, "relocate: no current device");
+    RelocScratch& sc = g_reloc[dev];
+    std::lock_guard<std::mutex> lock(sc.mu);
+    int rc = sc.ensure(num_gaussians);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    RelocParams P;
+    P.means = means3d; P.log_scales = log_scales; P.quats = quats; P.colors = logit_colors;
+    P.logit_opac = logit_opacities;
+    P.n = num_gaussians;
+    P.n_max = n_max;
+    P.min_opacity = min_opacity;
+    P.seed_lo = (uint32_t)seed;
+    P.seed_hi = (uint32_t)(seed >> 32);
+    P.cdf = sc.cdf; P.partials = sc.partials; P.counts = sc.counts; P.src = sc.src;
+    P.newv = sc.newv;
+    P.source_out = source;
+    P.reset_out = reset;
+    P.blocks = (num_gaussians + kRelocChunk - 1) / kRelocChunk;
+    const unsigned rows = grid_for(num_gaussians, 256);
+    hipLaunchKernelGGL(reloc_partials_kernel, dim3((unsigned)P.blocks), dim3(256), 0, s, P);
+    if ((rc = launched("relocate partials"))) return rc;
+    hipLaunchKernelGGL(reloc_scan_partials_kernel, dim3(1), dim3(256), 0, s, P);
+    if ((rc = launched("relocate scan"))) return rc;
+    hipLaunchKernelGGL(reloc_cdf_kernel, dim3((unsigned)P.blocks), dim3(256), 0, s, P);
+    if ((rc = launched("relocate cdf"))) return rc;
+    hipLaunchKernelGGL(reloc_sample_kernel, dim3(rows), dim3(256), 0, s, P);
+    if ((rc = launched("relocate sample"))) return rc;
+    hipLaunchKernelGGL(reloc_values_kernel, dim3(rows), dim3(256), 0, s, P);
+    if ((rc = launched("relocate values"))) return rc;
+    hipLaunchKernelGGL(reloc_apply_kernel, dim3(rows), dim3(256), 0, s, P);
+    return launched("relocate apply");
+}
+
+int splat_mcmc_compute_relocation(splat_stream_t stream, const float* opacities,
+                                  const float* scales, const float* ratios, int64_t n,
+                                  int32_t n_max, float* new_opacities, float* new_scales) {
+    if (n < 0) return fail(kErrArgs, "compute_relocation: negative count");
+    if (n_max < 1 || n_max > kMaxBinomRows)
+        return fail(kErrArgs, "compute_relocation: binomial table size must be in [1, 62]");
+    if (n == 0) return 0;
+    if (!opacities || !scales || !ratios || !new_opacities || !new_scales)
+        return fail(kErrArgs, "compute_relocation: missing arrays");
+    ComputeRelocParams P{opacities, scales, ratios, n, n_max, new_opacities, new_scales};
+    hipLaunchKernelGGL(compute_relocation_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), P);
+    return launched("compute_relocation");
+}
+
+}  // extern "C"

@@ -1,0 +1,95 @@
+"""The config-4 training step on the gfx950 library.
+
+One step is the reference trainer's step (scripts/train_lego.py:101-131,217-229) at a fixed
+gaussian budget with the loss reduced to L1:
+  1. ``render_log`` of the log / logit parameters from B cameras in one batched launch, with the
+     antialiasing opacity compensation (splax/_render.py:118-168, splax/_project/_project.py:95-117);
+  2. L1 = mean |img - target| and its gradient through the render's custom backward;
+  3. one fused Adam update of the five parameter groups (optax.adam per group,
+     scripts/train_lego.py:203-211, exponential decay on the means' learning rate);
+  4. one MCMC relocation (splax/mcmc.py:74-131) and the moment reset of the relocated rows
+     (scripts/train_lego.py:136-146, 217-222).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Mapping
+
+import numpy as np
+import torch
+
+from splax_amd import mcmc
+from splax_amd._render import render_log
+from splax_amd.optim import Adam, exponential_decay
+from splax_amd.scenes import Scene
+
+SPLAT_KEYS = ("means", "log_scales", "quats", "colors_logit", "opac_logit")
+
+# scripts/train_lego.py:407-411 (defaults of the reference trainer)
+DEFAULT_LRS = {"means": 1.5e-3, "log_scales": 5e-3, "quats": 1e-3, "colors_logit": 1e-2,
+               "opac_logit": 5e-2}
+
+
+def _logit(x: np.ndarray, eps: float = 1e-4) -> np.ndarray:
+    x = np.clip(x.astype(np.float64), eps, 1.0 - eps)
+    return np.log(x / (1.0 - x)).astype(np.float32)
+
+
+def params_from_scene(scene: Scene, device: torch.device | str = "cuda") -> dict[str, torch.Tensor]:
+    """Log / logit parameters (render_log's parameterization) of a synthetic scene."""
+    arrays = {
+        "means": scene.means.astype(np.float32),
+        "log_scales": np.log(scene.scales.astype(np.float64)).astype(np.float32),
+        "quats": scene.quats.astype(np.float32),
+        "colors_logit": _logit(scene.colors),
+        "opac_logit": _logit(scene.opacities.reshape(-1, 1)),
+    }
+    return {k: torch.from_numpy(np.ascontiguousarray(v)).to(device) for k, v in arrays.items()}
+
+
+class TrainStep:
+    """Fixed-budget training step over B cameras; ``params`` are updated in place."""
+
+    def __init__(self, params: Mapping[str, torch.Tensor], *, viewmats: torch.Tensor,
+                 targets: torch.Tensor, background: torch.Tensor, img_shape: tuple[int, int],
+                 f: tuple[float, float], c: tuple[float, float] | None = None,
+                 antialiased: bool = True, steps: int = 30_000,
+                 lrs: Mapping[str, float] | None = None, min_opacity: float = 0.005,
+                 n_max: int = 51, relocate_every: int = 1, seed: int = 0):
+        if tuple(params) != SPLAT_KEYS:
+            raise ValueError(f"params must hold {SPLAT_KEYS} in this order")
+        self.params = {k: p.detach().contiguous() for k, p in params.items()}
+        lr = dict(DEFAULT_LRS if lrs is None else lrs)
+        sched = dict(lr)
+        sched["means"] = exponential_decay(lr["means"], steps, 0.01)  # train_lego.py:203
+        self.opt = Adam(self.params, sched)
+        self.viewmats = viewmats
+        self.targets = targets
+        self.background = background
+        self.camera = dict(img_shape=img_shape, f=f, c=c, antialiased=antialiased)
+        self.binoms = mcmc.make_binoms(n_max)
+        self.min_opacity = min_opacity
+        self.relocate_every = relocate_every
+        self.seed = seed
+        self.step_idx = 0
+
+    def loss_and_grads(self) -> tuple[torch.Tensor, dict[str, torch.Tensor]]:
+        leaves = [p.requires_grad_(True) for p in self.params.values()]
+        img, _ = render_log(*leaves, viewmat=self.viewmats, background=self.background,
+                            **self.camera)
+        loss = (img - self.targets).abs().mean()
+        grads = torch.autograd.grad(loss, leaves)
+        for p in leaves:
+            p.requires_grad_(False)
+        return loss.detach(), dict(zip(SPLAT_KEYS, grads))
+
+    def __call__(self) -> torch.Tensor:
+        """One step; returns the L1 loss before the update (a device scalar)."""
+        loss, grads = self.loss_and_grads()
+        self.opt.step(grads)
+        self.step_idx += 1
+        if self.relocate_every and self.step_idx % self.relocate_every == 0:
+            key = (self.seed << 32) ^ self.step_idx
+            reset = mcmc.relocate_(key, *self.params.values(), self.binoms, self.min_opacity)
+            self.opt.reset_rows(reset)
+        return loss

@@ -1,0 +1,243 @@
+"""GPU parity of the training-step entry points against the CPU oracle (oracle/train_oracle.py).
+
+- Adam (splat_adam_step) and the moment reset: bit-exact, both sides run the same float32
+  sequence.
+- compute_relocation: within one float32 ulp (both evaluate in double and round once; the
+  double pow / log of the two math libraries may differ in the last double bit).
+- relocate: sources, reset rows and every copied parameter bit-exact (the draw is integer
+  arithmetic); relocated opacity logits and log scales within one float32 ulp. At the config-4
+  size (3M gaussians) through size-independent properties: determinism, alive sources, rows
+  sharing a source carry identical values, r copies of the new opacity compose to the old one,
+  and the draw frequencies follow opacity.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_bit_exact
+from oracle import train_oracle as T
+from splax_amd import _lib, mcmc, optim
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _max_ulp(a, b):
+    a = np.ascontiguousarray(a, np.float32).reshape(-1).view(np.int32).astype(np.int64)
+    b = np.ascontiguousarray(b, np.float32).reshape(-1).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, -(a & 0x7FFFFFFF), a)  # monotone integer order of the floats
+    b = np.where(b < 0, -(b & 0x7FFFFFFF), b)
+    return int(np.abs(a - b).max()) if a.size else 0
+
+
+GROUPS = {"means": 3, "log_scales": 3, "quats": 4, "colors_logit": 3, "opac_logit": 1}
+LRS = {"means": optim.exponential_decay(1.6e-3, 30000, 0.01), "log_scales": 5e-3,
+       "quats": 1e-3, "colors_logit": 1e-2, "opac_logit": 5e-2}
+
+
+def _params(n, seed):
+    rng = np.random.default_rng(seed)
+    return {k: rng.normal(size=(n, w)).astype(np.float32) for k, w in GROUPS.items()}
+
+
+@pytest.mark.parametrize("n", [1, 1000, 10007])
+def test_adam_step_bit_exact(n):
+    _case(f"adam n={n}")
+    rng = np.random.default_rng(n)
+    ref = _params(n, n)
+    mu = {k: np.zeros_like(v) for k, v in ref.items()}
+    nu = {k: np.zeros_like(v) for k, v in ref.items()}
+    dev = {k: _t(v) for k, v in ref.items()}
+    opt = optim.Adam(dev, LRS)
+    for step in range(1, 5):
+        grads = {k: (rng.normal(size=v.shape) * 10.0 ** rng.uniform(-6, 1)).astype(np.float32)
+                 for k, v in ref.items()}
+        grads["quats"][: n // 3] = 0.0
+        for k in ref:
+            lr = LRS[k](step - 1) if callable(LRS[k]) else LRS[k]
+            ref[k], mu[k], nu[k] = T.adam_step(ref[k], grads[k], mu[k], nu[k], lr=lr,
+                                               count=step)
+        opt.step({k: _t(g) for k, g in grads.items()})
+        torch.cuda.synchronize()
+        for k in ref:
+            assert_bit_exact(_np(dev[k]), ref[k], f"adam {k} step {step}")
+            assert_bit_exact(_np(opt.mu[k]), mu[k], f"adam mu {k} step {step}")
+            assert_bit_exact(_np(opt.nu[k]), nu[k], f"adam nu {k} step {step}")
+    reset = rng.uniform(size=n) < 0.3
+    opt.reset_rows(_t(reset))
+    torch.cuda.synchronize()
+    for k in ref:
+        m2, n2 = T.reset_rows(mu[k], nu[k], reset)
+        assert_bit_exact(_np(opt.mu[k]), m2, f"reset mu {k}")
+        assert_bit_exact(_np(opt.nu[k]), n2, f"reset nu {k}")
+
+
+def test_adam_rejects_bad_groups():
+    x = torch.zeros((4, 3), device="cuda")
+    with pytest.raises(ValueError):
+        optim.Adam({"a": x}, {"b": 1e-3})
+    opt = optim.Adam({"a": x}, {"a": 1e-3})
+    with pytest.raises(ValueError):
+        opt.step({"a": torch.zeros((4, 2), device="cuda")})
+
+
+def test_compute_relocation_within_one_ulp():
+    _case("compute_relocation")
+    rng = np.random.default_rng(0)
+    n = 5000
+    opac = rng.uniform(0.005, 0.999, n).astype(np.float32)
+    scales = rng.uniform(0.001, 0.5, (n, 3)).astype(np.float32)
+    ratios = rng.integers(1, 60, n).astype(np.float32)
+    ratios[:10] = [0.4, 1.5, 2.5, 50.5, 51.0, 52.0, 1e9, -3.0, float("nan"), 1.0]
+    ro, rs = T.compute_relocation(opac, scales, ratios, n_max=51)
+    go, gs = mcmc.compute_relocation(_t(opac), _t(scales), _t(ratios), mcmc.make_binoms(51))
+    assert _max_ulp(_np(go), ro) <= 1
+    assert _max_ulp(_np(gs), rs) <= 1
+
+
+def _scene(n, dead_frac, seed):
+    rng = np.random.default_rng(seed)
+    means = rng.uniform(-3, 3, (n, 3)).astype(np.float32)
+    log_scales = rng.normal(-5, 0.7, (n, 3)).astype(np.float32)
+    quats = rng.normal(size=(n, 4)).astype(np.float32)
+    colors = rng.normal(size=(n, 3)).astype(np.float32)
+    logit = rng.normal(1.0, 1.5, n).astype(np.float32)
+    dead = rng.uniform(size=n) < dead_frac
+    logit[dead] = rng.uniform(-25.0, -5.3, int(dead.sum())).astype(np.float32)
+    logit[:8] = [-5.2933, -5.2932, -5.29, -5.3, -30.0, -100.0, 0.0, 12.0]  # near the threshold
+    return means, log_scales, quats, colors, logit
+
+
+def _relocate_gpu(seed, arrays, n_max=51, min_opacity=0.005):
+    dev = [_t(a) for a in arrays]
+    reset, source = mcmc.relocate_(seed, *dev, mcmc.make_binoms(n_max), min_opacity,
+                                   return_source=True)
+    torch.cuda.synchronize()
+    return [_np(d) for d in dev], _np(source), _np(reset)
+
+
+@pytest.mark.parametrize("n,dead_frac,seed", [(1, 0.0, 0), (7, 1.0, 1), (4096, 0.05, 2),
+                                              (50000, 0.2, 3), (50000, 0.97, 4)])
+def test_relocate_matches_oracle(n, dead_frac, seed):
+    _case(f"relocate n={n} dead={dead_frac} seed={seed}")
+    arrays = tuple(np.ascontiguousarray(a[:n]) for a in _scene(max(n, 8), dead_frac, seed))
+    if dead_frac == 1.0:
+        arrays[4][:] = -40.0  # nothing alive: every row draws row 0
+    key = 0x9E3779B97F4A7C15 ^ seed
+    rm, rls, rq, rc, rl, rsrc, rreset = T.relocate(key, *arrays, n_max=51)
+    (gm, gls, gq, gc, gl), gsrc, greset = _relocate_gpu(key, arrays)
+    assert_bit_exact(gsrc, rsrc, "source")
+    assert np.array_equal(greset, rreset), "reset rows"
+    assert_bit_exact(gm, rm, "means")
+    assert_bit_exact(gq, rq, "quats")
+    assert_bit_exact(gc, rc, "logit_colors")
+    assert _max_ulp(gl, rl) <= 1, "logit_opacities"
+    assert _max_ulp(gls, rls) <= 1, "log_scales"
+
+
+def test_relocate_functional_equals_in_place_and_validates():
+    arrays = _scene(3000, 0.3, 9)
+    dev = [_t(a) for a in arrays]
+    binoms = mcmc.make_binoms(51)
+    new, reset = mcmc.relocate(5, *dev, binoms)
+    for d, a in zip(dev, arrays):  # inputs untouched
+        assert_bit_exact(_np(d), a, "relocate input")
+    (gm, gls, gq, gc, gl), _, greset = _relocate_gpu(5, arrays)
+    for x, y in zip(new, (gm, gls, gq, gc, gl)):
+        assert_bit_exact(_np(x), y, "functional vs in place")
+    assert np.array_equal(_np(reset), greset)
+    with pytest.raises(ValueError):
+        mcmc.relocate_(1, dev[0], dev[1], dev[2][:, :3].contiguous(), dev[3], dev[4], binoms)
+    with pytest.raises(ValueError):
+        mcmc.relocate_(1, *dev, mcmc.make_binoms(70))
+    ref = [[math.comb(i, k) if k <= i else 0 for k in range(6)] for i in range(6)]
+    assert mcmc.make_binoms(6).tolist() == ref
+
+
+def test_relocate_config4_size_properties():
+    """3M gaussians (config 4) with 5% dead: size-independent properties of the result."""
+    n = 3_000_000
+    _case(f"relocate properties n={n}")
+    arrays = _scene(n, 0.05, 11)
+    (gm, gls, gq, gc, gl), src, reset = _relocate_gpu(77, arrays)
+    (gm2, gls2, gq2, gc2, gl2), src2, reset2 = _relocate_gpu(77, arrays)
+    for x, y in zip((gm, gls, gq, gc, gl, src, reset), (gm2, gls2, gq2, gc2, gl2, src2, reset2)):
+        assert np.array_equal(x, y), "relocation is deterministic"
+    means, log_scales, quats, colors, logit = arrays
+    opac = T.sigmoid(logit)
+    dead = opac <= np.float32(0.005)
+    idx = np.arange(n)
+    assert np.array_equal(src[~dead], idx[~dead])
+    d = idx[dead]
+    s = src[dead]
+    assert (~dead[s]).all(), "sources are alive"
+    assert np.array_equal(gm[d], means[s]) and np.array_equal(gq[d], quats[s])
+    assert np.array_equal(gc[d], colors[s])
+    counts = np.bincount(s, minlength=n)
+    assert np.array_equal(reset, dead | (counts > 0))
+    keep = ~reset
+    for x, y in zip((gm, gls, gq, gc, gl), arrays):
+        assert np.array_equal(x[keep], y[keep])
+    assert np.array_equal(gl[d], gl[s]) and np.array_equal(gls[d], gls[s])
+    # r = counts + 1 copies at the new opacity composite to the old opacity
+    srcs = np.nonzero(counts)[0]
+    r = np.minimum(counts[srcs] + 1, 51).astype(np.float64)
+    new_o = 1.0 / (1.0 + np.exp(-gl[srcs].astype(np.float64)))
+    unclipped = new_o > 0.0051
+    comp = 1.0 - (1.0 - new_o) ** r
+    np.testing.assert_allclose(comp[unclipped], opac[srcs][unclipped], rtol=2e-5)
+    # draw frequencies by opacity decile of the alive rows follow the decile's opacity mass
+    alive = idx[~dead]
+    order = alive[np.argsort(opac[alive], kind="stable")]
+    bins = np.array_split(order, 10)
+    which = np.empty(n, np.int64)
+    for b, rows in enumerate(bins):
+        which[rows] = b
+    hist = np.bincount(which[s], minlength=10)
+    mass = np.array([opac[rows].astype(np.float64).sum() for rows in bins])
+    exp = mass / mass.sum() * d.size
+    chi2 = float(((hist - exp) ** 2 / exp).sum())
+    assert chi2 < 27.9, (hist, exp, chi2)  # p = 0.001 at 9 degrees of freedom
+    assert _lib.check_device() == 0
+
+
+def test_train_step_config4_small():
+    """The config-4 step end to end at 20k gaussians: finite loss, every group updated, dead
+    rows relocated and their moments zeroed, and the loss falls over a few steps."""
+    from splax_amd.scenes import make_scene
+    from splax_amd.train import TrainStep, params_from_scene
+
+    _case("train step config4 n=20000")
+    scene = make_scene(4, n=20_000)
+    params = params_from_scene(scene)
+    params["opac_logit"][:500] = -12.0  # dead rows to relocate
+    before = {k: v.clone() for k, v in params.items()}
+    train = TrainStep(params, viewmats=_t(scene.viewmats), targets=_t(scene.targets),
+                      background=_t(scene.background), img_shape=scene.img_shape, f=scene.f,
+                      antialiased=True, lrs={"means": 1e-3, "log_scales": 5e-3, "quats": 1e-3,
+                                             "colors_logit": 5e-2, "opac_logit": 5e-2})
+    losses = [float(train()) for _ in range(6)]
+    torch.cuda.synchronize()
+    assert all(np.isfinite(losses)) and losses[-1] < losses[0], losses
+    for k in params:
+        assert not torch.equal(train.params[k], before[k]), k
+    opac = torch.sigmoid(train.params["opac_logit"][:500])
+    assert bool((opac > 0.005).all()), "dead rows were relocated"
+    assert train.opt.count == 6
+    assert _lib.check_device() == 0

@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(handle, name), f"{name} declared in include/splat_hip.h but not exported"
     assert set(names) == set(_lib._SIGS), "Python binding and header disagree"
     lib = _lib.lib()
-    assert lib.splat_abi_version() == 5
+    assert lib.splat_abi_version() == 6
     assert isinstance(lib.splat_last_error(), bytes)
 
 
@@ -155,3 +155,22 @@ def test_abi_rejects_rows_that_are_neither_shared_nor_batched():
     rc = lib.splat_rasterize_fwd(null, null, n, null, n, null, n, null, 2, null, null, null,
                                  null, null, n, 3, 16, 16, null, null, null, null)
     assert rc == 1 and b"background" in lib.splat_last_error()
+
+
+def test_training_entry_points_validate_before_touching_the_device():
+    """Adam / relocation arguments are checked on the host (no device call is made)."""
+    lib = _lib.lib()
+    groups = (_lib.AdamGroup * 9)()
+    addr = ctypes.addressof(groups)
+    assert lib.splat_adam_step(None, addr, 9, 0.9, 0.999, 1e-8, 0.0, 1) == _lib.ERR_ARGS
+    assert lib.splat_adam_step(None, addr, 1, 0.9, 0.999, 1e-8, 0.0, 0) == _lib.ERR_ARGS
+    assert lib.splat_adam_reset_rows(None, addr, 9, None, 4) == _lib.ERR_ARGS
+    assert lib.splat_mcmc_relocate(None, None, None, None, None, None, 10, 63, 0.005, 1, None,
+                                   None) == _lib.ERR_ARGS
+    assert lib.splat_mcmc_relocate(None, None, None, None, None, None, 10, 51, 0.005, 1, None,
+                                   None) == _lib.ERR_ARGS
+    assert lib.splat_mcmc_compute_relocation(None, None, None, None, -1, 51, None,
+                                             None) == _lib.ERR_ARGS
+    assert lib.splat_mcmc_compute_relocation(None, None, None, None, 4, 0, None,
+                                             None) == _lib.ERR_ARGS
+    assert b"binomial" in lib.splat_last_error()
