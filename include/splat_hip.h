@@ -11,8 +11,8 @@
  * count exceeds num_gaussians (viewmat: exceeds 4 rows, transforms: exceeds num_transforms), and
  * broadcast otherwise. Flat item idx = image * num_gaussians + gaussian.
  *
- * Quaternions are xyzw here (the public Python API takes wxyz and rolls them,
- * splax/_project/_project.py:74-76). Matrices are row-major float32.
+ * Quaternions are xyzw, as the reference's kernels take them, unless a call selects wxyz (the
+ * public API's order, splax/_project/_project.py:74-76). Matrices are row-major float32.
  */
 #ifndef SPLAT_HIP_H
 #define SPLAT_HIP_H
@@ -30,9 +30,11 @@ typedef void* splat_stream_t; /* hipStream_t */
  * Outputs (total rows each): xys [total,2], depths [total], radii [total] int32, conics [total,3],
  * num_tiles_hit [total] int32, cum_tiles_hit [total] int32 (inclusive, global over the batch).
  * transforms: (rows_transforms, 4, 4); transform_ids: [num_gaussians] (read only when
- * has_transforms != 0). */
+ * has_transforms != 0). quats_wxyz = 0 reads quats as xyzw, the layout the reference's kernel
+ * receives after its roll (splax/_project/_project.py:76), so a binding of the reference passes
+ * 0; 1 reads the public API's wxyz directly and saves the roll. */
 int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
-                      const float* scales, int64_t rows_scales, const float* quats_xyzw,
+                      const float* scales, int64_t rows_scales, const float* quats,
                       int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
                       const float* opacities, int64_t rows_opac, const float* transforms,
                       int64_t rows_transforms, const int32_t* transform_ids,
@@ -40,14 +42,14 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
                       int64_t total, int32_t img_h, int32_t img_w, float fx, float fy, float cx,
                       float cy, float glob_scale, float clip_thresh, float* xys, float* depths,
                       int32_t* radii, float* conics, int32_t* num_tiles_hit,
-                      int32_t* cum_tiles_hit);
+                      int32_t* cum_tiles_hit, int32_t quats_wxyz);
 
 /* Replaces _project_bwd_warp (splax/_project/_kernels.py:257-341, FFI callable :344-353).
- * Outputs: v_mean3d [B*n,3], v_scale [B*n,3], v_quat [B*n,4] (xyzw), v_viewmat [4B,4],
- * v_transforms [B*num_transforms,4,4] (may be NULL when has_transforms == 0). All outputs are
- * fully written (no caller zeroing). */
+ * Outputs: v_mean3d [B*n,3], v_scale [B*n,3], v_quat [B*n,4] (in the quats layout chosen by
+ * quats_wxyz, as splat_project_fwd), v_viewmat [4B,4], v_transforms [B*num_transforms,4,4] (may
+ * be NULL when has_transforms == 0). All outputs are fully written (no caller zeroing). */
 int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
-                      const float* scales, int64_t rows_scales, const float* quats_xyzw,
+                      const float* scales, int64_t rows_scales, const float* quats,
                       int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
                       const int32_t* radii, int64_t rows_radii, const float* conics,
                       int64_t rows_conics, const float* v_xy, int64_t rows_vxy,
@@ -56,7 +58,8 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
                       const int32_t* transform_ids, int32_t num_gaussians,
                       int32_t num_transforms, int32_t has_transforms, int32_t B, float fx,
                       float fy, float glob_scale, float* v_mean3d, float* v_scale,
-                      float* v_quat, float* v_viewmat, float* v_transforms);
+                      float* v_quat, float* v_viewmat, float* v_transforms,
+                      int32_t quats_wxyz);
 
 /* Replaces _rasterize_warp (splax/_rasterize/_kernels.py:37-87, FFI callable :90-99): sort_and_bin
  * (one pinned device-to-host read of the intersection count) then the forward blend.
@@ -129,7 +132,11 @@ int splat_rasterize_depth_bwd(splat_stream_t stream, const float* colors, int64_
  * out_depth (may be NULL) selects the depth channel as in splat_rasterize_depth_fwd. records
  * (may be NULL) receives the packed blend record of every geometry item, 16 floats per item
  * ([B*num_gaussians, 16], 16-byte aligned), for splat_rasterize_bwd_sorted; it is written only
- * when M > 0. Other arguments and outputs as splat_rasterize_fwd. */
+ * when M > 0. compensate != 0 selects the antialiased blend of splax.render (splax/_render.py:
+ * 105-110): opacities are then the raw opacities, the blend uses opacities * rho(conic) with
+ * rho = sqrt(clip(1 - 0.3 (a + c) + 0.09 (a c - b^2), 0, 1)) (splax/_project/_project.py:95-117),
+ * and the intersection uses map_opacities as always. Other arguments and outputs as
+ * splat_rasterize_fwd. */
 int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t rows_colors,
                              const float* opacities, int64_t rows_opac,
                              const float* map_opacities, int64_t rows_map_opac,
@@ -139,7 +146,7 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
                              int32_t img_h, int32_t img_w, int64_t capacity, float* final_Ts,
                              int32_t* final_idx, float* out_img, float* out_depth,
                              int32_t* sorted_ids, int32_t* sorted_pos, int32_t* tile_bins,
-                             float* records, int64_t* num_intersects);
+                             float* records, int64_t* num_intersects, int32_t compensate);
 
 /* Backward over the sorted lists kept by splat_rasterize_fwd_keep (no re-sort). Arguments as
  * splat_rasterize_bwd plus sorted_ids / sorted_pos / tile_bins / records / num_intersects of
@@ -147,7 +154,8 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
  * inputs, which must be the forward's); the outputs equal splat_rasterize_bwd's (same kernels;
  * additions can differ in order only among a tile's four quadrant waves). v_depths (may be NULL)
  * selects the depth channel as in splat_rasterize_depth_bwd (then depths and v_out_depth are
- * read). */
+ * read). compensate as in the forward: v_opacity is then the raw opacities' cotangent and
+ * v_conic includes the cotangent through rho. */
 int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64_t rows_colors,
                                const float* opacities, int64_t rows_opac,
                                const float* background, int64_t rows_bg, const float* xys,
@@ -160,7 +168,8 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
                                int64_t vout_rows, const float* v_out_depth, int64_t vdepth_rows,
                                int32_t num_gaussians, int32_t B_out, int32_t B_geom,
                                int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
-                               float* v_xy, float* v_conic, float* v_depths);
+                               float* v_xy, float* v_conic, float* v_depths,
+                               int32_t compensate);
 
 /* Replaces sort_and_bin (splax/_rasterize/_sort/_sort.py:29-171), exposed for callers that keep
  * the sorted lists: writes the M sorted keys (as int64: the packed 32-bit key widened, or the

@@ -288,3 +288,46 @@ def project_bwd(means, scales, quats_xyzw, viewmat, radii, conics, v_xy, v_depth
 def set_threads(n: int) -> int:
     """Set the oracle's OpenMP thread count; returns the count in effect."""
     return int(lib().oracle_set_threads(ctypes.c_int(int(n))))
+
+
+# ---------------------------------------------------------------- antialiasing compensation
+
+_EPS = np.float32(0.3)        # splax/_project/_project.py:95 (eps), as float32
+_EPS2 = np.float32(0.3 * 0.3)  # the reference's (eps * eps), formed in Python, as float32
+
+
+def compensation_rho(conics):
+    """opacity_compensation's rho (splax/_project/_project.py:113-117) in float32, in the
+    expression's order; returns (rho, rho2) with rho2 the unclipped argument. Items with
+    radii <= 0 take 1 in the reference; the fused blend never reads them."""
+    cn = np.asarray(conics, np.float32).reshape(-1, 3)
+    a, b, c = cn[:, 0], cn[:, 1], cn[:, 2]
+    with np.errstate(invalid="ignore"):
+        rho2 = (np.float32(1.0) - _EPS * (a + c)) + _EPS2 * (a * c - b * b)
+        cl = np.where(rho2 < 0, np.float32(0), rho2)
+        cl = np.where(cl > 1, np.float32(1), cl)
+        return np.sqrt(cl).astype(np.float32), rho2.astype(np.float32)
+
+
+def compensation_vjp(v_blend_opac, opac, conics):
+    """Cotangents of blend_opac = opac * rho(conics) for a blend-opacity cotangent, by the
+    reverse-mode rules of the reference's expression (sqrt' = 0.5 / rho; maximum / minimum pass
+    1 inside, 1/2 at a tie, 0 outside); returns (v_opac, v_conics) in float32, per item."""
+    f = np.float32
+    vbo = np.asarray(v_blend_opac, np.float32).reshape(-1)
+    o = np.asarray(opac, np.float32).reshape(-1)
+    cn = np.asarray(conics, np.float32).reshape(-1, 3)
+    a, b, c = cn[:, 0], cn[:, 1], cn[:, 2]
+    rho, rho2 = compensation_rho(cn)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        v_o = vbo * rho
+        v_rho = vbo * o
+        v_cl = v_rho * (f(0.5) / rho)
+        m_lo = np.where(rho2 > 0, f(1), np.where(rho2 == 0, f(0.5), f(0)))
+        y = np.where(rho2 > 0, rho2, f(0))
+        m_hi = np.where(y < 1, f(1), np.where(y == 1, f(0.5), f(0)))
+        v_r2 = (v_cl * m_hi) * m_lo
+        v_s = -(_EPS * v_r2)
+        v_t = _EPS2 * v_r2
+        vc = np.stack([v_s + v_t * c, -(v_t * b) - v_t * b, v_s + v_t * a], axis=1)
+    return v_o.astype(np.float32), vc.astype(np.float32)

@@ -34,9 +34,9 @@ class AdamGroup(ctypes.Structure):
 # name -> argtypes, in the order of include/splat_hip.h
 _SIGS = {
     "splat_project_fwd": [_vp] + [_vp, _i64] * 6 + [_vp, _i32, _i32, _i32, _i64, _i32, _i32]
-    + [_f32] * 6 + [_vp] * 6,
+    + [_f32] * 6 + [_vp] * 6 + [_i32],
     "splat_project_bwd": [_vp] + [_vp, _i64] * 10 + [_vp, _i32, _i32, _i32, _i32, _f32, _f32,
-                                                     _f32] + [_vp] * 5,
+                                                     _f32] + [_vp] * 5 + [_i32],
     "splat_rasterize_fwd": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_i32] * 4 + [_vp] * 4,
     "splat_rasterize_depth_fwd": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_i32] * 4 + [_vp] * 5,
     "splat_rasterize_bwd": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_vp, _vp, _vp, _i64]
@@ -44,9 +44,9 @@ _SIGS = {
     "splat_rasterize_depth_bwd": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_vp, _vp, _vp, _i64]
     + [_vp, _i64] + [_i32] * 5 + [_vp] * 5,
     "splat_rasterize_fwd_keep": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_i32] * 4 + [_i64]
-    + [_vp] * 9,
+    + [_vp] * 9 + [_i32],
     "splat_rasterize_bwd_sorted": [_vp] + [_vp, _i64] * 3 + [_vp] * 8 + [_i64]
-    + [_vp, _vp, _vp, _i64] + [_vp, _i64] + [_i32] * 5 + [_vp] * 5,
+    + [_vp, _vp, _vp, _i64] + [_vp, _i64] + [_i32] * 5 + [_vp] * 5 + [_i32],
     "splat_sort_and_bin": [_vp] + [_vp] * 4 + [_vp, _i64, _vp] + [_i32] * 4
     + [_vp, _vp, _i64, _vp, _vp],
     "splat_set_wide_keys": [_i32],

@@ -31,10 +31,12 @@ def rows(t: torch.Tensor, width: int) -> int:
     return t.numel() // width
 
 
-def project_fwd(means, scales, quats_xyzw, viewmat, opac, transforms, transform_ids, *, n,
-                total, num_transforms, has_transforms, img_shape, f, c, glob_scale, clip_thresh):
-    """_project_warp (splax/_project/_kernels.py:31-107) over ``total`` flat items."""
-    means, scales, quats, viewmat, opac = map(_f32, (means, scales, quats_xyzw, viewmat, opac))
+def project_fwd(means, scales, quats, viewmat, opac, transforms, transform_ids, *, n,
+                total, num_transforms, has_transforms, img_shape, f, c, glob_scale, clip_thresh,
+                quats_wxyz=False):
+    """_project_warp (splax/_project/_kernels.py:31-107) over ``total`` flat items; quats are
+    xyzw as the reference's kernel takes them, or wxyz with ``quats_wxyz``."""
+    means, scales, quats, viewmat, opac = map(_f32, (means, scales, quats, viewmat, opac))
     transforms = _f32(transforms)
     transform_ids = _i32(transform_ids)
     dev = _lib.require_gpu(means, scales, quats, viewmat, opac, transforms, transform_ids)
@@ -54,18 +56,19 @@ def project_fwd(means, scales, quats_xyzw, viewmat, opac, transforms, transform_
             p(quats), rows(quats, 4), p(viewmat), rows(viewmat, 4), p(opac), opac.numel(),
             p(transforms), rows(transforms, 16), p(transform_ids), n, num_transforms,
             int(has_transforms), total, H, W, f[0], f[1], c[0], c[1], glob_scale, clip_thresh,
-            p(xys), p(depths), p(radii), p(conics), p(nth), p(cum))
+            p(xys), p(depths), p(radii), p(conics), p(nth), p(cum), int(quats_wxyz))
     _lib.check(st, "project")
     return xys, depths, radii, conics, nth, cum
 
 
-def project_bwd(means, scales, quats_xyzw, viewmat, radii, conics, v_xy, v_depth, v_conic,
+def project_bwd(means, scales, quats, viewmat, radii, conics, v_xy, v_depth, v_conic,
                 transforms, transform_ids, *, n, B, num_transforms, has_transforms, f,
-                glob_scale):
+                glob_scale, quats_wxyz=False):
     """_project_bwd_warp (splax/_project/_kernels.py:257-341).
 
-    v_depth may be None (a zero depth cotangent); v_tf is None without transforms."""
-    means, scales, quats, viewmat, conics = map(_f32, (means, scales, quats_xyzw, viewmat,
+    v_depth may be None (a zero depth cotangent); v_tf is None without transforms. v_quat comes
+    in the layout of quats (xyzw, or wxyz with ``quats_wxyz``)."""
+    means, scales, quats, viewmat, conics = map(_f32, (means, scales, quats, viewmat,
                                                        conics))
     v_xy, v_conic, transforms = map(_f32, (v_xy, v_conic, transforms))
     v_depth = None if v_depth is None else _f32(v_depth)
@@ -88,7 +91,7 @@ def project_bwd(means, scales, quats_xyzw, viewmat, radii, conics, v_xy, v_depth
             0 if v_depth is None else v_depth.numel(), p(v_conic), rows(v_conic, 3),
             p(transforms), rows(transforms, 16), p(transform_ids), n, num_transforms,
             int(has_transforms), B, f[0], f[1], glob_scale, p(v_mean), p(v_scale), p(v_quat),
-            p(v_view), p(v_tf))
+            p(v_view), p(v_tf), int(quats_wxyz))
     _lib.check(st, "project_bwd")
     return v_mean, v_scale, v_quat, v_view, v_tf
 
@@ -137,7 +140,7 @@ class KeptSort(NamedTuple):
 
 
 def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, conics, cum, *, n,
-                       B, img_shape, render_depth=False):
+                       B, img_shape, render_depth=False, compensate=False):
     """Forward that also keeps the sorted lists and packed records for the backward; returns
     (img, Ts, fidx, KeptSort, depth or None).
 
@@ -170,7 +173,7 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
                 _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
                 p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys),
                 p(depths), p(radii), p(conics), p(cum), n, B, H, W, cap, p(Ts), p(fidx), p(img),
-                p(depth), p(ids), p(pos), p(bins), p(recs), ctypes.byref(m))
+                p(depth), p(ids), p(pos), p(bins), p(recs), ctypes.byref(m), int(compensate))
         if st == _lib.ERR_TOO_MANY and m.value > cap:
             cap = int(m.value * 1.25) + 1
             _KEEP_CAPACITY[key] = cap
@@ -190,7 +193,7 @@ def _bwd_outputs(nout, dev, with_depth):
 
 def rasterize_bwd_sorted(colors, opac, background, xys, depths, conics, cum, kept: KeptSort,
                          final_Ts, final_idx, v_out, *, n, B_out, B_geom, img_shape,
-                         v_out_depth=None):
+                         v_out_depth=None, compensate=False):
     """Backward over the sorted lists (and records) of rasterize_fwd_keep for the same inputs
     (no re-sort); with v_out_depth also the depth channel's v_depths (last)."""
     colors, opac, background, xys, depths, conics, final_Ts, v_out = map(
@@ -213,7 +216,7 @@ def rasterize_bwd_sorted(colors, opac, background, xys, depths, conics, cum, kep
             p(pos), p(bins), p(recs), M, p(final_Ts), p(final_idx), p(v_out),
             v_out.numel() // (3 * W),
             p(vd), 0 if vd is None else vd.numel() // W, n, B_out, B_geom, H, W, p(v_colors),
-            p(v_opac), p(v_xy), p(v_conic), p(v_depths))
+            p(v_opac), p(v_xy), p(v_conic), p(v_depths), int(compensate))
     _lib.check(st, "rasterize_bwd")
     if vd is None:
         return v_colors, v_opac, v_xy, v_conic

@@ -48,14 +48,14 @@ def _flat(t: torch.Tensor, width: int) -> torch.Tensor:
 
 class _ProjectFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, means, scales, quats_xyzw, viewmat, opac, transforms, tf_ids, statics):
+    def forward(ctx, means, scales, quats_wxyz, viewmat, opac, transforms, tf_ids, statics):
         n, B, K, has_tf, img_shape, f, c, glob_scale, clip_thresh = statics
         xys, depths, radii, conics, nth, cum = _ops.project_fwd(
-            _flat(means, 3), _flat(scales, 3), _flat(quats_xyzw, 4), viewmat.reshape(-1, 4),
+            _flat(means, 3), _flat(scales, 3), _flat(quats_wxyz, 4), viewmat.reshape(-1, 4),
             opac.reshape(-1), transforms.reshape(-1, 4, 4), tf_ids.reshape(-1), n=n, total=B * n,
             num_transforms=K, has_transforms=has_tf, img_shape=img_shape, f=f, c=c,
-            glob_scale=glob_scale, clip_thresh=clip_thresh)
-        ctx.save_for_backward(means, scales, quats_xyzw, viewmat, transforms, tf_ids, radii,
+            glob_scale=glob_scale, clip_thresh=clip_thresh, quats_wxyz=True)
+        ctx.save_for_backward(means, scales, quats_wxyz, viewmat, transforms, tf_ids, radii,
                               conics)
         ctx.statics = statics
         ctx.mark_non_differentiable(radii, nth, cum)
@@ -76,7 +76,7 @@ class _ProjectFn(torch.autograd.Function):
             conics, v_xys.reshape(-1, 2), None if v_depths is None else v_depths.reshape(-1),
             v_conics.reshape(-1, 3),
             transforms.reshape(-1, 4, 4), tf_ids.reshape(-1), n=n, B=B, num_transforms=K,
-            has_transforms=has_tf, f=f, glob_scale=glob_scale)
+            has_transforms=has_tf, f=f, glob_scale=glob_scale, quats_wxyz=True)
 
         def fold(g: torch.Tensor, like: torch.Tensor, width: int) -> torch.Tensor:
             if g.numel() == like.numel():  # one image, or a batched operand
@@ -145,13 +145,12 @@ def project(mean3ds: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor,
                       gaussian_transforms=(gaussian_transforms, 3))
     batched = B is not None
     Bv = B if batched else 1
-    # Warp works scalar-last (xyzw); roll once here so autograd rolls the gradient back
-    # (splax/_project/_project.py:74-76).
-    quats_xyzw = torch.roll(quats, -1, dims=-1)
+    # The reference rolls wxyz to its kernel's xyzw here (splax/_project/_project.py:74-76);
+    # the library reads wxyz directly and returns the quaternion gradient in wxyz.
     statics = (n, Bv, K, has_tf, tuple(img_shape), tuple(map(float, f)), tuple(map(float, c)),
                float(glob_scale), float(clip_thresh))
     xys, depths, radii, conics, nth, cum = _ProjectFn.apply(
-        mean3ds, scales, quats_xyzw, viewmat, opacities, gaussian_transforms,
+        mean3ds, scales, quats, viewmat, opacities, gaussian_transforms,
         transform_ids.to(torch.int32), statics)
     lead = (Bv, n) if batched else (n,)
     return (xys.reshape(*lead, 2), depths.reshape(*lead, 1), radii.reshape(*lead, 1),

@@ -46,14 +46,14 @@ class _RasterizeFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, colors, opac, map_opac, background, xys, depths, radii, conics, cum,
                 statics):
-        n, B, img_shape, render_depth = statics
+        n, B, img_shape, render_depth, compensate = statics
         # The sorted lists stay resident for the backward (the reference re-sorts there,
         # splax/_rasterize/_kernels.py:422); the sort is deterministic, so both are identical.
         img, Ts, fidx, kept, depth = _ops.rasterize_fwd_keep(
             colors.reshape(-1, 3), opac.reshape(-1), map_opac.reshape(-1),
             background.reshape(-1, 3), xys.reshape(-1, 2), depths.reshape(-1), radii.reshape(-1),
             conics.reshape(-1, 3), cum.reshape(-1), n=n, B=B, img_shape=img_shape,
-            render_depth=render_depth)
+            render_depth=render_depth, compensate=compensate)
         ctx.save_for_backward(colors, opac, background, xys, depths, conics, cum, Ts, fidx,
                               kept.ids, kept.pos, kept.bins, kept.records)
         ctx.statics = statics
@@ -70,7 +70,7 @@ class _RasterizeFn(torch.autograd.Function):
     def backward(ctx, v_img, v_depth, _v_Ts, _v_idx):
         colors, opac, background, xys, depths, conics, cum, Ts, fidx, ids, pos, bins, recs = \
             ctx.saved_tensors
-        n, B, img_shape, render_depth = ctx.statics
+        n, B, img_shape, render_depth, compensate = ctx.statics
         H, W = img_shape
         if v_img is None:
             v_img = torch.zeros((B * H, W, 3), device=xys.device)
@@ -82,7 +82,7 @@ class _RasterizeFn(torch.autograd.Function):
             _ops.KeptSort(ids, pos, bins, ctx.num_intersects, recs), Ts, fidx,
             v_img.reshape(-1, 3), n=n, B_out=B,
             B_geom=B, img_shape=img_shape,
-            v_out_depth=v_depth.reshape(-1, W) if render_depth else None)
+            v_out_depth=v_depth.reshape(-1, W) if render_depth else None, compensate=compensate)
         v_colors, v_opac, v_xy, v_conic = grads[:4]
 
         def fold(g: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
@@ -98,7 +98,9 @@ class _RasterizeFn(torch.autograd.Function):
 
 
 def _rasterize_checked(colors, opacities, background, xys, depths, radii, conics, cum_tiles_hit,
-                       img_shape, map_opacities, render_depth):
+                       img_shape, map_opacities, render_depth, compensate=False):
+    """compensate: ``opacities`` are raw and the blend uses opacities * rho(conics), the
+    antialiased render of splax/_render.py:105-110 fused into the library's kernels."""
     n = int(colors.shape[-2])
     H, W = img_shape
     if map_opacities is None:
@@ -121,7 +123,8 @@ def _rasterize_checked(colors, opacities, background, xys, depths, radii, conics
     check_key_fits(Bg, int(H), int(W))
     img, depth, _, _ = _RasterizeFn.apply(colors, opacities, map_opacities, background, xys,
                                           depths, radii, conics, cum_tiles_hit,
-                                          (n, Bg, (int(H), int(W)), render_depth))
+                                          (n, Bg, (int(H), int(W)), render_depth,
+                                           bool(compensate)))
     img = img.reshape(Bg, H, W, 3) if batched else img.reshape(H, W, 3)
     if not render_depth:
         return img, None

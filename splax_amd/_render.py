@@ -11,8 +11,8 @@ from collections.abc import Sequence
 
 import torch
 
-from splax_amd._project import opacity_compensation, project, transform_ids
-from splax_amd._rasterize import rasterize, rasterize_depth
+from splax_amd._project import project, transform_ids
+from splax_amd._rasterize import _rasterize_checked
 
 
 def render(means3d: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor,
@@ -36,18 +36,12 @@ def render(means3d: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor,
         means3d, scales, quats, viewmat, opacities=opacities, img_shape=img_shape, f=f, c=c,
         glob_scale=glob_scale, clip_thresh=clip_thresh, gaussian_transforms=gaussian_transforms,
         transform_ids=tf_ids)
-    blend_opacities = opacities
-    map_opacities = None
-    if antialiased:
-        rho = opacity_compensation(conics, radii)  # (N,) or (B, N)
-        if opacities.ndim >= 2 and opacities.shape[-1] == 1:
-            rho = rho.unsqueeze(-1)
-        blend_opacities = opacities * rho  # per image when the render is batched
-        map_opacities = opacities  # the tile intersection stays on the raw opacity
-    inputs = (colors, blend_opacities, background, xys, depths, radii, conics, cum)
-    if render_depth:
-        return rasterize_depth(*inputs, img_shape=img_shape, map_opacities=map_opacities)
-    return rasterize(*inputs, img_shape=img_shape, map_opacities=map_opacities), None
+    # antialiased: the blend uses opacities * opacity_compensation(conics, radii) and the tile
+    # intersection the raw opacities (splax/_render.py:105-110); the library evaluates the
+    # compensation and its gradient inside the blend's record packing and gradient gather.
+    img, depth = _rasterize_checked(colors, opacities, background, xys, depths, radii, conics,
+                                    cum, img_shape, None, render_depth, compensate=antialiased)
+    return img, depth
 
 
 def render_log(means3d: torch.Tensor, log_scales: torch.Tensor, quats: torch.Tensor,

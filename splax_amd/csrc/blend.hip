@@ -58,6 +58,7 @@ struct PackParams {
     const float* opac; int64_t rows_opac;
     const float* xys; const float* conics; const float* depths;
     int64_t total;
+    int32_t compensate;  // blend with opac * rho(conic)
     float4* recs;
 };
 
@@ -70,7 +71,11 @@ __global__ void __launch_bounds__(256) pack_records_kernel(PackParams P) {
     if (g < P.total) {
         const float2 xy = reinterpret_cast<const float2*>(P.xys)[g];
         const float a = P.conics[3 * g], b = P.conics[3 * g + 1], c = P.conics[3 * g + 2];
-        const float o = P.opac[g % P.rows_opac];
+        float o = P.opac[g % P.rows_opac];
+        if (P.compensate) {
+            float rho2;
+            o = o * compensation_rho(a, b, c, rho2);
+        }
         const int64_t cg = g % P.rows_colors;
         float smax;
         if (o > 0.0f) {
@@ -286,6 +291,7 @@ int launch_pack_records(const RasterInputs& in, float4* recs, hipStream_t stream
     K.colors = in.colors; K.rows_colors = in.rows_colors;
     K.opac = in.opac; K.rows_opac = in.rows_opac;
     K.xys = in.xys; K.conics = in.conics; K.depths = in.depths;
+    K.compensate = in.compensate;
     K.total = (int64_t)in.B_geom * in.n;
     K.recs = recs;
     if (K.total <= 0) return 0;
@@ -531,7 +537,33 @@ struct GatherParams {
     int64_t M; int64_t nout; int32_t n; int32_t sel_geom;
     float* v_colors; float* v_opacity; float* v_xy; float* v_conic;
     float* v_depths;  // NG == 10
+    const float* opac; int64_t rows_opac; int32_t compensate;
 };
+
+// Cotangents of blend_opac = opac * rho(conic) (splax/_render.py:105-109 with
+// splax/_project/_project.py:113-117) for a blend-opacity cotangent vbo, by reverse-mode rules of
+// the reference's expression: sqrt' = 0.5 / rho, maximum / minimum pass 1 strictly inside, 1/2 at
+// a tie and 0 outside. Returns the raw-opacity cotangent and adds the conic cotangent to vc.
+// Items without intersections carry vbo = 0 and a zero conic (rho = 1), so the where(radii > 0)
+// select adds nothing for them.
+__device__ __forceinline__ float compensation_vjp(float vbo, float o, float a, float b, float c,
+                                                  float vc[3]) {
+    float rho2;
+    const float rho = compensation_rho(a, b, c, rho2);
+    const float v_o = vbo * rho;
+    const float v_rho = vbo * o;
+    const float v_cl = v_rho * (0.5f / rho);
+    const float m_lo = rho2 > 0.0f ? 1.0f : (rho2 == 0.0f ? 0.5f : 0.0f);
+    const float y = rho2 > 0.0f ? rho2 : 0.0f;
+    const float m_hi = y < 1.0f ? 1.0f : (y == 1.0f ? 0.5f : 0.0f);
+    const float v_r2 = (v_cl * m_hi) * m_lo;
+    const float v_s = -(kDilation * v_r2);  // through 1 - eps (a + c)
+    const float v_t = kDilation2 * v_r2;    // through eps^2 (a c - b b)
+    vc[0] = vc[0] + (v_s + v_t * c);
+    vc[1] = vc[1] + (-(v_t * b) - v_t * b);
+    vc[2] = vc[2] + (v_s + v_t * a);
+    return v_o;
+}
 
 template <int NG>
 __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
@@ -557,18 +589,21 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
     P.v_colors[3 * og] = s[0];
     P.v_colors[3 * og + 1] = s[1];
     P.v_colors[3 * og + 2] = s[2];
-    P.v_conic[3 * og] = s[3];
-    P.v_conic[3 * og + 1] = s[4];
-    P.v_conic[3 * og + 2] = s[5];
+    float vc[3] = {s[3], s[4], s[5]};
+    float vo = s[8];
     float vx = 0.f, vy = 0.f;
-    if (s[6] != 0.f || s[7] != 0.f) {
+    if (s[6] != 0.f || s[7] != 0.f || P.compensate) {
         const float a = P.conics[3 * gi], b = P.conics[3 * gi + 1], c = P.conics[3 * gi + 2];
         vx = a * s[6] + b * s[7];
         vy = b * s[6] + c * s[7];
+        if (P.compensate) vo = compensation_vjp(vo, P.opac[gi % P.rows_opac], a, b, c, vc);
     }
+    P.v_conic[3 * og] = vc[0];
+    P.v_conic[3 * og + 1] = vc[1];
+    P.v_conic[3 * og + 2] = vc[2];
     P.v_xy[2 * og] = vx;
     P.v_xy[2 * og + 1] = vy;
-    P.v_opacity[og] = s[8];
+    P.v_opacity[og] = vo;
     if constexpr (NG == 10) P.v_depths[og] = s[9];
 }
 
@@ -603,6 +638,7 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
     G.nout = nout; G.n = in.n; G.sel_geom = sel_geom;
     G.v_colors = a.v_colors; G.v_opacity = a.v_opacity; G.v_xy = a.v_xy; G.v_conic = a.v_conic;
     G.v_depths = a.v_depths;
+    G.opac = in.opac; G.rows_opac = in.rows_opac; G.compensate = in.compensate;
     const dim3 grid((unsigned)((nout + 255) / 256));
     if (depth)
         hipLaunchKernelGGL(grad_gather_kernel<10>, grid, dim3(256), 0, stream, G);

@@ -330,7 +330,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 6; }
+int splat_abi_version(void) { return 7; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();
@@ -385,7 +385,7 @@ int splat_get_stage_times(double* ms, int64_t* calls, int32_t n) {
 }
 
 int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
-                      const float* scales, int64_t rows_scales, const float* quats_xyzw,
+                      const float* scales, int64_t rows_scales, const float* quats,
                       int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
                       const float* opacities, int64_t rows_opac, const float* transforms,
                       int64_t rows_transforms, const int32_t* transform_ids,
@@ -393,7 +393,7 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
                       int64_t total, int32_t img_h, int32_t img_w, float fx, float fy, float cx,
                       float cy, float glob_scale, float clip_thresh, float* xys, float* depths,
                       int32_t* radii, float* conics, int32_t* num_tiles_hit,
-                      int32_t* cum_tiles_hit) {
+                      int32_t* cum_tiles_hit, int32_t quats_wxyz) {
     if (num_gaussians <= 0 || total < 0 || total % num_gaussians != 0 || img_h <= 0 ||
         img_w <= 0)
         return fail(kErrArgs, "project_fwd: invalid sizes");
@@ -417,7 +417,7 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
     ProjectArgs a;
     a.means = means3d; a.rows_means = rows_means;
     a.scales = scales; a.rows_scales = rows_scales;
-    a.quats = quats_xyzw; a.rows_quats = rows_quats;
+    a.quats = quats; a.rows_quats = rows_quats;
     a.viewmat = viewmat; a.rows_viewmat = rows_viewmat;
     a.opacities = opacities; a.rows_opac = rows_opac;
     a.transforms = transforms; a.rows_transforms = has_transforms ? rows_transforms : 0;
@@ -429,6 +429,7 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
     a.glob_scale = glob_scale; a.clip_thresh = clip_thresh;
     a.xys = xys; a.depths = depths; a.radii = radii; a.conics = conics;
     a.num_tiles_hit = num_tiles_hit; a.cum_tiles_hit = cum_tiles_hit;
+    a.quats_wxyz = quats_wxyz != 0;
     StageTimer tm(s, kStageProject);
     rc = launch_project_fwd(a, sc, s);
     if (rc && g_last_error.empty()) set_error("project_fwd launch failed");
@@ -436,7 +437,7 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
 }
 
 int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
-                      const float* scales, int64_t rows_scales, const float* quats_xyzw,
+                      const float* scales, int64_t rows_scales, const float* quats,
                       int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
                       const int32_t* radii, int64_t rows_radii, const float* conics,
                       int64_t rows_conics, const float* v_xy, int64_t rows_vxy,
@@ -445,7 +446,8 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
                       const int32_t* transform_ids, int32_t num_gaussians,
                       int32_t num_transforms, int32_t has_transforms, int32_t B, float fx,
                       float fy, float glob_scale, float* v_mean3d, float* v_scale,
-                      float* v_quat, float* v_viewmat, float* v_transforms) {
+                      float* v_quat, float* v_viewmat, float* v_transforms,
+                      int32_t quats_wxyz) {
     if (num_gaussians <= 0 || B <= 0) return fail(kErrArgs, "project_bwd: invalid sizes");
     if (!rows_match(rows_means, num_gaussians, B) || !rows_match(rows_scales, num_gaussians, B) ||
         !rows_match(rows_quats, num_gaussians, B) || !rows_match(rows_viewmat, 4, B) ||
@@ -463,7 +465,7 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
     ProjectBwdArgs a;
     a.means = means3d; a.rows_means = rows_means;
     a.scales = scales; a.rows_scales = rows_scales;
-    a.quats = quats_xyzw; a.rows_quats = rows_quats;
+    a.quats = quats; a.rows_quats = rows_quats;
     a.viewmat = viewmat; a.rows_viewmat = rows_viewmat;
     a.radii = radii; a.rows_radii = rows_radii;
     a.conics = conics; a.rows_conics = rows_conics;
@@ -477,6 +479,7 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
     a.fx = fx; a.fy = fy; a.glob_scale = glob_scale;
     a.v_mean3d = v_mean3d; a.v_scale = v_scale; a.v_quat = v_quat;
     a.v_viewmat = v_viewmat; a.v_transforms = has_transforms ? v_transforms : nullptr;
+    a.quats_wxyz = quats_wxyz != 0;
     StageTimer tm(s, kStageProjectBwd);
     int rc = launch_project_bwd(a, s);
     if (rc && g_last_error.empty()) set_error("project_bwd launch failed");
@@ -737,19 +740,21 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
                              int32_t img_h, int32_t img_w, int64_t capacity, float* final_Ts,
                              int32_t* final_idx, float* out_img, float* out_depth,
                              int32_t* sorted_ids, int32_t* sorted_pos, int32_t* tile_bins,
-                             float* records, int64_t* num_intersects) {
+                             float* records, int64_t* num_intersects, int32_t compensate) {
     if (capacity < 0 || !tile_bins || (capacity > 0 && (!sorted_ids || !sorted_pos)))
         return fail(kErrArgs, "rasterize_fwd_keep: missing sorted-list buffers");
     const RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac,
                                           map_opacities, rows_map_opac, background, rows_bg, xys,
                                           depths, radii, conics, cum_tiles_hit, num_gaussians, B,
                                           img_h, img_w);
+    RasterInputs inc = in;
+    inc.compensate = compensate != 0;
     SortTargets tgt;
     tgt.capacity = capacity;
     tgt.ids = sorted_ids;
     tgt.pos = sorted_pos;
     tgt.bins = tile_bins;
-    return rasterize_fwd_impl(static_cast<hipStream_t>(stream), in, &tgt, final_Ts, final_idx,
+    return rasterize_fwd_impl(static_cast<hipStream_t>(stream), inc, &tgt, final_Ts, final_idx,
                               out_img, out_depth, records, num_intersects);
 }
 
@@ -765,14 +770,15 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
                                int64_t vout_rows, const float* v_out_depth, int64_t vdepth_rows,
                                int32_t num_gaussians, int32_t B_out, int32_t B_geom,
                                int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
-                               float* v_xy, float* v_conic, float* v_depths) {
+                               float* v_xy, float* v_conic, float* v_depths,
+                               int32_t compensate) {
     if (num_intersects < 0 || !tile_bins ||
         (num_intersects > 0 && (!sorted_ids || !sorted_pos)))
         return fail(kErrArgs, "rasterize_bwd_sorted: invalid sorted lists");
-    const RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac, opacities,
-                                          rows_opac, background, rows_bg, xys, depths, nullptr,
-                                          conics, cum_tiles_hit, num_gaussians, B_geom, img_h,
-                                          img_w);
+    RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac, opacities,
+                                    rows_opac, background, rows_bg, xys, depths, nullptr, conics,
+                                    cum_tiles_hit, num_gaussians, B_geom, img_h, img_w);
+    in.compensate = compensate != 0;
     const BlendBwdArgs a = bwd_args(final_Ts, final_idx, v_out_img, vout_rows, B_out, v_colors,
                                     v_opacity, v_xy, v_conic, v_out_depth, vdepth_rows, v_depths);
     const KeptLists kept{sorted_ids, sorted_pos, tile_bins, num_intersects, records};

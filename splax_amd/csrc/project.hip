@@ -31,6 +31,7 @@ struct ProjectParams {
     float fx, fy, cx, cy, glob_scale, clip_thresh;
     float* xys; float* depths; int32_t* radii; float* conics;
     int32_t* num_tiles_hit; int32_t* cum_tiles_hit;
+    int32_t wxyz;  // quaternion storage order: 1 = wxyz (the public API's), 0 = xyzw
     // scan state
     uint64_t* status; uint32_t epoch; uint32_t* err;
 };
@@ -115,8 +116,13 @@ __device__ __forceinline__ int32_t project_item(const ProjectParams& P, int64_t 
     bool moved = apply_transform(P.transforms, bid, P.num_transforms,
                                  P.rows_transforms > P.num_transforms, tf_id, mean, R_tf);
     float W[9], p[3], M[9];
-    project_geom(mean, P.quats + 4 * q_idx, P.scales + 3 * s_idx, P.glob_scale,
-                 P.viewmat + vb * 4, R_tf, moved, W, p, M);
+    const float* qp = P.quats + 4 * q_idx;
+    float q[4] = {qp[0], qp[1], qp[2], qp[3]};
+    if (P.wxyz) {  // (w, x, y, z) -> (x, y, z, w)
+        q[0] = qp[1]; q[1] = qp[2]; q[2] = qp[3]; q[3] = qp[0];
+    }
+    project_geom(mean, q, P.scales + 3 * s_idx, P.glob_scale, P.viewmat + vb * 4, R_tf, moved,
+                 W, p, M);
     do {
         if (p[2] <= P.clip_thresh) break;
         float V[9];
@@ -251,6 +257,7 @@ struct ProjectBwdParams {
     int32_t n, num_transforms, has_transforms, B, blocks_per_image;
     float fx, fy, glob_scale;
     float* v_mean3d; float* v_scale; float* v_quat; float* v_viewmat; float* v_transforms;
+    int32_t wxyz;  // quats and v_quat stored wxyz (1) or xyzw (0)
 };
 
 __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdParams P) {
@@ -296,6 +303,9 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
                                     P.rows_transforms > P.num_transforms, tf_id, mean, R_tf);
             const float* q = P.quats + 4 * q_idx;
             float qx = q[0], qy = q[1], qz = q[2], qw = q[3];
+            if (P.wxyz) {
+                qw = q[0]; qx = q[1]; qy = q[2]; qz = q[3];
+            }
             float qv[4] = {qx, qy, qz, qw};
             const float* sc = P.scales + 3 * s_idx;
             float scv[3] = {sc[0], sc[1], sc[2]};
@@ -420,7 +430,8 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
         P.v_scale[3 * idx] = vscale[0];
         P.v_scale[3 * idx + 1] = vscale[1];
         P.v_scale[3 * idx + 2] = vscale[2];
-        reinterpret_cast<float4*>(P.v_quat)[idx] = make_float4(vq[0], vq[1], vq[2], vq[3]);
+        reinterpret_cast<float4*>(P.v_quat)[idx] =
+            P.wxyz ? make_float4(vq[3], vq[0], vq[1], vq[2]) : make_float4(vq[0], vq[1], vq[2], vq[3]);
     }
     // viewmat gradient: wave DPP reduction, then across the 4 waves in LDS, one atomic per entry
     float red[12];
@@ -502,6 +513,7 @@ int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stre
     P.glob_scale = a.glob_scale; P.clip_thresh = a.clip_thresh;
     P.xys = a.xys; P.depths = a.depths; P.radii = a.radii; P.conics = a.conics;
     P.num_tiles_hit = a.num_tiles_hit; P.cum_tiles_hit = a.cum_tiles_hit;
+    P.wxyz = a.quats_wxyz;
     P.status = sc.scan_status; P.epoch = sc.next_epoch();
     P.err = sc.tickets + kDeviceError;
     hipLaunchKernelGGL(project_fwd_kernel, dim3((unsigned)blocks), dim3(kProjThreads), 0, stream,
@@ -538,6 +550,7 @@ int launch_project_bwd(const ProjectBwdArgs& a, hipStream_t stream) {
     P.fx = a.fx; P.fy = a.fy; P.glob_scale = a.glob_scale;
     P.v_mean3d = a.v_mean3d; P.v_scale = a.v_scale; P.v_quat = a.v_quat;
     P.v_viewmat = a.v_viewmat; P.v_transforms = a.v_transforms;
+    P.wxyz = a.quats_wxyz;
     int64_t blocks = (int64_t)a.B * blocks_per_image;
     hipLaunchKernelGGL(project_bwd_kernel, dim3((unsigned)blocks), dim3(kProjThreads), 0, stream,
                        P);

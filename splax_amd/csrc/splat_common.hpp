@@ -26,6 +26,17 @@ constexpr float kTEps = 0x1.a36e2ep-14f;       // float32(1e-4)
 constexpr float kDilation = 0x1.333334p-2f;    // float32(0.3), splax/_project/_kernels.py:204-206
 constexpr float kFovClamp = 0x1.4ccccdp+0f;    // float32(1.3), splax/_project/_kernels.py:191-192
 constexpr float kZEps = 0x1.0c6f7ap-20f;       // float32(1e-6), splax/_project/_kernels.py:215
+constexpr float kDilation2 = 0x1.70a3d8p-4f;   // float32(0.3 * 0.3), splax/_project/_project.py:115
+
+// Antialiasing compensation rho = sqrt(clip(1 - eps (a + c) + eps^2 (a c - b^2), 0, 1)),
+// splax/_project/_project.py:113-117, in the expression's own evaluation order; rho2 receives the
+// unclipped argument. NaN propagates as through the reference's maximum / minimum.
+__device__ __forceinline__ float compensation_rho(float a, float b, float c, float& rho2) {
+    rho2 = (1.0f - kDilation * (a + c)) + kDilation2 * (a * c - b * b);
+    float cl = rho2 < 0.0f ? 0.0f : rho2;
+    cl = cl > 1.0f ? 1.0f : cl;
+    return sqrtf(cl);
+}
 
 __device__ __forceinline__ float minw(float a, float b) { return a < b ? a : b; }
 __device__ __forceinline__ float maxw(float a, float b) { return a > b ? a : b; }

@@ -40,6 +40,7 @@ struct ProjectArgs {
     float fx, fy, cx, cy, glob_scale, clip_thresh;
     float* xys; float* depths; int32_t* radii; float* conics;
     int32_t* num_tiles_hit; int32_t* cum_tiles_hit;
+    int32_t quats_wxyz = 0;  // quaternions stored wxyz instead of the kernel's xyzw
 };
 
 struct ProjectBwdArgs {
@@ -57,6 +58,7 @@ struct ProjectBwdArgs {
     int32_t n, num_transforms, has_transforms, B;
     float fx, fy, glob_scale;
     float* v_mean3d; float* v_scale; float* v_quat; float* v_viewmat; float* v_transforms;
+    int32_t quats_wxyz = 0;  // quats (and v_quat) stored wxyz instead of xyzw
 };
 
 // Geometry of one sort_and_bin call (splax/_rasterize/_sort/_sort.py:51-60).
@@ -82,6 +84,9 @@ struct RasterInputs {
     const float* xys; const float* depths; const int32_t* radii; const float* conics;
     const int32_t* cum;
     int32_t n, B_geom, img_h, img_w;
+    // opac holds raw opacities and the blend uses opac * rho(conic), the antialiasing
+    // compensation of splax/_project/_project.py:95-117 (kept-list entry points only)
+    int32_t compensate = 0;
 };
 
 // ------------------------------------------------------------------ device words / scratch

@@ -150,6 +150,35 @@ def test_antialiased_matches_compensated_oracle():
     assert np.abs(_np(plain) - _np(img_aa)).max() > 1e-3
 
 
+def test_antialiased_grads_match_unfused_path():
+    """render(antialiased=True) fuses the compensation into the blend; its gradients equal the
+    composition of opacity_compensation (torch autograd) and rasterize."""
+    _case("antialiased grads")
+    n, H, W = 3000, 96, 96
+    sc = random_scene(n, H, W, seed=4)
+    keys = ("means", "scales", "quats", "colors", "opac")
+    target = torch.rand((H, W, 3), device="cuda", generator=torch.Generator("cuda").manual_seed(3))
+
+    def leaves():
+        return [_t(sc[k]).requires_grad_(True) for k in keys]
+
+    a = leaves()
+    img, _ = splax_amd.render(*a, viewmat=_t(sc["vm"]), background=_t(sc["bg"]),
+                              img_shape=(H, W), f=sc["f"], c=sc["c"], antialiased=True)
+    (img - target).abs().mean().backward()
+    b = leaves()
+    xys, depths, radii, conics, _, cum = splax_amd.project(
+        b[0], b[1], b[2], _t(sc["vm"]), opacities=b[4], img_shape=(H, W), f=sc["f"], c=sc["c"])
+    rho = splax_amd.opacity_compensation(conics, radii).unsqueeze(-1)
+    img2 = splax_amd.rasterize(b[3], b[4] * rho, _t(sc["bg"]), xys, depths, radii, conics, cum,
+                               img_shape=(H, W), map_opacities=b[4])
+    assert_bit_exact(_np(img), _np(img2), "antialiased fused vs unfused image")
+    (img2 - target).abs().mean().backward()
+    for k, x, y in zip(keys, a, b):
+        g, r = _np(x.grad), _np(y.grad)
+        assert rel_fro(g, r) < 1e-5, (k, rel_fro(g, r))
+
+
 def test_render_log_equals_render():
     _case("render_log")
     n, H, W = 2000, 64, 64

@@ -192,6 +192,21 @@ def test_project_bwd_matches_oracle(name):
                             num_transforms=1, has_transforms=False, f=s.f, glob_scale=1.0)
     for label, a, b in zip(("v_mean3d", "v_scale", "v_quat"), zero[:3], none[:3]):
         assert_bit_exact(_np(b), _np(a), f"{name}/{label} null v_depth")
+    # wxyz storage (the public API's order): same results, v_quat in wxyz
+    wx = _ops.project_bwd(_t(s.means), _t(s.scales), _t(s.quats), _t(s.viewmats[0]), _t(radii),
+                          _t(conics), _t(v_xy), _t(v_depth), _t(v_conic), tf, ids, n=s.n, B=1,
+                          num_transforms=1, has_transforms=False, f=s.f, glob_scale=1.0,
+                          quats_wxyz=True)
+    for label, a, b in zip(("v_mean3d", "v_scale"), wx[:2], got[:2]):
+        assert_bit_exact(_np(a), _np(b), f"{name}/{label} wxyz")
+    assert_bit_exact(_np(wx[2]), np.roll(_np(got[2]), 1, axis=-1), f"{name}/v_quat wxyz")
+    fw = _ops.project_fwd(_t(s.means), _t(s.scales), _t(s.quats), _t(s.viewmats[0]),
+                          _t(s.opacities).reshape(-1), tf, ids, n=s.n, total=s.n,
+                          num_transforms=1, has_transforms=False, img_shape=s.img_shape, f=s.f,
+                          c=s.c, glob_scale=1.0, clip_thresh=0.01, quats_wxyz=True)
+    for label, a, r in zip(("xys", "depths", "radii", "conics", "nth", "cum"), fw,
+                           (xys, depths, radii, conics, nth, cum)):
+        assert_bit_exact(_np(a).reshape(np.shape(r)), r, f"{name}/{label} wxyz")
 
 
 def test_batched_cameras_one_launch():
@@ -344,6 +359,41 @@ def test_kept_sort_path_equals_resort_path(name):
     assert set(np.unique(mode)) <= {0, 1, 2}
     box = mode == 0
     assert np.all(r[box, 12] > 0) and np.all(r[box, 13] > 0)
+
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg2_50k"])
+def test_compensated_blend_matches_oracle(name):
+    """Antialiased blend fused into the kept path (splax/_render.py:105-110): the forward image
+    equals the oracle's blend of opacities * rho bit for bit; the backward equals the oracle's
+    blend cotangents pushed through the compensation's reverse-mode rule."""
+    _case(f"compensated blend {name}")
+    s = _scene_arrays(name)
+    xys, depths, radii, conics, nth, cum = _raster_inputs(s)
+    rho, _ = O.compensation_rho(conics)
+    rho = np.where(radii.reshape(-1) > 0, rho, np.float32(1))
+    ob = (s.opacities.reshape(-1) * rho).astype(np.float32)
+    rimg, rT, ridx, _, _ = O.rasterize_fwd(s.colors, ob, s.opacities, s.background, xys, depths,
+                                           radii, conics, cum, n=s.n, B=1, img_shape=s.img_shape)
+    o = _t(s.opacities).reshape(-1)
+    geo = (_t(xys), _t(depths), _t(radii), _t(conics), _t(cum))
+    img, Ts, fidx, kept, _ = _ops.rasterize_fwd_keep(
+        _t(s.colors), o, o, _t(s.background), *geo, n=s.n, B=1, img_shape=s.img_shape,
+        compensate=True)
+    assert_bit_exact(_np(img), rimg, f"{name}/compensated img")
+    assert_bit_exact(_np(kept.records)[:, 5], ob, f"{name}/record opacity = opacity * rho")
+    H, W = s.img_shape
+    vout = (2.0 * (rimg.reshape(H, W, 3) - s.targets[0]) / rimg.size).astype(np.float32)
+    ref = O.rasterize_bwd(s.colors, ob, s.opacities, s.background, xys, depths, radii, conics,
+                          cum, rT, ridx, vout, n=s.n, B_out=1, B_geom=1, img_shape=s.img_shape)
+    v_o, v_c = O.compensation_vjp(ref[1], s.opacities, conics)
+    want = (ref[0], v_o, ref[2], ref[3] + v_c)
+    for recs in (kept.records, None):
+        got = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[1],
+                                        geo[3], geo[4], kept._replace(records=recs), Ts, fidx,
+                                        _t(vout).reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
+                                        img_shape=s.img_shape, compensate=True)
+        for label, g, r in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), got, want):
+            _grad_compare(_np(g).reshape(r.shape), r, f"{name}/{label} compensated")
 
 
 # ---------------------------------------------------------------- depth channel

@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(handle, name), f"{name} declared in include/splat_hip.h but not exported"
     assert set(names) == set(_lib._SIGS), "Python binding and header disagree"
     lib = _lib.lib()
-    assert lib.splat_abi_version() == 6
+    assert lib.splat_abi_version() == 7
     assert isinstance(lib.splat_last_error(), bytes)
 
 
@@ -146,7 +146,7 @@ def test_abi_rejects_rows_that_are_neither_shared_nor_batched():
         return lib.splat_project_fwd(null, null, rows_means, null, n, null, n, null, rows_view,
                                      null, n, null, 1, null, n, 1, 0, total, 16, 16, f(10.0),
                                      f(10.0), f(8.0), f(8.0), f(1.0), f(0.01), null, null, null,
-                                     null, null, null)
+                                     null, null, null, 1)
 
     assert fwd(20, 4) == 1  # between n and B*n
     assert b"rows" in lib.splat_last_error()

@@ -87,3 +87,48 @@ def test_key_layout_table(B, H, W, tile_bits, image_bits, depth_bits, packed):
     nt = lay["num_tiles"]
     assert nt == ((W + 15) // 16) * ((H + 15) // 16)
     assert (nt - 1) < (1 << tile_bits) and (B - 1) < (1 << image_bits)
+
+
+def test_compensation_rho_closed_form_and_vjp():
+    """rho^2 = det(S) / det(S + 0.3 I) for the conic of S + 0.3 I (the projection's dilation,
+    splax/_project/_kernels.py:204-212); the cotangent rule equals float64 autograd of the
+    reference expression away from the clip boundaries, and follows the reference's conventions
+    on them (1/2 at a tie, NaN where rho = 0 and the cotangent is 0)."""
+    import torch
+
+    rng = np.random.default_rng(8)
+    n = 500
+    L = rng.normal(size=(n, 2, 2)) * rng.uniform(0.1, 3.0, (n, 1, 1))
+    S = L @ np.transpose(L, (0, 2, 1))
+    Sd = S + 0.3 * np.eye(2)
+    det = Sd[:, 0, 0] * Sd[:, 1, 1] - Sd[:, 0, 1] ** 2
+    conics = np.stack([Sd[:, 1, 1] / det, -Sd[:, 0, 1] / det, Sd[:, 0, 0] / det], 1)
+    conics = conics.astype(np.float32)
+    rho, rho2 = O.compensation_rho(conics)
+    want = (S[:, 0, 0] * S[:, 1, 1] - S[:, 0, 1] ** 2) / det
+    np.testing.assert_allclose(rho2, want, atol=2e-6)
+    np.testing.assert_allclose(rho, np.sqrt(np.clip(want, 0, 1)), atol=2e-3)
+    # cotangents against float64 autograd of the same expression (interior points)
+    vbo = rng.normal(size=n).astype(np.float32)
+    opac = rng.uniform(0.05, 1.0, n).astype(np.float32)
+    v_o, v_c = O.compensation_vjp(vbo, opac, conics)
+    c64 = torch.tensor(conics, dtype=torch.float64, requires_grad=True)
+    o64 = torch.tensor(opac, dtype=torch.float64, requires_grad=True)
+    a, b, c = c64[:, 0], c64[:, 1], c64[:, 2]
+    r2 = 1.0 - 0.3 * (a + c) + 0.09 * (a * c - b * b)
+    bo = o64 * torch.sqrt(torch.clamp(r2, 0.0, 1.0))
+    bo.backward(torch.tensor(vbo, dtype=torch.float64))
+    # float32 rho2 cancels: its absolute error is ~1e-7 of the terms, so compare where rho2 is
+    # well inside (0, 1)
+    inside = (rho2 > 0.05) & (rho2 < 1 - 1e-6)
+    assert inside.sum() > 300
+    np.testing.assert_allclose(v_o[inside], o64.grad.numpy()[inside], rtol=1e-4, atol=1e-7)
+    np.testing.assert_allclose(v_c[inside], c64.grad.numpy()[inside], rtol=1e-3, atol=1e-6)
+    # boundaries: zero conic (culled item) -> rho 1, a tie of the upper clip -> half gradient
+    v_o0, v_c0 = O.compensation_vjp([2.0], [0.5], [[0.0, 0.0, 0.0]])
+    assert v_o0[0] == 2.0
+    np.testing.assert_array_equal(v_c0[0], np.float32([-0.3, 0.0, -0.3]) * np.float32(0.25))
+    # rho = 0 with a zero cotangent: NaN, as the reference's sqrt rule gives
+    v_o1, v_c1 = O.compensation_vjp([0.0], [0.5], [[4.0, 0.0, 1.0]])
+    assert O.compensation_rho([[4.0, 0.0, 1.0]])[0][0] == 0.0  # rho2 = (1 - 1.2)(1 - 0.3) < 0
+    assert np.isnan(v_c1).all() and v_o1[0] == 0.0
