@@ -236,6 +236,33 @@ int splat_mcmc_compute_relocation(splat_stream_t stream, const float* opacities,
                                   const float* scales, const float* ratios, int64_t n,
                                   int32_t n_max, float* new_opacities, float* new_scales);
 
+/* Replaces render_log's parameter map (splax/_render.py:161-164), one pass over n gaussians:
+ * scales = exp(log_scales) [n,3], quats_out = quats / (|quats| + 1e-8) [n,4] (any order),
+ * colors = sigmoid(logit_colors) [n,3], opacities = sigmoid(logit_opacities) [n]. exp is the
+ * library's fixed-sequence exp. */
+int splat_log_params_fwd(splat_stream_t stream, const float* log_scales, const float* quats,
+                         const float* logit_colors, const float* logit_opacities, int64_t n,
+                         float* scales, float* quats_out, float* colors, float* opacities);
+
+/* Reverse mode of splat_log_params_fwd at the same inputs: cotangents of its four outputs (any
+ * may be NULL, a zero cotangent) to those of its four inputs. */
+int splat_log_params_bwd(splat_stream_t stream, const float* log_scales, const float* quats,
+                         const float* logit_colors, const float* logit_opacities, int64_t n,
+                         const float* v_scales, const float* v_quats, const float* v_colors,
+                         const float* v_opacities, float* v_log_scales, float* v_quats_in,
+                         float* v_logit_colors, float* v_logit_opacities);
+
+/* The trainers' L1 loss mean |img - target| over count elements (scripts/train_lego.py:111),
+ * summed in double in a fixed order; partials is scratch of ceil(count / 4096) doubles and loss
+ * one float, both device memory. */
+int splat_l1_loss_fwd(splat_stream_t stream, const float* img, const float* target,
+                      int64_t count, double* partials, float* loss);
+
+/* Cotangent of the L1 loss: v_img = sign(img - target) * (*v_loss / count), v_loss a device
+ * scalar. */
+int splat_l1_loss_bwd(splat_stream_t stream, const float* img, const float* target,
+                      int64_t count, const float* v_loss, float* v_img);
+
 /* Replaces clear_cache (splax/_cache.py:158-164): frees the per-device scratch. */
 void splat_clear_cache(void);
 

@@ -168,3 +168,62 @@ def relocate(seed: int, means, log_scales, quats, logit_colors, logit_opacities,
             out_means[i], out_q[i], out_c[i] = means[s], quats[s], colors[s]
         out_l[i], out_ls[i] = newv[s]
     return out_means, out_ls, out_q, out_c, out_l, src.astype(np.int32), reset
+
+
+# ---------------------------------------------------------------- render_log map and L1 loss
+
+_QUAT_EPS = np.float32(1e-8)  # splax/_render.py:162
+
+
+def _qnorm(q):
+    return np.sqrt(((q[:, 0] * q[:, 0] + q[:, 1] * q[:, 1]) + q[:, 2] * q[:, 2])
+                   + q[:, 3] * q[:, 3])
+
+
+def log_params_fwd(log_scales, quats, logit_colors, logit_opacities):
+    """render_log's parameter map (splax/_render.py:161-164) in float32 with the library's exp;
+    returns (scales, quats / (|quats| + 1e-8), colors, opacities)."""
+    ls = np.asarray(log_scales, np.float32).reshape(-1, 3)
+    q = np.asarray(quats, np.float32).reshape(-1, 4)
+    s = (_qnorm(q) + _QUAT_EPS)[:, None]
+    scales = O.expf(ls).reshape(ls.shape)
+    colors = sigmoid(logit_colors).reshape(-1, 3)
+    opac = sigmoid(logit_opacities).reshape(-1)
+    return scales, (q / s).astype(np.float32), colors, opac
+
+
+def log_params_bwd(log_scales, quats, logit_colors, logit_opacities, v_scales, v_quats,
+                   v_colors, v_opac):
+    """Reverse mode of log_params_fwd: exp' = exp, logistic' = s (1 - s), and for
+    q / (sqrt(sum q^2) + eps) the direct term g / s plus 2 q v_ss with
+    v_ss = (sum_k -(g_k q_k) / s^2) * 0.5 / |q|, in float32."""
+    f = np.float32
+    ls = np.asarray(log_scales, np.float32).reshape(-1, 3)
+    q = np.asarray(quats, np.float32).reshape(-1, 4)
+    sc = sigmoid(logit_colors).reshape(-1, 3)
+    so = sigmoid(logit_opacities).reshape(-1)
+    v_ls = np.asarray(v_scales, np.float32).reshape(-1, 3) * O.expf(ls).reshape(ls.shape)
+    v_lc = np.asarray(v_colors, np.float32).reshape(-1, 3) * (sc * (f(1) - sc))
+    v_lo = np.asarray(v_opac, np.float32).reshape(-1) * (so * (f(1) - so))
+    vy = np.asarray(v_quats, np.float32).reshape(-1, 4)
+    nrm = _qnorm(q)
+    s = nrm + _QUAT_EPS
+    inv_s2 = f(1) / (s * s)
+    v_s = np.zeros_like(s)
+    for k in range(4):
+        v_s = v_s + (-(vy[:, k] * q[:, k])) * inv_s2
+    with np.errstate(divide="ignore", invalid="ignore"):
+        v_ss = v_s * (f(0.5) / nrm)
+    vq = vy / s[:, None] + (v_ss[:, None] * q + v_ss[:, None] * q)
+    return (v_ls.astype(np.float32), vq.astype(np.float32), v_lc.astype(np.float32),
+            v_lo.astype(np.float32))
+
+
+def l1_loss(img, target, g=1.0):
+    """mean |img - target| (scripts/train_lego.py:111): float32 differences, summed in double,
+    rounded once; returns (loss, img cotangent sign(d) * (g / count) for loss cotangent g)."""
+    d = np.asarray(img, np.float32).reshape(-1) - np.asarray(target, np.float32).reshape(-1)
+    loss = np.float32(np.abs(d).astype(np.float64).sum() / d.size)
+    scale = np.float32(g) / np.float32(d.size)
+    sg = np.where(d > 0, np.float32(1), np.where(d < 0, np.float32(-1), d))
+    return loss, (sg * scale).astype(np.float32)

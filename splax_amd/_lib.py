@@ -54,6 +54,10 @@ _SIGS = {
     "splat_adam_reset_rows": [_vp, _vp, _i32, _vp, _i64],
     "splat_mcmc_relocate": [_vp] + [_vp] * 5 + [_i64, _i32, _f32, _u64, _vp, _vp],
     "splat_mcmc_compute_relocation": [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp],
+    "splat_log_params_fwd": [_vp] + [_vp] * 4 + [_i64] + [_vp] * 4,
+    "splat_log_params_bwd": [_vp] + [_vp] * 4 + [_i64] + [_vp] * 8,
+    "splat_l1_loss_fwd": [_vp, _vp, _vp, _i64, _vp, _vp],
+    "splat_l1_loss_bwd": [_vp, _vp, _vp, _i64, _vp, _vp],
     "splat_clear_cache": [],
     "splat_last_error": [],
     "splat_set_stage_timing": [_i32],

@@ -1,0 +1,217 @@
+// Elementwise stages around the render in a training step, each one pass over HBM:
+//   - the log / logit parameter map of render_log (splax/_render.py:161-164) and its reverse-mode
+//     rule: scales = exp(log_scales), quats / (|quats| + 1e-8), sigmoid of the colour and opacity
+//     logits;
+//   - the L1 loss mean |img - target| of the trainers (scripts/train_lego.py:111) and its
+//     cotangent sign(img - target) * g / count.
+//
+// exp is det_expf and sigmoid(x) = 1 / (1 + det_expf(-x)), so the CPU oracle reproduces every
+// bit. |q| = sqrt(((q0^2 + q1^2) + q2^2) + q3^2). Reverse-mode rules follow the reference's
+// primitives: exp' = exp, logistic' = s (1 - s), sqrt' = 0.5 / sqrt, x / s gives g / s and
+// -(g x) / s^2 to the divisor, and the square's two uses add 2 q v.
+#include <string>
+
+#include "../../include/splat_hip.h"
+#include "splat_common.hpp"
+#include "splat_internal.hpp"
+
+namespace splat {
+
+constexpr float kQuatEps = 0x1.5798eep-27f;  // float32(1e-8), splax/_render.py:162
+
+__device__ __forceinline__ float glue_sigmoid(float x) { return 1.0f / (1.0f + det_expf(-x)); }
+
+__device__ __forceinline__ float quat_norm(const float q[4]) {
+    return sqrtf(((q[0] * q[0] + q[1] * q[1]) + q[2] * q[2]) + q[3] * q[3]);
+}
+
+struct LogParams {
+    const float* log_scales; const float* quats; const float* logit_colors;
+    const float* logit_opac;
+    int64_t n;
+    float* scales; float* quats_out; float* colors; float* opac;              // forward
+    const float* v_scales; const float* v_quats; const float* v_colors;       // backward
+    const float* v_opac;
+    float* v_log_scales; float* v_quats_in; float* v_logit_colors; float* v_logit_opac;
+};
+
+__global__ void __launch_bounds__(256) log_params_fwd_kernel(LogParams P) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= P.n) return;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        P.scales[3 * i + k] = det_expf(P.log_scales[3 * i + k]);
+        P.colors[3 * i + k] = glue_sigmoid(P.logit_colors[3 * i + k]);
+    }
+    const float4 q4 = reinterpret_cast<const float4*>(P.quats)[i];
+    const float q[4] = {q4.x, q4.y, q4.z, q4.w};
+    const float s = quat_norm(q) + kQuatEps;
+    reinterpret_cast<float4*>(P.quats_out)[i] =
+        make_float4(q[0] / s, q[1] / s, q[2] / s, q[3] / s);
+    P.opac[i] = glue_sigmoid(P.logit_opac[i]);
+}
+
+// A null cotangent is a zero one.
+__device__ __forceinline__ float cot(const float* v, int64_t j) { return v ? v[j] : 0.0f; }
+
+__global__ void __launch_bounds__(256) log_params_bwd_kernel(LogParams P) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= P.n) return;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int64_t j = 3 * i + k;
+        P.v_log_scales[j] = cot(P.v_scales, j) * det_expf(P.log_scales[j]);
+        const float sc = glue_sigmoid(P.logit_colors[j]);
+        P.v_logit_colors[j] = cot(P.v_colors, j) * (sc * (1.0f - sc));
+    }
+    const float so = glue_sigmoid(P.logit_opac[i]);
+    P.v_logit_opac[i] = cot(P.v_opac, i) * (so * (1.0f - so));
+    const float4 q4 = reinterpret_cast<const float4*>(P.quats)[i];
+    const float q[4] = {q4.x, q4.y, q4.z, q4.w};
+    const float nrm = quat_norm(q);
+    const float s = nrm + kQuatEps;
+    float vy[4], vq[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) vy[k] = cot(P.v_quats, 4 * i + k);
+    // y = q / s: the divisor's cotangent sums -(g q) / s^2 over the four components
+    const float inv_s2 = 1.0f / (s * s);
+    float v_s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v_s = v_s + (-(vy[k] * q[k])) * inv_s2;
+    const float v_ss = v_s * (0.5f / nrm);  // s = sqrt(sum q^2) + eps
+#pragma unroll
+    for (int k = 0; k < 4; ++k) vq[k] = vy[k] / s + (v_ss * q[k] + v_ss * q[k]);
+    reinterpret_cast<float4*>(P.v_quats_in)[i] = make_float4(vq[0], vq[1], vq[2], vq[3]);
+}
+
+// ------------------------------------------------------------------ L1 loss
+
+constexpr int kL1Chunk = 4096;  // elements per workgroup (16 per thread)
+
+// Workgroup sums of |img - target| in double, in a fixed order: per thread sequential, then a
+// fixed tree over the workgroup.
+__global__ void __launch_bounds__(256) l1_partials_kernel(const float* img, const float* tgt,
+                                                          int64_t count, double* partials) {
+    __shared__ double s[256];
+    const int64_t base = (int64_t)blockIdx.x * kL1Chunk;
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 0; j < kL1Chunk / 256; ++j) {
+        const int64_t i = base + j * 256 + threadIdx.x;
+        if (i < count) acc += (double)fabsf(img[i] - tgt[i]);
+    }
+    s[threadIdx.x] = acc;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if ((int)threadIdx.x < off) s[threadIdx.x] += s[threadIdx.x + off];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partials[blockIdx.x] = s[0];
+}
+
+// One workgroup: the partials in the same fixed order, divided by the count.
+__global__ void __launch_bounds__(256) l1_final_kernel(const double* partials, int64_t blocks,
+                                                       int64_t count, float* loss) {
+    __shared__ double s[256];
+    double acc = 0.0;
+    for (int64_t b = threadIdx.x; b < blocks; b += 256) acc += partials[b];
+    s[threadIdx.x] = acc;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if ((int)threadIdx.x < off) s[threadIdx.x] += s[threadIdx.x + off];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *loss = (float)(s[0] / (double)count);
+}
+
+// v_img = sign(img - target) * (g / count), g read from device memory (the loss cotangent).
+__global__ void __launch_bounds__(256) l1_bwd_kernel(const float* img, const float* tgt,
+                                                     int64_t count, const float* g, float* v) {
+    const float scale = *g / (float)count;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count;
+         i += (int64_t)gridDim.x * 256) {
+        const float d = img[i] - tgt[i];
+        const float sg = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : d);  // sign: +-0 and NaN pass
+        v[i] = sg * scale;
+    }
+}
+
+static int glue_launched(const char* what) {
+    return hipGetLastError() == hipSuccess ? 0
+                                           : fail(kErrLaunch, std::string(what) + " launch failed");
+}
+
+}  // namespace splat
+
+using namespace splat;
+
+extern "C" {
+
+int splat_log_params_fwd(splat_stream_t stream, const float* log_scales, const float* quats,
+                         const float* logit_colors, const float* logit_opacities, int64_t n,
+                         float* scales, float* quats_out, float* colors, float* opacities) {
+    if (n < 0) return fail(kErrArgs, "log_params_fwd: negative count");
+    if (n == 0) return 0;
+    if (!log_scales || !quats || !logit_colors || !logit_opacities || !scales || !quats_out ||
+        !colors || !opacities)
+        return fail(kErrArgs, "log_params_fwd: missing arrays");
+    if (((uintptr_t)quats | (uintptr_t)quats_out) & 15)
+        return fail(kErrArgs, "log_params_fwd: quaternion arrays must be 16-byte aligned");
+    LogParams P{};
+    P.log_scales = log_scales; P.quats = quats; P.logit_colors = logit_colors;
+    P.logit_opac = logit_opacities; P.n = n;
+    P.scales = scales; P.quats_out = quats_out; P.colors = colors; P.opac = opacities;
+    hipLaunchKernelGGL(log_params_fwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), P);
+    return glue_launched("log_params_fwd");
+}
+
+int splat_log_params_bwd(splat_stream_t stream, const float* log_scales, const float* quats,
+                         const float* logit_colors, const float* logit_opacities, int64_t n,
+                         const float* v_scales, const float* v_quats, const float* v_colors,
+                         const float* v_opacities, float* v_log_scales, float* v_quats_in,
+                         float* v_logit_colors, float* v_logit_opacities) {
+    if (n < 0) return fail(kErrArgs, "log_params_bwd: negative count");
+    if (n == 0) return 0;
+    if (!log_scales || !quats || !logit_colors || !logit_opacities || !v_log_scales ||
+        !v_quats_in || !v_logit_colors || !v_logit_opacities)
+        return fail(kErrArgs, "log_params_bwd: missing arrays");
+    if (((uintptr_t)quats | (uintptr_t)v_quats_in) & 15)
+        return fail(kErrArgs, "log_params_bwd: quaternion arrays must be 16-byte aligned");
+    LogParams P{};
+    P.log_scales = log_scales; P.quats = quats; P.logit_colors = logit_colors;
+    P.logit_opac = logit_opacities; P.n = n;
+    P.v_scales = v_scales; P.v_quats = v_quats; P.v_colors = v_colors; P.v_opac = v_opacities;
+    P.v_log_scales = v_log_scales; P.v_quats_in = v_quats_in;
+    P.v_logit_colors = v_logit_colors; P.v_logit_opac = v_logit_opacities;
+    hipLaunchKernelGGL(log_params_bwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), P);
+    return glue_launched("log_params_bwd");
+}
+
+int splat_l1_loss_fwd(splat_stream_t stream, const float* img, const float* target,
+                      int64_t count, double* partials, float* loss) {
+    if (count <= 0 || !img || !target || !partials || !loss)
+        return fail(kErrArgs, "l1_loss_fwd: empty input or missing arrays");
+    const int64_t blocks = (count + kL1Chunk - 1) / kL1Chunk;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(l1_partials_kernel, dim3((unsigned)blocks), dim3(256), 0, s, img, target,
+                       count, partials);
+    int rc = glue_launched("l1_loss partials");
+    if (rc) return rc;
+    hipLaunchKernelGGL(l1_final_kernel, dim3(1), dim3(256), 0, s, partials, blocks, count, loss);
+    return glue_launched("l1_loss final");
+}
+
+int splat_l1_loss_bwd(splat_stream_t stream, const float* img, const float* target,
+                      int64_t count, const float* v_loss, float* v_img) {
+    if (count <= 0 || !img || !target || !v_loss || !v_img)
+        return fail(kErrArgs, "l1_loss_bwd: empty input or missing arrays");
+    int64_t blocks = (count + 255) / 256;
+    blocks = blocks < 8192 ? blocks : 8192;
+    hipLaunchKernelGGL(l1_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), img, target, count, v_loss, v_img);
+    return glue_launched("l1_loss_bwd");
+}
+
+}  // extern "C"

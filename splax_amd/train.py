@@ -18,7 +18,7 @@ from collections.abc import Mapping
 import numpy as np
 import torch
 
-from splax_amd import mcmc
+from splax_amd import _lib, mcmc
 from splax_amd._render import render_log
 from splax_amd.optim import Adam, exponential_decay
 from splax_amd.scenes import Scene
@@ -45,6 +45,44 @@ def params_from_scene(scene: Scene, device: torch.device | str = "cuda") -> dict
         "opac_logit": _logit(scene.opacities.reshape(-1, 1)),
     }
     return {k: torch.from_numpy(np.ascontiguousarray(v)).to(device) for k, v in arrays.items()}
+
+
+class _L1LossFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, img, target):
+        if img.shape != target.shape or img.dtype != torch.float32 or \
+                target.dtype != torch.float32:
+            raise ValueError("l1_loss: img and target must be float32 of one shape")
+        img, target = img.contiguous(), target.contiguous()
+        dev = _lib.require_gpu(img, target)
+        count = img.numel()
+        partials = torch.empty(((count + 4095) // 4096,), device=dev, dtype=torch.float64)
+        loss = torch.empty((), device=dev, dtype=torch.float32)
+        with torch.cuda.device(dev):
+            st = _lib.lib().splat_l1_loss_fwd(_lib.stream_handle(dev), img.data_ptr(),
+                                              target.data_ptr(), count, partials.data_ptr(),
+                                              loss.data_ptr())
+        _lib.check(st, "l1_loss_fwd")
+        ctx.save_for_backward(img, target)
+        return loss
+
+    @staticmethod
+    def backward(ctx, v_loss):
+        img, target = ctx.saved_tensors
+        v_loss = v_loss.to(torch.float32).contiguous()
+        v_img = torch.empty_like(img)
+        with torch.cuda.device(img.device):
+            st = _lib.lib().splat_l1_loss_bwd(_lib.stream_handle(img.device), img.data_ptr(),
+                                              target.data_ptr(), img.numel(), v_loss.data_ptr(),
+                                              v_img.data_ptr())
+        _lib.check(st, "l1_loss_bwd")
+        return v_img, None
+
+
+def l1_loss(img: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+    """mean |img - target| (scripts/train_lego.py:111), one library pass each way; the target
+    receives no gradient."""
+    return _L1LossFn.apply(img, target)
 
 
 class TrainStep:
@@ -77,7 +115,7 @@ class TrainStep:
         leaves = [p.requires_grad_(True) for p in self.params.values()]
         img, _ = render_log(*leaves, viewmat=self.viewmats, background=self.background,
                             **self.camera)
-        loss = (img - self.targets).abs().mean()
+        loss = l1_loss(img, self.targets)
         grads = torch.autograd.grad(loss, leaves)
         for p in leaves:
             p.requires_grad_(False)

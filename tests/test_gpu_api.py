@@ -192,11 +192,18 @@ def test_render_log_equals_render():
                c=sc["c"])
     a, _ = splax_amd.render_log(_t(sc["means"]), _t(log_s), _t(quats), _t(logit_c), _t(logit_o),
                                 **cam)
+    from oracle import train_oracle as TO
+
+    act = TO.log_params_fwd(log_s, quats, logit_c, logit_o)  # the library's parameter map
+    b, _ = splax_amd.render(_t(sc["means"]), _t(act[0]), _t(act[1]), _t(act[2]),
+                            _t(act[3].reshape(n, 1)), **cam)
+    assert_bit_exact(_np(a), _np(b), "render_log")
+    # within float32 rounding of torch's own exp / norm / sigmoid
     tq = _t(quats)
-    b, _ = splax_amd.render(_t(sc["means"]), torch.exp(_t(log_s)),
+    c, _ = splax_amd.render(_t(sc["means"]), torch.exp(_t(log_s)),
                             tq / (torch.linalg.norm(tq, dim=-1, keepdim=True) + 1e-8),
                             torch.sigmoid(_t(logit_c)), torch.sigmoid(_t(logit_o)), **cam)
-    assert_bit_exact(_np(a), _np(b), "render_log")
+    assert np.abs(_np(a) - _np(c)).max() < 1e-4
 
 
 def test_rigid_transforms_forward_and_grads():

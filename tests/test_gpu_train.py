@@ -241,3 +241,46 @@ def test_train_step_config4_small():
     assert bool((opac > 0.005).all()), "dead rows were relocated"
     assert train.opt.count == 6
     assert _lib.check_device() == 0
+
+
+@pytest.mark.parametrize("n", [1, 777, 20000])
+def test_log_params_bit_exact(n):
+    """render_log's parameter map and its reverse mode, one library pass each, against the
+    oracle; a missing cotangent is a zero one."""
+    from splax_amd._render import _LogParamsFn
+
+    _case(f"log_params n={n}")
+    rng = np.random.default_rng(n)
+    ins = [rng.normal(-4, 1, (n, 3)), rng.normal(size=(n, 4)), rng.normal(0, 2, (n, 3)),
+           rng.normal(0, 3, (n, 1))]
+    ins = [a.astype(np.float32) for a in ins]
+    ref = T.log_params_fwd(*ins)
+    leaves = [_t(a).requires_grad_(True) for a in ins]
+    outs = _LogParamsFn.apply(*leaves)
+    for label, g, r in zip(("scales", "quats", "colors", "opacities"), outs, ref):
+        assert_bit_exact(_np(g).reshape(r.shape), r, f"log_params {label}")
+    cots = [rng.normal(size=np.shape(r)).astype(np.float32) for r in ref]
+    cots[2] = np.zeros_like(cots[2])
+    torch.autograd.backward([outs[0], outs[1], outs[3]],
+                            [_t(cots[0]), _t(cots[1]), _t(cots[3]).reshape(n, 1)])
+    back = T.log_params_bwd(*ins, *cots)
+    for label, x, r in zip(("v_log_scales", "v_quats", "v_logit_colors", "v_logit_opac"),
+                           leaves, back):
+        assert_bit_exact(_np(x.grad).reshape(r.shape), r, f"log_params {label}")
+
+
+@pytest.mark.parametrize("count", [1, 4095, 4097, 3 * 1060 * 1600 * 4])
+def test_l1_loss(count):
+    from splax_amd.train import l1_loss
+
+    _case(f"l1 count={count}")
+    rng = np.random.default_rng(count)
+    img = rng.uniform(size=count).astype(np.float32)
+    tgt = rng.uniform(size=count).astype(np.float32)
+    tgt[: count // 7] = img[: count // 7]  # exact ties: zero cotangent
+    ref_loss, ref_v = T.l1_loss(img, tgt, g=3.0)
+    x = _t(img).requires_grad_(True)
+    loss = l1_loss(x, _t(tgt))
+    (loss * 3.0).backward()
+    assert abs(float(loss.detach()) - float(ref_loss)) <= 1e-6 * float(ref_loss)
+    assert_bit_exact(_np(x.grad), ref_v, "l1 cotangent")

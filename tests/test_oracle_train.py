@@ -214,3 +214,36 @@ def test_relocate_deterministic(seed):
     b = T.relocate(seed, *_scene(200, 50, 6), n_max=51)
     for x, y in zip(a, b):
         assert np.array_equal(x, y)
+
+
+def test_log_params_match_float64_autograd():
+    """render_log's parameter map and its reverse mode against float64 torch autograd of the
+    reference expression (splax/_render.py:161-164)."""
+    rng = np.random.default_rng(12)
+    n = 400
+    ls = rng.normal(-4, 1, (n, 3)).astype(np.float32)
+    q = rng.normal(size=(n, 4)).astype(np.float32)
+    lc = rng.normal(0, 2, (n, 3)).astype(np.float32)
+    lo = rng.normal(0, 3, n).astype(np.float32)
+    got = T.log_params_fwd(ls, q, lc, lo)
+    t = [torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (ls, q, lc, lo)]
+    want = (torch.exp(t[0]), t[1] / (torch.linalg.norm(t[1], dim=-1, keepdim=True) + 1e-8),
+            torch.sigmoid(t[2]), torch.sigmoid(t[3]))
+    for g, w in zip(got, want):
+        np.testing.assert_allclose(g, w.detach().numpy(), rtol=2e-6, atol=1e-9)
+    cots = [rng.normal(size=a.shape).astype(np.float32) for a in got]
+    back = T.log_params_bwd(ls, q, lc, lo, *cots)
+    torch.autograd.backward(want, [torch.tensor(c, dtype=torch.float64) for c in cots])
+    for b, x in zip(back, t):
+        np.testing.assert_allclose(b, x.grad.numpy(), rtol=2e-5, atol=1e-7)
+    # the normalized quaternion's gradient is orthogonal to it
+    u = got[1].astype(np.float64)
+    assert np.abs((back[1] * u).sum(1)).max() < 1e-4 * np.abs(back[1]).max()
+
+
+def test_l1_loss_closed_form():
+    img = np.array([0.5, 0.25, 1.0, 0.75], np.float32)
+    tgt = np.array([0.25, 0.25, 0.0, 1.0], np.float32)
+    loss, v = T.l1_loss(img, tgt)
+    assert loss == np.float32((0.25 + 0 + 1.0 + 0.25) / 4)
+    assert v.tolist() == [0.25, 0.0, 0.25, -0.25]
