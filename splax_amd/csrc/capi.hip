@@ -120,7 +120,6 @@ int DeviceScratch::grow_scan_status(int64_t blocks) {
 }
 
 int DeviceScratch::ensure_sort(int64_t M, int64_t bins, int32_t B, bool wide) {
-    const int64_t sort_tile = 256 * 8;  // keys per onesweep partition (sort.hip kSortTile)
     const int64_t mm_blocks = 2 * (int64_t)B * 4096;  // generous partial capacity bound below
     bool need_sync = true;
     auto sync_once = [&]() {
@@ -156,17 +155,17 @@ int DeviceScratch::ensure_sort(int64_t M, int64_t bins, int32_t B, bool wide) {
         if (rc) return rc;
         wide_cap = cap;
     }
-    const int64_t parts = (M + sort_tile - 1) / sort_tile;
-    if (parts * 256 > sort_status_cap) {
+    const int64_t parts = (M + kSortTileMin - 1) / kSortTileMin;
+    if (parts * 256 > part_counts_cap) {
         sync_once();
-        dev_free(&sort_status);
+        dev_free(&part_counts);
         int64_t cap = (int64_t)(parts * 1.25 + 1) * 256;
-        rc = dev_alloc(&sort_status, cap, true);
+        rc = dev_alloc(&part_counts, cap, false);
         if (rc) {
-            sort_status_cap = 0;
+            part_counts_cap = 0;
             return rc;
         }
-        sort_status_cap = cap;
+        part_counts_cap = cap;
     }
     if (2 * bins > bins_cap) {
         sync_once();
@@ -245,8 +244,8 @@ void DeviceScratch::release() {
     rgrad_cap = 0;
     dev_free(&recs);
     recs_cap = 0;
-    dev_free(&sort_status);
-    sort_status_cap = 0;
+    dev_free(&part_counts);
+    part_counts_cap = 0;
     dev_free(&tile_bins);
     bins_cap = 0;
     dev_free(&depth_mm);

@@ -1,16 +1,19 @@
-// sort_and_bin on gfx950: per-image depth range, packed-key emission, a stable onesweep LSD radix
-// sort, and tile bin edges. Restates splax/_rasterize/_sort/_sort.py:29-171 and
+// sort_and_bin on gfx950: per-image depth range, packed-key emission, a stable LSD radix sort,
+// and tile bin edges. Restates splax/_rasterize/_sort/_sort.py:29-171 and
 // splax/_rasterize/_sort/_kernels.py:28-153,214-241; the sort replaces warp-lang's
 // radix_sort_pairs (called at splax/_rasterize/_sort/_sort.py:136).
 //
-// Sort design: one global histogram launch counts all four 8-bit digits of every key; then each
-// of the four passes is a single launch in which a workgroup (4 wave64s) owns the 2048-key
-// partition of its workgroup index, ranks its keys stably with ballot-based digit matching per wave,
-// publishes its per-digit counts and resolves its global per-digit offsets by decoupled look-back
-// over the partitions before it, and scatters keys and values through LDS so that each digit's
-// run is written contiguously. Ranking follows position order (wave-striped items, lanes in order,
-// waves in order, partitions in index order), so the sort is stable: ties keep emission order,
-// which is the reference's (key, position) order.
+// Sort design: one global histogram launch counts every pass's 8-bit digits of every key. Each
+// pass is then reduce-then-scan over 8192-key partitions: (1) every partition counts its digits,
+// (2) one workgroup per digit scans that digit's counts over the partitions from the digit's
+// global base, (3) every partition ranks its keys stably with ballot-based digit matching per
+// wave and scatters keys and values through LDS so that each digit's run (about 32 keys) leaves
+// as a contiguous write. No partition waits on another: on MI355X the eight XCDs have separate
+// L2s, so the per-digit status polling of a single-pass (look-back) sort costs device-scope
+// round trips and partial-line writes that the extra count read does not. Ranking follows
+// position order (wave-striped items, lanes in order, waves in order, partitions in index
+// order), so the sort is stable: ties keep emission order, which is the reference's
+// (key, position) order.
 //
 // Each key carries two values: the reference's value (the flat item id) and the key's emission
 // position. The positions let the backward blend store each intersection's gradient in emission
@@ -76,14 +79,11 @@ minmax_partial_kernel(const float* depths, const int32_t* radii, int32_t n,
     }
 }
 
-// Stage 2; also clears the sort's digit histogram (4 x 256) for the histogram launch.
+// Stage 2.
 __global__ void __launch_bounds__(kMmThreads)
-minmax_final_kernel(const uint32_t* partial, int32_t blocks_per_image, float* mm,
-                    uint32_t* hist) {
+minmax_final_kernel(const uint32_t* partial, int32_t blocks_per_image, float* mm) {
     __shared__ uint32_t s_lo[kMmThreads / 64], s_hi[kMmThreads / 64];
     const int image = blockIdx.x;
-    if (image == 0)
-        for (int i = threadIdx.x; i < 4 * 256; i += kMmThreads) hist[i] = 0u;
     uint32_t lo = 0xffffffffu, hi = 0u;
     for (int b = threadIdx.x; b < blocks_per_image; b += kMmThreads) {
         int64_t slot = (int64_t)image * blocks_per_image + b;
@@ -179,101 +179,69 @@ __global__ void __launch_bounds__(256) emit_keys_kernel(EmitParams P) {
     }
 }
 
-// ------------------------------------------------------------------ digit histogram
-
-constexpr int kHistThreads = 256;
-// Workgroups of the histogram launch: each takes one contiguous chunk and adds its per-pass
-// 256-bin counts with one global atomic per non-zero bin. Same-address device-scope atomics
-// serialise, so the grid is kept small; 128 chunks still spread the read over half the CUs.
-constexpr int kHistBlocks = 128;
-constexpr int kHistChunkAlign = kHistThreads * 4;  // chunk starts stay 16-byte aligned
-
 // The digits a sort visits: 8-bit digits at these shifts (packed key: 0, 8, 16, 24).
 struct PassShifts {
     int32_t n;
     int32_t shift[kMaxPasses];
 };
 
-template <typename K, int kPasses>
-__device__ __forceinline__ void hist_add(uint32_t* h, K k, const PassShifts& ps) {
-#pragma unroll
-    for (int p = 0; p < kPasses; ++p)
-        if (p < ps.n) atomicAdd(&h[p * 256 + (uint32_t)((k >> ps.shift[p]) & 255u)], 1u);
-}
+// ------------------------------------------------------------------ reduce-then-scan passes
 
-template <typename K, int kPasses>
-__global__ void __launch_bounds__(kHistThreads)
-digit_hist_kernel(const K* keys, int64_t M, int64_t chunk, PassShifts ps, uint32_t* hist,
-                  int32_t* bins, int64_t nbins2) {
-    __shared__ uint32_t s_h[kHistThreads / 64][kPasses * 256];
+constexpr int kSortThreads = 1024;
+constexpr int kSortWaves = kSortThreads / 64;
+static_assert(kSortThreads * 4 == kSortTileMin, "smallest partition");
+
+// (1) digit counts of one partition of kItems * kSortThreads keys, stored digit-major:
+// counts[d * parts + p]. The first pass also clears the tile bins (nbins2 > 0).
+template <typename K, int kItems>
+__global__ void __launch_bounds__(kSortThreads)
+rts_count_kernel(const K* __restrict__ keys, int64_t M, int shift, uint32_t* __restrict__ counts,
+                 int64_t parts, int32_t* __restrict__ bins, int64_t nbins2) {
+    __shared__ uint32_t s_h[kSortWaves][256];
     const int tid = threadIdx.x, wave = tid >> 6;
-    for (int i = tid; i < kPasses * 256; i += kHistThreads)
-#pragma unroll
-        for (int w = 0; w < kHistThreads / 64; ++w) s_h[w][i] = 0u;
+    for (int i = tid; i < kSortWaves * 256; i += kSortThreads) (&s_h[0][0])[i] = 0u;
     // tile bins start at (0, 0): the bin-edge launch writes only tiles that own intersections
-    for (int64_t i = (int64_t)blockIdx.x * kHistThreads + tid; i < nbins2;
-         i += (int64_t)gridDim.x * kHistThreads)
+    for (int64_t i = (int64_t)blockIdx.x * kSortThreads + tid; i < nbins2;
+         i += (int64_t)gridDim.x * kSortThreads)
         bins[i] = 0;
     __syncthreads();
-    const int64_t lo = (int64_t)blockIdx.x * chunk;
-    const int64_t hi = lo + chunk < M ? lo + chunk : M;
-    uint32_t* h = s_h[wave];
-    // whole 16-byte groups, four in flight per thread
-    constexpr int kPer = 16 / sizeof(K);
-    const int64_t nvec = hi > lo ? (hi - lo) / kPer : 0;
-    const uint4* kv = reinterpret_cast<const uint4*>(keys + lo);
-    int64_t v = tid;
-    for (; v + 3 * kHistThreads < nvec; v += 4 * kHistThreads) {
-        uint4 q[4];
+    const int64_t base = (int64_t)blockIdx.x * (kItems * kSortThreads);
+    K key[kItems];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) q[u] = kv[v + u * kHistThreads];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const K* e = reinterpret_cast<const K*>(&q[u]);
-#pragma unroll
-            for (int x = 0; x < kPer; ++x) hist_add<K, kPasses>(h, e[x], ps);
-        }
+    for (int i = 0; i < kItems; ++i) {
+        const int64_t pos = base + i * kSortThreads + tid;
+        key[i] = pos < M ? keys[pos] : (K)0;
     }
-    for (; v < nvec; v += kHistThreads) {
-        const uint4 q = kv[v];
-        const K* e = reinterpret_cast<const K*>(&q);
 #pragma unroll
-        for (int x = 0; x < kPer; ++x) hist_add<K, kPasses>(h, e[x], ps);
+    for (int i = 0; i < kItems; ++i) {
+        const int64_t pos = base + i * kSortThreads + tid;
+        if (pos < M) atomicAdd(&s_h[wave][(uint32_t)(key[i] >> shift) & 255u], 1u);
     }
-    for (int64_t i = lo + kPer * nvec + tid; i < hi; i += kHistThreads)
-        hist_add<K, kPasses>(h, keys[i], ps);
     __syncthreads();
-    for (int i = tid; i < kPasses * 256; i += kHistThreads) {
+    if (tid < 256) {
         uint32_t c = 0;
 #pragma unroll
-        for (int w = 0; w < kHistThreads / 64; ++w) c += s_h[w][i];
-        if (c) atomicAdd(hist + i, c);
+        for (int w = 0; w < kSortWaves; ++w) c += s_h[w][tid];
+        counts[(int64_t)tid * parts + blockIdx.x] = c;
     }
 }
 
-// ------------------------------------------------------------------ onesweep pass
-
-constexpr int kSortThreads = 256;
-constexpr int kSortWaves = kSortThreads / 64;
-constexpr int kSortItems = 8;
-constexpr int kSortTile = kSortThreads * kSortItems;
-
-// Exclusive scan of one value per thread over a 256-thread workgroup.
-__device__ __forceinline__ uint32_t block_exclusive_scan_256(uint32_t v, uint32_t* s_tmp,
-                                                             uint32_t* total) {
+// Exclusive scan of one value per thread over the first 256 threads (waves 0-3) of the
+// workgroup; every thread of the workgroup must call it.
+__device__ __forceinline__ uint32_t scan_256(uint32_t v, uint32_t* s_tmp, uint32_t* total) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint32_t incl = v;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-        uint32_t o = __shfl_up(incl, off, 64);
+        const uint32_t o = __shfl_up(incl, off, 64);
         if (lane >= off) incl += o;
     }
-    if (lane == 63) s_tmp[wave] = incl;
+    if (lane == 63 && wave < 4) s_tmp[wave] = incl;
     __syncthreads();
     uint32_t off = 0, tot = 0;
 #pragma unroll
-    for (int w = 0; w < kSortWaves; ++w) {
-        uint32_t x = s_tmp[w];
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t x = s_tmp[w];
         if (w < wave) off += x;
         tot += x;
     }
@@ -282,49 +250,70 @@ __device__ __forceinline__ uint32_t block_exclusive_scan_256(uint32_t v, uint32_
     return off + incl - v;
 }
 
-// Two values travel with each key: its emission position and the flat item that emitted it.
-// The first pass generates the positions (vals_in == nullptr gives value = position) and reads
-// the items in emission order, so no pass gathers at random. K is the key word (uint32_t for the
+// (2) one workgroup per digit d: counts[d][p] <- sum_{q < p} counts[d][q], and totals[d].
+__global__ void __launch_bounds__(256)
+rts_scan_kernel(uint32_t* __restrict__ counts, int64_t parts, uint32_t* __restrict__ totals) {
+    __shared__ uint32_t s_tmp[4];
+    const int d = blockIdx.x, tid = threadIdx.x;
+    uint32_t carry = 0;
+    uint32_t* row = counts + (int64_t)d * parts;
+    for (int64_t p0 = 0; p0 < parts; p0 += 256) {
+        const int64_t p = p0 + tid;
+        const uint32_t v = p < parts ? row[p] : 0u;
+        uint32_t tot;
+        const uint32_t ex = scan_256(v, s_tmp, &tot);
+        if (p < parts) row[p] = carry + ex;
+        carry += tot;
+    }
+    if (tid == 0) totals[d] = carry;
+}
+
+// (3) Stable scatter of one partition. A key of digit d at partition-local sorted slot j goes
+// to (keys with a smaller digit) + offsets[d][p] + (j - first slot of d). The first pass
+// generates the emission positions (vals_in == nullptr gives value = position) and reads the
+// items in emission order, so no pass gathers at random. K is the key word (uint32_t for the
 // packed key, uint64_t for the 64-bit key, ordered as unsigned).
-template <typename K>
+template <typename K, int kItems>
 __global__ void __launch_bounds__(kSortThreads)
-onesweep_pass_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
-                     const int32_t* __restrict__ ids_in, K* __restrict__ keys_out,
-                     int32_t* __restrict__ vals_out, int32_t* __restrict__ ids_out, int64_t M,
-                     int shift, const uint32_t* __restrict__ hist, uint64_t* status,
-                     uint32_t epoch, uint32_t* err) {
-    __shared__ K s_keys[kSortTile];
-    __shared__ uint32_t s_vals[kSortTile];
-    __shared__ uint32_t s_ids[kSortTile];
+rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
+                   const int32_t* __restrict__ ids_in, K* __restrict__ keys_out,
+                   int32_t* __restrict__ vals_out, int32_t* __restrict__ ids_out, int64_t M,
+                   int shift, const uint32_t* __restrict__ offsets,
+                   const uint32_t* __restrict__ totals, int64_t parts) {
+    constexpr int kTile = kItems * kSortThreads;
+    __shared__ K s_keys[kTile];
+    __shared__ uint32_t s_vals[kTile];
+    __shared__ uint32_t s_ids[kTile];
     __shared__ uint32_t s_cnt[kSortWaves][256];
     __shared__ uint32_t s_local_start[256];
     __shared__ int32_t s_dest_base[256];
-    __shared__ uint32_t s_tmp[kSortWaves];
+    __shared__ uint32_t s_tmp[4];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-    for (int w = 0; w < kSortWaves; ++w) s_cnt[w][tid] = 0u;
+    for (int i = tid; i < kSortWaves * 256; i += kSortThreads) (&s_cnt[0][0])[i] = 0u;
     __syncthreads();
-    const uint32_t part = blockIdx.x;
-    const int64_t base = (int64_t)part * kSortTile;
-    const int64_t wbase = base + (int64_t)wave * (kSortItems * 64);
+    const int64_t part = blockIdx.x;
+    const int64_t base = part * kTile;
+    const int64_t wbase = base + (int64_t)wave * (kItems * 64);
 
     // keys and values are all loaded up front so their latencies overlap
-    K key[kSortItems];
-    uint32_t val[kSortItems], gid[kSortItems];
+    K key[kItems];
+    uint32_t val[kItems], gid[kItems];
 #pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
-        int64_t pos = wbase + i * 64 + lane;
+    for (int i = 0; i < kItems; ++i) {
+        const int64_t pos = wbase + i * 64 + lane;
         key[i] = pos < M ? keys_in[pos] : ~(K)0;
         val[i] = pos < M ? (vals_in ? (uint32_t)vals_in[pos] : (uint32_t)pos) : 0u;
         gid[i] = pos < M ? (uint32_t)ids_in[pos] : 0u;
     }
+    const uint32_t total_d = tid < 256 ? totals[tid] : 0u;
+    const uint32_t offset_d = tid < 256 ? offsets[(int64_t)tid * parts + part] : 0u;
 
     // stable per-wave ranking: lanes with equal digits found by 8 ballots
     const uint64_t lt_mask = (1ull << lane) - 1ull;
-    uint32_t rank[kSortItems];
+    uint32_t rank[kItems];
 #pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
+    for (int i = 0; i < kItems; ++i) {
         const uint32_t d = (uint32_t)(key[i] >> shift) & 255u;
         uint64_t peers = ~0ull;
 #pragma unroll
@@ -340,70 +329,33 @@ onesweep_pass_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ 
     }
     __syncthreads();
 
-    // per digit (thread = digit): wave offsets, local digit starts, look-back
-    const uint32_t d = (uint32_t)tid;
-    uint32_t c[kSortWaves];
+    // per digit (thread = digit): wave offsets, local digit starts, global destinations
     uint32_t tot = 0;
+    if (tid < 256) {
+        uint32_t c[kSortWaves];
 #pragma unroll
-    for (int w = 0; w < kSortWaves; ++w) {
-        c[w] = s_cnt[w][d];
-        tot += c[w];
-    }
-    uint32_t run = 0;
-#pragma unroll
-    for (int w = 0; w < kSortWaves; ++w) {
-        s_cnt[w][d] = run;
-        run += c[w];
-    }
-    const uint32_t local_start = block_exclusive_scan_256(tot, s_tmp, nullptr);
-    const uint32_t global_start = block_exclusive_scan_256(hist[d], s_tmp, nullptr);
-    s_local_start[d] = local_start;
-    // Decoupled look-back for digit d. Predecessors are polled four at a time (independent
-    // device-scope loads, one round trip per window) and folded nearest first until an inclusive
-    // prefix is found. Only lower workgroup indices are awaited, and in-order workgroup dispatch
-    // has placed them on the device already.
-    uint64_t* st = status + d;
-    uint32_t prefix = 0;
-    if (part == 0) {
-        atomic_store_relaxed(st, status_word(epoch, true, tot));
-    } else {
-        atomic_store_relaxed(st + (int64_t)part * 256, status_word(epoch, false, tot));
-        int64_t j = (int64_t)part - 1;
-        uint32_t spins = 0;
-        while (j >= 0) {
-            uint64_t w[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                w[k] = (j - k >= 0) ? atomic_load_relaxed(st + (j - k) * 256)
-                                    : status_word(epoch, true, 0u);
-            int consumed = 0;
-            bool found = false;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                if (found || consumed < k) continue;  // stop at the first gap or inclusive
-                if ((uint32_t)(w[k] >> 32) != epoch) continue;
-                prefix += (uint32_t)(w[k] & 0x7fffffffull);
-                consumed = k + 1;
-                found = (w[k] & kInclusiveBit) != 0;
-            }
-            if (found) break;
-            if (consumed == 0) {
-                if (++spins >= kSpinLimit) {
-                    atomicOr(err, kDevErrLookback);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-            j -= consumed;
+        for (int w = 0; w < kSortWaves; ++w) {
+            c[w] = s_cnt[w][tid];
+            tot += c[w];
         }
-        atomic_store_relaxed(st + (int64_t)part * 256, status_word(epoch, true, prefix + tot));
+        uint32_t run = 0;
+#pragma unroll
+        for (int w = 0; w < kSortWaves; ++w) {
+            s_cnt[w][tid] = run;
+            run += c[w];
+        }
     }
-    s_dest_base[d] = (int32_t)((int64_t)global_start + prefix - local_start);
+    const uint32_t local_start = scan_256(tot, s_tmp, nullptr);
+    const uint32_t digit_base = scan_256(total_d, s_tmp, nullptr);
+    if (tid < 256) {
+        s_local_start[tid] = local_start;
+        s_dest_base[tid] = (int32_t)((int64_t)digit_base + offset_d - local_start);
+    }
     __syncthreads();
 
     // keys and values into LDS at their partition-sorted slot
 #pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
+    for (int i = 0; i < kItems; ++i) {
         const uint32_t dd = (uint32_t)(key[i] >> shift) & 255u;
         const uint32_t slot = s_local_start[dd] + s_cnt[wave][dd] + rank[i];
         s_keys[slot] = key[i];
@@ -412,9 +364,9 @@ onesweep_pass_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ 
     }
     __syncthreads();
     // each digit's run is contiguous in the output: consecutive j write consecutive addresses
-    const int64_t valid = (M - base) < kSortTile ? (M - base) : kSortTile;
+    const int64_t valid = (M - base) < kTile ? (M - base) : kTile;
 #pragma unroll
-    for (int r = 0; r < kSortItems; ++r) {
+    for (int r = 0; r < kItems; ++r) {
         const int j = r * kSortThreads + tid;
         if (j < valid) {
             const K k = s_keys[j];
@@ -424,6 +376,21 @@ onesweep_pass_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ 
             ids_out[dest] = (int32_t)s_ids[j];
         }
     }
+}
+
+// One pass of the sort: count, scan, scatter with kItems keys per thread.
+template <typename K, int kItems>
+static void launch_pass(const K* keys_in, const int32_t* vals_in, const int32_t* ids_in,
+                        K* keys_out, int32_t* vals_out, int32_t* ids_out, int64_t M, int shift,
+                        uint32_t* counts, uint32_t* totals, int32_t* bins, int64_t nbins2,
+                        hipStream_t stream) {
+    const int64_t parts = (M + (int64_t)kItems * kSortThreads - 1) / ((int64_t)kItems * kSortThreads);
+    hipLaunchKernelGGL((rts_count_kernel<K, kItems>), dim3((unsigned)parts), dim3(kSortThreads),
+                       0, stream, keys_in, M, shift, counts, parts, bins, nbins2);
+    hipLaunchKernelGGL(rts_scan_kernel, dim3(256), dim3(256), 0, stream, counts, parts, totals);
+    hipLaunchKernelGGL((rts_scatter_kernel<K, kItems>), dim3((unsigned)parts),
+                       dim3(kSortThreads), 0, stream, keys_in, vals_in, ids_in, keys_out,
+                       vals_out, ids_out, M, shift, counts, totals, parts);
 }
 
 // ------------------------------------------------------------------ bin edges
@@ -540,11 +507,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
                                   hipMemcpyDeviceToHost, stream) != hipSuccess ||
                    hipEventRecord(sc.count_event, stream) != hipSuccess))
         return fail(kErrRuntime, "count readback enqueue failed");
-    if (wide) {
-        // the 64-bit key carries the raw depth: no depth range, only the histogram to clear
-        rc = fill_zero_i32(reinterpret_cast<int32_t*>(sc.hist), kMaxPasses * 256, stream);
-        if (rc) return rc;
-    } else {
+    if (!wide) {  // the 64-bit key carries the raw depth: no depth range
         const int32_t bpi =
             (int32_t)((in.n + kMmThreads * kMmItems - 1) / (kMmThreads * kMmItems));
         if ((int64_t)bpi * B * 2 > sc.mm_partial_cap)
@@ -553,7 +516,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         hipLaunchKernelGGL(minmax_partial_kernel, dim3(bpi, B), dim3(kMmThreads), 0, stream,
                            in.depths, in.radii, in.n, bpi, sc.mm_partial);
         hipLaunchKernelGGL(minmax_final_kernel, dim3(B), dim3(kMmThreads), 0, stream,
-                           sc.mm_partial, bpi, sc.depth_mm, sc.hist);
+                           sc.mm_partial, bpi, sc.depth_mm);
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "minmax launch failed");
     }
     int64_t M;
@@ -599,19 +562,9 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     }
     {
         StageTimer tm(stream, kStageSort);
-        int64_t chunk = (M + kHistBlocks - 1) / kHistBlocks;
-        chunk = (chunk + kHistChunkAlign - 1) / kHistChunkAlign * kHistChunkAlign;
-        const int64_t hb = (M + chunk - 1) / chunk;
-        if (wide)
-            hipLaunchKernelGGL((digit_hist_kernel<uint64_t, kMaxPasses>), dim3((unsigned)hb),
-                               dim3(kHistThreads), 0, stream, sc.wkeys[0], M, chunk, ps,
-                               sc.hist, bins, 2 * nbins);
-        else
-            hipLaunchKernelGGL((digit_hist_kernel<uint32_t, 4>), dim3((unsigned)hb),
-                               dim3(kHistThreads), 0, stream,
-                               reinterpret_cast<const uint32_t*>(sc.keys[0]), M, chunk, ps,
-                               sc.hist, bins, 2 * nbins);
-        const int64_t parts = (M + kSortTile - 1) / kSortTile;
+        // 8192-key partitions once there are enough of them to fill the device: their digit runs
+        // (about 32 keys) leave as whole 128-byte lines; smaller sorts use 4096-key partitions
+        const bool big = M >= kSortBigM;
         // passes ping-pong 0 -> 1 -> 0 ...; the first pass generates the emission positions,
         // the last writes positions and items straight into their final buffers (the caller's
         // when it keeps the sorted lists)
@@ -621,19 +574,27 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
             const int32_t* vin = pass == 0 ? nullptr : sc.vals[src];
             int32_t* vout = last ? pos_final : sc.vals[dst];
             int32_t* iout = last ? ids_final : sc.gids[dst];
-            if (wide)
-                hipLaunchKernelGGL(onesweep_pass_kernel<uint64_t>, dim3((unsigned)parts),
-                                   dim3(kSortThreads), 0, stream, sc.wkeys[src], vin,
-                                   sc.gids[src], sc.wkeys[dst], vout, iout, M, ps.shift[pass],
-                                   sc.hist + 256 * pass, sc.sort_status, sc.next_epoch(),
-                                   sc.tickets + kDeviceError);
-            else
-                hipLaunchKernelGGL(onesweep_pass_kernel<uint32_t>, dim3((unsigned)parts),
-                                   dim3(kSortThreads), 0, stream,
-                                   reinterpret_cast<const uint32_t*>(sc.keys[src]), vin,
-                                   sc.gids[src], reinterpret_cast<uint32_t*>(sc.keys[dst]), vout,
-                                   iout, M, ps.shift[pass], sc.hist + 256 * pass,
-                                   sc.sort_status, sc.next_epoch(), sc.tickets + kDeviceError);
+            const int shift = ps.shift[pass];
+            const int64_t nb2 = pass == 0 ? 2 * nbins : 0;
+            if (wide) {
+                const uint64_t* ki = sc.wkeys[src];
+                uint64_t* ko = sc.wkeys[dst];
+                if (big)
+                    launch_pass<uint64_t, 8>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                                             sc.part_counts, sc.hist, bins, nb2, stream);
+                else
+                    launch_pass<uint64_t, 4>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                                             sc.part_counts, sc.hist, bins, nb2, stream);
+            } else {
+                const uint32_t* ki = reinterpret_cast<const uint32_t*>(sc.keys[src]);
+                uint32_t* ko = reinterpret_cast<uint32_t*>(sc.keys[dst]);
+                if (big)
+                    launch_pass<uint32_t, 8>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                                             sc.part_counts, sc.hist, bins, nb2, stream);
+                else
+                    launch_pass<uint32_t, 4>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                                             sc.part_counts, sc.hist, bins, nb2, stream);
+            }
         }
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "sort launch failed");
     }

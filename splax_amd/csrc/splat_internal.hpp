@@ -74,6 +74,8 @@ void set_force_wide_keys(bool force);
 
 // Digit passes of the sort: at most 8 bytes of a 64-bit key.
 constexpr int kMaxPasses = 8;
+constexpr int kSortTileMin = 4096;   // keys per radix-sort partition (smallest size used)
+constexpr int64_t kSortBigM = 8 << 20;  // from this many keys on, partitions hold 8192 keys
 
 // Inputs of sort_and_bin and the blends.
 struct RasterInputs {
@@ -115,8 +117,8 @@ struct DeviceScratch {
     float* rgrad = nullptr; int64_t rgrad_cap = 0;
     // blends: packed per-item records (4 float4 each)
     float4* recs = nullptr; int64_t recs_cap = 0;
-    uint64_t* sort_status = nullptr; int64_t sort_status_cap = 0;  // partitions * 256
-    uint32_t* hist = nullptr;                                       // kMaxPasses * 256
+    uint32_t* part_counts = nullptr; int64_t part_counts_cap = 0;  // 256 * partitions
+    uint32_t* hist = nullptr;                                       // 256 digit totals
     int32_t* tile_bins = nullptr; int64_t bins_cap = 0;             // (start, end) pairs
     float* depth_mm = nullptr; int64_t mm_cap = 0;                  // 2 * B
     uint32_t* mm_partial = nullptr; int64_t mm_partial_cap = 0;     // 2 * blocks
