@@ -1,26 +1,31 @@
 // Forward and backward alpha blend on gfx950.
 //
 // One workgroup of 256 threads (four wave64s) per (image, 16x16 tile), as in the reference
-// (splax/_rasterize/_kernels.py:63-87,469-500). Each wave owns one 8x8 quadrant of the tile. The
-// tile's sorted range is staged in LDS in batches of 256 records (three float4 per record: every
-// lane of a wave reads the same record, an LDS broadcast). While staging, each record gets
+// (splax/_rasterize/_kernels.py:63-87,469-500). Each wave owns one 8x8 quadrant of the tile and
+// each 16-lane row of a wave one 4x4 sub-block of it. The tile's sorted range is staged in LDS in
+// batches of 256 records (three float4 per record). While staging, each record gets
 //   - sigma_max: a conservative bound (log(255 o) + 1e-3) above which o e^-sigma < 1/255, so a
 //     lane skips the exponential for pairs the reference rejects anyway, and
-//   - a 4-bit quadrant mask: the quadrants whose pixel centres can reach sigma <= sigma_max,
-//     from the ellipse's bounding box;
-// and each wave then walks only the compacted, order-preserving list of records that reach its
-// quadrant. Both filters remove only pairs that the reference's `sigma < 0 or alpha < 1/255`
-// test rejects, so the per-pixel sequence of blended pairs (and every float operation on it) is
-// the reference's, and the forward image is bit-identical to the CPU oracle.
+//   - a 16-bit sub-block mask: the 4x4 sub-blocks whose pixel centres can reach
+//     sigma <= sigma_max, from the ellipse's bounding box;
+// and each row then walks only the compacted, order-preserving list of records that reach its
+// sub-block (the four rows of a wave walk their own lists in lockstep, each row reading its own
+// record, an LDS broadcast within the row). A wave takes as many steps as its longest row list,
+// about 0.7 of the quadrant list a whole-wave walk would take. Both filters remove only pairs
+// that the reference's `sigma < 0 or alpha < 1/255` test rejects, so the per-pixel sequence of
+// blended pairs (and every float operation on it) is the reference's, and the forward image is
+// bit-identical to the CPU oracle.
 //
-// Backward: the same staging walked back to front from the workgroup's largest final_idx. A
-// pixel's contribution to a record is nine floats; per record the contributing lanes of a wave
-// reduce them with a reduce-scatter (v_permlane32_swap, v_permlane16_swap, then DPP row shifts:
-// 28 VALU for nine values) and add the totals into the record's LDS accumulator. After each batch
-// every record stores its nine sums (plain stores, no global atomics) at its emission position,
-// where all intersections of one item are contiguous; grad_gather_kernel then adds them per item
-// in a fixed order and writes the four gradient outputs. Only the LDS sums of one record over
-// the tile's four quadrant waves depend on the order in which the waves arrive.
+// Backward: the same staging walked back to front from the workgroup's largest final_idx, each
+// wave over the list of its whole quadrant (per-row walks there cost more in LDS bank conflicts
+// and same-record accumulator collisions than they save in steps). A pixel's contribution to a
+// record is nine floats; per record the contributing lanes of a wave reduce them with a
+// reduce-scatter (v_permlane32_swap, v_permlane16_swap, then DPP row shifts: 28 VALU for nine
+// values) and add the totals into the record's LDS accumulator. After each batch every record
+// stores its nine sums (plain stores, no global atomics) at its emission position, where all
+// intersections of one item are contiguous; grad_gather_kernel then adds them per item in a
+// fixed order and writes the four gradient outputs. Only the LDS sums of one record over the
+// tile's four quadrant waves depend on the order in which the waves arrive.
 #include "splat_common.hpp"
 #include "splat_internal.hpp"
 
@@ -36,11 +41,18 @@ struct BlendCommon {
     int64_t total;  // geometry rows (B_geom * n): ids outside [0, total) are ignored
 };
 
-// Pixel of thread `tid` in its tile: wave w = quadrant (w & 1, w >> 1), lane = 8x8 raster.
+// Pixel of thread `tid` in its tile: wave w = quadrant (w & 1, w >> 1), row r = lane >> 4 =
+// 4x4 sub-block (r & 1, r >> 1) of the quadrant, lane & 15 = 4x4 raster.
 __device__ __forceinline__ void tile_pixel(int tid, int tile_x, int tile_y, int& i, int& j) {
-    const int wave = tid >> 6, lane = tid & 63;
-    i = tile_y * kBlockWidth + (wave >> 1) * 8 + (lane >> 3);
-    j = tile_x * kBlockWidth + (wave & 1) * 8 + (lane & 7);
+    const int wave = tid >> 6, lane = tid & 63, row = lane >> 4, l = lane & 15;
+    i = tile_y * kBlockWidth + (wave >> 1) * 8 + (row >> 1) * 4 + (l >> 2);
+    j = tile_x * kBlockWidth + (wave & 1) * 8 + (row & 1) * 4 + (l & 3);
+}
+
+// Sub-block (0..15, row-major over the tile's 4x4 grid of 4x4 blocks) of the thread's row.
+__device__ __forceinline__ int row_subblock(int tid) {
+    const int wave = tid >> 6, row = (tid & 63) >> 4;
+    return ((wave >> 1) * 2 + (row >> 1)) * 4 + (wave & 1) * 2 + (row & 1);
 }
 
 // Packed record of one geometry item, 64 bytes (one aligned segment per staged intersection):
@@ -117,73 +129,101 @@ __global__ void __launch_bounds__(256) pack_records_kernel(PackParams P) {
     for (int k = threadIdx.x; k < count; k += 256) dst[k] = s_rec[k];
 }
 
-// Quadrants of the tile at (tile_x, tile_y) whose pixel centres a packed record can reach.
-__device__ __forceinline__ uint32_t quadrant_mask(const float4& r0, const float4& r3,
+// Sub-blocks (bit 4 r + c: block row r, column c of the tile's 4x4 grid of 4x4 pixel blocks)
+// of the tile at (tile_x, tile_y) whose pixel centres a packed record can reach.
+__device__ __forceinline__ uint32_t subblock_mask(const float4& r0, const float4& r3,
                                                   int tile_x, int tile_y) {
     const uint32_t mode = __float_as_uint(r3.z);
     if (mode == kCullNone) return 0u;
-    if (mode != kCullBox) return 0xfu;
-    uint32_t qmask = 0u;
+    if (mode != kCullBox) return 0xffffu;
+    uint32_t xm = 0u, ym = 0u;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const float x0 = (float)(tile_x * kBlockWidth + (q & 1) * 8) + 0.5f;
-        const float y0 = (float)(tile_y * kBlockWidth + (q >> 1) * 8) + 0.5f;
-        const bool hit = (r0.x + r3.x >= x0) && (r0.x - r3.x <= x0 + 7.0f) &&
-                         (r0.y + r3.y >= y0) && (r0.y - r3.y <= y0 + 7.0f);
-        qmask |= hit ? (1u << q) : 0u;
+    for (int c = 0; c < 4; ++c) {
+        const float x0 = (float)(tile_x * kBlockWidth + c * 4) + 0.5f;
+        const float y0 = (float)(tile_y * kBlockWidth + c * 4) + 0.5f;
+        xm |= ((r0.x + r3.x >= x0) && (r0.x - r3.x <= x0 + 3.0f)) ? (1u << c) : 0u;
+        ym |= ((r0.y + r3.y >= y0) && (r0.y - r3.y <= y0 + 3.0f)) ? (1u << c) : 0u;
     }
-    return qmask;
+    uint32_t m = 0u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) m |= ((ym >> r) & 1u) ? (xm << (4 * r)) : 0u;
+    return m;
 }
 
-// LDS record of one batch: r0 = (x, y, a, b), r1 = (c, o, sigma_max, quadrant mask bits),
-// r2 = (red, green, blue, depth or 0), plus per-quadrant compacted record lists.
+// LDS record of one batch: r0 = (x, y, a, b), r1 = (c, o, sigma_max, 0), r2 = (red, green,
+// blue, depth), each record's sub-block mask, and per-sub-block compacted record lists.
 struct BatchLds {
     float4 r0[kTile];
     float4 r1[kTile];
     float4 r2[kTile];
-    uint8_t list[4][kTile];
-    uint32_t cnt[4][4];  // [wave][quadrant]
+    uint16_t mask[kTile];
+    uint8_t list[16][kTile];
 };
 
-// Stages record `src` of the sorted range into slot `tid` and builds the quadrant lists.
-// `live` is false for the clamped tail slots of the last batch (they reach no quadrant).
-// Returns, for the calling wave's quadrant, the list length. Contains two barriers.
-__device__ __forceinline__ int stage_batch(const BlendCommon& C, BatchLds& L, int32_t src,
-                                           bool live, int tile_x, int tile_y) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+// Lengths of the calling lane's row list and of the longest row list of its wave.
+struct RowLens {
+    int mine;
+    int wave_max;
+};
+
+// Stages record `src` of the sorted range into slot `tid` (one barrier), then each wave builds
+// its own record lists from the staged masks, in slot order: with kRows the lists of its four
+// sub-blocks (one per 16-lane row), otherwise the list of its whole quadrant (a record reaches a
+// quadrant when it reaches one of its sub-blocks, which is the 8x8 box test). `live` is false
+// for the clamped tail slots of the last batch (they reach no sub-block).
+template <bool kRows>
+__device__ __forceinline__ RowLens stage_batch(const BlendCommon& C, BatchLds& L, int32_t src,
+                                               bool live, int tile_x, int tile_y) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, row = lane >> 4;
     int64_t g = C.ids[src];
-    uint32_t qm = 0u;
+    uint32_t m = 0u;
     float4 r0 = make_float4(0.f, 0.f, 0.f, 0.f), r1 = r0, r2 = r0;
     if (live && g >= 0 && g < C.total) {
         const float4* rec = C.recs + 4 * g;
         r0 = rec[0];
         r1 = rec[1];
         r2 = rec[2];
-        qm = quadrant_mask(r0, rec[3], tile_x, tile_y);
-        r1.w = __uint_as_float(qm);
+        m = subblock_mask(r0, rec[3], tile_x, tile_y);
     }
     L.r0[tid] = r0;
     L.r1[tid] = r1;
     L.r2[tid] = r2;
-    uint64_t bal[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        bal[q] = __ballot((qm >> q) & 1u);
-        if (lane == 0) L.cnt[wave][q] = (uint32_t)__popcll(bal[q]);
-    }
+    L.mask[tid] = (uint16_t)m;
     __syncthreads();
+    // this wave's sub-blocks: rows 0..3 -> sb0, sb0 + 1, sb0 + 4, sb0 + 5
+    const int sb0 = (wave >> 1) * 8 + (wave & 1) * 2;
     const uint64_t lt = (1ull << lane) - 1ull;
+    if constexpr (kRows) {
+        int n[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        if ((qm >> q) & 1u) {
-            uint32_t base = 0;
-            for (int w = 0; w < wave; ++w) base += L.cnt[w][q];
-            L.list[q][base + (uint32_t)__popcll(bal[q] & lt)] = (uint8_t)tid;
+        for (int c = 0; c < kTile / 64; ++c) {
+            const uint32_t mc = L.mask[c * 64 + lane];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int b = sb0 + (r & 1) + (r >> 1) * 4;
+                const bool bit = (mc >> b) & 1u;
+                const uint64_t bal = __ballot(bit);
+                if (bit) L.list[b][n[r] + (int)__popcll(bal & lt)] = (uint8_t)(c * 64 + lane);
+                n[r] += (int)__popcll(bal);
+            }
         }
+        __builtin_amdgcn_wave_barrier();
+        const int mine = row == 0 ? n[0] : row == 1 ? n[1] : row == 2 ? n[2] : n[3];
+        const int a = n[0] > n[1] ? n[0] : n[1], b = n[2] > n[3] ? n[2] : n[3];
+        return RowLens{mine, a > b ? a : b};
+    } else {
+        const uint32_t qbits = (0x33u << sb0);  // the quadrant's four sub-blocks
+        int nq = 0;
+#pragma unroll
+        for (int c = 0; c < kTile / 64; ++c) {
+            const bool bit = (L.mask[c * 64 + lane] & qbits) != 0u;
+            const uint64_t bal = __ballot(bit);
+            if (bit) L.list[wave][nq + (int)__popcll(bal & lt)] = (uint8_t)(c * 64 + lane);
+            nq += (int)__popcll(bal);
+        }
+        __builtin_amdgcn_wave_barrier();
+        return RowLens{nq, nq};
     }
-    const int len = (int)(L.cnt[0][wave] + L.cnt[1][wave] + L.cnt[2][wave] + L.cnt[3][wave]);
-    __syncthreads();
-    return len;
 }
 
 // Wave-uniform value as a scalar (the compiler cannot prove uniformity of values derived from
@@ -220,13 +260,14 @@ template <bool kDepth>
 __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
     __shared__ BatchLds L;
     const BlendCommon& C = P.c;
-    const int tid = threadIdx.x, wave = tid >> 6;
+    const int tid = threadIdx.x;
     const int32_t tile_g = blockIdx.x;
     const int32_t image_id = tile_g / C.num_tiles;
     const int32_t tile_local = tile_g - image_id * C.num_tiles;
     const int tile_x = tile_local % C.tiles_x, tile_y = tile_local / C.tiles_x;
     int i, j;
     tile_pixel(tid, tile_x, tile_y, i, j);
+    const int sb = row_subblock(tid);
     const float px = (float)j + 0.5f, py = (float)i + 0.5f;
     const bool inside = i < C.img_h && j < C.img_w;
     bool done = !inside;
@@ -242,19 +283,20 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
         if (__syncthreads_count(done) >= kTile) break;
         const int32_t batch_start = range_start + bt * kTile;
         const int32_t src = iminw(batch_start + tid, range_end - 1);
-        const int len =
-            uniform(stage_batch(C, L, src, batch_start + tid < range_end, tile_x, tile_y));
+        const RowLens len =
+            stage_batch<true>(C, L, src, batch_start + tid < range_end, tile_x, tile_y);
         if (__ballot(!done) == 0ull) continue;
-        const uint8_t* list = L.list[uniform(wave)];
-        for (int k = 0; k < len; ++k) {
-            // the wave stops walking its list once all of its pixels are done
+        const uint8_t* list = L.list[sb];
+        for (int k = 0; k < len.wave_max; ++k) {
+            // the wave stops walking once all of its pixels are done
             if (__builtin_amdgcn_ballot_w64(!done) == 0ull) break;
-            const int t = uniform(list[k]);
+            const bool has = k < len.mine;  // uniform per row
+            const int t = list[has ? k : 0];
             const float4 r0 = L.r0[t], r1 = L.r1[t];
             const float dx = r0.x - px, dy = r0.y - py;
             const float sigma = 0.5f * (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
             // bitwise: no short-circuit branch around the sigma_max read (NaN sigma fails both)
-            if (!((!done) & (sigma >= 0.0f) & (sigma <= r1.z))) continue;
+            if (!(has & (!done) & (sigma >= 0.0f) & (sigma <= r1.z))) continue;
             const float alpha = minw(kAlphaMax, r1.y * exp_core(-sigma));
             if (alpha < kAlphaThresh) continue;
             const float next_T = T * (1.0f - alpha);
@@ -433,7 +475,6 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     // a final_idx from the matching forward lies inside the tile's range; clamp anything else
     const int32_t start_idx = iminw(s_max, range_end - 1);
     const int32_t num_batches = (start_idx - range_start + kTile) / kTile;
-    const int row = lane >> 4;
     const int64_t rg_off = P.sel_geom ? 0 : (int64_t)image_id * P.M;
     {
         // intersections above every final index of the tile contribute nothing
@@ -446,12 +487,13 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
         }
     }
 
+    const int row = lane >> 4;
     for (int32_t bt = 0; bt < num_batches; ++bt) {
         const int32_t batch_end = start_idx - bt * kTile;
         const int32_t src = imaxw(batch_end - tid, range_start);
         const bool live = batch_end - tid >= range_start;
         const int32_t my_pos = live ? P.pos[src] : -1;  // emission position of slot tid
-        const int len = uniform(stage_batch(C, L, src, live, tile_x, tile_y));
+        const int len = uniform(stage_batch<false>(C, L, src, live, tile_x, tile_y).wave_max);
         const uint8_t* list = L.list[uniform(wave)];
         for (int k = 0; k < len; ++k) {
             const int t = uniform(list[k]);
