@@ -209,6 +209,8 @@ def main():
         p.requires_grad_(True)
     B = scene.B
     vm = t(scene.viewmats if B > 1 else scene.viewmats[0])
+    if args.config == 3:
+        vm.requires_grad_(True)  # config 3 differentiates the camera poses too
     bg = t(scene.background)
     target = t(scene.targets if B > 1 else scene.targets[0])
     H, W = scene.img_shape
@@ -221,6 +223,7 @@ def main():
     def step():
         for p in params:
             p.grad = None
+        vm.grad = None
         img = forward()
         loss = torch.nn.functional.mse_loss(img, target)
         loss.backward()
@@ -311,7 +314,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded numpy PCG64, BASELINE.json config distributions)",
         "config": {"workload": f"config{args.config}", "gaussians": scene.n, "cameras": B,
-                   "img_shape": [H, W], "loss": "mse", "parallelism": "single-gpu"},
+                   "img_shape": [H, W], "loss": "mse", "viewmat_grads": args.config == 3,
+                   "parallelism": "single-gpu"},
         "stage_ms_per_step": stage_ms_per_step,
         "counts": counts,
         "roofline": roofline,

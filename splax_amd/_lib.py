@@ -36,7 +36,7 @@ _SIGS = {
     "splat_project_fwd": [_vp] + [_vp, _i64] * 6 + [_vp, _i32, _i32, _i32, _i64, _i32, _i32]
     + [_f32] * 6 + [_vp] * 6 + [_i32],
     "splat_project_bwd": [_vp] + [_vp, _i64] * 10 + [_vp, _i32, _i32, _i32, _i32, _f32, _f32,
-                                                     _f32] + [_vp] * 5 + [_i32],
+                                                     _f32] + [_vp] * 5 + [_i32, _i32],
     "splat_rasterize_fwd": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_i32] * 4 + [_vp] * 4,
     "splat_rasterize_depth_fwd": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_i32] * 4 + [_vp] * 5,
     "splat_rasterize_bwd": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_vp, _vp, _vp, _i64]

@@ -63,18 +63,19 @@ def project_fwd(means, scales, quats, viewmat, opac, transforms, transform_ids, 
 
 def project_bwd(means, scales, quats, viewmat, radii, conics, v_xy, v_depth, v_conic,
                 transforms, transform_ids, *, n, B, num_transforms, has_transforms, f,
-                glob_scale, quats_wxyz=False):
+                glob_scale, quats_wxyz=False, fold=False):
     """_project_bwd_warp (splax/_project/_kernels.py:257-341).
 
     v_depth may be None (a zero depth cotangent); v_tf is None without transforms. v_quat comes
-    in the layout of quats (xyzw, or wxyz with ``quats_wxyz``)."""
+    in the layout of quats (xyzw, or wxyz with ``quats_wxyz``). With ``fold`` (shared means,
+    scales and quats) v_mean, v_scale and v_quat have n rows, summed over the B images."""
     means, scales, quats, viewmat, conics = map(_f32, (means, scales, quats, viewmat,
                                                        conics))
     v_xy, v_conic, transforms = map(_f32, (v_xy, v_conic, transforms))
     v_depth = None if v_depth is None else _f32(v_depth)
     radii, transform_ids = _i32(radii), _i32(transform_ids)
     dev = _lib.require_gpu(means, scales, quats, viewmat, conics, v_xy, v_conic)
-    total = B * n
+    total = n if fold else B * n
     v_mean = torch.empty((total, 3), device=dev, dtype=torch.float32)
     v_scale = torch.empty((total, 3), device=dev, dtype=torch.float32)
     v_quat = torch.empty((total, 4), device=dev, dtype=torch.float32)
@@ -91,7 +92,7 @@ def project_bwd(means, scales, quats, viewmat, radii, conics, v_xy, v_depth, v_c
             0 if v_depth is None else v_depth.numel(), p(v_conic), rows(v_conic, 3),
             p(transforms), rows(transforms, 16), p(transform_ids), n, num_transforms,
             int(has_transforms), B, f[0], f[1], glob_scale, p(v_mean), p(v_scale), p(v_quat),
-            p(v_view), p(v_tf), int(quats_wxyz))
+            p(v_view), p(v_tf), int(quats_wxyz), int(fold))
     _lib.check(st, "project_bwd")
     return v_mean, v_scale, v_quat, v_view, v_tf
 

@@ -71,12 +71,15 @@ class _ProjectFn(torch.autograd.Function):
             else v_xys
         v_conics = z(radii, dtype=torch.float32).unsqueeze(-1).expand(-1, 3) if v_conics is None \
             else v_conics
+        # shared gaussian parameters: the library sums their per-image rows itself
+        fold_here = B > 1 and all(t.numel() == n * w for t, w in ((means, 3), (scales, 3),
+                                                                   (quats, 4)))
         v_mean, v_scale, v_quat, v_view, v_tf = _ops.project_bwd(
             _flat(means, 3), _flat(scales, 3), _flat(quats, 4), viewmat.reshape(-1, 4), radii,
             conics, v_xys.reshape(-1, 2), None if v_depths is None else v_depths.reshape(-1),
             v_conics.reshape(-1, 3),
             transforms.reshape(-1, 4, 4), tf_ids.reshape(-1), n=n, B=B, num_transforms=K,
-            has_transforms=has_tf, f=f, glob_scale=glob_scale, quats_wxyz=True)
+            has_transforms=has_tf, f=f, glob_scale=glob_scale, quats_wxyz=True, fold=fold_here)
 
         def fold(g: torch.Tensor, like: torch.Tensor, width: int) -> torch.Tensor:
             if g.numel() == like.numel():  # one image, or a batched operand

@@ -329,7 +329,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 8; }
+int splat_abi_version(void) { return 9; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();
@@ -446,7 +446,7 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
                       int32_t num_transforms, int32_t has_transforms, int32_t B, float fx,
                       float fy, float glob_scale, float* v_mean3d, float* v_scale,
                       float* v_quat, float* v_viewmat, float* v_transforms,
-                      int32_t quats_wxyz) {
+                      int32_t quats_wxyz, int32_t fold_shared) {
     if (num_gaussians <= 0 || B <= 0) return fail(kErrArgs, "project_bwd: invalid sizes");
     if (!rows_match(rows_means, num_gaussians, B) || !rows_match(rows_scales, num_gaussians, B) ||
         !rows_match(rows_quats, num_gaussians, B) || !rows_match(rows_viewmat, 4, B) ||
@@ -460,6 +460,9 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
         return fail(kErrArgs, "project_bwd: transforms requested but not given");
     if ((int64_t)B * num_gaussians >= ((int64_t)1 << 31))
         return fail(kErrArgs, "project_bwd: more than 2^31 items");
+    if (fold_shared && (rows_means != num_gaussians || rows_scales != num_gaussians ||
+                        rows_quats != num_gaussians))
+        return fail(kErrArgs, "project_bwd: folding needs shared means, scales and quats");
     hipStream_t s = static_cast<hipStream_t>(stream);
     ProjectBwdArgs a;
     a.means = means3d; a.rows_means = rows_means;
@@ -479,6 +482,7 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
     a.v_mean3d = v_mean3d; a.v_scale = v_scale; a.v_quat = v_quat;
     a.v_viewmat = v_viewmat; a.v_transforms = has_transforms ? v_transforms : nullptr;
     a.quats_wxyz = quats_wxyz != 0;
+    a.fold = fold_shared != 0;
     StageTimer tm(s, kStageProjectBwd);
     int rc = launch_project_bwd(a, s);
     if (rc && g_last_error.empty()) set_error("project_bwd launch failed");

@@ -258,16 +258,24 @@ struct ProjectBwdParams {
     float fx, fy, glob_scale;
     float* v_mean3d; float* v_scale; float* v_quat; float* v_viewmat; float* v_transforms;
     int32_t wxyz;  // quats and v_quat stored wxyz (1) or xyzw (0)
+    int32_t fold;  // gaussian gradients summed over the images into n rows
 };
 
+// One workgroup per (image, block of gaussians); with P.fold one workgroup per block of
+// gaussians walks every image in order and sums the gaussian gradients in registers, so the
+// shared parameters are read once per gaussian and the per-image rows are never written.
 __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdParams P) {
     __shared__ float s_red[kProjThreads / 64][12];
     __shared__ int32_t s_tf[2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int32_t n = P.n;
-    const int32_t image_id = blockIdx.x / P.blocks_per_image;
-    const int32_t local_block = blockIdx.x - image_id * P.blocks_per_image;
+    const int32_t first_image = P.fold ? 0 : blockIdx.x / P.blocks_per_image;
+    const int32_t local_block =
+        P.fold ? (int32_t)blockIdx.x : (int32_t)blockIdx.x - first_image * P.blocks_per_image;
+    const int32_t end_image = P.fold ? P.B : first_image + 1;
     const int32_t gid = local_block * kProjThreads + tid;
+    float fm[3] = {0.f, 0.f, 0.f}, fs[3] = {0.f, 0.f, 0.f}, fq[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int32_t image_id = first_image; image_id < end_image; ++image_id) {
     const int64_t idx = (int64_t)image_id * n + gid;
     float vR[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
     float vt[3] = {0, 0, 0};
@@ -424,14 +432,25 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
 #pragma unroll
             for (int k = 0; k < 4; ++k) vq[k] = 0.0f;
         }
-        P.v_mean3d[3 * idx] = vmean_out[0];
-        P.v_mean3d[3 * idx + 1] = vmean_out[1];
-        P.v_mean3d[3 * idx + 2] = vmean_out[2];
-        P.v_scale[3 * idx] = vscale[0];
-        P.v_scale[3 * idx + 1] = vscale[1];
-        P.v_scale[3 * idx + 2] = vscale[2];
-        reinterpret_cast<float4*>(P.v_quat)[idx] =
-            P.wxyz ? make_float4(vq[3], vq[0], vq[1], vq[2]) : make_float4(vq[0], vq[1], vq[2], vq[3]);
+        if (P.fold) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                fm[k] = fm[k] + vmean_out[k];
+                fs[k] = fs[k] + vscale[k];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) fq[k] = fq[k] + vq[k];
+        } else {
+            P.v_mean3d[3 * idx] = vmean_out[0];
+            P.v_mean3d[3 * idx + 1] = vmean_out[1];
+            P.v_mean3d[3 * idx + 2] = vmean_out[2];
+            P.v_scale[3 * idx] = vscale[0];
+            P.v_scale[3 * idx + 1] = vscale[1];
+            P.v_scale[3 * idx + 2] = vscale[2];
+            reinterpret_cast<float4*>(P.v_quat)[idx] =
+                P.wxyz ? make_float4(vq[3], vq[0], vq[1], vq[2])
+                       : make_float4(vq[0], vq[1], vq[2], vq[3]);
+        }
     }
     // viewmat gradient: wave DPP reduction, then across the 4 waves in LDS, one atomic per entry
     float red[12];
@@ -488,6 +507,19 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
                 atomicAdd(dst + 4 * a + 3, vttf[a]);
             }
         }
+    }
+    __syncthreads();  // s_red / s_tf are reused by the next image
+    }
+    if (P.fold && gid < n) {
+        P.v_mean3d[3 * gid] = fm[0];
+        P.v_mean3d[3 * gid + 1] = fm[1];
+        P.v_mean3d[3 * gid + 2] = fm[2];
+        P.v_scale[3 * gid] = fs[0];
+        P.v_scale[3 * gid + 1] = fs[1];
+        P.v_scale[3 * gid + 2] = fs[2];
+        reinterpret_cast<float4*>(P.v_quat)[gid] =
+            P.wxyz ? make_float4(fq[3], fq[0], fq[1], fq[2])
+                   : make_float4(fq[0], fq[1], fq[2], fq[3]);
     }
 }
 
@@ -551,7 +583,8 @@ int launch_project_bwd(const ProjectBwdArgs& a, hipStream_t stream) {
     P.v_mean3d = a.v_mean3d; P.v_scale = a.v_scale; P.v_quat = a.v_quat;
     P.v_viewmat = a.v_viewmat; P.v_transforms = a.v_transforms;
     P.wxyz = a.quats_wxyz;
-    int64_t blocks = (int64_t)a.B * blocks_per_image;
+    P.fold = a.fold;
+    int64_t blocks = (a.fold ? 1 : (int64_t)a.B) * blocks_per_image;
     hipLaunchKernelGGL(project_bwd_kernel, dim3((unsigned)blocks), dim3(kProjThreads), 0, stream,
                        P);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;

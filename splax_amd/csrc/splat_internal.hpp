@@ -59,6 +59,7 @@ struct ProjectBwdArgs {
     float fx, fy, glob_scale;
     float* v_mean3d; float* v_scale; float* v_quat; float* v_viewmat; float* v_transforms;
     int32_t quats_wxyz = 0;  // quats (and v_quat) stored wxyz instead of xyzw
+    int32_t fold = 0;        // v_mean3d / v_scale / v_quat summed over the images (n rows)
 };
 
 // Geometry of one sort_and_bin call (splax/_rasterize/_sort/_sort.py:51-60).
