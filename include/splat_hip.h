@@ -158,7 +158,9 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
  * additions can differ in order only among a tile's four quadrant waves). v_depths (may be NULL)
  * selects the depth channel as in splat_rasterize_depth_bwd (then depths and v_out_depth are
  * read). compensate as in the forward: v_opacity is then the raw opacities' cotangent and
- * v_conic includes the cotangent through rho. */
+ * v_conic includes the cotangent through rho. fold_shared != 0 (colors and opacities shared,
+ * num_gaussians rows) writes v_colors [n,3] and v_opacity [n] summed over the B_out images in
+ * image order; v_xy, v_conic and v_depths keep their per-item rows. */
 int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64_t rows_colors,
                                const float* opacities, int64_t rows_opac,
                                const float* background, int64_t rows_bg, const float* xys,
@@ -172,7 +174,7 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
                                int32_t num_gaussians, int32_t B_out, int32_t B_geom,
                                int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
                                float* v_xy, float* v_conic, float* v_depths,
-                               int32_t compensate);
+                               int32_t compensate, int32_t fold_shared);
 
 /* Replaces sort_and_bin (splax/_rasterize/_sort/_sort.py:29-171), exposed for callers that keep
  * the sorted lists: writes the M sorted keys (as int64: the packed 32-bit key widened, or the

@@ -194,7 +194,7 @@ def _bwd_outputs(nout, dev, with_depth):
 
 def rasterize_bwd_sorted(colors, opac, background, xys, depths, conics, cum, kept: KeptSort,
                          final_Ts, final_idx, v_out, *, n, B_out, B_geom, img_shape,
-                         v_out_depth=None, compensate=False):
+                         v_out_depth=None, compensate=False, fold=False):
     """Backward over the sorted lists (and records) of rasterize_fwd_keep for the same inputs
     (no re-sort); with v_out_depth also the depth channel's v_depths (last)."""
     colors, opac, background, xys, depths, conics, final_Ts, v_out = map(
@@ -209,6 +209,8 @@ def rasterize_bwd_sorted(colors, opac, background, xys, depths, conics, cum, kep
                            v_out)
     H, W = img_shape
     v_colors, v_opac, v_xy, v_conic, v_depths = _bwd_outputs(B_out * n, dev, vd is not None)
+    if fold:  # shared colours and opacities: the library sums their per-image rows
+        v_colors, v_opac = v_colors[:n], v_opac[:n]
     p = _lib.ptr
     with torch.cuda.device(dev):
         st = _lib.lib().splat_rasterize_bwd_sorted(
@@ -217,7 +219,7 @@ def rasterize_bwd_sorted(colors, opac, background, xys, depths, conics, cum, kep
             p(pos), p(bins), p(recs), M, p(final_Ts), p(final_idx), p(v_out),
             v_out.numel() // (3 * W),
             p(vd), 0 if vd is None else vd.numel() // W, n, B_out, B_geom, H, W, p(v_colors),
-            p(v_opac), p(v_xy), p(v_conic), p(v_depths), int(compensate))
+            p(v_opac), p(v_xy), p(v_conic), p(v_depths), int(compensate), int(fold))
     _lib.check(st, "rasterize_bwd")
     if vd is None:
         return v_colors, v_opac, v_xy, v_conic

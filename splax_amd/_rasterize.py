@@ -76,13 +76,15 @@ class _RasterizeFn(torch.autograd.Function):
             v_img = torch.zeros((B * H, W, 3), device=xys.device)
         if render_depth and v_depth is None:
             v_depth = torch.zeros((B * H, W), device=xys.device)
+        fold_here = B > 1 and colors.numel() == n * 3 and opac.numel() == n
         grads = _ops.rasterize_bwd_sorted(
             colors.reshape(-1, 3), opac.reshape(-1), background.reshape(-1, 3),
             xys.reshape(-1, 2), depths.reshape(-1), conics.reshape(-1, 3), cum.reshape(-1),
             _ops.KeptSort(ids, pos, bins, ctx.num_intersects, recs), Ts, fidx,
             v_img.reshape(-1, 3), n=n, B_out=B,
             B_geom=B, img_shape=img_shape,
-            v_out_depth=v_depth.reshape(-1, W) if render_depth else None, compensate=compensate)
+            v_out_depth=v_depth.reshape(-1, W) if render_depth else None, compensate=compensate,
+            fold=fold_here)
         v_colors, v_opac, v_xy, v_conic = grads[:4]
 
         def fold(g: torch.Tensor, like: torch.Tensor) -> torch.Tensor:

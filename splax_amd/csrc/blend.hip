@@ -580,6 +580,7 @@ struct GatherParams {
     float* v_colors; float* v_opacity; float* v_xy; float* v_conic;
     float* v_depths;  // NG == 10
     const float* opac; int64_t rows_opac; int32_t compensate;
+    int32_t fold;  // v_colors / v_opacity summed over the images into n rows
 };
 
 // Cotangents of blend_opac = opac * rho(conic) (splax/_render.py:105-109 with
@@ -607,10 +608,16 @@ __device__ __forceinline__ float compensation_vjp(float vbo, float o, float a, f
     return v_o;
 }
 
+// With P.fold one thread per gaussian walks the images in order: per-item v_xy / v_conic /
+// v_depths rows as always, the colour and opacity cotangents summed into the gaussian's row.
 template <int NG>
 __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
-    const int64_t og = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (og >= P.nout) return;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (P.fold ? (int64_t)P.n : P.nout)) return;
+    const int32_t images = P.fold ? (int32_t)(P.nout / P.n) : 1;
+    float fc0 = 0.f, fc1 = 0.f, fc2 = 0.f, fo = 0.f;
+    for (int32_t image = 0; image < images; ++image) {
+    const int64_t og = P.fold ? (int64_t)image * P.n + t : t;
     int64_t gi = og, off = 0;
     if (!P.sel_geom) {
         const int64_t b = og / P.n;
@@ -628,9 +635,6 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
 #pragma unroll
         for (int k = 0; k < NG; ++k) s[k] += r[k];
     }
-    P.v_colors[3 * og] = s[0];
-    P.v_colors[3 * og + 1] = s[1];
-    P.v_colors[3 * og + 2] = s[2];
     float vc[3] = {s[3], s[4], s[5]};
     float vo = s[8];
     float vx = 0.f, vy = 0.f;
@@ -645,8 +649,25 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
     P.v_conic[3 * og + 2] = vc[2];
     P.v_xy[2 * og] = vx;
     P.v_xy[2 * og + 1] = vy;
-    P.v_opacity[og] = vo;
     if constexpr (NG == 10) P.v_depths[og] = s[9];
+    if (P.fold) {
+        fc0 = fc0 + s[0];
+        fc1 = fc1 + s[1];
+        fc2 = fc2 + s[2];
+        fo = fo + vo;
+    } else {
+        P.v_colors[3 * og] = s[0];
+        P.v_colors[3 * og + 1] = s[1];
+        P.v_colors[3 * og + 2] = s[2];
+        P.v_opacity[og] = vo;
+    }
+    }
+    if (P.fold) {
+        P.v_colors[3 * t] = fc0;
+        P.v_colors[3 * t + 1] = fc1;
+        P.v_colors[3 * t + 2] = fc2;
+        P.v_opacity[t] = fo;
+    }
 }
 
 int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
@@ -681,7 +702,9 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
     G.v_colors = a.v_colors; G.v_opacity = a.v_opacity; G.v_xy = a.v_xy; G.v_conic = a.v_conic;
     G.v_depths = a.v_depths;
     G.opac = in.opac; G.rows_opac = in.rows_opac; G.compensate = in.compensate;
-    const dim3 grid((unsigned)((nout + 255) / 256));
+    G.fold = a.fold;
+    const int64_t threads = a.fold ? (int64_t)in.n : nout;
+    const dim3 grid((unsigned)((threads + 255) / 256));
     if (depth)
         hipLaunchKernelGGL(grad_gather_kernel<10>, grid, dim3(256), 0, stream, G);
     else

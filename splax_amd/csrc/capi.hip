@@ -329,7 +329,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 9; }
+int splat_abi_version(void) { return 10; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();
@@ -774,7 +774,7 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
                                int32_t num_gaussians, int32_t B_out, int32_t B_geom,
                                int32_t img_h, int32_t img_w, float* v_colors, float* v_opacity,
                                float* v_xy, float* v_conic, float* v_depths,
-                               int32_t compensate) {
+                               int32_t compensate, int32_t fold_shared) {
     if (num_intersects < 0 || !tile_bins ||
         (num_intersects > 0 && (!sorted_ids || !sorted_pos)))
         return fail(kErrArgs, "rasterize_bwd_sorted: invalid sorted lists");
@@ -782,8 +782,11 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
                                     rows_opac, background, rows_bg, xys, depths, nullptr, conics,
                                     cum_tiles_hit, num_gaussians, B_geom, img_h, img_w);
     in.compensate = compensate != 0;
-    const BlendBwdArgs a = bwd_args(final_Ts, final_idx, v_out_img, vout_rows, B_out, v_colors,
-                                    v_opacity, v_xy, v_conic, v_out_depth, vdepth_rows, v_depths);
+    if (fold_shared && (rows_colors != num_gaussians || rows_opac != num_gaussians))
+        return fail(kErrArgs, "rasterize_bwd_sorted: folding needs shared colors and opacities");
+    BlendBwdArgs a = bwd_args(final_Ts, final_idx, v_out_img, vout_rows, B_out, v_colors,
+                              v_opacity, v_xy, v_conic, v_out_depth, vdepth_rows, v_depths);
+    a.fold = fold_shared != 0;
     const KeptLists kept{sorted_ids, sorted_pos, tile_bins, num_intersects, records};
     return rasterize_bwd_impl(static_cast<hipStream_t>(stream), in, &kept, a);
 }

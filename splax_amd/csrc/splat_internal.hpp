@@ -220,6 +220,7 @@ struct BlendBwdArgs {
     float* v_colors; float* v_opacity; float* v_xy; float* v_conic;
     const float* v_out_depth = nullptr; int64_t vdepth_rows = 0; float* v_depths = nullptr;
     const float4* recs = nullptr;  // launch_pack_records output for the same inputs
+    int32_t fold = 0;  // v_colors / v_opacity summed over the B_out images (n rows)
 };
 int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, const BlendBwdArgs& a, hipStream_t stream);

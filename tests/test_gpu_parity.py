@@ -241,6 +241,42 @@ def test_project_bwd_fold_equals_summed_rows():
     _grad_compare(_np(folded[3]), _np(rows[3]), "fold/v_viewmat")
 
 
+@pytest.mark.parametrize("compensate", [False, True])
+def test_gather_fold_equals_summed_rows(compensate):
+    """Shared colours and opacities over B cameras: the folded backward's v_colors / v_opacity
+    equal the per-image rows summed in image order, and per-item rows are unchanged, to the
+    float-sum tolerance (two backward calls differ in the order a tile's quadrant waves add into
+    a record's LDS sums)."""
+    _case(f"gather fold B=4 compensate={compensate}")
+    s = make_scene(4, n=30_000)
+    B, n = s.B, s.n
+    q = np.roll(s.quats, -1, axis=-1)
+    xys, depths, radii, conics, nth, cum = O.project_fwd(
+        s.means, s.scales, q, s.viewmats.reshape(-1, 4), s.opacities, n=n, total=B * n,
+        img_shape=s.img_shape, f=s.f, c=s.c)
+    o = _t(s.opacities).reshape(-1)
+    geo = (_t(xys), _t(depths), _t(radii), _t(conics), _t(cum))
+    H, W = s.img_shape
+    img, Ts, fidx, kept, _ = _ops.rasterize_fwd_keep(
+        _t(s.colors), o, o, _t(s.background), *geo, n=n, B=B, img_shape=s.img_shape,
+        compensate=compensate)
+    vout = (img.reshape(-1, 3) - _t(s.targets).reshape(-1, 3)).contiguous() * (2.0 / img.numel())
+    kw = dict(n=n, B_out=B, B_geom=B, img_shape=s.img_shape, compensate=compensate)
+    args = (_t(s.colors), o, _t(s.background), geo[0], geo[1], geo[3], geo[4], kept, Ts, fidx,
+            vout)
+    rows = _ops.rasterize_bwd_sorted(*args, **kw)
+    folded = _ops.rasterize_bwd_sorted(*args, **kw, fold=True)
+    torch.cuda.synchronize()
+    for label, r, fd in zip(("v_colors", "v_opacity"), rows[:2], folded[:2]):
+        per = _np(r).reshape(B, n, -1)
+        want = np.zeros_like(per[0])
+        for b in range(B):
+            want = (want + per[b]).astype(np.float32)
+        _grad_compare(_np(fd).reshape(want.shape), want, f"fold/{label}")
+    for label, r, fd in zip(("v_xy", "v_conic"), rows[2:4], folded[2:4]):
+        _grad_compare(_np(fd), _np(r), f"fold/{label} per item")
+
+
 def test_batched_cameras_one_launch():
     """Config-3-style orbit, B=16 cameras folded into the key (smaller N)."""
     _case("batched B=16")
