@@ -406,12 +406,14 @@ __device__ __forceinline__ float swap16_add(float a, float b) {
                                               false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
-// Lanes 7 and 15 of each 16-lane row end with the sums of the row's lower and upper halves;
-// both add into LDS (a two-lane collision there costs less than one more DPP step).
-__device__ __forceinline__ float row_halves_to_lanes_7_15(float v) {
+// Lane 15 of each 16-lane row ends with the row's sum. The fourth step costs one VALU per
+// value but leaves one adding lane per row: two lanes of a row adding into one LDS word
+// serialize, and that cost more than the step.
+__device__ __forceinline__ float row_sum_to_lane_15(float v) {
     v = dpp_add<0x111, 0xf>(v);  // row_shr:1
     v = dpp_add<0x112, 0xf>(v);  // row_shr:2
     v = dpp_add<0x114, 0xf>(v);  // row_shr:4
+    v = dpp_add<0x118, 0xf>(v);  // row_shr:8
     return v;
 }
 
@@ -533,20 +535,20 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             const float g9 = kDepth ? vd * fac : 0.0f;
             float* a = &ACC(t, 0);
             // reduce-scatter over the wave: after the swaps, row r of qa holds g0/g2/g1/g3 and
-            // of qb g4/g6/g5/g7 (rows 0..3), qc holds g8 in every row; the half-row sums land
-            // in lanes 7 and 15.
+            // of qb g4/g6/g5/g7 (rows 0..3), qc holds g8 in every row; each row's sum lands in
+            // its lane 15.
             const float p01 = swap32_add(g0, g1), p23 = swap32_add(g2, g3);
             const float p45 = swap32_add(g4, g5), p67 = swap32_add(g6, g7);
             // depth: g8 and g9 share the first swap (rows 0-1 then carry g8, rows 2-3 g9)
             const float p8 = kDepth ? swap32_add(g8, g9) : swap32_add(g8, g8);
             float qa = swap16_add(p01, p23), qb = swap16_add(p45, p67), qc = swap16_add(p8, p8);
-            qa = row_halves_to_lanes_7_15(qa);
-            qb = row_halves_to_lanes_7_15(qb);
-            qc = row_halves_to_lanes_7_15(qc);
+            qa = row_sum_to_lane_15(qa);
+            qb = row_sum_to_lane_15(qb);
+            qc = row_sum_to_lane_15(qc);
             // Empty uses keep the last DPP adds in this block: sunk into the branch below they
             // would no longer fuse with their DPP moves (two extra VALU each).
             asm volatile("" ::"v"(qa), "v"(qb), "v"(qc));
-            if ((lane & 7) == 7) {
+            if ((lane & 15) == 15) {
                 const int ka = (row == 0) ? 0 : (row == 1) ? 2 : (row == 2) ? 1 : 3;
                 atomicAdd(a + ka, qa);
                 atomicAdd(a + 4 + ka, qb);
