@@ -118,6 +118,15 @@ float oracle_expf(float x) {
     return ldexpf(p, (int)kf);
 }
 
+/* The blends' Gaussian exponent 0.5 (a dx^2 + c dy^2) + b dx dy (splax/_rasterize/_kernels.py:187,
+ * 1039), evaluated as (a/2 dx dx + c/2 dy dy) + b dx dy with the halving applied to a and c
+ * first. Scaling by 1/2 is exact, so this is the reference's expression bit for bit unless an
+ * intermediate falls below the normal range. */
+static inline float blend_sigma(const float* cn, float dx, float dy) {
+    const float ha = 0.5f * cn[0], hc = 0.5f * cn[2];
+    return (ha * dx * dx + hc * dy * dy) + cn[1] * dx * dy;
+}
+
 /* ---------------------------------------------------------------- 3x3 helpers (row major) */
 
 static inline void mat_mul(const float* a, const float* b, float* c) {
@@ -799,8 +808,7 @@ void oracle_blend_fwd(const float* colors, int64_t rows_colors, const float* opa
                 for (int32_t k = start; k < end; ++k) {
                     int64_t g = sorted_ids[k];
                     float dx = xys[2 * g] - px, dy = xys[2 * g + 1] - py;
-                    const float* cn = conics + 3 * g;
-                    float sigma = 0.5f * (cn[0] * dx * dx + cn[2] * dy * dy) + cn[1] * dx * dy;
+                    float sigma = blend_sigma(conics + 3 * g, dx, dy);
                     float op = opacities[g % rows_opac];
                     float alpha = fminw(ALPHA_MAX, op * oracle_expf(-sigma));
                     if (sigma < 0.0f || alpha < ALPHA_THRESHOLD) {
@@ -927,7 +935,7 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
                         float dx = xys[2 * g] - px, dy = xys[2 * g + 1] - py;
                         const float* cn = conics + 3 * g;
                         float a = cn[0], b = cn[1], c = cn[2];
-                        float sigma = 0.5f * (a * dx * dx + c * dy * dy) + b * dx * dy;
+                        float sigma = blend_sigma(cn, dx, dy);
                         if (sigma < 0.0f) {
                             ++qr;
                             continue;

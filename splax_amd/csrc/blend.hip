@@ -37,6 +37,7 @@ struct BlendCommon {
     const float* background; int64_t rows_bg;
     const float4* recs;  // packed records, four float4 per geometry item (pack_records_kernel)
     const int32_t* ids; const int32_t* bins;
+    const int32_t* order;  // workgroup -> (image, tile), tile_order_kernel
     int32_t img_h, img_w, tiles_x, num_tiles;
     int64_t total;  // geometry rows (B_geom * n): ids outside [0, total) are ignored
 };
@@ -56,7 +57,7 @@ __device__ __forceinline__ int row_subblock(int tid) {
 }
 
 // Packed record of one geometry item, 64 bytes (one aligned segment per staged intersection):
-//   r0 = (x, y, a, b), r1 = (c, o, sigma_max, 0), r2 = (red, green, blue, depth),
+//   r0 = (x, y, a/2, b), r1 = (c/2, o, sigma_max, 0), r2 = (red, green, blue, depth),
 //   r3 = (ex, ey, cull mode, 0).
 // They depend only on the rasterizer's inputs, so a forward's records serve its backward.
 // sigma_max = log(255 o) + 1e-3 bounds sigma where o e^-sigma can still reach 1/255. The cull mode
@@ -116,8 +117,10 @@ __global__ void __launch_bounds__(256) pack_records_kernel(PackParams P) {
             }
         }
         float4* r = s_rec + 4 * threadIdx.x;
-        r[0] = make_float4(xy.x, xy.y, a, b);
-        r[1] = make_float4(c, o, smax, 0.0f);
+        // the blends evaluate sigma = (a/2 dx dx + c/2 dy dy) + b dx dy: halving exactly before
+        // the products leaves every rounding where 0.5 (a dx dx + c dy dy) puts it
+        r[0] = make_float4(xy.x, xy.y, 0.5f * a, b);
+        r[1] = make_float4(0.5f * c, o, smax, 0.0f);
         r[2] = make_float4(P.colors[3 * cg], P.colors[3 * cg + 1], P.colors[3 * cg + 2],
                            P.depths ? P.depths[g] : 0.0f);
         r[3] = make_float4(ex, ey, __uint_as_float(mode), 0.0f);
@@ -261,7 +264,7 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
     __shared__ BatchLds L;
     const BlendCommon& C = P.c;
     const int tid = threadIdx.x;
-    const int32_t tile_g = blockIdx.x;
+    const int32_t tile_g = C.order[blockIdx.x];
     const int32_t image_id = tile_g / C.num_tiles;
     const int32_t tile_local = tile_g - image_id * C.num_tiles;
     const int tile_x = tile_local % C.tiles_x, tile_y = tile_local / C.tiles_x;
@@ -294,7 +297,7 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
             const int t = list[has ? k : 0];
             const float4 r0 = L.r0[t], r1 = L.r1[t];
             const float dx = r0.x - px, dy = r0.y - py;
-            const float sigma = 0.5f * (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
+            const float sigma = (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
             // bitwise: no short-circuit branch around the sigma_max read (NaN sigma fails both)
             if (!(has & (!done) & (sigma >= 0.0f) & (sigma <= r1.z))) continue;
             const float alpha = minw(kAlphaMax, r1.y * exp_core(-sigma));
@@ -346,21 +349,88 @@ static void fill_common(BlendCommon& c, const RasterInputs& in, const KeyLayout&
                         const int32_t* sorted_ids, const int32_t* tile_bins) {
     c.background = in.background; c.rows_bg = in.rows_bg;
     c.recs = nullptr;
-    c.ids = sorted_ids; c.bins = tile_bins;
+    c.ids = sorted_ids; c.bins = tile_bins; c.order = nullptr;
     c.img_h = in.img_h; c.img_w = in.img_w;
     c.tiles_x = lay.tiles_x; c.num_tiles = lay.num_tiles;
     c.total = (int64_t)in.B_geom * in.n;
 }
 
+// ------------------------------------------------------------------ tile dispatch order
+// Workgroup b of a blend takes tile order[b]: tiles by descending intersection count, in buckets
+// of eight per octave, so the longest tiles start first and the grid ends with short ones instead
+// of a straggler. Any permutation gives the same outputs (each workgroup owns its tile's pixels
+// and its intersections' gradient slots); positions inside a bucket come from LDS atomics.
+
+constexpr int kOrderThreads = 1024;
+
+// 0 for an empty tile, else monotone in the count: c below 8 as is, then 8 steps per octave
+// (at most 247 for an int32 count).
+__device__ __forceinline__ int order_bucket(int32_t c) {
+    if (c <= 0) return 0;
+    const int e = 31 - __clz(c);
+    return e < 3 ? c : e * 8 + ((c >> (e - 3)) & 7);
+}
+
+// Intersection count of workgroup b's tile: (image, tile) = divmod(b, num_tiles), bins of the
+// image's geometry (image 0 when the geometry is shared).
+__device__ __forceinline__ int32_t order_cost(const int32_t* bins, int64_t b, int32_t num_tiles,
+                                              int32_t per_image) {
+    const int64_t image = b / num_tiles;
+    const int64_t g = (per_image ? image : 0) * num_tiles + (b - image * num_tiles);
+    return bins[2 * g + 1] - bins[2 * g];
+}
+
+// One workgroup: bucket histogram, exclusive scan from the largest bucket down, scatter.
+__global__ void __launch_bounds__(kOrderThreads)
+tile_order_kernel(const int32_t* bins, int64_t blocks, int32_t num_tiles, int32_t per_image,
+                  int32_t* order) {
+    __shared__ uint32_t s_cnt[256], s_scan[2][256];
+    const int tid = threadIdx.x;
+    if (tid < 256) s_cnt[tid] = 0;
+    __syncthreads();
+    for (int64_t b = tid; b < blocks; b += kOrderThreads)
+        atomicAdd(&s_cnt[255 - order_bucket(order_cost(bins, b, num_tiles, per_image))], 1u);
+    __syncthreads();
+    // inclusive Hillis-Steele scan over the 256 buckets (largest counts first)
+    int cur = 0;
+    if (tid < 256) s_scan[0][tid] = s_cnt[tid];
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+        if (tid < 256) {
+            const uint32_t v = s_scan[cur][tid];
+            s_scan[cur ^ 1][tid] = tid >= off ? v + s_scan[cur][tid - off] : v;
+        }
+        cur ^= 1;
+        __syncthreads();
+    }
+    if (tid < 256) s_cnt[tid] = s_scan[cur][tid] - s_cnt[tid];  // exclusive
+    __syncthreads();
+    for (int64_t b = tid; b < blocks; b += kOrderThreads) {
+        const uint32_t at =
+            atomicAdd(&s_cnt[255 - order_bucket(order_cost(bins, b, num_tiles, per_image))], 1u);
+        order[at] = (int32_t)b;
+    }
+}
+
+static int launch_tile_order(const int32_t* bins, int64_t blocks, int32_t num_tiles,
+                             int32_t per_image, int32_t* order, hipStream_t stream) {
+    hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, stream, bins, blocks,
+                       num_tiles, per_image, order);
+    return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
+}
+
 int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,
-                     float* out_img, float* out_depth, const float4* recs,
+                     float* out_img, float* out_depth, const float4* recs, int32_t* order,
                      hipStream_t stream) {
     const int64_t blocks = (int64_t)in.B_geom * lay.num_tiles;
     if (blocks <= 0) return 0;
+    int rc = launch_tile_order(tile_bins, blocks, lay.num_tiles, 1, order, stream);
+    if (rc) return rc;
     BlendFwdParams P;
     fill_common(P.c, in, lay, sorted_ids, tile_bins);
     P.c.recs = recs;
+    P.c.order = order;
     P.final_Ts = final_Ts; P.final_idx = final_idx; P.out_img = out_img;
     P.out_depth = out_depth;
     if (out_depth)
@@ -406,20 +476,35 @@ __device__ __forceinline__ float swap16_add(float a, float b) {
                                               false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
-// Lane 15 of each 16-lane row ends with the row's sum. The fourth step costs one VALU per
-// value but leaves one adding lane per row: two lanes of a row adding into one LDS word
-// serialize, and that cost more than the step.
-__device__ __forceinline__ float row_sum_to_lane_15(float v) {
-    v = dpp_add<0x111, 0xf>(v);  // row_shr:1
-    v = dpp_add<0x112, 0xf>(v);  // row_shr:2
-    v = dpp_add<0x114, 0xf>(v);  // row_shr:4
-    v = dpp_add<0x118, 0xf>(v);  // row_shr:8
-    return v;
+// keep + the `send` value of the lane that DPP control kCtrl names (all lanes valid).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_pair_add(float keep, float send) {
+    const int r = __builtin_amdgcn_update_dpp(0, __float_as_int(send), kCtrl, 0xf, 0xf, false);
+    return keep + __int_as_float(r);
 }
 
-// Record accumulator slot k of batch record t ([t][NG] layout: the lanes that add at once hit
-// different banks).
-#define ACC(t, k) acc[(t) * NG + (k)]
+// Reduce-scatter of three values over each 16-lane row. Lane l pairs with 15 - l (row_mirror):
+// the lower half keeps a and sends b, the upper half the reverse, and c is summed on its own;
+// then lane j of each 8-lane half pairs with 7 - j (row_half_mirror), the lower quad keeping the
+// a/b partial and the upper one c; two quad butterflies finish. Lanes 0-3 of the row then hold
+// the row sum of a, lanes 8-11 that of b, lanes 4-7 and 12-15 that of c: nine VALU, where
+// four DPP steps per value take twelve and leave three values to add into LDS.
+__device__ __forceinline__ float row_reduce_scatter3(float a, float b, float c, bool hi8,
+                                                     bool hi4) {
+    const float r = dpp_pair_add<0x140>(hi8 ? b : a, hi8 ? a : b);  // row_mirror
+    c = dpp_pair_add<0x140>(c, c);
+    float s = dpp_pair_add<0x141>(hi4 ? c : r, hi4 ? r : c);  // row_half_mirror
+    s = dpp_pair_add<0xb1>(s, s);  // quad_perm [1, 0, 3, 2]
+    s = dpp_pair_add<0x4e>(s, s);  // quad_perm [2, 3, 0, 1]
+    return s;
+}
+
+// Record accumulator slot k of batch record t ([t][kAccSlots] layout: the lanes that add at once
+// hit different banks). Slots 0-7 hold g0..g7; slots 8-11 hold per-row partials of the last
+// sums, which the batch readout adds: g8 from each of the four rows, or with the depth channel
+// g8 from rows 0-1 and g9 from rows 2-3.
+constexpr int kAccSlots = 12;
+#define ACC(t, k) acc[(t) * kAccSlots + (k)]
 
 // kDepth adds the depth channel of _rasterize_bwd_depth_kernel / _blend_depth_vjp
 // (splax/_rasterize/_kernels.py:935-1080,1257-1302): the record's depth joins the colour dot
@@ -428,12 +513,12 @@ template <bool kDepth>
 __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     constexpr int NG = kDepth ? 10 : 9;
     __shared__ BatchLds L;
-    __shared__ float acc[kTile * NG];
+    __shared__ float acc[kTile * kAccSlots];
     __shared__ int32_t s_max;
 
     const BlendCommon& C = P.c;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int32_t tile_g = blockIdx.x;  // (output image, tile)
+    const int32_t tile_g = C.order[blockIdx.x];  // (output image, tile)
     const int32_t image_id = tile_g / C.num_tiles;
     const int32_t tile_local = tile_g - image_id * C.num_tiles;
     const int32_t geom_image = P.sel_geom ? image_id : 0;
@@ -462,7 +547,7 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     }
     float bufv = 0.f;  // sum_k buffer_k * v_k of the reference's colour accumulator
     if (tid == 0) s_max = range_start - 1;
-    for (int k = tid; k < kTile * NG; k += kTile) acc[k] = 0.0f;
+    for (int k = tid; k < kTile * kAccSlots; k += kTile) acc[k] = 0.0f;
     __syncthreads();
     atomicMax(&s_max, bin_final);
     // wave-wide largest final index: a record above it has no contributing lane in this wave
@@ -489,7 +574,13 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
         }
     }
 
-    const int row = lane >> 4;
+    const int row = lane >> 4, l16 = lane & 15;
+    // After the wave reduction below, lane 0 of row r holds the sum of g[ka], lane 8 that of
+    // g[4 + ka] and lane 4 the row's partial for slot 8 + r; they alone add into LDS.
+    const bool hi8 = (l16 & 8) != 0, hi4 = (l16 & 4) != 0;
+    const int ka = (row == 0) ? 0 : (row == 1) ? 2 : (row == 2) ? 1 : 3;
+    const bool adds = l16 == 0 || l16 == 4 || l16 == 8;
+    const int kslot = l16 == 0 ? ka : l16 == 8 ? 4 + ka : 8 + row;
     for (int32_t bt = 0; bt < num_batches; ++bt) {
         const int32_t batch_end = start_idx - bt * kTile;
         const int32_t src = imaxw(batch_end - tid, range_start);
@@ -503,7 +594,7 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             if (idx > wmax) continue;  // wave-uniform
             const float4 r0 = L.r0[t], r1 = L.r1[t];
             const float dx = r0.x - px, dy = r0.y - py;
-            const float sigma = 0.5f * (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
+            const float sigma = (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
             // bitwise: no short-circuit branch around the sigma_max read
             const bool in_range = (idx <= bin_final) & (sigma >= 0.0f) & (sigma <= r1.z);
             if (__builtin_amdgcn_ballot_w64(in_range) == 0ull) continue;
@@ -533,36 +624,38 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             const float g6 = hx, g7 = hy;
             const float g8 = geo ? vis * v_alpha : 0.0f;
             const float g9 = kDepth ? vd * fac : 0.0f;
-            float* a = &ACC(t, 0);
             // reduce-scatter over the wave: after the swaps, row r of qa holds g0/g2/g1/g3 and
-            // of qb g4/g6/g5/g7 (rows 0..3), qc holds g8 in every row; each row's sum lands in
-            // its lane 15.
+            // of qb g4/g6/g5/g7 (rows 0..3); qc is g8 unswapped (each row reduces its own lanes)
+            // or with depth the one swap of g8 with g9 (rows 0-1 then carry g8, rows 2-3 g9).
+            // The row reduce-scatter leaves each sum in one adding lane.
             const float p01 = swap32_add(g0, g1), p23 = swap32_add(g2, g3);
             const float p45 = swap32_add(g4, g5), p67 = swap32_add(g6, g7);
-            // depth: g8 and g9 share the first swap (rows 0-1 then carry g8, rows 2-3 g9)
-            const float p8 = kDepth ? swap32_add(g8, g9) : swap32_add(g8, g8);
-            float qa = swap16_add(p01, p23), qb = swap16_add(p45, p67), qc = swap16_add(p8, p8);
-            qa = row_sum_to_lane_15(qa);
-            qb = row_sum_to_lane_15(qb);
-            qc = row_sum_to_lane_15(qc);
-            // Empty uses keep the last DPP adds in this block: sunk into the branch below they
-            // would no longer fuse with their DPP moves (two extra VALU each).
-            asm volatile("" ::"v"(qa), "v"(qb), "v"(qc));
-            if ((lane & 15) == 15) {
-                const int ka = (row == 0) ? 0 : (row == 1) ? 2 : (row == 2) ? 1 : 3;
-                atomicAdd(a + ka, qa);
-                atomicAdd(a + 4 + ka, qb);
-                if (row == 0) atomicAdd(a + 8, qc);
-                if (kDepth && row == 2) atomicAdd(a + 9, qc);
-            }
+            const float qa = swap16_add(p01, p23), qb = swap16_add(p45, p67);
+            const float qc = kDepth ? swap32_add(g8, g9) : g8;
+            const float sum = row_reduce_scatter3(qa, qb, qc, hi8, hi4);
+            // An empty use keeps the last DPP add in this block: sunk into the branch below it
+            // would no longer fuse with its DPP move.
+            asm volatile("" ::"v"(sum));
+            if (adds) atomicAdd(&acc[t * kAccSlots + kslot], sum);
         }
         __syncthreads();
         {
-            float s[NG];
+            float s[NG], part[4];
 #pragma unroll
-            for (int k = 0; k < NG; ++k) {
+            for (int k = 0; k < 8; ++k) {
                 s[k] = ACC(tid, k);
                 ACC(tid, k) = 0.0f;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                part[r] = ACC(tid, 8 + r);
+                ACC(tid, 8 + r) = 0.0f;
+            }
+            if constexpr (kDepth) {
+                s[8] = part[0] + part[1];
+                s[9] = part[2] + part[3];
+            } else {
+                s[8] = (part[0] + part[1]) + (part[2] + part[3]);
             }
             if (my_pos >= 0 && my_pos < P.M) store_rgrad<NG>(P.rgrad, rg_off + my_pos, s);
         }
@@ -673,15 +766,19 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
 }
 
 int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
-                     const int32_t* tile_bins, const BlendBwdArgs& a, hipStream_t stream) {
+                     const int32_t* tile_bins, const BlendBwdArgs& a, int32_t* order,
+                     hipStream_t stream) {
     const int64_t nout = (int64_t)a.B_out * in.n;
     const int32_t sel_geom = in.B_geom > 1;
     const int64_t blocks = (int64_t)a.B_out * lay.num_tiles;
     const bool depth = a.v_depths != nullptr;
     if (blocks > 0 && sorted_ids != nullptr && a.M > 0) {
+        const int rc = launch_tile_order(tile_bins, blocks, lay.num_tiles, sel_geom, order, stream);
+        if (rc) return rc;
         BlendBwdParams P;
         fill_common(P.c, in, lay, sorted_ids, tile_bins);
         P.c.recs = a.recs;
+        P.c.order = order;
         P.final_Ts = a.final_Ts; P.final_idx = a.final_idx;
         P.v_out = a.v_out; P.vout_rows = a.vout_rows;
         P.n = in.n; P.sel_geom = sel_geom;

@@ -215,6 +215,17 @@ int DeviceScratch::ensure_recs(int64_t items) {
     return 0;
 }
 
+int DeviceScratch::ensure_order(int64_t blocks) {
+    if (blocks <= order_cap) return 0;
+    (void)hipDeviceSynchronize();
+    dev_free(&tile_order);
+    order_cap = 0;
+    int rc = dev_alloc(&tile_order, blocks, false);
+    if (rc) return rc;
+    order_cap = blocks;
+    return 0;
+}
+
 static int ensure_minmax_partials(DeviceScratch& sc, int64_t count) {
     if (count <= sc.mm_partial_cap) return 0;
     (void)hipDeviceSynchronize();
@@ -244,6 +255,8 @@ void DeviceScratch::release() {
     rgrad_cap = 0;
     dev_free(&recs);
     recs_cap = 0;
+    dev_free(&tile_order);
+    order_cap = 0;
     dev_free(&part_counts);
     part_counts_cap = 0;
     dev_free(&tile_bins);
@@ -611,11 +624,13 @@ static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortT
         if (rc) return rc;
         recs = sc.recs;
     }
+    rc = sc.ensure_order((int64_t)in.B_geom * L.num_tiles);
+    if (rc) return rc;
     StageTimer tm(s, kStageBlendFwd);
     if (M > 0) rc = launch_pack_records(in, recs, s);
     if (!rc)
         rc = launch_blend_fwd(in, L, M > 0 ? ids : nullptr, bins, final_Ts, final_idx, out_img,
-                              out_depth, recs, s);
+                              out_depth, recs, sc.tile_order, s);
     if (rc) return fail(rc, "blend_fwd launch failed");
     return 0;
 }
@@ -671,6 +686,7 @@ static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptL
     const float4* recs = kept ? reinterpret_cast<const float4*>(kept->records) : nullptr;
     rc = sc.ensure_rgrad(images * M * (args.v_depths ? 10 : 9));
     if (!rc && !recs && M > 0) rc = sc.ensure_recs((int64_t)in.B_geom * in.n);
+    if (!rc) rc = sc.ensure_order((int64_t)args.B_out * L.num_tiles);
     if (rc) return rc;
     BlendBwdArgs a = args;
     a.sorted_pos = pos;
@@ -683,7 +699,7 @@ static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptL
         recs = sc.recs;
     }
     a.recs = recs;
-    rc = launch_blend_bwd(in, L, M > 0 ? ids : nullptr, bins, a, s);
+    rc = launch_blend_bwd(in, L, M > 0 ? ids : nullptr, bins, a, sc.tile_order, s);
     if (rc) return fail(rc, "blend_bwd launch failed");
     return 0;
 }

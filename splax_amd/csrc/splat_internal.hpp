@@ -118,6 +118,8 @@ struct DeviceScratch {
     float* rgrad = nullptr; int64_t rgrad_cap = 0;
     // blends: packed per-item records (4 float4 each)
     float4* recs = nullptr; int64_t recs_cap = 0;
+    // blends: workgroup -> (image, tile) dispatch order
+    int32_t* tile_order = nullptr; int64_t order_cap = 0;
     uint32_t* part_counts = nullptr; int64_t part_counts_cap = 0;  // 256 * partitions
     uint32_t* hist = nullptr;                                       // 256 digit totals
     int32_t* tile_bins = nullptr; int64_t bins_cap = 0;             // (start, end) pairs
@@ -136,6 +138,7 @@ struct DeviceScratch {
     int ensure_sort(int64_t M, int64_t bins, int32_t B, bool wide);
     int ensure_rgrad(int64_t count);
     int ensure_recs(int64_t items);
+    int ensure_order(int64_t blocks);
     void release();
 };
 
@@ -206,7 +209,8 @@ int launch_pack_records(const RasterInputs& in, float4* recs, hipStream_t stream
 // the records written by launch_pack_records for the same inputs.
 int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,
-                     float* out_img, float* out_depth, const float4* recs, hipStream_t stream);
+                     float* out_img, float* out_depth, const float4* recs, int32_t* order,
+                     hipStream_t stream);
 
 // Backward over sorted lists of M intersections: sorted_ids / sorted_pos / tile_bins as produced
 // by sort_and_bin; in.cum gives each item's emission range; rgrad is scratch of
@@ -223,7 +227,8 @@ struct BlendBwdArgs {
     int32_t fold = 0;  // v_colors / v_opacity summed over the B_out images (n rows)
 };
 int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
-                     const int32_t* tile_bins, const BlendBwdArgs& a, hipStream_t stream);
+                     const int32_t* tile_bins, const BlendBwdArgs& a, int32_t* order,
+                     hipStream_t stream);
 
 // ------------------------------------------------------------------ device helpers
 

@@ -413,13 +413,15 @@ def test_kept_sort_path_equals_resort_path(name):
     for label, x, y, z in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), a, b, a2):
         _grad_compare(_np(x), _np(y), f"{name}/{label} kept vs re-sorted")
         _grad_compare(_np(x), _np(z), f"{name}/{label} repacked records")
-    # packed record layout: (x, y, a, b), (c, o, sigma_max, 0), (r, g, b, depth), (ex, ey, mode, 0)
+    # packed record layout: (x, y, a/2, b), (c/2, o, sigma_max, 0), (r, g, b, depth),
+    # (ex, ey, mode, 0); halving a float32 is exact, so a/2 and c/2 compare bit for bit
     r = _np(recs)
     flat = lambda x: np.ascontiguousarray(x).reshape(-1)  # noqa: E731
     cn = np.asarray(conics).reshape(-1, 3)
     assert_bit_exact(flat(r[:, 0:2]), flat(xys), f"{name}/record xy")
-    assert_bit_exact(flat(r[:, 2:4]), flat(cn[:, 0:2]), f"{name}/record a, b")
-    assert_bit_exact(r[:, 4], cn[:, 2], f"{name}/record c")
+    assert_bit_exact(r[:, 2], flat(cn[:, 0]) * np.float32(0.5), f"{name}/record a/2")
+    assert_bit_exact(r[:, 3], flat(cn[:, 1]), f"{name}/record b")
+    assert_bit_exact(r[:, 4], flat(cn[:, 2]) * np.float32(0.5), f"{name}/record c/2")
     assert_bit_exact(r[:, 5], flat(s.opacities), f"{name}/record opacity")
     assert_bit_exact(flat(r[:, 8:11]), flat(s.colors), f"{name}/record colour")
     assert_bit_exact(r[:, 11], flat(depths), f"{name}/record depth")
