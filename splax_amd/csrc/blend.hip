@@ -153,7 +153,7 @@ __device__ __forceinline__ uint32_t subblock_mask(const float4& r0, const float4
     return m;
 }
 
-// LDS record of one batch: r0 = (x, y, a, b), r1 = (c, o, sigma_max, 0), r2 = (red, green,
+// LDS record of one batch: r0 = (x, y, a/2, b), r1 = (c/2, o, sigma_max, 0), r2 = (red, green,
 // blue, depth), each record's sub-block mask, and per-sub-block compacted record lists.
 struct BatchLds {
     float4 r0[kTile];
@@ -356,10 +356,12 @@ static void fill_common(BlendCommon& c, const RasterInputs& in, const KeyLayout&
 }
 
 // ------------------------------------------------------------------ tile dispatch order
-// Workgroup b of a blend takes tile order[b]: tiles by descending intersection count, in buckets
-// of eight per octave, so the longest tiles start first and the grid ends with short ones instead
-// of a straggler. Any permutation gives the same outputs (each workgroup owns its tile's pixels
-// and its intersections' gradient slots); positions inside a bucket come from LDS atomics.
+// Workgroup b of a blend takes tile order[b]. The images stay in order, so one image's records
+// and lists are what the caches hold at a time; inside an image the tiles go by descending
+// intersection count, in buckets of eight per octave, so the longest tiles start first and each
+// image ends with short ones instead of a straggler. Any permutation gives the same outputs (each
+// workgroup owns its tile's pixels and its intersections' gradient slots); positions inside a
+// bucket come from LDS atomics.
 
 constexpr int kOrderThreads = 1024;
 
@@ -371,25 +373,19 @@ __device__ __forceinline__ int order_bucket(int32_t c) {
     return e < 3 ? c : e * 8 + ((c >> (e - 3)) & 7);
 }
 
-// Intersection count of workgroup b's tile: (image, tile) = divmod(b, num_tiles), bins of the
-// image's geometry (image 0 when the geometry is shared).
-__device__ __forceinline__ int32_t order_cost(const int32_t* bins, int64_t b, int32_t num_tiles,
-                                              int32_t per_image) {
-    const int64_t image = b / num_tiles;
-    const int64_t g = (per_image ? image : 0) * num_tiles + (b - image * num_tiles);
-    return bins[2 * g + 1] - bins[2 * g];
-}
-
-// One workgroup: bucket histogram, exclusive scan from the largest bucket down, scatter.
+// One workgroup per image: bucket histogram of the image's tiles, exclusive scan from the largest
+// bucket down, scatter into the image's num_tiles entries of order. Bins of the image's geometry
+// (image 0 when the geometry is shared).
 __global__ void __launch_bounds__(kOrderThreads)
-tile_order_kernel(const int32_t* bins, int64_t blocks, int32_t num_tiles, int32_t per_image,
-                  int32_t* order) {
+tile_order_kernel(const int32_t* bins, int32_t num_tiles, int32_t per_image, int32_t* order) {
     __shared__ uint32_t s_cnt[256], s_scan[2][256];
     const int tid = threadIdx.x;
+    const int64_t image = blockIdx.x;
+    const int32_t* ib = bins + 2 * (per_image ? image : 0) * (int64_t)num_tiles;
     if (tid < 256) s_cnt[tid] = 0;
     __syncthreads();
-    for (int64_t b = tid; b < blocks; b += kOrderThreads)
-        atomicAdd(&s_cnt[255 - order_bucket(order_cost(bins, b, num_tiles, per_image))], 1u);
+    for (int32_t t = tid; t < num_tiles; t += kOrderThreads)
+        atomicAdd(&s_cnt[255 - order_bucket(ib[2 * t + 1] - ib[2 * t])], 1u);
     __syncthreads();
     // inclusive Hillis-Steele scan over the 256 buckets (largest counts first)
     int cur = 0;
@@ -405,17 +401,18 @@ tile_order_kernel(const int32_t* bins, int64_t blocks, int32_t num_tiles, int32_
     }
     if (tid < 256) s_cnt[tid] = s_scan[cur][tid] - s_cnt[tid];  // exclusive
     __syncthreads();
-    for (int64_t b = tid; b < blocks; b += kOrderThreads) {
-        const uint32_t at =
-            atomicAdd(&s_cnt[255 - order_bucket(order_cost(bins, b, num_tiles, per_image))], 1u);
-        order[at] = (int32_t)b;
+    const int32_t first = (int32_t)(image * num_tiles);
+    for (int32_t t = tid; t < num_tiles; t += kOrderThreads) {
+        const uint32_t at = atomicAdd(&s_cnt[255 - order_bucket(ib[2 * t + 1] - ib[2 * t])], 1u);
+        order[first + at] = first + t;
     }
 }
 
+// blocks = images * num_tiles workgroups of a blend.
 static int launch_tile_order(const int32_t* bins, int64_t blocks, int32_t num_tiles,
                              int32_t per_image, int32_t* order, hipStream_t stream) {
-    hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, stream, bins, blocks,
-                       num_tiles, per_image, order);
+    hipLaunchKernelGGL(tile_order_kernel, dim3((unsigned)(blocks / num_tiles)),
+                       dim3(kOrderThreads), 0, stream, bins, num_tiles, per_image, order);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
 }
 
@@ -537,15 +534,22 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
         bin_final = P.final_idx[frow * C.img_w + j];
         const float t_final = P.final_Ts[frow * C.img_w + j];
         T = t_final;
+        // The cotangents enter halved (exact), so every product below that is linear in them
+        // (v_alpha, v_sigma and all sums but the conic's a and c terms) is half the reference's;
+        // the batch readout doubles those sums, exactly again. The conic's a and c terms,
+        // 0.5 v_sigma dx dx and 0.5 v_sigma dy dy, need no 0.5 factor of their own then.
         const int64_t vrow = ((int64_t)image_id * C.img_h + i) % P.vout_rows;
         const float* vo = P.v_out + 3 * (vrow * C.img_w + j);
-        v0 = vo[0]; v1 = vo[1]; v2 = vo[2];
+        v0 = 0.5f * vo[0]; v1 = 0.5f * vo[1]; v2 = 0.5f * vo[2];
         const float* bg = C.background + 3 * (C.rows_bg > 1 ? image_id : 0);
         tfbg = t_final * ((bg[0] * v0 + bg[1] * v1) + bg[2] * v2);
         if constexpr (kDepth)
-            vd = P.v_out_depth[(((int64_t)image_id * C.img_h + i) % P.vdepth_rows) * C.img_w + j];
+            vd = 0.5f * P.v_out_depth[(((int64_t)image_id * C.img_h + i) % P.vdepth_rows) *
+                                          C.img_w + j];
     }
-    float bufv = 0.f;  // sum_k buffer_k * v_k of the reference's colour accumulator
+    // T_final (bg . v) plus sum_k buffer_k * v_k of the reference's colour accumulator, as one
+    // running sum
+    float acc_v = tfbg;
     if (tid == 0) s_max = range_start - 1;
     for (int k = tid; k < kTile * kAccSlots; k += kTile) acc[k] = 0.0f;
     __syncthreads();
@@ -587,12 +591,17 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
         const bool live = batch_end - tid >= range_start;
         const int32_t my_pos = live ? P.pos[src] : -1;  // emission position of slot tid
         const int len = uniform(stage_batch<false>(C, L, src, live, tile_x, tile_y).wave_max);
-        const uint8_t* list = L.list[uniform(wave)];
+        // the wave's list in one register: lane l holds entries 4l .. 4l + 3
+        const uint32_t list4 = reinterpret_cast<const uint32_t*>(L.list[uniform(wave)])[lane];
+        uint32_t word = 0;
         for (int k = 0; k < len; ++k) {
-            const int t = uniform(list[k]);
+            if ((k & 3) == 0) word = __builtin_amdgcn_readlane(list4, k >> 2);
+            const int t = (int)((word >> (8 * (k & 3))) & 255u);
             const int32_t idx = batch_end - t;
             if (idx > wmax) continue;  // wave-uniform
-            const float4 r0 = L.r0[t], r1 = L.r1[t];
+            const float4 r0 = L.r0[t], r1 = L.r1[t], r2 = L.r2[t];
+            // the whole record in the first reads (full-width reads, one address)
+            asm volatile("" ::"v"(r1.y), "v"(r2.x), "v"(r2.y), "v"(r2.z), "v"(r2.w));
             const float dx = r0.x - px, dy = r0.y - py;
             const float sigma = (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
             // bitwise: no short-circuit branch around the sigma_max read
@@ -602,27 +611,29 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             // (an exec-masked instruction costs the same issue slot), so the wave reduction
             // below always sees exact zeros there and no branch is needed.
             const float vis = exp_core(-sigma);
-            const float alpha = minw(kAlphaMax, r1.y * vis);
-            const bool valid = in_range && alpha >= kAlphaThresh;
-            const float4 r2 = L.r2[t];
+            const float ov = r1.y * vis;
+            const float alpha_c = minw(kAlphaMax, ov);
+            const bool valid = in_range && alpha_c >= kAlphaThresh;
+            // a lane outside the accepted set blends alpha = 0: T / (1 - 0) = T and its weight
+            // alpha T is zero, so T and the running sum need no select
+            const float alpha = valid ? alpha_c : 0.0f;
             const float d = 1.0f - alpha;
             float ra = __builtin_amdgcn_rcpf(d);
             ra = fmaf(ra, fmaf(-d, ra, 1.0f), ra);
-            const float Tn = T * ra;
-            T = valid ? Tn : T;
-            const float fac = valid ? alpha * Tn : 0.0f;
+            T = T * ra;
+            const float fac = alpha * T;
             float cv = fmaf(r2.x, v0, fmaf(r2.y, v1, r2.z * v2));
             if constexpr (kDepth) cv = fmaf(r2.w, vd, cv);  // depth as a fourth channel
-            const float v_alpha = fmaf(Tn, cv, -ra * (bufv + tfbg));
-            bufv = fmaf(cv, fac, bufv);
-            const float ov = r1.y * vis;
+            const float v_alpha = fmaf(T, cv, -ra * acc_v);  // halved
+            acc_v = fmaf(cv, fac, acc_v);
             const bool geo = valid && ov <= kAlphaMax;
-            const float vs = geo ? -ov * v_alpha : 0.0f;
+            const float va = geo ? v_alpha : 0.0f;
+            const float vs = -ov * va;  // v_sigma, halved
             const float hx = vs * dx, hy = vs * dy;
             const float g0 = v0 * fac, g1 = v1 * fac, g2 = v2 * fac;
-            const float g3 = 0.5f * hx * dx, g4 = hx * dy, g5 = 0.5f * hy * dy;
+            const float g3 = hx * dx, g4 = hx * dy, g5 = hy * dy;  // g3, g5 whole
             const float g6 = hx, g7 = hy;
-            const float g8 = geo ? vis * v_alpha : 0.0f;
+            const float g8 = vis * va;
             const float g9 = kDepth ? vd * fac : 0.0f;
             // reduce-scatter over the wave: after the swaps, row r of qa holds g0/g2/g1/g3 and
             // of qb g4/g6/g5/g7 (rows 0..3); qc is g8 unswapped (each row reduces its own lanes)
@@ -643,7 +654,8 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             float s[NG], part[4];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                s[k] = ACC(tid, k);
+                // the halved sums doubled (the conic's a and c terms, slots 3 and 5, are whole)
+                s[k] = (k == 3 || k == 5) ? ACC(tid, k) : 2.0f * ACC(tid, k);
                 ACC(tid, k) = 0.0f;
             }
 #pragma unroll
@@ -652,10 +664,10 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
                 ACC(tid, 8 + r) = 0.0f;
             }
             if constexpr (kDepth) {
-                s[8] = part[0] + part[1];
-                s[9] = part[2] + part[3];
+                s[8] = 2.0f * (part[0] + part[1]);
+                s[9] = 2.0f * (part[2] + part[3]);
             } else {
-                s[8] = (part[0] + part[1]) + (part[2] + part[3]);
+                s[8] = 2.0f * ((part[0] + part[1]) + (part[2] + part[3]));
             }
             if (my_pos >= 0 && my_pos < P.M) store_rgrad<NG>(P.rgrad, rg_off + my_pos, s);
         }
