@@ -290,31 +290,38 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
             stage_batch<true>(C, L, src, batch_start + tid < range_end, tile_x, tile_y);
         if (__ballot(!done) == 0ull) continue;
         const uint8_t* list = L.list[sb];
+        const int my_len = len.mine;  // uniform per row
         for (int k = 0; k < len.wave_max; ++k) {
-            // the wave stops walking once all of its pixels are done
-            if (__builtin_amdgcn_ballot_w64(!done) == 0ull) break;
-            const bool has = k < len.mine;  // uniform per row
-            const int t = list[has ? k : 0];
+            // A lane leaves once its pixel is done or its row's list is walked; the wave walks
+            // while any lane is left, which is exec-mask bookkeeping only.
+            if (done || k >= my_len) break;
+            const int t = list[k];
             const float4 r0 = L.r0[t], r1 = L.r1[t];
+            // all of r1 in the first read (one full-width read, one address)
+            asm volatile("" ::"v"(r1.y));
             const float dx = r0.x - px, dy = r0.y - py;
             const float sigma = (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
-            // bitwise: no short-circuit branch around the sigma_max read (NaN sigma fails both)
-            if (!(has & (!done) & (sigma >= 0.0f) & (sigma <= r1.z))) continue;
-            const float alpha = minw(kAlphaMax, r1.y * exp_core(-sigma));
-            if (alpha < kAlphaThresh) continue;
-            const float next_T = T * (1.0f - alpha);
-            if (next_T <= kTEps) {
-                done = true;
-                continue;
+            // Nested conditions and the one exit above: every other path falls through to the
+            // next step, which keeps the loop's control flow in the exec mask. Bitwise: no
+            // short-circuit branch around the sigma_max read (NaN sigma fails both).
+            if ((sigma >= 0.0f) & (sigma <= r1.z)) {
+                const float alpha = minw(kAlphaMax, r1.y * exp_core(-sigma));
+                if (alpha >= kAlphaThresh) {
+                    const float next_T = T * (1.0f - alpha);
+                    if (next_T <= kTEps) {
+                        done = true;  // leaves at the next step
+                    } else {
+                        const float4 r2 = L.r2[t];
+                        const float vis = alpha * T;
+                        o0 = o0 + r2.x * vis;
+                        o1 = o1 + r2.y * vis;
+                        o2 = o2 + r2.z * vis;
+                        if constexpr (kDepth) od = od + r2.w * vis;
+                        T = next_T;
+                        cur_idx = batch_start + t;
+                    }
+                }
             }
-            const float4 r2 = L.r2[t];
-            const float vis = alpha * T;
-            o0 = o0 + r2.x * vis;
-            o1 = o1 + r2.y * vis;
-            o2 = o2 + r2.z * vis;
-            if constexpr (kDepth) od = od + r2.w * vis;
-            T = next_T;
-            cur_idx = batch_start + t;
         }
     }
     if (inside) {
