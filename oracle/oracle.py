@@ -87,6 +87,14 @@ def expf(x) -> np.ndarray:
     return y
 
 
+def blend_expf(x) -> np.ndarray:
+    """The blends' exp(-sigma) sequence (x <= 0)."""
+    x = _c32(x).ravel()
+    y = np.empty_like(x)
+    lib().oracle_blend_expf_n(_f(x), _f(y), _i64(x.size))
+    return y
+
+
 def key_layout(B: int, H: int, W: int) -> tuple[dict, bool]:
     out = np.zeros(6, np.int32)
     ok = lib().oracle_key_layout(_i32(B), _i32(H), _i32(W), _i(out))

@@ -12,7 +12,9 @@
  *   - Division and sqrt are correctly rounded.
  *   - exp and log are the fixed-sequence routines oracle_expf / oracle_logf below (Cody-Waite
  *     range reduction plus a Taylor / atanh series), not a libm call, because libm and the GPU's
- *     device library round differently in the last place.
+ *     device library round differently in the last place. The blends' exp(-sigma) is its own
+ *     shorter sequence, oracle_blend_expf (magic-constant rounding, a degree-6 polynomial and an
+ *     exponent-field scale), and their sigma and colour sums are written with fmaf.
  *   - min(a, b) = a < b ? a : b and max(a, b) = a > b ? a : b (scalar min/max semantics of the
  *     reference's Warp kernels); float -> int32 truncates toward zero and saturates, NaN -> 0.
  *   - 3x3 products associate as (a0*b0 + a1*b1) + a2*b2.
@@ -38,6 +40,10 @@ static const float GAUSSIAN_EXTEND_SQ = 0x1.62d844p+3f; /* float32(3.33 * 3.33) 
 static const float ALPHA_THRESHOLD = 0x1.010102p-8f;    /* float32(1 / 255) */
 static const float ALPHA_MAX = 0x1.ff7ceep-1f;          /* float32(0.999) */
 static const float T_EPS = 0x1.a36e2ep-14f;             /* float32(1e-4) */
+/* Largest sigma the blends accept: oracle_blend_expf(-87) is still a normal float. A larger sigma
+ * is rejected, as the exact alpha would be for opacities below 2.4e35 (the GPU caps its packed
+ * sigma_max at the same value). */
+static const float BLEND_SIGMA_CAP = 87.0f;
 static const float DILATION = 0x1.333334p-2f;           /* float32(0.3) */
 static const float FOV_CLAMP = 0x1.4ccccdp+0f;          /* float32(1.3) */
 static const float Z_EPS = 0x1.0c6f7ap-20f;             /* float32(1e-6) */
@@ -119,12 +125,38 @@ float oracle_expf(float x) {
 }
 
 /* The blends' Gaussian exponent 0.5 (a dx^2 + c dy^2) + b dx dy (splax/_rasterize/_kernels.py:187,
- * 1039), evaluated as (a/2 dx dx + c/2 dy dy) + b dx dy with the halving applied to a and c
- * first. Scaling by 1/2 is exact, so this is the reference's expression bit for bit unless an
- * intermediate falls below the normal range. */
+ * 1039), evaluated as dx (a/2 dx + b dy) + (c/2 dy) dy with two FMAs (the same value in exact
+ * arithmetic; the halving of a and c is exact). */
 static inline float blend_sigma(const float* cn, float dx, float dy) {
     const float ha = 0.5f * cn[0], hc = 0.5f * cn[2];
-    return (ha * dx * dx + hc * dy * dy) + cn[1] * dx * dy;
+    return fmaf(dx, fmaf(ha, dx, cn[1] * dy), (hc * dy) * dy);
+}
+
+/* e^x for the blends' x = -sigma <= 0: k = round(x log2 e) by adding 1.5 * 2^23 (the integer then
+ * sits in the low mantissa bits of the sum), r = x - k fl(ln2) in one FMA, e^r by a degree-6
+ * polynomial with c0 = c1 = 1 fitted by Lawson's iteration (relative error 4.4e-9 on
+ * |r| <= ln2 / 2 with these float coefficients), and 2^k added to the exponent field as an
+ * integer: at most 1 ulp from e^x on [-8, 0], 2 ulp down to -30, 5 ulp down to -87
+ * (tests/test_oracle_math.py). Below 2^-126 the result is not e^x but tiny,
+ * negative or NaN, so an alpha built from it fails the 1/255 test as the exact one would for
+ * opacities below 1e30. */
+float oracle_blend_expf(float x) {
+    const float t = fmaf(x, LOG2E, 0x1.8p23f);
+    const float kf = t - 0x1.8p23f;
+    const float r = fmaf(kf, -0x1.62e430p-1f, x);
+    float p = fmaf(r, 0x1.6a2352p-10f, 0x1.123a6cp-7f);
+    p = fmaf(r, p, 0x1.5558f4p-5f);
+    p = fmaf(r, p, 0x1.55549p-3f);
+    p = fmaf(r, p, 0x1.fffffcp-2f);
+    p = fmaf(r, p, 1.0f);
+    p = fmaf(r, p, 1.0f);
+    uint32_t pb, tb;
+    memcpy(&pb, &p, 4);
+    memcpy(&tb, &t, 4);
+    pb += tb << 23;
+    float y;
+    memcpy(&y, &pb, 4);
+    return y;
 }
 
 /* ---------------------------------------------------------------- 3x3 helpers (row major) */
@@ -810,8 +842,8 @@ void oracle_blend_fwd(const float* colors, int64_t rows_colors, const float* opa
                     float dx = xys[2 * g] - px, dy = xys[2 * g + 1] - py;
                     float sigma = blend_sigma(conics + 3 * g, dx, dy);
                     float op = opacities[g % rows_opac];
-                    float alpha = fminw(ALPHA_MAX, op * oracle_expf(-sigma));
-                    if (sigma < 0.0f || alpha < ALPHA_THRESHOLD) {
+                    float alpha = fminw(ALPHA_MAX, op * oracle_blend_expf(-sigma));
+                    if (sigma < 0.0f || sigma > BLEND_SIGMA_CAP || alpha < ALPHA_THRESHOLD) {
                         ++pr;
                         continue;
                     }
@@ -823,10 +855,10 @@ void oracle_blend_fwd(const float* colors, int64_t rows_colors, const float* opa
                     ++pc;
                     float vis = alpha * T;
                     const float* c = colors + 3 * (g % rows_colors);
-                    o0 = o0 + c[0] * vis;
-                    o1 = o1 + c[1] * vis;
-                    o2 = o2 + c[2] * vis;
-                    if (out_depth) od = od + depths[g] * vis;
+                    o0 = fmaf(c[0], vis, o0);
+                    o1 = fmaf(c[1], vis, o1);
+                    o2 = fmaf(c[2], vis, o2);
+                    if (out_depth) od = fmaf(depths[g], vis, od);
                     T = next_T;
                     cur_idx = k;
                 }
@@ -936,11 +968,11 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
                         const float* cn = conics + 3 * g;
                         float a = cn[0], b = cn[1], c = cn[2];
                         float sigma = blend_sigma(cn, dx, dy);
-                        if (sigma < 0.0f) {
+                        if (sigma < 0.0f || sigma > BLEND_SIGMA_CAP) {
                             ++qr;
                             continue;
                         }
-                        float vis = oracle_expf(-sigma);
+                        float vis = oracle_blend_expf(-sigma);
                         float op = opacities[g % rows_opac];
                         float alpha = fminw(ALPHA_MAX, op * vis);
                         if (alpha < ALPHA_THRESHOLD) {
@@ -1202,6 +1234,10 @@ void oracle_logf_n(const float* x, float* y, int64_t n) {
 
 void oracle_expf_n(const float* x, float* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = oracle_expf(x[i]);
+}
+
+void oracle_blend_expf_n(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = oracle_blend_expf(x[i]);
 }
 
 #ifdef _OPENMP

@@ -22,6 +22,7 @@ float oracle_logf(float x);
 float oracle_expf(float x);
 void oracle_logf_n(const float* x, float* y, int64_t n);
 void oracle_expf_n(const float* x, float* y, int64_t n);
+void oracle_blend_expf_n(const float* x, float* y, int64_t n);
 int oracle_set_threads(int n);
 
 /* Key layout of the packed 32-bit sort key (splax/_rasterize/_sort/_sort.py:51-60).

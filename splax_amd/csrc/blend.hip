@@ -42,6 +42,11 @@ struct BlendCommon {
     int64_t total;  // geometry rows (B_geom * n): ids outside [0, total) are ignored
 };
 
+// Largest sigma a blend accepts: blend_exp(-87) is still a normal float. An intersection with a
+// larger sigma is rejected, as the exact alpha would be for opacities below 2.4e35 (the CPU oracle
+// applies the same cap).
+constexpr float kBlendSigmaCap = 87.0f;
+
 // Pixel of thread `tid` in its tile: wave w = quadrant (w & 1, w >> 1), row r = lane >> 4 =
 // 4x4 sub-block (r & 1, r >> 1) of the quadrant, lane & 15 = 4x4 raster.
 __device__ __forceinline__ void tile_pixel(int tid, int tile_x, int tile_y, int& i, int& j) {
@@ -90,11 +95,12 @@ __global__ void __launch_bounds__(256) pack_records_kernel(PackParams P) {
             o = o * compensation_rho(a, b, c, rho2);
         }
         const int64_t cg = g % P.rows_colors;
+        // sigma_max is capped at kBlendSigmaCap, where blend_exp's range ends
         float smax;
         if (o > 0.0f) {
-            smax = __logf(o * 255.0f) + 1e-3f;
+            smax = fminf(__logf(o * 255.0f) + 1e-3f, kBlendSigmaCap);
         } else {
-            smax = (o != o) ? __builtin_inff() : -__builtin_inff();
+            smax = (o != o) ? kBlendSigmaCap : -__builtin_inff();
         }
         uint32_t mode = kCullKeep;
         float ex = 0.0f, ey = 0.0f;
@@ -234,18 +240,36 @@ __device__ __forceinline__ RowLens stage_batch(const BlendCommon& C, BatchLds& L
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // e^x for x in [-88, 0] (no range handling needed there); equal to det_expf on that domain.
-__device__ __forceinline__ float exp_core(float x) {
-    float kf = rintf(x * kLog2e);
-    float r = fmaf(kf, -kLn2Hi, x);
-    r = fmaf(kf, -kLn2Lo, r);
-    float p = fmaf(r, 0x1.a01a02p-13f, 0x1.6c16c2p-10f);
-    p = fmaf(r, p, 0x1.111112p-7f);
-    p = fmaf(r, p, 0x1.555556p-5f);
-    p = fmaf(r, p, 0x1.555556p-3f);
-    p = fmaf(r, p, 0.5f);
+// e^x for the blends' x = -sigma (x <= 0; below 2^-126 the result is garbage, tiny, negative or
+// NaN, and every such alpha fails the 1/255 test as the exact one would for opacities below
+// 1e30):
+// k = round(x log2 e) by adding 1.5 * 2^23, whose integer then sits in the sum's low mantissa
+// bits; r = x - k ln2 with float ln2 in one FMA (the blends' |k| is small, so k (ln2 - fl(ln2))
+// stays far below an ulp); a degree-6 polynomial of e^r with c0 = c1 = 1 fitted by Lawson's
+// iteration (relative error 4.4e-9 on |r| <= ln2 / 2 with these float coefficients); 2^k added
+// to the exponent field. At most 1 ulp from e^x on [-8, 0], 2 ulp down to -30 and 5 ulp down to
+// -87 (the reduction's error grows with |k|). Ten VALU; the CPU oracle evaluates the same
+// sequence.
+constexpr float kBlendLn2 = 0x1.62e430p-1f;
+__device__ __forceinline__ float blend_exp(float x) {
+    const float t = fmaf(x, kLog2e, 0x1.8p23f);
+    const float kf = t - 0x1.8p23f;
+    const float r = fmaf(kf, -kBlendLn2, x);
+    float p = fmaf(r, 0x1.6a2352p-10f, 0x1.123a6cp-7f);
+    p = fmaf(r, p, 0x1.5558f4p-5f);
+    p = fmaf(r, p, 0x1.55549p-3f);
+    p = fmaf(r, p, 0x1.fffffcp-2f);
     p = fmaf(r, p, 1.0f);
     p = fmaf(r, p, 1.0f);
-    return ldexpf(p, (int)kf);
+    return __uint_as_float(__float_as_uint(p) + (__float_as_uint(t) << 23));
+}
+
+// The Gaussian exponent 0.5 (a dx^2 + c dy^2) + b dx dy of a packed record (r0.z = a/2,
+// r0.w = b, r1.x = c/2) as dx (a/2 dx + b dy) + (c/2 dy) dy: two FMAs, seven VALU with the
+// offsets. The CPU oracle evaluates the same expression.
+__device__ __forceinline__ float blend_sigma(const float4& r0, const float4& r1, float dx,
+                                             float dy) {
+    return fmaf(dx, fmaf(r0.z, dx, r0.w * dy), (r1.x * dy) * dy);
 }
 
 // ------------------------------------------------------------------ forward
@@ -300,12 +324,12 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
             // all of r1 in the first read (one full-width read, one address)
             asm volatile("" ::"v"(r1.y));
             const float dx = r0.x - px, dy = r0.y - py;
-            const float sigma = (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
+            const float sigma = blend_sigma(r0, r1, dx, dy);
             // Nested conditions and the one exit above: every other path falls through to the
             // next step, which keeps the loop's control flow in the exec mask. Bitwise: no
             // short-circuit branch around the sigma_max read (NaN sigma fails both).
             if ((sigma >= 0.0f) & (sigma <= r1.z)) {
-                const float alpha = minw(kAlphaMax, r1.y * exp_core(-sigma));
+                const float alpha = minw(kAlphaMax, r1.y * blend_exp(-sigma));
                 if (alpha >= kAlphaThresh) {
                     const float next_T = T * (1.0f - alpha);
                     if (next_T <= kTEps) {
@@ -313,10 +337,10 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
                     } else {
                         const float4 r2 = L.r2[t];
                         const float vis = alpha * T;
-                        o0 = o0 + r2.x * vis;
-                        o1 = o1 + r2.y * vis;
-                        o2 = o2 + r2.z * vis;
-                        if constexpr (kDepth) od = od + r2.w * vis;
+                        o0 = fmaf(r2.x, vis, o0);
+                        o1 = fmaf(r2.y, vis, o1);
+                        o2 = fmaf(r2.z, vis, o2);
+                        if constexpr (kDepth) od = fmaf(r2.w, vis, od);
                         T = next_T;
                         cur_idx = batch_start + t;
                     }
@@ -610,19 +634,20 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             // the whole record in the first reads (full-width reads, one address)
             asm volatile("" ::"v"(r1.y), "v"(r2.x), "v"(r2.y), "v"(r2.z), "v"(r2.w));
             const float dx = r0.x - px, dy = r0.y - py;
-            const float sigma = (r0.z * dx * dx + r1.x * dy * dy) + r0.w * dx * dy;
+            const float sigma = blend_sigma(r0, r1, dx, dy);
             // bitwise: no short-circuit branch around the sigma_max read
             const bool in_range = (idx <= bin_final) & (sigma >= 0.0f) & (sigma <= r1.z);
             if (__builtin_amdgcn_ballot_w64(in_range) == 0ull) continue;
             // Every lane computes and the lanes outside the accepted set are masked by selects
             // (an exec-masked instruction costs the same issue slot), so the wave reduction
             // below always sees exact zeros there and no branch is needed.
-            const float vis = exp_core(-sigma);
+            const float vis = blend_exp(-sigma);
             const float ov = r1.y * vis;
             const float alpha_c = minw(kAlphaMax, ov);
             const bool valid = in_range && alpha_c >= kAlphaThresh;
-            // a lane outside the accepted set blends alpha = 0: T / (1 - 0) = T and its weight
-            // alpha T is zero, so T and the running sum need no select
+            // a lane outside the accepted set blends alpha = 0 (a select, so whatever vis is):
+            // T / (1 - 0) = T and its weight alpha T is zero, so T and the running sum need no
+            // select of their own
             const float alpha = valid ? alpha_c : 0.0f;
             const float d = 1.0f - alpha;
             float ra = __builtin_amdgcn_rcpf(d);
@@ -634,13 +659,14 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             const float v_alpha = fmaf(T, cv, -ra * acc_v);  // halved
             acc_v = fmaf(cv, fac, acc_v);
             const bool geo = valid && ov <= kAlphaMax;
-            const float va = geo ? v_alpha : 0.0f;
-            const float vs = -ov * va;  // v_sigma, halved
+            // selects, not products with a masked zero: outside the accepted set vis and ov may be
+            // inf or NaN (blend_exp is defined for sigma <= kBlendSigmaCap only)
+            const float vs = geo ? -ov * v_alpha : 0.0f;  // v_sigma, halved
             const float hx = vs * dx, hy = vs * dy;
             const float g0 = v0 * fac, g1 = v1 * fac, g2 = v2 * fac;
             const float g3 = hx * dx, g4 = hx * dy, g5 = hy * dy;  // g3, g5 whole
             const float g6 = hx, g7 = hy;
-            const float g8 = vis * va;
+            const float g8 = geo ? vis * v_alpha : 0.0f;
             const float g9 = kDepth ? vd * fac : 0.0f;
             // reduce-scatter over the wave: after the swaps, row r of qa holds g0/g2/g1/g3 and
             // of qb g4/g6/g5/g7 (rows 0..3); qc is g8 unswapped (each row reduces its own lanes)

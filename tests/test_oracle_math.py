@@ -66,6 +66,43 @@ def test_expf_monotone_on_blend_range():
     assert np.all(np.diff(y.astype(np.float64)) >= 0.0)
 
 
+def test_blend_expf_accuracy_sweep():
+    """The blends' exp(-sigma) sequence against float64 exp: random points over its whole normal
+    domain plus every 64th float of [-8, 0] (where the blends' x lives)."""
+    rng = np.random.default_rng(5)
+    dense = (np.arange(np.float32(-8.0).view(np.uint32), np.uint32(0x80000000) - 1, -64,
+                       dtype=np.int64).astype(np.uint32).view(np.float32))
+    # one float ln2 in the reduction: the error k (ln2 - fl(ln2)) grows with |k|, so the bound
+    # widens with the range (opacity <= 1 keeps the blends inside [-5.6, 0])
+    for lo, hi, bound, extra in ((-8.0, 0.0, 1.0, dense), (-30.0, -8.0, 2.0, None),
+                                 (-87.0, -30.0, 5.0, None)):
+        x = rng.uniform(lo, hi, 400_000).astype(np.float32)
+        if extra is not None:
+            x = np.concatenate([x, extra])
+        err = _ulp_err(O.blend_expf(x), np.exp(x.astype(np.float64)))
+        assert err.max() <= bound, f"[{lo}, {hi}]: max ulp error {err.max()} at {x[np.argmax(err)]}"
+    assert O.blend_expf(np.float32(0.0))[0] == 1.0
+    assert O.blend_expf(np.float32(-0.0))[0] == 1.0
+    # where x = -m fl(ln2) is exact in float32 (fl(ln2) has 20 significant bits), the reduction
+    # leaves r = 0 and the result is exactly 2^-m
+    m = np.arange(0, 40)
+    x64 = -m * np.float64(np.float32(np.log(2.0)))
+    exact = x64.astype(np.float32).astype(np.float64) == x64
+    assert exact.sum() >= 20
+    y = O.blend_expf(x64[exact].astype(np.float32)).astype(np.float64)
+    assert np.all(y == 2.0 ** -m[exact])
+
+
+def test_blend_expf_monotone_and_below_range():
+    x = np.sort(np.random.default_rng(6).uniform(-8.0, 0.0, 400_000).astype(np.float32))
+    assert np.all(np.diff(O.blend_expf(x).astype(np.float64)) >= 0.0)
+    # under 2^-126 the value is no exponential any more but tiny, negative or NaN, never a large
+    # positive one, so the blends' alpha test (alpha >= 1/255, false for NaN) rejects it as it
+    # would the exact value
+    low = np.linspace(-95.0, -87.4, 20_000).astype(np.float32)
+    assert not np.any(O.blend_expf(low) >= 2.0 ** -125)
+
+
 @pytest.mark.parametrize(
     "B,H,W,tile_bits,image_bits,depth_bits,packed",
     [
