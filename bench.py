@@ -177,10 +177,24 @@ def bench_train(args):
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(adam_bytes / adam_s / 1e9 / HBM_PEAK_GBS, 4)
                      if adam_s > 0 else None,
-                     "traffic": None, "work_per_launch": adam_bytes},
+                     "traffic": profiled_traffic("adam_step", 4), "work_per_launch": adam_bytes},
         "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
+    if args.calibrate_copy:
+        calibrate_copy(dev)
+
+
+def calibrate_copy(dev):
+    """Three plain 256 MiB device copies after the bench line: the FETCH_SIZE / WRITE_SIZE scale
+    of the HBM traffic summaries under profiles/ comes from them."""
+    import torch
+
+    src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def main():
@@ -323,11 +337,7 @@ def main():
     }
     print(json.dumps(out), flush=True)
     if args.calibrate_copy:
-        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+        calibrate_copy(dev)
 
 
 if __name__ == "__main__":
