@@ -274,16 +274,18 @@ rts_scan_kernel(uint32_t* __restrict__ counts, int64_t parts, uint32_t* __restri
 // items in emission order, so no pass gathers at random. K is the key word (uint32_t for the
 // packed key, uint64_t for the 64-bit key, ordered as unsigned).
 template <typename K, int kItems>
-__global__ void __launch_bounds__(kSortThreads)
+// at most 64 VGPRs (eight waves per SIMD), so two 1024-thread workgroups share a CU
+__global__ void __launch_bounds__(kSortThreads, 8)
 rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
                    const int32_t* __restrict__ ids_in, K* __restrict__ keys_out,
                    int32_t* __restrict__ vals_out, int32_t* __restrict__ ids_out, int64_t M,
                    int shift, const uint32_t* __restrict__ offsets,
                    const uint32_t* __restrict__ totals, int64_t parts) {
     constexpr int kTile = kItems * kSortThreads;
+    // one staging buffer carries keys, then positions, then ids (three rounds), so two
+    // 1024-thread workgroups fit a CU's LDS at eight keys per thread
     __shared__ K s_keys[kTile];
-    __shared__ uint32_t s_vals[kTile];
-    __shared__ uint32_t s_ids[kTile];
+    uint32_t* const s_u32 = reinterpret_cast<uint32_t*>(s_keys);
     __shared__ uint32_t s_cnt[kSortWaves][256];
     __shared__ uint32_t s_local_start[256];
     __shared__ int32_t s_dest_base[256];
@@ -296,16 +298,15 @@ rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ va
     const int64_t base = part * kTile;
     const int64_t wbase = base + (int64_t)wave * (kItems * 64);
 
-    // keys and values are all loaded up front so their latencies overlap
+    // the keys first; positions and ids are loaded a round ahead of their own LDS round, so the
+    // ranking runs with only keys and ranks live
+    // item i of this thread sits at my0 + 64 i (in range while 64 i < rem): one base address and
+    // immediate offsets for every load
+    const int64_t my0 = wbase + lane;
+    const int64_t rem = M - my0;
     K key[kItems];
-    uint32_t val[kItems], gid[kItems];
 #pragma unroll
-    for (int i = 0; i < kItems; ++i) {
-        const int64_t pos = wbase + i * 64 + lane;
-        key[i] = pos < M ? keys_in[pos] : ~(K)0;
-        val[i] = pos < M ? (vals_in ? (uint32_t)vals_in[pos] : (uint32_t)pos) : 0u;
-        gid[i] = pos < M ? (uint32_t)ids_in[pos] : 0u;
-    }
+    for (int i = 0; i < kItems; ++i) key[i] = i * 64 < rem ? keys_in[my0 + i * 64] : ~(K)0;
     const uint32_t total_d = tid < 256 ? totals[tid] : 0u;
     const uint32_t offset_d = tid < 256 ? offsets[(int64_t)tid * parts + part] : 0u;
 
@@ -332,17 +333,11 @@ rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ va
     // per digit (thread = digit): wave offsets, local digit starts, global destinations
     uint32_t tot = 0;
     if (tid < 256) {
-        uint32_t c[kSortWaves];
-#pragma unroll
+        // exclusive running sum over the waves, in place (one value live)
         for (int w = 0; w < kSortWaves; ++w) {
-            c[w] = s_cnt[w][tid];
-            tot += c[w];
-        }
-        uint32_t run = 0;
-#pragma unroll
-        for (int w = 0; w < kSortWaves; ++w) {
-            s_cnt[w][tid] = run;
-            run += c[w];
+            const uint32_t c = s_cnt[w][tid];
+            s_cnt[w][tid] = tot;
+            tot += c;
         }
     }
     const uint32_t local_start = scan_256(tot, s_tmp, nullptr);
@@ -353,28 +348,62 @@ rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ va
     }
     __syncthreads();
 
-    // keys and values into LDS at their partition-sorted slot
+    // partition-sorted slot of each of this thread's keys
+    uint32_t slot[kItems];
 #pragma unroll
     for (int i = 0; i < kItems; ++i) {
         const uint32_t dd = (uint32_t)(key[i] >> shift) & 255u;
-        const uint32_t slot = s_local_start[dd] + s_cnt[wave][dd] + rank[i];
-        s_keys[slot] = key[i];
-        s_vals[slot] = val[i];
-        s_ids[slot] = gid[i];
+        slot[i] = s_local_start[dd] + s_cnt[wave][dd] + rank[i];
     }
+    uint32_t val[kItems];
+#pragma unroll
+    for (int i = 0; i < kItems; ++i)
+        val[i] = i * 64 < rem ? (vals_in ? (uint32_t)vals_in[my0 + i * 64]
+                                          : (uint32_t)(my0 + i * 64))
+                              : 0u;
+    // round 1, keys. Each digit's run is contiguous in the output, so consecutive j write
+    // consecutive addresses; the destinations are kept for the other two rounds.
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) s_keys[slot[i]] = key[i];
     __syncthreads();
-    // each digit's run is contiguous in the output: consecutive j write consecutive addresses
     const int64_t valid = (M - base) < kTile ? (M - base) : kTile;
+    // the digit of output slot r * kSortThreads + tid, four to a register: rounds 2 and 3 take the
+    // destination from s_dest_base again
+    uint32_t dig[(kItems + 3) / 4] = {};
 #pragma unroll
     for (int r = 0; r < kItems; ++r) {
         const int j = r * kSortThreads + tid;
         if (j < valid) {
             const K k = s_keys[j];
-            const int64_t dest = (int64_t)s_dest_base[(uint32_t)(k >> shift) & 255u] + j;
-            keys_out[dest] = k;
-            vals_out[dest] = (int32_t)s_vals[j];
-            ids_out[dest] = (int32_t)s_ids[j];
+            const uint32_t d = (uint32_t)(k >> shift) & 255u;
+            dig[r >> 2] |= d << (8 * (r & 3));
+            keys_out[s_dest_base[d] + j] = k;
         }
+    }
+    __syncthreads();
+    // round 2, emission positions
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) s_u32[slot[i]] = val[i];
+    uint32_t gid[kItems];
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) gid[i] = i * 64 < rem ? (uint32_t)ids_in[my0 + i * 64] : 0u;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kItems; ++r) {
+        const int j = r * kSortThreads + tid;
+        if (j < valid)
+            vals_out[s_dest_base[(dig[r >> 2] >> (8 * (r & 3))) & 255u] + j] = (int32_t)s_u32[j];
+    }
+    __syncthreads();
+    // round 3, item ids
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) s_u32[slot[i]] = gid[i];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kItems; ++r) {
+        const int j = r * kSortThreads + tid;
+        if (j < valid)
+            ids_out[s_dest_base[(dig[r >> 2] >> (8 * (r & 3))) & 255u] + j] = (int32_t)s_u32[j];
     }
 }
 
@@ -562,8 +591,8 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     }
     {
         StageTimer tm(stream, kStageSort);
-        // 8192-key partitions once there are enough of them to fill the device: their digit runs
-        // (about 32 keys) leave as whole 128-byte lines; smaller sorts use 4096-key partitions
+        // 8192-key partitions from 1M keys on: their digit runs (about 32 keys) leave as whole
+        // 128-byte lines; smaller sorts use 4096-key partitions, so they still spread over the CUs
         const bool big = M >= kSortBigM;
         // passes ping-pong 0 -> 1 -> 0 ...; the first pass generates the emission positions,
         // the last writes positions and items straight into their final buffers (the caller's

@@ -76,7 +76,7 @@ void set_force_wide_keys(bool force);
 // Digit passes of the sort: at most 8 bytes of a 64-bit key.
 constexpr int kMaxPasses = 8;
 constexpr int kSortTileMin = 4096;   // keys per radix-sort partition (smallest size used)
-constexpr int64_t kSortBigM = 8 << 20;  // from this many keys on, partitions hold 8192 keys
+constexpr int64_t kSortBigM = 1 << 20;  // from this many keys on, partitions hold 8192 keys
 
 // Inputs of sort_and_bin and the blends.
 struct RasterInputs {
