@@ -283,8 +283,9 @@ int splat_set_stage_timing(int stage_mask);
 int splat_get_stage_times(double* ms, int64_t* calls, int32_t n);
 
 /* Waits for the current device and returns (then clears) its device error word: 0 when every
- * kernel ran within its invariants; bit 0 = a scan / sort look-back gave up waiting on a
- * predecessor (its results are then invalid). No counterpart in the reference. */
+ * kernel ran within its invariants. No kernel of this version waits on another workgroup, so no
+ * bit is in use; the word stays for kernels that would need such an invariant. No counterpart in
+ * the reference. */
 int splat_check_device(void);
 
 /* Library ABI version (bumped on any signature change). */

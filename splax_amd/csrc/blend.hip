@@ -404,21 +404,8 @@ __device__ __forceinline__ int order_bucket(int32_t c) {
     return e < 3 ? c : e * 8 + ((c >> (e - 3)) & 7);
 }
 
-// One workgroup per image: bucket histogram of the image's tiles, exclusive scan from the largest
-// bucket down, scatter into the image's num_tiles entries of order. Bins of the image's geometry
-// (image 0 when the geometry is shared).
-__global__ void __launch_bounds__(kOrderThreads)
-tile_order_kernel(const int32_t* bins, int32_t num_tiles, int32_t per_image, int32_t* order) {
-    __shared__ uint32_t s_cnt[256], s_scan[2][256];
-    const int tid = threadIdx.x;
-    const int64_t image = blockIdx.x;
-    const int32_t* ib = bins + 2 * (per_image ? image : 0) * (int64_t)num_tiles;
-    if (tid < 256) s_cnt[tid] = 0;
-    __syncthreads();
-    for (int32_t t = tid; t < num_tiles; t += kOrderThreads)
-        atomicAdd(&s_cnt[255 - order_bucket(ib[2 * t + 1] - ib[2 * t])], 1u);
-    __syncthreads();
-    // inclusive Hillis-Steele scan over the 256 buckets (largest counts first)
+// Exclusive scan of the 256 bucket counts in s_cnt, in place (all threads call it).
+__device__ __forceinline__ void order_scan(uint32_t* s_cnt, uint32_t (*s_scan)[256], int tid) {
     int cur = 0;
     if (tid < 256) s_scan[0][tid] = s_cnt[tid];
     __syncthreads();
@@ -430,9 +417,46 @@ tile_order_kernel(const int32_t* bins, int32_t num_tiles, int32_t per_image, int
         cur ^= 1;
         __syncthreads();
     }
-    if (tid < 256) s_cnt[tid] = s_scan[cur][tid] - s_cnt[tid];  // exclusive
+    if (tid < 256) s_cnt[tid] = s_scan[cur][tid] - s_cnt[tid];
     __syncthreads();
+}
+
+constexpr int kOrderPer = 8;  // tiles per thread kept in registers (images up to 8192 tiles)
+
+// One workgroup per image: bucket histogram of the image's tiles, exclusive scan from the largest
+// bucket down, scatter into the image's num_tiles entries of order. Bins of the image's geometry
+// (image 0 when the geometry is shared). Up to 8192 tiles every thread loads its counts at once
+// and keeps their buckets for the scatter; larger images take two strided passes.
+__global__ void __launch_bounds__(kOrderThreads)
+tile_order_kernel(const int32_t* bins, int32_t num_tiles, int32_t per_image, int32_t* order) {
+    __shared__ uint32_t s_cnt[256], s_scan[2][256];
+    const int tid = threadIdx.x;
+    const int64_t image = blockIdx.x;
+    const int32_t* ib = bins + 2 * (per_image ? image : 0) * (int64_t)num_tiles;
     const int32_t first = (int32_t)(image * num_tiles);
+    if (tid < 256) s_cnt[tid] = 0;
+    __syncthreads();
+    if (num_tiles <= kOrderThreads * kOrderPer) {
+        int bk[kOrderPer];
+#pragma unroll
+        for (int i = 0; i < kOrderPer; ++i) {
+            const int32_t t = i * kOrderThreads + tid;
+            bk[i] = t < num_tiles ? 255 - order_bucket(ib[2 * t + 1] - ib[2 * t]) : -1;
+        }
+#pragma unroll
+        for (int i = 0; i < kOrderPer; ++i)
+            if (bk[i] >= 0) atomicAdd(&s_cnt[bk[i]], 1u);
+        __syncthreads();
+        order_scan(s_cnt, s_scan, tid);
+#pragma unroll
+        for (int i = 0; i < kOrderPer; ++i)
+            if (bk[i] >= 0) order[first + atomicAdd(&s_cnt[bk[i]], 1u)] = first + i * kOrderThreads + tid;
+        return;
+    }
+    for (int32_t t = tid; t < num_tiles; t += kOrderThreads)
+        atomicAdd(&s_cnt[255 - order_bucket(ib[2 * t + 1] - ib[2 * t])], 1u);
+    __syncthreads();
+    order_scan(s_cnt, s_scan, tid);
     for (int32_t t = tid; t < num_tiles; t += kOrderThreads) {
         const uint32_t at = atomicAdd(&s_cnt[255 - order_bucket(ib[2 * t + 1] - ib[2 * t])], 1u);
         order[first + at] = first + t;

@@ -93,9 +93,9 @@ int DeviceScratch::ensure_base() {
     if (tickets) return 0;
     int rc = dev_alloc(&tickets, kNumTickets, true);
     if (!rc) rc = dev_alloc(&hist, kMaxPasses * 256, true);
-    if (!rc) rc = dev_alloc(&scan_status, 4096, true);
+    if (!rc) rc = dev_alloc(&chunk_sums, 4096, true);
     if (rc) return rc;
-    scan_status_cap = 4096;
+    chunk_sums_cap = 4096;
     void* h = nullptr;
     if (hipHostMalloc(&h, sizeof(int32_t), hipHostMallocDefault) != hipSuccess)
         return fail(kErrAlloc, "pinned readback allocation failed");
@@ -105,17 +105,17 @@ int DeviceScratch::ensure_base() {
     return 0;
 }
 
-int DeviceScratch::grow_scan_status(int64_t blocks) {
-    if (blocks <= scan_status_cap) return 0;
+int DeviceScratch::grow_chunk_sums(int64_t blocks) {
+    if (blocks <= chunk_sums_cap) return 0;
     (void)hipDeviceSynchronize();
-    dev_free(&scan_status);
+    dev_free(&chunk_sums);
     int64_t cap = (int64_t)(blocks * 1.25) + 1;
-    int rc = dev_alloc(&scan_status, cap, true);
+    int rc = dev_alloc(&chunk_sums, cap, true);
     if (rc) {
-        scan_status_cap = 0;
+        chunk_sums_cap = 0;
         return rc;
     }
-    scan_status_cap = cap;
+    chunk_sums_cap = cap;
     return 0;
 }
 
@@ -265,8 +265,8 @@ void DeviceScratch::release() {
     mm_cap = 0;
     dev_free(&mm_partial);
     mm_partial_cap = 0;
-    dev_free(&scan_status);
-    scan_status_cap = 0;
+    dev_free(&chunk_sums);
+    chunk_sums_cap = 0;
     dev_free(&tickets);
     dev_free(&hist);
     if (pinned_count) (void)hipHostFree(pinned_count);

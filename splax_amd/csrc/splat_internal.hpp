@@ -1,5 +1,5 @@
 // Internal interfaces of the gfx950 splat library: argument bundles, the per-device scratch
-// cache, error codes and device-side scan / look-back helpers shared by the kernels.
+// cache, error codes and device-side scan helpers shared by the kernels.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -103,9 +103,8 @@ enum : int {
 struct DeviceScratch {
     int device = -1;
     std::mutex mu;
-    uint32_t epoch = 0;
     // projection scan
-    uint64_t* scan_status = nullptr; int64_t scan_status_cap = 0;
+    uint32_t* chunk_sums = nullptr; int64_t chunk_sums_cap = 0;  // projection scan partials
     uint32_t* tickets = nullptr;
     // sort
     int32_t* keys[2] = {nullptr, nullptr};   // packed 32-bit keys (ping-pong)
@@ -128,13 +127,8 @@ struct DeviceScratch {
     int32_t* pinned_count = nullptr;
     hipEvent_t count_event = nullptr;
 
-    uint32_t next_epoch() {
-        ++epoch;
-        if (epoch == 0) epoch = 1;
-        return epoch;
-    }
     int ensure_base();
-    int grow_scan_status(int64_t blocks);
+    int grow_chunk_sums(int64_t blocks);
     int ensure_sort(int64_t M, int64_t bins, int32_t B, bool wide);
     int ensure_rgrad(int64_t count);
     int ensure_recs(int64_t items);
@@ -231,77 +225,6 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
                      hipStream_t stream);
 
 // ------------------------------------------------------------------ device helpers
-
-template <typename T>
-__device__ __forceinline__ void atomic_store_relaxed(T* p, T v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <typename T>
-__device__ __forceinline__ T atomic_load_relaxed(const T* p) {
-    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Status words of the decoupled look-back: bits 63..32 epoch of the launch that wrote them,
-// bit 31 set when the value is an inclusive prefix (else the chunk's own aggregate),
-// bits 30..0 the value. A word from another launch has a different epoch and reads as "not yet
-// published", so the arrays never need clearing between launches.
-constexpr uint64_t kInclusiveBit = 0x80000000ull;
-
-__device__ __forceinline__ uint64_t status_word(uint32_t epoch, bool inclusive, uint32_t v) {
-    return ((uint64_t)epoch << 32) | (inclusive ? kInclusiveBit : 0ull) | (uint64_t)v;
-}
-
-// Every spin-wait is bounded: a predecessor that has not published after this many polls means
-// a broken invariant (never expected); the waiter records it in the device error word and
-// proceeds, so the kernel always terminates. splat_check_device() reports the word.
-constexpr uint32_t kSpinLimit = 1u << 22;
-enum : uint32_t { kDevErrLookback = 1u };
-
-// Single-value decoupled look-back run by one whole wave (all 64 lanes call it; the result is
-// wave-uniform). Publishes this chunk's aggregate, then polls 64 predecessors per round trip
-// (lane l reads chunk j - l): the run of published words nearest to the chunk is folded in, up to
-// and including the first inclusive prefix; a gap means a predecessor has not published yet, so
-// the wave waits and re-polls from the gap. Publishes its own inclusive prefix and returns the
-// exclusive one. Chunk indices are workgroup indices; a chunk only waits on lower indices, which
-// in-order workgroup dispatch has already placed on the device.
-__device__ __forceinline__ uint32_t lookback_wave(uint64_t* status, uint32_t part, uint32_t agg,
-                                                  uint32_t epoch, uint32_t* err) {
-    const int lane = threadIdx.x & 63;
-    if (part == 0) {
-        if (lane == 0) atomic_store_relaxed(status, status_word(epoch, true, agg));
-        return 0;
-    }
-    if (lane == 0) atomic_store_relaxed(status + part, status_word(epoch, false, agg));
-    uint32_t prefix = 0, spins = 0;
-    int64_t j = (int64_t)part - 1;
-    for (;;) {
-        const int64_t q = j - lane;
-        // positions before chunk 0 read as an inclusive prefix of 0, so every walk ends there
-        const uint64_t w = q >= 0 ? atomic_load_relaxed(status + q) : status_word(epoch, true, 0u);
-        const bool valid = (uint32_t)(w >> 32) == epoch;
-        const uint64_t invalid = __ballot(!valid);
-        const uint64_t incl = __ballot(valid && (w & kInclusiveBit) != 0);
-        const int first_gap = invalid ? __builtin_ctzll(invalid) : 64;
-        const int first_incl = incl ? __builtin_ctzll(incl) : 64;
-        const bool done = first_incl < first_gap;
-        const int take = done ? first_incl + 1 : first_gap;  // lanes [0, take) are folded in
-        uint32_t v = lane < take ? (uint32_t)(w & 0x7fffffffull) : 0u;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-        prefix += v;
-        if (done) break;
-        if (take == 0) {
-            if (++spins >= kSpinLimit) {
-                if (lane == 0) atomicOr(err, kDevErrLookback);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        j -= take;
-    }
-    if (lane == 0) atomic_store_relaxed(status + part, status_word(epoch, true, prefix + agg));
-    return prefix;
-}
 
 __device__ __forceinline__ int32_t wave_inclusive_scan_i32(int32_t v, int lane) {
 #pragma unroll

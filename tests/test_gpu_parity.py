@@ -26,7 +26,7 @@ def _device_healthy():
     yield
     from splax_amd import _lib
 
-    assert _lib.check_device() == 0, "a device-side invariant failed (look-back timeout)"
+    assert _lib.check_device() == 0, "a device-side invariant failed"
 
 
 def _t(a, dtype=None):
