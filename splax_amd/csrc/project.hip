@@ -246,8 +246,20 @@ __global__ void __launch_bounds__(kChunkScanThreads) chunk_scan_kernel(uint32_t*
     const int64_t per = (chunks + kChunkScanThreads - 1) / kChunkScanThreads;
     const int64_t lo = (int64_t)tid * per;
     const int64_t hi = lo + per < chunks ? lo + per : chunks;
+    // runs of up to kChunkScanPer chunks (up to 64Ki chunks, 16.7M items) are loaded into
+    // registers at once, so their load latencies overlap; longer runs take a sequential loop
+    constexpr int kChunkScanPer = 64;
+    const bool in_regs = per <= kChunkScanPer;
+    uint32_t v[kChunkScanPer];
     uint32_t total = 0;
-    for (int64_t c = lo; c < hi; ++c) total += sums[c];
+    if (in_regs) {
+#pragma unroll
+        for (int k = 0; k < kChunkScanPer; ++k) v[k] = lo + k < hi ? sums[lo + k] : 0u;
+#pragma unroll
+        for (int k = 0; k < kChunkScanPer; ++k) total += v[k];
+    } else {
+        for (int64_t c = lo; c < hi; ++c) total += sums[c];
+    }
     s_run[tid] = total;
     __syncthreads();
     // Hillis-Steele inclusive scan of the run totals
@@ -258,10 +270,18 @@ __global__ void __launch_bounds__(kChunkScanThreads) chunk_scan_kernel(uint32_t*
         __syncthreads();
     }
     uint32_t run = s_run[tid] - total;
-    for (int64_t c = lo; c < hi; ++c) {
-        const uint32_t v = sums[c];
-        sums[c] = run;
-        run += v;
+    if (in_regs) {
+#pragma unroll
+        for (int k = 0; k < kChunkScanPer; ++k) {
+            if (lo + k < hi) sums[lo + k] = run;
+            run += v[k];
+        }
+    } else {
+        for (int64_t c = lo; c < hi; ++c) {
+            const uint32_t x = sums[c];
+            sums[c] = run;
+            run += x;
+        }
     }
 }
 
