@@ -843,7 +843,9 @@ void oracle_blend_fwd(const float* colors, int64_t rows_colors, const float* opa
                     float sigma = blend_sigma(conics + 3 * g, dx, dy);
                     float op = opacities[g % rows_opac];
                     float alpha = fminw(ALPHA_MAX, op * oracle_blend_expf(-sigma));
-                    if (sigma < 0.0f || sigma > BLEND_SIGMA_CAP || alpha < ALPHA_THRESHOLD) {
+                    /* !(alpha >= threshold): a NaN opacity is rejected, as the GPU's pack
+                     * culls such records */
+                    if (sigma < 0.0f || sigma > BLEND_SIGMA_CAP || !(alpha >= ALPHA_THRESHOLD)) {
                         ++pr;
                         continue;
                     }
@@ -975,7 +977,7 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
                         float vis = oracle_blend_expf(-sigma);
                         float op = opacities[g % rows_opac];
                         float alpha = fminw(ALPHA_MAX, op * vis);
-                        if (alpha < ALPHA_THRESHOLD) {
+                        if (!(alpha >= ALPHA_THRESHOLD)) {
                             ++qr;
                             continue;
                         }

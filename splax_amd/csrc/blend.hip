@@ -100,7 +100,7 @@ __global__ void __launch_bounds__(256) pack_records_kernel(PackParams P) {
         if (o > 0.0f) {
             smax = fminf(__logf(o * 255.0f) + 1e-3f, kBlendSigmaCap);
         } else {
-            smax = (o != o) ? kBlendSigmaCap : -__builtin_inff();
+            smax = -__builtin_inff();  // o <= 0 or NaN: no pixel accepts it
         }
         uint32_t mode = kCullKeep;
         float ex = 0.0f, ey = 0.0f;
@@ -329,7 +329,9 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
             // next step, which keeps the loop's control flow in the exec mask. Bitwise: no
             // short-circuit branch around the sigma_max read (NaN sigma fails both).
             if ((sigma >= 0.0f) & (sigma <= r1.z)) {
-                const float alpha = minw(kAlphaMax, r1.y * blend_exp(-sigma));
+                // v_min: no accepted record has a NaN opacity (the pack culls those), so it
+                // equals the reference's compare-and-select minimum here
+                const float alpha = fminf(kAlphaMax, r1.y * blend_exp(-sigma));
                 if (alpha >= kAlphaThresh) {
                     const float next_T = T * (1.0f - alpha);
                     if (next_T <= kTEps) {
@@ -667,7 +669,7 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             // below always sees exact zeros there and no branch is needed.
             const float vis = blend_exp(-sigma);
             const float ov = r1.y * vis;
-            const float alpha_c = minw(kAlphaMax, ov);
+            const float alpha_c = fminf(kAlphaMax, ov);  // as in the forward
             const bool valid = in_range && alpha_c >= kAlphaThresh;
             // a lane outside the accepted set blends alpha = 0 (a select, so whatever vis is):
             // T / (1 - 0) = T and its weight alpha T is zero, so T and the running sum need no
