@@ -1109,11 +1109,17 @@ int oracle_project_bwd(const float* means3d, int64_t rows_means, const float* sc
         float s[3] = {glob_scale * sc[0], glob_scale * sc[1], glob_scale * sc[2]};
         float rz = 1.0f / p[2];
         float rz2 = rz * rz;
-        /* J from the unclamped position (:428-431) */
-        float J[9] = {fx * rz, 0.0f, -fx * p[0] * rz2, 0.0f, fy * rz, -fy * p[1] * rz2,
-                      0.0f, 0.0f, 0.0f};
-        float T[9];
-        mat_mul(J, W, T);
+        /* J = [[j00, 0, j02], [0, j11, j12], [0, 0, 0]] from the unclamped position (:428-431).
+         * The products of this VJP drop every term with a structural zero factor (J's last row;
+         * the last row and column of the 2D covariance cotangent) and keep the others in the full
+         * 3x3 products' order, as the GPU kernel does. */
+        const float j00 = fx * rz, j02 = -fx * p[0] * rz2;
+        const float j11 = fy * rz, j12 = -fy * p[1] * rz2;
+        float T0[3], T1[3]; /* rows 0 and 1 of T = J W (row 2 is zero) */
+        for (int b = 0; b < 3; ++b) {
+            T0[b] = j00 * W[b] + j02 * W[6 + b];
+            T1[b] = j11 * W[3 + b] + j12 * W[6 + b];
+        }
         /* S = X G X, vcov2d (:434-439) */
         const float* cn = conics + 3 * c_idx;
         const float* vc = v_conic_in + 3 * vc_idx;
@@ -1135,15 +1141,33 @@ int oracle_project_bwd(const float* means3d, int64_t rows_means, const float* sc
         float vvx = vpx * rw, vvy = vpy * rw;
         float vvz = -(vpx * tx + vpy * ty) * rw * rw;
         vvz = vvz + v_depth_in[vd_idx];
-        float v_cov[9] = {vcov[0], 0.5f * vcov[1], 0.0f, 0.5f * vcov[1], vcov[2], 0.0f,
-                          0.0f, 0.0f, 0.0f};
-        float tmp[9], v_V[9], v_T[9], v_J[9], two_vcov[9];
-        mat_mul_tn(T, v_cov, tmp);
-        mat_mul(tmp, T, v_V);
-        for (int k = 0; k < 9; ++k) two_vcov[k] = 2.0f * v_cov[k];
-        mat_mul(two_vcov, T, tmp);
-        mat_mul(tmp, V, v_T);
-        mat_mul_nt(v_T, W, v_J);
+        /* v_cov = [[c0, c1, 0], [c1, c2, 0], [0, 0, 0]] */
+        const float c0 = vcov[0], c1 = 0.5f * vcov[1], c2 = vcov[2];
+        /* v_V = T^T v_cov T (T^T v_cov has a zero last column) */
+        float tmp0[3], tmp1[3], v_V[9];
+        for (int a = 0; a < 3; ++a) {
+            tmp0[a] = T0[a] * c0 + T1[a] * c1;
+            tmp1[a] = T0[a] * c1 + T1[a] * c2;
+        }
+        for (int a = 0; a < 3; ++a)
+            for (int b = 0; b < 3; ++b) v_V[3 * a + b] = tmp0[a] * T0[b] + tmp1[a] * T1[b];
+        /* v_T = (2 v_cov) T V, rows 0 and 1 (row 2 is zero) */
+        const float d0 = 2.0f * c0, d1 = 2.0f * c1, d2 = 2.0f * c2;
+        float u0[3], u1[3], v_T[6];
+        for (int b = 0; b < 3; ++b) {
+            u0[b] = d0 * T0[b] + d1 * T1[b];
+            u1[b] = d1 * T0[b] + d2 * T1[b];
+        }
+        for (int b = 0; b < 3; ++b) {
+            v_T[b] = (u0[0] * V[b] + u0[1] * V[3 + b]) + u0[2] * V[6 + b];
+            v_T[3 + b] = (u1[0] * V[b] + u1[1] * V[3 + b]) + u1[2] * V[6 + b];
+        }
+        /* v_J = v_T W^T, rows 0 and 1 */
+        float v_J[6];
+        for (int a = 0; a < 2; ++a)
+            for (int b = 0; b < 3; ++b)
+                v_J[3 * a + b] = (v_T[3 * a] * W[3 * b] + v_T[3 * a + 1] * W[3 * b + 1]) +
+                                 v_T[3 * a + 2] * W[3 * b + 2];
         float v_t_x = -fx * prz2 * v_J[2];
         float v_t_y = -fy * prz2 * v_J[5];
         float v_t_z = -fx * prz2 * v_J[0] + 2.0f * fx * tx * prz3 * v_J[2] - fy * prz2 * v_J[4] +
@@ -1196,8 +1220,12 @@ int oracle_project_bwd(const float* means3d, int64_t rows_means, const float* sc
         v_quat[4 * idx + 2] = vq_z;
         v_quat[4 * idx + 3] = vq_w;
         /* _view_vjp (:602-606): v_R = v_p (x) mean + J^T v_T, v_t = v_p */
-        float JtvT[9];
-        mat_mul_tn(J, v_T, JtvT);
+        float JtvT[9]; /* J^T v_T */
+        for (int b = 0; b < 3; ++b) {
+            JtvT[b] = j00 * v_T[b];
+            JtvT[3 + b] = j11 * v_T[3 + b];
+            JtvT[6 + b] = j02 * v_T[b] + j12 * v_T[3 + b];
+        }
         double* vv = vview_loc + 16 * (int64_t)image_id;
         for (int a = 0; a < 3; ++a) {
             for (int b = 0; b < 3; ++b) vv[4 * a + b] += v_p[a] * mean[b] + JtvT[3 * a + b];

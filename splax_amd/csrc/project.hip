@@ -382,10 +382,18 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
             const float fx = P.fx, fy = P.fy;
             float rz = 1.0f / p[2];
             float rz2 = rz * rz;
-            float J[9] = {fx * rz, 0.0f, -fx * p[0] * rz2, 0.0f, fy * rz, -fy * p[1] * rz2,
-                          0.0f, 0.0f, 0.0f};
-            float T[9];
-            mat_mul(J, W, T);
+            // J = [[j00, 0, j02], [0, j11, j12], [0, 0, 0]]. The products of this VJP drop every
+            // term with a structural zero factor (J's last row; the last row and column of the
+            // 2D covariance cotangent) and keep the others in the full products' order; the CPU
+            // oracle evaluates the same expressions.
+            const float j00 = fx * rz, j02 = -fx * p[0] * rz2;
+            const float j11 = fy * rz, j12 = -fy * p[1] * rz2;
+            float T0[3], T1[3];  // rows 0 and 1 of T = J W (row 2 is zero)
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                T0[b] = j00 * W[b] + j02 * W[6 + b];
+                T1[b] = j11 * W[3 + b] + j12 * W[6 + b];
+            }
             const float* cn = P.conics + 3 * c_idx;
             const float* vc = P.v_conic + 3 * vc_idx;
             float X0 = cn[0], X1 = cn[1], X3 = cn[2];
@@ -406,16 +414,40 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
             float vvx = vpx * rw, vvy = vpy * rw;
             float vvz = -(vpx * tx + vpy * ty) * rw * rw;
             vvz = vvz + (P.v_depth ? P.v_depth[vd_idx] : 0.0f);  // NULL: zero cotangent
-            float v_cov[9] = {vcov0, 0.5f * vcov1, 0.0f, 0.5f * vcov1, vcov2, 0.0f,
-                              0.0f, 0.0f, 0.0f};
-            float tmp[9], v_V[9], v_T[9], v_J[9], two_vcov[9];
-            mat_mul_tn(T, v_cov, tmp);
-            mat_mul(tmp, T, v_V);
+            // v_cov = [[c0, c1, 0], [c1, c2, 0], [0, 0, 0]]
+            const float c0 = vcov0, c1 = 0.5f * vcov1, c2 = vcov2;
+            // v_V = T^T v_cov T: tmp = T^T v_cov has a zero last column
+            float tmp0[3], tmp1[3], v_V[9];
 #pragma unroll
-            for (int k = 0; k < 9; ++k) two_vcov[k] = 2.0f * v_cov[k];
-            mat_mul(two_vcov, T, tmp);
-            mat_mul(tmp, V, v_T);
-            mat_mul_nt(v_T, W, v_J);
+            for (int a = 0; a < 3; ++a) {
+                tmp0[a] = T0[a] * c0 + T1[a] * c1;
+                tmp1[a] = T0[a] * c1 + T1[a] * c2;
+            }
+#pragma unroll
+            for (int a = 0; a < 3; ++a)
+#pragma unroll
+                for (int b = 0; b < 3; ++b) v_V[3 * a + b] = tmp0[a] * T0[b] + tmp1[a] * T1[b];
+            // v_T = (2 v_cov) T V: rows 0 and 1 (row 2 is zero)
+            const float d0 = 2.0f * c0, d1 = 2.0f * c1, d2 = 2.0f * c2;
+            float u0[3], u1[3], v_T[6];
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                u0[b] = d0 * T0[b] + d1 * T1[b];
+                u1[b] = d1 * T0[b] + d2 * T1[b];
+            }
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                v_T[b] = (u0[0] * V[b] + u0[1] * V[3 + b]) + u0[2] * V[6 + b];
+                v_T[3 + b] = (u1[0] * V[b] + u1[1] * V[3 + b]) + u1[2] * V[6 + b];
+            }
+            // v_J = v_T W^T, rows 0 and 1
+            float v_J[6];
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 3; ++b)
+                    v_J[3 * a + b] = (v_T[3 * a] * W[3 * b] + v_T[3 * a + 1] * W[3 * b + 1]) +
+                                     v_T[3 * a + 2] * W[3 * b + 2];
             float v_t_x = -fx * prz2 * v_J[2];
             float v_t_y = -fy * prz2 * v_J[5];
             float v_t_z = -fx * prz2 * v_J[0] + 2.0f * fx * tx * prz3 * v_J[2] -
@@ -469,8 +501,13 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
             vq[2] = 2.0f * (((x * (r[6] + r[2]) + y * (r[7] + r[5])) -
                              2.0f * z * (r[0] + r[4])) + w * (r[3] - r[1]));
             // _view_vjp: v_R = v_p (x) mean + J^T v_T, v_t = v_p
-            float JtvT[9];
-            mat_mul_tn(J, v_T, JtvT);
+            float JtvT[9];  // J^T v_T
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                JtvT[b] = j00 * v_T[b];
+                JtvT[3 + b] = j11 * v_T[3 + b];
+                JtvT[6 + b] = j02 * v_T[b] + j12 * v_T[3 + b];
+            }
 #pragma unroll
             for (int a = 0; a < 3; ++a) {
 #pragma unroll
