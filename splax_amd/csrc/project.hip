@@ -2,7 +2,7 @@
 // backward, gfx950.
 //
 // project_fwd: one thread per flat item (image b, gaussian g), restating _project_kernel
-// (splax/_project/_kernels.py:122-248). Each workgroup owns a contiguous chunk of 256 items;
+// (splax/_project/_kernels.py:122-248). Each workgroup owns a contiguous chunk of 1024 items;
 // after counting tiles it scans its chunk in LDS, writes the chunk-local inclusive prefix to
 // cum_tiles_hit and the chunk's total to a partials array. One workgroup then scans the
 // partials, and a last pass adds each chunk's offset, which gives the global inclusive scan the
@@ -37,6 +37,9 @@ struct ProjectParams {
 };
 
 constexpr int kProjThreads = 256;
+// Items per chunk of the projection's tile-count scan (one forward workgroup each): 1024 keeps the
+// chunk-total scan short (about 12 totals per scan thread at 12M items).
+constexpr int kProjFwdThreads = 1024;
 
 __device__ __forceinline__ bool apply_transform(const float* transforms, int32_t image_id,
                                                 int32_t num_transforms, bool sel_tf,
@@ -198,11 +201,11 @@ __device__ __forceinline__ int32_t project_item(const ProjectParams& P, int64_t 
 // waves in flight.
 constexpr int kProjItems = 1;
 
-__global__ void __launch_bounds__(kProjThreads) project_fwd_kernel(ProjectParams P) {
-    __shared__ int32_t s_wave[kProjThreads / 64];
+__global__ void __launch_bounds__(kProjFwdThreads) project_fwd_kernel(ProjectParams P) {
+    __shared__ int32_t s_wave[kProjFwdThreads / 64];
     const int tid = threadIdx.x;
     const uint32_t part = blockIdx.x;
-    const int64_t base = (int64_t)part * (kProjThreads * kProjItems);
+    const int64_t base = (int64_t)part * (kProjFwdThreads * kProjItems);
     // Items are blocked per thread (thread t owns base + t*K .. +K-1) so the per-thread running
     // sum plus one block scan gives the inclusive prefix.
     int32_t cnt[kProjItems];
@@ -220,7 +223,7 @@ __global__ void __launch_bounds__(kProjThreads) project_fwd_kernel(ProjectParams
     __syncthreads();
     int32_t wave_off = 0, block_total = 0;
 #pragma unroll
-    for (int w = 0; w < kProjThreads / 64; ++w) {
+    for (int w = 0; w < kProjFwdThreads / 64; ++w) {
         int32_t v = s_wave[w];
         if (w < wave) wave_off += v;
         block_total += v;
@@ -289,9 +292,9 @@ __global__ void __launch_bounds__(kChunkScanThreads) chunk_scan_kernel(uint32_t*
 // the host reports a negative total as too many intersections. A chunk is one workgroup of the
 // projection, one item per thread.
 static_assert(kProjItems == 1, "chunk_offset_kernel maps one thread to one item");
-__global__ void __launch_bounds__(256) chunk_offset_kernel(int32_t* cum, int64_t total,
+__global__ void __launch_bounds__(kProjFwdThreads) chunk_offset_kernel(int32_t* cum, int64_t total,
                                                            const uint32_t* offsets) {
-    const int64_t idx = (int64_t)(blockIdx.x + 1) * kProjThreads + threadIdx.x;
+    const int64_t idx = (int64_t)(blockIdx.x + 1) * kProjFwdThreads + threadIdx.x;
     if (idx < total) cum[idx] = (int32_t)((uint32_t)cum[idx] + offsets[blockIdx.x + 1]);
 }
 
@@ -617,7 +620,7 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
 
 int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stream) {
     if (a.total <= 0) return 0;
-    const int64_t per_block = (int64_t)kProjThreads * kProjItems;
+    const int64_t per_block = (int64_t)kProjFwdThreads * kProjItems;
     const int64_t blocks = (a.total + per_block - 1) / per_block;
     if (blocks > (int64_t)sc.chunk_sums_cap) {
         int rc = sc.grow_chunk_sums(blocks);
@@ -639,12 +642,12 @@ int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stre
     P.num_tiles_hit = a.num_tiles_hit; P.cum_tiles_hit = a.cum_tiles_hit;
     P.wxyz = a.quats_wxyz;
     P.chunk_sums = sc.chunk_sums;
-    hipLaunchKernelGGL(project_fwd_kernel, dim3((unsigned)blocks), dim3(kProjThreads), 0, stream,
+    hipLaunchKernelGGL(project_fwd_kernel, dim3((unsigned)blocks), dim3(kProjFwdThreads), 0, stream,
                        P);
     if (blocks > 1) {
         hipLaunchKernelGGL(chunk_scan_kernel, dim3(1), dim3(kChunkScanThreads), 0, stream,
                            P.chunk_sums, blocks);
-        hipLaunchKernelGGL(chunk_offset_kernel, dim3((unsigned)(blocks - 1)), dim3(kProjThreads),
+        hipLaunchKernelGGL(chunk_offset_kernel, dim3((unsigned)(blocks - 1)), dim3(kProjFwdThreads),
                            0, stream, P.cum_tiles_hit, a.total, P.chunk_sums);
     }
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;

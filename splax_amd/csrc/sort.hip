@@ -47,11 +47,16 @@ minmax_partial_kernel(const float* depths, const int32_t* radii, int32_t n,
     const int64_t base = (int64_t)image * n + (int64_t)blockIdx.x * (kMmThreads * kMmItems);
     const int64_t end = (int64_t)image * n + n;
     uint32_t lo = 0xffffffffu, hi = 0u;
+    // both arrays are loaded for every item (not the depth behind the radius test), so all the
+    // loads of a thread are in flight together
 #pragma unroll
     for (int k = 0; k < kMmItems; ++k) {
-        int64_t idx = base + (int64_t)k * kMmThreads + threadIdx.x;
-        if (idx < end && radii[idx] > 0) {
-            uint32_t o = f2ord(depths[idx]);
+        const int64_t idx = base + (int64_t)k * kMmThreads + threadIdx.x;
+        const bool in = idx < end;
+        const int32_t r = in ? radii[idx] : 0;
+        const float d = in ? depths[idx] : 0.0f;
+        if (r > 0) {
+            const uint32_t o = f2ord(d);
             lo = o < lo ? o : lo;
             hi = o > hi ? o : hi;
         }
@@ -442,24 +447,37 @@ __device__ __forceinline__ int32_t key_bin(const void* keys, int64_t i, int32_t 
     }
 }
 
+constexpr int kBinKeys = 4;  // keys per thread of bin_edges_kernel
+
 template <bool kWide>
 __global__ void __launch_bounds__(256)
 bin_edges_kernel(const void* keys, int64_t M, int32_t num_tiles, int32_t tile_bits,
                  int32_t depth_bits, int64_t nbins, int32_t* bins) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= M) return;
-    const int32_t cur = key_bin<kWide>(keys, idx, num_tiles, tile_bits, depth_bits);
-    // keys emitted from consistent inputs always decode inside [0, nbins)
-    if (cur < 0 || cur >= nbins) return;
-    if (idx == 0) {
-        bins[2 * cur] = 0;
-        return;
-    }
-    if (idx == M - 1) bins[2 * cur + 1] = (int32_t)M;
-    const int32_t prev = key_bin<kWide>(keys, idx - 1, num_tiles, tile_bits, depth_bits);
-    if (prev != cur && prev >= 0 && prev < nbins) {
-        bins[2 * prev + 1] = (int32_t)idx;
-        bins[2 * cur] = (int32_t)idx;
+    // kBinKeys consecutive keys and the one before them per thread, all loads issued together
+    const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * kBinKeys;
+    if (i0 >= M) return;
+    int32_t cur[kBinKeys];
+#pragma unroll
+    for (int k = 0; k < kBinKeys; ++k)
+        cur[k] = i0 + k < M ? key_bin<kWide>(keys, i0 + k, num_tiles, tile_bits, depth_bits) : -1;
+    const int32_t before =
+        i0 > 0 ? key_bin<kWide>(keys, i0 - 1, num_tiles, tile_bits, depth_bits) : -1;
+#pragma unroll
+    for (int k = 0; k < kBinKeys; ++k) {
+        const int64_t idx = i0 + k;
+        const int32_t c = cur[k];
+        // keys emitted from consistent inputs always decode inside [0, nbins)
+        if (idx >= M || c < 0 || c >= nbins) continue;
+        if (idx == 0) {
+            bins[2 * c] = 0;
+            continue;
+        }
+        if (idx == M - 1) bins[2 * c + 1] = (int32_t)M;
+        const int32_t prev = k == 0 ? before : cur[k - 1];
+        if (prev != c && prev >= 0 && prev < nbins) {
+            bins[2 * prev + 1] = (int32_t)idx;
+            bins[2 * c] = (int32_t)idx;
+        }
     }
 }
 
@@ -629,7 +647,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     }
     {
         StageTimer tm(stream, kStageBins);
-        const dim3 grid((unsigned)((M + 255) / 256));
+        const dim3 grid((unsigned)((M + 256 * kBinKeys - 1) / (256 * kBinKeys)));
         if (wide)
             hipLaunchKernelGGL(bin_edges_kernel<true>, grid, dim3(256), 0, stream, o.keys, M,
                                L.num_tiles, L.tile_bits, L.depth_bits, nbins, bins);
