@@ -60,7 +60,7 @@ class _RasterizeFn(torch.autograd.Function):
         ctx.num_intersects = kept.M
         ctx.set_materialize_grads(False)  # no zero tensors for the unused Ts / fidx grads
         if depth is None:
-            depth = Ts.new_zeros(())  # placeholder output of the colour-only path
+            depth = Ts.new_empty(())  # placeholder output of the colour-only path (never read)
             ctx.mark_non_differentiable(Ts, fidx, depth)  # one call: it replaces the set
         else:
             ctx.mark_non_differentiable(Ts, fidx)
