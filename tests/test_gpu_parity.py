@@ -138,6 +138,55 @@ def _grad_compare(got, ref, label, rel_tol=1e-5):
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5 * scale, err_msg=label)
 
 
+def test_config2_full_size_matches_oracle():
+    """The bench workload itself (config 2: 1M gaussians, 1920x1080): projection, keys, sorted
+    ids, tile bins, final_Ts / final_idx and the image bit for bit, the blend backward within the
+    gradient bar. The C oracle runs multi-threaded (a few seconds)."""
+    _case("config 2 full size")
+    O.set_threads(16)
+    s = make_scene(2)
+    ref, got = _project_both(s.means, s.scales, s.quats, s.viewmats[0], s.opacities, n=s.n, B=1,
+                             img_shape=s.img_shape, f=s.f, c=s.c)
+    for label, r, g in zip(("xys", "depths", "radii", "conics", "num_tiles_hit", "cum"), ref,
+                           got):
+        assert_bit_exact(g.reshape(r.shape), r, f"config2/{label}")
+    xys, depths, radii, conics, nth, cum = ref
+    rk, rid, rbins = O.sort_and_bin(xys, depths, radii, conics, s.opacities, cum, n=s.n, B=1,
+                                    img_shape=s.img_shape)
+    gk, gid, gbins = _ops.sort_and_bin(_t(xys), _t(depths), _t(radii), _t(conics),
+                                       _t(s.opacities).reshape(-1), _t(cum), n=s.n, B=1,
+                                       img_shape=s.img_shape)
+    torch.cuda.synchronize()
+    assert_bit_exact(_np(gk), rk, "config2/keys")
+    assert_bit_exact(_np(gid), rid, "config2/ids")
+    assert_bit_exact(_np(gbins), rbins, "config2/bins")
+    rimg, rT, ridx, _, M = O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background, xys,
+                                           depths, radii, conics, cum, n=s.n, B=1,
+                                           img_shape=s.img_shape)
+    gimg, gT, gidx, gM = _ops.rasterize_fwd(
+        _t(s.colors), _t(s.opacities).reshape(-1), _t(s.opacities).reshape(-1),
+        _t(s.background), _t(xys), _t(depths), _t(radii), _t(conics), _t(cum), n=s.n, B=1,
+        img_shape=s.img_shape)
+    torch.cuda.synchronize()
+    assert gM == M == 2_660_700
+    assert_bit_exact(_np(gT), rT, "config2/final_Ts")
+    assert_bit_exact(_np(gidx), ridx, "config2/final_idx")
+    assert_bit_exact(_np(gimg), rimg, "config2/img")
+    H, W = s.img_shape
+    vout = (2.0 * (rimg.reshape(H, W, 3) - s.targets[0]) / rimg.size).astype(np.float32)
+    rg = O.rasterize_bwd(s.colors, s.opacities, s.opacities, s.background, xys, depths, radii,
+                         conics, cum, rT, ridx, vout, n=s.n, B_out=1, B_geom=1,
+                         img_shape=s.img_shape)
+    gg = _ops.rasterize_bwd(_t(s.colors), _t(s.opacities).reshape(-1),
+                            _t(s.opacities).reshape(-1), _t(s.background), _t(xys), _t(depths),
+                            _t(radii), _t(conics), _t(cum), _t(rT), _t(ridx),
+                            _t(vout).reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
+                            img_shape=s.img_shape)
+    torch.cuda.synchronize()
+    for label, g, r in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), gg, rg[:4]):
+        _grad_compare(_np(g).reshape(r.shape), r, f"config2/{label}")
+
+
 @pytest.mark.parametrize("name", list(CASES))
 def test_rasterize_bwd_matches_oracle(name):
     _case(f"rasterize_bwd {name}")
