@@ -135,7 +135,10 @@ int splat_rasterize_depth_bwd(splat_stream_t stream, const float* colors, int64_
  * out_depth (may be NULL) selects the depth channel as in splat_rasterize_depth_fwd. records
  * (may be NULL) receives the packed blend record of every geometry item, 16 floats per item
  * ([B*num_gaussians, 16], 16-byte aligned), for splat_rasterize_bwd_sorted; it is written only
- * when M > 0. compensate != 0 selects the antialiased blend of splax.render (splax/_render.py:
+ * when M > 0. tile_order (may be NULL) receives the order in which the blend dispatched the
+ * image tiles ([B*num_tiles] int32, a permutation of the tile indices, heaviest first within each
+ * image) for splat_rasterize_bwd_sorted. compensate != 0 selects the antialiased blend of
+ * splax.render (splax/_render.py:
  * 105-110): opacities are then the raw opacities, the blend uses opacities * rho(conic) with
  * rho = sqrt(clip(1 - 0.3 (a + c) + 0.09 (a c - b^2), 0, 1)) (splax/_project/_project.py:95-117),
  * and the intersection uses map_opacities as always. Other arguments and outputs as
@@ -149,12 +152,15 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
                              int32_t img_h, int32_t img_w, int64_t capacity, float* final_Ts,
                              int32_t* final_idx, float* out_img, float* out_depth,
                              int32_t* sorted_ids, int32_t* sorted_pos, int32_t* tile_bins,
-                             float* records, int64_t* num_intersects, int32_t compensate);
+                             float* records, int32_t* tile_order, int64_t* num_intersects,
+                             int32_t compensate);
 
 /* Backward over the sorted lists kept by splat_rasterize_fwd_keep (no re-sort). Arguments as
- * splat_rasterize_bwd plus sorted_ids / sorted_pos / tile_bins / records / num_intersects of
- * the matching forward (records may be NULL: the backward then packs them again from its
- * inputs, which must be the forward's); the outputs equal splat_rasterize_bwd's (same kernels;
+ * splat_rasterize_bwd plus sorted_ids / sorted_pos / tile_bins / records / tile_order /
+ * num_intersects of the matching forward (records may be NULL: the backward then packs them
+ * again from its inputs, which must be the forward's; tile_order may be NULL: the backward then
+ * orders the tiles again, as it also does when B_out != B_geom; the order only schedules the
+ * tiles, the outputs do not depend on it); the outputs equal splat_rasterize_bwd's (same kernels;
  * additions can differ in order only among a tile's four quadrant waves). v_depths (may be NULL)
  * selects the depth channel as in splat_rasterize_depth_bwd (then depths and v_out_depth are
  * read). compensate as in the forward: v_opacity is then the raw opacities' cotangent and
@@ -167,8 +173,8 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
                                const float* depths, const float* conics,
                                const int32_t* cum_tiles_hit, const int32_t* sorted_ids,
                                const int32_t* sorted_pos, const int32_t* tile_bins,
-                               const float* records, int64_t num_intersects,
-                               const float* final_Ts,
+                               const float* records, const int32_t* tile_order,
+                               int64_t num_intersects, const float* final_Ts,
                                const int32_t* final_idx, const float* v_out_img,
                                int64_t vout_rows, const float* v_out_depth, int64_t vdepth_rows,
                                int32_t num_gaussians, int32_t B_out, int32_t B_geom,

@@ -44,8 +44,8 @@ _SIGS = {
     "splat_rasterize_depth_bwd": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_vp, _vp, _vp, _i64]
     + [_vp, _i64] + [_i32] * 5 + [_vp] * 5,
     "splat_rasterize_fwd_keep": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_i32] * 4 + [_i64]
-    + [_vp] * 9 + [_i32],
-    "splat_rasterize_bwd_sorted": [_vp] + [_vp, _i64] * 3 + [_vp] * 8 + [_i64]
+    + [_vp] * 10 + [_i32],
+    "splat_rasterize_bwd_sorted": [_vp] + [_vp, _i64] * 3 + [_vp] * 9 + [_i64]
     + [_vp, _vp, _vp, _i64] + [_vp, _i64] + [_i32] * 5 + [_vp] * 5 + [_i32, _i32],
     "splat_sort_and_bin": [_vp] + [_vp] * 4 + [_vp, _i64, _vp] + [_i32] * 4
     + [_vp, _vp, _i64, _vp, _vp],

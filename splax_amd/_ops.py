@@ -131,13 +131,15 @@ _KEEP_CAPACITY: dict = {}  # per device: capacity estimate for the kept sorted l
 
 class KeptSort(NamedTuple):
     """What rasterize_fwd_keep leaves for rasterize_bwd_sorted: the sorted gaussian ids, their
-    emission positions, the tile bins, the intersection count and the packed blend records
-    ([B*n, 16], or None to have the backward pack them again)."""
+    emission positions, the tile bins, the intersection count, the packed blend records
+    ([B*n, 16], or None to have the backward pack them again) and the blend's tile order
+    ([B*num_tiles], or None to have the backward order the tiles again)."""
     ids: torch.Tensor
     pos: torch.Tensor
     bins: torch.Tensor
     M: int
     records: Optional[torch.Tensor]
+    order: Optional[torch.Tensor] = None
 
 
 def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, conics, cum, *, n,
@@ -162,6 +164,7 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
     depth = torch.empty((B * H, W), device=dev, dtype=torch.float32) if render_depth else None
     bins = torch.empty((B * tiles, 2), device=dev, dtype=torch.int32)
     recs = torch.empty((xys.shape[0], 16), device=dev, dtype=torch.float32)
+    order = torch.empty((B * tiles,), device=dev, dtype=torch.int32)
     key = str(dev)
     cap = _KEEP_CAPACITY.get(key, 0)
     m = ctypes.c_int64(0)
@@ -174,7 +177,8 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
                 _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
                 p(map_opac), map_opac.numel(), p(background), rows(background, 3), p(xys),
                 p(depths), p(radii), p(conics), p(cum), n, B, H, W, cap, p(Ts), p(fidx), p(img),
-                p(depth), p(ids), p(pos), p(bins), p(recs), ctypes.byref(m), int(compensate))
+                p(depth), p(ids), p(pos), p(bins), p(recs), p(order), ctypes.byref(m),
+                int(compensate))
         if st == _lib.ERR_TOO_MANY and m.value > cap:
             cap = int(m.value * 1.25) + 1
             _KEEP_CAPACITY[key] = cap
@@ -184,7 +188,7 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
     M = int(m.value)
     if M > _KEEP_CAPACITY.get(key, 0):
         _KEEP_CAPACITY[key] = int(M * 1.25) + 1
-    return img, Ts, fidx, KeptSort(ids, pos, bins, M, recs), depth
+    return img, Ts, fidx, KeptSort(ids, pos, bins, M, recs, order), depth
 
 
 def _bwd_outputs(nout, dev, with_depth):
@@ -203,6 +207,9 @@ def rasterize_bwd_sorted(colors, opac, background, xys, depths, conics, cum, kep
     recs = None if kept.records is None else _f32(kept.records)
     if recs is not None and recs.shape != (xys.shape[0], 16):
         raise ValueError(f"records must be [{xys.shape[0]}, 16], got {tuple(recs.shape)}")
+    order = None if kept.order is None else _i32(kept.order)
+    if order is not None and order.numel() != bins.shape[0]:
+        raise ValueError(f"tile order must have {bins.shape[0]} entries, got {order.numel()}")
     cum, final_idx = _i32(cum), _i32(final_idx)
     vd = None if v_out_depth is None else _f32(v_out_depth)
     dev = _lib.require_gpu(colors, opac, xys, conics, cum, ids, pos, bins, final_Ts, final_idx,
@@ -216,7 +223,7 @@ def rasterize_bwd_sorted(colors, opac, background, xys, depths, conics, cum, kep
         st = _lib.lib().splat_rasterize_bwd_sorted(
             _lib.stream_handle(dev), p(colors), rows(colors, 3), p(opac), opac.numel(),
             p(background), rows(background, 3), p(xys), p(depths), p(conics), p(cum), p(ids),
-            p(pos), p(bins), p(recs), M, p(final_Ts), p(final_idx), p(v_out),
+            p(pos), p(bins), p(recs), p(order), M, p(final_Ts), p(final_idx), p(v_out),
             v_out.numel() // (3 * W),
             p(vd), 0 if vd is None else vd.numel() // W, n, B_out, B_geom, H, W, p(v_colors),
             p(v_opac), p(v_xy), p(v_conic), p(v_depths), int(compensate), int(fold))

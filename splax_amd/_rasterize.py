@@ -55,7 +55,7 @@ class _RasterizeFn(torch.autograd.Function):
             conics.reshape(-1, 3), cum.reshape(-1), n=n, B=B, img_shape=img_shape,
             render_depth=render_depth, compensate=compensate)
         ctx.save_for_backward(colors, opac, background, xys, depths, conics, cum, Ts, fidx,
-                              kept.ids, kept.pos, kept.bins, kept.records)
+                              kept.ids, kept.pos, kept.bins, kept.records, kept.order)
         ctx.statics = statics
         ctx.num_intersects = kept.M
         ctx.set_materialize_grads(False)  # no zero tensors for the unused Ts / fidx grads
@@ -68,8 +68,8 @@ class _RasterizeFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, v_img, v_depth, _v_Ts, _v_idx):
-        colors, opac, background, xys, depths, conics, cum, Ts, fidx, ids, pos, bins, recs = \
-            ctx.saved_tensors
+        (colors, opac, background, xys, depths, conics, cum, Ts, fidx, ids, pos, bins, recs,
+         order) = ctx.saved_tensors
         n, B, img_shape, render_depth, compensate = ctx.statics
         H, W = img_shape
         if v_img is None:
@@ -80,7 +80,7 @@ class _RasterizeFn(torch.autograd.Function):
         grads = _ops.rasterize_bwd_sorted(
             colors.reshape(-1, 3), opac.reshape(-1), background.reshape(-1, 3),
             xys.reshape(-1, 2), depths.reshape(-1), conics.reshape(-1, 3), cum.reshape(-1),
-            _ops.KeptSort(ids, pos, bins, ctx.num_intersects, recs), Ts, fidx,
+            _ops.KeptSort(ids, pos, bins, ctx.num_intersects, recs, order), Ts, fidx,
             v_img.reshape(-1, 3), n=n, B_out=B,
             B_geom=B, img_shape=img_shape,
             v_out_depth=v_depth.reshape(-1, W) if render_depth else None, compensate=compensate,

@@ -838,18 +838,24 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
 
 int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, const BlendBwdArgs& a, int32_t* order,
-                     hipStream_t stream) {
+                     const int32_t* kept_order, hipStream_t stream) {
     const int64_t nout = (int64_t)a.B_out * in.n;
     const int32_t sel_geom = in.B_geom > 1;
     const int64_t blocks = (int64_t)a.B_out * lay.num_tiles;
     const bool depth = a.v_depths != nullptr;
     if (blocks > 0 && sorted_ids != nullptr && a.M > 0) {
-        const int rc = launch_tile_order(tile_bins, blocks, lay.num_tiles, sel_geom, order, stream);
-        if (rc) return rc;
+        // the forward's order covers its B_geom images; shared geometry with B_out > 1 orders
+        // each output image by image 0's bins here
+        const bool reuse = kept_order != nullptr && a.B_out == in.B_geom;
+        if (!reuse) {
+            const int rc =
+                launch_tile_order(tile_bins, blocks, lay.num_tiles, sel_geom, order, stream);
+            if (rc) return rc;
+        }
         BlendBwdParams P;
         fill_common(P.c, in, lay, sorted_ids, tile_bins);
         P.c.recs = a.recs;
-        P.c.order = order;
+        P.c.order = reuse ? kept_order : order;
         P.final_Ts = a.final_Ts; P.final_idx = a.final_idx;
         P.v_out = a.v_out; P.vout_rows = a.vout_rows;
         P.n = in.n; P.sel_geom = sel_geom;

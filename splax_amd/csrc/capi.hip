@@ -342,7 +342,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 10; }
+int splat_abi_version(void) { return 11; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();
@@ -594,11 +594,12 @@ static RasterInputs raster_inputs(const float* colors, int64_t rows_colors,
 
 // Forward: sort_and_bin into the library scratch or the caller's kept lists (tgt), then the
 // blend; out_depth non-null adds the expected-depth channel.
-// records: caller buffer for the packed blend records (kept for the backward), or null for
-// library scratch.
+// records / order: caller buffers for the packed blend records and the tile dispatch order
+// (kept for the backward), or null for library scratch.
 static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortTargets* tgt,
                               float* final_Ts, int32_t* final_idx, float* out_img,
-                              float* out_depth, float* records, int64_t* num_intersects) {
+                              float* out_depth, float* records, int32_t* order,
+                              int64_t* num_intersects) {
     int rc = check_raster(in, in.B_geom);
     if (rc) return rc;
     if (out_depth && !in.depths) return fail(kErrArgs, "rasterize: depth channel needs depths");
@@ -624,22 +625,25 @@ static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortT
         if (rc) return rc;
         recs = sc.recs;
     }
-    rc = sc.ensure_order((int64_t)in.B_geom * L.num_tiles);
-    if (rc) return rc;
+    if (!order) {
+        rc = sc.ensure_order((int64_t)in.B_geom * L.num_tiles);
+        if (rc) return rc;
+        order = sc.tile_order;
+    }
     StageTimer tm(s, kStageBlendFwd);
     if (M > 0) rc = launch_pack_records(in, recs, s);
     if (!rc)
         rc = launch_blend_fwd(in, L, M > 0 ? ids : nullptr, bins, final_Ts, final_idx, out_img,
-                              out_depth, recs, sc.tile_order, s);
+                              out_depth, recs, order, s);
     if (rc) return fail(rc, "blend_fwd launch failed");
     return 0;
 }
 
-// Sorted lists (and, when non-null, the packed records) kept from the forward
-// (splat_rasterize_fwd_keep).
+// Sorted lists (and, when non-null, the packed records and the tile order) kept from the
+// forward (splat_rasterize_fwd_keep).
 struct KeptLists {
     const int32_t* ids; const int32_t* pos; const int32_t* bins; int64_t M;
-    const float* records;
+    const float* records; const int32_t* order;
 };
 
 // Backward over kept sorted lists or, with kept == nullptr, over a fresh sort_and_bin.
@@ -699,7 +703,8 @@ static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptL
         recs = sc.recs;
     }
     a.recs = recs;
-    rc = launch_blend_bwd(in, L, M > 0 ? ids : nullptr, bins, a, sc.tile_order, s);
+    rc = launch_blend_bwd(in, L, M > 0 ? ids : nullptr, bins, a, sc.tile_order,
+                          kept ? kept->order : nullptr, s);
     if (rc) return fail(rc, "blend_bwd launch failed");
     return 0;
 }
@@ -730,7 +735,7 @@ int splat_rasterize_fwd(splat_stream_t stream, const float* colors, int64_t rows
                                           depths, radii, conics, cum_tiles_hit, num_gaussians, B,
                                           img_h, img_w);
     return rasterize_fwd_impl(static_cast<hipStream_t>(stream), in, nullptr, final_Ts,
-                              final_idx, out_img, nullptr, nullptr, num_intersects);
+                              final_idx, out_img, nullptr, nullptr, nullptr, num_intersects);
 }
 
 int splat_rasterize_depth_fwd(splat_stream_t stream, const float* colors, int64_t rows_colors,
@@ -747,7 +752,7 @@ int splat_rasterize_depth_fwd(splat_stream_t stream, const float* colors, int64_
                                           depths, radii, conics, cum_tiles_hit, num_gaussians, B,
                                           img_h, img_w);
     return rasterize_fwd_impl(static_cast<hipStream_t>(stream), in, nullptr, final_Ts,
-                              final_idx, out_img, out_depth, nullptr, num_intersects);
+                              final_idx, out_img, out_depth, nullptr, nullptr, num_intersects);
 }
 
 int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t rows_colors,
@@ -759,7 +764,8 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
                              int32_t img_h, int32_t img_w, int64_t capacity, float* final_Ts,
                              int32_t* final_idx, float* out_img, float* out_depth,
                              int32_t* sorted_ids, int32_t* sorted_pos, int32_t* tile_bins,
-                             float* records, int64_t* num_intersects, int32_t compensate) {
+                             float* records, int32_t* tile_order, int64_t* num_intersects,
+                             int32_t compensate) {
     if (capacity < 0 || !tile_bins || (capacity > 0 && (!sorted_ids || !sorted_pos)))
         return fail(kErrArgs, "rasterize_fwd_keep: missing sorted-list buffers");
     const RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac,
@@ -774,7 +780,7 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
     tgt.pos = sorted_pos;
     tgt.bins = tile_bins;
     return rasterize_fwd_impl(static_cast<hipStream_t>(stream), inc, &tgt, final_Ts, final_idx,
-                              out_img, out_depth, records, num_intersects);
+                              out_img, out_depth, records, tile_order, num_intersects);
 }
 
 int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64_t rows_colors,
@@ -783,8 +789,8 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
                                const float* depths, const float* conics,
                                const int32_t* cum_tiles_hit, const int32_t* sorted_ids,
                                const int32_t* sorted_pos, const int32_t* tile_bins,
-                               const float* records, int64_t num_intersects,
-                               const float* final_Ts,
+                               const float* records, const int32_t* tile_order,
+                               int64_t num_intersects, const float* final_Ts,
                                const int32_t* final_idx, const float* v_out_img,
                                int64_t vout_rows, const float* v_out_depth, int64_t vdepth_rows,
                                int32_t num_gaussians, int32_t B_out, int32_t B_geom,
@@ -803,7 +809,7 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
     BlendBwdArgs a = bwd_args(final_Ts, final_idx, v_out_img, vout_rows, B_out, v_colors,
                               v_opacity, v_xy, v_conic, v_out_depth, vdepth_rows, v_depths);
     a.fold = fold_shared != 0;
-    const KeptLists kept{sorted_ids, sorted_pos, tile_bins, num_intersects, records};
+    const KeptLists kept{sorted_ids, sorted_pos, tile_bins, num_intersects, records, tile_order};
     return rasterize_bwd_impl(static_cast<hipStream_t>(stream), in, &kept, a);
 }
 

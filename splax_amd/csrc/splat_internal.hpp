@@ -200,7 +200,8 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
 int launch_pack_records(const RasterInputs& in, float4* recs, hipStream_t stream);
 
 // out_depth non-null: also the expected-depth channel (in.depths per geometry item). recs holds
-// the records written by launch_pack_records for the same inputs.
+// the records written by launch_pack_records for the same inputs. order (in.B_geom * num_tiles)
+// receives the tile dispatch order the blend runs in.
 int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,
                      float* out_img, float* out_depth, const float4* recs, int32_t* order,
@@ -220,9 +221,11 @@ struct BlendBwdArgs {
     const float4* recs = nullptr;  // launch_pack_records output for the same inputs
     int32_t fold = 0;  // v_colors / v_opacity summed over the B_out images (n rows)
 };
+// order: scratch of B_out * num_tiles for the tile dispatch order; kept_order (may be null) is the
+// order a forward over the same bins wrote, used instead when B_out == in.B_geom.
 int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, const BlendBwdArgs& a, int32_t* order,
-                     hipStream_t stream);
+                     const int32_t* kept_order, hipStream_t stream);
 
 // ------------------------------------------------------------------ device helpers
 

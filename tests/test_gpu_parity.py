@@ -433,7 +433,7 @@ def test_kept_sort_path_equals_resort_path(name):
     geo = (_t(xys), _t(depths), _t(radii), _t(conics), _t(cum))
     img, Ts, fidx, kept, _ = _ops.rasterize_fwd_keep(
         _t(s.colors), o, o, _t(s.background), *geo, n=s.n, B=1, img_shape=s.img_shape)
-    ids, pos, bins, M, recs = kept
+    ids, pos, bins, M, recs, order = kept
     rk, rid, rbins = O.sort_and_bin(xys, depths, radii, conics, s.opacities, cum, n=s.n, B=1,
                                     img_shape=s.img_shape)
     assert M == rid.size
@@ -444,6 +444,14 @@ def test_kept_sort_path_equals_resort_path(name):
     want_pos = np.argsort(ekeys, kind="stable").astype(np.int32)
     assert_bit_exact(_np(pos)[:M], want_pos, f"{name}/kept emission positions")
     assert_bit_exact(eids[want_pos], rid, f"{name}/owner of each sorted position")
+    # the blend's tile order: a permutation of the tiles, longest lists first up to the 9/8
+    # width of its count buckets (exact below 8)
+    ordr = _np(order)
+    assert np.array_equal(np.sort(ordr), np.arange(rbins.shape[0])), f"{name}/order permutation"
+    cnt = (rbins[:, 1] - rbins[:, 0]).astype(np.int64)[ordr]
+    prev, nxt = cnt[:-1], cnt[1:]
+    ok = np.where(prev < 8, nxt <= prev, 8 * nxt < 9 * prev)
+    assert ok.all(), f"{name}/order not heaviest first at {np.flatnonzero(~ok)[:5]}"
     rimg, rT, ridx, _, _ = O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background, xys,
                                            depths, radii, conics, cum, n=s.n, B=1,
                                            img_shape=s.img_shape)
@@ -459,9 +467,14 @@ def test_kept_sort_path_equals_resort_path(name):
                                    geo[4], kept._replace(records=None), Ts, fidx,
                                    vout.reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
                                    img_shape=s.img_shape)
-    for label, x, y, z in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), a, b, a2):
+    a3 = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[1], geo[3],
+                                   geo[4], kept._replace(order=None), Ts, fidx,
+                                   vout.reshape(-1, 3), n=s.n, B_out=1, B_geom=1,
+                                   img_shape=s.img_shape)
+    for label, x, y, z, w in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), a, b, a2, a3):
         _grad_compare(_np(x), _np(y), f"{name}/{label} kept vs re-sorted")
         _grad_compare(_np(x), _np(z), f"{name}/{label} repacked records")
+        _grad_compare(_np(x), _np(w), f"{name}/{label} tile order computed again")
     # packed record layout: (x, y, a/2, b), (c/2, o, sigma_max, 0), (r, g, b, depth),
     # (ex, ey, mode, 0); halving a float32 is exact, so a/2 and c/2 compare bit for bit
     r = _np(recs)
