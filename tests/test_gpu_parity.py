@@ -187,6 +187,60 @@ def test_config2_full_size_matches_oracle():
         _grad_compare(_np(g).reshape(r.shape), r, f"config2/{label}")
 
 
+@pytest.mark.parametrize("config", [3, 4])
+def test_batched_full_size_matches_oracle(config):
+    """Configs 3 (500K gaussians, 16 cameras at 512x512) and 4 (3M gaussians, 4 cameras at
+    1600x1060, antialiased) at full size through the kept-list path the benchmarks run: batched
+    projection, keys, sorted ids, tile bins, final_Ts / final_idx and the image bit for bit, the
+    blend backward (with the compensation cotangents for config 4) within the gradient bar."""
+    _case(f"config {config} full size")
+    O.set_threads(16)
+    s = make_scene(config)
+    B, n = s.B, s.n
+    ref, got = _project_both(s.means, s.scales, s.quats, s.viewmats, s.opacities, n=n, B=B,
+                             img_shape=s.img_shape, f=s.f, c=s.c)
+    for label, r, g in zip(("xys", "depths", "radii", "conics", "nth", "cum"), ref, got):
+        assert_bit_exact(g.reshape(r.shape), r, f"config{config}/{label}")
+    del got
+    xys, depths, radii, conics, nth, cum = ref
+    rk, rid, rbins = O.sort_and_bin(xys, depths, radii, conics, s.opacities, cum, n=n, B=B,
+                                    img_shape=s.img_shape)
+    ob = s.opacities.reshape(-1)
+    if s.antialiased:
+        rho, _ = O.compensation_rho(conics)
+        ob = (np.tile(ob, B) * np.where(radii.reshape(-1) > 0, rho, np.float32(1)))
+        ob = ob.astype(np.float32)
+    rimg, rT, ridx, _, M = O.rasterize_fwd(s.colors, ob, s.opacities, s.background, xys, depths,
+                                           radii, conics, cum, n=n, B=B, img_shape=s.img_shape)
+    o = _t(s.opacities).reshape(-1)
+    geo = (_t(xys), _t(depths), _t(radii), _t(conics), _t(cum))
+    img, Ts, fidx, kept, _ = _ops.rasterize_fwd_keep(
+        _t(s.colors), o, o, _t(s.background), *geo, n=n, B=B, img_shape=s.img_shape,
+        compensate=s.antialiased)
+    torch.cuda.synchronize()
+    assert kept.M == M == rid.size
+    assert_bit_exact(_np(kept.ids)[:M], rid, f"config{config}/ids")
+    assert_bit_exact(_np(kept.bins), rbins, f"config{config}/bins")
+    assert_bit_exact(_np(Ts), rT, f"config{config}/final_Ts")
+    assert_bit_exact(_np(fidx), ridx, f"config{config}/final_idx")
+    assert_bit_exact(_np(img), rimg, f"config{config}/img")
+    H, W = s.img_shape
+    vout = (2.0 * (rimg.reshape(B, H, W, 3) - s.targets) / rimg.size).astype(np.float32)
+    rg = O.rasterize_bwd(s.colors, ob, s.opacities, s.background, xys, depths, radii, conics,
+                         cum, rT, ridx, vout, n=n, B_out=B, B_geom=B, img_shape=s.img_shape)
+    want = list(rg[:4])
+    if s.antialiased:
+        v_o, v_c = O.compensation_vjp(rg[1], np.tile(s.opacities.reshape(-1), B), conics)
+        want[1], want[3] = v_o, rg[3] + v_c
+    gg = _ops.rasterize_bwd_sorted(_t(s.colors), o, _t(s.background), geo[0], geo[1], geo[3],
+                                   geo[4], kept, Ts, fidx, _t(vout).reshape(-1, 3), n=n,
+                                   B_out=B, B_geom=B, img_shape=s.img_shape,
+                                   compensate=s.antialiased)
+    torch.cuda.synchronize()
+    for label, g, r in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), gg, want):
+        _grad_compare(_np(g).reshape(r.shape), r, f"config{config}/{label}")
+
+
 @pytest.mark.parametrize("name", list(CASES))
 def test_rasterize_bwd_matches_oracle(name):
     _case(f"rasterize_bwd {name}")
