@@ -6,6 +6,11 @@
  * default stream). Every entry point returns 0 on success or a nonzero status; the message of
  * the last failure on the calling thread is splat_last_error().
  *
+ * The library keeps one set of scratch buffers per device, shared by every call on it. A call
+ * issued on a different stream than the previous call on that device first waits on the host
+ * (hipDeviceSynchronize) for the device's outstanding work, so calls from several streams or
+ * threads run one after the other; calls that stay on one stream never wait.
+ *
  * Batch convention (splax/_project/_kernels.py:58-75, splax/_rasterize/_kernels.py:56,408-418):
  * operands arrive flattened into their leading dimension; an operand is batched when its row
  * count exceeds num_gaussians (viewmat: exceeds 4 rows, transforms: exceeds num_transforms), and

@@ -105,6 +105,19 @@ int DeviceScratch::ensure_base() {
     return 0;
 }
 
+// A host wait only when the stream changes: an event recorded after every call would put a
+// barrier into every single-stream step (1.3% of the config-2 step).
+int DeviceScratch::order_after_last(hipStream_t s) {
+    if (has_last && s != last_stream && hipDeviceSynchronize() != hipSuccess)
+        return fail(kErrRuntime, "device synchronize before a stream change failed");
+    return 0;
+}
+
+void DeviceScratch::mark_done(hipStream_t s) {
+    has_last = true;
+    last_stream = s;
+}
+
 int DeviceScratch::grow_chunk_sums(int64_t blocks) {
     if (blocks <= chunk_sums_cap) return 0;
     (void)hipDeviceSynchronize();
@@ -273,6 +286,8 @@ void DeviceScratch::release() {
     pinned_count = nullptr;
     if (count_event) (void)hipEventDestroy(count_event);
     count_event = nullptr;
+    has_last = false;
+    last_stream = nullptr;
 }
 
 DeviceScratch& scratch_for_current_device() {
@@ -423,8 +438,8 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
         return fail(kErrArgs, "project_fwd: more than 2^31 items");
     hipStream_t s = static_cast<hipStream_t>(stream);
     DeviceScratch& sc = scratch_for_current_device();
-    std::lock_guard<std::mutex> lock(sc.mu);
-    int rc = sc.ensure_base();
+    ScratchUse use(sc, s);
+    int rc = use.rc;
     if (rc) return rc;
     ProjectArgs a;
     a.means = means3d; a.rows_means = rows_means;
@@ -443,8 +458,10 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
     a.num_tiles_hit = num_tiles_hit; a.cum_tiles_hit = cum_tiles_hit;
     a.quats_wxyz = quats_wxyz != 0;
     StageTimer tm(s, kStageProject);
+    g_last_error.clear();
     rc = launch_project_fwd(a, sc, s);
-    if (rc && g_last_error.empty()) set_error("project_fwd launch failed");
+    if (rc && g_last_error.empty())  // launchers that name their failure set the message
+        set_error("project_fwd launch failed");
     return rc;
 }
 
@@ -497,8 +514,10 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
     a.quats_wxyz = quats_wxyz != 0;
     a.fold = fold_shared != 0;
     StageTimer tm(s, kStageProjectBwd);
+    g_last_error.clear();
     int rc = launch_project_bwd(a, s);
-    if (rc && g_last_error.empty()) set_error("project_bwd launch failed");
+    if (rc && g_last_error.empty())  // launchers that name their failure set the message
+        set_error("project_bwd launch failed");
     return rc;
 }
 
@@ -539,8 +558,8 @@ int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* dep
     if (rc) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     DeviceScratch& sc = scratch_for_current_device();
-    std::lock_guard<std::mutex> lock(sc.mu);
-    rc = sc.ensure_base();
+    ScratchUse use(sc, s);
+    rc = use.rc;
     if (!rc) {
         const int32_t bpi = (num_gaussians + 4095) / 4096;
         rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * B);
@@ -604,8 +623,8 @@ static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortT
     if (rc) return rc;
     if (out_depth && !in.depths) return fail(kErrArgs, "rasterize: depth channel needs depths");
     DeviceScratch& sc = scratch_for_current_device();
-    std::lock_guard<std::mutex> lock(sc.mu);
-    rc = sc.ensure_base();
+    ScratchUse use(sc, s);
+    rc = use.rc;
     if (!rc) {
         const int32_t bpi = (in.n + 4095) / 4096;
         rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * in.B_geom);
@@ -660,8 +679,8 @@ static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptL
     if ((int64_t)args.B_out * in.n >= ((int64_t)1 << 31))
         return fail(kErrArgs, "rasterize_bwd: more than 2^31 gradient rows");
     DeviceScratch& sc = scratch_for_current_device();
-    std::lock_guard<std::mutex> lock(sc.mu);
-    rc = sc.ensure_base();
+    ScratchUse use(sc, s);
+    rc = use.rc;
     if (rc) return rc;
     KeyLayout L;
     const int32_t* ids = nullptr;

@@ -126,8 +126,15 @@ struct DeviceScratch {
     uint32_t* mm_partial = nullptr; int64_t mm_partial_cap = 0;     // 2 * blocks
     int32_t* pinned_count = nullptr;
     hipEvent_t count_event = nullptr;
+    // Calls on one device share these buffers: a call on another stream than the last user's
+    // first waits on the host for the device's work, so calls from different streams run one
+    // after the other.
+    hipStream_t last_stream = nullptr;
+    bool has_last = false;
 
     int ensure_base();
+    int order_after_last(hipStream_t s);
+    void mark_done(hipStream_t s);
     int grow_chunk_sums(int64_t blocks);
     int ensure_sort(int64_t M, int64_t bins, int32_t B, bool wide);
     int ensure_rgrad(int64_t count);
@@ -138,6 +145,24 @@ struct DeviceScratch {
 
 DeviceScratch& scratch_for_current_device();
 void release_all_scratch();
+
+// Holds the device's scratch for one entry point: takes its lock, allocates the base buffers,
+// orders the call's stream after the previous user's, and on exit records the stream.
+struct ScratchUse {
+    DeviceScratch& sc;
+    hipStream_t stream;
+    std::lock_guard<std::mutex> lock;
+    int rc;
+    ScratchUse(DeviceScratch& d, hipStream_t s) : sc(d), stream(s), lock(d.mu) {
+        rc = sc.ensure_base();
+        if (!rc) rc = sc.order_after_last(s);
+    }
+    ~ScratchUse() {
+        if (!rc) sc.mark_done(stream);
+    }
+    ScratchUse(const ScratchUse&) = delete;
+    ScratchUse& operator=(const ScratchUse&) = delete;
+};
 
 // ------------------------------------------------------------------ stage timing
 enum Stage : int {

@@ -421,6 +421,34 @@ def test_batched_cameras_one_launch():
         _grad_compare(_np(g).reshape(r.shape), r, f"batched/{label}")
 
 
+def test_calls_on_two_streams_share_scratch_in_order():
+    """Forwards issued alternately on two streams (default priority) without a sync by the
+    caller: a call on a new stream waits for the device's work on the shared scratch, so every
+    image equals the oracle's bit for bit."""
+    _case("two streams")
+    scenes = [make_scene(0), make_scene(2, n=50_000)]
+    refs, ins = [], []
+    for s in scenes:
+        xys, depths, radii, conics, nth, cum = _raster_inputs(s)
+        refs.append(O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background, xys,
+                                    depths, radii, conics, cum, n=s.n, B=1,
+                                    img_shape=s.img_shape)[0])
+        o = _t(s.opacities).reshape(-1)
+        ins.append((_t(s.colors), o, o, _t(s.background), _t(xys), _t(depths), _t(radii),
+                    _t(conics), _t(cum)))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = []
+    for rep in range(3):
+        for s, args, st in zip(scenes, ins, streams):
+            with torch.cuda.stream(st):
+                outs.append((rep, s.name, _ops.rasterize_fwd(*args, n=s.n, B=1,
+                                                             img_shape=s.img_shape)[0]))
+    torch.cuda.synchronize()
+    for k, (rep, name, img) in enumerate(outs):
+        assert_bit_exact(_np(img), refs[k % 2], f"two streams/{name} call {rep}")
+
+
 @pytest.mark.parametrize("H,W", [(37, 53), (16, 16), (100, 33)])
 def test_ragged_images(H, W):
     _case(f"ragged {H}x{W}")
