@@ -289,7 +289,9 @@ const char* splat_last_error(void);
  * the benchmark). Stages whose bit is set in stage_mask (0 turns timing off) are bracketed by
  * events at every launch; get_stage_times waits for them and returns, per stage, the summed
  * milliseconds and the number of calls, then resets. Stages: 0 project, 1 minmax, 2 emit,
- * 3 sort, 4 bins, 5 blend_fwd, 6 blend_bwd, 7 project_bwd. */
+ * 3 sort, 4 bins, 5 blend_fwd, 6 blend_bwd, 7 project_bwd; 8 and 9 time the forward and backward
+ * blend kernels alone, with the events carried by their dispatch (hipExtLaunchKernelGGL), so no
+ * marker is enqueued between kernels. */
 int splat_set_stage_timing(int stage_mask);
 int splat_get_stage_times(double* ms, int64_t* calls, int32_t n);
 

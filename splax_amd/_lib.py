@@ -66,7 +66,8 @@ _SIGS = {
     "splat_abi_version": [],
 }
 
-STAGES = ("project", "minmax", "emit", "sort", "bins", "blend_fwd", "blend_bwd", "project_bwd")
+STAGES = ("project", "minmax", "emit", "sort", "bins", "blend_fwd", "blend_bwd", "project_bwd",
+          "blend_fwd_kernel", "blend_bwd_kernel")
 
 # status codes (splax_amd/csrc/splat_internal.hpp)
 ERR_ARGS, ERR_KEY_OVERFLOW, ERR_TOO_MANY = 1, 2, 6

@@ -26,6 +26,8 @@
 // intersections of one item are contiguous; grad_gather_kernel then adds them per item in a
 // fixed order and writes the four gradient outputs. Only the LDS sums of one record over the
 // tile's four quadrant waves depend on the order in which the waves arrive.
+#include <hip/hip_ext.h>
+
 #include "splat_common.hpp"
 #include "splat_internal.hpp"
 
@@ -487,12 +489,14 @@ int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
     P.c.order = order;
     P.final_Ts = final_Ts; P.final_idx = final_idx; P.out_img = out_img;
     P.out_depth = out_depth;
+    hipEvent_t ka, kb;  // null unless this kernel is timed
+    (void)kernel_timer_events(kKernelBlendFwd, &ka, &kb);
     if (out_depth)
-        hipLaunchKernelGGL(blend_fwd_kernel<true>, dim3((unsigned)blocks), dim3(kTile), 0, stream,
-                           P);
+        hipExtLaunchKernelGGL(blend_fwd_kernel<true>, dim3((unsigned)blocks), dim3(kTile), 0,
+                              stream, ka, kb, 0, P);
     else
-        hipLaunchKernelGGL(blend_fwd_kernel<false>, dim3((unsigned)blocks), dim3(kTile), 0, stream,
-                           P);
+        hipExtLaunchKernelGGL(blend_fwd_kernel<false>, dim3((unsigned)blocks), dim3(kTile), 0,
+                              stream, ka, kb, 0, P);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
 }
 
@@ -862,12 +866,14 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
         P.pos = a.sorted_pos; P.M = a.M;
         P.v_out_depth = a.v_out_depth; P.vdepth_rows = a.vdepth_rows;
         P.rgrad = a.rgrad;
+        hipEvent_t ka, kb;  // null unless this kernel is timed
+        (void)kernel_timer_events(kKernelBlendBwd, &ka, &kb);
         if (depth)
-            hipLaunchKernelGGL(blend_bwd_kernel<true>, dim3((unsigned)blocks), dim3(kTile), 0,
-                               stream, P);
+            hipExtLaunchKernelGGL(blend_bwd_kernel<true>, dim3((unsigned)blocks), dim3(kTile),
+                                  0, stream, ka, kb, 0, P);
         else
-            hipLaunchKernelGGL(blend_bwd_kernel<false>, dim3((unsigned)blocks), dim3(kTile), 0,
-                               stream, P);
+            hipExtLaunchKernelGGL(blend_bwd_kernel<false>, dim3((unsigned)blocks), dim3(kTile),
+                                  0, stream, ka, kb, 0, P);
         if (hipGetLastError() != hipSuccess) return kErrLaunch;
     }
     if (nout <= 0) return 0;

@@ -333,6 +333,16 @@ static hipEvent_t take_event() {
     return e;
 }
 
+bool kernel_timer_events(int stage, hipEvent_t* start, hipEvent_t* end) {
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    *start = *end = nullptr;
+    if (!((g_timing_mask >> stage) & 1u)) return false;
+    *start = take_event();
+    *end = take_event();
+    g_spans.push_back({stage, *start, *end});
+    return true;
+}
+
 StageTimer::StageTimer(hipStream_t s, int st) : stream(s), stage(st) {
     std::lock_guard<std::mutex> lock(g_timing_mu);
     if (!((g_timing_mask >> st) & 1u)) return;

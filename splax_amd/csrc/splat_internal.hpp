@@ -174,8 +174,13 @@ enum Stage : int {
     kStageBlendFwd,
     kStageBlendBwd,
     kStageProjectBwd,
+    kKernelBlendFwd,  // the blend kernel alone (its dispatch carries the events)
+    kKernelBlendBwd,
     kNumStages
 };
+// When timing is on for a kernel entry, hands out the two events its hipExtLaunchKernelGGL
+// dispatch records (start and end of that kernel only) and queues them for splat_get_stage_times.
+bool kernel_timer_events(int stage, hipEvent_t* start, hipEvent_t* end);
 struct StageTimer {
     hipStream_t stream;
     int stage;
