@@ -51,8 +51,9 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
 
 /* Replaces _project_bwd_warp (splax/_project/_kernels.py:257-341, FFI callable :344-353).
  * Outputs: v_mean3d [B*n,3], v_scale [B*n,3], v_quat [B*n,4] (in the quats layout chosen by
- * quats_wxyz, as splat_project_fwd), v_viewmat [4B,4], v_transforms [B*num_transforms,4,4] (may
- * be NULL when has_transforms == 0). All outputs are fully written (no caller zeroing).
+ * quats_wxyz, as splat_project_fwd), v_viewmat [4B,4] (may be NULL: no viewmat gradient is
+ * formed), v_transforms [B*num_transforms,4,4] (may be NULL when has_transforms == 0). All
+ * outputs are fully written (no caller zeroing).
  * fold_shared != 0 (means3d, scales and quats shared, num_gaussians rows each) writes
  * v_mean3d [n,3], v_scale [n,3] and v_quat [n,4] summed over the B images in image order: the
  * cotangent of a shared parameter, which splax forms by summing the batched rows. */

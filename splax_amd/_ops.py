@@ -63,12 +63,13 @@ def project_fwd(means, scales, quats, viewmat, opac, transforms, transform_ids, 
 
 def project_bwd(means, scales, quats, viewmat, radii, conics, v_xy, v_depth, v_conic,
                 transforms, transform_ids, *, n, B, num_transforms, has_transforms, f,
-                glob_scale, quats_wxyz=False, fold=False):
+                glob_scale, quats_wxyz=False, fold=False, want_viewmat=True):
     """_project_bwd_warp (splax/_project/_kernels.py:257-341).
 
     v_depth may be None (a zero depth cotangent); v_tf is None without transforms. v_quat comes
     in the layout of quats (xyzw, or wxyz with ``quats_wxyz``). With ``fold`` (shared means,
-    scales and quats) v_mean, v_scale and v_quat have n rows, summed over the B images."""
+    scales and quats) v_mean, v_scale and v_quat have n rows, summed over the B images. Without
+    ``want_viewmat`` no viewmat gradient is formed and v_view is None."""
     means, scales, quats, viewmat, conics = map(_f32, (means, scales, quats, viewmat,
                                                        conics))
     v_xy, v_conic, transforms = map(_f32, (v_xy, v_conic, transforms))
@@ -79,7 +80,7 @@ def project_bwd(means, scales, quats, viewmat, radii, conics, v_xy, v_depth, v_c
     v_mean = torch.empty((total, 3), device=dev, dtype=torch.float32)
     v_scale = torch.empty((total, 3), device=dev, dtype=torch.float32)
     v_quat = torch.empty((total, 4), device=dev, dtype=torch.float32)
-    v_view = torch.empty((B * 4, 4), device=dev, dtype=torch.float32)
+    v_view = torch.empty((B * 4, 4), device=dev, dtype=torch.float32) if want_viewmat else None
     v_tf = None
     if has_transforms:
         v_tf = torch.empty((B * num_transforms, 4, 4), device=dev, dtype=torch.float32)

@@ -79,7 +79,8 @@ class _ProjectFn(torch.autograd.Function):
             conics, v_xys.reshape(-1, 2), None if v_depths is None else v_depths.reshape(-1),
             v_conics.reshape(-1, 3),
             transforms.reshape(-1, 4, 4), tf_ids.reshape(-1), n=n, B=B, num_transforms=K,
-            has_transforms=has_tf, f=f, glob_scale=glob_scale, quats_wxyz=True, fold=fold_here)
+            has_transforms=has_tf, f=f, glob_scale=glob_scale, quats_wxyz=True, fold=fold_here,
+            want_viewmat=ctx.needs_input_grad[3])
 
         def fold(g: torch.Tensor, like: torch.Tensor, width: int) -> torch.Tensor:
             if g.numel() == like.numel():  # one image, or a batched operand

@@ -547,23 +547,26 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
                        : make_float4(vq[0], vq[1], vq[2], vq[3]);
         }
     }
-    // viewmat gradient: wave DPP reduction, then across the 4 waves in LDS, one atomic per entry
-    float red[12];
+    // viewmat gradient (when asked for): wave DPP reduction, then across the 4 waves in LDS,
+    // one atomic per entry
+    if (P.v_viewmat) {
+        float red[12];
 #pragma unroll
-    for (int a = 0; a < 3; ++a) {
+        for (int a = 0; a < 3; ++a) {
 #pragma unroll
-        for (int b = 0; b < 3; ++b) red[4 * a + b] = vR[3 * a + b];
-        red[4 * a + 3] = vt[a];
-    }
+            for (int b = 0; b < 3; ++b) red[4 * a + b] = vR[3 * a + b];
+            red[4 * a + 3] = vt[a];
+        }
 #pragma unroll
-    for (int k = 0; k < 12; ++k) {
-        float v = wave_sum_to_lane63(red[k]);
-        if (lane == 63) s_red[wave][k] = v;
-    }
-    __syncthreads();
-    if (tid < 12) {
-        float v = ((s_red[0][tid] + s_red[1][tid]) + s_red[2][tid]) + s_red[3][tid];
-        atomicAdd(P.v_viewmat + (int64_t)image_id * 16 + tid, v);
+        for (int k = 0; k < 12; ++k) {
+            float v = wave_sum_to_lane63(red[k]);
+            if (lane == 63) s_red[wave][k] = v;
+        }
+        __syncthreads();
+        if (tid < 12) {
+            float v = ((s_red[0][tid] + s_red[1][tid]) + s_red[2][tid]) + s_red[3][tid];
+            atomicAdd(P.v_viewmat + (int64_t)image_id * 16 + tid, v);
+        }
     }
     // Transform gradient: uniform block -> block reduction; mixed -> per-thread atomics
     // (splax/_project/_kernels.py:461-484).
@@ -658,7 +661,7 @@ int launch_project_bwd(const ProjectBwdArgs& a, hipStream_t stream) {
     // zero the reduction targets (per-item outputs are fully written by the kernel)
     int64_t nview = (int64_t)a.B * 16;
     int64_t ntf = (int64_t)a.B * a.num_transforms * 16;
-    int rc = fill_zero_f32(a.v_viewmat, nview, stream);
+    int rc = a.v_viewmat ? fill_zero_f32(a.v_viewmat, nview, stream) : 0;
     if (rc) return rc;
     if (a.v_transforms && ntf > 0) {
         rc = fill_zero_f32(a.v_transforms, ntf, stream);

@@ -295,6 +295,14 @@ def test_project_bwd_matches_oracle(name):
                             num_transforms=1, has_transforms=False, f=s.f, glob_scale=1.0)
     for label, a, b in zip(("v_mean3d", "v_scale", "v_quat"), zero[:3], none[:3]):
         assert_bit_exact(_np(b), _np(a), f"{name}/{label} null v_depth")
+    # without the viewmat gradient (NULL v_viewmat) the per-gaussian outputs are unchanged
+    nov = _ops.project_bwd(_t(s.means), _t(s.scales), _t(q), _t(s.viewmats[0]), _t(radii),
+                           _t(conics), _t(v_xy), _t(v_depth), _t(v_conic), tf, ids, n=s.n, B=1,
+                           num_transforms=1, has_transforms=False, f=s.f, glob_scale=1.0,
+                           want_viewmat=False)
+    assert nov[3] is None
+    for label, a, b in zip(("v_mean3d", "v_scale", "v_quat"), got[:3], nov[:3]):
+        assert_bit_exact(_np(b), _np(a), f"{name}/{label} without v_viewmat")
     # wxyz storage (the public API's order): same results, v_quat in wxyz
     wx = _ops.project_bwd(_t(s.means), _t(s.scales), _t(s.quats), _t(s.viewmats[0]), _t(radii),
                           _t(conics), _t(v_xy), _t(v_depth), _t(v_conic), tf, ids, n=s.n, B=1,
