@@ -228,6 +228,18 @@ int DeviceScratch::ensure_recs(int64_t items) {
     return 0;
 }
 
+int DeviceScratch::ensure_view_partials(int64_t count) {
+    if (count <= view_partials_cap) return 0;
+    (void)hipDeviceSynchronize();
+    dev_free(&view_partials);
+    view_partials_cap = 0;
+    const int64_t cap = (int64_t)(count * 1.25) + 1;
+    int rc = dev_alloc(&view_partials, cap, false);
+    if (rc) return rc;
+    view_partials_cap = cap;
+    return 0;
+}
+
 int DeviceScratch::ensure_order(int64_t blocks) {
     if (blocks <= order_cap) return 0;
     (void)hipDeviceSynchronize();
@@ -270,6 +282,8 @@ void DeviceScratch::release() {
     recs_cap = 0;
     dev_free(&tile_order);
     order_cap = 0;
+    dev_free(&view_partials);
+    view_partials_cap = 0;
     dev_free(&part_counts);
     part_counts_cap = 0;
     dev_free(&tile_bins);
@@ -523,9 +537,13 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
     a.v_viewmat = v_viewmat; a.v_transforms = has_transforms ? v_transforms : nullptr;
     a.quats_wxyz = quats_wxyz != 0;
     a.fold = fold_shared != 0;
+    DeviceScratch& sc = scratch_for_current_device();
+    ScratchUse use(sc, s);
+    int rc = use.rc;
+    if (rc) return rc;
     StageTimer tm(s, kStageProjectBwd);
     g_last_error.clear();
-    int rc = launch_project_bwd(a, s);
+    rc = launch_project_bwd(a, sc, s);
     if (rc && g_last_error.empty())  // launchers that name their failure set the message
         set_error("project_bwd launch failed");
     return rc;

@@ -315,6 +315,7 @@ struct ProjectBwdParams {
     int32_t n, num_transforms, has_transforms, B, blocks_per_image;
     float fx, fy, glob_scale;
     float* v_mean3d; float* v_scale; float* v_quat; float* v_viewmat; float* v_transforms;
+    float* view_partials;  // [B * blocks_per_image, 12] or null (no viewmat gradient)
     int32_t wxyz;  // quats and v_quat stored wxyz (1) or xyzw (0)
     int32_t fold;  // gaussian gradients summed over the images into n rows
 };
@@ -547,9 +548,10 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
                        : make_float4(vq[0], vq[1], vq[2], vq[3]);
         }
     }
-    // viewmat gradient (when asked for): wave DPP reduction, then across the 4 waves in LDS,
-    // one atomic per entry
-    if (P.v_viewmat) {
+    // viewmat gradient (when asked for): wave DPP reduction, then across the 4 waves in LDS, one
+    // partial per (image, workgroup) that viewmat_reduce_kernel sums in a fixed order (atomics
+    // from thousands of workgroups into the same 12 words serialize in the L2)
+    if (P.view_partials) {
         float red[12];
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
@@ -565,7 +567,7 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
         __syncthreads();
         if (tid < 12) {
             float v = ((s_red[0][tid] + s_red[1][tid]) + s_red[2][tid]) + s_red[3][tid];
-            atomicAdd(P.v_viewmat + (int64_t)image_id * 16 + tid, v);
+            P.view_partials[((int64_t)image_id * P.blocks_per_image + local_block) * 12 + tid] = v;
         }
     }
     // Transform gradient: uniform block -> block reduction; mixed -> per-thread atomics
@@ -621,6 +623,32 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
     }
 }
 
+// One workgroup per image: the image's workgroup partials summed in a fixed order (each thread a
+// strided run, then the waves), written with the zero bottom row as the viewmat gradient.
+__global__ void __launch_bounds__(kProjThreads)
+viewmat_reduce_kernel(const float* partials, int32_t blocks_per_image, float* v_viewmat) {
+    __shared__ float s_red[kProjThreads / 64][12];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t image = blockIdx.x;
+    const float* src = partials + image * blocks_per_image * 12;
+    float acc[12];
+#pragma unroll
+    for (int k = 0; k < 12; ++k) acc[k] = 0.f;
+    for (int32_t j = tid; j < blocks_per_image; j += kProjThreads) {
+#pragma unroll
+        for (int k = 0; k < 12; ++k) acc[k] = acc[k] + src[(int64_t)j * 12 + k];
+    }
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+        const float v = wave_sum_to_lane63(acc[k]);
+        if (lane == 63) s_red[wave][k] = v;
+    }
+    __syncthreads();
+    if (tid < 16)
+        v_viewmat[image * 16 + tid] =
+            tid < 12 ? ((s_red[0][tid] + s_red[1][tid]) + s_red[2][tid]) + s_red[3][tid] : 0.f;
+}
+
 int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stream) {
     if (a.total <= 0) return 0;
     const int64_t per_block = (int64_t)kProjFwdThreads * kProjItems;
@@ -656,18 +684,22 @@ int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stre
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
 }
 
-int launch_project_bwd(const ProjectBwdArgs& a, hipStream_t stream) {
+int launch_project_bwd(const ProjectBwdArgs& a, DeviceScratch& sc, hipStream_t stream) {
     const int32_t blocks_per_image = (a.n + kProjThreads - 1) / kProjThreads;
-    // zero the reduction targets (per-item outputs are fully written by the kernel)
-    int64_t nview = (int64_t)a.B * 16;
+    // zero the transforms' atomic targets (per-item outputs and the viewmat gradient are fully
+    // written by the kernels)
     int64_t ntf = (int64_t)a.B * a.num_transforms * 16;
-    int rc = a.v_viewmat ? fill_zero_f32(a.v_viewmat, nview, stream) : 0;
-    if (rc) return rc;
+    int rc = 0;
     if (a.v_transforms && ntf > 0) {
         rc = fill_zero_f32(a.v_transforms, ntf, stream);
         if (rc) return rc;
     }
-    if (a.n <= 0 || a.B <= 0) return 0;
+    if (a.n <= 0 || a.B <= 0)
+        return a.v_viewmat && a.B > 0 ? fill_zero_f32(a.v_viewmat, (int64_t)a.B * 16, stream) : 0;
+    if (a.v_viewmat) {
+        rc = sc.ensure_view_partials((int64_t)a.B * blocks_per_image * 12);
+        if (rc) return rc;
+    }
     ProjectBwdParams P;
     P.means = a.means; P.rows_means = a.rows_means;
     P.scales = a.scales; P.rows_scales = a.rows_scales;
@@ -685,11 +717,15 @@ int launch_project_bwd(const ProjectBwdArgs& a, hipStream_t stream) {
     P.fx = a.fx; P.fy = a.fy; P.glob_scale = a.glob_scale;
     P.v_mean3d = a.v_mean3d; P.v_scale = a.v_scale; P.v_quat = a.v_quat;
     P.v_viewmat = a.v_viewmat; P.v_transforms = a.v_transforms;
+    P.view_partials = a.v_viewmat ? sc.view_partials : nullptr;
     P.wxyz = a.quats_wxyz;
     P.fold = a.fold;
     int64_t blocks = (a.fold ? 1 : (int64_t)a.B) * blocks_per_image;
     hipLaunchKernelGGL(project_bwd_kernel, dim3((unsigned)blocks), dim3(kProjThreads), 0, stream,
                        P);
+    if (a.v_viewmat)
+        hipLaunchKernelGGL(viewmat_reduce_kernel, dim3((unsigned)a.B), dim3(kProjThreads), 0,
+                           stream, sc.view_partials, blocks_per_image, a.v_viewmat);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
 }
 

@@ -119,6 +119,8 @@ struct DeviceScratch {
     float4* recs = nullptr; int64_t recs_cap = 0;
     // blends: workgroup -> (image, tile) dispatch order
     int32_t* tile_order = nullptr; int64_t order_cap = 0;
+    // projection backward: 12 viewmat-gradient partials per (image, workgroup)
+    float* view_partials = nullptr; int64_t view_partials_cap = 0;
     uint32_t* part_counts = nullptr; int64_t part_counts_cap = 0;  // 256 * partitions
     uint32_t* hist = nullptr;                                       // 256 digit totals
     int32_t* tile_bins = nullptr; int64_t bins_cap = 0;             // (start, end) pairs
@@ -140,6 +142,7 @@ struct DeviceScratch {
     int ensure_rgrad(int64_t count);
     int ensure_recs(int64_t items);
     int ensure_order(int64_t blocks);
+    int ensure_view_partials(int64_t count);
     void release();
 };
 
@@ -196,7 +199,7 @@ void release_train_scratch();
 int fill_zero_f32(float* p, int64_t n, hipStream_t stream);
 int fill_zero_i32(int32_t* p, int64_t n, hipStream_t stream);
 int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stream);
-int launch_project_bwd(const ProjectBwdArgs& a, hipStream_t stream);
+int launch_project_bwd(const ProjectBwdArgs& a, DeviceScratch& sc, hipStream_t stream);
 
 // Optional caller-owned destinations of sort_and_bin: M_known >= 0 skips the count readback
 // (it must equal cum[B*n - 1]); ids / pos / bins (when non-null) receive the sorted gaussian ids,
