@@ -240,6 +240,9 @@ def main():
             p.grad = None
         vm.grad = None
         img = forward()
+        # torch's mse_loss (C++ autograd): the library's fused MSE (splax_amd.train.mse_loss, 29 us
+        # of GPU time vs 55) runs as a Python autograd Function, and its host time made this
+        # step host-bound (the count readback in each forward stops the host running ahead)
         loss = torch.nn.functional.mse_loss(img, target)
         loss.backward()
 

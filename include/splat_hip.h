@@ -280,6 +280,17 @@ int splat_l1_loss_fwd(splat_stream_t stream, const float* img, const float* targ
 int splat_l1_loss_bwd(splat_stream_t stream, const float* img, const float* target,
                       int64_t count, const float* v_loss, float* v_img);
 
+/* MSE loss mean (img - target)^2 over count elements, the loss of the benchmark workloads 0-3
+ * (no counterpart in the reference library; its callers form the loss in JAX), summed in double
+ * in a fixed order; arguments as splat_l1_loss_fwd. One pass each way, where torch's mse_loss
+ * takes four kernels and a fill. */
+int splat_mse_loss_fwd(splat_stream_t stream, const float* img, const float* target,
+                       int64_t count, double* partials, float* loss);
+
+/* Cotangent of the MSE loss: v_img = 2 (img - target) * (*v_loss / count). */
+int splat_mse_loss_bwd(splat_stream_t stream, const float* img, const float* target,
+                       int64_t count, const float* v_loss, float* v_img);
+
 /* Replaces clear_cache (splax/_cache.py:158-164): frees the per-device scratch. */
 void splat_clear_cache(void);
 

@@ -227,3 +227,15 @@ def l1_loss(img, target, g=1.0):
     scale = np.float32(g) / np.float32(d.size)
     sg = np.where(d > 0, np.float32(1), np.where(d < 0, np.float32(-1), d))
     return loss, (sg * scale).astype(np.float32)
+
+
+def mse_loss(img, target, g=1.0):
+    """mean (img - target)^2, the benchmark workloads' loss (configs 0-3 take the MSE to a
+    seeded target; the reference library has no loss of its own): float32 differences, squared
+    and summed in double, rounded once; returns (loss, img cotangent 2 d * (g / count) for loss
+    cotangent g, with 2 d formed as d + d)."""
+    d = np.asarray(img, np.float32).reshape(-1) - np.asarray(target, np.float32).reshape(-1)
+    d64 = d.astype(np.float64)
+    loss = np.float32((d64 * d64).sum() / d.size)
+    scale = np.float32(g) / np.float32(d.size)
+    return loss, ((d + d) * scale).astype(np.float32)

@@ -58,6 +58,8 @@ _SIGS = {
     "splat_log_params_bwd": [_vp] + [_vp] * 4 + [_i64] + [_vp] * 8,
     "splat_l1_loss_fwd": [_vp, _vp, _vp, _i64, _vp, _vp],
     "splat_l1_loss_bwd": [_vp, _vp, _vp, _i64, _vp, _vp],
+    "splat_mse_loss_fwd": [_vp, _vp, _vp, _i64, _vp, _vp],
+    "splat_mse_loss_bwd": [_vp, _vp, _vp, _i64, _vp, _vp],
     "splat_clear_cache": [],
     "splat_last_error": [],
     "splat_set_stage_timing": [_i32],

@@ -84,21 +84,25 @@ __global__ void __launch_bounds__(256) log_params_bwd_kernel(LogParams P) {
     reinterpret_cast<float4*>(P.v_quats_in)[i] = make_float4(vq[0], vq[1], vq[2], vq[3]);
 }
 
-// ------------------------------------------------------------------ L1 loss
+// ------------------------------------------------------------------ L1 and MSE losses
 
 constexpr int kL1Chunk = 4096;  // elements per workgroup (16 per thread)
 
-// Workgroup sums of |img - target| in double, in a fixed order: per thread sequential, then a
-// fixed tree over the workgroup.
-__global__ void __launch_bounds__(256) l1_partials_kernel(const float* img, const float* tgt,
-                                                          int64_t count, double* partials) {
+// Workgroup sums of |img - target| (kSquare: (img - target)^2, exact in double) in double, in a
+// fixed order: per thread sequential, then a fixed tree over the workgroup.
+template <bool kSquare>
+__global__ void __launch_bounds__(256) loss_partials_kernel(const float* img, const float* tgt,
+                                                            int64_t count, double* partials) {
     __shared__ double s[256];
     const int64_t base = (int64_t)blockIdx.x * kL1Chunk;
     double acc = 0.0;
 #pragma unroll
     for (int j = 0; j < kL1Chunk / 256; ++j) {
         const int64_t i = base + j * 256 + threadIdx.x;
-        if (i < count) acc += (double)fabsf(img[i] - tgt[i]);
+        if (i < count) {
+            const float d = img[i] - tgt[i];
+            acc += kSquare ? (double)d * (double)d : (double)fabsf(d);
+        }
     }
     s[threadIdx.x] = acc;
     __syncthreads();
@@ -124,21 +128,53 @@ __global__ void __launch_bounds__(256) l1_final_kernel(const double* partials, i
     if (threadIdx.x == 0) *loss = (float)(s[0] / (double)count);
 }
 
-// v_img = sign(img - target) * (g / count), g read from device memory (the loss cotangent).
-__global__ void __launch_bounds__(256) l1_bwd_kernel(const float* img, const float* tgt,
-                                                     int64_t count, const float* g, float* v) {
+// v_img = sign(img - target) * (g / count) (kSquare: 2 (img - target) * (g / count)), g read
+// from device memory (the loss cotangent).
+template <bool kSquare>
+__global__ void __launch_bounds__(256) loss_bwd_kernel(const float* img, const float* tgt,
+                                                       int64_t count, const float* g, float* v) {
     const float scale = *g / (float)count;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count;
          i += (int64_t)gridDim.x * 256) {
         const float d = img[i] - tgt[i];
-        const float sg = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : d);  // sign: +-0 and NaN pass
-        v[i] = sg * scale;
+        if (kSquare) {
+            v[i] = (d + d) * scale;
+        } else {
+            const float sg = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : d);  // sign: +-0 and NaN pass
+            v[i] = sg * scale;
+        }
     }
 }
 
 static int glue_launched(const char* what) {
     return hipGetLastError() == hipSuccess ? 0
                                            : fail(kErrLaunch, std::string(what) + " launch failed");
+}
+
+template <bool kSquare>
+static int loss_fwd(hipStream_t s, const float* img, const float* target, int64_t count,
+                    double* partials, float* loss, const char* name) {
+    if (count <= 0 || !img || !target || !partials || !loss)
+        return fail(kErrArgs, std::string(name) + ": empty input or missing arrays");
+    const int64_t blocks = (count + kL1Chunk - 1) / kL1Chunk;
+    hipLaunchKernelGGL(loss_partials_kernel<kSquare>, dim3((unsigned)blocks), dim3(256), 0, s,
+                       img, target, count, partials);
+    int rc = glue_launched(name);
+    if (rc) return rc;
+    hipLaunchKernelGGL(l1_final_kernel, dim3(1), dim3(256), 0, s, partials, blocks, count, loss);
+    return glue_launched(name);
+}
+
+template <bool kSquare>
+static int loss_bwd(hipStream_t s, const float* img, const float* target, int64_t count,
+                    const float* v_loss, float* v_img, const char* name) {
+    if (count <= 0 || !img || !target || !v_loss || !v_img)
+        return fail(kErrArgs, std::string(name) + ": empty input or missing arrays");
+    int64_t blocks = (count + 255) / 256;
+    blocks = blocks < 8192 ? blocks : 8192;
+    hipLaunchKernelGGL(loss_bwd_kernel<kSquare>, dim3((unsigned)blocks), dim3(256), 0, s, img,
+                       target, count, v_loss, v_img);
+    return glue_launched(name);
 }
 
 }  // namespace splat
@@ -191,27 +227,26 @@ int splat_log_params_bwd(splat_stream_t stream, const float* log_scales, const f
 
 int splat_l1_loss_fwd(splat_stream_t stream, const float* img, const float* target,
                       int64_t count, double* partials, float* loss) {
-    if (count <= 0 || !img || !target || !partials || !loss)
-        return fail(kErrArgs, "l1_loss_fwd: empty input or missing arrays");
-    const int64_t blocks = (count + kL1Chunk - 1) / kL1Chunk;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(l1_partials_kernel, dim3((unsigned)blocks), dim3(256), 0, s, img, target,
-                       count, partials);
-    int rc = glue_launched("l1_loss partials");
-    if (rc) return rc;
-    hipLaunchKernelGGL(l1_final_kernel, dim3(1), dim3(256), 0, s, partials, blocks, count, loss);
-    return glue_launched("l1_loss final");
+    return loss_fwd<false>(static_cast<hipStream_t>(stream), img, target, count, partials, loss,
+                           "l1_loss_fwd");
 }
 
 int splat_l1_loss_bwd(splat_stream_t stream, const float* img, const float* target,
                       int64_t count, const float* v_loss, float* v_img) {
-    if (count <= 0 || !img || !target || !v_loss || !v_img)
-        return fail(kErrArgs, "l1_loss_bwd: empty input or missing arrays");
-    int64_t blocks = (count + 255) / 256;
-    blocks = blocks < 8192 ? blocks : 8192;
-    hipLaunchKernelGGL(l1_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), img, target, count, v_loss, v_img);
-    return glue_launched("l1_loss_bwd");
+    return loss_bwd<false>(static_cast<hipStream_t>(stream), img, target, count, v_loss, v_img,
+                           "l1_loss_bwd");
+}
+
+int splat_mse_loss_fwd(splat_stream_t stream, const float* img, const float* target,
+                       int64_t count, double* partials, float* loss) {
+    return loss_fwd<true>(static_cast<hipStream_t>(stream), img, target, count, partials, loss,
+                          "mse_loss_fwd");
+}
+
+int splat_mse_loss_bwd(splat_stream_t stream, const float* img, const float* target,
+                       int64_t count, const float* v_loss, float* v_img) {
+    return loss_bwd<true>(static_cast<hipStream_t>(stream), img, target, count, v_loss, v_img,
+                          "mse_loss_bwd");
 }
 
 }  // extern "C"

@@ -47,23 +47,26 @@ def params_from_scene(scene: Scene, device: torch.device | str = "cuda") -> dict
     return {k: torch.from_numpy(np.ascontiguousarray(v)).to(device) for k, v in arrays.items()}
 
 
-class _L1LossFn(torch.autograd.Function):
+class _PixelLossFn(torch.autograd.Function):
+    """Mean of |img - target| ("l1") or (img - target)^2 ("mse"): one library pass each way."""
+
     @staticmethod
-    def forward(ctx, img, target):
+    def forward(ctx, img, target, kind):
         if img.shape != target.shape or img.dtype != torch.float32 or \
                 target.dtype != torch.float32:
-            raise ValueError("l1_loss: img and target must be float32 of one shape")
+            raise ValueError(f"{kind}_loss: img and target must be float32 of one shape")
         img, target = img.contiguous(), target.contiguous()
         dev = _lib.require_gpu(img, target)
         count = img.numel()
         partials = torch.empty(((count + 4095) // 4096,), device=dev, dtype=torch.float64)
         loss = torch.empty((), device=dev, dtype=torch.float32)
+        fwd = getattr(_lib.lib(), f"splat_{kind}_loss_fwd")
         with torch.cuda.device(dev):
-            st = _lib.lib().splat_l1_loss_fwd(_lib.stream_handle(dev), img.data_ptr(),
-                                              target.data_ptr(), count, partials.data_ptr(),
-                                              loss.data_ptr())
-        _lib.check(st, "l1_loss_fwd")
+            st = fwd(_lib.stream_handle(dev), img.data_ptr(), target.data_ptr(), count,
+                     partials.data_ptr(), loss.data_ptr())
+        _lib.check(st, f"{kind}_loss_fwd")
         ctx.save_for_backward(img, target)
+        ctx.kind = kind
         return loss
 
     @staticmethod
@@ -71,18 +74,24 @@ class _L1LossFn(torch.autograd.Function):
         img, target = ctx.saved_tensors
         v_loss = v_loss.to(torch.float32).contiguous()
         v_img = torch.empty_like(img)
+        bwd = getattr(_lib.lib(), f"splat_{ctx.kind}_loss_bwd")
         with torch.cuda.device(img.device):
-            st = _lib.lib().splat_l1_loss_bwd(_lib.stream_handle(img.device), img.data_ptr(),
-                                              target.data_ptr(), img.numel(), v_loss.data_ptr(),
-                                              v_img.data_ptr())
-        _lib.check(st, "l1_loss_bwd")
-        return v_img, None
+            st = bwd(_lib.stream_handle(img.device), img.data_ptr(), target.data_ptr(),
+                     img.numel(), v_loss.data_ptr(), v_img.data_ptr())
+        _lib.check(st, f"{ctx.kind}_loss_bwd")
+        return v_img, None, None
 
 
 def l1_loss(img: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
     """mean |img - target| (scripts/train_lego.py:111), one library pass each way; the target
     receives no gradient."""
-    return _L1LossFn.apply(img, target)
+    return _PixelLossFn.apply(img, target, "l1")
+
+
+def mse_loss(img: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+    """mean (img - target)^2, one library pass each way (torch's mse_loss runs four kernels and
+    a fill); the target receives no gradient."""
+    return _PixelLossFn.apply(img, target, "mse")
 
 
 class TrainStep:

@@ -284,3 +284,19 @@ def test_l1_loss(count):
     (loss * 3.0).backward()
     assert abs(float(loss.detach()) - float(ref_loss)) <= 1e-6 * float(ref_loss)
     assert_bit_exact(_np(x.grad), ref_v, "l1 cotangent")
+
+
+@pytest.mark.parametrize("count", [1, 4095, 4097, 3 * 1080 * 1920])
+def test_mse_loss(count):
+    from splax_amd.train import mse_loss
+
+    _case(f"mse count={count}")
+    rng = np.random.default_rng(count + 1)
+    img = rng.uniform(size=count).astype(np.float32)
+    tgt = rng.uniform(size=count).astype(np.float32)
+    ref_loss, ref_v = T.mse_loss(img, tgt, g=3.0)
+    x = _t(img).requires_grad_(True)
+    loss = mse_loss(x, _t(tgt))
+    (loss * 3.0).backward()
+    assert abs(float(loss.detach()) - float(ref_loss)) <= 1e-6 * float(ref_loss)
+    assert_bit_exact(_np(x.grad), ref_v, "mse cotangent")

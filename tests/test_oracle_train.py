@@ -247,3 +247,23 @@ def test_l1_loss_closed_form():
     loss, v = T.l1_loss(img, tgt)
     assert loss == np.float32((0.25 + 0 + 1.0 + 0.25) / 4)
     assert v.tolist() == [0.25, 0.0, 0.25, -0.25]
+
+
+def test_mse_loss_closed_form_and_torch():
+    img = np.array([0.5, 0.25, 1.0, 0.75], np.float32)
+    tgt = np.array([0.25, 0.25, 0.0, 1.0], np.float32)
+    loss, v = T.mse_loss(img, tgt)
+    assert loss == np.float32((0.0625 + 0 + 1.0 + 0.0625) / 4)
+    assert v.tolist() == [0.125, 0.0, 0.5, -0.125]
+    # against torch's own mse_loss and its gradient (float64, random inputs)
+    import torch
+
+    rng = np.random.default_rng(3)
+    a = rng.uniform(size=10_000).astype(np.float32)
+    b = rng.uniform(size=10_000).astype(np.float32)
+    loss, v = T.mse_loss(a, b, g=2.0)
+    x = torch.tensor(a, dtype=torch.float64, requires_grad=True)
+    ref = torch.nn.functional.mse_loss(x, torch.tensor(b, dtype=torch.float64))
+    (2.0 * ref).backward()
+    assert abs(float(loss) - ref.item()) <= 1e-6 * ref.item()
+    np.testing.assert_allclose(v, x.grad.numpy(), rtol=1e-6, atol=0)
