@@ -166,7 +166,9 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
  * num_intersects of the matching forward (records may be NULL: the backward then packs them
  * again from its inputs, which must be the forward's; tile_order may be NULL: the backward then
  * orders the tiles again, as it also does when B_out != B_geom; the order only schedules the
- * tiles, the outputs do not depend on it); the outputs equal splat_rasterize_bwd's (same kernels;
+ * tiles, the outputs do not depend on it; these buffers must be the forward's, unchanged: their
+ * contents are not validated, except that a tile_order entry out of range skips that tile); the
+ * outputs equal splat_rasterize_bwd's (same kernels;
  * additions can differ in order only among a tile's four quadrant waves). v_depths (may be NULL)
  * selects the depth channel as in splat_rasterize_depth_bwd (then depths and v_out_depth are
  * read). compensate as in the forward: v_opacity is then the raw opacities' cotangent and

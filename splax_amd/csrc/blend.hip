@@ -577,6 +577,9 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     const BlendCommon& C = P.c;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int32_t tile_g = C.order[blockIdx.x];  // (output image, tile)
+    // the order may come from the caller (a kept forward's): an entry out of range skips the
+    // workgroup instead of reading bins out of bounds (uniform, before any barrier)
+    if ((uint32_t)tile_g >= gridDim.x) return;
     const int32_t image_id = tile_g / C.num_tiles;
     const int32_t tile_local = tile_g - image_id * C.num_tiles;
     const int32_t geom_image = P.sel_geom ? image_id : 0;
