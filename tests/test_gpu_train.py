@@ -56,14 +56,24 @@ def _params(n, seed):
     return {k: rng.normal(size=(n, w)).astype(np.float32) for k, w in GROUPS.items()}
 
 
-@pytest.mark.parametrize("n", [1, 1000, 10007])
-def test_adam_step_bit_exact(n):
-    _case(f"adam n={n}")
+def _misaligned(a: np.ndarray) -> torch.Tensor:
+    """A device copy of ``a`` that starts one float into its allocation (4-byte aligned only)."""
+    flat = torch.empty(a.size + 1, device="cuda", dtype=torch.float32)
+    flat[1:] = _t(a.reshape(-1))
+    return flat[1:].view(a.shape)
+
+
+@pytest.mark.parametrize("n,misalign", [(1, False), (1000, False), (10007, False),
+                                        (10007, True)])
+def test_adam_step_bit_exact(n, misalign):
+    """Four steps and a row reset bit-exact against the oracle, also for parameters that start
+    off a 16-byte boundary (views one float into their allocation)."""
+    _case(f"adam n={n} misalign={misalign}")
     rng = np.random.default_rng(n)
     ref = _params(n, n)
     mu = {k: np.zeros_like(v) for k, v in ref.items()}
     nu = {k: np.zeros_like(v) for k, v in ref.items()}
-    dev = {k: _t(v) for k, v in ref.items()}
+    dev = {k: (_misaligned(v) if misalign else _t(v)) for k, v in ref.items()}
     opt = optim.Adam(dev, LRS)
     for step in range(1, 5):
         grads = {k: (rng.normal(size=v.shape) * 10.0 ** rng.uniform(-6, 1)).astype(np.float32)
