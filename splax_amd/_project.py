@@ -6,40 +6,23 @@ every gradient; ``opacity_compensation`` (:95-117) and ``transform_ids`` (:120-1
 as plain tensor code.
 
 Batching. The reference folds ``jax.vmap`` over cameras into one launch (splax/_batching.py). Here
-the same launch is reached by passing a leading batch dimension: ``viewmat`` of shape (B, 4, 4)
-and/or gaussian parameters of shape (B, N, ...). Unbatched operands are shared across the batch
-(read at the gaussian index), batched ones at the flat index; gradients of shared operands are
-summed over the batch, as jax does for broadcast vmap inputs.
+the same launch is reached by passing leading batch dimensions: ``viewmat`` of shape (..., 4, 4)
+and/or gaussian parameters of shape (..., N, ...), any number of them, aligned from the right as in
+broadcasting; they fold into one flat batch, outer axis major (``_batching``). Unbatched operands
+are shared across the batch (read at the gaussian index), batched ones at the flat index;
+gradients of shared operands are summed over the batch, as jax does for broadcast vmap inputs.
 """
 
 from __future__ import annotations
 
 from collections.abc import Sequence
 
+import math
+
 import torch
 
 from splax_amd import _ops
-
-
-def _batch_of(t: torch.Tensor, base_ndim: int, name: str) -> int | None:
-    if t.ndim == base_ndim:
-        return None
-    if t.ndim == base_ndim + 1:
-        return int(t.shape[0])
-    raise ValueError(f"{name}: expected {base_ndim} or {base_ndim + 1} dims, got {tuple(t.shape)}")
-
-
-def resolve_batch(**named: tuple[torch.Tensor, int]) -> int | None:
-    """Common leading batch size of the batched operands (None if all are unbatched)."""
-    B = None
-    for name, (t, nd) in named.items():
-        b = _batch_of(t, nd, name)
-        if b is None:
-            continue
-        if B is not None and b != B:
-            raise ValueError(f"inconsistent batch sizes: {B} vs {b} ({name})")
-        B = b
-    return B
+from splax_amd._batching import batch_shape, fold
 
 
 def _flat(t: torch.Tensor, width: int) -> torch.Tensor:
@@ -126,9 +109,11 @@ def project(mean3ds: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor,
     Same arguments and outputs as splax.project (splax/_project/_project.py:25-92): quats are wxyz,
     outputs are xys (N, 2), depths (N, 1), radii (N, 1) int32, conics (N, 3), num_tiles_hit (N, 1)
     and the inclusive prefix sum cum_tiles_hit (N, 1) (int32; the reference returns uint32, which
-    torch does not support as a general dtype). With a leading batch dimension B on viewmat and/or
-    the gaussian parameters, every output gains it, and cum_tiles_hit is global over the batch.
-    Gradients flow to means, scales, quats, viewmat and gaussian_transforms.
+    torch does not support as a general dtype). With leading batch dimensions on viewmat and/or
+    the gaussian parameters (any number, broadcast against each other: the nested vmap of
+    splax/_batching.py), every output gains the broadcast batch shape, and cum_tiles_hit is
+    global over the flattened batch. Gradients flow to means, scales, quats, viewmat and
+    gaussian_transforms.
     """
     n = int(mean3ds.shape[-2])
     if c is None:
@@ -144,11 +129,14 @@ def project(mean3ds: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor,
         K = int(gaussian_transforms.shape[-3])
     opacities = opacities.reshape(*opacities.shape[:-2], n) if opacities.shape[-1] == 1 \
         and opacities.ndim >= 2 else opacities
-    B = resolve_batch(means=(mean3ds, 2), scales=(scales, 2), quats=(quats, 2),
-                      viewmat=(viewmat, 2), opacities=(opacities, 1),
-                      gaussian_transforms=(gaussian_transforms, 3))
-    batched = B is not None
-    Bv = B if batched else 1
+    S = batch_shape(dict(means=(mean3ds, 2), scales=(scales, 2), quats=(quats, 2),
+                         viewmat=(viewmat, 2), opacities=(opacities, 1),
+                         gaussian_transforms=(gaussian_transforms, 3)))
+    mean3ds, scales, quats = fold(mean3ds, 2, S), fold(scales, 2, S), fold(quats, 2, S)
+    viewmat, opacities = fold(viewmat, 2, S), fold(opacities, 1, S)
+    gaussian_transforms = fold(gaussian_transforms, 3, S)
+    batched = len(S) > 0
+    Bv = math.prod(S) if batched else 1
     # The reference rolls wxyz to its kernel's xyzw here (splax/_project/_project.py:74-76);
     # the library reads wxyz directly and returns the quaternion gradient in wxyz.
     statics = (n, Bv, K, has_tf, tuple(img_shape), tuple(map(float, f)), tuple(map(float, c)),
@@ -156,7 +144,7 @@ def project(mean3ds: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor,
     xys, depths, radii, conics, nth, cum = _ProjectFn.apply(
         mean3ds, scales, quats, viewmat, opacities, gaussian_transforms,
         transform_ids.to(torch.int32), statics)
-    lead = (Bv, n) if batched else (n,)
+    lead = (*S, n)
     return (xys.reshape(*lead, 2), depths.reshape(*lead, 1), radii.reshape(*lead, 1),
             conics.reshape(*lead, 3), nth.reshape(*lead, 1), cum.reshape(*lead, 1))
 

@@ -9,10 +9,12 @@ and conics, and on the depth path also depths.
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 from splax_amd import _ops
-from splax_amd._project import resolve_batch
+from splax_amd._batching import batch_shape, fold
 
 
 def key_layout(B: int, H: int, W: int) -> dict:
@@ -87,16 +89,16 @@ class _RasterizeFn(torch.autograd.Function):
             fold=fold_here)
         v_colors, v_opac, v_xy, v_conic = grads[:4]
 
-        def fold(g: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
+        def rows_of(g: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
             if like.numel() == g.numel():
                 return g.reshape(like.shape)
             return g.reshape(B, -1).sum(0).reshape(like.shape)  # shared over the batch
 
         # the depths cotangent exists only on the depth path
         # (splax/_rasterize/_rasterize.py:231 vs :357)
-        v_depths = fold(grads[4], depths) if render_depth else None
-        return (fold(v_colors, colors), fold(v_opac, opac), None, None, fold(v_xy, xys),
-                v_depths, None, fold(v_conic, conics), None, None)
+        v_depths = rows_of(grads[4], depths) if render_depth else None
+        return (rows_of(v_colors, colors), rows_of(v_opac, opac), None, None, rows_of(v_xy, xys),
+                v_depths, None, rows_of(v_conic, conics), None, None)
 
 
 def _rasterize_checked(colors, opacities, background, xys, depths, radii, conics, cum_tiles_hit,
@@ -107,9 +109,39 @@ def _rasterize_checked(colors, opacities, background, xys, depths, radii, conics
     H, W = img_shape
     if map_opacities is None:
         map_opacities = opacities
-    B = resolve_batch(xys=(xys, 2), conics=(conics, 2))
-    batched = B is not None
-    Bg = B if batched else 1
+    per_g = lambda t: t.reshape(*t.shape[:-2], n) if t.ndim >= 2 and t.shape[-1] == 1 \
+        and t.shape[-2] == n else t  # noqa: E731 ((..., N, 1) -> (..., N))
+    opacities, map_opacities = per_g(opacities), per_g(map_opacities)
+    glead = tuple(xys.shape[:-2])
+    G = math.prod(glead)
+    if (depths.numel() != G * n or radii.numel() != G * n or cum_tiles_hit.numel() != G * n
+            or conics.numel() != G * n * 3):
+        raise ValueError(
+            f"geometry rows ({xys.numel() // 2}) do not match {G} image(s) of {n} gaussians")
+    # geometry, colours, opacities and background broadcast to one batch shape, folded into one
+    # flat batch (the nested vmap of splax/_batching.py)
+    S = batch_shape(dict(xys=(xys, 2), conics=(conics, 2), colors=(colors, 2),
+                         opacities=(opacities, 1), map_opacities=(map_opacities, 1),
+                         background=(background, 1)))
+    Bg = math.prod(S) if S else 1
+    if S:
+        if G == Bg:
+            xys, conics = xys.reshape(Bg, n, 2), conics.reshape(Bg, n, 3)
+            depths, radii = depths.reshape(Bg, n), radii.reshape(Bg, n)
+            cum_tiles_hit = cum_tiles_hit.reshape(Bg * n)
+        else:
+            # geometry batched over some axes only: the library takes one geometry item per
+            # (image, gaussian), so it is tiled / repeated like any partly batched operand, and
+            # the tile-count prefix, global over the batch, is formed again for the new order
+            xys, conics = fold(xys, 2, S, True), fold(conics, 2, S, True)
+            depths = fold(depths.reshape(*glead, n), 1, S, True)
+            radii = fold(radii.reshape(*glead, n), 1, S, True)
+            flat = cum_tiles_hit.reshape(-1).to(torch.int64)
+            nth = torch.diff(flat, prepend=flat.new_zeros(1))
+            nth = fold(nth.reshape(*glead, n), 1, S, True)
+            cum_tiles_hit = torch.cumsum(nth.reshape(-1), 0).to(torch.int32)
+        colors, opacities = fold(colors, 2, S), fold(opacities, 1, S)
+        map_opacities, background = fold(map_opacities, 1, S), fold(background, 1, S)
     if cum_tiles_hit.numel() != Bg * n or xys.numel() != Bg * n * 2:
         raise ValueError(
             f"geometry rows ({xys.numel() // 2}) do not match {Bg} image(s) of {n} gaussians")
@@ -127,10 +159,10 @@ def _rasterize_checked(colors, opacities, background, xys, depths, radii, conics
                                           depths, radii, conics, cum_tiles_hit,
                                           (n, Bg, (int(H), int(W)), render_depth,
                                            bool(compensate)))
-    img = img.reshape(Bg, H, W, 3) if batched else img.reshape(H, W, 3)
+    img = img.reshape(*S, H, W, 3)
     if not render_depth:
         return img, None
-    return img, (depth.reshape(Bg, H, W) if batched else depth.reshape(H, W))
+    return img, depth.reshape(*S, H, W)
 
 
 def rasterize(colors: torch.Tensor, opacities: torch.Tensor, background: torch.Tensor,
@@ -139,10 +171,11 @@ def rasterize(colors: torch.Tensor, opacities: torch.Tensor, background: torch.T
               map_opacities: torch.Tensor | None = None) -> torch.Tensor:
     """Blend projected gaussians into an (H, W, 3) image (splax/_rasterize/_rasterize.py:24-60).
 
-    Geometry (xys, depths, radii, conics, cum_tiles_hit) with a leading batch dimension B renders
-    B images in one launch and returns (B, H, W, 3); colors / opacities may be shared (N, ...) or
-    per image (B, N, ...), background (3,) or (B, 3). map_opacities (default: opacities) drive the
-    tile intersection only and carry no gradient.
+    Geometry (xys, depths, radii, conics, cum_tiles_hit) with leading batch dimensions S (as
+    project returns them for batched cameras) renders prod(S) images in one launch and returns
+    (*S, H, W, 3); colors / opacities may be shared (N, ...) or batched (..., N, ...), background
+    (3,) or (..., 3), all broadcast against S (the nested vmap of splax/_batching.py).
+    map_opacities (default: opacities) drive the tile intersection only and carry no gradient.
     """
     return _rasterize_checked(colors, opacities, background, xys, depths, radii, conics,
                               cum_tiles_hit, img_shape, map_opacities, False)[0]

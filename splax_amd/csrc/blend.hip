@@ -512,6 +512,7 @@ struct BlendBwdParams {
     const int32_t* pos; int64_t M;
     const float* v_out_depth; int64_t vdepth_rows;  // kDepth
     float* rgrad;  // [images][M][NG], images = 1 when geometry is batched, else B_out
+    uint32_t* dev_err;  // the device error word: kDevErrKeptLists when a kept list is bad
 };
 
 // Partial sums of one intersection: v_colour (3), v_conic (3), the two sums sum v_sigma * dx,
@@ -577,15 +578,25 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     const BlendCommon& C = P.c;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int32_t tile_g = C.order[blockIdx.x];  // (output image, tile)
-    // the order may come from the caller (a kept forward's): an entry out of range skips the
-    // workgroup instead of reading bins out of bounds (uniform, before any barrier)
-    if ((uint32_t)tile_g >= gridDim.x) return;
+    // The order and the bins may come from the caller (a kept forward's). An order entry out of
+    // range skips the workgroup, and a bin range outside [0, M] is clamped to it, so nothing is
+    // read out of bounds; either sets kDevErrKeptLists in the device error word, because the
+    // gradients of that call are then not the forward's (uniform, before any barrier).
+    if ((uint32_t)tile_g >= gridDim.x) {
+        if (threadIdx.x == 0) atomicOr(P.dev_err, kDevErrKeptLists);
+        return;
+    }
     const int32_t image_id = tile_g / C.num_tiles;
     const int32_t tile_local = tile_g - image_id * C.num_tiles;
     const int32_t geom_image = P.sel_geom ? image_id : 0;
     const int tile_x = tile_local % C.tiles_x, tile_y = tile_local / C.tiles_x;
     const int32_t gtile = geom_image * C.num_tiles + tile_local;
-    const int32_t range_start = C.bins[2 * gtile], range_end = C.bins[2 * gtile + 1];
+    int32_t range_start = C.bins[2 * gtile], range_end = C.bins[2 * gtile + 1];
+    if (range_start < 0 || (int64_t)range_end > P.M) {
+        if (threadIdx.x == 0) atomicOr(P.dev_err, kDevErrKeptLists);
+        range_start = imaxw(range_start, 0);
+        range_end = (int32_t)((int64_t)range_end > P.M ? P.M : (int64_t)range_end);
+    }
     if (range_end <= range_start) return;  // uniform per workgroup
     int i, j;
     tile_pixel(tid, tile_x, tile_y, i, j);
@@ -869,6 +880,7 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
         P.pos = a.sorted_pos; P.M = a.M;
         P.v_out_depth = a.v_out_depth; P.vdepth_rows = a.vdepth_rows;
         P.rgrad = a.rgrad;
+        P.dev_err = a.dev_err;
         hipEvent_t ka, kb;  // null unless this kernel is timed
         (void)kernel_timer_events(kKernelBlendBwd, &ka, &kb);
         if (depth)

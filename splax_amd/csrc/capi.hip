@@ -460,6 +460,8 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
                               "num_transforms / B * num_transforms)");
     if (total >= ((int64_t)1 << 31))
         return fail(kErrArgs, "project_fwd: more than 2^31 items");
+    // xys rows are stored as one 8-byte vector each
+    if ((uintptr_t)xys & 7) return fail(kErrArgs, "project_fwd: xys must be 8-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
     DeviceScratch& sc = scratch_for_current_device();
     ScratchUse use(sc, s);
@@ -517,6 +519,9 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
     if (fold_shared && (rows_means != num_gaussians || rows_scales != num_gaussians ||
                         rows_quats != num_gaussians))
         return fail(kErrArgs, "project_bwd: folding needs shared means, scales and quats");
+    // v_quat rows are stored as one 16-byte vector each
+    if ((uintptr_t)v_quat & 15)
+        return fail(kErrArgs, "project_bwd: v_quat must be 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
     ProjectBwdArgs a;
     a.means = means3d; a.rows_means = rows_means;
@@ -552,6 +557,8 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
 static int check_raster(const RasterInputs& in, int32_t B_out) {
     if (in.n <= 0 || in.B_geom <= 0 || in.img_h <= 0 || in.img_w <= 0)
         return fail(kErrArgs, "rasterize: invalid sizes");
+    // xys rows are read as one 8-byte vector each
+    if ((uintptr_t)in.xys & 7) return fail(kErrArgs, "rasterize: xys must be 8-byte aligned");
     if (in.rows_colors < in.n || in.rows_opac < in.n || in.rows_map_opac < in.n ||
         in.rows_bg < 1)
         return fail(kErrArgs, "rasterize: operand has fewer rows than num_gaussians");
@@ -743,6 +750,7 @@ static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptL
     a.sorted_pos = pos;
     a.M = M;
     a.rgrad = sc.rgrad;
+    a.dev_err = sc.tickets + kDeviceError;
     StageTimer tm(s, kStageBlendBwd);
     if (!recs && M > 0) {
         rc = launch_pack_records(in, sc.recs, s);
@@ -815,6 +823,8 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
                              int32_t compensate) {
     if (capacity < 0 || !tile_bins || (capacity > 0 && (!sorted_ids || !sorted_pos)))
         return fail(kErrArgs, "rasterize_fwd_keep: missing sorted-list buffers");
+    if ((uintptr_t)records & 15)
+        return fail(kErrArgs, "rasterize_fwd_keep: records must be 16-byte aligned");
     const RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac,
                                           map_opacities, rows_map_opac, background, rows_bg, xys,
                                           depths, radii, conics, cum_tiles_hit, num_gaussians, B,
@@ -847,6 +857,8 @@ int splat_rasterize_bwd_sorted(splat_stream_t stream, const float* colors, int64
     if (num_intersects < 0 || !tile_bins ||
         (num_intersects > 0 && (!sorted_ids || !sorted_pos)))
         return fail(kErrArgs, "rasterize_bwd_sorted: invalid sorted lists");
+    if ((uintptr_t)records & 15)
+        return fail(kErrArgs, "rasterize_bwd_sorted: records must be 16-byte aligned");
     RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac, opacities,
                                     rows_opac, background, rows_bg, xys, depths, nullptr, conics,
                                     cum_tiles_hit, num_gaussians, B_geom, img_h, img_w);

@@ -11,8 +11,11 @@
 // polls cross the eight XCD-local L2s.
 //
 // project_bwd: one thread per flat item, restating _project_bwd_kernel
-// (splax/_project/_kernels.py:356-484); the per-image viewmat gradient is reduced per wave with
-// DPP, then per workgroup in LDS, and added with one atomic per entry per workgroup.
+// (splax/_project/_kernels.py:356-484); the per-image viewmat gradient (formed only when asked
+// for) is reduced per wave with DPP, then per workgroup in LDS into 12 partials per (image,
+// workgroup), which viewmat_reduce_kernel sums in a fixed order. The transform gradient follows
+// the reference's three cases: a workgroup whose gaussians share one transform reduces in LDS
+// and adds with one atomic per entry, a workgroup on a slice boundary adds per thread.
 #include "splat_common.hpp"
 #include "splat_internal.hpp"
 
@@ -577,7 +580,8 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
         int32_t tmin = block_min_i32(in_range ? tf_id : 2147483647, s_tf);
         int32_t tmax = block_max_i32(in_range ? tf_id : (-2147483647 - 1), s_tf);
         (void)id;
-        if (tmin == tmax && tmin >= 0) {
+        // ids at or beyond num_transforms are static (apply_transform), like negative ones
+        if (tmin == tmax && tmin >= 0 && tmin < P.num_transforms) {
             __syncthreads();
             float rt[12];
 #pragma unroll

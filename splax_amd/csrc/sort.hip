@@ -3,12 +3,11 @@
 // splax/_rasterize/_sort/_kernels.py:28-153,214-241; the sort replaces warp-lang's
 // radix_sort_pairs (called at splax/_rasterize/_sort/_sort.py:136).
 //
-// Sort design: one global histogram launch counts every pass's 8-bit digits of every key. Each
-// pass is then reduce-then-scan over 8192-key partitions: (1) every partition counts its digits,
-// (2) one workgroup per digit scans that digit's counts over the partitions from the digit's
-// global base, (3) every partition ranks its keys stably with ballot-based digit matching per
-// wave and scatters keys and values through LDS so that each digit's run (about 32 keys) leaves
-// as a contiguous write. No partition waits on another: on MI355X the eight XCDs have separate
+// Sort design: each pass is reduce-then-scan over partitions of 4096 or 8192 keys: (1) every
+// partition counts its digits, (2) one workgroup per digit scans that digit's counts over the
+// partitions and writes the digit's total, (3) every partition ranks its keys stably with
+// ballot-based digit matching per wave and scatters keys and values through LDS so that each
+// digit's run (about 32 keys) leaves as a contiguous write. No partition waits on another: on MI355X the eight XCDs have separate
 // L2s, so the per-digit status polling of a single-pass (look-back) sort costs device-scope
 // round trips and partial-line writes that the extra count read does not. Ranking follows
 // position order (wave-striped items, lanes in order, waves in order, partitions in index

@@ -97,6 +97,10 @@ enum : int {
     kDeviceError = 63,   // device error word in `tickets` (bit flags, see kDevErr*)
     kNumTickets = 64,
 };
+// Bits of the device error word (splat_check_device).
+enum : uint32_t {
+    kDevErrKeptLists = 1u,  // a kept tile order / tile-bin entry was out of range (bwd_sorted)
+};
 
 // Grow-only per-device scratch, the counterpart of splax/_cache.py:52-90. The intersection
 // buffers grow with 1.25x headroom; everything is freed by splat_clear_cache().
@@ -253,6 +257,7 @@ struct BlendBwdArgs {
     const float* v_out_depth = nullptr; int64_t vdepth_rows = 0; float* v_depths = nullptr;
     const float4* recs = nullptr;  // launch_pack_records output for the same inputs
     int32_t fold = 0;  // v_colors / v_opacity summed over the B_out images (n rows)
+    uint32_t* dev_err = nullptr;  // the device's error word (DeviceScratch::tickets)
 };
 // order: scratch of B_out * num_tiles for the tile dispatch order; kept_order (may be null) is the
 // order a forward over the same bins wrote, used instead when B_out == in.B_geom.

@@ -174,3 +174,56 @@ def test_training_entry_points_validate_before_touching_the_device():
     assert lib.splat_mcmc_compute_relocation(None, None, None, None, 4, 0, None,
                                              None) == _lib.ERR_ARGS
     assert b"binomial" in lib.splat_last_error()
+
+
+def _reference_fold_two_axes(x, outer: bool, inner: bool, A: int, Bn: int):
+    """The reference's nested_vmap rule (splax/_batching.py:91-100) applied for an inner vmap of
+    size Bn then an outer one of size A: per operand, the flat rows it hands the kernel."""
+    # inner vmap: batched operands keep their rows, others stay shared
+    if inner and outer:  # folded before and newly batched: reshape(sz * cur)
+        return x.reshape(A * Bn, *x.shape[2:])
+    if inner:  # folded before, not newly batched: tile over the outer axis
+        return x.repeat(A, *(1,) * (x.ndim - 1))
+    if outer:  # newly batched, not folded before: repeat each row over the inner axis
+        return x.repeat_interleave(Bn, dim=0)
+    return x  # shared
+
+
+@pytest.mark.parametrize("outer,inner", [(True, True), (True, False), (False, True),
+                                         (False, False)])
+def test_nested_batch_fold_matches_reference_rule(outer, inner):
+    """splax_amd._batching folds leading axes exactly as the reference's nested vmap flattens
+    them: outer axis major, tile for inner-only, repeat for outer-only, shared otherwise."""
+    from splax_amd._batching import batch_shape, fold
+
+    A, Bn, n = 3, 4, 5
+    base = torch.arange(n * 3, dtype=torch.float32).reshape(n, 3)
+    full = base + 100 * torch.arange(A * Bn, dtype=torch.float32).reshape(A, Bn, 1, 1)
+    if outer and inner:
+        x, ref_in = full, full
+    elif outer:
+        x = full[:, :1]  # (A, 1, n, 3)
+        ref_in = x[:, 0]
+    elif inner:
+        x = full[0]  # (Bn, n, 3): aligned from the right, the inner axis
+        ref_in = x
+    else:
+        x, ref_in = base, base
+    other = torch.zeros((A, Bn, 4, 4))  # a fully batched operand fixes the batch shape
+    S = batch_shape({"x": (x, 2), "viewmat": (other, 2)})
+    assert S == (A, Bn)
+    got = fold(x, 2, S)
+    want = _reference_fold_two_axes(ref_in, outer, inner, A, Bn)
+    assert torch.equal(got, want)
+
+
+def test_nested_batch_shapes_and_errors():
+    from splax_amd._batching import batch_shape, fold
+
+    x = torch.zeros((2, 1, 7, 3))
+    v = torch.zeros((3, 4, 4))
+    assert batch_shape({"x": (x, 2), "v": (v, 2)}) == (2, 3)
+    assert fold(torch.zeros((1, 1, 7, 3)), 2, (2, 3)).shape == (7, 3)  # size-1 axes: shared
+    assert fold(x, 2, ()).shape == x.shape
+    with pytest.raises(ValueError, match="inconsistent batch shapes"):
+        batch_shape({"x": (torch.zeros((2, 7, 3)), 2), "v": (torch.zeros((3, 4, 4)), 2)})

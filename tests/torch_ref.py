@@ -27,14 +27,21 @@ def quat_rotation_wxyz(q: torch.Tensor) -> torch.Tensor:
 
 
 def project_ref(means, scales, quats_wxyz, viewmat, *, f, c, img_shape, glob_scale=1.0,
-                clamp=True):
-    """Returns xys (N,2), depths (N,), conics (N,3), cov2d (N,2,2) in float64."""
+                clamp=True, tf_R=None, tf_t=None):
+    """Returns xys (N,2), depths (N,), conics (N,3), cov2d (N,2,2) in float64.
+
+    tf_R (N,3,3) / tf_t (N,3), when given, move each gaussian rigidly before the camera: the mean
+    becomes tf_R mean + tf_t and the covariance factor tf_R R(q) S (splax/_project/_kernels.py:
+    627-664)."""
     H, W = img_shape
     Rv = viewmat[:3, :3]
     tv = viewmat[:3, 3]
-    p = means @ Rv.T + tv
     R = quat_rotation_wxyz(quats_wxyz)
     M = R * (glob_scale * scales)[:, None, :]
+    if tf_R is not None:
+        means = (tf_R @ means[..., None])[..., 0] + tf_t
+        M = tf_R @ M
+    p = means @ Rv.T + tv
     V = M @ M.transpose(-1, -2)
     tz = p[:, 2]
     lim_x = 1.3 * 0.5 * W / f[0]
