@@ -49,6 +49,27 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
                       int32_t* radii, float* conics, int32_t* num_tiles_hit,
                       int32_t* cum_tiles_hit, int32_t quats_wxyz);
 
+/* No counterpart in the reference: splat_project_fwd for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, validation and outputs as splat_project_fwd, bit for bit; the projection's
+ * chunk-total scratch lives in a fixed device array of 65536 entries (256 KiB per device, held
+ * until the process ends), so total is at most 65536 * 1024 = 67,108,864 items (status 1
+ * beyond). It calls no allocating routine and uses none of the library's per-device scratch.
+ * Every call on one device shares that array: calls that overlap on one device (different
+ * streams or threads) race on it and must be serialized by the caller. */
+int splat_project_fwd_noalloc(splat_stream_t stream, const float* means3d, int64_t rows_means,
+                              const float* scales, int64_t rows_scales, const float* quats,
+                              int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
+                              const float* opacities, int64_t rows_opac,
+                              const float* transforms, int64_t rows_transforms,
+                              const int32_t* transform_ids, int32_t num_gaussians,
+                              int32_t num_transforms, int32_t has_transforms, int64_t total,
+                              int32_t img_h, int32_t img_w, float fx, float fy, float cx,
+                              float cy, float glob_scale, float clip_thresh, float* xys,
+                              float* depths, int32_t* radii, float* conics,
+                              int32_t* num_tiles_hit, int32_t* cum_tiles_hit,
+                              int32_t quats_wxyz);
+
 /* Replaces _project_bwd_warp (splax/_project/_kernels.py:257-341, FFI callable :344-353).
  * Outputs: v_mean3d [B*n,3], v_scale [B*n,3], v_quat [B*n,4] (in the quats layout chosen by
  * quats_wxyz, as splat_project_fwd), v_viewmat [4B,4] (may be NULL: no viewmat gradient is
@@ -167,7 +188,9 @@ int splat_rasterize_fwd_keep(splat_stream_t stream, const float* colors, int64_t
  * again from its inputs, which must be the forward's; tile_order may be NULL: the backward then
  * orders the tiles again, as it also does when B_out != B_geom; the order only schedules the
  * tiles, the outputs do not depend on it; these buffers must be the forward's, unchanged: their
- * contents are not validated, except that a tile_order entry out of range skips that tile); the
+ * contents are not validated, except that a tile_order entry out of range skips that tile and a
+ * bin range outside [0, num_intersects] is clamped, either setting bit 0 of the device error
+ * word, splat_check_device; records must be 16-byte aligned); the
  * outputs equal splat_rasterize_bwd's (same kernels;
  * additions can differ in order only among a tile's four quadrant waves). v_depths (may be NULL)
  * selects the depth channel as in splat_rasterize_depth_bwd (then depths and v_out_depth are
@@ -310,9 +333,10 @@ int splat_set_stage_timing(int stage_mask);
 int splat_get_stage_times(double* ms, int64_t* calls, int32_t n);
 
 /* Waits for the current device and returns (then clears) its device error word: 0 when every
- * kernel ran within its invariants. No kernel of this version waits on another workgroup, so no
- * bit is in use; the word stays for kernels that would need such an invariant. No counterpart in
- * the reference. */
+ * kernel ran within its invariants; bit 0 (value 1) when splat_rasterize_bwd_sorted met a kept
+ * tile order entry or tile-bin range out of range (that tile is then skipped or its range
+ * clamped to [0, M], so nothing is read out of bounds, but the call's gradients are not the
+ * forward's). No counterpart in the reference. */
 int splat_check_device(void);
 
 /* Library ABI version (bumped on any signature change). */

@@ -35,6 +35,8 @@ class AdamGroup(ctypes.Structure):
 _SIGS = {
     "splat_project_fwd": [_vp] + [_vp, _i64] * 6 + [_vp, _i32, _i32, _i32, _i64, _i32, _i32]
     + [_f32] * 6 + [_vp] * 6 + [_i32],
+    "splat_project_fwd_noalloc": [_vp] + [_vp, _i64] * 6 + [_vp, _i32, _i32, _i32, _i64, _i32,
+                                                         _i32] + [_f32] * 6 + [_vp] * 6 + [_i32],
     "splat_project_bwd": [_vp] + [_vp, _i64] * 10 + [_vp, _i32, _i32, _i32, _i32, _f32, _f32,
                                                      _f32] + [_vp] * 5 + [_i32, _i32],
     "splat_rasterize_fwd": [_vp] + [_vp, _i64] * 4 + [_vp] * 5 + [_i32] * 4 + [_vp] * 4,

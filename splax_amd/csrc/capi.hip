@@ -381,7 +381,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 11; }
+int splat_abi_version(void) { return 12; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();
@@ -435,16 +435,20 @@ int splat_get_stage_times(double* ms, int64_t* calls, int32_t n) {
     return 0;
 }
 
-int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
-                      const float* scales, int64_t rows_scales, const float* quats,
-                      int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
-                      const float* opacities, int64_t rows_opac, const float* transforms,
-                      int64_t rows_transforms, const int32_t* transform_ids,
-                      int32_t num_gaussians, int32_t num_transforms, int32_t has_transforms,
-                      int64_t total, int32_t img_h, int32_t img_w, float fx, float fy, float cx,
-                      float cy, float glob_scale, float clip_thresh, float* xys, float* depths,
-                      int32_t* radii, float* conics, int32_t* num_tiles_hit,
-                      int32_t* cum_tiles_hit, int32_t quats_wxyz) {
+}  // extern "C"
+
+// Validates splat_project_fwd's arguments and fills its argument bundle (shared with the
+// no-allocation variant).
+static int project_fwd_args(const float* means3d, int64_t rows_means, const float* scales,
+                            int64_t rows_scales, const float* quats, int64_t rows_quats,
+                            const float* viewmat, int64_t rows_viewmat, const float* opacities,
+                            int64_t rows_opac, const float* transforms, int64_t rows_transforms,
+                            const int32_t* transform_ids, int32_t num_gaussians,
+                            int32_t num_transforms, int32_t has_transforms, int64_t total,
+                            int32_t img_h, int32_t img_w, float fx, float fy, float cx, float cy,
+                            float glob_scale, float clip_thresh, float* xys, float* depths,
+                            int32_t* radii, float* conics, int32_t* num_tiles_hit,
+                            int32_t* cum_tiles_hit, int32_t quats_wxyz, ProjectArgs* out) {
     if (num_gaussians <= 0 || total < 0 || total % num_gaussians != 0 || img_h <= 0 ||
         img_w <= 0)
         return fail(kErrArgs, "project_fwd: invalid sizes");
@@ -462,12 +466,7 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
         return fail(kErrArgs, "project_fwd: more than 2^31 items");
     // xys rows are stored as one 8-byte vector each
     if ((uintptr_t)xys & 7) return fail(kErrArgs, "project_fwd: xys must be 8-byte aligned");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    DeviceScratch& sc = scratch_for_current_device();
-    ScratchUse use(sc, s);
-    int rc = use.rc;
-    if (rc) return rc;
-    ProjectArgs a;
+    ProjectArgs& a = *out;
     a.means = means3d; a.rows_means = rows_means;
     a.scales = scales; a.rows_scales = rows_scales;
     a.quats = quats; a.rows_quats = rows_quats;
@@ -483,11 +482,70 @@ int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_
     a.xys = xys; a.depths = depths; a.radii = radii; a.conics = conics;
     a.num_tiles_hit = num_tiles_hit; a.cum_tiles_hit = cum_tiles_hit;
     a.quats_wxyz = quats_wxyz != 0;
+    return 0;
+}
+
+extern "C" {
+
+int splat_project_fwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
+                      const float* scales, int64_t rows_scales, const float* quats,
+                      int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
+                      const float* opacities, int64_t rows_opac, const float* transforms,
+                      int64_t rows_transforms, const int32_t* transform_ids,
+                      int32_t num_gaussians, int32_t num_transforms, int32_t has_transforms,
+                      int64_t total, int32_t img_h, int32_t img_w, float fx, float fy, float cx,
+                      float cy, float glob_scale, float clip_thresh, float* xys, float* depths,
+                      int32_t* radii, float* conics, int32_t* num_tiles_hit,
+                      int32_t* cum_tiles_hit, int32_t quats_wxyz) {
+    ProjectArgs a;
+    int rc = project_fwd_args(means3d, rows_means, scales, rows_scales, quats, rows_quats,
+                              viewmat, rows_viewmat, opacities, rows_opac, transforms,
+                              rows_transforms, transform_ids, num_gaussians, num_transforms,
+                              has_transforms, total, img_h, img_w, fx, fy, cx, cy, glob_scale,
+                              clip_thresh, xys, depths, radii, conics, num_tiles_hit,
+                              cum_tiles_hit, quats_wxyz, &a);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    DeviceScratch& sc = scratch_for_current_device();
+    ScratchUse use(sc, s);
+    rc = use.rc;
+    if (rc) return rc;
     StageTimer tm(s, kStageProject);
     g_last_error.clear();
     rc = launch_project_fwd(a, sc, s);
     if (rc && g_last_error.empty())  // launchers that name their failure set the message
         set_error("project_fwd launch failed");
+    return rc;
+}
+
+int splat_project_fwd_noalloc(splat_stream_t stream, const float* means3d, int64_t rows_means,
+                              const float* scales, int64_t rows_scales, const float* quats,
+                              int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
+                              const float* opacities, int64_t rows_opac,
+                              const float* transforms, int64_t rows_transforms,
+                              const int32_t* transform_ids, int32_t num_gaussians,
+                              int32_t num_transforms, int32_t has_transforms, int64_t total,
+                              int32_t img_h, int32_t img_w, float fx, float fy, float cx,
+                              float cy, float glob_scale, float clip_thresh, float* xys,
+                              float* depths, int32_t* radii, float* conics,
+                              int32_t* num_tiles_hit, int32_t* cum_tiles_hit,
+                              int32_t quats_wxyz) {
+    ProjectArgs a;
+    int rc = project_fwd_args(means3d, rows_means, scales, rows_scales, quats, rows_quats,
+                              viewmat, rows_viewmat, opacities, rows_opac, transforms,
+                              rows_transforms, transform_ids, num_gaussians, num_transforms,
+                              has_transforms, total, img_h, img_w, fx, fy, cx, cy, glob_scale,
+                              clip_thresh, xys, depths, radii, conics, num_tiles_hit,
+                              cum_tiles_hit, quats_wxyz, &a);
+    if (rc) return rc;
+    if (project_fwd_chunks(total) > kNoAllocMaxChunks)
+        return fail(kErrArgs, "project_fwd_noalloc: more than " +
+                                  std::to_string(kNoAllocMaxChunks * 1024) +
+                                  " items (the size of its fixed scratch)");
+    // no library scratch, stage timer or stream bookkeeping: nothing here allocates
+    g_last_error.clear();
+    rc = launch_project_fwd_noalloc(a, static_cast<hipStream_t>(stream));
+    if (rc && g_last_error.empty()) set_error("project_fwd_noalloc launch failed");
     return rc;
 }
 

@@ -653,14 +653,25 @@ viewmat_reduce_kernel(const float* partials, int32_t blocks_per_image, float* v_
             tid < 12 ? ((s_red[0][tid] + s_red[1][tid]) + s_red[2][tid]) + s_red[3][tid] : 0.f;
 }
 
+// Chunks (workgroups) of a projection over `total` items: one chunk total of scratch each.
+int64_t project_fwd_chunks(int64_t total) {
+    const int64_t per_block = (int64_t)kProjFwdThreads * kProjItems;
+    return (total + per_block - 1) / per_block;
+}
+
 int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stream) {
     if (a.total <= 0) return 0;
-    const int64_t per_block = (int64_t)kProjFwdThreads * kProjItems;
-    const int64_t blocks = (a.total + per_block - 1) / per_block;
+    const int64_t blocks = project_fwd_chunks(a.total);
     if (blocks > (int64_t)sc.chunk_sums_cap) {
         int rc = sc.grow_chunk_sums(blocks);
         if (rc) return rc;
     }
+    return launch_project_fwd_into(a, sc.chunk_sums, stream);
+}
+
+int launch_project_fwd_into(const ProjectArgs& a, uint32_t* chunk_sums, hipStream_t stream) {
+    if (a.total <= 0) return 0;
+    const int64_t blocks = project_fwd_chunks(a.total);
     ProjectParams P;
     P.means = a.means; P.rows_means = a.rows_means;
     P.scales = a.scales; P.rows_scales = a.rows_scales;
@@ -676,7 +687,7 @@ int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stre
     P.xys = a.xys; P.depths = a.depths; P.radii = a.radii; P.conics = a.conics;
     P.num_tiles_hit = a.num_tiles_hit; P.cum_tiles_hit = a.cum_tiles_hit;
     P.wxyz = a.quats_wxyz;
-    P.chunk_sums = sc.chunk_sums;
+    P.chunk_sums = chunk_sums;
     hipLaunchKernelGGL(project_fwd_kernel, dim3((unsigned)blocks), dim3(kProjFwdThreads), 0, stream,
                        P);
     if (blocks > 1) {
@@ -731,6 +742,48 @@ int launch_project_bwd(const ProjectBwdArgs& a, DeviceScratch& sc, hipStream_t s
         hipLaunchKernelGGL(viewmat_reduce_kernel, dim3((unsigned)a.B), dim3(kProjThreads), 0,
                            stream, sc.view_partials, blocks_per_image, a.v_viewmat);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
+}
+
+// ------------------------------------------------------------------ projection without allocation
+// splat_project_fwd_noalloc keeps its chunk totals in this fixed array of kNoAllocMaxChunks
+// uint32 (256 KiB), which each device the library runs on holds until the process ends. In host
+// code `scratch` names a host-side stand-in, not the device array: its device address comes from
+// hipGetSymbolAddress, once per device with that device current, and only that address is
+// passed to kernels. Every no-allocation call on a device shares the array, so such calls must
+// not overlap on one device (they would race on it); nothing in it needs to start at zero (the
+// projection writes every chunk total before the scan reads it).
+static __device__ __align__(256) uint32_t scratch[kNoAllocMaxChunks];
+
+constexpr int kNoAllocDevices = 64;
+static std::mutex g_noalloc_mu;
+static uint32_t* g_noalloc_scratch[kNoAllocDevices] = {};
+
+int launch_project_fwd_noalloc(const ProjectArgs& a, hipStream_t stream) {
+    if (project_fwd_chunks(a.total) > kNoAllocMaxChunks)
+        return fail(kErrArgs, "project_fwd_noalloc: more than " +
+                                  std::to_string(kNoAllocMaxChunks * kProjFwdThreads) +
+                                  " items (the fixed scratch holds " +
+                                  std::to_string(kNoAllocMaxChunks) + " chunk totals)");
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoAllocDevices)
+        return fail(kErrRuntime, "project_fwd_noalloc: no usable current device");
+    uint32_t* chunk_sums = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_noalloc_mu);
+        if (!g_noalloc_scratch[dev]) {  // set-up, once per device
+            void* ptr = nullptr;
+            const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || ptr == nullptr) {
+                (void)hipGetLastError();
+                return fail(kErrRuntime,
+                            std::string("project_fwd_noalloc: hipGetSymbolAddress failed: ") +
+                                hipGetErrorString(e));
+            }
+            g_noalloc_scratch[dev] = static_cast<uint32_t*>(ptr);
+        }
+        chunk_sums = g_noalloc_scratch[dev];
+    }
+    return launch_project_fwd_into(a, chunk_sums, stream);
 }
 
 }  // namespace splat

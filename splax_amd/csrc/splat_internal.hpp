@@ -203,6 +203,13 @@ void release_train_scratch();
 int fill_zero_f32(float* p, int64_t n, hipStream_t stream);
 int fill_zero_i32(int32_t* p, int64_t n, hipStream_t stream);
 int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stream);
+// The projection with its chunk-total scratch (project_fwd_chunks(a.total) uint32) supplied.
+int launch_project_fwd_into(const ProjectArgs& a, uint32_t* chunk_sums, hipStream_t stream);
+int64_t project_fwd_chunks(int64_t total);
+// The projection with no allocation: its chunk totals in a fixed device array of
+// kNoAllocMaxChunks entries per device (one per 1024 items).
+constexpr int64_t kNoAllocMaxChunks = 65536;
+int launch_project_fwd_noalloc(const ProjectArgs& a, hipStream_t stream);
 int launch_project_bwd(const ProjectBwdArgs& a, DeviceScratch& sc, hipStream_t stream);
 
 // Optional caller-owned destinations of sort_and_bin: M_known >= 0 skips the count readback
