@@ -13,8 +13,13 @@ The JSON line carries:
   dominant stage).
   Blend work is the reference loop's pair count from the CPU oracle (26 Pc + 16 Pr FLOPs
   forward, 65 Qc + 16 Qr backward); sort+bin bytes are 12G + 32V + 76M + 16T.
+- stages: every stage's average duration per call (HIP events around each stage, in an untimed
+  pass) with its algorithmic bytes or FLOPs per call and the achieved rate against MI355X's peak
+  (HBM 8 TB/s for projection, depth range, emission, sort, bins and the projection backward;
+  FP32 157.3 TFLOP/s for the two blends).
 - cpu_baseline: the CPU oracle (the C restatement of the reference kernels, "port") timed on the
-  host on one full forward+backward frame of the same workload, OpenMP over `cores` threads.
+  host on one full forward+backward frame of the same workload, OpenMP over `cores` threads
+  (the host's share, at most 16), and again on one thread (`single_thread`), with the CPU model.
 """
 
 from __future__ import annotations
@@ -96,6 +101,58 @@ def oracle_leg(scene, threads):
     return (t1 - t0), (t2 - t0), counts
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# Algorithmic work per call of each library stage: (bound, work, unit) from the workload counts
+# (G items, N gaussians, V visible items, M intersections, T tiles, Pc/Pr and Qc/Qr the
+# contributing / rejected pixel-gaussian pairs of the forward / backward walk).
+def stage_work(counts, N, T):
+    G, V, M = counts["G"], counts["V"], counts["M"]
+    fwd_flops = 26 * counts["Pc"] + 16 * counts["Pr"]
+    bwd_flops = 65 * counts["Qc"] + 16 * counts["Qr"]
+    return {
+        "project": ("hbm", 44 * N + 40 * G, "GB/s"),
+        "minmax": ("hbm", 8 * G, "GB/s"),
+        "emit": ("hbm", 4 * G + 32 * V + 8 * M, "GB/s"),
+        "sort": ("hbm", 64 * M, "GB/s"),
+        "bins": ("hbm", 4 * M + 16 * T, "GB/s"),
+        "blend_fwd": ("valu", fwd_flops, "TFLOP/s"),
+        "blend_fwd_kernel": ("valu", fwd_flops, "TFLOP/s"),
+        "blend_bwd": ("valu", bwd_flops, "TFLOP/s"),
+        "blend_bwd_kernel": ("valu", bwd_flops, "TFLOP/s"),
+        "project_bwd": ("hbm", 40 * N + 80 * G, "GB/s"),
+    }
+
+
+def stage_rates(cal, cal_steps, counts, N, T):
+    """Per-stage average ms per call and achieved rate against peak, from a pass with every stage
+    bracketed by HIP events."""
+    out = {}
+    work = stage_work(counts, N, T) if counts else {}
+    for name, (ms, calls) in cal.items():
+        if not calls:
+            continue
+        per_call = ms / calls
+        row = {"ms_per_call": round(per_call, 4), "calls_per_step": round(calls / cal_steps, 2)}
+        if name in work:
+            bound, w, unit = work[name]
+            scale = 1e12 if unit == "TFLOP/s" else 1e9
+            rate = w / (per_call / 1e3) / scale
+            peak = FP32_PEAK_TFLOPS if unit == "TFLOP/s" else HBM_PEAK_GBS
+            row.update(bound=bound, work_per_call=int(w), achieved=round(rate, 2), unit=unit,
+                       frac=round(rate / peak, 4))
+        out[name] = row
+    return out
+
+
 def bench_train(args):
     """Config 4: the full training step (render_log fwd+bwd over B=4 cameras with antialiasing,
     L1, fused Adam, one MCMC relocation), steps/s."""
@@ -172,6 +229,7 @@ def bench_train(args):
                    "optimizer": "adam (5 groups, fused)", "relocate_every": 1,
                    "parallelism": "single-gpu"},
         "stage_ms_per_step": stage_ms_per_step,
+        "stages": stage_rates(cal, cal_steps, None, n, 0),
         "part_ms_per_step": part_ms,
         "roofline": {"kernel": "adam_step", "bound": "hbm",
                      "achieved": round(adam_bytes / adam_s / 1e9, 1) if adam_s > 0 else None,
@@ -294,7 +352,15 @@ def main():
                "kind": "port",
                "sample": f"one full fwd+bwd frame of config {args.config} "
                          f"({scene.n} gaussians, B={B}, {H}x{W}) by the C oracle; "
-                         f"fwd alone {cpu_fwd_s:.2f} s"}
+                         f"fwd alone {cpu_fwd_s:.2f} s",
+               "cpu_model": cpu_model(), "host_logical_cpus": os.cpu_count()}
+        # one thread as well (Warp's CPU device runs a launch on one thread), for frames up to
+        # about 2M items (config 2 takes about 20 s there)
+        if B * scene.n <= 2_000_000 and threads > 1:
+            st_fwd_s, st_s, _ = oracle_leg(scene, 1)
+            cpu["single_thread"] = {"value": round(1.0 / st_s, 4), "unit": "frames/s",
+                                    "cores": 1, "fwd_s": round(st_fwd_s, 3),
+                                    "fwd_bwd_s": round(st_s, 3)}
 
     per_stage = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in stages.items()}
     roofline = None
@@ -337,6 +403,8 @@ def main():
                    "img_shape": [H, W], "loss": "mse", "viewmat_grads": args.config == 3,
                    "parallelism": "single-gpu"},
         "stage_ms_per_step": stage_ms_per_step,
+        "stages": stage_rates(cal, cal_steps, counts, scene.n,
+                              B * ((W + 15) // 16) * ((H + 15) // 16)),
         "counts": counts,
         "roofline": roofline,
         "cpu_baseline": cpu,
