@@ -272,6 +272,7 @@ def main():
     import splax_amd
     from splax_amd import _lib
     from splax_amd.scenes import make_scene
+    from splax_amd.train import mse_loss
 
     dev = torch.device("cuda:0")
     scene = make_scene(args.config, n=args.n)
@@ -298,10 +299,10 @@ def main():
             p.grad = None
         vm.grad = None
         img = forward()
-        # torch's mse_loss (C++ autograd): the library's fused MSE (splax_amd.train.mse_loss, 29 us
-        # of GPU time vs 55) runs as a Python autograd Function, and its host time made this
-        # step host-bound (the count readback in each forward stops the host running ahead)
-        loss = torch.nn.functional.mse_loss(img, target)
+        # the library's fused MSE, one pass each way (29 us of GPU time; torch's mse_loss runs
+        # three kernels and a 25 MB zero fill, 56 us); the host stays ahead of the GPU after
+        # each forward's count readback either way (0.65 ms of queued GPU work at the end)
+        loss = mse_loss(img, target)
         loss.backward()
 
     for _ in range(args.warmup):
