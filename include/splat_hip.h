@@ -230,6 +230,64 @@ int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* dep
  * reference's tests patch: force != 0 makes every sort take the 64-bit key (process-wide). */
 int splat_set_wide_keys(int force);
 
+/* ---------------------------------------------------------------- fused render path
+ * splax.render (splax/_render.py:29-115, project then rasterize, each with its custom VJP) as one
+ * forward and one backward call: the forward's projection also writes each item's packed blend
+ * record and, for the packed key with num_gaussians >= 1024, the per-image depth range of the
+ * visible items, so no record pack and no depth-range pass run; the backward keeps the per-item
+ * v_xy / v_conic / v_depth rows between the blend backward and the projection VJP in library
+ * scratch. Every output equals the two-call path's (splat_project_fwd +
+ * splat_rasterize_fwd_keep, then splat_rasterize_bwd_sorted + splat_project_bwd) bit for bit,
+ * except that sums the GPU forms with float atomics may add in another order. */
+
+/* Forward. Arguments as splat_project_fwd over total = B * num_gaussians items (its outputs xys
+ * .. cum_tiles_hit, every row written) and as splat_rasterize_fwd_keep for colors (rows
+ * num_gaussians or B * num_gaussians), background, the kept lists, records (required, [B *
+ * num_gaussians, 16], 16-byte aligned) and the image outputs; opacities are the raw ones, which
+ * both the projection and, with compensate, the antialiased blend use (splax/_render.py:
+ * 105-110). Status 6 when M > capacity, after the count readback (projection outputs written). */
+int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
+                     const float* scales, int64_t rows_scales, const float* quats,
+                     int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
+                     const float* opacities, int64_t rows_opac, const float* colors,
+                     int64_t rows_colors, const float* background, int64_t rows_bg,
+                     const float* transforms, int64_t rows_transforms,
+                     const int32_t* transform_ids, int32_t num_gaussians,
+                     int32_t num_transforms, int32_t has_transforms, int32_t B, int32_t img_h,
+                     int32_t img_w, float fx, float fy, float cx, float cy, float glob_scale,
+                     float clip_thresh, int32_t quats_wxyz, int32_t compensate, float* xys,
+                     float* depths, int32_t* radii, float* conics, int32_t* num_tiles_hit,
+                     int32_t* cum_tiles_hit, int64_t capacity, int32_t* sorted_ids,
+                     int32_t* sorted_pos, int32_t* tile_bins, float* records,
+                     int32_t* tile_order, float* final_Ts, int32_t* final_idx, float* out_img,
+                     float* out_depth, int64_t* num_intersects);
+
+/* Backward of splat_render_fwd at the same inputs, given its outputs and kept buffers and the
+ * image cotangent (and, with out_depth in the forward, v_out_depth). Outputs: v_means [.,3],
+ * v_scales [.,3], v_quats [.,4] (quats layout as quats_wxyz; 16-byte aligned), v_colors [.,3],
+ * v_opacities [.] (the raw opacities' cotangent), v_viewmat [4B,4] (may be NULL: not formed),
+ * v_transforms [B*num_transforms,4,4] (with has_transforms). Rows: num_gaussians with
+ * fold_shared != 0 (means, scales, quats, colors and opacities all shared: the cotangents summed
+ * over the B images in image order), else B * num_gaussians. */
+int splat_render_bwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
+                     const float* scales, int64_t rows_scales, const float* quats,
+                     int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
+                     const float* opacities, int64_t rows_opac, const float* colors,
+                     int64_t rows_colors, const float* background, int64_t rows_bg,
+                     const float* transforms, int64_t rows_transforms,
+                     const int32_t* transform_ids, int32_t num_gaussians,
+                     int32_t num_transforms, int32_t has_transforms, int32_t B, int32_t img_h,
+                     int32_t img_w, float fx, float fy, float glob_scale, int32_t quats_wxyz,
+                     int32_t compensate, const float* xys, const float* depths,
+                     const int32_t* radii, const float* conics, const int32_t* cum_tiles_hit,
+                     const int32_t* sorted_ids, const int32_t* sorted_pos,
+                     const int32_t* tile_bins, const float* records, const int32_t* tile_order,
+                     int64_t num_intersects, const float* final_Ts, const int32_t* final_idx,
+                     const float* v_out_img, int64_t vout_rows, const float* v_out_depth,
+                     int64_t vdepth_rows, float* v_means, float* v_scales, float* v_quats,
+                     float* v_colors, float* v_opacities, float* v_viewmat,
+                     float* v_transforms, int32_t fold_shared);
+
 /* ---------------------------------------------------------------- training step
  * The config-4 training step around the render: the per-parameter Adam of the trainers and the
  * MCMC relocation of splax.mcmc. All arrays are contiguous float32 device buffers, updated in

@@ -192,6 +192,103 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
     return img, Ts, fidx, KeptSort(ids, pos, bins, M, recs, order), depth
 
 
+class RenderKept(NamedTuple):
+    """What splat_render_fwd keeps for splat_render_bwd: the projection outputs and the
+    rasterizer's kept lists."""
+    xys: torch.Tensor
+    depths: torch.Tensor
+    radii: torch.Tensor
+    conics: torch.Tensor
+    cum: torch.Tensor
+    sort: KeptSort
+
+
+def render_fwd(means, scales, quats_wxyz, colors, opac, viewmat, background, transforms,
+               transform_ids, *, n, B, num_transforms, has_transforms, img_shape, f, c,
+               glob_scale, clip_thresh, compensate=False, render_depth=False):
+    """The fused render forward (splat_render_fwd): projection, sort and blend in one call over
+    B images of n gaussians; quaternions wxyz. Returns (img, Ts, fidx, RenderKept, depth or None).
+    Kept-list capacity as rasterize_fwd_keep."""
+    means, scales, quats_wxyz, colors, opac, viewmat, background, transforms = map(
+        _f32, (means, scales, quats_wxyz, colors, opac, viewmat, background, transforms))
+    transform_ids = _i32(transform_ids)
+    dev = _lib.require_gpu(means, scales, quats_wxyz, colors, opac, viewmat, background)
+    H, W = img_shape
+    total = B * n
+    tiles = ((W + 15) // 16) * ((H + 15) // 16)
+    e = lambda *shape, dt=torch.float32: torch.empty(shape, device=dev, dtype=dt)  # noqa: E731
+    xys, depths, conics = e(total, 2), e(total), e(total, 3)
+    radii, nth, cum = e(total, dt=torch.int32), e(total, dt=torch.int32), e(total, dt=torch.int32)
+    Ts, fidx, img = e(B * H, W), e(B * H, W, dt=torch.int32), e(B * H, W, 3)
+    depth = e(B * H, W) if render_depth else None
+    bins, recs, order = e(B * tiles, 2, dt=torch.int32), e(total, 16), e(B * tiles, dt=torch.int32)
+    key = str(dev)
+    cap = _KEEP_CAPACITY.get(key, 0)
+    m = ctypes.c_int64(0)
+    p = _lib.ptr
+    for _ in range(2):
+        ids = e(max(cap, 1), dt=torch.int32)
+        pos = e(max(cap, 1), dt=torch.int32)
+        with torch.cuda.device(dev):
+            st = _lib.lib().splat_render_fwd(
+                _lib.stream_handle(dev), p(means), rows(means, 3), p(scales), rows(scales, 3),
+                p(quats_wxyz), rows(quats_wxyz, 4), p(viewmat), rows(viewmat, 4), p(opac),
+                opac.numel(), p(colors), rows(colors, 3), p(background), rows(background, 3),
+                p(transforms), rows(transforms, 16), p(transform_ids), n, num_transforms,
+                int(has_transforms), B, H, W, f[0], f[1], c[0], c[1], glob_scale, clip_thresh, 1,
+                int(compensate), p(xys), p(depths), p(radii), p(conics), p(nth), p(cum), cap,
+                p(ids), p(pos), p(bins), p(recs), p(order), p(Ts), p(fidx), p(img), p(depth),
+                ctypes.byref(m))
+        if st == _lib.ERR_TOO_MANY and m.value > cap:
+            cap = int(m.value * 1.25) + 1
+            _KEEP_CAPACITY[key] = cap
+            continue
+        break
+    _lib.check(st, "render")
+    M = int(m.value)
+    if M > _KEEP_CAPACITY.get(key, 0):
+        _KEEP_CAPACITY[key] = int(M * 1.25) + 1
+    kept = RenderKept(xys, depths, radii, conics, cum, KeptSort(ids, pos, bins, M, recs, order))
+    return img, Ts, fidx, kept, depth
+
+
+def render_bwd(means, scales, quats_wxyz, colors, opac, viewmat, background, transforms,
+               transform_ids, kept: RenderKept, final_Ts, final_idx, v_out, *, n, B,
+               num_transforms, has_transforms, img_shape, f, glob_scale, compensate=False,
+               v_out_depth=None, fold=False, want_viewmat=True):
+    """The fused render backward (splat_render_bwd). Returns (v_means, v_scales, v_quats (wxyz),
+    v_colors, v_opac, v_viewmat or None, v_transforms or None), n rows each with ``fold`` (every
+    gaussian operand shared), else B * n."""
+    means, scales, quats_wxyz, colors, opac, viewmat, background, transforms = map(
+        _f32, (means, scales, quats_wxyz, colors, opac, viewmat, background, transforms))
+    v_out = _f32(v_out)
+    vd = None if v_out_depth is None else _f32(v_out_depth)
+    dev = _lib.require_gpu(means, v_out)
+    H, W = img_shape
+    rows_out = n if fold else B * n
+    e = lambda *shape: torch.empty(shape, device=dev, dtype=torch.float32)  # noqa: E731
+    v_means, v_scales, v_quats = e(rows_out, 3), e(rows_out, 3), e(rows_out, 4)
+    v_colors, v_opac = e(rows_out, 3), e(rows_out)
+    v_view = e(B * 4, 4) if want_viewmat else None
+    v_tf = e(B * num_transforms, 4, 4) if has_transforms else None
+    ks = kept.sort
+    p = _lib.ptr
+    with torch.cuda.device(dev):
+        st = _lib.lib().splat_render_bwd(
+            _lib.stream_handle(dev), p(means), rows(means, 3), p(scales), rows(scales, 3),
+            p(quats_wxyz), rows(quats_wxyz, 4), p(viewmat), rows(viewmat, 4), p(opac),
+            opac.numel(), p(colors), rows(colors, 3), p(background), rows(background, 3),
+            p(transforms), rows(transforms, 16), p(_i32(transform_ids)), n, num_transforms,
+            int(has_transforms), B, H, W, f[0], f[1], glob_scale, 1, int(compensate),
+            p(kept.xys), p(kept.depths), p(kept.radii), p(kept.conics), p(kept.cum), p(ks.ids),
+            p(ks.pos), p(ks.bins), p(ks.records), p(ks.order), ks.M, p(final_Ts), p(final_idx),
+            p(v_out), v_out.numel() // (3 * W), p(vd), 0 if vd is None else vd.numel() // W,
+            p(v_means), p(v_scales), p(v_quats), p(v_colors), p(v_opac), p(v_view), p(v_tf),
+            int(fold))
+    _lib.check(st, "render_bwd")
+    return v_means, v_scales, v_quats, v_colors, v_opac, v_view, v_tf
+
+
 def _bwd_outputs(nout, dev, with_depth):
     f = lambda *shape: torch.empty(shape, device=dev, dtype=torch.float32)  # noqa: E731
     return f(nout, 3), f(nout), f(nout, 2), f(nout, 3), (f(nout) if with_depth else None)

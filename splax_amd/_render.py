@@ -11,9 +11,12 @@ from collections.abc import Sequence
 
 import torch
 
-from splax_amd import _lib
-from splax_amd._project import project, transform_ids
-from splax_amd._rasterize import _rasterize_checked
+import math
+
+from splax_amd import _lib, _ops
+from splax_amd._batching import batch_shape, fold
+from splax_amd._project import _no_transforms, transform_ids
+from splax_amd._rasterize import check_key_fits
 
 
 class _LogParamsFn(torch.autograd.Function):
@@ -56,6 +59,88 @@ class _LogParamsFn(torch.autograd.Function):
         return tuple(outs)
 
 
+class _RenderFn(torch.autograd.Function):
+    """project then rasterize (splax/_render.py:94-115) with their custom VJPs
+    (splax/_project/_project.py:142-275, splax/_rasterize/_rasterize.py:105-234) as one library
+    forward and one library backward (splat_render_fwd / splat_render_bwd): the projection packs
+    the blend records and the depth range, and the backward keeps the per-item 2D cotangents in
+    library scratch. Operands are shared ([n, ...]) or batched ([B, n, ...]); the forward
+    keeps the projection outputs and the sorted lists as residuals."""
+
+    @staticmethod
+    def forward(ctx, means, scales, quats, colors, opac, viewmat, background, transforms, tf_ids,
+                statics):
+        n, B, K, has_tf, img_shape, f, c, glob_scale, clip_thresh, compensate, render_depth = \
+            statics
+        flat = lambda t, w: t.reshape(-1, w) if w > 1 else t.reshape(-1)  # noqa: E731
+        img, Ts, fidx, kept, depth = _ops.render_fwd(
+            flat(means, 3), flat(scales, 3), flat(quats, 4), flat(colors, 3), flat(opac, 1),
+            viewmat.reshape(-1, 4), flat(background, 3), transforms.reshape(-1, 4, 4),
+            tf_ids.reshape(-1), n=n, B=B, num_transforms=K, has_transforms=has_tf,
+            img_shape=img_shape, f=f, c=c, glob_scale=glob_scale, clip_thresh=clip_thresh,
+            compensate=compensate, render_depth=render_depth)
+        ks = kept.sort
+        ctx.save_for_backward(means, scales, quats, colors, opac, viewmat, background,
+                              transforms, tf_ids, Ts, fidx, kept.xys, kept.depths, kept.radii,
+                              kept.conics, kept.cum, ks.ids, ks.pos, ks.bins, ks.records,
+                              ks.order)
+        ctx.statics = statics
+        ctx.num_intersects = ks.M
+        ctx.set_materialize_grads(False)
+        if depth is None:
+            depth = Ts.new_empty(())  # placeholder output of the colour-only path (never read)
+            ctx.mark_non_differentiable(depth)
+        return img, depth
+
+    @staticmethod
+    def backward(ctx, v_img, v_depth):
+        (means, scales, quats, colors, opac, viewmat, background, transforms, tf_ids, Ts, fidx,
+         xys, depths, radii, conics, cum, ids, pos, bins, recs, order) = ctx.saved_tensors
+        n, B, K, has_tf, img_shape, f, c, glob_scale, clip_thresh, compensate, render_depth = \
+            ctx.statics
+        H, W = img_shape
+        if v_img is None:
+            v_img = torch.zeros((B * H, W, 3), device=means.device)
+        if render_depth and v_depth is None:
+            v_depth = torch.zeros((B * H, W), device=means.device)
+        shared = [t.numel() == n * w for t, w in ((means, 3), (scales, 3), (quats, 4),
+                                                  (colors, 3), (opac, 1))]
+        fold_here = B > 1 and all(shared)
+        flat = lambda t, w: t.reshape(-1, w) if w > 1 else t.reshape(-1)  # noqa: E731
+        kept = _ops.RenderKept(xys, depths, radii, conics, cum,
+                               _ops.KeptSort(ids, pos, bins, ctx.num_intersects, recs, order))
+        gm, gs, gq, gc, go, gv, gt = _ops.render_bwd(
+            flat(means, 3), flat(scales, 3), flat(quats, 4), flat(colors, 3), flat(opac, 1),
+            viewmat.reshape(-1, 4), flat(background, 3), transforms.reshape(-1, 4, 4),
+            tf_ids.reshape(-1), kept, Ts, fidx, v_img.reshape(-1, 3), n=n, B=B,
+            num_transforms=K, has_transforms=has_tf, img_shape=img_shape, f=f,
+            glob_scale=glob_scale, compensate=compensate,
+            v_out_depth=v_depth.reshape(-1, W) if render_depth else None, fold=fold_here,
+            want_viewmat=ctx.needs_input_grad[5])
+
+        def rows_of(g: torch.Tensor, like: torch.Tensor, w: int) -> torch.Tensor:
+            if g.numel() == like.numel():  # batched, one image, or folded by the library
+                return g.reshape(like.shape)
+            g = g.reshape(B, n, w) if w > 1 else g.reshape(B, n)
+            return g.sum(0).reshape(like.shape)  # shared operand: sum over the batch
+
+        need = ctx.needs_input_grad
+        g_view = None
+        if need[5]:
+            g_view = gv.reshape(B, 4, 4)
+            g_view = g_view.reshape(viewmat.shape) if viewmat.ndim == 3 else g_view.sum(0)
+        g_tf = None
+        if has_tf and need[7]:
+            g_tf = gt.reshape(B, K, 4, 4)
+            g_tf = g_tf.reshape(transforms.shape) if transforms.ndim == 4 else g_tf.sum(0)
+        return (rows_of(gm, means, 3) if need[0] else None,
+                rows_of(gs, scales, 3) if need[1] else None,
+                rows_of(gq, quats, 4) if need[2] else None,
+                rows_of(gc, colors, 3) if need[3] else None,
+                rows_of(go, opac, 1) if need[4] else None,
+                g_view, None, g_tf, None, None)
+
+
 def render(means3d: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor,
            colors: torch.Tensor, opacities: torch.Tensor, *, viewmat: torch.Tensor,
            background: torch.Tensor, img_shape: tuple[int, int], f: tuple[float, float],
@@ -66,23 +151,42 @@ def render(means3d: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor,
     """Render a splat; returns (image, depth-or-None) like splax.render (splax/_render.py:29-115)."""
     if (gaussian_transforms is None) != (gaussian_slices is None):
         raise ValueError("gaussian_transforms and gaussian_slices must be passed together")
-    tf_ids = None
+    n = int(means3d.shape[-2])
+    if c is None:
+        c = (img_shape[1] / 2, img_shape[0] / 2)
+    dev = means3d.device
     if gaussian_transforms is not None and gaussian_slices is not None:
         if tuple(gaussian_transforms.shape[-3:]) != (len(gaussian_slices), 4, 4):
             raise ValueError(
                 f"gaussian_transforms shape {tuple(gaussian_transforms.shape)} does not "
                 f"match {len(gaussian_slices)} slices, expected (K, 4, 4)")
-        tf_ids = transform_ids(means3d.shape[-2], gaussian_slices, device=means3d.device)
-    xys, depths, radii, conics, _, cum = project(
-        means3d, scales, quats, viewmat, opacities=opacities, img_shape=img_shape, f=f, c=c,
-        glob_scale=glob_scale, clip_thresh=clip_thresh, gaussian_transforms=gaussian_transforms,
-        transform_ids=tf_ids)
+        tf_ids = transform_ids(n, gaussian_slices, device=dev)
+        has_tf, K = True, len(gaussian_slices)
+    else:
+        gaussian_transforms, tf_ids = _no_transforms(dev)
+        has_tf, K = False, 1
+    per_g = lambda t: t.reshape(*t.shape[:-2], n) if t.ndim >= 2 and t.shape[-1] == 1 \
+        and t.shape[-2] == n else t  # noqa: E731 ((..., N, 1) -> (..., N))
+    opacities = per_g(opacities)
+    # every operand's leading axes broadcast to one batch shape, folded into one flat batch
+    # (the nested vmap of splax/_batching.py); the batch folds into one launch
+    S = batch_shape(dict(means=(means3d, 2), scales=(scales, 2), quats=(quats, 2),
+                         colors=(colors, 2), opacities=(opacities, 1), viewmat=(viewmat, 2),
+                         background=(background, 1), gaussian_transforms=(gaussian_transforms, 3)))
+    B = math.prod(S) if S else 1
+    ops = [fold(t, w, S) for t, w in ((means3d, 2), (scales, 2), (quats, 2), (colors, 2),
+                                      (opacities, 1), (viewmat, 2), (background, 1),
+                                      (gaussian_transforms, 3))]
+    H, W = img_shape
+    check_key_fits(B, int(H), int(W))
     # antialiased: the blend uses opacities * opacity_compensation(conics, radii) and the tile
     # intersection the raw opacities (splax/_render.py:105-110); the library evaluates the
-    # compensation and its gradient inside the blend's record packing and gradient gather.
-    img, depth = _rasterize_checked(colors, opacities, background, xys, depths, radii, conics,
-                                    cum, img_shape, None, render_depth, compensate=antialiased)
-    return img, depth
+    # compensation and its gradient inside the record packing and the gradient gather.
+    statics = (n, B, K, has_tf, (int(H), int(W)), tuple(map(float, f)), tuple(map(float, c)),
+               float(glob_scale), float(clip_thresh), bool(antialiased), bool(render_depth))
+    img, depth = _RenderFn.apply(*ops[:7], ops[7], tf_ids.to(torch.int32), statics)
+    img = img.reshape(*S, H, W, 3)
+    return img, (depth.reshape(*S, H, W) if render_depth else None)
 
 
 def render_log(means3d: torch.Tensor, log_scales: torch.Tensor, quats: torch.Tensor,

@@ -44,10 +44,6 @@ struct BlendCommon {
     int64_t total;  // geometry rows (B_geom * n): ids outside [0, total) are ignored
 };
 
-// Largest sigma a blend accepts: blend_exp(-87) is still a normal float. An intersection with a
-// larger sigma is rejected, as the exact alpha would be for opacities below 2.4e35 (the CPU oracle
-// applies the same cap).
-constexpr float kBlendSigmaCap = 87.0f;
 
 // Pixel of thread `tid` in its tile: wave w = quadrant (w & 1, w >> 1), row r = lane >> 4 =
 // 4x4 sub-block (r & 1, r >> 1) of the quadrant, lane & 15 = 4x4 raster.
@@ -62,16 +58,6 @@ __device__ __forceinline__ int row_subblock(int tid) {
     const int wave = tid >> 6, row = (tid & 63) >> 4;
     return ((wave >> 1) * 2 + (row >> 1)) * 4 + (wave & 1) * 2 + (row & 1);
 }
-
-// Packed record of one geometry item, 64 bytes (one aligned segment per staged intersection):
-//   r0 = (x, y, a/2, b), r1 = (c/2, o, sigma_max, 0), r2 = (red, green, blue, depth),
-//   r3 = (ex, ey, cull mode, 0).
-// They depend only on the rasterizer's inputs, so a forward's records serve its backward.
-// sigma_max = log(255 o) + 1e-3 bounds sigma where o e^-sigma can still reach 1/255. The cull mode
-// says whether the tile-independent box (+-ex, +-ey) around the centre holds every pixel centre
-// with sigma <= sigma_max (kCullBox), or no pixel can pass (kCullNone: sigma_max < 0), or the box
-// cannot be trusted and every quadrant is kept (kCullKeep).
-enum : uint32_t { kCullBox = 0u, kCullKeep = 1u, kCullNone = 2u };
 
 struct PackParams {
     const float* colors; int64_t rows_colors;
@@ -90,48 +76,10 @@ __global__ void __launch_bounds__(256) pack_records_kernel(PackParams P) {
     const int64_t g = base + threadIdx.x;
     if (g < P.total) {
         const float2 xy = reinterpret_cast<const float2*>(P.xys)[g];
-        const float a = P.conics[3 * g], b = P.conics[3 * g + 1], c = P.conics[3 * g + 2];
-        float o = P.opac[g % P.rows_opac];
-        if (P.compensate) {
-            float rho2;
-            o = o * compensation_rho(a, b, c, rho2);
-        }
         const int64_t cg = g % P.rows_colors;
-        // sigma_max is capped at kBlendSigmaCap, where blend_exp's range ends
-        float smax;
-        if (o > 0.0f) {
-            smax = fminf(__logf(o * 255.0f) + 1e-3f, kBlendSigmaCap);
-        } else {
-            smax = -__builtin_inff();  // o <= 0 or NaN: no pixel accepts it
-        }
-        uint32_t mode = kCullKeep;
-        float ex = 0.0f, ey = 0.0f;
-        if (!(smax >= 0.0f)) {
-            mode = kCullNone;  // every pixel rejected
-        } else {
-            // Points beyond k times the bounding box of {sigma <= smax} have exact
-            // sigma >= k^2 smax. The evaluated sigma differs from the exact one by at most
-            // ~6e-7 * cond(Q) relative (Q the conic), so with cond(Q) <= (a + c)^2 / det < 1e4
-            // and k = 1.01 every point outside the box evaluates above smax.
-            // Worse-conditioned conics keep all four quadrants.
-            const float det = a * c - b * b;
-            const float tr = a + c;
-            const float ex2 = 2.0f * smax * c / det, ey2 = 2.0f * smax * a / det;
-            if (a > 0.0f && c > 0.0f && det > 0.0f && tr * tr < 1e4f * det && ex2 < 1e30f &&
-                ey2 < 1e30f) {
-                ex = sqrtf(ex2) * 1.01f + 0.01f;
-                ey = sqrtf(ey2) * 1.01f + 0.01f;
-                mode = kCullBox;
-            }
-        }
-        float4* r = s_rec + 4 * threadIdx.x;
-        // the blends evaluate sigma = (a/2 dx dx + c/2 dy dy) + b dx dy: halving exactly before
-        // the products leaves every rounding where 0.5 (a dx dx + c dy dy) puts it
-        r[0] = make_float4(xy.x, xy.y, 0.5f * a, b);
-        r[1] = make_float4(0.5f * c, o, smax, 0.0f);
-        r[2] = make_float4(P.colors[3 * cg], P.colors[3 * cg + 1], P.colors[3 * cg + 2],
-                           P.depths ? P.depths[g] : 0.0f);
-        r[3] = make_float4(ex, ey, __uint_as_float(mode), 0.0f);
+        pack_record(xy.x, xy.y, P.conics[3 * g], P.conics[3 * g + 1], P.conics[3 * g + 2],
+                    P.opac[g % P.rows_opac], P.compensate, P.colors + 3 * cg,
+                    P.depths ? P.depths[g] : 0.0f, s_rec + 4 * threadIdx.x);
     }
     __syncthreads();
     const int64_t left = P.total - base;
@@ -767,37 +715,19 @@ struct GatherParams {
     int32_t fold;  // v_colors / v_opacity summed over the images into n rows
 };
 
-// Cotangents of blend_opac = opac * rho(conic) (splax/_render.py:105-109 with
-// splax/_project/_project.py:113-117) for a blend-opacity cotangent vbo, by reverse-mode rules of
-// the reference's expression: sqrt' = 0.5 / rho, maximum / minimum pass 1 strictly inside, 1/2 at
-// a tie and 0 outside. Returns the raw-opacity cotangent and adds the conic cotangent to vc.
-// Items without intersections carry vbo = 0 and a zero conic (rho = 1), so the where(radii > 0)
-// select adds nothing for them.
-__device__ __forceinline__ float compensation_vjp(float vbo, float o, float a, float b, float c,
-                                                  float vc[3]) {
-    float rho2;
-    const float rho = compensation_rho(a, b, c, rho2);
-    const float v_o = vbo * rho;
-    const float v_rho = vbo * o;
-    const float v_cl = v_rho * (0.5f / rho);
-    const float m_lo = rho2 > 0.0f ? 1.0f : (rho2 == 0.0f ? 0.5f : 0.0f);
-    const float y = rho2 > 0.0f ? rho2 : 0.0f;
-    const float m_hi = y < 1.0f ? 1.0f : (y == 1.0f ? 0.5f : 0.0f);
-    const float v_r2 = (v_cl * m_hi) * m_lo;
-    const float v_s = -(kDilation * v_r2);  // through 1 - eps (a + c)
-    const float v_t = kDilation2 * v_r2;    // through eps^2 (a c - b b)
-    vc[0] = vc[0] + (v_s + v_t * c);
-    vc[1] = vc[1] + (-(v_t * b) - v_t * b);
-    vc[2] = vc[2] + (v_s + v_t * a);
-    return v_o;
-}
-
 // With P.fold one thread per gaussian walks the images in order: per-item v_xy / v_conic /
 // v_depths rows as always, the colour and opacity cotangents summed into the gaussian's row.
+// The workgroup's items of one pass (one image with P.fold) read their rows cooperatively
+// (block_gather) when they lie in one contiguous range of rgrad: always with per-item geometry,
+// and with shared geometry when the workgroup's items belong to one output image.
 template <int NG>
 __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
+    __shared__ float s_buf[kGatherChunk * NG];
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= (P.fold ? (int64_t)P.n : P.nout)) return;
+    const int64_t limit = P.fold ? (int64_t)P.n : P.nout;
+    const int64_t t_first = (int64_t)blockIdx.x * 256;
+    const int64_t t_last = (t_first + 255 < limit ? t_first + 255 : limit - 1);
+    const bool valid = t < limit;
     const int32_t images = P.fold ? (int32_t)(P.nout / P.n) : 1;
     float fc0 = 0.f, fc1 = 0.f, fc2 = 0.f, fo = 0.f;
     for (int32_t image = 0; image < images; ++image) {
@@ -808,17 +738,41 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
         gi = og - b * P.n;
         off = b * P.M;
     }
-    int64_t lo = gi > 0 ? (int64_t)P.cum[gi - 1] : 0, hi = P.cum[gi];
-    lo = lo < 0 ? 0 : lo;
-    hi = hi > P.M ? P.M : hi;
-    float s[NG];
-#pragma unroll
-    for (int k = 0; k < NG; ++k) s[k] = 0.0f;
-    for (int64_t e = lo; e < hi; ++e) {
-        const float* r = P.rgrad + (off + e) * NG;
-#pragma unroll
-        for (int k = 0; k < NG; ++k) s[k] += r[k];
+    int64_t lo = 0, hi = 0;
+    if (valid) {
+        lo = gi > 0 ? (int64_t)P.cum[gi - 1] : 0;
+        hi = P.cum[gi];
+        lo = lo < 0 ? 0 : lo;
+        hi = hi > P.M ? P.M : hi;
+        hi = hi < lo ? lo : hi;
     }
+    // the workgroup's range (uniform)
+    const int64_t og_first = P.fold ? (int64_t)image * P.n + t_first : t_first;
+    const int64_t og_last = P.fold ? (int64_t)image * P.n + t_last : t_last;
+    const bool one_range = P.sel_geom || og_first / P.n == og_last / P.n;
+    float s[NG];
+    if (one_range) {
+        int64_t gf = og_first, gl = og_last, woff = 0;
+        if (!P.sel_geom) {
+            const int64_t b = og_first / P.n;
+            gf -= b * P.n;
+            gl -= b * P.n;
+            woff = b * P.M;
+        }
+        int64_t wlo = gf > 0 ? (int64_t)P.cum[gf - 1] : 0, whi = P.cum[gl];
+        wlo = wlo < 0 ? 0 : wlo;
+        whi = whi > P.M ? P.M : whi;
+        block_gather<NG, 256>(P.rgrad, woff, wlo, whi, lo, hi, s_buf, s);
+    } else {
+#pragma unroll
+        for (int k = 0; k < NG; ++k) s[k] = 0.0f;
+        for (int64_t e = lo; e < hi; ++e) {
+            const float* r = P.rgrad + (off + e) * NG;
+#pragma unroll
+            for (int k = 0; k < NG; ++k) s[k] += r[k];
+        }
+    }
+    if (!valid) continue;
     float vc[3] = {s[3], s[4], s[5]};
     float vo = s[8];
     float vx = 0.f, vy = 0.f;
@@ -846,7 +800,7 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
         P.v_opacity[og] = vo;
     }
     }
-    if (P.fold) {
+    if (P.fold && valid) {
         P.v_colors[3 * t] = fc0;
         P.v_colors[3 * t + 1] = fc1;
         P.v_colors[3 * t + 2] = fc2;

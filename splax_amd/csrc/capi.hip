@@ -216,6 +216,18 @@ int DeviceScratch::ensure_rgrad(int64_t count) {
     return 0;
 }
 
+int DeviceScratch::ensure_item_grads(int64_t items) {
+    if (items <= item_grads_cap) return 0;
+    (void)hipDeviceSynchronize();
+    dev_free(&item_grads);
+    item_grads_cap = 0;
+    const int64_t cap = (int64_t)(items * 1.25) + 1;
+    int rc = dev_alloc(&item_grads, 6 * cap, false);
+    if (rc) return rc;
+    item_grads_cap = cap;
+    return 0;
+}
+
 int DeviceScratch::ensure_recs(int64_t items) {
     if (items <= recs_cap) return 0;
     (void)hipDeviceSynchronize();
@@ -280,6 +292,8 @@ void DeviceScratch::release() {
     rgrad_cap = 0;
     dev_free(&recs);
     recs_cap = 0;
+    dev_free(&item_grads);
+    item_grads_cap = 0;
     dev_free(&tile_order);
     order_cap = 0;
     dev_free(&view_partials);
@@ -381,7 +395,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 12; }
+int splat_abi_version(void) { return 13; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();
@@ -708,6 +722,11 @@ static RasterInputs raster_inputs(const float* colors, int64_t rows_colors,
 // blend; out_depth non-null adds the expected-depth channel.
 // records / order: caller buffers for the packed blend records and the tile dispatch order
 // (kept for the backward), or null for library scratch.
+static int rasterize_fwd_core(hipStream_t s, DeviceScratch& sc, const RasterInputs& in,
+                              const SortTargets* tgt, float* final_Ts, int32_t* final_idx,
+                              float* out_img, float* out_depth, float* records, int32_t* order,
+                              int64_t* num_intersects, bool packed);
+
 static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortTargets* tgt,
                               float* final_Ts, int32_t* final_idx, float* out_img,
                               float* out_depth, float* records, int32_t* order,
@@ -718,7 +737,19 @@ static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortT
     DeviceScratch& sc = scratch_for_current_device();
     ScratchUse use(sc, s);
     rc = use.rc;
-    if (!rc) {
+    if (rc) return rc;
+    return rasterize_fwd_core(s, sc, in, tgt, final_Ts, final_idx, out_img, out_depth, records,
+                              order, num_intersects, false);
+}
+
+// The forward with the device's scratch held: sort_and_bin (into tgt's buffers when given), the
+// record pack (skipped when packed: the fused projection wrote them into records) and the blend.
+static int rasterize_fwd_core(hipStream_t s, DeviceScratch& sc, const RasterInputs& in,
+                              const SortTargets* tgt, float* final_Ts, int32_t* final_idx,
+                              float* out_img, float* out_depth, float* records, int32_t* order,
+                              int64_t* num_intersects, bool packed) {
+    int rc = 0;
+    {
         const int32_t bpi = (in.n + 4095) / 4096;
         rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * in.B_geom);
     }
@@ -743,7 +774,7 @@ static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortT
         order = sc.tile_order;
     }
     StageTimer tm(s, kStageBlendFwd);
-    if (M > 0) rc = launch_pack_records(in, recs, s);
+    if (M > 0 && !packed) rc = launch_pack_records(in, recs, s);
     if (!rc)
         rc = launch_blend_fwd(in, L, M > 0 ? ids : nullptr, bins, final_Ts, final_idx, out_img,
                               out_depth, recs, order, s);
@@ -760,8 +791,7 @@ struct KeptLists {
 
 // Backward over kept sorted lists or, with kept == nullptr, over a fresh sort_and_bin.
 // v_depths non-null selects the depth channel.
-static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptLists* kept,
-                              const BlendBwdArgs& args) {
+static int check_raster_bwd(const RasterInputs& in, const BlendBwdArgs& args) {
     int rc = check_raster(in, args.B_out);
     if (rc) return rc;
     if (args.B_out <= 0 || (in.B_geom > 1 && in.B_geom != args.B_out))
@@ -771,10 +801,27 @@ static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptL
         return fail(kErrArgs, "rasterize_bwd: depth channel needs depths and v_out_depth");
     if ((int64_t)args.B_out * in.n >= ((int64_t)1 << 31))
         return fail(kErrArgs, "rasterize_bwd: more than 2^31 gradient rows");
+    return 0;
+}
+
+static int rasterize_bwd_core(hipStream_t s, DeviceScratch& sc, const RasterInputs& in,
+                              const KeptLists* kept, const BlendBwdArgs& args);
+
+static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptLists* kept,
+                              const BlendBwdArgs& args) {
+    int rc = check_raster_bwd(in, args);
+    if (rc) return rc;
     DeviceScratch& sc = scratch_for_current_device();
     ScratchUse use(sc, s);
     rc = use.rc;
     if (rc) return rc;
+    return rasterize_bwd_core(s, sc, in, kept, args);
+}
+
+// The backward with the device's scratch held.
+static int rasterize_bwd_core(hipStream_t s, DeviceScratch& sc, const RasterInputs& in,
+                              const KeptLists* kept, const BlendBwdArgs& args) {
+    int rc = 0;
     KeyLayout L;
     const int32_t* ids = nullptr;
     const int32_t* pos = nullptr;
@@ -967,6 +1014,172 @@ int splat_rasterize_depth_bwd(splat_stream_t stream, const float* colors, int64_
     const BlendBwdArgs a = bwd_args(final_Ts, final_idx, v_out_img, vout_rows, B_out, v_colors,
                                     v_opacity, v_xy, v_conic, v_out_depth, vdepth_rows, v_depths);
     return rasterize_bwd_impl(static_cast<hipStream_t>(stream), in, nullptr, a);
+}
+
+// ------------------------------------------------------------------ fused render path
+
+int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
+                     const float* scales, int64_t rows_scales, const float* quats,
+                     int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
+                     const float* opacities, int64_t rows_opac, const float* colors,
+                     int64_t rows_colors, const float* background, int64_t rows_bg,
+                     const float* transforms, int64_t rows_transforms,
+                     const int32_t* transform_ids, int32_t num_gaussians,
+                     int32_t num_transforms, int32_t has_transforms, int32_t B, int32_t img_h,
+                     int32_t img_w, float fx, float fy, float cx, float cy, float glob_scale,
+                     float clip_thresh, int32_t quats_wxyz, int32_t compensate, float* xys,
+                     float* depths, int32_t* radii, float* conics, int32_t* num_tiles_hit,
+                     int32_t* cum_tiles_hit, int64_t capacity, int32_t* sorted_ids,
+                     int32_t* sorted_pos, int32_t* tile_bins, float* records,
+                     int32_t* tile_order, float* final_Ts, int32_t* final_idx, float* out_img,
+                     float* out_depth, int64_t* num_intersects) {
+    if (B <= 0) return fail(kErrArgs, "render_fwd: invalid sizes");
+    const int64_t total = (int64_t)B * num_gaussians;
+    ProjectArgs a;
+    int rc = project_fwd_args(means3d, rows_means, scales, rows_scales, quats, rows_quats,
+                              viewmat, rows_viewmat, opacities, rows_opac, transforms,
+                              rows_transforms, transform_ids, num_gaussians, num_transforms,
+                              has_transforms, total, img_h, img_w, fx, fy, cx, cy, glob_scale,
+                              clip_thresh, xys, depths, radii, conics, num_tiles_hit,
+                              cum_tiles_hit, quats_wxyz, &a);
+    if (rc) return rc;
+    if (capacity < 0 || !tile_bins || !records || (capacity > 0 && (!sorted_ids || !sorted_pos)))
+        return fail(kErrArgs, "render_fwd: missing sorted-list or record buffers");
+    if ((uintptr_t)records & 15)
+        return fail(kErrArgs, "render_fwd: records must be 16-byte aligned");
+    RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac, opacities,
+                                    rows_opac, background, rows_bg, xys, depths, radii, conics,
+                                    cum_tiles_hit, num_gaussians, B, img_h, img_w);
+    in.compensate = compensate != 0;
+    rc = check_raster(in, B);
+    if (rc) return rc;
+    if (!rows_match(rows_colors, num_gaussians, B))
+        return fail(kErrArgs, "render_fwd: colors rows must be num_gaussians or B * num_gaussians");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    DeviceScratch& sc = scratch_for_current_device();
+    ScratchUse use(sc, s);
+    rc = use.rc;
+    if (rc) return rc;
+    const KeyLayout L = key_layout(B, img_h, img_w);
+    if (L.overflow) return fail(kErrKeyOverflow, "render_fwd: intersection key overflow");
+    // the depth range from the projection: packed key, chunks meeting at most two images
+    const bool fuse_range = L.packed && num_gaussians >= 1024;
+    const int64_t chunks = project_fwd_chunks(total);
+    {
+        const int32_t bpi = (num_gaussians + 4095) / 4096;
+        const int64_t need = std::max<int64_t>(4 * chunks, 2 * (int64_t)bpi * B);
+        rc = ensure_minmax_partials(sc, need);
+        if (!rc) rc = sc.ensure_sort(0, (int64_t)B * L.num_tiles, B, false);
+    }
+    if (rc) return rc;
+    FusedRecords f;
+    f.colors = colors; f.rows_colors = rows_colors; f.compensate = in.compensate;
+    f.recs = reinterpret_cast<float4*>(records);
+    f.mm_partial = fuse_range ? sc.mm_partial : nullptr;
+    f.depth_mm = fuse_range ? sc.depth_mm : nullptr;
+    g_last_error.clear();
+    {
+        StageTimer tm(s, kStageProject);
+        rc = launch_project_fwd_fused(a, f, sc, s);
+    }
+    if (rc) return fail(rc, "render_fwd: projection launch failed");
+    SortTargets tgt;
+    tgt.capacity = capacity;
+    tgt.ids = sorted_ids;
+    tgt.pos = sorted_pos;
+    tgt.bins = tile_bins;
+    tgt.depth_mm = fuse_range ? sc.depth_mm : nullptr;
+    return rasterize_fwd_core(s, sc, in, &tgt, final_Ts, final_idx, out_img, out_depth, records,
+                              tile_order, num_intersects, true);
+}
+
+int splat_render_bwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
+                     const float* scales, int64_t rows_scales, const float* quats,
+                     int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
+                     const float* opacities, int64_t rows_opac, const float* colors,
+                     int64_t rows_colors, const float* background, int64_t rows_bg,
+                     const float* transforms, int64_t rows_transforms,
+                     const int32_t* transform_ids, int32_t num_gaussians,
+                     int32_t num_transforms, int32_t has_transforms, int32_t B, int32_t img_h,
+                     int32_t img_w, float fx, float fy, float glob_scale, int32_t quats_wxyz,
+                     int32_t compensate, const float* xys, const float* depths,
+                     const int32_t* radii, const float* conics, const int32_t* cum_tiles_hit,
+                     const int32_t* sorted_ids, const int32_t* sorted_pos,
+                     const int32_t* tile_bins, const float* records, const int32_t* tile_order,
+                     int64_t num_intersects, const float* final_Ts, const int32_t* final_idx,
+                     const float* v_out_img, int64_t vout_rows, const float* v_out_depth,
+                     int64_t vdepth_rows, float* v_means, float* v_scales, float* v_quats,
+                     float* v_colors, float* v_opacities, float* v_viewmat,
+                     float* v_transforms, int32_t fold_shared) {
+    const int32_t n = num_gaussians;
+    if (n <= 0 || B <= 0) return fail(kErrArgs, "render_bwd: invalid sizes");
+    if (!rows_match(rows_means, n, B) || !rows_match(rows_scales, n, B) ||
+        !rows_match(rows_quats, n, B) || !rows_match(rows_viewmat, 4, B) ||
+        !rows_match(rows_opac, n, B) || !rows_match(rows_colors, n, B))
+        return fail(kErrArgs, "render_bwd: operand rows must be num_gaussians (shared) or "
+                              "B * num_gaussians (batched); viewmat 4 or 4 * B");
+    if (has_transforms && (num_transforms <= 0 || !transforms || !transform_ids ||
+                           !v_transforms || !rows_match(rows_transforms, num_transforms, B)))
+        return fail(kErrArgs, "render_bwd: transforms requested but not given");
+    if (fold_shared && (rows_means != n || rows_scales != n || rows_quats != n ||
+                        rows_colors != n || rows_opac != n))
+        return fail(kErrArgs, "render_bwd: folding needs shared means, scales, quats, colors "
+                              "and opacities");
+    if (((uintptr_t)v_quats & 15) || ((uintptr_t)records & 15))
+        return fail(kErrArgs, "render_bwd: v_quats and records must be 16-byte aligned");
+    if (num_intersects < 0 || !tile_bins || (num_intersects > 0 && (!sorted_ids || !sorted_pos)))
+        return fail(kErrArgs, "render_bwd: invalid sorted lists");
+    RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac, opacities,
+                                    rows_opac, background, rows_bg, xys, depths, nullptr, conics,
+                                    cum_tiles_hit, n, B, img_h, img_w);
+    in.compensate = compensate != 0;
+    const bool depth = v_out_depth != nullptr;
+    const int64_t items = (int64_t)B * n;
+    // the 2D cotangents (v_xy, v_conic, v_depth per item) live in library scratch; v_depths is
+    // only the depth flag for the check
+    BlendBwdArgs ba = bwd_args(final_Ts, final_idx, v_out_img, vout_rows, B, v_colors,
+                               v_opacities, nullptr, nullptr, v_out_depth, vdepth_rows,
+                               depth ? const_cast<float*>(v_out_depth) : nullptr);
+    ba.fold = fold_shared != 0;
+    int rc = check_raster_bwd(in, ba);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    DeviceScratch& sc = scratch_for_current_device();
+    ScratchUse use(sc, s);
+    rc = use.rc;
+    if (rc) return rc;
+    rc = sc.ensure_item_grads(items);
+    if (rc) return rc;
+    ba.v_xy = sc.item_grads;
+    ba.v_conic = sc.item_grads + 2 * items;
+    ba.v_depths = depth ? sc.item_grads + 5 * items : nullptr;
+    const KeptLists kept{sorted_ids, sorted_pos, tile_bins, num_intersects, records, tile_order};
+    g_last_error.clear();
+    rc = rasterize_bwd_core(s, sc, in, &kept, ba);
+    if (rc) return rc;
+    ProjectBwdArgs pa;
+    pa.means = means3d; pa.rows_means = rows_means;
+    pa.scales = scales; pa.rows_scales = rows_scales;
+    pa.quats = quats; pa.rows_quats = rows_quats;
+    pa.viewmat = viewmat; pa.rows_viewmat = rows_viewmat;
+    pa.radii = radii; pa.rows_radii = items;
+    pa.conics = conics; pa.rows_conics = items;
+    pa.v_xy = ba.v_xy; pa.rows_vxy = items;
+    pa.v_depth = ba.v_depths; pa.rows_vdepth = items;
+    pa.v_conic = ba.v_conic; pa.rows_vconic = items;
+    pa.transforms = transforms; pa.rows_transforms = has_transforms ? rows_transforms : 0;
+    pa.transform_ids = transform_ids;
+    pa.n = n; pa.num_transforms = has_transforms ? num_transforms : 0;
+    pa.has_transforms = has_transforms; pa.B = B;
+    pa.fx = fx; pa.fy = fy; pa.glob_scale = glob_scale;
+    pa.v_mean3d = v_means; pa.v_scale = v_scales; pa.v_quat = v_quats;
+    pa.v_viewmat = v_viewmat; pa.v_transforms = has_transforms ? v_transforms : nullptr;
+    pa.quats_wxyz = quats_wxyz != 0;
+    pa.fold = fold_shared != 0;
+    StageTimer tm(s, kStageProjectBwd);
+    rc = launch_project_bwd(pa, sc, s);
+    if (rc) return fail(rc, "render_bwd: projection backward launch failed");
+    return 0;
 }
 
 }  // extern "C"

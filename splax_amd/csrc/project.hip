@@ -37,6 +37,12 @@ struct ProjectParams {
     int32_t* num_tiles_hit; int32_t* cum_tiles_hit;
     int32_t wxyz;  // quaternion storage order: 1 = wxyz (the public API's), 0 = xyzw
     uint32_t* chunk_sums;  // one per workgroup: its chunk's tile total
+    // fused render forward (project_fwd_kernel<true>): each item's packed blend record and, per
+    // chunk, the depth range of its visible items for the chunk's (at most two) images
+    const float* colors; int64_t rows_colors;
+    int32_t compensate;
+    float4* recs;
+    uint32_t* mm_partial;  // [chunks, 4]: ordered (lo, hi) of the first image, then the second
 };
 
 constexpr int kProjThreads = 256;
@@ -100,8 +106,14 @@ __device__ __forceinline__ void project_geom(const float* mean, const float* q, 
     }
 }
 
-// Per-item projection; returns the tile count (0 when culled) and writes the item's outputs.
-__device__ __forceinline__ int32_t project_item(const ProjectParams& P, int64_t idx) {
+// What the projection wrote for one item, kept in registers for the fused record packing.
+struct ItemOut {
+    int32_t count;
+    float x, y, depth, a, b, c, opac;
+};
+
+// Per-item projection; writes the item's outputs and returns them (count 0 when culled).
+__device__ __forceinline__ ItemOut project_item(const ProjectParams& P, int64_t idx) {
     const int32_t n = P.n;
     const int32_t bid = (int32_t)(idx / n), gid = (int32_t)(idx - (int64_t)bid * n);
     const int64_t m_idx = P.rows_means > n ? idx : gid;
@@ -115,6 +127,7 @@ __device__ __forceinline__ int32_t project_item(const ProjectParams& P, int64_t 
     int32_t radius = 0;
     float con0 = 0.f, con1 = 0.f, con2 = 0.f;
     int32_t count = 0;
+    const float opac = P.opac[o_idx];
 
     float mean[3] = {P.means[3 * m_idx], P.means[3 * m_idx + 1], P.means[3 * m_idx + 2]};
     int32_t tf_id = P.has_transforms ? P.transform_ids[gid] : -1;
@@ -166,7 +179,6 @@ __device__ __forceinline__ int32_t project_item(const ProjectParams& P, int64_t 
         float rw = 1.0f / (p[2] + kZEps);
         float center_x = (p[0] * rw) * P.fx + P.cx;
         float center_y = (p[1] * rw) * P.fy + P.cy;
-        float opac = P.opac[o_idx];
         if (opac < kAlphaThresh) break;
         float t = iso_level(opac);
         float ext = sqrtf(t);
@@ -196,7 +208,7 @@ __device__ __forceinline__ int32_t project_item(const ProjectParams& P, int64_t 
     P.conics[3 * idx + 1] = con1;
     P.conics[3 * idx + 2] = con2;
     P.num_tiles_hit[idx] = count;
-    return count;
+    return ItemOut{count, xy.x, xy.y, depth, con0, con1, con2, opac};
 }
 
 // Items per thread of the fused projection + scan; one workgroup covers 256 * kProjItems items.
@@ -204,8 +216,12 @@ __device__ __forceinline__ int32_t project_item(const ProjectParams& P, int64_t 
 // waves in flight.
 constexpr int kProjItems = 1;
 
+// kFused (the fused render forward): also the item's packed blend record and the chunk's depth
+// range partials (the chunk spans at most two images: num_gaussians >= 1024).
+template <bool kFused>
 __global__ void __launch_bounds__(kProjFwdThreads) project_fwd_kernel(ProjectParams P) {
     __shared__ int32_t s_wave[kProjFwdThreads / 64];
+    __shared__ uint32_t s_mm[kProjFwdThreads / 64][4];
     const int tid = threadIdx.x;
     const uint32_t part = blockIdx.x;
     const int64_t base = (int64_t)part * (kProjFwdThreads * kProjItems);
@@ -213,17 +229,68 @@ __global__ void __launch_bounds__(kProjFwdThreads) project_fwd_kernel(ProjectPar
     // sum plus one block scan gives the inclusive prefix.
     int32_t cnt[kProjItems];
     int32_t local = 0;
+    uint32_t mm[4] = {0xffffffffu, 0u, 0xffffffffu, 0u};  // (lo, hi) per image slot
 #pragma unroll
     for (int k = 0; k < kProjItems; ++k) {
         int64_t idx = base + (int64_t)tid * kProjItems + k;
-        cnt[k] = idx < P.total ? project_item(P, idx) : 0;
+        cnt[k] = 0;
+        if (idx < P.total) {
+            const ItemOut o = project_item(P, idx);
+            cnt[k] = o.count;
+            if constexpr (kFused) {
+                float4 r[4];
+                pack_record(o.x, o.y, o.a, o.b, o.c, o.opac, P.compensate,
+                            P.colors + 3 * (idx % P.rows_colors), o.depth, r);
+                float4* dst = P.recs + 4 * idx;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) dst[q] = r[q];
+                // visible items (radii > 0) set the range, splax/_rasterize/_sort/_kernels.py:38-73;
+                // slot 0 or 1: with n >= 1024 a chunk meets at most two images
+                if (P.mm_partial && o.count > 0) {
+                    const bool second = idx / P.n != base / P.n;
+                    const uint32_t u = f2ord(o.depth);
+                    if (second) {
+                        mm[2] = u;
+                        mm[3] = u;
+                    } else {
+                        mm[0] = u;
+                        mm[1] = u;
+                    }
+                }
+            }
+        }
         local += cnt[k];
     }
     // block inclusive scan of `local`
     const int lane = tid & 63, wave = tid >> 6;
     int32_t incl = wave_inclusive_scan_i32(local, lane);
     if (lane == 63) s_wave[wave] = incl;
+    if constexpr (kFused) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t o = __shfl_xor(mm[q], off, 64);
+                mm[q] = (q & 1) ? (o > mm[q] ? o : mm[q]) : (o < mm[q] ? o : mm[q]);
+            }
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s_mm[wave][q] = mm[q];
+        }
+    }
     __syncthreads();
+    if constexpr (kFused) {
+        if (P.mm_partial && tid < 4) {
+            uint32_t v = s_mm[0][tid];
+#pragma unroll
+            for (int w = 1; w < kProjFwdThreads / 64; ++w) {
+                const uint32_t o = s_mm[w][tid];
+                v = (tid & 1) ? (o > v ? o : v) : (o < v ? o : v);
+            }
+            P.mm_partial[4 * (int64_t)part + tid] = v;
+        }
+    }
     int32_t wave_off = 0, block_total = 0;
 #pragma unroll
     for (int w = 0; w < kProjFwdThreads / 64; ++w) {
@@ -299,6 +366,46 @@ __global__ void __launch_bounds__(kProjFwdThreads) chunk_offset_kernel(int32_t* 
                                                            const uint32_t* offsets) {
     const int64_t idx = (int64_t)(blockIdx.x + 1) * kProjFwdThreads + threadIdx.x;
     if (idx < total) cum[idx] = (int32_t)((uint32_t)cum[idx] + offsets[blockIdx.x + 1]);
+}
+
+// Per-image depth range of the visible items from the fused projection's chunk partials, one
+// workgroup per image (the result minmax_partial_kernel / minmax_final_kernel give): chunk c
+// holds items [1024 c, 1024 c + 1024), its slot 0 the image of its first item, slot 1 the next.
+__global__ void __launch_bounds__(256)
+depth_range_kernel(const uint32_t* partial, int32_t n, int64_t chunks, float* mm) {
+    __shared__ uint32_t s_lo[4], s_hi[4];
+    const int64_t image = blockIdx.x;
+    const int64_t c0 = image * n / kProjFwdThreads;
+    int64_t c1 = ((image + 1) * n - 1) / kProjFwdThreads;
+    c1 = c1 < chunks - 1 ? c1 : chunks - 1;
+    uint32_t lo = 0xffffffffu, hi = 0u;
+    for (int64_t c = c0 + threadIdx.x; c <= c1; c += 256) {
+        const int64_t slot = image - c * kProjFwdThreads / n;  // 0 or 1
+        const uint32_t a = partial[4 * c + 2 * slot], b = partial[4 * c + 2 * slot + 1];
+        lo = a < lo ? a : lo;
+        hi = b > hi ? b : hi;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t a = __shfl_xor(lo, off, 64), b = __shfl_xor(hi, off, 64);
+        lo = a < lo ? a : lo;
+        hi = b > hi ? b : hi;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        s_lo[wave] = lo;
+        s_hi[wave] = hi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) {
+            lo = s_lo[w] < lo ? s_lo[w] : lo;
+            hi = s_hi[w] > hi ? s_hi[w] : hi;
+        }
+        // no visible item: the reference's +-1e30 seeds remain (drange < 0 -> depth_q = 0)
+        mm[2 * image] = hi == 0u ? 1.0e30f : ord2f(lo);
+        mm[2 * image + 1] = hi == 0u ? -1.0e30f : ord2f(hi);
+    }
 }
 
 // ------------------------------------------------------------------ projection backward
@@ -670,6 +777,22 @@ int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stre
 }
 
 int launch_project_fwd_into(const ProjectArgs& a, uint32_t* chunk_sums, hipStream_t stream) {
+    return launch_project_fwd_impl(a, chunk_sums, nullptr, stream);
+}
+
+int launch_project_fwd_fused(const ProjectArgs& a, const FusedRecords& f, DeviceScratch& sc,
+                             hipStream_t stream) {
+    if (a.total <= 0) return 0;
+    const int64_t blocks = project_fwd_chunks(a.total);
+    if (blocks > (int64_t)sc.chunk_sums_cap) {
+        int rc = sc.grow_chunk_sums(blocks);
+        if (rc) return rc;
+    }
+    return launch_project_fwd_impl(a, sc.chunk_sums, &f, stream);
+}
+
+int launch_project_fwd_impl(const ProjectArgs& a, uint32_t* chunk_sums, const FusedRecords* f,
+                            hipStream_t stream) {
     if (a.total <= 0) return 0;
     const int64_t blocks = project_fwd_chunks(a.total);
     ProjectParams P;
@@ -688,14 +811,25 @@ int launch_project_fwd_into(const ProjectArgs& a, uint32_t* chunk_sums, hipStrea
     P.num_tiles_hit = a.num_tiles_hit; P.cum_tiles_hit = a.cum_tiles_hit;
     P.wxyz = a.quats_wxyz;
     P.chunk_sums = chunk_sums;
-    hipLaunchKernelGGL(project_fwd_kernel, dim3((unsigned)blocks), dim3(kProjFwdThreads), 0, stream,
-                       P);
+    P.colors = f ? f->colors : nullptr; P.rows_colors = f ? f->rows_colors : 1;
+    P.compensate = f ? f->compensate : 0;
+    P.recs = f ? f->recs : nullptr;
+    P.mm_partial = f ? f->mm_partial : nullptr;
+    if (f)
+        hipLaunchKernelGGL(project_fwd_kernel<true>, dim3((unsigned)blocks),
+                           dim3(kProjFwdThreads), 0, stream, P);
+    else
+        hipLaunchKernelGGL(project_fwd_kernel<false>, dim3((unsigned)blocks),
+                           dim3(kProjFwdThreads), 0, stream, P);
     if (blocks > 1) {
         hipLaunchKernelGGL(chunk_scan_kernel, dim3(1), dim3(kChunkScanThreads), 0, stream,
                            P.chunk_sums, blocks);
         hipLaunchKernelGGL(chunk_offset_kernel, dim3((unsigned)(blocks - 1)), dim3(kProjFwdThreads),
                            0, stream, P.cum_tiles_hit, a.total, P.chunk_sums);
     }
+    if (f && f->depth_mm)
+        hipLaunchKernelGGL(depth_range_kernel, dim3((unsigned)(a.total / a.n)), dim3(256), 0,
+                           stream, f->mm_partial, a.n, blocks, f->depth_mm);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
 }
 

@@ -30,13 +30,6 @@ namespace splat {
 constexpr int kMmThreads = 256;
 constexpr int kMmItems = 16;
 
-__device__ __forceinline__ uint32_t f2ord(float f) {
-    uint32_t u = __float_as_uint(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float ord2f(uint32_t u) {
-    return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
-}
 
 __global__ void __launch_bounds__(kMmThreads)
 minmax_partial_kernel(const float* depths, const int32_t* radii, int32_t n,
@@ -553,7 +546,10 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
                                   hipMemcpyDeviceToHost, stream) != hipSuccess ||
                    hipEventRecord(sc.count_event, stream) != hipSuccess))
         return fail(kErrRuntime, "count readback enqueue failed");
-    if (!wide) {  // the 64-bit key carries the raw depth: no depth range
+    const float* depth_mm = sc.depth_mm;
+    if (!wide && tgt && tgt->depth_mm) {
+        depth_mm = tgt->depth_mm;  // formed by the fused projection
+    } else if (!wide) {  // the 64-bit key carries the raw depth: no depth range
         const int32_t bpi =
             (int32_t)((in.n + kMmThreads * kMmItems - 1) / (kMmThreads * kMmItems));
         if ((int64_t)bpi * B * 2 > sc.mm_partial_cap)
@@ -596,7 +592,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         EmitParams E;
         E.xys = in.xys; E.depths = in.depths; E.radii = in.radii; E.conics = in.conics;
         E.map_opac = in.map_opac; E.rows_map_opac = in.rows_map_opac;
-        E.cum = in.cum; E.mm = sc.depth_mm; E.n = in.n; E.total = total; E.M = M;
+        E.cum = in.cum; E.mm = depth_mm; E.n = in.n; E.total = total; E.M = M;
         E.tiles_x = L.tiles_x; E.tiles_y = L.tiles_y; E.tile_bits = L.tile_bits;
         E.depth_bits = L.depth_bits; E.keys = kbuf[0]; E.owner = sc.gids[0];
         const dim3 grid((unsigned)((total + 255) / 256));

@@ -38,6 +38,40 @@ __device__ __forceinline__ float compensation_rho(float a, float b, float c, flo
     return sqrtf(cl);
 }
 
+// Cotangents of blend_opac = opac * rho(conic) (splax/_render.py:105-109 with
+// splax/_project/_project.py:113-117) for a blend-opacity cotangent vbo, by reverse-mode rules of
+// the reference's expression: sqrt' = 0.5 / rho, maximum / minimum pass 1 strictly inside, 1/2 at
+// a tie and 0 outside. Returns the raw-opacity cotangent and adds the conic cotangent to vc.
+// Items without intersections carry vbo = 0 and a zero conic (rho = 1), so the where(radii > 0)
+// select adds nothing for them.
+__device__ __forceinline__ float compensation_vjp(float vbo, float o, float a, float b, float c,
+                                                  float vc[3]) {
+    float rho2;
+    const float rho = compensation_rho(a, b, c, rho2);
+    const float v_o = vbo * rho;
+    const float v_rho = vbo * o;
+    const float v_cl = v_rho * (0.5f / rho);
+    const float m_lo = rho2 > 0.0f ? 1.0f : (rho2 == 0.0f ? 0.5f : 0.0f);
+    const float y = rho2 > 0.0f ? rho2 : 0.0f;
+    const float m_hi = y < 1.0f ? 1.0f : (y == 1.0f ? 0.5f : 0.0f);
+    const float v_r2 = (v_cl * m_hi) * m_lo;
+    const float v_s = -(kDilation * v_r2);  // through 1 - eps (a + c)
+    const float v_t = kDilation2 * v_r2;    // through eps^2 (a c - b b)
+    vc[0] = vc[0] + (v_s + v_t * c);
+    vc[1] = vc[1] + (-(v_t * b) - v_t * b);
+    vc[2] = vc[2] + (v_s + v_t * a);
+    return v_o;
+}
+
+// Floats as order-preserving unsigned integers (for min / max reductions) and back.
+__device__ __forceinline__ uint32_t f2ord(float f) {
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float ord2f(uint32_t u) {
+    return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+
 __device__ __forceinline__ float minw(float a, float b) { return a < b ? a : b; }
 __device__ __forceinline__ float maxw(float a, float b) { return a > b ? a : b; }
 __device__ __forceinline__ int32_t iminw(int32_t a, int32_t b) { return a < b ? a : b; }
@@ -294,6 +328,69 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
 
 __device__ __forceinline__ float lane63(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// ------------------------------------------------------------------ packed blend records
+
+// Largest sigma a blend accepts: blend_exp(-87) is still a normal float. An intersection with a
+// larger sigma is rejected, as the exact alpha would be for opacities below 2.4e35 (the CPU oracle
+// applies the same cap).
+constexpr float kBlendSigmaCap = 87.0f;
+
+// Packed record of one geometry item, 64 bytes (one aligned segment per staged intersection):
+//   r0 = (x, y, a/2, b), r1 = (c/2, o, sigma_max, 0), r2 = (red, green, blue, depth),
+//   r3 = (ex, ey, cull mode, 0).
+// They depend only on the rasterizer's inputs, so a forward's records serve its backward.
+// sigma_max = log(255 o) + 1e-3 bounds sigma where o e^-sigma can still reach 1/255. The cull mode
+// says whether the tile-independent box (+-ex, +-ey) around the centre holds every pixel centre
+// with sigma <= sigma_max (kCullBox), or no pixel can pass (kCullNone: sigma_max < 0), or the box
+// cannot be trusted and every quadrant is kept (kCullKeep).
+enum : uint32_t { kCullBox = 0u, kCullKeep = 1u, kCullNone = 2u };
+
+// The record of one item from its projection outputs (xy, conic a b c, depth), its raw opacity
+// o_raw and colour (3 floats); with compensate the blend opacity is o_raw * rho(conic)
+// (splax/_render.py:105-110). Written to r[0..3].
+__device__ __forceinline__ void pack_record(float x, float y, float a, float b, float c,
+                                            float o_raw, int32_t compensate, const float* color,
+                                            float depth, float4* r) {
+    float o = o_raw;
+    if (compensate) {
+        float rho2;
+        o = o * compensation_rho(a, b, c, rho2);
+    }
+    // sigma_max is capped at kBlendSigmaCap, where blend_exp's range ends
+    float smax;
+    if (o > 0.0f) {
+        smax = fminf(__logf(o * 255.0f) + 1e-3f, kBlendSigmaCap);
+    } else {
+        smax = -__builtin_inff();  // o <= 0 or NaN: no pixel accepts it
+    }
+    uint32_t mode = kCullKeep;
+    float ex = 0.0f, ey = 0.0f;
+    if (!(smax >= 0.0f)) {
+        mode = kCullNone;  // every pixel rejected
+    } else {
+        // Points beyond k times the bounding box of {sigma <= smax} have exact
+        // sigma >= k^2 smax. The evaluated sigma differs from the exact one by at most
+        // ~6e-7 * cond(Q) relative (Q the conic), so with cond(Q) <= (a + c)^2 / det < 1e4
+        // and k = 1.01 every point outside the box evaluates above smax.
+        // Worse-conditioned conics keep all four quadrants.
+        const float det = a * c - b * b;
+        const float tr = a + c;
+        const float ex2 = 2.0f * smax * c / det, ey2 = 2.0f * smax * a / det;
+        if (a > 0.0f && c > 0.0f && det > 0.0f && tr * tr < 1e4f * det && ex2 < 1e30f &&
+            ey2 < 1e30f) {
+            ex = sqrtf(ex2) * 1.01f + 0.01f;
+            ey = sqrtf(ey2) * 1.01f + 0.01f;
+            mode = kCullBox;
+        }
+    }
+    // the blends evaluate sigma = (a/2 dx dx + c/2 dy dy) + b dx dy: halving exactly before
+    // the products leaves every rounding where 0.5 (a dx dx + c dy dy) puts it
+    r[0] = make_float4(x, y, 0.5f * a, b);
+    r[1] = make_float4(0.5f * c, o, smax, 0.0f);
+    r[2] = make_float4(color[0], color[1], color[2], depth);
+    r[3] = make_float4(ex, ey, __uint_as_float(mode), 0.0f);
 }
 
 }  // namespace splat

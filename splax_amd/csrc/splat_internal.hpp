@@ -121,6 +121,8 @@ struct DeviceScratch {
     float* rgrad = nullptr; int64_t rgrad_cap = 0;
     // blends: packed per-item records (4 float4 each)
     float4* recs = nullptr; int64_t recs_cap = 0;
+    // fused render backward: per-item 2D cotangents (v_xy 2, v_conic 3, v_depth 1 per item)
+    float* item_grads = nullptr; int64_t item_grads_cap = 0;
     // blends: workgroup -> (image, tile) dispatch order
     int32_t* tile_order = nullptr; int64_t order_cap = 0;
     // projection backward: 12 viewmat-gradient partials per (image, workgroup)
@@ -145,6 +147,7 @@ struct DeviceScratch {
     int ensure_sort(int64_t M, int64_t bins, int32_t B, bool wide);
     int ensure_rgrad(int64_t count);
     int ensure_recs(int64_t items);
+    int ensure_item_grads(int64_t items);
     int ensure_order(int64_t blocks);
     int ensure_view_partials(int64_t count);
     void release();
@@ -205,6 +208,21 @@ int fill_zero_i32(int32_t* p, int64_t n, hipStream_t stream);
 int launch_project_fwd(const ProjectArgs& a, DeviceScratch& sc, hipStream_t stream);
 // The projection with its chunk-total scratch (project_fwd_chunks(a.total) uint32) supplied.
 int launch_project_fwd_into(const ProjectArgs& a, uint32_t* chunk_sums, hipStream_t stream);
+// The fused render forward's projection: also each item's packed blend record (recs, 4 float4
+// per item, from colors / compensate as launch_pack_records would write it) and, with depth_mm
+// non-null (requires n >= 1024), the per-image depth range of the visible items (mm_partial:
+// scratch of 4 uint32 per chunk), as the sort's depth-range kernels would compute it.
+struct FusedRecords {
+    const float* colors; int64_t rows_colors;
+    int32_t compensate;
+    float4* recs;
+    uint32_t* mm_partial;
+    float* depth_mm;
+};
+int launch_project_fwd_fused(const ProjectArgs& a, const FusedRecords& f, DeviceScratch& sc,
+                             hipStream_t stream);
+int launch_project_fwd_impl(const ProjectArgs& a, uint32_t* chunk_sums, const FusedRecords* f,
+                            hipStream_t stream);
 int64_t project_fwd_chunks(int64_t total);
 // The projection with no allocation: its chunk totals in a fixed device array of
 // kNoAllocMaxChunks entries per device (one per 1024 items).
@@ -223,6 +241,7 @@ struct SortTargets {
     int32_t* ids = nullptr;
     int32_t* pos = nullptr;
     int32_t* bins = nullptr;
+    const float* depth_mm = nullptr;  // per-image depth range already formed (fused projection)
 };
 
 // Where sort_and_bin left its results: sorted keys (int32 when packed, uint64 when wide), ids,
@@ -273,6 +292,49 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
                      const int32_t* kept_order, hipStream_t stream);
 
 // ------------------------------------------------------------------ device helpers
+
+// Records of the per-item gradient gather staged per LDS round (kGatherChunk * NG floats).
+constexpr int kGatherChunk = 768;
+
+// Per-item sums of NG floats over the item's emission range [my_lo, my_hi) of rgrad rows
+// (row e at rgrad + (off + e) * NG), added in emission order. The workgroup's items cover one
+// contiguous range [wg_lo, wg_hi) of rows (uniform over the workgroup), which is read with
+// coalesced loads into s_buf (kGatherChunk * NG floats of LDS) a round at a time; each thread then
+// adds its own rows from LDS. Every thread of the workgroup calls it (an item outside the
+// workgroup's range passes my_lo = my_hi).
+template <int NG, int kThreads>
+__device__ __forceinline__ void block_gather(const float* __restrict__ rgrad, int64_t off,
+                                             int64_t wg_lo, int64_t wg_hi, int64_t my_lo,
+                                             int64_t my_hi, float* s_buf, float* s) {
+#pragma unroll
+    for (int k = 0; k < NG; ++k) s[k] = 0.0f;
+    for (int64_t cs = wg_lo; cs < wg_hi; cs += kGatherChunk) {
+        const int64_t ce = cs + kGatherChunk < wg_hi ? cs + kGatherChunk : wg_hi;
+        const int nf = (int)((ce - cs) * NG);
+        const float* src = rgrad + (off + cs) * NG;
+        __syncthreads();  // the previous round's reads of s_buf are done
+        for (int i0 = 0; i0 < nf; i0 += 4 * kThreads) {
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u * kThreads + (int)threadIdx.x;
+                v[u] = i < nf ? src[i] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u * kThreads + (int)threadIdx.x;
+                if (i < nf) s_buf[i] = v[u];
+            }
+        }
+        __syncthreads();
+        const int64_t a = my_lo > cs ? my_lo : cs, b = my_hi < ce ? my_hi : ce;
+        for (int64_t e = a; e < b; ++e) {
+            const float* r = s_buf + (e - cs) * NG;
+#pragma unroll
+            for (int k = 0; k < NG; ++k) s[k] += r[k];
+        }
+    }
+}
 
 __device__ __forceinline__ int32_t wave_inclusive_scan_i32(int32_t v, int lane) {
 #pragma unroll

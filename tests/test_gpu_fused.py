@@ -1,0 +1,195 @@
+"""The fused render path (splat_render_fwd / splat_render_bwd, behind splax_amd.render) against
+the two-call path (project then rasterize, each with its own backward) on the GPU.
+
+The fused forward's projection also packs the blend records and forms the per-image depth range
+(the sort's depth-range pass and the record pack do not run); the fused backward keeps the
+per-item 2D cotangents in library scratch. Bars: projection outputs, kept lists, records
+and the image bit-exact; gradients within relative Frobenius 1e-5 plus allclose(rtol=1e-4,
+atol=1e-5 * max|ref|) (the viewmat and transform gradients, and the blend's per-record sums over
+a tile's waves, add in an order the GPU's scheduling decides).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import splax_amd
+from conftest import assert_bit_exact, random_scene, rel_fro
+from splax_amd import _lib, _ops
+from splax_amd._rasterize import _rasterize_checked
+from splax_amd.scenes import make_scene
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _device_healthy():
+    yield
+    assert _lib.check_device() == 0
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _t(a, grad=False):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t.requires_grad_(True) if grad else t
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _grad_compare(got, ref, label, rel_tol=1e-5):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    r = rel_fro(got, ref)
+    assert r < rel_tol, f"{label}: relative Frobenius error {r:.3e}"
+    scale = float(np.abs(ref).max()) + 1e-30
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5 * scale, err_msg=label)
+
+
+def _two_call(p, vm, bg, cam, antialiased, render_depth, tf=None, slices=None):
+    """splax.render composed from the public project and rasterize calls (the unfused path)."""
+    tf_ids = None
+    if tf is not None:
+        tf_ids = splax_amd.transform_ids(p["means"].shape[-2], slices, device="cuda")
+    xys, depths, radii, conics, _, cum = splax_amd.project(
+        p["means"], p["scales"], p["quats"], vm, opacities=p["opac"], gaussian_transforms=tf,
+        transform_ids=tf_ids, **cam)
+    return _rasterize_checked(p["colors"], p["opac"], bg, xys, depths, radii, conics, cum,
+                              cam["img_shape"], None, render_depth, compensate=antialiased)
+
+
+CASES = {
+    "cfg0": dict(scene=lambda: make_scene(0), B=1),
+    "cfg2_60k": dict(scene=lambda: make_scene(2, n=60_000), B=1),
+    "cfg3_20k_B4": dict(scene=lambda: make_scene(3, n=20_000), B=4),
+    "aa_depth": dict(scene=lambda: make_scene(1, n=30_000), B=1, antialiased=True, depth=True),
+    "small_n": dict(scene=lambda: make_scene(0, n=700), B=2),  # depth range via the sort's pass
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_fused_render_equals_two_call_path(name):
+    _case(f"fused render {name}")
+    cfg = CASES[name]
+    s = cfg["scene"]()
+    B = cfg["B"]
+    aa, rd = cfg.get("antialiased", False), cfg.get("depth", False)
+    cam = dict(img_shape=s.img_shape, f=s.f, c=s.c)
+    vms = s.viewmats[:B] if s.B >= B else np.stack([s.viewmats[0]] * B)
+    vm_np = vms if B > 1 else vms[0]
+    outs = []
+    for fused in (True, False):
+        p = {k: _t(v, grad=True) for k, v in (("means", s.means), ("scales", s.scales),
+                                               ("quats", s.quats), ("colors", s.colors),
+                                               ("opac", s.opacities))}
+        vm = _t(vm_np, grad=True)
+        bg = _t(s.background)
+        if fused:
+            img, depth = splax_amd.render(p["means"], p["scales"], p["quats"], p["colors"],
+                                          p["opac"], viewmat=vm, background=bg, antialiased=aa,
+                                          render_depth=rd, **cam)
+        else:
+            img, depth = _two_call(p, vm, bg, cam, aa, rd)
+        w = torch.from_numpy(np.random.default_rng(7).uniform(-1, 1, img.shape)
+                             .astype(np.float32)).cuda()
+        loss = (img * w).sum()
+        if rd:
+            wd = torch.from_numpy(np.random.default_rng(8).uniform(-1, 1, depth.shape)
+                                  .astype(np.float32)).cuda()
+            loss = loss + (depth * wd).sum()
+        loss.backward()
+        torch.cuda.synchronize()
+        grads = {k: _np(v.grad) for k, v in p.items()}
+        grads["viewmat"] = _np(vm.grad)
+        outs.append((_np(img), None if depth is None else _np(depth), grads))
+    (fi, fd, fg), (ui, ud, ug) = outs
+    assert_bit_exact(fi, ui, f"{name}/img")
+    if rd:
+        assert_bit_exact(fd, ud, f"{name}/depth")
+    for k in ug:
+        _grad_compare(fg[k], ug[k], f"{name}/{k}")
+
+
+def test_fused_render_with_transforms_and_nested_batch():
+    """Rigid transforms with per-world transforms on the outer axis, viewmats on both axes."""
+    _case("fused render transforms + nested batch")
+    n, H, W = 3000, 72, 96
+    sc = random_scene(n, H, W, seed=51)
+    slices = [(0, 1400), (1400, 2600)]
+    tfs = np.tile(np.eye(4, dtype=np.float32), (2, 2, 1, 1))
+    tfs[1, :, 0, 3] = 0.05
+    tfs[0, 1, 1, 3] = -0.04
+    vms = np.stack([np.stack([sc["vm"]] * 3)] * 2)
+    vms[:, 1, 0, 3] += 0.1
+    vms[:, 2, 1, 3] -= 0.1
+    cam = dict(img_shape=(H, W), f=sc["f"], c=sc["c"])
+    outs = []
+    for fused in (True, False):
+        p = {k: _t(sc[k], grad=True) for k in ("means", "scales", "quats", "colors", "opac")}
+        tf = _t(tfs[:, None], grad=True)  # (2, 1, K, 4, 4): outer axis only
+        vm = _t(vms)
+        bg = _t(sc["bg"])
+        if fused:
+            img, _ = splax_amd.render(p["means"], p["scales"], p["quats"], p["colors"],
+                                      p["opac"], viewmat=vm, background=bg,
+                                      gaussian_transforms=tf, gaussian_slices=slices, **cam)
+        else:
+            # the two-call path takes one flat batch: fold the axes by hand
+            tff = tf.expand(2, 3, 2, 4, 4).reshape(6, 2, 4, 4)
+            img, _ = _two_call(p, vm.reshape(6, 4, 4), bg, cam, False, False, tf=tff,
+                               slices=slices)
+            img = img.reshape(2, 3, H, W, 3)
+        assert img.shape == (2, 3, H, W, 3)
+        w = torch.from_numpy(np.random.default_rng(3).uniform(-1, 1, img.shape)
+                             .astype(np.float32)).cuda()
+        (img * w).sum().backward()
+        torch.cuda.synchronize()
+        g = {k: _np(v.grad) for k, v in p.items()}
+        g["transforms"] = _np(tf.grad)
+        outs.append((_np(img), g))
+    assert_bit_exact(outs[0][0], outs[1][0], "img")
+    for k in outs[1][1]:
+        _grad_compare(outs[0][1][k], outs[1][1][k], k)
+
+
+def test_fused_forward_buffers_equal_two_call_buffers():
+    """Through the tensor wrappers: projection outputs, sorted lists, bins, records and image of
+    splat_render_fwd equal splat_project_fwd + splat_rasterize_fwd_keep bit for bit."""
+    _case("fused forward buffers")
+    s = make_scene(2, n=40_000)
+    n = s.n
+    q = _t(s.quats)
+    args = (_t(s.means), _t(s.scales), q, _t(s.colors), _t(s.opacities).reshape(-1),
+            _t(s.viewmats[0]), _t(s.background))
+    tf = torch.zeros((1, 4, 4), device="cuda")
+    ids = torch.full((1,), -1, device="cuda", dtype=torch.int32)
+    for aa in (False, True):
+        img, Ts, fidx, kept, _ = _ops.render_fwd(
+            *args, tf, ids, n=n, B=1, num_transforms=1, has_transforms=False,
+            img_shape=s.img_shape, f=s.f, c=s.c, glob_scale=1.0, clip_thresh=0.01,
+            compensate=aa)
+        proj = _ops.project_fwd(args[0], args[1], q, args[5], args[4], tf, ids, n=n, total=n,
+                                num_transforms=1, has_transforms=False, img_shape=s.img_shape,
+                                f=s.f, c=s.c, glob_scale=1.0, clip_thresh=0.01,
+                                quats_wxyz=True)
+        xys, depths, radii, conics, nth, cum = proj
+        img2, Ts2, fidx2, k2, _ = _ops.rasterize_fwd_keep(
+            args[3], args[4], args[4], args[6], xys, depths, radii, conics, cum, n=n, B=1,
+            img_shape=s.img_shape, compensate=aa)
+        torch.cuda.synchronize()
+        for label, a, b in (("xys", kept.xys, xys), ("depths", kept.depths, depths),
+                            ("radii", kept.radii, radii), ("conics", kept.conics, conics),
+                            ("cum", kept.cum, cum), ("img", img, img2), ("Ts", Ts, Ts2),
+                            ("fidx", fidx, fidx2), ("bins", kept.sort.bins, k2.bins),
+                            ("records", kept.sort.records, k2.records)):
+            assert_bit_exact(_np(a), _np(b), f"aa={aa} {label}")
+        M = kept.sort.M
+        assert M == k2.M and M > 0
+        assert_bit_exact(_np(kept.sort.ids)[:M], _np(k2.ids)[:M], f"aa={aa} ids")
+        assert_bit_exact(_np(kept.sort.pos)[:M], _np(k2.pos)[:M], f"aa={aa} pos")
