@@ -102,6 +102,11 @@ int DeviceScratch::ensure_base() {
     pinned_count = static_cast<int32_t*>(h);
     if (hipEventCreateWithFlags(&count_event, hipEventDisableTiming) != hipSuccess)
         return fail(kErrRuntime, "event creation failed");
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        cus <= 0)
+        return fail(kErrRuntime, "compute-unit count query failed");
+    compute_units = cus;
     return 0;
 }
 

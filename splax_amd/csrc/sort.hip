@@ -3,7 +3,7 @@
 // splax/_rasterize/_sort/_kernels.py:28-153,214-241; the sort replaces warp-lang's
 // radix_sort_pairs (called at splax/_rasterize/_sort/_sort.py:136).
 //
-// Sort design: each pass is reduce-then-scan over partitions of 4096 or 8192 keys: (1) every
+// Sort design: each pass is reduce-then-scan over partitions of 4096 to 8192 keys: (1) every
 // partition counts its digits, (2) one workgroup per digit scans that digit's counts over the
 // partitions and writes the digit's total, (3) every partition ranks its keys stably with
 // ballot-based digit matching per wave and scatters keys and values through LDS so that each
@@ -604,9 +604,22 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     }
     {
         StageTimer tm(stream, kStageSort);
-        // 8192-key partitions from 1M keys on: their digit runs (about 32 keys) leave as whole
-        // 128-byte lines; smaller sorts use 4096-key partitions, so they still spread over the CUs
+        // 64-bit keys: 8192-key partitions from 1M keys on (digit runs of about 32 keys leave as
+        // whole 128-byte lines), 4096-key partitions below, so small sorts still spread over the
+        // CUs
         const bool big = M >= kSortBigM;
+        // packed keys: one partition per workgroup and two 1024-thread workgroups per CU. The
+        // smallest of 4..8 keys per thread whose partitions all fit in one round of workgroups,
+        // else 8: a second round that only a few partitions occupy costs nearly a whole round
+        // (at 2.66M keys, 6 keys per thread sort in 0.109 ms, 5 in 0.128 and 8 in 0.121)
+        const int64_t slots = 2 * (int64_t)(sc.compute_units > 0 ? sc.compute_units : 256);
+        int items = 8;
+        for (int k = 4; k < 8; ++k) {
+            if ((M + (int64_t)k * kSortThreads - 1) / ((int64_t)k * kSortThreads) <= slots) {
+                items = k;
+                break;
+            }
+        }
         // passes ping-pong 0 -> 1 -> 0 ...; the first pass generates the emission positions,
         // the last writes positions and items straight into their final buffers (the caller's
         // when it keeps the sorted lists)
@@ -630,12 +643,27 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
             } else {
                 const uint32_t* ki = reinterpret_cast<const uint32_t*>(sc.keys[src]);
                 uint32_t* ko = reinterpret_cast<uint32_t*>(sc.keys[dst]);
-                if (big)
-                    launch_pass<uint32_t, 8>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
-                                             sc.part_counts, sc.hist, bins, nb2, stream);
-                else
+                switch (items) {
+                case 4:
                     launch_pass<uint32_t, 4>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
                                              sc.part_counts, sc.hist, bins, nb2, stream);
+                    break;
+                case 5:
+                    launch_pass<uint32_t, 5>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                                             sc.part_counts, sc.hist, bins, nb2, stream);
+                    break;
+                case 6:
+                    launch_pass<uint32_t, 6>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                                             sc.part_counts, sc.hist, bins, nb2, stream);
+                    break;
+                case 7:
+                    launch_pass<uint32_t, 7>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                                             sc.part_counts, sc.hist, bins, nb2, stream);
+                    break;
+                default:
+                    launch_pass<uint32_t, 8>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                                             sc.part_counts, sc.hist, bins, nb2, stream);
+                }
             }
         }
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "sort launch failed");

@@ -106,6 +106,7 @@ enum : uint32_t {
 // buffers grow with 1.25x headroom; everything is freed by splat_clear_cache().
 struct DeviceScratch {
     int device = -1;
+    int compute_units = 0;
     std::mutex mu;
     // projection scan
     uint32_t* chunk_sums = nullptr; int64_t chunk_sums_cap = 0;  // projection scan partials

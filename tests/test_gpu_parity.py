@@ -99,6 +99,29 @@ def test_sort_and_bin_bit_exact(name):
     assert_bit_exact(_np(gbins), rbins, f"{name}/bins")
 
 
+@pytest.mark.parametrize("n", [820_000, 1_300_000, 1_450_000])
+def test_sort_partition_sizes_bit_exact(n):
+    """Packed-key sorts whose partition size the library picks from M and the CU count: on 256
+    CUs these scenes (M of about 2.2M, 3.5M and 3.9M) take 5, 7 and 8 keys per thread; config 2
+    itself (2.66M) takes 6, covered by the full-size test."""
+    _case(f"sort partition sizes n={n}")
+    O.set_threads(16)
+    s = make_scene(2, n=n)
+    q = np.roll(s.quats, -1, axis=-1)
+    xys, depths, radii, conics, nth, cum = O.project_fwd(
+        s.means, s.scales, q, s.viewmats[0], s.opacities, n=s.n, total=s.n,
+        img_shape=s.img_shape, f=s.f, c=s.c)
+    rk, rid, rbins = O.sort_and_bin(xys, depths, radii, conics, s.opacities, cum, n=s.n, B=1,
+                                    img_shape=s.img_shape)
+    gk, gid, gbins = _ops.sort_and_bin(_t(xys), _t(depths), _t(radii), _t(conics),
+                                       _t(s.opacities).reshape(-1), _t(cum), n=s.n, B=1,
+                                       img_shape=s.img_shape)
+    torch.cuda.synchronize()
+    assert_bit_exact(_np(gk), rk, f"n={n}/keys")
+    assert_bit_exact(_np(gid), rid, f"n={n}/ids")
+    assert_bit_exact(_np(gbins), rbins, f"n={n}/bins")
+
+
 def _raster_inputs(s):
     q = np.roll(s.quats, -1, axis=-1)
     proj = O.project_fwd(s.means, s.scales, q, s.viewmats[0], s.opacities, n=s.n, total=s.n,
