@@ -391,8 +391,8 @@ int splat_set_stage_timing(int stage_mask);
 int splat_get_stage_times(double* ms, int64_t* calls, int32_t n);
 
 /* Waits for the current device and returns (then clears) its device error word: 0 when every
- * kernel ran within its invariants; bit 0 (value 1) when splat_rasterize_bwd_sorted met a kept
- * tile order entry or tile-bin range out of range (that tile is then skipped or its range
+ * kernel ran within its invariants; bit 0 (value 1) when splat_rasterize_bwd_sorted or
+ * splat_render_bwd met a kept tile order entry or tile-bin range out of range (that tile is then skipped or its range
  * clamped to [0, M], so nothing is read out of bounds, but the call's gradients are not the
  * forward's). No counterpart in the reference. */
 int splat_check_device(void);
