@@ -109,6 +109,63 @@ __device__ __forceinline__ uint32_t subblock_mask(const float4& r0, const float4
     return m;
 }
 
+// The forward's sub-block mask: the sub-blocks whose pixel centres the record can reach, from the
+// exact x-extent of its ellipse over each 4-row band of the tile's pixel centres (the box test
+// above also keeps sub-blocks that only the box's corners reach; on config 2 the forward's row
+// walks take 23% fewer steps with this mask).
+// With Q(dx, dy) = a/2 dx^2 + b dx dy + c/2 dy^2 (dx, dy from the centre), the test uses the
+// ellipse Q <= s' with s' = 1.0201 sigma_max, i.e. {sigma <= sigma_max} scaled by 1.01: an
+// evaluated sigma <= sigma_max has an exact Q within 0.6% of it for the conics the box mode
+// accepts ((a + c)^2 / det < 1e4), so every such pixel centre lies inside. The chord of that
+// ellipse at height dy is centred at -b dy / a with half-width sqrt(2 a s' - det dy^2) / a, so its
+// right end is concave in dy and peaks at the rightmost point (dx, dy) = (ex, -b ex / c), ex =
+// sqrt(2 s' c / det); over a band [dy0, dy1] clipped to |dy| <= ey the extent is therefore
+// [min of the left ends at dy0 and dy1, or -ex when the leftmost point lies in the band,
+//  max of the right ends, or ex when the rightmost point lies in it], widened by m = 0.01 px +
+// 1e-3 ex against rounding (the rows are clipped to |dy| <= ey + m, where the chord's width is
+// taken as 0 beyond ey). A sub-block is kept when its pixel-centre columns meet that extent.
+constexpr float kTightScale2 = 1.0201f;
+__device__ __forceinline__ uint32_t subblock_mask_tight(const float4& r0, const float4& r1,
+                                                        const float4& r3, int tile_x,
+                                                        int tile_y) {
+    const uint32_t mode = __float_as_uint(r3.z);
+    if (mode == kCullNone) return 0u;
+    if (mode != kCullBox) return 0xffffu;
+    // hardware reciprocal and square root (about 1 ulp each): the margins absorb them
+    const float a = 2.0f * r0.z, b = r0.w, c = 2.0f * r1.x;
+    const float s2 = 2.0f * (kTightScale2 * r1.z);  // 2 s'
+    const float det = a * c - b * b;
+    const float inv_a = __builtin_amdgcn_rcpf(a), inv_det = __builtin_amdgcn_rcpf(det);
+    const float ex = __builtin_amdgcn_sqrtf(s2 * c * inv_det);
+    const float ey = __builtin_amdgcn_sqrtf(s2 * a * inv_det);
+    const float dy_r = -(b * ex) * __builtin_amdgcn_rcpf(c);  // rightmost point; leftmost at -dy_r
+    const float m = 0.01f + 1e-3f * ex;
+    const float two_a_s = a * s2, nb_a = -b * inv_a;
+    const float bx = (float)(tile_x * kBlockWidth) + 0.5f - r0.x;  // dx of the tile's first column
+    const float by = (float)(tile_y * kBlockWidth) + 0.5f - r0.y;
+    uint32_t mask = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float y0 = by + (float)(4 * j);
+        const float d0 = fmaxf(y0, -ey - m), d1 = fminf(y0 + 3.0f, ey + m);
+        const float w0 = __builtin_amdgcn_sqrtf(fmaxf(two_a_s - det * (d0 * d0), 0.0f)) * inv_a;
+        const float w1 = __builtin_amdgcn_sqrtf(fmaxf(two_a_s - det * (d1 * d1), 0.0f)) * inv_a;
+        const float c0 = nb_a * d0, c1 = nb_a * d1;
+        float hi = fmaxf(c0 + w0, c1 + w1), lo = fminf(c0 - w0, c1 - w1);
+        hi = (dy_r >= d0 && dy_r <= d1) ? ex : hi;
+        lo = (-dy_r >= d0 && -dy_r <= d1) ? -ex : lo;
+        hi = hi + m;
+        lo = lo - m;
+        const bool band = d0 <= d1;  // the band's rows meet |dy| <= ey + m
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x0 = bx + (float)(4 * i);
+            mask |= (band && x0 <= hi && x0 + 3.0f >= lo) ? (1u << (4 * j + i)) : 0u;
+        }
+    }
+    return mask;
+}
+
 // LDS record of one batch: r0 = (x, y, a/2, b), r1 = (c/2, o, sigma_max, 0), r2 = (red, green,
 // blue, depth), each record's sub-block mask, and per-sub-block compacted record lists.
 struct BatchLds {
@@ -142,7 +199,8 @@ __device__ __forceinline__ RowLens stage_batch(const BlendCommon& C, BatchLds& L
         r0 = rec[0];
         r1 = rec[1];
         r2 = rec[2];
-        m = subblock_mask(r0, rec[3], tile_x, tile_y);
+        m = kRows ? subblock_mask_tight(r0, r1, rec[3], tile_x, tile_y)
+                  : subblock_mask(r0, rec[3], tile_x, tile_y);
     }
     L.r0[tid] = r0;
     L.r1[tid] = r1;
