@@ -125,44 +125,63 @@ __device__ __forceinline__ uint32_t subblock_mask(const float4& r0, const float4
 // 1e-3 ex against rounding (the rows are clipped to |dy| <= ey + m, where the chord's width is
 // taken as 0 beyond ey). A sub-block is kept when its pixel-centre columns meet that extent.
 constexpr float kTightScale2 = 1.0201f;
+
+// The tile-relative quantities of that test for one kCullBox record (hardware reciprocal and
+// square root, about 1 ulp each: the margins absorb them).
+struct TightEllipse {
+    float det, inv_a, ex, ey, dy_r, m, two_a_s, nb_a, bx, by;
+};
+__device__ __forceinline__ TightEllipse tight_setup(const float4& r0, const float4& r1,
+                                                    int tile_x, int tile_y) {
+    TightEllipse e;
+    const float a = 2.0f * r0.z, b = r0.w, c = 2.0f * r1.x;
+    const float s2 = 2.0f * (kTightScale2 * r1.z);  // 2 s'
+    e.det = a * c - b * b;
+    e.inv_a = __builtin_amdgcn_rcpf(a);
+    const float inv_det = __builtin_amdgcn_rcpf(e.det);
+    e.ex = __builtin_amdgcn_sqrtf(s2 * c * inv_det);
+    e.ey = __builtin_amdgcn_sqrtf(s2 * a * inv_det);
+    e.dy_r = -(b * e.ex) * __builtin_amdgcn_rcpf(c);  // rightmost point; leftmost at -dy_r
+    e.m = 0.01f + 1e-3f * e.ex;
+    e.two_a_s = a * s2;
+    e.nb_a = -b * e.inv_a;
+    e.bx = (float)(tile_x * kBlockWidth) + 0.5f - r0.x;  // dx of the tile's first column
+    e.by = (float)(tile_y * kBlockWidth) + 0.5f - r0.y;
+    return e;
+}
+
+// Bits 4 j .. 4 j + 3 of the mask: the sub-blocks of band j (pixel-centre rows 4 j .. 4 j + 3).
+__device__ __forceinline__ uint32_t tight_band(const TightEllipse& e, int j) {
+    const float y0 = e.by + (float)(4 * j);
+    const float d0 = fmaxf(y0, -e.ey - e.m), d1 = fminf(y0 + 3.0f, e.ey + e.m);
+    const float w0 = __builtin_amdgcn_sqrtf(fmaxf(e.two_a_s - e.det * (d0 * d0), 0.0f)) * e.inv_a;
+    const float w1 = __builtin_amdgcn_sqrtf(fmaxf(e.two_a_s - e.det * (d1 * d1), 0.0f)) * e.inv_a;
+    const float c0 = e.nb_a * d0, c1 = e.nb_a * d1;
+    float hi = fmaxf(c0 + w0, c1 + w1), lo = fminf(c0 - w0, c1 - w1);
+    hi = (e.dy_r >= d0 && e.dy_r <= d1) ? e.ex : hi;
+    lo = (-e.dy_r >= d0 && -e.dy_r <= d1) ? -e.ex : lo;
+    hi = hi + e.m;
+    lo = lo - e.m;
+    const bool band = d0 <= d1;  // the band's rows meet |dy| <= ey + m
+    uint32_t bits = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float x0 = e.bx + (float)(4 * i);
+        bits |= (band && x0 <= hi && x0 + 3.0f >= lo) ? (1u << (4 * j + i)) : 0u;
+    }
+    return bits;
+}
+
 __device__ __forceinline__ uint32_t subblock_mask_tight(const float4& r0, const float4& r1,
                                                         const float4& r3, int tile_x,
                                                         int tile_y) {
     const uint32_t mode = __float_as_uint(r3.z);
     if (mode == kCullNone) return 0u;
     if (mode != kCullBox) return 0xffffu;
-    // hardware reciprocal and square root (about 1 ulp each): the margins absorb them
-    const float a = 2.0f * r0.z, b = r0.w, c = 2.0f * r1.x;
-    const float s2 = 2.0f * (kTightScale2 * r1.z);  // 2 s'
-    const float det = a * c - b * b;
-    const float inv_a = __builtin_amdgcn_rcpf(a), inv_det = __builtin_amdgcn_rcpf(det);
-    const float ex = __builtin_amdgcn_sqrtf(s2 * c * inv_det);
-    const float ey = __builtin_amdgcn_sqrtf(s2 * a * inv_det);
-    const float dy_r = -(b * ex) * __builtin_amdgcn_rcpf(c);  // rightmost point; leftmost at -dy_r
-    const float m = 0.01f + 1e-3f * ex;
-    const float two_a_s = a * s2, nb_a = -b * inv_a;
-    const float bx = (float)(tile_x * kBlockWidth) + 0.5f - r0.x;  // dx of the tile's first column
-    const float by = (float)(tile_y * kBlockWidth) + 0.5f - r0.y;
+    const TightEllipse e = tight_setup(r0, r1, tile_x, tile_y);
     uint32_t mask = 0u;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float y0 = by + (float)(4 * j);
-        const float d0 = fmaxf(y0, -ey - m), d1 = fminf(y0 + 3.0f, ey + m);
-        const float w0 = __builtin_amdgcn_sqrtf(fmaxf(two_a_s - det * (d0 * d0), 0.0f)) * inv_a;
-        const float w1 = __builtin_amdgcn_sqrtf(fmaxf(two_a_s - det * (d1 * d1), 0.0f)) * inv_a;
-        const float c0 = nb_a * d0, c1 = nb_a * d1;
-        float hi = fmaxf(c0 + w0, c1 + w1), lo = fminf(c0 - w0, c1 - w1);
-        hi = (dy_r >= d0 && dy_r <= d1) ? ex : hi;
-        lo = (-dy_r >= d0 && -dy_r <= d1) ? -ex : lo;
-        hi = hi + m;
-        lo = lo - m;
-        const bool band = d0 <= d1;  // the band's rows meet |dy| <= ey + m
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float x0 = bx + (float)(4 * i);
-            mask |= (band && x0 <= hi && x0 + 3.0f >= lo) ? (1u << (4 * j + i)) : 0u;
-        }
-    }
+    for (int j = 0; j < 4; ++j) mask |= tight_band(e, j);
     return mask;
 }
 
