@@ -28,6 +28,8 @@
 // tile's four quadrant waves depend on the order in which the waves arrive.
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 #include "splat_common.hpp"
 #include "splat_internal.hpp"
 
@@ -185,30 +187,29 @@ __device__ __forceinline__ uint32_t subblock_mask_tight(const float4& r0, const 
     return mask;
 }
 
-// LDS record of one batch: r0 = (x, y, a/2, b), r1 = (c/2, o, sigma_max, 0), r2 = (red, green,
-// blue, depth), each record's sub-block mask, and per-sub-block compacted record lists.
+// LDS records of one batch: r0 = (x, y, a/2, b), r1 = (c/2, o, sigma_max, 0), r2 = (red, green,
+// blue, depth), each record's sub-block mask, and compacted record lists: with kRows (the
+// forward) one per sub-block, of record byte offsets (16 t for slot t: the address needs no
+// shift), otherwise (the backward) one per quadrant wave, of slot indices. The backward's four
+// lists keep its LDS at 26 KB, six workgroups per CU (sixteen lists: five).
+template <bool kRows>
 struct BatchLds {
     float4 r0[kTile];
     float4 r1[kTile];
     float4 r2[kTile];
     uint16_t mask[kTile];
-    uint8_t list[16][kTile];
-};
-
-// Lengths of the calling lane's row list and of the longest row list of its wave.
-struct RowLens {
-    int mine;
-    int wave_max;
+    typename std::conditional<kRows, uint16_t, uint8_t>::type list[kRows ? 16 : 4][kTile];
 };
 
 // Stages record `src` of the sorted range into slot `tid` (one barrier), then each wave builds
 // its own record lists from the staged masks, in slot order: with kRows the lists of its four
 // sub-blocks (one per 16-lane row), otherwise the list of its whole quadrant (a record reaches a
 // quadrant when it reaches one of its sub-blocks, which is the 8x8 box test). `live` is false
-// for the clamped tail slots of the last batch (they reach no sub-block).
+// for the clamped tail slots of the last batch (they reach no sub-block). Returns the length of
+// the wave's longest list, with kRows plus 65536 times the calling lane's row list length.
 template <bool kRows>
-__device__ __forceinline__ RowLens stage_batch(const BlendCommon& C, BatchLds& L, int32_t src,
-                                               bool live, int tile_x, int tile_y) {
+__device__ __forceinline__ int stage_batch(const BlendCommon& C, BatchLds<kRows>& L, int32_t src,
+                                           bool live, int tile_x, int tile_y) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, row = lane >> 4;
     int64_t g = C.ids[src];
     uint32_t m = 0u;
@@ -239,14 +240,14 @@ __device__ __forceinline__ RowLens stage_batch(const BlendCommon& C, BatchLds& L
                 const int b = sb0 + (r & 1) + (r >> 1) * 4;
                 const bool bit = (mc >> b) & 1u;
                 const uint64_t bal = __ballot(bit);
-                if (bit) L.list[b][n[r] + (int)__popcll(bal & lt)] = (uint8_t)(c * 64 + lane);
+                if (bit) L.list[b][n[r] + (int)__popcll(bal & lt)] = (uint16_t)((c * 64 + lane) * 16);
                 n[r] += (int)__popcll(bal);
             }
         }
         __builtin_amdgcn_wave_barrier();
         const int mine = row == 0 ? n[0] : row == 1 ? n[1] : row == 2 ? n[2] : n[3];
         const int a = n[0] > n[1] ? n[0] : n[1], b = n[2] > n[3] ? n[2] : n[3];
-        return RowLens{mine, a > b ? a : b};
+        return (a > b ? a : b) | (mine << 16);
     } else {
         const uint32_t qbits = (0x33u << sb0);  // the quadrant's four sub-blocks
         int nq = 0;
@@ -258,7 +259,7 @@ __device__ __forceinline__ RowLens stage_batch(const BlendCommon& C, BatchLds& L
             nq += (int)__popcll(bal);
         }
         __builtin_amdgcn_wave_barrier();
-        return RowLens{nq, nq};
+        return nq;
     }
 }
 
@@ -278,11 +279,14 @@ __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirs
 // -87 (the reduction's error grows with |k|). Ten VALU; the CPU oracle evaluates the same
 // sequence.
 constexpr float kBlendLn2 = 0x1.62e430p-1f;
-__device__ __forceinline__ float blend_exp(float x) {
-    const float t = fmaf(x, kLog2e, 0x1.8p23f);
+constexpr float kBlendExpC5 = 0x1.123a6cp-7f;
+__device__ __forceinline__ float blend_exp(float x, float round_c = 0x1.8p23f,
+                                           float c5 = kBlendExpC5) {
+    // round_c = 1.5 * 2^23 and c5 may come in as register copies of the constants
+    const float t = fmaf(x, kLog2e, round_c);
     const float kf = t - 0x1.8p23f;
     const float r = fmaf(kf, -kBlendLn2, x);
-    float p = fmaf(r, 0x1.6a2352p-10f, 0x1.123a6cp-7f);
+    float p = fmaf(r, 0x1.6a2352p-10f, c5);
     p = fmaf(r, p, 0x1.5558f4p-5f);
     p = fmaf(r, p, 0x1.55549p-3f);
     p = fmaf(r, p, 0x1.fffffcp-2f);
@@ -312,7 +316,7 @@ struct BlendFwdParams {
 // (splax/_rasterize/_kernels.py:277-383): depth times the same blend weight, no background term.
 template <bool kDepth>
 __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
-    __shared__ BatchLds L;
+    __shared__ BatchLds<true> L;
     const BlendCommon& C = P.c;
     const int tid = threadIdx.x;
     const int32_t tile_g = C.order[blockIdx.x];
@@ -331,23 +335,31 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
     float T = 1.0f;
     int32_t cur_idx = 0;
     float o0 = 0.f, o1 = 0.f, o2 = 0.f, od = 0.f;
+    // blend_exp's constants that enter as addends held in registers (the compiler would
+    // re-materialize them in every step)
+    float exp_round = 0x1.8p23f, exp_c5 = kBlendExpC5;
+    asm volatile("" : "+v"(exp_round), "+v"(exp_c5));
+    const char* rec_base = reinterpret_cast<const char*>(L.r0);
 
     for (int32_t bt = 0; bt < num_batches; ++bt) {
         // every pixel done -> stop; also the barrier before the LDS records are overwritten
         if (__syncthreads_count(done) >= kTile) break;
         const int32_t batch_start = range_start + bt * kTile;
         const int32_t src = iminw(batch_start + tid, range_end - 1);
-        const RowLens len =
+        const int lens =
             stage_batch<true>(C, L, src, batch_start + tid < range_end, tile_x, tile_y);
         if (__ballot(!done) == 0ull) continue;
-        const uint8_t* list = L.list[sb];
-        const int my_len = len.mine;  // uniform per row
-        for (int k = 0; k < len.wave_max; ++k) {
+        const int wave_max = lens & 0xffff, my_len = lens >> 16;  // my_len uniform per row
+        const uint16_t* list = L.list[sb];
+        int32_t last_off = -1;  // the last accepted record of this batch (byte offset)
+        for (int k = 0; k < wave_max; ++k) {
             // A lane leaves once its pixel is done or its row's list is walked; the wave walks
-            // while any lane is left, which is exec-mask bookkeeping only.
+            // while any lane is left, which is exec-mask bookkeeping only. (Padding the shorter
+            // lists with a record no pixel accepts instead of the length test measured slower.)
             if (done || k >= my_len) break;
-            const int t = list[k];
-            const float4 r0 = L.r0[t], r1 = L.r1[t];
+            const int off = list[k];
+            const float4 r0 = *reinterpret_cast<const float4*>(rec_base + off);
+            const float4 r1 = *reinterpret_cast<const float4*>(rec_base + off + sizeof(L.r0));
             // all of r1 in the first read (one full-width read, one address)
             asm volatile("" ::"v"(r1.y));
             const float dx = r0.x - px, dy = r0.y - py;
@@ -358,24 +370,26 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
             if ((sigma >= 0.0f) & (sigma <= r1.z)) {
                 // v_min: no accepted record has a NaN opacity (the pack culls those), so it
                 // equals the reference's compare-and-select minimum here
-                const float alpha = fminf(kAlphaMax, r1.y * blend_exp(-sigma));
+                const float alpha = fminf(kAlphaMax, r1.y * blend_exp(-sigma, exp_round, exp_c5));
                 if (alpha >= kAlphaThresh) {
                     const float next_T = T * (1.0f - alpha);
                     if (next_T <= kTEps) {
                         done = true;  // leaves at the next step
                     } else {
-                        const float4 r2 = L.r2[t];
+                        const float4 r2 = *reinterpret_cast<const float4*>(
+                            rec_base + off + 2 * sizeof(L.r0));
                         const float vis = alpha * T;
                         o0 = fmaf(r2.x, vis, o0);
                         o1 = fmaf(r2.y, vis, o1);
                         o2 = fmaf(r2.z, vis, o2);
                         if constexpr (kDepth) od = fmaf(r2.w, vis, od);
                         T = next_T;
-                        cur_idx = batch_start + t;
+                        last_off = off;
                     }
                 }
             }
         }
+        if (last_off >= 0) cur_idx = batch_start + (last_off >> 4);
     }
     if (inside) {
         const int64_t bgi = C.rows_bg > 1 ? image_id : 0;
@@ -596,7 +610,7 @@ constexpr int kAccSlots = 12;
 template <bool kDepth>
 __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     constexpr int NG = kDepth ? 10 : 9;
-    __shared__ BatchLds L;
+    __shared__ BatchLds<false> L;
     __shared__ float acc[kTile * kAccSlots];
     __shared__ int32_t s_max;
 
@@ -690,7 +704,7 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
         const int32_t src = imaxw(batch_end - tid, range_start);
         const bool live = batch_end - tid >= range_start;
         const int32_t my_pos = live ? P.pos[src] : -1;  // emission position of slot tid
-        const int len = uniform(stage_batch<false>(C, L, src, live, tile_x, tile_y).wave_max);
+        const int len = uniform(stage_batch<false>(C, L, src, live, tile_x, tile_y));
         // the wave's list in one register: lane l holds entries 4l .. 4l + 3
         const uint32_t list4 = reinterpret_cast<const uint32_t*>(L.list[uniform(wave)])[lane];
         uint32_t word = 0;
