@@ -192,14 +192,19 @@ __device__ __forceinline__ uint32_t subblock_mask_tight(const float4& r0, const 
 // forward) one per sub-block, of record byte offsets (16 t for slot t: the address needs no
 // shift), otherwise (the backward) one per quadrant wave, of slot indices. The backward's four
 // lists keep its LDS at 26 KB, six workgroups per CU (sixteen lists: five).
-template <bool kRows>
+template <bool kRows, int kBatch>
 struct BatchLds {
-    float4 r0[kTile];
-    float4 r1[kTile];
-    float4 r2[kTile];
-    uint16_t mask[kTile];
+    float4 r0[kBatch];
+    float4 r1[kBatch];
+    float4 r2[kBatch];
+    uint16_t mask[kBatch];
+    // a backward wave reads its whole list row as one dword per lane: rows of kTile bytes
     typename std::conditional<kRows, uint16_t, uint8_t>::type list[kRows ? 16 : 4][kTile];
 };
+// Records per batch of the backward: 192 keeps its LDS at 20 KB, so with at most 64 VGPRs eight
+// workgroups share a CU (eight waves per SIMD: 0.43 ms at config 2 against 0.44 with 224 records
+// and seven, 0.46 with 256 and six).
+constexpr int kBwdBatch = 192;
 
 // Stages record `src` of the sorted range into slot `tid` (one barrier), then each wave builds
 // its own record lists from the staged masks, in slot order: with kRows the lists of its four
@@ -207,9 +212,9 @@ struct BatchLds {
 // quadrant when it reaches one of its sub-blocks, which is the 8x8 box test). `live` is false
 // for the clamped tail slots of the last batch (they reach no sub-block). Returns the length of
 // the wave's longest list, with kRows plus 65536 times the calling lane's row list length.
-template <bool kRows>
-__device__ __forceinline__ int stage_batch(const BlendCommon& C, BatchLds<kRows>& L, int32_t src,
-                                           bool live, int tile_x, int tile_y) {
+template <bool kRows, int kBatch>
+__device__ __forceinline__ int stage_batch(const BlendCommon& C, BatchLds<kRows, kBatch>& L,
+                                           int32_t src, bool live, int tile_x, int tile_y) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, row = lane >> 4;
     int64_t g = C.ids[src];
     uint32_t m = 0u;
@@ -222,10 +227,12 @@ __device__ __forceinline__ int stage_batch(const BlendCommon& C, BatchLds<kRows>
         m = kRows ? subblock_mask_tight(r0, r1, rec[3], tile_x, tile_y)
                   : subblock_mask(r0, rec[3], tile_x, tile_y);
     }
-    L.r0[tid] = r0;
-    L.r1[tid] = r1;
-    L.r2[tid] = r2;
-    L.mask[tid] = (uint16_t)m;
+    if (kBatch == kTile || tid < kBatch) {
+        L.r0[tid] = r0;
+        L.r1[tid] = r1;
+        L.r2[tid] = r2;
+        L.mask[tid] = (uint16_t)m;
+    }
     __syncthreads();
     // this wave's sub-blocks: rows 0..3 -> sb0, sb0 + 1, sb0 + 4, sb0 + 5
     const int sb0 = (wave >> 1) * 8 + (wave & 1) * 2;
@@ -233,8 +240,9 @@ __device__ __forceinline__ int stage_batch(const BlendCommon& C, BatchLds<kRows>
     if constexpr (kRows) {
         int n[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int c = 0; c < kTile / 64; ++c) {
-            const uint32_t mc = L.mask[c * 64 + lane];
+        for (int c = 0; c < (kBatch + 63) / 64; ++c) {
+            const uint32_t mc =
+                (kBatch % 64 == 0 || c * 64 + lane < kBatch) ? L.mask[c * 64 + lane] : 0u;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int b = sb0 + (r & 1) + (r >> 1) * 4;
@@ -252,8 +260,9 @@ __device__ __forceinline__ int stage_batch(const BlendCommon& C, BatchLds<kRows>
         const uint32_t qbits = (0x33u << sb0);  // the quadrant's four sub-blocks
         int nq = 0;
 #pragma unroll
-        for (int c = 0; c < kTile / 64; ++c) {
-            const bool bit = (L.mask[c * 64 + lane] & qbits) != 0u;
+        for (int c = 0; c < (kBatch + 63) / 64; ++c) {
+            const bool bit = (kBatch % 64 == 0 || c * 64 + lane < kBatch) &&
+                             (L.mask[c * 64 + lane] & qbits) != 0u;
             const uint64_t bal = __ballot(bit);
             if (bit) L.list[wave][nq + (int)__popcll(bal & lt)] = (uint8_t)(c * 64 + lane);
             nq += (int)__popcll(bal);
@@ -314,9 +323,11 @@ struct BlendFwdParams {
 
 // kDepth adds the expected-depth channel of _rasterize_depth_kernel
 // (splax/_rasterize/_kernels.py:277-383): depth times the same blend weight, no background term.
+// At most 72 VGPRs: seven waves per SIMD (0.187 ms at config 2 against 0.195 at the compiler's
+// own 79 VGPRs and six; forcing eight spills registers).
 template <bool kDepth>
-__global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
-    __shared__ BatchLds<true> L;
+__global__ void __launch_bounds__(kTile, 7) blend_fwd_kernel(BlendFwdParams P) {
+    __shared__ BatchLds<true, kTile> L;
     const BlendCommon& C = P.c;
     const int tid = threadIdx.x;
     const int32_t tile_g = C.order[blockIdx.x];
@@ -347,7 +358,7 @@ __global__ void __launch_bounds__(kTile) blend_fwd_kernel(BlendFwdParams P) {
         const int32_t batch_start = range_start + bt * kTile;
         const int32_t src = iminw(batch_start + tid, range_end - 1);
         const int lens =
-            stage_batch<true>(C, L, src, batch_start + tid < range_end, tile_x, tile_y);
+            stage_batch<true, kTile>(C, L, src, batch_start + tid < range_end, tile_x, tile_y);
         if (__ballot(!done) == 0ull) continue;
         const int wave_max = lens & 0xffff, my_len = lens >> 16;  // my_len uniform per row
         const uint16_t* list = L.list[sb];
@@ -610,8 +621,8 @@ constexpr int kAccSlots = 12;
 template <bool kDepth>
 __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     constexpr int NG = kDepth ? 10 : 9;
-    __shared__ BatchLds<false> L;
-    __shared__ float acc[kTile * kAccSlots];
+    __shared__ BatchLds<false, kBwdBatch> L;
+    __shared__ float acc[kBwdBatch * kAccSlots];
     __shared__ int32_t s_max;
 
     const BlendCommon& C = P.c;
@@ -665,7 +676,7 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     // running sum
     float acc_v = tfbg;
     if (tid == 0) s_max = range_start - 1;
-    for (int k = tid; k < kTile * kAccSlots; k += kTile) acc[k] = 0.0f;
+    for (int k = tid; k < kBwdBatch * kAccSlots; k += kTile) acc[k] = 0.0f;
     __syncthreads();
     atomicMax(&s_max, bin_final);
     // wave-wide largest final index: a record above it has no contributing lane in this wave
@@ -679,7 +690,7 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     __syncthreads();
     // a final_idx from the matching forward lies inside the tile's range; clamp anything else
     const int32_t start_idx = iminw(s_max, range_end - 1);
-    const int32_t num_batches = (start_idx - range_start + kTile) / kTile;
+    const int32_t num_batches = (start_idx - range_start + kBwdBatch) / kBwdBatch;
     const int64_t rg_off = P.sel_geom ? 0 : (int64_t)image_id * P.M;
     {
         // intersections above every final index of the tile contribute nothing
@@ -700,11 +711,11 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     const bool adds = l16 == 0 || l16 == 4 || l16 == 8;
     const int kslot = l16 == 0 ? ka : l16 == 8 ? 4 + ka : 8 + row;
     for (int32_t bt = 0; bt < num_batches; ++bt) {
-        const int32_t batch_end = start_idx - bt * kTile;
+        const int32_t batch_end = start_idx - bt * kBwdBatch;
         const int32_t src = imaxw(batch_end - tid, range_start);
-        const bool live = batch_end - tid >= range_start;
+        const bool live = tid < kBwdBatch && batch_end - tid >= range_start;
         const int32_t my_pos = live ? P.pos[src] : -1;  // emission position of slot tid
-        const int len = uniform(stage_batch<false>(C, L, src, live, tile_x, tile_y));
+        const int len = uniform(stage_batch<false, kBwdBatch>(C, L, src, live, tile_x, tile_y));
         // the wave's list in one register: lane l holds entries 4l .. 4l + 3
         const uint32_t list4 = reinterpret_cast<const uint32_t*>(L.list[uniform(wave)])[lane];
         uint32_t word = 0;
@@ -766,7 +777,7 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             if (adds) atomicAdd(&acc[t * kAccSlots + kslot], sum);
         }
         __syncthreads();
-        {
+        if (tid < kBwdBatch) {
             float s[NG], part[4];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
