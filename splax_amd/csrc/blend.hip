@@ -128,22 +128,22 @@ __device__ __forceinline__ uint32_t subblock_mask(const float4& r0, const float4
 // taken as 0 beyond ey). A sub-block is kept when its pixel-centre columns meet that extent.
 constexpr float kTightScale2 = 1.0201f;
 
-// The tile-relative quantities of that test for one kCullBox record (hardware reciprocal and
-// square root, about 1 ulp each: the margins absorb them).
+// The tile-relative quantities of that test for one kCullBox record. The record carries the
+// tile-independent parts, formed once per item by the pack: 1 / a in r1.w, the scaled ellipse's
+// half-widths as the box's minus its 0.01 px, and the rightmost point's height in r3.w.
 struct TightEllipse {
     float det, inv_a, ex, ey, dy_r, m, two_a_s, nb_a, bx, by;
 };
 __device__ __forceinline__ TightEllipse tight_setup(const float4& r0, const float4& r1,
-                                                    int tile_x, int tile_y) {
+                                                    const float4& r3, int tile_x, int tile_y) {
     TightEllipse e;
     const float a = 2.0f * r0.z, b = r0.w, c = 2.0f * r1.x;
     const float s2 = 2.0f * (kTightScale2 * r1.z);  // 2 s'
     e.det = a * c - b * b;
-    e.inv_a = __builtin_amdgcn_rcpf(a);
-    const float inv_det = __builtin_amdgcn_rcpf(e.det);
-    e.ex = __builtin_amdgcn_sqrtf(s2 * c * inv_det);
-    e.ey = __builtin_amdgcn_sqrtf(s2 * a * inv_det);
-    e.dy_r = -(b * e.ex) * __builtin_amdgcn_rcpf(c);  // rightmost point; leftmost at -dy_r
+    e.inv_a = r1.w;
+    e.ex = r3.x - 0.01f;
+    e.ey = r3.y - 0.01f;
+    e.dy_r = r3.w;  // rightmost point; leftmost at -dy_r
     e.m = 0.01f + 1e-3f * e.ex;
     e.two_a_s = a * s2;
     e.nb_a = -b * e.inv_a;
@@ -180,14 +180,14 @@ __device__ __forceinline__ uint32_t subblock_mask_tight(const float4& r0, const 
     const uint32_t mode = __float_as_uint(r3.z);
     if (mode == kCullNone) return 0u;
     if (mode != kCullBox) return 0xffffu;
-    const TightEllipse e = tight_setup(r0, r1, tile_x, tile_y);
+    const TightEllipse e = tight_setup(r0, r1, r3, tile_x, tile_y);
     uint32_t mask = 0u;
 #pragma unroll
     for (int j = 0; j < 4; ++j) mask |= tight_band(e, j);
     return mask;
 }
 
-// LDS records of one batch: r0 = (x, y, a/2, b), r1 = (c/2, o, sigma_max, 0), r2 = (red, green,
+// LDS records of one batch: r0 = (x, y, a/2, b), r1 = (c/2, o, sigma_max, 1/a), r2 = (red, green,
 // blue, depth), each record's sub-block mask, and compacted record lists: with kRows (the
 // forward) one per sub-block, of record byte offsets (16 t for slot t: the address needs no
 // shift), otherwise (the backward) one per quadrant wave, of slot indices. The backward's four

@@ -247,20 +247,46 @@ __device__ __forceinline__ uint32_t scan_256(uint32_t v, uint32_t* s_tmp, uint32
     return off + incl - v;
 }
 
-// (2) one workgroup per digit d: counts[d][p] <- sum_{q < p} counts[d][q], and totals[d].
-__global__ void __launch_bounds__(256)
+// (2) one workgroup per digit d: counts[d][p] <- sum_{q < p} counts[d][q], and totals[d]. 1024
+// threads, four counts each: up to 4096 partitions (16M keys at 4 keys per thread, 32M at 8) in
+// one pass over the row.
+constexpr int kScanThreads = 1024;
+__global__ void __launch_bounds__(kScanThreads)
 rts_scan_kernel(uint32_t* __restrict__ counts, int64_t parts, uint32_t* __restrict__ totals) {
-    __shared__ uint32_t s_tmp[4];
-    const int d = blockIdx.x, tid = threadIdx.x;
+    __shared__ uint32_t s_wave[kScanThreads / 64];
+    const int d = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint32_t carry = 0;
     uint32_t* row = counts + (int64_t)d * parts;
-    for (int64_t p0 = 0; p0 < parts; p0 += 256) {
-        const int64_t p = p0 + tid;
-        const uint32_t v = p < parts ? row[p] : 0u;
-        uint32_t tot;
-        const uint32_t ex = scan_256(v, s_tmp, &tot);
-        if (p < parts) row[p] = carry + ex;
-        carry += tot;
+    for (int64_t p0 = 0; p0 < parts; p0 += 4 * kScanThreads) {
+        // four consecutive counts per thread
+        const int64_t p = p0 + 4 * (int64_t)tid;
+        uint32_t v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = p + k < parts ? row[p + k] : 0u;
+        const uint32_t mine = (v[0] + v[1]) + (v[2] + v[3]);
+        uint32_t incl = mine;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += o;
+        }
+        if (lane == 63) s_wave[wave] = incl;
+        __syncthreads();
+        uint32_t before = carry, tot = carry;
+#pragma unroll
+        for (int w = 0; w < kScanThreads / 64; ++w) {
+            const uint32_t x = s_wave[w];
+            before += w < wave ? x : 0u;
+            tot += x;
+        }
+        uint32_t run = before + incl - mine;  // exclusive prefix of this thread's first count
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (p + k < parts) row[p + k] = run;
+            run += v[k];
+        }
+        carry = tot;
+        __syncthreads();  // s_wave is rewritten by the next round
     }
     if (tid == 0) totals[d] = carry;
 }
@@ -413,7 +439,8 @@ static void launch_pass(const K* keys_in, const int32_t* vals_in, const int32_t*
     const int64_t parts = (M + (int64_t)kItems * kSortThreads - 1) / ((int64_t)kItems * kSortThreads);
     hipLaunchKernelGGL((rts_count_kernel<K, kItems>), dim3((unsigned)parts), dim3(kSortThreads),
                        0, stream, keys_in, M, shift, counts, parts, bins, nbins2);
-    hipLaunchKernelGGL(rts_scan_kernel, dim3(256), dim3(256), 0, stream, counts, parts, totals);
+    hipLaunchKernelGGL(rts_scan_kernel, dim3(256), dim3(kScanThreads), 0, stream, counts, parts,
+                       totals);
     hipLaunchKernelGGL((rts_scatter_kernel<K, kItems>), dim3((unsigned)parts),
                        dim3(kSortThreads), 0, stream, keys_in, vals_in, ids_in, keys_out,
                        vals_out, ids_out, M, shift, counts, totals, parts);

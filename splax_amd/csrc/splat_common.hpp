@@ -338,8 +338,9 @@ __device__ __forceinline__ float lane63(float v) {
 constexpr float kBlendSigmaCap = 87.0f;
 
 // Packed record of one geometry item, 64 bytes (one aligned segment per staged intersection):
-//   r0 = (x, y, a/2, b), r1 = (c/2, o, sigma_max, 0), r2 = (red, green, blue, depth),
-//   r3 = (ex, ey, cull mode, 0).
+//   r0 = (x, y, a/2, b), r1 = (c/2, o, sigma_max, 1/a), r2 = (red, green, blue, depth),
+//   r3 = (ex, ey, cull mode, dy_r) (1/a and dy_r, the height of the 1.01-scaled ellipse's
+//   rightmost point, for the forward's tight sub-block test; 0 unless the cull mode is the box).
 // They depend only on the rasterizer's inputs, so a forward's records serve its backward.
 // sigma_max = log(255 o) + 1e-3 bounds sigma where o e^-sigma can still reach 1/255. The cull mode
 // says whether the tile-independent box (+-ex, +-ey) around the centre holds every pixel centre
@@ -366,7 +367,7 @@ __device__ __forceinline__ void pack_record(float x, float y, float a, float b, 
         smax = -__builtin_inff();  // o <= 0 or NaN: no pixel accepts it
     }
     uint32_t mode = kCullKeep;
-    float ex = 0.0f, ey = 0.0f;
+    float ex = 0.0f, ey = 0.0f, inv_a = 0.0f, dy_r = 0.0f;
     if (!(smax >= 0.0f)) {
         mode = kCullNone;  // every pixel rejected
     } else {
@@ -380,17 +381,23 @@ __device__ __forceinline__ void pack_record(float x, float y, float a, float b, 
         const float ex2 = 2.0f * smax * c / det, ey2 = 2.0f * smax * a / det;
         if (a > 0.0f && c > 0.0f && det > 0.0f && tr * tr < 1e4f * det && ex2 < 1e30f &&
             ey2 < 1e30f) {
-            ex = sqrtf(ex2) * 1.01f + 0.01f;
-            ey = sqrtf(ey2) * 1.01f + 0.01f;
+            // half-widths of the ellipse {sigma <= 1.0201 smax} (the 1.01-scaled one), and the box
+            const float sx = sqrtf(ex2) * 1.01f, sy = sqrtf(ey2) * 1.01f;
+            ex = sx + 0.01f;
+            ey = sy + 0.01f;
+            // for the forward's tight sub-block test: 1 / a and the height of the scaled
+            // ellipse's rightmost point relative to its centre
+            inv_a = 1.0f / a;
+            dy_r = -(b * sx) / c;
             mode = kCullBox;
         }
     }
     // the blends evaluate sigma = (a/2 dx dx + c/2 dy dy) + b dx dy: halving exactly before
     // the products leaves every rounding where 0.5 (a dx dx + c dy dy) puts it
     r[0] = make_float4(x, y, 0.5f * a, b);
-    r[1] = make_float4(0.5f * c, o, smax, 0.0f);
+    r[1] = make_float4(0.5f * c, o, smax, inv_a);
     r[2] = make_float4(color[0], color[1], color[2], depth);
-    r[3] = make_float4(ex, ey, __uint_as_float(mode), 0.0f);
+    r[3] = make_float4(ex, ey, __uint_as_float(mode), dy_r);
 }
 
 }  // namespace splat

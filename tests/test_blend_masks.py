@@ -4,9 +4,10 @@ blend_fwd_kernel walks, per 4x4 sub-block, only the records whose 16-bit mask ha
 sub-block's bit; a record is dropped from a sub-block only when no pixel centre there can pass the
 blend's `0 <= sigma <= sigma_max` test, so the blended sequence and the image stay the
 reference's. `subblock_mask_tight` (csrc/blend.hip) forms the mask from the exact x-extent of the
-ellipse Q <= 1.0201 sigma_max over each 4-row band; this test restates it step by step in float32
-(the hardware reciprocal and square root as correctly rounded ones: the function's margins are
-orders of magnitude above their error) and checks, against a brute force of the blend's own
+ellipse Q <= 1.0201 sigma_max over each 4-row band, from tile-independent parts the record pack
+forms (1 / a, the scaled ellipse's half-widths, its rightmost point's height); this test restates
+both step by step in float32 (the hardware square root as a correctly rounded one: the function's
+margins are orders of magnitude above its error) and checks, against a brute force of the blend's own
 sigma expression (two FMAs, float32) over all 256 pixel centres of each tile, that
 - no pixel centre with sigma in [0, sigma_max] lies in a sub-block the mask drops, on records
   from the benchmark scenes' projections and on synthetic extremes (thin ellipses up to the box
@@ -47,11 +48,15 @@ def pack(x, y, a, b, c, o):
         ey2 = (f32(2) * smax * a / det).astype(f32)
         box = (a > 0) & (c > 0) & (det > 0) & (tr * tr < f32(1e4) * det) & (ex2 < f32(1e30)) & \
             (ey2 < f32(1e30))
-        ex = np.where(box, np.sqrt(ex2) * f32(1.01) + f32(0.01), 0).astype(f32)
-        ey = np.where(box, np.sqrt(ey2) * f32(1.01) + f32(0.01), 0).astype(f32)
+        sx = (np.sqrt(ex2).astype(f32) * f32(1.01)).astype(f32)
+        sy = (np.sqrt(ey2).astype(f32) * f32(1.01)).astype(f32)
+        ex = np.where(box, sx + f32(0.01), 0).astype(f32)
+        ey = np.where(box, sy + f32(0.01), 0).astype(f32)
+        inv_a = np.where(box, f32(1) / a, 0).astype(f32)
+        dy_r = np.where(box, (-(b * sx).astype(f32) / c).astype(f32), 0).astype(f32)
     mode = np.where(~(smax >= 0), 2, np.where(box, 0, 1))
     return dict(x=x, y=y, ha=(f32(0.5) * a).astype(f32), b=b, hc=(f32(0.5) * c).astype(f32),
-                smax=smax, ex=ex, ey=ey, mode=mode)
+                smax=smax, ex=ex, ey=ey, inv_a=inv_a, dy_r=dy_r, mode=mode)
 
 
 def mask_tight(R, tx, ty, peaks=True, peak_sign=1):
@@ -65,11 +70,10 @@ def mask_tight(R, tx, ty, peaks=True, peak_sign=1):
         c = (f32(2) * R["hc"]).astype(f32)
         s2 = (f32(2) * (scale2 * R["smax"]).astype(f32)).astype(f32)
         det = (a * c - b * b).astype(f32)
-        inv_a = (f32(1) / a).astype(f32)
-        inv_det = (f32(1) / det).astype(f32)
-        ex = np.sqrt((s2 * c * inv_det).astype(f32)).astype(f32)
-        ey = np.sqrt((s2 * a * inv_det).astype(f32)).astype(f32)
-        dy_r = (f32(peak_sign) * (-(b * ex) * (f32(1) / c))).astype(f32)
+        inv_a = R["inv_a"]
+        ex = (R["ex"] - f32(0.01)).astype(f32)
+        ey = (R["ey"] - f32(0.01)).astype(f32)
+        dy_r = (f32(peak_sign) * R["dy_r"]).astype(f32)
         m = (f32(0.01) + f32(1e-3) * ex).astype(f32) if margin else np.zeros_like(ex)
         two_a_s = (a * s2).astype(f32)
         nb_a = (-b * inv_a).astype(f32)
