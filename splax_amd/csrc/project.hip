@@ -312,48 +312,93 @@ __global__ void __launch_bounds__(kProjFwdThreads) project_fwd_kernel(ProjectPar
 // contiguous run of chunks, the runs are scanned in LDS, then each thread writes its run's
 // prefixes.
 constexpr int kChunkScanThreads = 1024;
-__global__ void __launch_bounds__(kChunkScanThreads) chunk_scan_kernel(uint32_t* sums,
-                                                                       int64_t chunks) {
-    __shared__ uint32_t s_run[kChunkScanThreads];
-    const int tid = threadIdx.x;
-    const int64_t per = (chunks + kChunkScanThreads - 1) / kChunkScanThreads;
-    const int64_t lo = (int64_t)tid * per;
-    const int64_t hi = lo + per < chunks ? lo + per : chunks;
-    // runs of up to kChunkScanPer chunks (up to 64Ki chunks, 16.7M items) are loaded into
-    // registers at once, so their load latencies overlap; longer runs take a sequential loop
-    constexpr int kChunkScanPer = 64;
-    const bool in_regs = per <= kChunkScanPer;
-    uint32_t v[kChunkScanPer];
-    uint32_t total = 0;
-    if (in_regs) {
+// Two independent single-workgroup passes between the projection and the sort, in one launch:
+// (1) block 0 (when chunks > 1) turns the chunk totals into exclusive prefixes, which
+//     chunk_offset_kernel then adds to the chunks' items;
+// (2) with mm non-null, block b < images folds the fused projection's per-chunk depth-range
+//     partials of image b into the image's range of visible items (what minmax_partial_kernel /
+//     minmax_final_kernel give): chunk c holds items [1024 c, 1024 c + 1024), its slot 0 the
+//     image of its first item, slot 1 the next.
+__global__ void __launch_bounds__(kChunkScanThreads)
+chunk_scan_kernel(uint32_t* sums, int64_t chunks, const uint32_t* partial, int32_t n, float* mm,
+                  int64_t images) {
+    __shared__ uint32_t s_wave[kChunkScanThreads / 64];
+    __shared__ uint32_t s_lo[kChunkScanThreads / 64], s_hi[kChunkScanThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (blockIdx.x == 0 && chunks > 1) {
+        const int64_t per = (chunks + kChunkScanThreads - 1) / kChunkScanThreads;
+        const int64_t lo = (int64_t)tid * per;
+        const int64_t hi = lo + per < chunks ? lo + per : chunks;
+        // runs of up to kChunkScanPer chunks (up to 64Ki chunks, 67M items) are loaded into
+        // registers at once, so their load latencies overlap; longer runs take a sequential loop
+        constexpr int kChunkScanPer = 64;
+        const bool in_regs = per <= kChunkScanPer;
+        uint32_t v[kChunkScanPer];
+        uint32_t total = 0;
+        if (in_regs) {
 #pragma unroll
-        for (int k = 0; k < kChunkScanPer; ++k) v[k] = lo + k < hi ? sums[lo + k] : 0u;
+            for (int k = 0; k < kChunkScanPer; ++k) v[k] = lo + k < hi ? sums[lo + k] : 0u;
 #pragma unroll
-        for (int k = 0; k < kChunkScanPer; ++k) total += v[k];
-    } else {
-        for (int64_t c = lo; c < hi; ++c) total += sums[c];
-    }
-    s_run[tid] = total;
-    __syncthreads();
-    // Hillis-Steele inclusive scan of the run totals
-    for (int off = 1; off < kChunkScanThreads; off <<= 1) {
-        const uint32_t v = tid >= off ? s_run[tid - off] : 0u;
-        __syncthreads();
-        s_run[tid] += v;
-        __syncthreads();
-    }
-    uint32_t run = s_run[tid] - total;
-    if (in_regs) {
-#pragma unroll
-        for (int k = 0; k < kChunkScanPer; ++k) {
-            if (lo + k < hi) sums[lo + k] = run;
-            run += v[k];
+            for (int k = 0; k < kChunkScanPer; ++k) total += v[k];
+        } else {
+            for (int64_t c = lo; c < hi; ++c) total += sums[c];
         }
-    } else {
-        for (int64_t c = lo; c < hi; ++c) {
-            const uint32_t x = sums[c];
-            sums[c] = run;
-            run += x;
+        // exclusive prefix of the run totals: a wave scan, then the totals of the waves before
+        uint32_t incl = total;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += o;
+        }
+        if (lane == 63) s_wave[wave] = incl;
+        __syncthreads();
+        uint32_t run = incl - total;
+        for (int w = 0; w < wave; ++w) run += s_wave[w];
+        if (in_regs) {
+#pragma unroll
+            for (int k = 0; k < kChunkScanPer; ++k) {
+                if (lo + k < hi) sums[lo + k] = run;
+                run += v[k];
+            }
+        } else {
+            for (int64_t c = lo; c < hi; ++c) {
+                const uint32_t x = sums[c];
+                sums[c] = run;
+                run += x;
+            }
+        }
+    }
+    if (mm != nullptr && (int64_t)blockIdx.x < images) {
+        const int64_t image = blockIdx.x;
+        const int64_t c0 = image * n / kProjFwdThreads;
+        int64_t c1 = ((image + 1) * n - 1) / kProjFwdThreads;
+        c1 = c1 < chunks - 1 ? c1 : chunks - 1;
+        uint32_t lo = 0xffffffffu, hi = 0u;
+        for (int64_t c = c0 + tid; c <= c1; c += kChunkScanThreads) {
+            const int64_t slot = image - c * kProjFwdThreads / n;  // 0 or 1
+            const uint32_t x = partial[4 * c + 2 * slot], y = partial[4 * c + 2 * slot + 1];
+            lo = x < lo ? x : lo;
+            hi = y > hi ? y : hi;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const uint32_t x = __shfl_xor(lo, off, 64), y = __shfl_xor(hi, off, 64);
+            lo = x < lo ? x : lo;
+            hi = y > hi ? y : hi;
+        }
+        if (lane == 0) {
+            s_lo[wave] = lo;
+            s_hi[wave] = hi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < kChunkScanThreads / 64; ++w) {
+                lo = s_lo[w] < lo ? s_lo[w] : lo;
+                hi = s_hi[w] > hi ? s_hi[w] : hi;
+            }
+            // no visible item: the reference's +-1e30 seeds remain (drange < 0 -> depth_q = 0)
+            mm[2 * image] = hi == 0u ? 1.0e30f : ord2f(lo);
+            mm[2 * image + 1] = hi == 0u ? -1.0e30f : ord2f(hi);
         }
     }
 }
@@ -366,46 +411,6 @@ __global__ void __launch_bounds__(kProjFwdThreads) chunk_offset_kernel(int32_t* 
                                                            const uint32_t* offsets) {
     const int64_t idx = (int64_t)(blockIdx.x + 1) * kProjFwdThreads + threadIdx.x;
     if (idx < total) cum[idx] = (int32_t)((uint32_t)cum[idx] + offsets[blockIdx.x + 1]);
-}
-
-// Per-image depth range of the visible items from the fused projection's chunk partials, one
-// workgroup per image (the result minmax_partial_kernel / minmax_final_kernel give): chunk c
-// holds items [1024 c, 1024 c + 1024), its slot 0 the image of its first item, slot 1 the next.
-__global__ void __launch_bounds__(256)
-depth_range_kernel(const uint32_t* partial, int32_t n, int64_t chunks, float* mm) {
-    __shared__ uint32_t s_lo[4], s_hi[4];
-    const int64_t image = blockIdx.x;
-    const int64_t c0 = image * n / kProjFwdThreads;
-    int64_t c1 = ((image + 1) * n - 1) / kProjFwdThreads;
-    c1 = c1 < chunks - 1 ? c1 : chunks - 1;
-    uint32_t lo = 0xffffffffu, hi = 0u;
-    for (int64_t c = c0 + threadIdx.x; c <= c1; c += 256) {
-        const int64_t slot = image - c * kProjFwdThreads / n;  // 0 or 1
-        const uint32_t a = partial[4 * c + 2 * slot], b = partial[4 * c + 2 * slot + 1];
-        lo = a < lo ? a : lo;
-        hi = b > hi ? b : hi;
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t a = __shfl_xor(lo, off, 64), b = __shfl_xor(hi, off, 64);
-        lo = a < lo ? a : lo;
-        hi = b > hi ? b : hi;
-    }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) {
-        s_lo[wave] = lo;
-        s_hi[wave] = hi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w) {
-            lo = s_lo[w] < lo ? s_lo[w] : lo;
-            hi = s_hi[w] > hi ? s_hi[w] : hi;
-        }
-        // no visible item: the reference's +-1e30 seeds remain (drange < 0 -> depth_q = 0)
-        mm[2 * image] = hi == 0u ? 1.0e30f : ord2f(lo);
-        mm[2 * image + 1] = hi == 0u ? -1.0e30f : ord2f(hi);
-    }
 }
 
 // ------------------------------------------------------------------ projection backward
@@ -821,15 +826,15 @@ int launch_project_fwd_impl(const ProjectArgs& a, uint32_t* chunk_sums, const Fu
     else
         hipLaunchKernelGGL(project_fwd_kernel<false>, dim3((unsigned)blocks),
                            dim3(kProjFwdThreads), 0, stream, P);
-    if (blocks > 1) {
-        hipLaunchKernelGGL(chunk_scan_kernel, dim3(1), dim3(kChunkScanThreads), 0, stream,
-                           P.chunk_sums, blocks);
+    const int64_t images = (f && f->depth_mm) ? a.total / a.n : 0;
+    if (blocks > 1 || images > 0)
+        hipLaunchKernelGGL(chunk_scan_kernel, dim3((unsigned)(images > 1 ? images : 1)),
+                           dim3(kChunkScanThreads), 0, stream, P.chunk_sums, blocks,
+                           f ? f->mm_partial : nullptr, a.n, images > 0 ? f->depth_mm : nullptr,
+                           images);
+    if (blocks > 1)
         hipLaunchKernelGGL(chunk_offset_kernel, dim3((unsigned)(blocks - 1)), dim3(kProjFwdThreads),
                            0, stream, P.cum_tiles_hit, a.total, P.chunk_sums);
-    }
-    if (f && f->depth_mm)
-        hipLaunchKernelGGL(depth_range_kernel, dim3((unsigned)(a.total / a.n)), dim3(256), 0,
-                           stream, f->mm_partial, a.n, blocks, f->depth_mm);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
 }
 
