@@ -157,12 +157,15 @@ int splat_rasterize_depth_bwd(splat_stream_t stream, const float* colors, int64_
  * buffers sorted_ids [capacity], sorted_pos [capacity] and tile_bins [B*num_tiles, 2]; sorted_ids
  * and tile_bins receive exactly what splat_sort_and_bin returns, sorted_pos each sorted
  * intersection's emission position (its index in the cum_tiles_hit-ordered emission sequence).
- * num_intersects receives M. When M > capacity the call returns status 6 after the count
- * readback, with M reported and nothing written; the caller retries with larger buffers.
+ * num_intersects receives M. The host does not wait for M before launching the sort and the
+ * blend: they are sized by capacity and bounded on the device by the count, and M is read after
+ * the last launch. When M > capacity the call returns status 6 with M reported; sorted_ids,
+ * sorted_pos, tile_bins, records and the image outputs then hold the results of a list cut at
+ * capacity entries (every access inside the buffers), and the caller retries with larger ones.
  * out_depth (may be NULL) selects the depth channel as in splat_rasterize_depth_fwd. records
  * (may be NULL) receives the packed blend record of every geometry item, 16 floats per item
  * ([B*num_gaussians, 16], 16-byte aligned), for splat_rasterize_bwd_sorted; it is written only
- * when M > 0. tile_order (may be NULL) receives the order in which the blend dispatched the
+ * when capacity > 0. tile_order (may be NULL) receives the order in which the blend dispatched the
  * image tiles ([B*num_tiles] int32, a permutation of the tile indices, heaviest first within each
  * image) for splat_rasterize_bwd_sorted. compensate != 0 selects the antialiased blend of
  * splax.render (splax/_render.py:
@@ -245,7 +248,8 @@ int splat_set_wide_keys(int force);
  * num_gaussians or B * num_gaussians), background, the kept lists, records (required, [B *
  * num_gaussians, 16], 16-byte aligned) and the image outputs; opacities are the raw ones, which
  * both the projection and, with compensate, the antialiased blend use (splax/_render.py:
- * 105-110). Status 6 when M > capacity, after the count readback (projection outputs written). */
+ * 105-110). Status 6 when M > capacity, with M reported, as splat_rasterize_fwd_keep (the
+ * projection outputs are whole, the lists and image those of a list cut at capacity). */
 int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
                      const float* scales, int64_t rows_scales, const float* quats,
                      int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,

@@ -749,6 +749,8 @@ static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortT
 
 // The forward with the device's scratch held: sort_and_bin (into tgt's buffers when given), the
 // record pack (skipped when packed: the fused projection wrote them into records) and the blend.
+// With a capacity-bounded tgt the count is settled after the blend's launch (the host waits only
+// there, by when the stream is normally well past the count's copy).
 static int rasterize_fwd_core(hipStream_t s, DeviceScratch& sc, const RasterInputs& in,
                               const SortTargets* tgt, float* final_Ts, int32_t* final_idx,
                               float* out_img, float* out_depth, float* records, int32_t* order,
@@ -763,8 +765,11 @@ static int rasterize_fwd_core(hipStream_t s, DeviceScratch& sc, const RasterInpu
     KeyLayout L;
     SortOutputs o;
     rc = run_sort_and_bin(in, sc, s, &M, &L, tgt, &o);
-    if (num_intersects) *num_intersects = M;
+    if (num_intersects && M >= 0) *num_intersects = M;
     if (rc) return rc;
+    // with a deferred count M is its bound (the capacity) until settled
+    const bool deferred = o.count_deferred;
+    if (deferred) M = tgt->capacity;
     const int32_t* ids = o.ids;
     const int32_t* bins = o.bins;
     float4* recs = reinterpret_cast<float4*>(records);
@@ -784,6 +789,12 @@ static int rasterize_fwd_core(hipStream_t s, DeviceScratch& sc, const RasterInpu
         rc = launch_blend_fwd(in, L, M > 0 ? ids : nullptr, bins, final_Ts, final_idx, out_img,
                               out_depth, recs, order, s);
     if (rc) return fail(rc, "blend_fwd launch failed");
+    if (deferred) {
+        int64_t count = 0;
+        rc = settle_count(sc, tgt->capacity, &count);
+        if (num_intersects) *num_intersects = count;
+        return rc;
+    }
     return 0;
 }
 

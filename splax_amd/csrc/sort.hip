@@ -22,6 +22,16 @@
 
 namespace splat {
 
+// The intersection count a sort kernel works on: `bound` when the host knows the count (m_dev
+// null), else the count the projection left in device memory clamped to [0, bound], where bound
+// is the caller's list capacity (a count above it, or a wrapped negative one, is reported by the
+// host once the call's launches are queued; the kernels meanwhile stay inside the buffers).
+__device__ __forceinline__ int64_t live_count(const int32_t* m_dev, int64_t bound) {
+    if (!m_dev) return bound;
+    const int64_t m = *m_dev;
+    return m < 0 ? 0 : (m > bound ? bound : m);
+}
+
 // ------------------------------------------------------------------ depth range
 // _depth_minmax, splax/_rasterize/_sort/_kernels.py:38-73: per-image [dmin, dmax] over items with
 // radii > 0. Stage 1 writes one partial per workgroup; stage 2 (one workgroup per image) folds
@@ -119,6 +129,7 @@ struct EmitParams {
     const float* map_opac; int64_t rows_map_opac;
     const int32_t* cum; const float* mm;
     int32_t n; int64_t total; int64_t M;
+    const int32_t* m_dev;  // device-resident count (live_count), or null: M is the count
     int32_t tiles_x, tiles_y, tile_bits, depth_bits;
     void* keys; int32_t* owner;
 };
@@ -135,6 +146,7 @@ __global__ void __launch_bounds__(256) emit_keys_kernel(EmitParams P) {
     int64_t cur = idx > 0 ? P.cum[idx - 1] : 0;
     // a consistent (radii, conics, cum) never leaves [0, M); inconsistent inputs stop here
     if (cur < 0) return;
+    const int64_t M = live_count(P.m_dev, P.M);
     int32_t dq = 0, iid_enc = 0;
     uint64_t wide_base = 0;
     if constexpr (kWide) {
@@ -163,7 +175,7 @@ __global__ void __launch_bounds__(256) emit_keys_kernel(EmitParams P) {
         int32_t mn, mx;
         ellipse_column(e, u, I0, I1, mn, mx);
         for (int32_t v = mn; v < mx; ++v) {
-            if (cur >= P.M) return;
+            if (cur >= M) return;
             int32_t tile_id = e.isY ? u * P.tiles_x + v : v * P.tiles_x + u;
             if constexpr (kWide)
                 static_cast<uint64_t*>(P.keys)[cur] =
@@ -192,8 +204,10 @@ static_assert(kSortThreads * 4 == kSortTileMin, "smallest partition");
 // counts[d * parts + p]. The first pass also clears the tile bins (nbins2 > 0).
 template <typename K, int kItems>
 __global__ void __launch_bounds__(kSortThreads)
-rts_count_kernel(const K* __restrict__ keys, int64_t M, int shift, uint32_t* __restrict__ counts,
-                 int64_t parts, int32_t* __restrict__ bins, int64_t nbins2) {
+rts_count_kernel(const K* __restrict__ keys, int64_t M_bound, const int32_t* __restrict__ m_dev,
+                 int shift, uint32_t* __restrict__ counts, int64_t parts,
+                 int32_t* __restrict__ bins, int64_t nbins2) {
+    // partitions past the count (a grid sized by capacity) count nothing: zero columns
     __shared__ uint32_t s_h[kSortWaves][256];
     const int tid = threadIdx.x, wave = tid >> 6;
     for (int i = tid; i < kSortWaves * 256; i += kSortThreads) (&s_h[0][0])[i] = 0u;
@@ -202,6 +216,7 @@ rts_count_kernel(const K* __restrict__ keys, int64_t M, int shift, uint32_t* __r
          i += (int64_t)gridDim.x * kSortThreads)
         bins[i] = 0;
     __syncthreads();
+    const int64_t M = live_count(m_dev, M_bound);
     const int64_t base = (int64_t)blockIdx.x * (kItems * kSortThreads);
     K key[kItems];
 #pragma unroll
@@ -301,9 +316,10 @@ template <typename K, int kItems>
 __global__ void __launch_bounds__(kSortThreads, 8)
 rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
                    const int32_t* __restrict__ ids_in, K* __restrict__ keys_out,
-                   int32_t* __restrict__ vals_out, int32_t* __restrict__ ids_out, int64_t M,
-                   int shift, const uint32_t* __restrict__ offsets,
-                   const uint32_t* __restrict__ totals, int64_t parts) {
+                   int32_t* __restrict__ vals_out, int32_t* __restrict__ ids_out,
+                   int64_t M_bound, const int32_t* __restrict__ m_dev, int shift,
+                   const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals,
+                   int64_t parts) {
     constexpr int kTile = kItems * kSortThreads;
     // one staging buffer carries keys, then positions, then ids (three rounds), so two
     // 1024-thread workgroups fit a CU's LDS at eight keys per thread
@@ -315,10 +331,12 @@ rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ va
     __shared__ uint32_t s_tmp[4];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < kSortWaves * 256; i += kSortThreads) (&s_cnt[0][0])[i] = 0u;
-    __syncthreads();
+    const int64_t M = live_count(m_dev, M_bound);
     const int64_t part = blockIdx.x;
     const int64_t base = part * kTile;
+    if (base >= M) return;  // a partition past the count (uniform, before any barrier)
+    for (int i = tid; i < kSortWaves * 256; i += kSortThreads) (&s_cnt[0][0])[i] = 0u;
+    __syncthreads();
     const int64_t wbase = base + (int64_t)wave * (kItems * 64);
 
     // the keys first; positions and ids are loaded a round ahead of their own LDS round, so the
@@ -433,17 +451,18 @@ rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ va
 // One pass of the sort: count, scan, scatter with kItems keys per thread.
 template <typename K, int kItems>
 static void launch_pass(const K* keys_in, const int32_t* vals_in, const int32_t* ids_in,
-                        K* keys_out, int32_t* vals_out, int32_t* ids_out, int64_t M, int shift,
-                        uint32_t* counts, uint32_t* totals, int32_t* bins, int64_t nbins2,
-                        hipStream_t stream) {
+                        K* keys_out, int32_t* vals_out, int32_t* ids_out, int64_t M,
+                        const int32_t* m_dev, int shift, uint32_t* counts, uint32_t* totals,
+                        int32_t* bins, int64_t nbins2, hipStream_t stream) {
+    // M bounds the count (live_count): the grid covers M keys
     const int64_t parts = (M + (int64_t)kItems * kSortThreads - 1) / ((int64_t)kItems * kSortThreads);
     hipLaunchKernelGGL((rts_count_kernel<K, kItems>), dim3((unsigned)parts), dim3(kSortThreads),
-                       0, stream, keys_in, M, shift, counts, parts, bins, nbins2);
+                       0, stream, keys_in, M, m_dev, shift, counts, parts, bins, nbins2);
     hipLaunchKernelGGL(rts_scan_kernel, dim3(256), dim3(kScanThreads), 0, stream, counts, parts,
                        totals);
     hipLaunchKernelGGL((rts_scatter_kernel<K, kItems>), dim3((unsigned)parts),
                        dim3(kSortThreads), 0, stream, keys_in, vals_in, ids_in, keys_out,
-                       vals_out, ids_out, M, shift, counts, totals, parts);
+                       vals_out, ids_out, M, m_dev, shift, counts, totals, parts);
 }
 
 // ------------------------------------------------------------------ bin edges
@@ -470,8 +489,9 @@ constexpr int kBinKeys = 4;  // keys per thread of bin_edges_kernel
 
 template <bool kWide>
 __global__ void __launch_bounds__(256)
-bin_edges_kernel(const void* keys, int64_t M, int32_t num_tiles, int32_t tile_bits,
-                 int32_t depth_bits, int64_t nbins, int32_t* bins) {
+bin_edges_kernel(const void* keys, int64_t M_bound, const int32_t* m_dev, int32_t num_tiles,
+                 int32_t tile_bits, int32_t depth_bits, int64_t nbins, int32_t* bins) {
+    const int64_t M = live_count(m_dev, M_bound);
     // kBinKeys consecutive keys and the one before them per thread, all loads issued together
     const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * kBinKeys;
     if (i0 >= M) return;
@@ -568,7 +588,11 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     }
     // The one device-to-host read: the intersection count (skipped when the caller supplies it).
     // The copy is enqueued first; the depth range launches run while the host waits
-    // (splax/_rasterize/_sort/_sort.py:71-96).
+    // (splax/_rasterize/_sort/_sort.py:71-96). With a capacity-bounded target the host does not
+    // wait here at all: every launch below is sized by the capacity and bounded on the device by
+    // the count itself (live_count), and the caller settles the count after its last launch
+    // (settle_count), so the host never stalls the stream between the projection and the blend.
+    const bool deferred = !known && tgt && tgt->capacity >= 0;
     if (!known && (hipMemcpyAsync(sc.pinned_count, in.cum + (total - 1), sizeof(int32_t),
                                   hipMemcpyDeviceToHost, stream) != hipSuccess ||
                    hipEventRecord(sc.count_event, stream) != hipSuccess))
@@ -588,20 +612,33 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
                            sc.mm_partial, bpi, sc.depth_mm);
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "minmax launch failed");
     }
+    // M: the count, or with a deferred count its bound (the capacity); m_dev then points at the
+    // count in device memory and m_est (the previous settled count, for the partition shape
+    // only) stands in for it on the host
     int64_t M;
+    const int32_t* m_dev = nullptr;
     if (known) {
         M = tgt->M_known;
+    } else if (deferred) {
+        M = tgt->capacity;
+        m_dev = in.cum + (total - 1);
     } else {
         if (hipEventSynchronize(sc.count_event) != hipSuccess)
             return fail(kErrRuntime, "count readback failed");
         M = *sc.pinned_count;
     }
-    if (M < 0) return fail(kErrTooMany, "intersection count overflowed int32");
-    if (M >= ((int64_t)1 << 31)) return fail(kErrTooMany, "more than 2^31 - 1 intersections");
-    *M_out = M;
-    if (tgt && tgt->capacity >= 0 && M > tgt->capacity)
-        return fail(kErrTooMany, "sorted-list buffers hold " + std::to_string(tgt->capacity) +
-                                     " intersections, " + std::to_string(M) + " needed");
+    if (!deferred) {
+        if (M < 0) return fail(kErrTooMany, "intersection count overflowed int32");
+        if (M >= ((int64_t)1 << 31)) return fail(kErrTooMany, "more than 2^31 - 1 intersections");
+        if (tgt && tgt->capacity >= 0 && M > tgt->capacity)
+            return fail(kErrTooMany, "sorted-list buffers hold " + std::to_string(tgt->capacity) +
+                                         " intersections, " + std::to_string(M) + " needed");
+    }
+    *M_out = deferred ? -1 : M;
+    o.count_deferred = deferred;
+    if (out) *out = o;
+    const int64_t m_est =
+        deferred && sc.last_count >= 0 && sc.last_count < M ? sc.last_count : M;
     rc = sc.ensure_sort(M, nbins, B, wide);
     if (rc) return rc;
     if (M == 0) return fill_zero_i32(bins, 2 * nbins, stream);
@@ -619,7 +656,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         EmitParams E;
         E.xys = in.xys; E.depths = in.depths; E.radii = in.radii; E.conics = in.conics;
         E.map_opac = in.map_opac; E.rows_map_opac = in.rows_map_opac;
-        E.cum = in.cum; E.mm = depth_mm; E.n = in.n; E.total = total; E.M = M;
+        E.cum = in.cum; E.mm = depth_mm; E.n = in.n; E.total = total; E.M = M; E.m_dev = m_dev;
         E.tiles_x = L.tiles_x; E.tiles_y = L.tiles_y; E.tile_bits = L.tile_bits;
         E.depth_bits = L.depth_bits; E.keys = kbuf[0]; E.owner = sc.gids[0];
         const dim3 grid((unsigned)((total + 255) / 256));
@@ -634,7 +671,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         // 64-bit keys: 8192-key partitions from 1M keys on (digit runs of about 32 keys leave as
         // whole 128-byte lines), 4096-key partitions below, so small sorts still spread over the
         // CUs
-        const bool big = M >= kSortBigM;
+        const bool big = m_est >= kSortBigM;
         // packed keys: one partition per workgroup and two 1024-thread workgroups per CU. The
         // smallest of 4..8 keys per thread whose partitions all fit in one round of workgroups,
         // else 8: a second round that only a few partitions occupy costs nearly a whole round
@@ -642,7 +679,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         const int64_t slots = 2 * (int64_t)(sc.compute_units > 0 ? sc.compute_units : 256);
         int items = 8;
         for (int k = 4; k < 8; ++k) {
-            if ((M + (int64_t)k * kSortThreads - 1) / ((int64_t)k * kSortThreads) <= slots) {
+            if ((m_est + (int64_t)k * kSortThreads - 1) / ((int64_t)k * kSortThreads) <= slots) {
                 items = k;
                 break;
             }
@@ -662,33 +699,33 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
                 const uint64_t* ki = sc.wkeys[src];
                 uint64_t* ko = sc.wkeys[dst];
                 if (big)
-                    launch_pass<uint64_t, 8>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                    launch_pass<uint64_t, 8>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
                                              sc.part_counts, sc.hist, bins, nb2, stream);
                 else
-                    launch_pass<uint64_t, 4>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                    launch_pass<uint64_t, 4>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
                                              sc.part_counts, sc.hist, bins, nb2, stream);
             } else {
                 const uint32_t* ki = reinterpret_cast<const uint32_t*>(sc.keys[src]);
                 uint32_t* ko = reinterpret_cast<uint32_t*>(sc.keys[dst]);
                 switch (items) {
                 case 4:
-                    launch_pass<uint32_t, 4>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                    launch_pass<uint32_t, 4>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
                                              sc.part_counts, sc.hist, bins, nb2, stream);
                     break;
                 case 5:
-                    launch_pass<uint32_t, 5>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                    launch_pass<uint32_t, 5>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
                                              sc.part_counts, sc.hist, bins, nb2, stream);
                     break;
                 case 6:
-                    launch_pass<uint32_t, 6>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                    launch_pass<uint32_t, 6>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
                                              sc.part_counts, sc.hist, bins, nb2, stream);
                     break;
                 case 7:
-                    launch_pass<uint32_t, 7>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                    launch_pass<uint32_t, 7>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
                                              sc.part_counts, sc.hist, bins, nb2, stream);
                     break;
                 default:
-                    launch_pass<uint32_t, 8>(ki, vin, sc.gids[src], ko, vout, iout, M, shift,
+                    launch_pass<uint32_t, 8>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
                                              sc.part_counts, sc.hist, bins, nb2, stream);
                 }
             }
@@ -700,12 +737,25 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         const dim3 grid((unsigned)((M + 256 * kBinKeys - 1) / (256 * kBinKeys)));
         if (wide)
             hipLaunchKernelGGL(bin_edges_kernel<true>, grid, dim3(256), 0, stream, o.keys, M,
-                               L.num_tiles, L.tile_bits, L.depth_bits, nbins, bins);
+                               m_dev, L.num_tiles, L.tile_bits, L.depth_bits, nbins, bins);
         else
             hipLaunchKernelGGL(bin_edges_kernel<false>, grid, dim3(256), 0, stream, o.keys, M,
-                               L.num_tiles, L.tile_bits, L.depth_bits, nbins, bins);
+                               m_dev, L.num_tiles, L.tile_bits, L.depth_bits, nbins, bins);
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "bins launch failed");
     }
+    return 0;
+}
+
+int settle_count(DeviceScratch& sc, int64_t capacity, int64_t* M_out) {
+    if (hipEventSynchronize(sc.count_event) != hipSuccess)
+        return fail(kErrRuntime, "count readback failed");
+    const int64_t M = *sc.pinned_count;
+    *M_out = M;
+    if (M < 0) return fail(kErrTooMany, "intersection count overflowed int32");
+    sc.last_count = M;
+    if (M > capacity)
+        return fail(kErrTooMany, "sorted-list buffers hold " + std::to_string(capacity) +
+                                     " intersections, " + std::to_string(M) + " needed");
     return 0;
 }
 

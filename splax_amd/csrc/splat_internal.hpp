@@ -135,6 +135,7 @@ struct DeviceScratch {
     uint32_t* mm_partial = nullptr; int64_t mm_partial_cap = 0;     // 2 * blocks
     int32_t* pinned_count = nullptr;
     hipEvent_t count_event = nullptr;
+    int64_t last_count = -1;  // the last settled deferred count: the sort's partition shape
     // Calls on one device share these buffers: a call on another stream than the last user's
     // first waits on the host for the device's work, so calls from different streams run one
     // after the other.
@@ -234,8 +235,10 @@ int launch_project_bwd(const ProjectBwdArgs& a, DeviceScratch& sc, hipStream_t s
 // Optional caller-owned destinations of sort_and_bin: M_known >= 0 skips the count readback
 // (it must equal cum[B*n - 1]); ids / pos / bins (when non-null) receive the sorted gaussian ids,
 // the sorted emission positions and the tile bins instead of the library scratch. With
-// capacity >= 0, an M above it stops the call with kErrTooMany (M is still reported) before
-// anything is written to ids / pos / bins.
+// capacity >= 0 (and no M_known) the count is not waited for: the launches are sized by the
+// capacity and bounded on the device by the count, and the caller calls settle_count after its
+// last launch, which reports a count above the capacity as kErrTooMany (the outputs of that call
+// are then those of a truncated list, every access still inside the buffers).
 struct SortTargets {
     int64_t M_known = -1;
     int64_t capacity = -1;
@@ -253,12 +256,17 @@ struct SortOutputs {
     const int32_t* ids = nullptr;
     const int32_t* pos = nullptr;
     const int32_t* bins = nullptr;
+    bool count_deferred = false;  // the count is still to be settled (settle_count)
 };
 
-// sort_and_bin: returns M (>= 0) in *M_out and the result locations in *out.
+// sort_and_bin: returns M (>= 0) in *M_out, or -1 with a deferred count, and the result
+// locations in *out.
 int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stream,
                      int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt,
                      SortOutputs* out);
+// Waits for the deferred count's readback (enqueued after the projection, so normally long
+// complete), reports it in *M_out and fails with kErrTooMany above the capacity.
+int settle_count(DeviceScratch& sc, int64_t capacity, int64_t* M_out);
 
 // Writes the packed blend record (4 float4) of each of the in.B_geom * in.n geometry items.
 int launch_pack_records(const RasterInputs& in, float4* recs, hipStream_t stream);

@@ -193,3 +193,59 @@ def test_fused_forward_buffers_equal_two_call_buffers():
         assert M == k2.M and M > 0
         assert_bit_exact(_np(kept.sort.ids)[:M], _np(k2.ids)[:M], f"aa={aa} ids")
         assert_bit_exact(_np(kept.sort.pos)[:M], _np(k2.pos)[:M], f"aa={aa} pos")
+
+
+def test_deferred_count_at_every_capacity():
+    """The kept forwards (splat_render_fwd, splat_rasterize_fwd_keep) launch the sort and the
+    blend before the intersection count reaches the host: the launches are sized by the list
+    capacity and bounded on the device by the count, which the host settles after its last
+    launch. Capacities below the count (0, half, one short) must report ERR_TOO_MANY with the
+    count, after a truncated run that stays inside the buffers (the wrapper then retries with a
+    larger capacity); capacities at or above it must give the same lists and image bit for bit."""
+    _case("deferred count")
+    s = make_scene(2, n=40_000)
+    n = s.n
+    q = _t(s.quats)
+    args = (_t(s.means), _t(s.scales), q, _t(s.colors), _t(s.opacities).reshape(-1),
+            _t(s.viewmats[0]), _t(s.background))
+    tf = torch.zeros((1, 4, 4), device="cuda")
+    tids = torch.full((1,), -1, device="cuda", dtype=torch.int32)
+    key = str(args[0].device)
+
+    def fused():
+        img, Ts, fidx, kept, _ = _ops.render_fwd(
+            *args, tf, tids, n=n, B=1, num_transforms=1, has_transforms=False,
+            img_shape=s.img_shape, f=s.f, c=s.c, glob_scale=1.0, clip_thresh=0.01)
+        return img, Ts, fidx, kept.sort, kept.cum
+
+    def keep():
+        xys, depths, radii, conics, _, cum = _ops.project_fwd(
+            args[0], args[1], q, args[5], args[4], tf, tids, n=n, total=n, num_transforms=1,
+            has_transforms=False, img_shape=s.img_shape, f=s.f, c=s.c, glob_scale=1.0,
+            clip_thresh=0.01, quats_wxyz=True)
+        img, Ts, fidx, ks, _ = _ops.rasterize_fwd_keep(
+            args[3], args[4], args[4], args[6], xys, depths, radii, conics, cum, n=n, B=1,
+            img_shape=s.img_shape)
+        return img, Ts, fidx, ks, cum
+
+    for label, call in (("render_fwd", fused), ("rasterize_fwd_keep", keep)):
+        _ops._KEEP_CAPACITY[key] = 0
+        ref = call()
+        torch.cuda.synchronize()
+        M = ref[3].M
+        assert M > 1000 and M == int(ref[4][-1].item())
+        assert _ops._KEEP_CAPACITY[key] == int(M * 1.25) + 1  # the first attempt fell short
+        for cap in (0, M // 2, M - 1, M, M + 1, 3 * M):
+            _case(f"deferred count {label} capacity {cap} (M = {M})")
+            _ops._KEEP_CAPACITY[key] = cap
+            got = call()
+            torch.cuda.synchronize()
+            # below the count the first attempt reports it and the wrapper retries larger
+            assert _ops._KEEP_CAPACITY[key] == (cap if cap >= M else int(M * 1.25) + 1), cap
+            assert got[3].M == M
+            for name, a, b in (("img", got[0], ref[0]), ("Ts", got[1], ref[1]),
+                               ("fidx", got[2], ref[2]), ("bins", got[3].bins, ref[3].bins)):
+                assert_bit_exact(_np(a), _np(b), f"{label} cap={cap} {name}")
+            assert_bit_exact(_np(got[3].ids)[:M], _np(ref[3].ids)[:M], f"{label} cap={cap} ids")
+            assert_bit_exact(_np(got[3].pos)[:M], _np(ref[3].pos)[:M], f"{label} cap={cap} pos")
+    _ops._KEEP_CAPACITY.pop(key, None)
