@@ -13,7 +13,8 @@ The JSON line carries:
   a separate untimed pass with every stage bracketed gives stage_ms_per_step and picks the
   dominant stage).
   Blend work is the reference loop's pair count from the CPU oracle (26 Pc + 16 Pr FLOPs
-  forward, 65 Qc + 16 Qr backward); sort+bin bytes are 12G + 32V + 76M + 16T.
+  forward, 65 Qc + 16 Qr backward); depth range, emission, sort and bin bytes are
+  12G + 32V + 104M + 16T.
 - stages: every stage's average duration per call (HIP events around each stage, in an untimed
   pass) with its algorithmic bytes or FLOPs per call and the achieved rate against MI355X's peak
   (HBM 8 TB/s for projection, depth range, emission, sort, bins and the projection backward;
@@ -125,8 +126,11 @@ def stage_work(counts, N, T):
         "project": ("hbm", 56 * N + 104 * G, "GB/s"),
         "minmax": ("hbm", 8 * G, "GB/s"),
         "emit": ("hbm", 4 * G + 32 * V + 8 * M, "GB/s"),
-        "sort": ("hbm", 64 * M, "GB/s"),
-        "bins": ("hbm", 4 * M + 16 * T, "GB/s"),
+        # four passes: counts read 4 + 4 + 2 + 2 B, scatters move 20 + 22 + 20 + 20 B per key
+        # (key, emission position, id; the pass over bits 8-15 writes the keys' 16-bit high
+        # halves, which the last two passes and the bin edges read)
+        "sort": ("hbm", 94 * M, "GB/s"),
+        "bins": ("hbm", 2 * M + 16 * T, "GB/s"),
         "blend_fwd": ("valu", fwd_flops, "TFLOP/s"),
         "blend_fwd_kernel": ("valu", fwd_flops, "TFLOP/s"),
         "blend_bwd": ("valu", bwd_flops, "TFLOP/s"),

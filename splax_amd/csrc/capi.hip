@@ -680,7 +680,7 @@ int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* dep
     int64_t M = 0;
     KeyLayout L;
     SortOutputs o;
-    rc = run_sort_and_bin(in, sc, s, &M, &L, nullptr, &o);
+    rc = run_sort_and_bin(in, sc, s, &M, &L, nullptr, &o, true);
     if (num_intersects) *num_intersects = M;
     if (rc) return rc;
     if (M > capacity) return fail(kErrTooMany, "sort_and_bin: capacity below intersection count");

@@ -310,21 +310,28 @@ rts_scan_kernel(uint32_t* __restrict__ counts, int64_t parts, uint32_t* __restri
 // to (keys with a smaller digit) + offsets[d][p] + (j - first slot of d). The first pass
 // generates the emission positions (vals_in == nullptr gives value = position) and reads the
 // items in emission order, so no pass gathers at random. K is the key word (uint32_t for the
-// packed key, uint64_t for the 64-bit key, ordered as unsigned).
-template <typename K, int kItems>
+// packed key, uint64_t for the 64-bit key, ordered as unsigned). KO is the key word written:
+// K, or uint16_t from uint32_t keys, the key's high half (the pass that sorts bits 8-15 of a
+// packed key leaves only bits 16-30 to sort and to bin, and a packed key's depth field is at
+// least 16 bits wide, so the image and tile fields sit in that half).
+template <typename K, int kItems, typename KO = K>
 // at most 64 VGPRs (eight waves per SIMD), so two 1024-thread workgroups share a CU
 __global__ void __launch_bounds__(kSortThreads, 8)
 rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
-                   const int32_t* __restrict__ ids_in, K* __restrict__ keys_out,
+                   const int32_t* __restrict__ ids_in, KO* __restrict__ keys_out,
                    int32_t* __restrict__ vals_out, int32_t* __restrict__ ids_out,
                    int64_t M_bound, const int32_t* __restrict__ m_dev, int shift,
                    const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals,
                    int64_t parts) {
     constexpr int kTile = kItems * kSortThreads;
+    static_assert(sizeof(KO) == sizeof(K) || (sizeof(K) == 4 && sizeof(KO) == 2),
+                  "narrowing writes a 32-bit key's high half");
     // one staging buffer carries keys, then positions, then ids (three rounds), so two
     // 1024-thread workgroups fit a CU's LDS at eight keys per thread
-    __shared__ K s_keys[kTile];
-    uint32_t* const s_u32 = reinterpret_cast<uint32_t*>(s_keys);
+    constexpr int kStageWords = kTile * (sizeof(K) > 4 ? (int)(sizeof(K) / 4) : 1);
+    __shared__ __attribute__((aligned(16))) uint32_t s_stage[kStageWords];
+    K* const s_keys = reinterpret_cast<K*>(s_stage);
+    uint32_t* const s_u32 = s_stage;
     __shared__ uint32_t s_cnt[kSortWaves][256];
     __shared__ uint32_t s_local_start[256];
     __shared__ int32_t s_dest_base[256];
@@ -347,7 +354,7 @@ rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ va
     const int64_t rem = M - my0;
     K key[kItems];
 #pragma unroll
-    for (int i = 0; i < kItems; ++i) key[i] = i * 64 < rem ? keys_in[my0 + i * 64] : ~(K)0;
+    for (int i = 0; i < kItems; ++i) key[i] = i * 64 < rem ? keys_in[my0 + i * 64] : (K)~(K)0;
     const uint32_t total_d = tid < 256 ? totals[tid] : 0u;
     const uint32_t offset_d = tid < 256 ? offsets[(int64_t)tid * parts + part] : 0u;
 
@@ -418,7 +425,10 @@ rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ va
             const K k = s_keys[j];
             const uint32_t d = (uint32_t)(k >> shift) & 255u;
             dig[r >> 2] |= d << (8 * (r & 3));
-            keys_out[s_dest_base[d] + j] = k;
+            if constexpr (sizeof(KO) < sizeof(K))
+                keys_out[s_dest_base[d] + j] = (KO)(k >> 16);
+            else
+                keys_out[s_dest_base[d] + j] = k;
         }
     }
     __syncthreads();
@@ -449,9 +459,9 @@ rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ va
 }
 
 // One pass of the sort: count, scan, scatter with kItems keys per thread.
-template <typename K, int kItems>
+template <typename K, int kItems, typename KO = K>
 static void launch_pass(const K* keys_in, const int32_t* vals_in, const int32_t* ids_in,
-                        K* keys_out, int32_t* vals_out, int32_t* ids_out, int64_t M,
+                        KO* keys_out, int32_t* vals_out, int32_t* ids_out, int64_t M,
                         const int32_t* m_dev, int shift, uint32_t* counts, uint32_t* totals,
                         int32_t* bins, int64_t nbins2, hipStream_t stream) {
     // M bounds the count (live_count): the grid covers M keys
@@ -460,34 +470,61 @@ static void launch_pass(const K* keys_in, const int32_t* vals_in, const int32_t*
                        0, stream, keys_in, M, m_dev, shift, counts, parts, bins, nbins2);
     hipLaunchKernelGGL(rts_scan_kernel, dim3(256), dim3(kScanThreads), 0, stream, counts, parts,
                        totals);
-    hipLaunchKernelGGL((rts_scatter_kernel<K, kItems>), dim3((unsigned)parts),
+    hipLaunchKernelGGL((rts_scatter_kernel<K, kItems, KO>), dim3((unsigned)parts),
                        dim3(kSortThreads), 0, stream, keys_in, vals_in, ids_in, keys_out,
                        vals_out, ids_out, M, m_dev, shift, counts, totals, parts);
+}
+
+// A pass over packed keys of one of three forms: 32-bit keys in and out (kind 0), 32-bit in and
+// their high halves out (kind 1), 16-bit high halves in and out (kind 2; shift counts from bit
+// 16).
+template <int kItems>
+static void packed_pass(int kind, const void* ki, const int32_t* vin, const int32_t* gin,
+                        void* ko, int32_t* vout, int32_t* iout, int64_t M, const int32_t* m_dev,
+                        int shift, uint32_t* counts, uint32_t* totals, int32_t* bins,
+                        int64_t nb2, hipStream_t stream) {
+    if (kind == 0)
+        launch_pass<uint32_t, kItems>(static_cast<const uint32_t*>(ki), vin, gin,
+                                      static_cast<uint32_t*>(ko), vout, iout, M, m_dev, shift,
+                                      counts, totals, bins, nb2, stream);
+    else if (kind == 1)
+        launch_pass<uint32_t, kItems, uint16_t>(static_cast<const uint32_t*>(ki), vin, gin,
+                                                static_cast<uint16_t*>(ko), vout, iout, M, m_dev,
+                                                shift, counts, totals, bins, nb2, stream);
+    else
+        launch_pass<uint16_t, kItems>(static_cast<const uint16_t*>(ki), vin, gin,
+                                      static_cast<uint16_t*>(ko), vout, iout, M, m_dev,
+                                      shift - 16, counts, totals, bins, nb2, stream);
 }
 
 // ------------------------------------------------------------------ bin edges
 // _tile_bin_edges_32bit, splax/_rasterize/_sort/_kernels.py:214-241 (including its M == 1
 // behaviour: index 0 writes only the start, so a lone bin stays [0, 0)).
 
-// kWide: _tile_bin_edges_64bit (splax/_rasterize/_sort/_kernels.py:244-269), the (image, tile)
-// field read from the high word.
-template <bool kWide>
+// kKind 2: _tile_bin_edges_64bit (splax/_rasterize/_sort/_kernels.py:244-269), the (image,
+// tile) field read from the high word; 0: the packed 32-bit key; 1: the packed key's high half
+// (bits 16-31: its image and tile fields, depth_bits >= 16).
+constexpr int kKeysPacked = 0, kKeysPackedHigh = 1, kKeysWide = 2;
+template <int kKind>
 __device__ __forceinline__ int32_t key_bin(const void* keys, int64_t i, int32_t num_tiles,
                                            int32_t tile_bits, int32_t depth_bits) {
-    if constexpr (kWide) {
+    if constexpr (kKind == kKeysWide) {
         const uint64_t k = static_cast<const uint64_t*>(keys)[i] >> 32;
         const uint64_t mask = ((uint64_t)1 << tile_bits) - 1;
         return (int32_t)(k >> tile_bits) * num_tiles + (int32_t)(k & mask);
     } else {
         const int32_t mask = (1 << tile_bits) - 1;
-        const int32_t k = static_cast<const int32_t*>(keys)[i] >> depth_bits;
+        const int32_t k =
+            kKind == kKeysPacked
+                ? static_cast<const int32_t*>(keys)[i] >> depth_bits
+                : (int32_t)static_cast<const uint16_t*>(keys)[i] >> (depth_bits - 16);
         return (k >> tile_bits) * num_tiles + (k & mask);
     }
 }
 
 constexpr int kBinKeys = 4;  // keys per thread of bin_edges_kernel
 
-template <bool kWide>
+template <int kKind>
 __global__ void __launch_bounds__(256)
 bin_edges_kernel(const void* keys, int64_t M_bound, const int32_t* m_dev, int32_t num_tiles,
                  int32_t tile_bits, int32_t depth_bits, int64_t nbins, int32_t* bins) {
@@ -498,9 +535,9 @@ bin_edges_kernel(const void* keys, int64_t M_bound, const int32_t* m_dev, int32_
     int32_t cur[kBinKeys];
 #pragma unroll
     for (int k = 0; k < kBinKeys; ++k)
-        cur[k] = i0 + k < M ? key_bin<kWide>(keys, i0 + k, num_tiles, tile_bits, depth_bits) : -1;
+        cur[k] = i0 + k < M ? key_bin<kKind>(keys, i0 + k, num_tiles, tile_bits, depth_bits) : -1;
     const int32_t before =
-        i0 > 0 ? key_bin<kWide>(keys, i0 - 1, num_tiles, tile_bits, depth_bits) : -1;
+        i0 > 0 ? key_bin<kKind>(keys, i0 - 1, num_tiles, tile_bits, depth_bits) : -1;
 #pragma unroll
     for (int k = 0; k < kBinKeys; ++k) {
         const int64_t idx = i0 + k;
@@ -550,7 +587,7 @@ KeyLayout key_layout(int32_t B, int32_t img_h, int32_t img_w) {
 
 int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stream,
                      int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt,
-                     SortOutputs* out) {
+                     SortOutputs* out, bool full_keys) {
     const int32_t B = in.B_geom;
     const KeyLayout L = key_layout(B, in.img_h, in.img_w);
     *lay_out = L;
@@ -572,6 +609,8 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     if (wide)
         for (int b = 0; b < (L.image_bits + L.tile_bits + 7) / 8; ++b) ps.shift[ps.n++] = 32 + 8 * b;
     const int last_dst = ((ps.n - 1) & 1) ? 0 : 1;  // buffer the last pass writes
+    // packed keys whose sorted form nobody reads end as their 16-bit high halves
+    const bool narrow = !wide && !full_keys;
     const int64_t total = (int64_t)B * in.n;
     const int64_t nbins = (int64_t)B * L.num_tiles;
     int rc = sc.ensure_sort(0, nbins, B, wide);
@@ -580,6 +619,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     SortOutputs o;
     o.bins = bins;
     o.wide = wide;
+    o.high_keys = narrow;
     if (out) *out = o;
     const bool known = tgt && tgt->M_known >= 0;
     if (total <= 0) {
@@ -705,28 +745,33 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
                     launch_pass<uint64_t, 4>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
                                              sc.part_counts, sc.hist, bins, nb2, stream);
             } else {
-                const uint32_t* ki = reinterpret_cast<const uint32_t*>(sc.keys[src]);
-                uint32_t* ko = reinterpret_cast<uint32_t*>(sc.keys[dst]);
+                // narrow: the pass over bits 8-15 writes the keys' high halves and the passes
+                // over bits 16-30 move 16-bit keys (the buffers hold either)
+                const int kind = !narrow || pass == 0 ? 0 : pass == 1 ? 1 : 2;
+                const void* ki = sc.keys[src];
+                void* ko = sc.keys[dst];
+                const int32_t* gi = sc.gids[src];
+                uint32_t* pc = sc.part_counts;
                 switch (items) {
                 case 4:
-                    launch_pass<uint32_t, 4>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
-                                             sc.part_counts, sc.hist, bins, nb2, stream);
+                    packed_pass<4>(kind, ki, vin, gi, ko, vout, iout, M, m_dev, shift, pc,
+                                   sc.hist, bins, nb2, stream);
                     break;
                 case 5:
-                    launch_pass<uint32_t, 5>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
-                                             sc.part_counts, sc.hist, bins, nb2, stream);
+                    packed_pass<5>(kind, ki, vin, gi, ko, vout, iout, M, m_dev, shift, pc,
+                                   sc.hist, bins, nb2, stream);
                     break;
                 case 6:
-                    launch_pass<uint32_t, 6>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
-                                             sc.part_counts, sc.hist, bins, nb2, stream);
+                    packed_pass<6>(kind, ki, vin, gi, ko, vout, iout, M, m_dev, shift, pc,
+                                   sc.hist, bins, nb2, stream);
                     break;
                 case 7:
-                    launch_pass<uint32_t, 7>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
-                                             sc.part_counts, sc.hist, bins, nb2, stream);
+                    packed_pass<7>(kind, ki, vin, gi, ko, vout, iout, M, m_dev, shift, pc,
+                                   sc.hist, bins, nb2, stream);
                     break;
                 default:
-                    launch_pass<uint32_t, 8>(ki, vin, sc.gids[src], ko, vout, iout, M, m_dev, shift,
-                                             sc.part_counts, sc.hist, bins, nb2, stream);
+                    packed_pass<8>(kind, ki, vin, gi, ko, vout, iout, M, m_dev, shift, pc,
+                                   sc.hist, bins, nb2, stream);
                 }
             }
         }
@@ -736,11 +781,16 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         StageTimer tm(stream, kStageBins);
         const dim3 grid((unsigned)((M + 256 * kBinKeys - 1) / (256 * kBinKeys)));
         if (wide)
-            hipLaunchKernelGGL(bin_edges_kernel<true>, grid, dim3(256), 0, stream, o.keys, M,
-                               m_dev, L.num_tiles, L.tile_bits, L.depth_bits, nbins, bins);
+            hipLaunchKernelGGL(bin_edges_kernel<kKeysWide>, grid, dim3(256), 0, stream, o.keys,
+                               M, m_dev, L.num_tiles, L.tile_bits, L.depth_bits, nbins, bins);
+        else if (narrow)
+            hipLaunchKernelGGL(bin_edges_kernel<kKeysPackedHigh>, grid, dim3(256), 0, stream,
+                               o.keys, M, m_dev, L.num_tiles, L.tile_bits, L.depth_bits, nbins,
+                               bins);
         else
-            hipLaunchKernelGGL(bin_edges_kernel<false>, grid, dim3(256), 0, stream, o.keys, M,
-                               m_dev, L.num_tiles, L.tile_bits, L.depth_bits, nbins, bins);
+            hipLaunchKernelGGL(bin_edges_kernel<kKeysPacked>, grid, dim3(256), 0, stream,
+                               o.keys, M, m_dev, L.num_tiles, L.tile_bits, L.depth_bits, nbins,
+                               bins);
         if (hipGetLastError() != hipSuccess) return fail(kErrLaunch, "bins launch failed");
     }
     return 0;

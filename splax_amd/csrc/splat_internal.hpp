@@ -257,13 +257,15 @@ struct SortOutputs {
     const int32_t* pos = nullptr;
     const int32_t* bins = nullptr;
     bool count_deferred = false;  // the count is still to be settled (settle_count)
+    bool high_keys = false;  // packed keys kept as their 16-bit high halves (image, tile)
 };
 
 // sort_and_bin: returns M (>= 0) in *M_out, or -1 with a deferred count, and the result
-// locations in *out.
+// locations in *out. full_keys keeps the whole sorted keys (splat_sort_and_bin returns them);
+// otherwise packed keys leave the sort as their 16-bit high halves.
 int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stream,
                      int64_t* M_out, KeyLayout* lay_out, const SortTargets* tgt,
-                     SortOutputs* out);
+                     SortOutputs* out, bool full_keys = false);
 // Waits for the deferred count's readback (enqueued after the projection, so normally long
 // complete), reports it in *M_out and fails with kErrTooMany above the capacity.
 int settle_count(DeviceScratch& sc, int64_t capacity, int64_t* M_out);
