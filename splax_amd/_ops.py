@@ -205,10 +205,11 @@ class RenderKept(NamedTuple):
 
 def render_fwd(means, scales, quats_wxyz, colors, opac, viewmat, background, transforms,
                transform_ids, *, n, B, num_transforms, has_transforms, img_shape, f, c,
-               glob_scale, clip_thresh, compensate=False, render_depth=False):
+               glob_scale, clip_thresh, compensate=False, render_depth=False, backward=True):
     """The fused render forward (splat_render_fwd): projection, sort and blend in one call over
     B images of n gaussians; quaternions wxyz. Returns (img, Ts, fidx, RenderKept, depth or None).
-    Kept-list capacity as rasterize_fwd_keep."""
+    Kept-list capacity as rasterize_fwd_keep. backward=False (no render_bwd will follow) sorts no
+    emission positions: the kept lists then carry pos None."""
     means, scales, quats_wxyz, colors, opac, viewmat, background, transforms = map(
         _f32, (means, scales, quats_wxyz, colors, opac, viewmat, background, transforms))
     transform_ids = _i32(transform_ids)
@@ -228,7 +229,7 @@ def render_fwd(means, scales, quats_wxyz, colors, opac, viewmat, background, tra
     p = _lib.ptr
     for _ in range(2):
         ids = e(max(cap, 1), dt=torch.int32)
-        pos = e(max(cap, 1), dt=torch.int32)
+        pos = e(max(cap, 1), dt=torch.int32) if backward else None
         with torch.cuda.device(dev):
             st = _lib.lib().splat_render_fwd(
                 _lib.stream_handle(dev), p(means), rows(means, 3), p(scales), rows(scales, 3),

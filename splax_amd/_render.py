@@ -59,6 +59,20 @@ class _LogParamsFn(torch.autograd.Function):
         return tuple(outs)
 
 
+def _fused_forward(means, scales, quats, colors, opac, viewmat, background, transforms, tf_ids,
+                   statics, backward):
+    """splat_render_fwd over the flat operands; backward=False when no render_bwd will read the
+    kept lists (the sort then carries no emission positions)."""
+    n, B, K, has_tf, img_shape, f, c, glob_scale, clip_thresh, compensate, render_depth = statics
+    flat = lambda t, w: t.reshape(-1, w) if w > 1 else t.reshape(-1)  # noqa: E731
+    return _ops.render_fwd(
+        flat(means, 3), flat(scales, 3), flat(quats, 4), flat(colors, 3), flat(opac, 1),
+        viewmat.reshape(-1, 4), flat(background, 3), transforms.reshape(-1, 4, 4),
+        tf_ids.reshape(-1), n=n, B=B, num_transforms=K, has_transforms=has_tf,
+        img_shape=img_shape, f=f, c=c, glob_scale=glob_scale, clip_thresh=clip_thresh,
+        compensate=compensate, render_depth=render_depth, backward=backward)
+
+
 class _RenderFn(torch.autograd.Function):
     """project then rasterize (splax/_render.py:94-115) with their custom VJPs
     (splax/_project/_project.py:142-275, splax/_rasterize/_rasterize.py:105-234) as one library
@@ -70,15 +84,9 @@ class _RenderFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means, scales, quats, colors, opac, viewmat, background, transforms, tf_ids,
                 statics):
-        n, B, K, has_tf, img_shape, f, c, glob_scale, clip_thresh, compensate, render_depth = \
-            statics
-        flat = lambda t, w: t.reshape(-1, w) if w > 1 else t.reshape(-1)  # noqa: E731
-        img, Ts, fidx, kept, depth = _ops.render_fwd(
-            flat(means, 3), flat(scales, 3), flat(quats, 4), flat(colors, 3), flat(opac, 1),
-            viewmat.reshape(-1, 4), flat(background, 3), transforms.reshape(-1, 4, 4),
-            tf_ids.reshape(-1), n=n, B=B, num_transforms=K, has_transforms=has_tf,
-            img_shape=img_shape, f=f, c=c, glob_scale=glob_scale, clip_thresh=clip_thresh,
-            compensate=compensate, render_depth=render_depth)
+        img, Ts, fidx, kept, depth = _fused_forward(means, scales, quats, colors, opac, viewmat,
+                                                    background, transforms, tf_ids, statics,
+                                                    backward=True)
         ks = kept.sort
         ctx.save_for_backward(means, scales, quats, colors, opac, viewmat, background,
                               transforms, tf_ids, Ts, fidx, kept.xys, kept.depths, kept.radii,
@@ -184,7 +192,11 @@ def render(means3d: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor,
     # compensation and its gradient inside the record packing and the gradient gather.
     statics = (n, B, K, has_tf, (int(H), int(W)), tuple(map(float, f)), tuple(map(float, c)),
                float(glob_scale), float(clip_thresh), bool(antialiased), bool(render_depth))
-    img, depth = _RenderFn.apply(*ops[:7], ops[7], tf_ids.to(torch.int32), statics)
+    tf_ids = tf_ids.to(torch.int32)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in ops):
+        img, depth = _RenderFn.apply(*ops[:7], ops[7], tf_ids, statics)
+    else:  # no backward can follow: the forward alone, keeping no emission positions
+        img, _, _, _, depth = _fused_forward(*ops, tf_ids, statics, backward=False)
     img = img.reshape(*S, H, W, 3)
     return img, (depth.reshape(*S, H, W) if render_depth else None)
 

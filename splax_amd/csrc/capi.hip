@@ -1059,7 +1059,8 @@ int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_m
                               clip_thresh, xys, depths, radii, conics, num_tiles_hit,
                               cum_tiles_hit, quats_wxyz, &a);
     if (rc) return rc;
-    if (capacity < 0 || !tile_bins || !records || (capacity > 0 && (!sorted_ids || !sorted_pos)))
+    // sorted_pos may be null: a forward with no backward sorts no emission positions
+    if (capacity < 0 || !tile_bins || !records || (capacity > 0 && !sorted_ids))
         return fail(kErrArgs, "render_fwd: missing sorted-list or record buffers");
     if ((uintptr_t)records & 15)
         return fail(kErrArgs, "render_fwd: records must be 16-byte aligned");

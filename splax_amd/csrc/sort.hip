@@ -309,7 +309,8 @@ rts_scan_kernel(uint32_t* __restrict__ counts, int64_t parts, uint32_t* __restri
 // (3) Stable scatter of one partition. A key of digit d at partition-local sorted slot j goes
 // to (keys with a smaller digit) + offsets[d][p] + (j - first slot of d). The first pass
 // generates the emission positions (vals_in == nullptr gives value = position) and reads the
-// items in emission order, so no pass gathers at random. K is the key word (uint32_t for the
+// items in emission order, so no pass gathers at random; vals_out == nullptr moves no positions
+// (a forward whose lists no backward reads). K is the key word (uint32_t for the
 // packed key, uint64_t for the 64-bit key, ordered as unsigned). KO is the key word written:
 // K, or uint16_t from uint32_t keys, the key's high half (the pass that sorts bits 8-15 of a
 // packed key leaves only bits 16-30 to sort and to bin, and a packed key's depth field is at
@@ -403,12 +404,13 @@ rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ va
         const uint32_t dd = (uint32_t)(key[i] >> shift) & 255u;
         slot[i] = s_local_start[dd] + s_cnt[wave][dd] + rank[i];
     }
+    const bool with_pos = vals_out != nullptr;  // uniform
     uint32_t val[kItems];
 #pragma unroll
     for (int i = 0; i < kItems; ++i)
-        val[i] = i * 64 < rem ? (vals_in ? (uint32_t)vals_in[my0 + i * 64]
-                                          : (uint32_t)(my0 + i * 64))
-                              : 0u;
+        val[i] = with_pos && i * 64 < rem ? (vals_in ? (uint32_t)vals_in[my0 + i * 64]
+                                                     : (uint32_t)(my0 + i * 64))
+                                          : 0u;
     // round 1, keys. Each digit's run is contiguous in the output, so consecutive j write
     // consecutive addresses; the destinations are kept for the other two rounds.
 #pragma unroll
@@ -433,19 +435,24 @@ rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ va
     }
     __syncthreads();
     // round 2, emission positions
-#pragma unroll
-    for (int i = 0; i < kItems; ++i) s_u32[slot[i]] = val[i];
     uint32_t gid[kItems];
+    if (with_pos) {
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) s_u32[slot[i]] = val[i];
+    }
 #pragma unroll
     for (int i = 0; i < kItems; ++i) gid[i] = i * 64 < rem ? (uint32_t)ids_in[my0 + i * 64] : 0u;
-    __syncthreads();
+    if (with_pos) {
+        __syncthreads();
 #pragma unroll
-    for (int r = 0; r < kItems; ++r) {
-        const int j = r * kSortThreads + tid;
-        if (j < valid)
-            vals_out[s_dest_base[(dig[r >> 2] >> (8 * (r & 3))) & 255u] + j] = (int32_t)s_u32[j];
+        for (int r = 0; r < kItems; ++r) {
+            const int j = r * kSortThreads + tid;
+            if (j < valid)
+                vals_out[s_dest_base[(dig[r >> 2] >> (8 * (r & 3))) & 255u] + j] =
+                    (int32_t)s_u32[j];
+        }
+        __syncthreads();
     }
-    __syncthreads();
     // round 3, item ids
 #pragma unroll
     for (int i = 0; i < kItems; ++i) s_u32[slot[i]] = gid[i];
@@ -611,6 +618,9 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     const int last_dst = ((ps.n - 1) & 1) ? 0 : 1;  // buffer the last pass writes
     // packed keys whose sorted form nobody reads end as their 16-bit high halves
     const bool narrow = !wide && !full_keys;
+    // a kept forward given no position buffer (no backward will read its lists) sorts no
+    // emission positions
+    const bool with_pos = !(tgt && tgt->ids && !tgt->pos);
     const int64_t total = (int64_t)B * in.n;
     const int64_t nbins = (int64_t)B * L.num_tiles;
     int rc = sc.ensure_sort(0, nbins, B, wide);
@@ -688,7 +698,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
                      wide ? (void*)sc.wkeys[1] : (void*)sc.keys[1]};
     o.keys = kbuf[last_dst];
     o.ids = ids_final;
-    o.pos = pos_final;
+    o.pos = with_pos ? pos_final : nullptr;
     if (out) *out = o;
 
     {
@@ -730,8 +740,8 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         for (int pass = 0; pass < ps.n; ++pass) {
             const int src = pass & 1, dst = 1 - src;
             const bool last = pass == ps.n - 1;
-            const int32_t* vin = pass == 0 ? nullptr : sc.vals[src];
-            int32_t* vout = last ? pos_final : sc.vals[dst];
+            const int32_t* vin = pass == 0 || !with_pos ? nullptr : sc.vals[src];
+            int32_t* vout = !with_pos ? nullptr : last ? pos_final : sc.vals[dst];
             int32_t* iout = last ? ids_final : sc.gids[dst];
             const int shift = ps.shift[pass];
             const int64_t nb2 = pass == 0 ? 2 * nbins : 0;

@@ -249,3 +249,48 @@ def test_deferred_count_at_every_capacity():
             assert_bit_exact(_np(got[3].ids)[:M], _np(ref[3].ids)[:M], f"{label} cap={cap} ids")
             assert_bit_exact(_np(got[3].pos)[:M], _np(ref[3].pos)[:M], f"{label} cap={cap} pos")
     _ops._KEEP_CAPACITY.pop(key, None)
+
+
+@pytest.mark.parametrize("name", ["cfg2_60k", "cfg3_20k_B4", "aa_depth"])
+def test_forward_only_render_equals_autograd_forward(name):
+    """Under no_grad (or with no operand requiring grad) splax_amd.render runs splat_render_fwd
+    with no position buffer, so the sort moves no emission positions: image, depth, sorted ids
+    and bins must equal those of the forward that keeps everything for a backward, bit for
+    bit."""
+    _case(f"forward-only render {name}")
+    cfg = CASES[name]
+    s = cfg["scene"]()
+    B = cfg["B"]
+    aa, rd = cfg.get("antialiased", False), cfg.get("depth", False)
+    cam = dict(img_shape=s.img_shape, f=s.f, c=s.c)
+    vms = s.viewmats[:B] if s.B >= B else np.stack([s.viewmats[0]] * B)
+    vm_np = vms if B > 1 else vms[0]
+    outs = []
+    for grad in (True, False):
+        p = [_t(v, grad=grad) for v in (s.means, s.scales, s.quats, s.colors, s.opacities)]
+        with torch.set_grad_enabled(grad):
+            img, depth = splax_amd.render(*p, viewmat=_t(vm_np), background=_t(s.background),
+                                          antialiased=aa, render_depth=rd, **cam)
+        assert img.requires_grad == grad
+        torch.cuda.synchronize()
+        outs.append((_np(img), None if depth is None else _np(depth)))
+    assert_bit_exact(outs[1][0], outs[0][0], f"{name}/img")
+    if rd:
+        assert_bit_exact(outs[1][1], outs[0][1], f"{name}/depth")
+    # the library lists themselves, with and without positions
+    q = _t(s.quats)
+    args = (_t(s.means), _t(s.scales), q, _t(s.colors), _t(s.opacities).reshape(-1),
+            _t(vm_np).reshape(-1, 4), _t(s.background))
+    tf = torch.zeros((1, 4, 4), device="cuda")
+    tids = torch.full((1,), -1, device="cuda", dtype=torch.int32)
+    kept = []
+    for backward in (True, False):
+        r = _ops.render_fwd(*args, tf, tids, n=s.n, B=B, num_transforms=1, has_transforms=False,
+                            img_shape=s.img_shape, f=s.f, c=s.c, glob_scale=1.0,
+                            clip_thresh=0.01, compensate=aa, render_depth=rd, backward=backward)
+        torch.cuda.synchronize()
+        kept.append(r[3].sort)
+    assert kept[1].pos is None and kept[0].M == kept[1].M > 0
+    M = kept[0].M
+    assert_bit_exact(_np(kept[1].ids)[:M], _np(kept[0].ids)[:M], f"{name}/ids")
+    assert_bit_exact(_np(kept[1].bins), _np(kept[0].bins), f"{name}/bins")
