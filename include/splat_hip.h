@@ -250,8 +250,9 @@ int splat_set_wide_keys(int force);
  * both the projection and, with compensate, the antialiased blend use (splax/_render.py:
  * 105-110). Status 6 when M > capacity, with M reported, as splat_rasterize_fwd_keep (the
  * projection outputs are whole, the lists and image those of a list cut at capacity).
- * sorted_pos may be NULL when no backward will follow (a forward-only render): the sort then
- * moves no emission positions, and the kept lists cannot feed splat_render_bwd. */
+ * sorted_pos, final_Ts and final_idx may be NULL when no backward will follow (a forward-only
+ * render): the sort then moves no emission positions and the blend writes only the image (and
+ * depth), and the kept lists cannot feed splat_render_bwd. */
 int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
                      const float* scales, int64_t rows_scales, const float* quats,
                      int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,

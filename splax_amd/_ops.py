@@ -209,7 +209,8 @@ def render_fwd(means, scales, quats_wxyz, colors, opac, viewmat, background, tra
     """The fused render forward (splat_render_fwd): projection, sort and blend in one call over
     B images of n gaussians; quaternions wxyz. Returns (img, Ts, fidx, RenderKept, depth or None).
     Kept-list capacity as rasterize_fwd_keep. backward=False (no render_bwd will follow) sorts no
-    emission positions: the kept lists then carry pos None."""
+    emission positions and writes no final_Ts / final_idx: Ts, fidx and the kept lists' pos are
+    then None."""
     means, scales, quats_wxyz, colors, opac, viewmat, background, transforms = map(
         _f32, (means, scales, quats_wxyz, colors, opac, viewmat, background, transforms))
     transform_ids = _i32(transform_ids)
@@ -220,7 +221,8 @@ def render_fwd(means, scales, quats_wxyz, colors, opac, viewmat, background, tra
     e = lambda *shape, dt=torch.float32: torch.empty(shape, device=dev, dtype=dt)  # noqa: E731
     xys, depths, conics = e(total, 2), e(total), e(total, 3)
     radii, nth, cum = e(total, dt=torch.int32), e(total, dt=torch.int32), e(total, dt=torch.int32)
-    Ts, fidx, img = e(B * H, W), e(B * H, W, dt=torch.int32), e(B * H, W, 3)
+    img = e(B * H, W, 3)
+    Ts, fidx = (e(B * H, W), e(B * H, W, dt=torch.int32)) if backward else (None, None)
     depth = e(B * H, W) if render_depth else None
     bins, recs, order = e(B * tiles, 2, dt=torch.int32), e(total, 16), e(B * tiles, dt=torch.int32)
     key = str(dev)

@@ -406,8 +406,9 @@ __global__ void __launch_bounds__(kTile, 7) blend_fwd_kernel(BlendFwdParams P) {
         const int64_t bgi = C.rows_bg > 1 ? image_id : 0;
         const float* bg = C.background + 3 * bgi;
         const int64_t pix = ((int64_t)image_id * C.img_h + i) * C.img_w + j;
-        P.final_Ts[pix] = T;
-        P.final_idx[pix] = cur_idx;
+        // final_Ts / final_idx serve the backward only: a forward-only caller may pass neither
+        if (P.final_Ts) P.final_Ts[pix] = T;
+        if (P.final_idx) P.final_idx[pix] = cur_idx;
         P.out_img[3 * pix] = o0 + T * bg[0];
         P.out_img[3 * pix + 1] = o1 + T * bg[1];
         P.out_img[3 * pix + 2] = o2 + T * bg[2];
