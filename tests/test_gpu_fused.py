@@ -294,3 +294,54 @@ def test_forward_only_render_equals_autograd_forward(name):
     M = kept[0].M
     assert_bit_exact(_np(kept[1].ids)[:M], _np(kept[0].ids)[:M], f"{name}/ids")
     assert_bit_exact(_np(kept[1].bins), _np(kept[0].bins), f"{name}/bins")
+
+
+@pytest.fixture
+def _forced_wide_keys():
+    from oracle import oracle as O
+
+    _lib.set_wide_keys(True)
+    O.set_wide_keys(True)
+    yield O
+    _lib.set_wide_keys(False)
+    O.set_wide_keys(False)
+
+
+@pytest.mark.parametrize("backward", [True, False])
+def test_fused_forward_with_wide_keys_matches_oracle(_forced_wide_keys, backward):
+    """The fused forward (deferred count, capacity-sized grids) on the 64-bit key path, forced as
+    the reference's tests force it, with and without the positions a backward needs: sorted ids,
+    bins and the image bit-exact against the oracle (its sort_and_bin and rasterize_fwd on the
+    projection's outputs)."""
+    O = _forced_wide_keys
+    _case(f"fused forward wide keys backward={backward}")
+    s = make_scene(2, n=40_000)
+    q = _t(s.quats)
+    args = (_t(s.means), _t(s.scales), q, _t(s.colors), _t(s.opacities).reshape(-1),
+            _t(s.viewmats[0]), _t(s.background))
+    tf = torch.zeros((1, 4, 4), device="cuda")
+    tids = torch.full((1,), -1, device="cuda", dtype=torch.int32)
+    img, Ts, fidx, kept, _ = _ops.render_fwd(
+        *args, tf, tids, n=s.n, B=1, num_transforms=1, has_transforms=False,
+        img_shape=s.img_shape, f=s.f, c=s.c, glob_scale=1.0, clip_thresh=0.01,
+        backward=backward)
+    torch.cuda.synchronize()
+    xys, depths, radii, conics, cum = (_np(t) for t in (kept.xys, kept.depths, kept.radii,
+                                                         kept.conics, kept.cum))
+    rk, rid, rbins = O.sort_and_bin(xys, depths, radii, conics, s.opacities, cum, n=s.n, B=1,
+                                    img_shape=s.img_shape)
+    assert rk.dtype == np.int64  # the 64-bit key
+    M = kept.sort.M
+    assert M == len(rid) > 0
+    assert_bit_exact(_np(kept.sort.ids)[:M], rid, "wide fused ids")
+    assert_bit_exact(_np(kept.sort.bins), rbins, "wide fused bins")
+    rimg, rT, ridx, _, rM = O.rasterize_fwd(s.colors, s.opacities, s.opacities, s.background,
+                                            xys, depths, radii, conics, cum, n=s.n, B=1,
+                                            img_shape=s.img_shape)
+    assert rM == M
+    assert_bit_exact(_np(img).reshape(rimg.shape), rimg, "wide fused img")
+    if backward:
+        assert_bit_exact(_np(fidx).reshape(ridx.shape), ridx, "wide fused final_idx")
+        assert kept.sort.pos is not None
+    else:
+        assert Ts is None and fidx is None and kept.sort.pos is None
