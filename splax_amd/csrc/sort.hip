@@ -16,7 +16,11 @@
 //
 // Each key carries two values: the reference's value (the flat item id) and the key's emission
 // position. The positions let the backward blend store each intersection's gradient in emission
-// order, where every item's intersections are contiguous.
+// order, where every item's intersections are contiguous; a forward that no backward follows
+// sorts without them. Packed keys leave the pass over bits 8-15 as their 16-bit high halves
+// (image and tile fields), which the last two passes and the bin edges move, unless the caller
+// returns the sorted keys. A capacity-bounded caller need not know the count: the kernels then
+// read it from device memory (live_count) and the grids cover the capacity.
 #include "splat_common.hpp"
 #include "splat_internal.hpp"
 
