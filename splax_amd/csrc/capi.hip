@@ -1094,6 +1094,9 @@ int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_m
     f.recs = reinterpret_cast<float4*>(records);
     f.mm_partial = fuse_range ? sc.mm_partial : nullptr;
     f.depth_mm = fuse_range ? sc.depth_mm : nullptr;
+    // several chunks: the chunk scan writes the count and the emission finalizes cum_tiles_hit
+    int32_t* count_word = reinterpret_cast<int32_t*>(sc.tickets + kCountWord);
+    f.count_word = chunks > 1 ? count_word : nullptr;
     g_last_error.clear();
     {
         StageTimer tm(s, kStageProject);
@@ -1106,6 +1109,11 @@ int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_m
     tgt.pos = sorted_pos;
     tgt.bins = tile_bins;
     tgt.depth_mm = fuse_range ? sc.depth_mm : nullptr;
+    if (chunks > 1) {
+        tgt.chunk_prefix = sc.chunk_sums;
+        tgt.num_tiles_hit = num_tiles_hit;
+        tgt.count_src = count_word;
+    }
     return rasterize_fwd_core(s, sc, in, &tgt, final_Ts, final_idx, out_img, out_depth, records,
                               tile_order, num_intersects, true);
 }

@@ -215,6 +215,7 @@ __device__ __forceinline__ ItemOut project_item(const ProjectParams& P, int64_t 
 // One item per thread keeps the loads coalesced and gives the latency-bound projection the most
 // waves in flight.
 constexpr int kProjItems = 1;
+static_assert(kProjFwdThreads * kProjItems == kProjChunkItems, "one chunk per projection workgroup");
 
 // kFused (the fused render forward): also the item's packed blend record and the chunk's depth
 // range partials (the chunk spans at most two images: num_gaussians >= 1024).
@@ -314,14 +315,15 @@ __global__ void __launch_bounds__(kProjFwdThreads) project_fwd_kernel(ProjectPar
 constexpr int kChunkScanThreads = 1024;
 // Two independent single-workgroup passes between the projection and the sort, in one launch:
 // (1) block 0 (when chunks > 1) turns the chunk totals into exclusive prefixes, which
-//     chunk_offset_kernel then adds to the chunks' items;
+//     chunk_offset_kernel (or, on the render path, the emission) then adds to the chunks' items,
+//     and with total_out non-null writes the grand total (the intersection count) there;
 // (2) with mm non-null, block b < images folds the fused projection's per-chunk depth-range
 //     partials of image b into the image's range of visible items (what minmax_partial_kernel /
 //     minmax_final_kernel give): chunk c holds items [1024 c, 1024 c + 1024), its slot 0 the
 //     image of its first item, slot 1 the next.
 __global__ void __launch_bounds__(kChunkScanThreads)
 chunk_scan_kernel(uint32_t* sums, int64_t chunks, const uint32_t* partial, int32_t n, float* mm,
-                  int64_t images) {
+                  int64_t images, int32_t* total_out) {
     __shared__ uint32_t s_wave[kChunkScanThreads / 64];
     __shared__ uint32_t s_lo[kChunkScanThreads / 64], s_hi[kChunkScanThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -367,6 +369,9 @@ chunk_scan_kernel(uint32_t* sums, int64_t chunks, const uint32_t* partial, int32
                 run += x;
             }
         }
+        // the last thread's run ends at the grand total (runs past the chunks are empty); int32
+        // wrap-around on overflow is kept, as in cum_tiles_hit
+        if (total_out && tid == kChunkScanThreads - 1) *total_out = (int32_t)run;
     }
     if (mm != nullptr && (int64_t)blockIdx.x < images) {
         const int64_t image = blockIdx.x;
@@ -820,6 +825,8 @@ int launch_project_fwd_impl(const ProjectArgs& a, uint32_t* chunk_sums, const Fu
     P.compensate = f ? f->compensate : 0;
     P.recs = f ? f->recs : nullptr;
     P.mm_partial = f ? f->mm_partial : nullptr;
+    // the render path leaves the chunk offsets to the emission when there are several chunks
+    const bool offsets_later = f && f->count_word && blocks > 1;
     if (f)
         hipLaunchKernelGGL(project_fwd_kernel<true>, dim3((unsigned)blocks),
                            dim3(kProjFwdThreads), 0, stream, P);
@@ -831,10 +838,18 @@ int launch_project_fwd_impl(const ProjectArgs& a, uint32_t* chunk_sums, const Fu
         hipLaunchKernelGGL(chunk_scan_kernel, dim3((unsigned)(images > 1 ? images : 1)),
                            dim3(kChunkScanThreads), 0, stream, P.chunk_sums, blocks,
                            f ? f->mm_partial : nullptr, a.n, images > 0 ? f->depth_mm : nullptr,
-                           images);
+                           images, offsets_later ? f->count_word : nullptr);
+    if (blocks > 1 && !offsets_later)
+        return launch_chunk_offsets(P.cum_tiles_hit, a.total, P.chunk_sums, stream);
+    return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
+}
+
+int launch_chunk_offsets(int32_t* cum, int64_t total, const uint32_t* chunk_prefix,
+                         hipStream_t stream) {
+    const int64_t blocks = project_fwd_chunks(total);
     if (blocks > 1)
         hipLaunchKernelGGL(chunk_offset_kernel, dim3((unsigned)(blocks - 1)), dim3(kProjFwdThreads),
-                           0, stream, P.cum_tiles_hit, a.total, P.chunk_sums);
+                           0, stream, cum, total, chunk_prefix);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
 }
 

@@ -134,6 +134,9 @@ struct EmitParams {
     const int32_t* cum; const float* mm;
     int32_t n; int64_t total; int64_t M;
     const int32_t* m_dev;  // device-resident count (live_count), or null: M is the count
+    // the render path: cum is chunk-local, finalized here (cum_fix, the same array) from each
+    // chunk's exclusive prefix; nth holds the items' own counts
+    const uint32_t* chunk_prefix; const int32_t* nth; int32_t* cum_fix;
     int32_t tiles_x, tiles_y, tile_bits, depth_bits;
     void* keys; int32_t* owner;
 };
@@ -145,9 +148,19 @@ template <bool kWide>
 __global__ void __launch_bounds__(256) emit_keys_kernel(EmitParams P) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= P.total) return;
+    int64_t cur;
+    if (P.chunk_prefix) {
+        // every item's final inclusive prefix (an output of the call), and the start of its
+        // keys as that prefix less its own count: each thread reads and writes its own entry
+        // only. Unsigned adds keep cum_tiles_hit's int32 wrap-around.
+        const uint32_t fin = (uint32_t)P.cum_fix[idx] + P.chunk_prefix[idx / kProjChunkItems];
+        P.cum_fix[idx] = (int32_t)fin;
+        cur = (int32_t)(fin - (uint32_t)P.nth[idx]);
+    } else {
+        cur = idx > 0 ? P.cum[idx - 1] : 0;
+    }
     if (P.radii[idx] <= 0) return;
     const int32_t bid = (int32_t)(idx / P.n);
-    int64_t cur = idx > 0 ? P.cum[idx - 1] : 0;
     // a consistent (radii, conics, cum) never leaves [0, M); inconsistent inputs stop here
     if (cur < 0) return;
     const int64_t M = live_count(P.m_dev, P.M);
@@ -647,7 +660,8 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     // the count itself (live_count), and the caller settles the count after its last launch
     // (settle_count), so the host never stalls the stream between the projection and the blend.
     const bool deferred = !known && tgt && tgt->capacity >= 0;
-    if (!known && (hipMemcpyAsync(sc.pinned_count, in.cum + (total - 1), sizeof(int32_t),
+    const int32_t* count_src = tgt && tgt->count_src ? tgt->count_src : in.cum + (total - 1);
+    if (!known && (hipMemcpyAsync(sc.pinned_count, count_src, sizeof(int32_t),
                                   hipMemcpyDeviceToHost, stream) != hipSuccess ||
                    hipEventRecord(sc.count_event, stream) != hipSuccess))
         return fail(kErrRuntime, "count readback enqueue failed");
@@ -675,7 +689,7 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         M = tgt->M_known;
     } else if (deferred) {
         M = tgt->capacity;
-        m_dev = in.cum + (total - 1);
+        m_dev = count_src;
     } else {
         if (hipEventSynchronize(sc.count_event) != hipSuccess)
             return fail(kErrRuntime, "count readback failed");
@@ -695,7 +709,15 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         deferred && sc.last_count >= 0 && sc.last_count < M ? sc.last_count : M;
     rc = sc.ensure_sort(M, nbins, B, wide);
     if (rc) return rc;
-    if (M == 0) return fill_zero_i32(bins, 2 * nbins, stream);
+    const uint32_t* chunk_prefix = tgt ? tgt->chunk_prefix : nullptr;
+    if (M == 0) {
+        // no emission: the chunk-local cum_tiles_hit is finalized here
+        if (chunk_prefix) {
+            rc = launch_chunk_offsets(const_cast<int32_t*>(in.cum), total, chunk_prefix, stream);
+            if (rc) return fail(rc, "chunk offset launch failed");
+        }
+        return fill_zero_i32(bins, 2 * nbins, stream);
+    }
     int32_t* ids_final = (tgt && tgt->ids) ? tgt->ids : sc.gids[last_dst];
     int32_t* pos_final = (tgt && tgt->pos) ? tgt->pos : sc.vals[last_dst];
     void* kbuf[2] = {wide ? (void*)sc.wkeys[0] : (void*)sc.keys[0],
@@ -711,6 +733,9 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         E.xys = in.xys; E.depths = in.depths; E.radii = in.radii; E.conics = in.conics;
         E.map_opac = in.map_opac; E.rows_map_opac = in.rows_map_opac;
         E.cum = in.cum; E.mm = depth_mm; E.n = in.n; E.total = total; E.M = M; E.m_dev = m_dev;
+        E.chunk_prefix = chunk_prefix;
+        E.nth = tgt ? tgt->num_tiles_hit : nullptr;
+        E.cum_fix = const_cast<int32_t*>(in.cum);
         E.tiles_x = L.tiles_x; E.tiles_y = L.tiles_y; E.tile_bits = L.tile_bits;
         E.depth_bits = L.depth_bits; E.keys = kbuf[0]; E.owner = sc.gids[0];
         const dim3 grid((unsigned)((total + 255) / 256));

@@ -94,6 +94,7 @@ struct RasterInputs {
 
 // ------------------------------------------------------------------ device words / scratch
 enum : int {
+    kCountWord = 62,     // the render path's intersection count (chunk_scan_kernel) in `tickets`
     kDeviceError = 63,   // device error word in `tickets` (bit flags, see kDevErr*)
     kNumTickets = 64,
 };
@@ -220,12 +221,21 @@ struct FusedRecords {
     float4* recs;
     uint32_t* mm_partial;
     float* depth_mm;
+    // non-null: with several chunks the chunk scan writes the intersection count here and the
+    // projection leaves cum_tiles_hit chunk-local (chunk_sums then hold the chunks' exclusive
+    // prefixes): the emission adds them (SortTargets::chunk_prefix)
+    int32_t* count_word = nullptr;
 };
 int launch_project_fwd_fused(const ProjectArgs& a, const FusedRecords& f, DeviceScratch& sc,
                              hipStream_t stream);
 int launch_project_fwd_impl(const ProjectArgs& a, uint32_t* chunk_sums, const FusedRecords* f,
                             hipStream_t stream);
+// Items per chunk of the projection's tile-count scan (one projection workgroup each).
+constexpr int64_t kProjChunkItems = 1024;
 int64_t project_fwd_chunks(int64_t total);
+// Adds chunk c's exclusive prefix to the items of chunk c (1024 items per chunk), c >= 1.
+int launch_chunk_offsets(int32_t* cum, int64_t total, const uint32_t* chunk_prefix,
+                         hipStream_t stream);
 // The projection with no allocation: its chunk totals in a fixed device array of
 // kNoAllocMaxChunks entries per device (one per 1024 items).
 constexpr int64_t kNoAllocMaxChunks = 65536;
@@ -246,6 +256,12 @@ struct SortTargets {
     int32_t* pos = nullptr;
     int32_t* bins = nullptr;
     const float* depth_mm = nullptr;  // per-image depth range already formed (fused projection)
+    // the fused projection's chunk-local cum_tiles_hit (FusedRecords::count_word): the emission
+    // finalizes each item's entry in place (in.cum) from these per-chunk exclusive prefixes, and
+    // count_src (else in.cum's last entry) holds the intersection count
+    const uint32_t* chunk_prefix = nullptr;
+    const int32_t* num_tiles_hit = nullptr;
+    const int32_t* count_src = nullptr;
 };
 
 // Where sort_and_bin left its results: sorted keys (int32 when packed, uint64 when wide), ids,

@@ -345,3 +345,53 @@ def test_fused_forward_with_wide_keys_matches_oracle(_forced_wide_keys, backward
         assert kept.sort.pos is not None
     else:
         assert Ts is None and fidx is None and kept.sort.pos is None
+
+
+def test_render_fwd_cum_is_whole_at_every_capacity():
+    """splat_render_fwd leaves cum_tiles_hit chunk-local in the projection and finalizes it in the
+    emission (or, with no emission at capacity 0, in a separate pass): at capacity 0 (status 6),
+    below the count (status 6) and above it, xys, radii and cum_tiles_hit equal the two-call
+    projection's bit for bit, and num_intersects is the count."""
+    import ctypes
+
+    _case("render_fwd cum at every capacity")
+    s = make_scene(2, n=40_000)
+    n = s.n
+    H, W = s.img_shape
+    tiles = ((W + 15) // 16) * ((H + 15) // 16)
+    dev = torch.device("cuda", 0)
+    q, means, scales = _t(s.quats), _t(s.means), _t(s.scales)
+    colors, opac = _t(s.colors), _t(s.opacities).reshape(-1)
+    vm, bg = _t(s.viewmats[0]), _t(s.background)
+    tf = torch.zeros((1, 4, 4), device="cuda")
+    tids = torch.full((1,), -1, device="cuda", dtype=torch.int32)
+    ref = _ops.project_fwd(means, scales, q, vm, opac, tf, tids, n=n, total=n, num_transforms=1,
+                           has_transforms=False, img_shape=s.img_shape, f=s.f, c=s.c,
+                           glob_scale=1.0, clip_thresh=0.01, quats_wxyz=True)
+    torch.cuda.synchronize()
+    M = int(ref[5][-1].item())
+    assert n > 2 * 1024 and M > 0  # several projection chunks
+    e = lambda *shape, dt=torch.float32: torch.empty(shape, device=dev, dtype=dt)  # noqa: E731
+    p = _lib.ptr
+    for cap in (0, M // 3, M, 2 * M):
+        _case(f"render_fwd cum capacity {cap} (M = {M})")
+        xys, depths, conics = e(n, 2), e(n), e(n, 3)
+        radii, nth = e(n, dt=torch.int32), e(n, dt=torch.int32)
+        cum = torch.full((n,), -7, device=dev, dtype=torch.int32)
+        ids, pos = e(max(cap, 1), dt=torch.int32), e(max(cap, 1), dt=torch.int32)
+        bins, recs = e(tiles, 2, dt=torch.int32), e(n, 16)
+        order, Ts, fidx = e(tiles, dt=torch.int32), e(H, W), e(H, W, dt=torch.int32)
+        img = e(H, W, 3)
+        m = ctypes.c_int64(-1)
+        st = _lib.lib().splat_render_fwd(
+            _lib.stream_handle(dev), p(means), n, p(scales), n, p(q), n, p(vm), 4, p(opac), n,
+            p(colors), n, p(bg), 1, p(tf), 1, p(tids), n, 1, 0, 1, H, W, s.f[0], s.f[1],
+            s.c[0], s.c[1], 1.0, 0.01, 1, 0, p(xys), p(depths), p(radii), p(conics), p(nth),
+            p(cum), cap, p(ids), p(pos), p(bins), p(recs), p(order), p(Ts), p(fidx), p(img),
+            None, ctypes.byref(m))
+        torch.cuda.synchronize()
+        assert st == (0 if cap >= M else _lib.ERR_TOO_MANY), (cap, st)
+        assert m.value == M
+        for label, got, want in (("xys", xys, ref[0]), ("radii", radii, ref[2]),
+                                 ("num_tiles_hit", nth, ref[4]), ("cum", cum, ref[5])):
+            assert_bit_exact(_np(got), _np(want), f"capacity {cap} {label}")
