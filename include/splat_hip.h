@@ -404,7 +404,7 @@ int splat_get_stage_times(double* ms, int64_t* calls, int32_t n);
  * forward's). No counterpart in the reference. */
 int splat_check_device(void);
 
-/* Library ABI version (bumped on any signature change). */
+/* Library ABI version (bumped on any signature or contract change). */
 int splat_abi_version(void);
 
 #ifdef __cplusplus

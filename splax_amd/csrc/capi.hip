@@ -400,7 +400,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 13; }
+int splat_abi_version(void) { return 14; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();

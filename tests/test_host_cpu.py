@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(handle, name), f"{name} declared in include/splat_hip.h but not exported"
     assert set(names) == set(_lib._SIGS), "Python binding and header disagree"
     lib = _lib.lib()
-    assert lib.splat_abi_version() == 13
+    assert lib.splat_abi_version() == 14
     assert isinstance(lib.splat_last_error(), bytes)
 
 
