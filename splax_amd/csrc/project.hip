@@ -267,15 +267,12 @@ __global__ void __launch_bounds__(kProjFwdThreads) project_fwd_kernel(ProjectPar
     int32_t incl = wave_inclusive_scan_i32(local, lane);
     if (lane == 63) s_wave[wave] = incl;
     if constexpr (kFused) {
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t o = __shfl_xor(mm[q], off, 64);
-                mm[q] = (q & 1) ? (o > mm[q] ? o : mm[q]) : (o < mm[q] ? o : mm[q]);
-            }
-        }
-        if (lane == 0) {
+        // the wave's (lo, hi) per image slot, in lane 63 (DPP, every lane active here)
+        mm[0] = wave_minmax_to_lane63<false>(mm[0]);
+        mm[1] = wave_minmax_to_lane63<true>(mm[1]);
+        mm[2] = wave_minmax_to_lane63<false>(mm[2]);
+        mm[3] = wave_minmax_to_lane63<true>(mm[3]);
+        if (lane == 63) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) s_mm[wave][q] = mm[q];
         }

@@ -326,6 +326,26 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
     return v;
 }
 
+// Minimum (kMax: maximum) of an unsigned value over the 64 lanes, valid in lane 63: the same DPP
+// row shifts and row broadcasts, lanes without a source reading the identity.
+template <bool kMax, int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_minmax_step(uint32_t x) {
+    const uint32_t id = kMax ? 0u : 0xffffffffu;
+    const uint32_t y = (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)x, kCtrl, kRowMask, 0xf,
+                                                            false);
+    return kMax ? (y > x ? y : x) : (y < x ? y : x);
+}
+template <bool kMax>
+__device__ __forceinline__ uint32_t wave_minmax_to_lane63(uint32_t x) {
+    x = dpp_minmax_step<kMax, 0x111, 0xf>(x);  // row_shr:1
+    x = dpp_minmax_step<kMax, 0x112, 0xf>(x);  // row_shr:2
+    x = dpp_minmax_step<kMax, 0x114, 0xf>(x);  // row_shr:4
+    x = dpp_minmax_step<kMax, 0x118, 0xf>(x);  // row_shr:8
+    x = dpp_minmax_step<kMax, 0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+    x = dpp_minmax_step<kMax, 0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+    return x;
+}
+
 __device__ __forceinline__ float lane63(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }

@@ -364,12 +364,20 @@ __device__ __forceinline__ void block_gather(const float* __restrict__ rgrad, in
     }
 }
 
-__device__ __forceinline__ int32_t wave_inclusive_scan_i32(int32_t v, int lane) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        int32_t o = __shfl_up(v, off, 64);
-        if (lane >= off) v += o;
-    }
+// Inclusive prefix sum over the 64 lanes (every lane active): DPP row shifts scan each row of 16,
+// then row broadcasts add row 0's total into row 1 and row 2's into row 3, and the first two
+// rows' total (lane 31) into rows 2 and 3. Lanes without a shift source add 0.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ int32_t dpp_scan_add(int32_t x) {
+    return x + __builtin_amdgcn_update_dpp(0, x, kCtrl, kRowMask, 0xf, false);
+}
+__device__ __forceinline__ int32_t wave_inclusive_scan_i32(int32_t v, int /*lane*/) {
+    v = dpp_scan_add<0x111, 0xf>(v);  // row_shr:1
+    v = dpp_scan_add<0x112, 0xf>(v);  // row_shr:2
+    v = dpp_scan_add<0x114, 0xf>(v);  // row_shr:4
+    v = dpp_scan_add<0x118, 0xf>(v);  // row_shr:8
+    v = dpp_scan_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v = dpp_scan_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
     return v;
 }
 
