@@ -343,12 +343,7 @@ chunk_scan_kernel(uint32_t* sums, int64_t chunks, const uint32_t* partial, int32
             for (int64_t c = lo; c < hi; ++c) total += sums[c];
         }
         // exclusive prefix of the run totals: a wave scan, then the totals of the waves before
-        uint32_t incl = total;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint32_t o = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += o;
-        }
+        const uint32_t incl = (uint32_t)wave_inclusive_scan_i32((int32_t)total, lane);
         if (lane == 63) s_wave[wave] = incl;
         __syncthreads();
         uint32_t run = incl - total;

@@ -259,12 +259,7 @@ rts_count_kernel(const K* __restrict__ keys, int64_t M_bound, const int32_t* __r
 // workgroup; every thread of the workgroup must call it.
 __device__ __forceinline__ uint32_t scan_256(uint32_t v, uint32_t* s_tmp, uint32_t* total) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    uint32_t incl = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t o = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += o;
-    }
+    const uint32_t incl = (uint32_t)wave_inclusive_scan_i32((int32_t)v, lane);
     if (lane == 63 && wave < 4) s_tmp[wave] = incl;
     __syncthreads();
     uint32_t off = 0, tot = 0;
@@ -296,12 +291,7 @@ rts_scan_kernel(uint32_t* __restrict__ counts, int64_t parts, uint32_t* __restri
 #pragma unroll
         for (int k = 0; k < 4; ++k) v[k] = p + k < parts ? row[p + k] : 0u;
         const uint32_t mine = (v[0] + v[1]) + (v[2] + v[3]);
-        uint32_t incl = mine;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint32_t o = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += o;
-        }
+        const uint32_t incl = (uint32_t)wave_inclusive_scan_i32((int32_t)mine, lane);
         if (lane == 63) s_wave[wave] = incl;
         __syncthreads();
         uint32_t before = carry, tot = carry;
