@@ -681,13 +681,11 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     __syncthreads();
     atomicMax(&s_max, bin_final);
     // wave-wide largest final index: a record above it has no contributing lane in this wave
-    int32_t wmax = bin_final;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        int32_t o = __shfl_xor(wmax, off, 64);
-        wmax = o > wmax ? o : wmax;
-    }
-    wmax = uniform(wmax);
+    // (a DPP maximum into lane 63 with the sign bit flipped, so the unsigned order is the signed
+    // one; every lane is active here)
+    const uint32_t wm = wave_minmax_to_lane63<true>((uint32_t)bin_final ^ 0x80000000u);
+    const int32_t wmax =
+        (int32_t)((uint32_t)__builtin_amdgcn_readlane((int)wm, 63) ^ 0x80000000u);
     __syncthreads();
     // a final_idx from the matching forward lies inside the tile's range; clamp anything else
     const int32_t start_idx = iminw(s_max, range_end - 1);

@@ -377,19 +377,18 @@ chunk_scan_kernel(uint32_t* sums, int64_t chunks, const uint32_t* partial, int32
             lo = x < lo ? x : lo;
             hi = y > hi ? y : hi;
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const uint32_t x = __shfl_xor(lo, off, 64), y = __shfl_xor(hi, off, 64);
-            lo = x < lo ? x : lo;
-            hi = y > hi ? y : hi;
-        }
-        if (lane == 0) {
+        // the wave's range in lane 63 (DPP; every lane of the workgroup is here)
+        lo = wave_minmax_to_lane63<false>(lo);
+        hi = wave_minmax_to_lane63<true>(hi);
+        if (lane == 63) {
             s_lo[wave] = lo;
             s_hi[wave] = hi;
         }
         __syncthreads();
         if (tid == 0) {
-            for (int w = 1; w < kChunkScanThreads / 64; ++w) {
+            lo = 0xffffffffu;
+            hi = 0u;
+            for (int w = 0; w < kChunkScanThreads / 64; ++w) {
                 lo = s_lo[w] < lo ? s_lo[w] : lo;
                 hi = s_hi[w] > hi ? s_hi[w] : hi;
             }

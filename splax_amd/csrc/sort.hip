@@ -67,20 +67,19 @@ minmax_partial_kernel(const float* depths, const int32_t* radii, int32_t n,
             hi = o > hi ? o : hi;
         }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        uint32_t a = __shfl_xor(lo, off, 64), b = __shfl_xor(hi, off, 64);
-        lo = a < lo ? a : lo;
-        hi = b > hi ? b : hi;
-    }
+    // the wave's range in lane 63 (DPP; every lane is active here)
+    lo = wave_minmax_to_lane63<false>(lo);
+    hi = wave_minmax_to_lane63<true>(hi);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) {
+    if (lane == 63) {
         s_lo[wave] = lo;
         s_hi[wave] = hi;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < kMmThreads / 64; ++w) {
+        lo = 0xffffffffu;
+        hi = 0u;
+        for (int w = 0; w < kMmThreads / 64; ++w) {
             lo = s_lo[w] < lo ? s_lo[w] : lo;
             hi = s_hi[w] > hi ? s_hi[w] : hi;
         }
@@ -102,20 +101,19 @@ minmax_final_kernel(const uint32_t* partial, int32_t blocks_per_image, float* mm
         lo = a < lo ? a : lo;
         hi = c > hi ? c : hi;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        uint32_t a = __shfl_xor(lo, off, 64), c = __shfl_xor(hi, off, 64);
-        lo = a < lo ? a : lo;
-        hi = c > hi ? c : hi;
-    }
+    // the wave's range in lane 63 (DPP; every lane is active here)
+    lo = wave_minmax_to_lane63<false>(lo);
+    hi = wave_minmax_to_lane63<true>(hi);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) {
+    if (lane == 63) {
         s_lo[wave] = lo;
         s_hi[wave] = hi;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < kMmThreads / 64; ++w) {
+        lo = 0xffffffffu;
+        hi = 0u;
+        for (int w = 0; w < kMmThreads / 64; ++w) {
             lo = s_lo[w] < lo ? s_lo[w] : lo;
             hi = s_hi[w] > hi ? s_hi[w] : hi;
         }
