@@ -88,12 +88,24 @@ __global__ void __launch_bounds__(256) log_params_bwd_kernel(LogParams P) {
 
 constexpr int kL1Chunk = 4096;  // elements per workgroup (16 per thread)
 
+// x plus the double of the lane DPP control kCtrl names (0 where it names none), in two 32-bit
+// halves.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ double dpp_add_f64(double x) {
+    const int64_t b = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, kCtrl, kRowMask, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), kCtrl, kRowMask, 0xf,
+                                               false);
+    return x + __longlong_as_double((int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+
 // Workgroup sums of |img - target| (kSquare: (img - target)^2, exact in double) in double, in a
-// fixed order: per thread sequential, then a fixed tree over the workgroup.
+// fixed order: per thread sequential over its 16 elements, then the wave's 64 sums by DPP row
+// shifts and broadcasts into lane 63, then the four waves in order.
 template <bool kSquare>
 __global__ void __launch_bounds__(256) loss_partials_kernel(const float* img, const float* tgt,
                                                             int64_t count, double* partials) {
-    __shared__ double s[256];
+    __shared__ double s[4];
     const int64_t base = (int64_t)blockIdx.x * kL1Chunk;
     double acc = 0.0;
 #pragma unroll
@@ -104,13 +116,15 @@ __global__ void __launch_bounds__(256) loss_partials_kernel(const float* img, co
             acc += kSquare ? (double)d * (double)d : (double)fabsf(d);
         }
     }
-    s[threadIdx.x] = acc;
+    acc = dpp_add_f64<0x111, 0xf>(acc);  // row_shr:1
+    acc = dpp_add_f64<0x112, 0xf>(acc);  // row_shr:2
+    acc = dpp_add_f64<0x114, 0xf>(acc);  // row_shr:4
+    acc = dpp_add_f64<0x118, 0xf>(acc);  // row_shr:8
+    acc = dpp_add_f64<0x142, 0xa>(acc);  // row_bcast:15 into rows 1 and 3
+    acc = dpp_add_f64<0x143, 0xc>(acc);  // row_bcast:31 into rows 2 and 3
+    if ((threadIdx.x & 63) == 63) s[threadIdx.x >> 6] = acc;
     __syncthreads();
-    for (int off = 128; off > 0; off >>= 1) {
-        if ((int)threadIdx.x < off) s[threadIdx.x] += s[threadIdx.x + off];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) partials[blockIdx.x] = s[0];
+    if (threadIdx.x == 0) partials[blockIdx.x] = ((s[0] + s[1]) + s[2]) + s[3];
 }
 
 // One workgroup: the partials in the same fixed order, divided by the count.

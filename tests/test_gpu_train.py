@@ -279,7 +279,7 @@ def test_log_params_bit_exact(n):
         assert_bit_exact(_np(x.grad).reshape(r.shape), r, f"log_params {label}")
 
 
-@pytest.mark.parametrize("count", [1, 4095, 4097, 3 * 1060 * 1600 * 4])
+@pytest.mark.parametrize("count", [1, 4095, 4097, 16383, 16385, 3 * 1060 * 1600 * 4])
 def test_l1_loss(count):
     from splax_amd.train import l1_loss
 
@@ -296,7 +296,7 @@ def test_l1_loss(count):
     assert_bit_exact(_np(x.grad), ref_v, "l1 cotangent")
 
 
-@pytest.mark.parametrize("count", [1, 4095, 4097, 3 * 1080 * 1920])
+@pytest.mark.parametrize("count", [1, 4095, 4097, 16383, 16385, 3 * 1080 * 1920])
 def test_mse_loss(count):
     from splax_amd.train import mse_loss
 
