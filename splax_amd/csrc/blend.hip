@@ -460,19 +460,22 @@ __device__ __forceinline__ int order_bucket(int32_t c) {
 }
 
 // Exclusive scan of the 256 bucket counts in s_cnt, in place (all threads call it).
-__device__ __forceinline__ void order_scan(uint32_t* s_cnt, uint32_t (*s_scan)[256], int tid) {
-    int cur = 0;
-    if (tid < 256) s_scan[0][tid] = s_cnt[tid];
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-        if (tid < 256) {
-            const uint32_t v = s_scan[cur][tid];
-            s_scan[cur ^ 1][tid] = tid >= off ? v + s_scan[cur][tid - off] : v;
-        }
-        cur ^= 1;
-        __syncthreads();
+// Exclusive scan of the 256 bucket counts in place: waves 0-3 (threads 0-255, whole waves) scan
+// by DPP, then add the totals of the waves before them. Every thread of the workgroup calls it.
+__device__ __forceinline__ void order_scan(uint32_t* s_cnt, uint32_t* s_tot, int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+    uint32_t v = 0, incl = 0;
+    if (tid < 256) {
+        v = s_cnt[tid];
+        incl = (uint32_t)wave_inclusive_scan_i32((int32_t)v, lane);
+        if (lane == 63) s_tot[wave] = incl;
     }
-    if (tid < 256) s_cnt[tid] = s_scan[cur][tid] - s_cnt[tid];
+    __syncthreads();
+    if (tid < 256) {
+        uint32_t before = 0;
+        for (int w = 0; w < wave; ++w) before += s_tot[w];
+        s_cnt[tid] = before + incl - v;
+    }
     __syncthreads();
 }
 
@@ -484,7 +487,7 @@ constexpr int kOrderPer = 8;  // tiles per thread kept in registers (images up t
 // and keeps their buckets for the scatter; larger images take two strided passes.
 __global__ void __launch_bounds__(kOrderThreads)
 tile_order_kernel(const int32_t* bins, int32_t num_tiles, int32_t per_image, int32_t* order) {
-    __shared__ uint32_t s_cnt[256], s_scan[2][256];
+    __shared__ uint32_t s_cnt[256], s_tot[4];
     const int tid = threadIdx.x;
     const int64_t image = blockIdx.x;
     const int32_t* ib = bins + 2 * (per_image ? image : 0) * (int64_t)num_tiles;
@@ -502,7 +505,7 @@ tile_order_kernel(const int32_t* bins, int32_t num_tiles, int32_t per_image, int
         for (int i = 0; i < kOrderPer; ++i)
             if (bk[i] >= 0) atomicAdd(&s_cnt[bk[i]], 1u);
         __syncthreads();
-        order_scan(s_cnt, s_scan, tid);
+        order_scan(s_cnt, s_tot, tid);
 #pragma unroll
         for (int i = 0; i < kOrderPer; ++i)
             if (bk[i] >= 0) order[first + atomicAdd(&s_cnt[bk[i]], 1u)] = first + i * kOrderThreads + tid;
@@ -511,7 +514,7 @@ tile_order_kernel(const int32_t* bins, int32_t num_tiles, int32_t per_image, int
     for (int32_t t = tid; t < num_tiles; t += kOrderThreads)
         atomicAdd(&s_cnt[255 - order_bucket(ib[2 * t + 1] - ib[2 * t])], 1u);
     __syncthreads();
-    order_scan(s_cnt, s_scan, tid);
+    order_scan(s_cnt, s_tot, tid);
     for (int32_t t = tid; t < num_tiles; t += kOrderThreads) {
         const uint32_t at = atomicAdd(&s_cnt[255 - order_bucket(ib[2 * t + 1] - ib[2 * t])], 1u);
         order[first + at] = first + t;
