@@ -813,6 +813,10 @@ static int check_raster_bwd(const RasterInputs& in, const BlendBwdArgs& args) {
     if (args.B_out <= 0 || (in.B_geom > 1 && in.B_geom != args.B_out))
         return fail(kErrArgs, "rasterize_bwd: B_geom must be 1 or equal to B_out");
     if (args.vout_rows <= 0 || !in.cum) return fail(kErrArgs, "rasterize_bwd: empty cotangent");
+    // a forward-only render may leave its final buffers out: the backward needs both
+    if (!args.final_Ts || !args.final_idx || !args.v_out)
+        return fail(kErrArgs, "rasterize_bwd: final_Ts, final_idx and the image cotangent are "
+                              "required");
     if (args.v_depths && (!in.depths || !args.v_out_depth || args.vdepth_rows <= 0))
         return fail(kErrArgs, "rasterize_bwd: depth channel needs depths and v_out_depth");
     if ((int64_t)args.B_out * in.n >= ((int64_t)1 << 31))

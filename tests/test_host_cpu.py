@@ -227,3 +227,24 @@ def test_nested_batch_shapes_and_errors():
     assert fold(x, 2, ()).shape == x.shape
     with pytest.raises(ValueError, match="inconsistent batch shapes"):
         batch_shape({"x": (torch.zeros((2, 7, 3)), 2), "v": (torch.zeros((3, 4, 4)), 2)})
+
+
+def test_backward_requires_the_final_buffers():
+    """A forward-only render may leave final_Ts / final_idx out; the backward entry points
+    reject missing final buffers or a missing image cotangent with status 1 before touching the
+    device (the placeholder addresses are never dereferenced)."""
+    import ctypes
+
+    lib = _lib.lib()
+    lib.splat_last_error.restype = ctypes.c_char_p
+    n = 10
+    buf = 256  # a stand-in device address (8-byte aligned; only the host checks run)
+
+    def bwd(final_Ts, final_idx, v_out):
+        return lib.splat_rasterize_bwd(None, buf, n, buf, n, buf, n, buf, 1, buf, buf, buf, buf,
+                                       buf, final_Ts, final_idx, v_out, 16, n, 1, 1, 16, 16, buf,
+                                       buf, buf, buf)
+
+    for args in ((None, buf, buf), (buf, None, buf), (buf, buf, None)):
+        assert bwd(*args) == _lib.ERR_ARGS, args
+        assert b"final_Ts, final_idx and the image cotangent" in lib.splat_last_error()
