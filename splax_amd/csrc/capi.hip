@@ -738,6 +738,7 @@ static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortT
                               int64_t* num_intersects) {
     int rc = check_raster(in, in.B_geom);
     if (rc) return rc;
+    if (!out_img) return fail(kErrArgs, "rasterize: missing image output");
     if (out_depth && !in.depths) return fail(kErrArgs, "rasterize: depth channel needs depths");
     DeviceScratch& sc = scratch_for_current_device();
     ScratchUse use(sc, s);
@@ -1068,6 +1069,7 @@ int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_m
         return fail(kErrArgs, "render_fwd: missing sorted-list or record buffers");
     if ((uintptr_t)records & 15)
         return fail(kErrArgs, "render_fwd: records must be 16-byte aligned");
+    if (!out_img) return fail(kErrArgs, "render_fwd: missing image output");
     RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac, opacities,
                                     rows_opac, background, rows_bg, xys, depths, radii, conics,
                                     cum_tiles_hit, num_gaussians, B, img_h, img_w);

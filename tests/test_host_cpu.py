@@ -248,3 +248,17 @@ def test_backward_requires_the_final_buffers():
     for args in ((None, buf, buf), (buf, None, buf), (buf, buf, None)):
         assert bwd(*args) == _lib.ERR_ARGS, args
         assert b"final_Ts, final_idx and the image cotangent" in lib.splat_last_error()
+
+
+def test_forward_requires_the_image_output():
+    """The blends write the image unconditionally, so a missing image output is status 1 before
+    any launch (placeholder addresses are never dereferenced)."""
+    import ctypes
+
+    lib = _lib.lib()
+    lib.splat_last_error.restype = ctypes.c_char_p
+    n, buf = 10, 256
+    m = ctypes.c_int64(0)
+    rc = lib.splat_rasterize_fwd(None, buf, n, buf, n, buf, n, buf, 1, buf, buf, buf, buf, buf, n,
+                                 1, 16, 16, buf, buf, None, ctypes.byref(m))
+    assert rc == _lib.ERR_ARGS and b"missing image output" in lib.splat_last_error()
