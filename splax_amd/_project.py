@@ -149,13 +149,45 @@ def project(mean3ds: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor,
             conics.reshape(*lead, 3), nth.reshape(*lead, 1), cum.reshape(*lead, 1))
 
 
+class _CompensationFn(torch.autograd.Function):
+    """rho = sqrt(clip(rho2, 0, 1)) of the conics with the reverse-mode rules of the reference's
+    jax expression (splax/_project/_project.py:113-116), not torch's: sqrt' = 0.5 / rho times the
+    cotangent (so rho = 0 gives NaN or inf even for a zero cotangent), and each clip bound passes
+    1 strictly inside, 1/2 at a tie and 0 outside, as multipliers (inf times 0 is NaN). The fused
+    antialiased blend (grad_gather_kernel) and the oracle apply the same rules."""
+
+    @staticmethod
+    def forward(ctx, conics, eps):
+        a, b, c = conics[..., 0], conics[..., 1], conics[..., 2]
+        rho2 = 1.0 - eps * (a + c) + (eps * eps) * (a * c - b * b)
+        rho = torch.sqrt(torch.clamp(rho2, 0.0, 1.0))
+        ctx.save_for_backward(conics, rho2, rho)
+        ctx.eps = eps
+        return rho
+
+    @staticmethod
+    def backward(ctx, g):
+        conics, rho2, rho = ctx.saved_tensors
+        eps = ctx.eps
+        a, b, c = conics[..., 0], conics[..., 1], conics[..., 2]
+        one, half, zero = (torch.full_like(rho2, v) for v in (1.0, 0.5, 0.0))
+        v_cl = g * (0.5 / rho)
+        m_lo = torch.where(rho2 > 0, one, torch.where(rho2 == 0, half, zero))
+        y = torch.where(rho2 > 0, rho2, zero)
+        m_hi = torch.where(y < 1, one, torch.where(y == 1, half, zero))
+        v_r2 = (v_cl * m_hi) * m_lo
+        v_s, v_t = -(eps * v_r2), (eps * eps) * v_r2
+        v_conics = torch.stack([v_s + v_t * c, -(v_t * b) - v_t * b, v_s + v_t * a], dim=-1)
+        return v_conics, None
+
+
 def opacity_compensation(conics: torch.Tensor, radii: torch.Tensor,
                          eps: float = 0.3) -> torch.Tensor:
-    """Mip-Splatting opacity compensation rho per gaussian (splax/_project/_project.py:95-117)."""
+    """Mip-Splatting opacity compensation rho per gaussian (splax/_project/_project.py:95-117),
+    differentiated by the reference's rules (a visible item whose rho2 <= 0 gets NaN conic
+    cotangents, as jax's sqrt and clip rules give there)."""
     lead = conics.shape[:-1]
-    a, b, c = conics[..., 0], conics[..., 1], conics[..., 2]
-    rho2 = 1.0 - eps * (a + c) + (eps * eps) * (a * c - b * b)
-    rho = torch.sqrt(torch.clamp(rho2, 0.0, 1.0))
+    rho = _CompensationFn.apply(conics, eps)
     return torch.where(radii.reshape(lead) > 0, rho, torch.ones_like(rho))
 
 

@@ -262,3 +262,36 @@ def test_forward_requires_the_image_output():
     rc = lib.splat_rasterize_fwd(None, buf, n, buf, n, buf, n, buf, 1, buf, buf, buf, buf, buf, n,
                                  1, 16, 16, buf, buf, None, ctypes.byref(m))
     assert rc == _lib.ERR_ARGS and b"missing image output" in lib.splat_last_error()
+
+
+def test_opacity_compensation_backward_follows_the_reference_rules():
+    """opacity_compensation's backward follows the reference's jax rules, like the oracle's
+    compensation_vjp (which the fused antialiased blend follows): the same float32 cotangents
+    inside the clip and NaN conic cotangents where rho2 <= 0 (sqrt' = 0.5 / rho times the
+    cotangent, then the clip's 0 multiplier), where torch's own clamp rule would give 0."""
+    from oracle import oracle as O
+
+    rng = np.random.default_rng(3)
+    n = 400
+    a = rng.uniform(0.05, 3.0, n)
+    c = rng.uniform(0.05, 3.0, n)
+    b = rng.uniform(-0.9, 0.9, n) * np.sqrt(a * c)
+    conics = np.stack([a, b, c], -1).astype(np.float32)
+    conics[:5] = 0.0  # rho2 = 1: the upper clip's tie
+    opac = rng.uniform(0.05, 1.0, n).astype(np.float32)
+    vbo = rng.normal(size=n).astype(np.float32)
+    _, rho2 = O.compensation_rho(conics)
+    assert (rho2 < 0).sum() > 20 and ((rho2 > 0) & (rho2 < 1)).sum() > 100
+    c_t = torch.tensor(conics, requires_grad=True)
+    o_t = torch.tensor(opac, requires_grad=True)
+    bo = o_t * splax_amd.opacity_compensation(c_t, torch.ones(n, 1, dtype=torch.int32))
+    bo.backward(torch.tensor(vbo))
+    v_o, v_c = O.compensation_vjp(vbo, opac, conics)
+    g_c = c_t.grad.numpy()
+    # NaN exactly where the oracle has it (every rho2 < 0 row); the rest within float32 rounding
+    # of the two evaluations (torch's CPU kernels and numpy may differ by an ulp in rho)
+    np.testing.assert_array_equal(np.isnan(g_c), np.isnan(v_c))
+    assert np.isnan(g_c[rho2 < 0]).all() and not np.isnan(g_c[rho2 >= 0]).any()
+    np.testing.assert_allclose(o_t.grad.numpy(), v_o, rtol=1e-6, atol=0)
+    fin = ~np.isnan(v_c)
+    np.testing.assert_allclose(g_c[fin], v_c[fin], rtol=1e-5, atol=1e-7)
