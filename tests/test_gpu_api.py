@@ -40,22 +40,33 @@ def _np(t):
     return t.detach().cpu().numpy()
 
 
-def _oracle_render_and_grads(sc, n, w, opac_blend=None):
+def _oracle_render_and_grads(sc, n, w, opac_blend=None, vm=None):
+    """The oracle's forward and chained backward of sum(img * w); with B stacked viewmats (vm of
+    shape (B, 4, 4), w of shape (B, H, W, 3)) the per-camera item gradients are summed."""
     H, W = sc["img_shape"]
+    vm = sc["vm"] if vm is None else vm
+    B = vm.size // 16
     q = np.roll(sc["quats"], -1, axis=-1)
     xys, depths, radii, conics, nth, cum = O.project_fwd(
-        sc["means"], sc["scales"], q, sc["vm"], sc["opac"], n=n, total=n, img_shape=(H, W),
-        f=sc["f"], c=sc["c"])
+        sc["means"], sc["scales"], q, vm.reshape(-1, 4), sc["opac"], n=n, total=B * n,
+        img_shape=(H, W), f=sc["f"], c=sc["c"])
     ob = sc["opac"] if opac_blend is None else opac_blend
     img, Ts, fidx, _, _ = O.rasterize_fwd(sc["colors"], ob, sc["opac"], sc["bg"], xys, depths,
-                                          radii, conics, cum, n=n, B=1, img_shape=(H, W))
+                                          radii, conics, cum, n=n, B=B, img_shape=(H, W))
     vc, vo, vxy, vcon, _ = O.rasterize_bwd(sc["colors"], ob, sc["opac"], sc["bg"], xys, depths,
-                                           radii, conics, cum, Ts, fidx, w.astype(np.float32),
-                                           n=n, B_out=1, B_geom=1, img_shape=(H, W))
-    vm_, vs_, vq_, vv_, _ = O.project_bwd(sc["means"], sc["scales"], q, sc["vm"], radii, conics,
-                                          vxy, np.zeros(n, np.float32), vcon, n=n, B=1, f=sc["f"])
-    return img.reshape(H, W, 3), dict(means=vm_, scales=vs_, quats=np.roll(vq_, 1, axis=-1),
-                                      colors=vc, opac=vo.reshape(-1, 1), viewmat=vv_)
+                                           radii, conics, cum, Ts, fidx,
+                                           w.reshape(-1, 3).astype(np.float32), n=n, B_out=B,
+                                           B_geom=B, img_shape=(H, W))
+    vm_, vs_, vq_, vv_, _ = O.project_bwd(sc["means"], sc["scales"], q, vm.reshape(-1, 4), radii,
+                                          conics, vxy, np.zeros(B * n, np.float32), vcon, n=n,
+                                          B=B, f=sc["f"])
+    fold = (lambda a: a.reshape(B, n, -1).astype(np.float64).sum(0).astype(np.float32)) \
+        if B > 1 else (lambda a: a)
+    shape = (B, H, W, 3) if B > 1 else (H, W, 3)
+    return img.reshape(shape), dict(means=fold(vm_), scales=fold(vs_),
+                                    quats=np.roll(fold(vq_), 1, axis=-1), colors=fold(vc),
+                                    opac=fold(vo.reshape(-1, 1)),
+                                    viewmat=vv_.reshape(B, 4, 4) if B > 1 else vv_)
 
 
 def test_render_and_grads_match_oracle():
@@ -79,10 +90,27 @@ def test_render_and_grads_match_oracle():
     assert (_np(vm.grad)[3] == 0).all()
 
 
-def test_batched_cameras_equal_stacked():
-    _case("batched viewmats")
-    n, H, W = 4000, 96, 96
-    sc = random_scene(n, H, W, seed=8)
+def _stress_scene():
+    """test_gpu_parity's extremes scene (huge, needle-thin and near-plane gaussians, opacities at
+    the clamp and the threshold), in random_scene's dictionary form."""
+    import importlib.util
+    from pathlib import Path
+
+    spec = importlib.util.spec_from_file_location(
+        "gpu_parity", Path(__file__).with_name("test_gpu_parity.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod._stress_scene()
+
+
+@pytest.mark.parametrize("scene", ["random", "stress"])
+def test_batched_cameras_equal_stacked(scene):
+    _case(f"batched viewmats {scene}")
+    if scene == "random":
+        sc = random_scene(4000, 96, 96, seed=8)
+    else:
+        sc = _stress_scene()
+    H, W = sc["img_shape"]
     vms = np.stack([sc["vm"]] * 3)
     vms[1, 0, 3] += 0.25
     vms[2, 1, 3] -= 0.2
@@ -99,12 +127,49 @@ def test_batched_cameras_equal_stacked():
     bimg, bg = run(vms, w)
     assert bimg.shape == (3, H, W, 3)
     singles = [run(vms[b], w[b]) for b in range(3)]
+    if scene == "random":
+        for b in range(3):
+            assert_bit_exact(bimg[b], singles[b][0], f"batched/img[{b}]")
+        for k in bg:
+            summed = sum(s[1][k].astype(np.float64) for s in singles)
+            r = rel_fro(bg[k], summed)
+            assert r < 1e-5, f"batched/{k}: {r:.2e}"
+        return
+    # three images leave 20 depth bits against a single render's 22 (the key's image field), so
+    # items whose quantized depths tie only in the batch blend in another order there, as in the
+    # reference, whose batched key has this layout: the batch is held to the oracle's batched
+    # forward bit for bit, the single renders to within float rounding
+    n = len(sc["means"])
+    rimg, rg = _oracle_render_and_grads(sc, n, w, vm=vms)
+    assert_bit_exact(bimg, rimg, "batched/img vs the batched oracle")
     for b in range(3):
-        assert_bit_exact(bimg[b], singles[b][0], f"batched/img[{b}]")
+        np.testing.assert_allclose(bimg[b], singles[b][0], rtol=1e-5, atol=1e-6)
+    # the mean / scale / quaternion gradients of a needle-thin item are ill-conditioned in float32:
+    # v_cov2d = -conic v_conic conic scales rounding in v_conic (and the conic-weighted v_xy) by
+    # up to cond(conic)^2, so two float32 evaluations that sum pixels in different orders (the
+    # oracle's and the kernel's, or a batch's and a single render's) differ there. Items below
+    # condition 1e2 in every camera are held to the usual bar; the whole arrays to a bound that a
+    # wrong camera, item or order exceeds (measured against the oracle's batched chain, quats:
+    # below 3e-6 under condition 3e2, 7e-5 up to 1e3, 2e-3 up to 1e4, 3e-2 past it; a single
+    # render against the single-camera oracle shows the same; colors and opacities 5e-7 in every
+    # band)
+    q = np.roll(sc["quats"], -1, axis=-1)
+    _, _, radii, conics, _, _ = O.project_fwd(
+        sc["means"], sc["scales"], q, vms.reshape(-1, 4), sc["opac"], n=n, total=3 * n,
+        img_shape=(H, W), f=sc["f"], c=sc["c"])
+    ca, cb, cc = (conics.reshape(-1, 3)[:, k].astype(np.float64) for k in range(3))
+    cond = np.where(radii.ravel() > 0, (ca + cc) ** 2 / np.maximum(ca * cc - cb * cb, 1e-300), 1.0)
+    well = cond.reshape(3, n).max(0) < 1e2
+    assert well.sum() > 4000 and (~well).sum() > 2000
     for k in bg:
         summed = sum(s[1][k].astype(np.float64) for s in singles)
-        r = rel_fro(bg[k], summed)
-        assert r < 1e-5, f"batched/{k}: {r:.2e}"
+        for label, ref in (("the batched oracle", rg[k]), ("the summed single renders", summed)):
+            ref = np.asarray(ref, np.float64).reshape(bg[k].shape)
+            r = rel_fro(bg[k][well], ref[well])
+            assert r < 1e-5, f"batched/{k} (cond < 1e2) vs {label}: {r:.2e}"
+            bound = 1e-5 if k in ("colors", "opac") else 1e-1
+            r = rel_fro(bg[k], ref)
+            assert r < bound, f"batched/{k} vs {label}: {r:.2e}"
 
 
 def test_batched_viewmat_grads_per_pose():
