@@ -279,7 +279,6 @@ def main():
     import splax_amd
     from splax_amd import _lib
     from splax_amd.scenes import make_scene
-    from splax_amd.train import mse_loss
 
     dev = torch.device("cuda:0")
     scene = make_scene(args.config, n=args.n)
@@ -307,11 +306,12 @@ def main():
         for p in params:
             p.grad = None
         vm.grad = None
-        img = forward()
-        # the library's fused MSE, one pass each way (29 us of GPU time; torch's mse_loss runs
-        # three kernels and a 25 MB zero fill, 56 us); the host stays ahead of the GPU after
-        # each forward's count readback either way (0.65 ms of queued GPU work at the end)
-        loss = mse_loss(img, target)
+        # the MSE fused into the blends: the forward blend sums each tile's squared errors as
+        # it writes the image, the backward blend forms each pixel's image cotangent (no loss
+        # passes over the image: 30 us of GPU time as separate launches)
+        loss, _ = splax_amd.render_loss(*params, target=target, loss="mse", viewmat=vm,
+                                        background=bg, img_shape=(H, W), f=scene.f,
+                                        antialiased=scene.antialiased)
         loss.backward(one)
 
     for _ in range(args.warmup):

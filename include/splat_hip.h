@@ -252,7 +252,14 @@ int splat_set_wide_keys(int force);
  * projection outputs are whole, the lists and image those of a list cut at capacity).
  * sorted_pos, final_Ts and final_idx may be NULL when no backward will follow (a forward-only
  * render): the sort then moves no emission positions and the blend writes only the image (and
- * depth), and the kept lists cannot feed splat_render_bwd. */
+ * depth), and the kept lists cannot feed splat_render_bwd.
+ * loss_kind 1 (L1) or 2 (MSE) fuses a per-pixel loss into the blend: *loss (one float, device
+ * memory) receives the mean over the B * img_h * img_w * 3 colour values of |img - target| or
+ * (img - target)^2 against loss_target ([B, img_h, img_w, 3]); the blend leaves each tile's
+ * sum (in double, per-pixel terms exact) in library scratch and one more launch adds them in a
+ * fixed order. That is the value splat_l1_loss_fwd / splat_mse_loss_fwd give for the same image,
+ * up to the order of the double additions. loss_kind 0: no loss (loss_target and loss unused).
+ * The reference has no fused loss: its callers apply the loss to the rendered image. */
 int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
                      const float* scales, int64_t rows_scales, const float* quats,
                      int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
@@ -267,7 +274,8 @@ int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_m
                      int32_t* cum_tiles_hit, int64_t capacity, int32_t* sorted_ids,
                      int32_t* sorted_pos, int32_t* tile_bins, float* records,
                      int32_t* tile_order, float* final_Ts, int32_t* final_idx, float* out_img,
-                     float* out_depth, int64_t* num_intersects);
+                     float* out_depth, int64_t* num_intersects, const float* loss_target,
+                     int32_t loss_kind, float* loss);
 
 /* Backward of splat_render_fwd at the same inputs, given its outputs and kept buffers and the
  * image cotangent (and, with out_depth in the forward, v_out_depth). Outputs: v_means [.,3],
@@ -275,7 +283,11 @@ int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_m
  * v_opacities [.] (the raw opacities' cotangent), v_viewmat [4B,4] (may be NULL: not formed),
  * v_transforms [B*num_transforms,4,4] (with has_transforms). Rows: num_gaussians with
  * fold_shared != 0 (means, scales, quats, colors and opacities all shared: the cotangents summed
- * over the B images in image order), else B * num_gaussians. */
+ * over the B images in image order), else B * num_gaussians. With loss_kind 1 or 2 (the fused
+ * loss of the forward) the image cotangent is formed per pixel from out_img (the forward's
+ * image), loss_target and the loss cotangent *v_loss (one float, device memory) with the
+ * operations of splat_l1_loss_bwd / splat_mse_loss_bwd, so the gradients equal those of the
+ * separate loss's cotangent; v_out_img and vout_rows are then unused (may be NULL / 0). */
 int splat_render_bwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
                      const float* scales, int64_t rows_scales, const float* quats,
                      int64_t rows_quats, const float* viewmat, int64_t rows_viewmat,
@@ -293,7 +305,8 @@ int splat_render_bwd(splat_stream_t stream, const float* means3d, int64_t rows_m
                      const float* v_out_img, int64_t vout_rows, const float* v_out_depth,
                      int64_t vdepth_rows, float* v_means, float* v_scales, float* v_quats,
                      float* v_colors, float* v_opacities, float* v_viewmat,
-                     float* v_transforms, int32_t fold_shared);
+                     float* v_transforms, int32_t fold_shared, const float* loss_target,
+                     int32_t loss_kind, const float* out_img, const float* v_loss);
 
 /* ---------------------------------------------------------------- training step
  * The config-4 training step around the render: the per-parameter Adam of the trainers and the

@@ -13,7 +13,7 @@ from splax_amd import utils
 from splax_amd._lib import clear_cache
 from splax_amd._project import opacity_compensation, project, transform_ids
 from splax_amd._rasterize import rasterize, rasterize_depth
-from splax_amd._render import render, render_log
+from splax_amd._render import render, render_log, render_log_loss, render_loss
 
 __all__ = [
     "clear_cache",
@@ -23,6 +23,8 @@ __all__ = [
     "rasterize_depth",
     "render",
     "render_log",
+    "render_log_loss",
+    "render_loss",
     "transform_ids",
     "utils",
 ]

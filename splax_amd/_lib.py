@@ -53,9 +53,10 @@ _SIGS = {
     + [_vp, _vp, _i64, _vp, _vp],
     "splat_set_wide_keys": [_i32],
     "splat_render_fwd": [_vp] + [_vp, _i64] * 8 + [_vp] + [_i32] * 6 + [_f32] * 6
-    + [_i32, _i32] + [_vp] * 6 + [_i64] + [_vp] * 10,
+    + [_i32, _i32] + [_vp] * 6 + [_i64] + [_vp] * 10 + [_vp, _i32, _vp],
     "splat_render_bwd": [_vp] + [_vp, _i64] * 8 + [_vp] + [_i32] * 6 + [_f32] * 3
-    + [_i32, _i32] + [_vp] * 10 + [_i64] + [_vp] * 3 + [_i64, _vp, _i64] + [_vp] * 7 + [_i32],
+    + [_i32, _i32] + [_vp] * 10 + [_i64] + [_vp] * 3 + [_i64, _vp, _i64] + [_vp] * 7 + [_i32]
+    + [_vp, _i32, _vp, _vp],
     "splat_adam_step": [_vp, _vp, _i32, _f64, _f64, _f64, _f64, _i64],
     "splat_adam_reset_rows": [_vp, _vp, _i32, _vp, _i64],
     "splat_mcmc_relocate": [_vp] + [_vp] * 5 + [_i64, _i32, _f32, _u64, _vp, _vp],

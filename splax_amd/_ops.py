@@ -205,18 +205,23 @@ class RenderKept(NamedTuple):
 
 def render_fwd(means, scales, quats_wxyz, colors, opac, viewmat, background, transforms,
                transform_ids, *, n, B, num_transforms, has_transforms, img_shape, f, c,
-               glob_scale, clip_thresh, compensate=False, render_depth=False, backward=True):
+               glob_scale, clip_thresh, compensate=False, render_depth=False, backward=True,
+               loss_kind=0, loss_target=None, loss_out=None):
     """The fused render forward (splat_render_fwd): projection, sort and blend in one call over
     B images of n gaussians; quaternions wxyz. Returns (img, Ts, fidx, RenderKept, depth or None).
     Kept-list capacity as rasterize_fwd_keep. backward=False (no render_bwd will follow) sorts no
     emission positions and writes no final_Ts / final_idx: Ts, fidx and the kept lists' pos are
-    then None."""
+    then None. loss_kind LOSS_L1 / LOSS_MSE fuses the mean pixel loss against loss_target
+    ([B * H, W, 3] values) into the blend, its value written into loss_out (a float32 scalar)."""
     means, scales, quats_wxyz, colors, opac, viewmat, background, transforms = map(
         _f32, (means, scales, quats_wxyz, colors, opac, viewmat, background, transforms))
     transform_ids = _i32(transform_ids)
     dev = _lib.require_gpu(means, scales, quats_wxyz, colors, opac, viewmat, background)
     H, W = img_shape
     total = B * n
+    if loss_kind:
+        loss_target = _f32(loss_target)
+        _check_loss_operands(loss_kind, loss_target, B, H, W, dev, loss_out)
     tiles = ((W + 15) // 16) * ((H + 15) // 16)
     e = lambda *shape, dt=torch.float32: torch.empty(shape, device=dev, dtype=dt)  # noqa: E731
     xys, depths, conics = e(total, 2), e(total), e(total, 3)
@@ -241,7 +246,8 @@ def render_fwd(means, scales, quats_wxyz, colors, opac, viewmat, background, tra
                 int(has_transforms), B, H, W, f[0], f[1], c[0], c[1], glob_scale, clip_thresh, 1,
                 int(compensate), p(xys), p(depths), p(radii), p(conics), p(nth), p(cum), cap,
                 p(ids), p(pos), p(bins), p(recs), p(order), p(Ts), p(fidx), p(img), p(depth),
-                ctypes.byref(m))
+                ctypes.byref(m), p(loss_target) if loss_kind else None, int(loss_kind),
+                p(loss_out) if loss_kind else None)
         if st == _lib.ERR_TOO_MANY and m.value > cap:
             cap = int(m.value * 1.25) + 1
             _KEEP_CAPACITY[key] = cap
@@ -258,16 +264,27 @@ def render_fwd(means, scales, quats_wxyz, colors, opac, viewmat, background, tra
 def render_bwd(means, scales, quats_wxyz, colors, opac, viewmat, background, transforms,
                transform_ids, kept: RenderKept, final_Ts, final_idx, v_out, *, n, B,
                num_transforms, has_transforms, img_shape, f, glob_scale, compensate=False,
-               v_out_depth=None, fold=False, want_viewmat=True):
+               v_out_depth=None, fold=False, want_viewmat=True, loss_kind=0, loss_target=None,
+               out_img=None, v_loss=None):
     """The fused render backward (splat_render_bwd). Returns (v_means, v_scales, v_quats (wxyz),
     v_colors, v_opac, v_viewmat or None, v_transforms or None), n rows each with ``fold`` (every
-    gaussian operand shared), else B * n."""
+    gaussian operand shared), else B * n. With loss_kind (the forward's fused loss) the image
+    cotangent comes from out_img (the forward's image), loss_target and the loss cotangent v_loss
+    (a float32 scalar); v_out is then unused (may be None)."""
     means, scales, quats_wxyz, colors, opac, viewmat, background, transforms = map(
         _f32, (means, scales, quats_wxyz, colors, opac, viewmat, background, transforms))
-    v_out = _f32(v_out)
-    vd = None if v_out_depth is None else _f32(v_out_depth)
-    dev = _lib.require_gpu(means, v_out)
     H, W = img_shape
+    if loss_kind:
+        loss_target, out_img = _f32(loss_target), _f32(out_img)
+        v_loss = _f32(v_loss.reshape(()))
+        _check_loss_operands(loss_kind, loss_target, B, H, W, means.device, v_loss)
+        if out_img.shape != loss_target.shape:
+            raise ValueError("render_bwd: the forward's image and the loss target differ in shape")
+        v_out = None
+    else:
+        v_out = _f32(v_out)
+    vd = None if v_out_depth is None else _f32(v_out_depth)
+    dev = _lib.require_gpu(means, *(t for t in (v_out, loss_target) if t is not None))
     rows_out = n if fold else B * n
     e = lambda *shape: torch.empty(shape, device=dev, dtype=torch.float32)  # noqa: E731
     v_means, v_scales, v_quats = e(rows_out, 3), e(rows_out, 3), e(rows_out, 4)
@@ -285,11 +302,26 @@ def render_bwd(means, scales, quats_wxyz, colors, opac, viewmat, background, tra
             int(has_transforms), B, H, W, f[0], f[1], glob_scale, 1, int(compensate),
             p(kept.xys), p(kept.depths), p(kept.radii), p(kept.conics), p(kept.cum), p(ks.ids),
             p(ks.pos), p(ks.bins), p(ks.records), p(ks.order), ks.M, p(final_Ts), p(final_idx),
-            p(v_out), v_out.numel() // (3 * W), p(vd), 0 if vd is None else vd.numel() // W,
-            p(v_means), p(v_scales), p(v_quats), p(v_colors), p(v_opac), p(v_view), p(v_tf),
-            int(fold))
+            p(v_out), 0 if v_out is None else v_out.numel() // (3 * W), p(vd),
+            0 if vd is None else vd.numel() // W, p(v_means), p(v_scales), p(v_quats),
+            p(v_colors), p(v_opac), p(v_view), p(v_tf), int(fold),
+            p(loss_target) if loss_kind else None, int(loss_kind),
+            p(out_img) if loss_kind else None, p(v_loss) if loss_kind else None)
     _lib.check(st, "render_bwd")
     return v_means, v_scales, v_quats, v_colors, v_opac, v_view, v_tf
+
+
+LOSS_L1, LOSS_MSE = 1, 2  # loss_kind of the fused render loss
+
+
+def _check_loss_operands(kind, target, B, H, W, dev, scalar):
+    if kind not in (LOSS_L1, LOSS_MSE):
+        raise ValueError(f"loss_kind must be {LOSS_L1} (L1) or {LOSS_MSE} (MSE), got {kind}")
+    if target is None or target.numel() != B * H * W * 3 or target.device != dev:
+        raise ValueError(f"the loss target must hold {B} x {H} x {W} x 3 values on {dev}")
+    if scalar is None or scalar.numel() != 1 or scalar.dtype != torch.float32 or \
+            scalar.device != dev:
+        raise ValueError(f"the loss value / cotangent must be one float32 on {dev}")
 
 
 def _bwd_outputs(nout, dev, with_depth):

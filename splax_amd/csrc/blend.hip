@@ -319,6 +319,9 @@ struct BlendFwdParams {
     BlendCommon c;
     float* final_Ts; int32_t* final_idx; float* out_img;
     float* out_depth;  // kDepth: expected depth per pixel
+    // fused loss (loss_kind != kLossNone): the tile's sum of (img - target)^2 or |img - target|
+    // over its pixels' colour values into loss_partials[tile_g]
+    int32_t loss_kind; const float* loss_target; double* loss_partials;
 };
 
 // kDepth adds the expected-depth channel of _rasterize_depth_kernel
@@ -402,6 +405,7 @@ __global__ void __launch_bounds__(kTile, 7) blend_fwd_kernel(BlendFwdParams P) {
         }
         if (last_off >= 0) cur_idx = batch_start + (last_off >> 4);
     }
+    double err = 0.0;  // this pixel's part of the fused loss
     if (inside) {
         const int64_t bgi = C.rows_bg > 1 ? image_id : 0;
         const float* bg = C.background + 3 * bgi;
@@ -409,10 +413,27 @@ __global__ void __launch_bounds__(kTile, 7) blend_fwd_kernel(BlendFwdParams P) {
         // final_Ts / final_idx serve the backward only: a forward-only caller may pass neither
         if (P.final_Ts) P.final_Ts[pix] = T;
         if (P.final_idx) P.final_idx[pix] = cur_idx;
-        P.out_img[3 * pix] = o0 + T * bg[0];
-        P.out_img[3 * pix + 1] = o1 + T * bg[1];
-        P.out_img[3 * pix + 2] = o2 + T * bg[2];
+        const float c0 = o0 + T * bg[0], c1 = o1 + T * bg[1], c2 = o2 + T * bg[2];
+        P.out_img[3 * pix] = c0;
+        P.out_img[3 * pix + 1] = c1;
+        P.out_img[3 * pix + 2] = c2;
         if constexpr (kDepth) P.out_depth[pix] = od;
+        if (P.loss_kind != kLossNone) {
+            // each term exact in double ((float)d^2 has at most 48 significant bits)
+            const float* tg = P.loss_target + 3 * pix;
+            const float d0 = c0 - tg[0], d1 = c1 - tg[1], d2 = c2 - tg[2];
+            err = P.loss_kind == kLossMse
+                      ? ((double)d0 * (double)d0 + (double)d1 * (double)d1) + (double)d2 * (double)d2
+                      : ((double)fabsf(d0) + (double)fabsf(d1)) + (double)fabsf(d2);
+        }
+    }
+    if (P.loss_kind != kLossNone) {  // uniform; every lane active again for the DPP sum
+        __shared__ double s_err[kTile / 64];
+        err = wave_sum_f64_to_lane63(err);
+        if ((tid & 63) == 63) s_err[tid >> 6] = err;
+        __syncthreads();
+        if (tid == 0)
+            P.loss_partials[tile_g] = ((s_err[0] + s_err[1]) + s_err[2]) + s_err[3];
     }
 }
 
@@ -532,7 +553,7 @@ static int launch_tile_order(const int32_t* bins, int64_t blocks, int32_t num_ti
 int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,
                      float* out_img, float* out_depth, const float4* recs, int32_t* order,
-                     hipStream_t stream) {
+                     const PixelLoss* loss, hipStream_t stream) {
     const int64_t blocks = (int64_t)in.B_geom * lay.num_tiles;
     if (blocks <= 0) return 0;
     int rc = launch_tile_order(tile_bins, blocks, lay.num_tiles, 1, order, stream);
@@ -543,6 +564,9 @@ int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
     P.c.order = order;
     P.final_Ts = final_Ts; P.final_idx = final_idx; P.out_img = out_img;
     P.out_depth = out_depth;
+    P.loss_kind = loss ? loss->kind : kLossNone;
+    P.loss_target = loss ? loss->target : nullptr;
+    P.loss_partials = loss ? loss->partials : nullptr;
     hipEvent_t ka, kb;  // null unless this kernel is timed
     (void)kernel_timer_events(kKernelBlendFwd, &ka, &kb);
     if (out_depth)
@@ -567,6 +591,10 @@ struct BlendBwdParams {
     const float* v_out_depth; int64_t vdepth_rows;  // kDepth
     float* rgrad;  // [images][M][NG], images = 1 when geometry is batched, else B_out
     uint32_t* dev_err;  // the device error word: kDevErrKeptLists when a kept list is bad
+    // fused loss (loss_kind != kLossNone): the image cotangent of each pixel from the forward's
+    // image, the target and the loss cotangent, as loss_bwd_kernel forms it (v_out unused)
+    int32_t loss_kind; const float* loss_target; const float* loss_img; const float* v_loss;
+    int64_t loss_count;
 };
 
 // Partial sums of one intersection: v_colour (3), v_conic (3), the two sums sum v_sigma * dx,
@@ -667,9 +695,24 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
         // (v_alpha, v_sigma and all sums but the conic's a and c terms) is half the reference's;
         // the batch readout doubles those sums, exactly again. The conic's a and c terms,
         // 0.5 v_sigma dx dx and 0.5 v_sigma dy dy, need no 0.5 factor of their own then.
-        const int64_t vrow = ((int64_t)image_id * C.img_h + i) % P.vout_rows;
-        const float* vo = P.v_out + 3 * (vrow * C.img_w + j);
-        v0 = 0.5f * vo[0]; v1 = 0.5f * vo[1]; v2 = 0.5f * vo[2];
+        if (P.loss_kind != kLossNone) {
+            // v = 2 (img - target) * (g / count) (MSE) or sign(img - target) * (g / count) (L1),
+            // the same float operations as loss_bwd_kernel, then halved as below
+            const int64_t pix = ((int64_t)image_id * C.img_h + i) * C.img_w + j;
+            const float scale = *P.v_loss / (float)P.loss_count;
+            float v[3];
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                const float d = P.loss_img[3 * pix + k] - P.loss_target[3 * pix + k];
+                const float sg = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : d);
+                v[k] = P.loss_kind == kLossMse ? (d + d) * scale : sg * scale;
+            }
+            v0 = 0.5f * v[0]; v1 = 0.5f * v[1]; v2 = 0.5f * v[2];
+        } else {
+            const int64_t vrow = ((int64_t)image_id * C.img_h + i) % P.vout_rows;
+            const float* vo = P.v_out + 3 * (vrow * C.img_w + j);
+            v0 = 0.5f * vo[0]; v1 = 0.5f * vo[1]; v2 = 0.5f * vo[2];
+        }
         const float* bg = C.background + 3 * (C.rows_bg > 1 ? image_id : 0);
         tfbg = t_final * ((bg[0] * v0 + bg[1] * v1) + bg[2] * v2);
         if constexpr (kDepth)
@@ -939,6 +982,8 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
         P.v_out_depth = a.v_out_depth; P.vdepth_rows = a.vdepth_rows;
         P.rgrad = a.rgrad;
         P.dev_err = a.dev_err;
+        P.loss_kind = a.loss.kind; P.loss_target = a.loss.target; P.loss_img = a.loss.img;
+        P.v_loss = a.loss.v_loss; P.loss_count = a.loss.count;
         hipEvent_t ka, kb;  // null unless this kernel is timed
         (void)kernel_timer_events(kKernelBlendBwd, &ka, &kb);
         if (depth)

@@ -257,6 +257,17 @@ int DeviceScratch::ensure_view_partials(int64_t count) {
     return 0;
 }
 
+int DeviceScratch::ensure_loss_partials(int64_t count) {
+    if (count <= loss_partials_cap) return 0;
+    (void)hipDeviceSynchronize();
+    dev_free(&loss_partials);
+    loss_partials_cap = 0;
+    int rc = dev_alloc(&loss_partials, count, false);
+    if (rc) return rc;
+    loss_partials_cap = count;
+    return 0;
+}
+
 int DeviceScratch::ensure_order(int64_t blocks) {
     if (blocks <= order_cap) return 0;
     (void)hipDeviceSynchronize();
@@ -303,6 +314,8 @@ void DeviceScratch::release() {
     order_cap = 0;
     dev_free(&view_partials);
     view_partials_cap = 0;
+    dev_free(&loss_partials);
+    loss_partials_cap = 0;
     dev_free(&part_counts);
     part_counts_cap = 0;
     dev_free(&tile_bins);
@@ -400,7 +413,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 14; }
+int splat_abi_version(void) { return 15; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();
@@ -730,7 +743,8 @@ static RasterInputs raster_inputs(const float* colors, int64_t rows_colors,
 static int rasterize_fwd_core(hipStream_t s, DeviceScratch& sc, const RasterInputs& in,
                               const SortTargets* tgt, float* final_Ts, int32_t* final_idx,
                               float* out_img, float* out_depth, float* records, int32_t* order,
-                              int64_t* num_intersects, bool packed);
+                              int64_t* num_intersects, bool packed,
+                              const PixelLoss* loss = nullptr, float* loss_out = nullptr);
 
 static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortTargets* tgt,
                               float* final_Ts, int32_t* final_idx, float* out_img,
@@ -751,11 +765,13 @@ static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortT
 // The forward with the device's scratch held: sort_and_bin (into tgt's buffers when given), the
 // record pack (skipped when packed: the fused projection wrote them into records) and the blend.
 // With a capacity-bounded tgt the count is settled after the blend's launch (the host waits only
-// there, by when the stream is normally well past the count's copy).
+// there, by when the stream is normally well past the count's copy). loss (may be null): a loss
+// fused into the blend, its value into *loss_out.
 static int rasterize_fwd_core(hipStream_t s, DeviceScratch& sc, const RasterInputs& in,
                               const SortTargets* tgt, float* final_Ts, int32_t* final_idx,
                               float* out_img, float* out_depth, float* records, int32_t* order,
-                              int64_t* num_intersects, bool packed) {
+                              int64_t* num_intersects, bool packed, const PixelLoss* loss,
+                              float* loss_out) {
     int rc = 0;
     {
         const int32_t bpi = (in.n + 4095) / 4096;
@@ -784,11 +800,21 @@ static int rasterize_fwd_core(hipStream_t s, DeviceScratch& sc, const RasterInpu
         if (rc) return rc;
         order = sc.tile_order;
     }
+    const int64_t blocks = (int64_t)in.B_geom * L.num_tiles;
+    PixelLoss lp;
+    if (loss) {
+        rc = sc.ensure_loss_partials(blocks);
+        if (rc) return rc;
+        lp = *loss;
+        lp.partials = sc.loss_partials;
+    }
     StageTimer tm(s, kStageBlendFwd);
     if (M > 0 && !packed) rc = launch_pack_records(in, recs, s);
     if (!rc)
         rc = launch_blend_fwd(in, L, M > 0 ? ids : nullptr, bins, final_Ts, final_idx, out_img,
-                              out_depth, recs, order, s);
+                              out_depth, recs, order, loss ? &lp : nullptr, s);
+    if (!rc && loss)
+        rc = launch_loss_final(lp.partials, blocks, loss->count, loss_out, s);
     if (rc) return fail(rc, "blend_fwd launch failed");
     if (deferred) {
         int64_t count = 0;
@@ -815,9 +841,13 @@ static int check_raster_bwd(const RasterInputs& in, const BlendBwdArgs& args) {
         return fail(kErrArgs, "rasterize_bwd: B_geom must be 1 or equal to B_out");
     if (args.vout_rows <= 0 || !in.cum) return fail(kErrArgs, "rasterize_bwd: empty cotangent");
     // a forward-only render may leave its final buffers out: the backward needs both
-    if (!args.final_Ts || !args.final_idx || !args.v_out)
+    const bool fused_loss = args.loss.kind != kLossNone;
+    if (!args.final_Ts || !args.final_idx || (!args.v_out && !fused_loss))
         return fail(kErrArgs, "rasterize_bwd: final_Ts, final_idx and the image cotangent are "
                               "required");
+    if (fused_loss && (!args.loss.target || !args.loss.img || !args.loss.v_loss))
+        return fail(kErrArgs, "render_bwd: a fused loss needs the target, the forward's image "
+                              "and the loss cotangent");
     if (args.v_depths && (!in.depths || !args.v_out_depth || args.vdepth_rows <= 0))
         return fail(kErrArgs, "rasterize_bwd: depth channel needs depths and v_out_depth");
     if ((int64_t)args.B_out * in.n >= ((int64_t)1 << 31))
@@ -1053,8 +1083,13 @@ int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_m
                      int32_t* cum_tiles_hit, int64_t capacity, int32_t* sorted_ids,
                      int32_t* sorted_pos, int32_t* tile_bins, float* records,
                      int32_t* tile_order, float* final_Ts, int32_t* final_idx, float* out_img,
-                     float* out_depth, int64_t* num_intersects) {
+                     float* out_depth, int64_t* num_intersects, const float* loss_target,
+                     int32_t loss_kind, float* loss) {
     if (B <= 0) return fail(kErrArgs, "render_fwd: invalid sizes");
+    if (loss_kind != kLossNone && loss_kind != kLossL1 && loss_kind != kLossMse)
+        return fail(kErrArgs, "render_fwd: loss_kind must be 0 (none), 1 (L1) or 2 (MSE)");
+    if (loss_kind != kLossNone && (!loss_target || !loss))
+        return fail(kErrArgs, "render_fwd: a fused loss needs the target and the loss output");
     const int64_t total = (int64_t)B * num_gaussians;
     ProjectArgs a;
     int rc = project_fwd_args(means3d, rows_means, scales, rows_scales, quats, rows_quats,
@@ -1120,8 +1155,13 @@ int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_m
         tgt.num_tiles_hit = num_tiles_hit;
         tgt.count_src = count_word;
     }
+    PixelLoss lp;
+    lp.kind = loss_kind;
+    lp.target = loss_target;
+    lp.count = (int64_t)B * img_h * img_w * 3;
     return rasterize_fwd_core(s, sc, in, &tgt, final_Ts, final_idx, out_img, out_depth, records,
-                              tile_order, num_intersects, true);
+                              tile_order, num_intersects, true,
+                              loss_kind != kLossNone ? &lp : nullptr, loss);
 }
 
 int splat_render_bwd(splat_stream_t stream, const float* means3d, int64_t rows_means,
@@ -1141,9 +1181,17 @@ int splat_render_bwd(splat_stream_t stream, const float* means3d, int64_t rows_m
                      const float* v_out_img, int64_t vout_rows, const float* v_out_depth,
                      int64_t vdepth_rows, float* v_means, float* v_scales, float* v_quats,
                      float* v_colors, float* v_opacities, float* v_viewmat,
-                     float* v_transforms, int32_t fold_shared) {
+                     float* v_transforms, int32_t fold_shared, const float* loss_target,
+                     int32_t loss_kind, const float* out_img, const float* v_loss) {
     const int32_t n = num_gaussians;
     if (n <= 0 || B <= 0) return fail(kErrArgs, "render_bwd: invalid sizes");
+    if (loss_kind != kLossNone && loss_kind != kLossL1 && loss_kind != kLossMse)
+        return fail(kErrArgs, "render_bwd: loss_kind must be 0 (none), 1 (L1) or 2 (MSE)");
+    if (loss_kind != kLossNone) {
+        // the image cotangent comes from the fused loss: every output image's rows
+        v_out_img = nullptr;
+        vout_rows = (int64_t)B * img_h;
+    }
     if (!rows_match(rows_means, n, B) || !rows_match(rows_scales, n, B) ||
         !rows_match(rows_quats, n, B) || !rows_match(rows_viewmat, 4, B) ||
         !rows_match(rows_opac, n, B) || !rows_match(rows_colors, n, B))
@@ -1172,6 +1220,11 @@ int splat_render_bwd(splat_stream_t stream, const float* means3d, int64_t rows_m
                                v_opacities, nullptr, nullptr, v_out_depth, vdepth_rows,
                                depth ? const_cast<float*>(v_out_depth) : nullptr);
     ba.fold = fold_shared != 0;
+    ba.loss.kind = loss_kind;
+    ba.loss.target = loss_target;
+    ba.loss.img = out_img;
+    ba.loss.v_loss = v_loss;
+    ba.loss.count = (int64_t)B * img_h * img_w * 3;
     int rc = check_raster_bwd(in, ba);
     if (rc) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);

@@ -88,17 +88,6 @@ __global__ void __launch_bounds__(256) log_params_bwd_kernel(LogParams P) {
 
 constexpr int kL1Chunk = 4096;  // elements per workgroup (16 per thread)
 
-// x plus the double of the lane DPP control kCtrl names (0 where it names none), in two 32-bit
-// halves.
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ double dpp_add_f64(double x) {
-    const int64_t b = __double_as_longlong(x);
-    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, kCtrl, kRowMask, 0xf, false);
-    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), kCtrl, kRowMask, 0xf,
-                                               false);
-    return x + __longlong_as_double((int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
-}
-
 // Workgroup sums of |img - target| (kSquare: (img - target)^2, exact in double) in double, in a
 // fixed order: per thread sequential over its 16 elements, then the wave's 64 sums by DPP row
 // shifts and broadcasts into lane 63, then the four waves in order.
@@ -116,23 +105,30 @@ __global__ void __launch_bounds__(256) loss_partials_kernel(const float* img, co
             acc += kSquare ? (double)d * (double)d : (double)fabsf(d);
         }
     }
-    acc = dpp_add_f64<0x111, 0xf>(acc);  // row_shr:1
-    acc = dpp_add_f64<0x112, 0xf>(acc);  // row_shr:2
-    acc = dpp_add_f64<0x114, 0xf>(acc);  // row_shr:4
-    acc = dpp_add_f64<0x118, 0xf>(acc);  // row_shr:8
-    acc = dpp_add_f64<0x142, 0xa>(acc);  // row_bcast:15 into rows 1 and 3
-    acc = dpp_add_f64<0x143, 0xc>(acc);  // row_bcast:31 into rows 2 and 3
+    acc = wave_sum_f64_to_lane63(acc);
     if ((threadIdx.x & 63) == 63) s[threadIdx.x >> 6] = acc;
     __syncthreads();
     if (threadIdx.x == 0) partials[blockIdx.x] = ((s[0] + s[1]) + s[2]) + s[3];
 }
 
-// One workgroup: the partials in the same fixed order, divided by the count.
+// One workgroup: thread t adds partials t, t + 256, t + 512, ... in that order (loads issued
+// sixteen at a time; the padding adds +0.0 to a sum of non-negative terms, which changes no bit),
+// then a fixed tree over the 256 sums, divided by the count.
+constexpr int kFinalLoads = 16;
 __global__ void __launch_bounds__(256) l1_final_kernel(const double* partials, int64_t blocks,
                                                        int64_t count, float* loss) {
     __shared__ double s[256];
     double acc = 0.0;
-    for (int64_t b = threadIdx.x; b < blocks; b += 256) acc += partials[b];
+    for (int64_t b0 = threadIdx.x; b0 < blocks; b0 += 256 * kFinalLoads) {
+        double v[kFinalLoads];
+#pragma unroll
+        for (int k = 0; k < kFinalLoads; ++k) {
+            const int64_t b = b0 + 256 * k;
+            v[k] = b < blocks ? partials[b] : 0.0;
+        }
+#pragma unroll
+        for (int k = 0; k < kFinalLoads; ++k) acc += v[k];
+    }
     s[threadIdx.x] = acc;
     __syncthreads();
     for (int off = 128; off > 0; off >>= 1) {
@@ -189,6 +185,13 @@ static int loss_bwd(hipStream_t s, const float* img, const float* target, int64_
     hipLaunchKernelGGL(loss_bwd_kernel<kSquare>, dim3((unsigned)blocks), dim3(256), 0, s, img,
                        target, count, v_loss, v_img);
     return glue_launched(name);
+}
+
+int launch_loss_final(const double* partials, int64_t blocks, int64_t count, float* loss,
+                      hipStream_t stream) {
+    hipLaunchKernelGGL(l1_final_kernel, dim3(1), dim3(256), 0, stream, partials, blocks, count,
+                       loss);
+    return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;
 }
 
 }  // namespace splat

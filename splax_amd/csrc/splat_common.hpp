@@ -346,6 +346,27 @@ __device__ __forceinline__ uint32_t wave_minmax_to_lane63(uint32_t x) {
     return x;
 }
 
+// x plus the double of the lane DPP control kCtrl names (0 where it names none), in two 32-bit
+// halves.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ double dpp_add_f64(double x) {
+    const int64_t b = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, kCtrl, kRowMask, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), kCtrl, kRowMask, 0xf,
+                                               false);
+    return x + __longlong_as_double((int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+// Sum of a double over the 64 lanes in a fixed order, valid in lane 63 (every lane active).
+__device__ __forceinline__ double wave_sum_f64_to_lane63(double x) {
+    x = dpp_add_f64<0x111, 0xf>(x);  // row_shr:1
+    x = dpp_add_f64<0x112, 0xf>(x);  // row_shr:2
+    x = dpp_add_f64<0x114, 0xf>(x);  // row_shr:4
+    x = dpp_add_f64<0x118, 0xf>(x);  // row_shr:8
+    x = dpp_add_f64<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+    x = dpp_add_f64<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+    return x;
+}
+
 __device__ __forceinline__ float lane63(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }

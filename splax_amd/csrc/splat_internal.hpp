@@ -129,6 +129,8 @@ struct DeviceScratch {
     int32_t* tile_order = nullptr; int64_t order_cap = 0;
     // projection backward: 12 viewmat-gradient partials per (image, workgroup)
     float* view_partials = nullptr; int64_t view_partials_cap = 0;
+    // fused render loss: one partial sum per blend workgroup (image, tile)
+    double* loss_partials = nullptr; int64_t loss_partials_cap = 0;
     uint32_t* part_counts = nullptr; int64_t part_counts_cap = 0;  // 256 * partitions
     uint32_t* hist = nullptr;                                       // 256 digit totals
     int32_t* tile_bins = nullptr; int64_t bins_cap = 0;             // (start, end) pairs
@@ -153,6 +155,7 @@ struct DeviceScratch {
     int ensure_item_grads(int64_t items);
     int ensure_order(int64_t blocks);
     int ensure_view_partials(int64_t count);
+    int ensure_loss_partials(int64_t count);
     void release();
 };
 
@@ -289,13 +292,33 @@ int settle_count(DeviceScratch& sc, int64_t capacity, int64_t* M_out);
 // Writes the packed blend record (4 float4) of each of the in.B_geom * in.n geometry items.
 int launch_pack_records(const RasterInputs& in, float4* recs, hipStream_t stream);
 
+// A per-pixel loss fused into the blends, the mean over every colour value of the images of
+// |img - target| (kind kLossL1) or (img - target)^2 (kLossMse). The forward blend leaves one
+// double partial sum per workgroup, at its tile's index (image * num_tiles + tile), for
+// launch_loss_final; the backward blend forms the image cotangent of each pixel from the image,
+// the target and the loss cotangent *v_loss as the loss's own backward does (loss_bwd_kernel).
+constexpr int32_t kLossNone = 0, kLossL1 = 1, kLossMse = 2;
+struct PixelLoss {
+    int32_t kind = kLossNone;
+    const float* target = nullptr;  // [images][H][W][3], as the image
+    double* partials = nullptr;     // forward: images * num_tiles
+    const float* img = nullptr;     // backward: the forward's image
+    const float* v_loss = nullptr;  // backward: the loss cotangent (one float, device memory)
+    int64_t count = 0;              // images * H * W * 3 (the mean's divisor)
+};
+
 // out_depth non-null: also the expected-depth channel (in.depths per geometry item). recs holds
 // the records written by launch_pack_records for the same inputs. order (in.B_geom * num_tiles)
-// receives the tile dispatch order the blend runs in.
+// receives the tile dispatch order the blend runs in. loss (may be null): the fused loss's
+// per-tile partials.
 int launch_blend_fwd(const RasterInputs& in, const KeyLayout& lay, const int32_t* sorted_ids,
                      const int32_t* tile_bins, float* final_Ts, int32_t* final_idx,
                      float* out_img, float* out_depth, const float4* recs, int32_t* order,
-                     hipStream_t stream);
+                     const PixelLoss* loss, hipStream_t stream);
+// The fused loss's value: the blocks partials summed in a fixed order, divided by count (the
+// number of colour values), into *loss.
+int launch_loss_final(const double* partials, int64_t blocks, int64_t count, float* loss,
+                      hipStream_t stream);
 
 // Backward over sorted lists of M intersections: sorted_ids / sorted_pos / tile_bins as produced
 // by sort_and_bin; in.cum gives each item's emission range; rgrad is scratch of
@@ -311,6 +334,7 @@ struct BlendBwdArgs {
     const float4* recs = nullptr;  // launch_pack_records output for the same inputs
     int32_t fold = 0;  // v_colors / v_opacity summed over the B_out images (n rows)
     uint32_t* dev_err = nullptr;  // the device's error word (DeviceScratch::tickets)
+    PixelLoss loss;  // kind != kLossNone: the image cotangent from the fused loss, v_out unused
 };
 // order: scratch of B_out * num_tiles for the tile dispatch order; kept_order (may be null) is the
 // order a forward over the same bins wrote, used instead when B_out == in.B_geom.

@@ -4,7 +4,8 @@ One step is the reference trainer's step (scripts/train_lego.py:101-131,217-229)
 gaussian budget with the loss reduced to L1:
   1. ``render_log`` of the log / logit parameters from B cameras in one batched launch, with the
      antialiasing opacity compensation (splax/_render.py:118-168, splax/_project/_project.py:95-117);
-  2. L1 = mean |img - target| and its gradient through the render's custom backward;
+  2. L1 = mean |img - target| and its gradient through the render's custom backward, the loss
+     fused into the blends (``render_log_loss``);
   3. one fused Adam update of the five parameter groups (optax.adam per group,
      scripts/train_lego.py:203-211, exponential decay on the means' learning rate);
   4. one MCMC relocation (splax/mcmc.py:74-131) and the moment reset of the relocated rows
@@ -19,7 +20,7 @@ import numpy as np
 import torch
 
 from splax_amd import _lib, mcmc
-from splax_amd._render import render_log
+from splax_amd._render import render_log_loss
 from splax_amd.optim import Adam, exponential_decay
 from splax_amd.scenes import Scene
 
@@ -122,9 +123,11 @@ class TrainStep:
 
     def loss_and_grads(self) -> tuple[torch.Tensor, dict[str, torch.Tensor]]:
         leaves = [p.requires_grad_(True) for p in self.params.values()]
-        img, _ = render_log(*leaves, viewmat=self.viewmats, background=self.background,
-                            **self.camera)
-        loss = l1_loss(img, self.targets)
+        # the L1 loss fused into the blends (render_log then l1_loss, without the loss's own
+        # passes over the images)
+        loss, _ = render_log_loss(*leaves, target=self.targets, loss="l1",
+                                  viewmat=self.viewmats, background=self.background,
+                                  **self.camera)
         grads = torch.autograd.grad(loss, leaves)
         for p in leaves:
             p.requires_grad_(False)

@@ -447,10 +447,88 @@ def test_render_fwd_cum_is_whole_at_every_capacity():
             p(colors), n, p(bg), 1, p(tf), 1, p(tids), n, 1, 0, 1, H, W, s.f[0], s.f[1],
             s.c[0], s.c[1], 1.0, 0.01, 1, 0, p(xys), p(depths), p(radii), p(conics), p(nth),
             p(cum), cap, p(ids), p(pos), p(bins), p(recs), p(order), p(Ts), p(fidx), p(img),
-            None, ctypes.byref(m))
+            None, ctypes.byref(m), None, 0, None)
         torch.cuda.synchronize()
         assert st == (0 if cap >= M else _lib.ERR_TOO_MANY), (cap, st)
         assert m.value == M
         for label, got, want in (("xys", xys, ref[0]), ("radii", radii, ref[2]),
                                  ("num_tiles_hit", nth, ref[4]), ("cum", cum, ref[5])):
             assert_bit_exact(_np(got), _np(want), f"capacity {cap} {label}")
+
+
+LOSS_CASES = {
+    "cfg2_60k_mse": dict(scene=lambda: make_scene(2, n=60_000), B=1, loss="mse"),
+    "cfg3_20k_B4_mse_pose": dict(scene=lambda: make_scene(3, n=20_000), B=4, loss="mse",
+                                 pose=True),
+    "cfg1_30k_aa_l1": dict(scene=lambda: make_scene(1, n=30_000), B=1, loss="l1",
+                           antialiased=True),
+    "cfg4_20k_B2_aa_l1": dict(scene=lambda: make_scene(4, n=20_000), B=2, loss="l1",
+                              antialiased=True),
+}
+
+
+@pytest.mark.parametrize("name", list(LOSS_CASES))
+def test_render_loss_equals_render_then_loss(name):
+    """render_loss (the pixel loss fused into the blends) against render followed by the
+    library's own loss (splat_mse_loss_* / splat_l1_loss_*): the image bit for bit, the loss
+    value within one float ulp (both are double sums of exact terms, added in another order),
+    and the gradients, scaled by a non-unit loss cotangent, within the bar."""
+    from splax_amd.train import l1_loss, mse_loss
+
+    _case(f"render_loss {name}")
+    cfg = LOSS_CASES[name]
+    s = cfg["scene"]()
+    B, kind = cfg["B"], cfg["loss"]
+    aa, pose = cfg.get("antialiased", False), cfg.get("pose", False)
+    cam = dict(img_shape=s.img_shape, f=s.f, c=s.c, antialiased=aa)
+    vm_np = s.viewmats[:B] if B > 1 else s.viewmats[0]
+    tgt = _t(s.targets[:B] if B > 1 else s.targets[0])
+    g = 2.5  # the loss cotangent
+    outs = []
+    for fused in (True, False):
+        p = {k: _t(v, grad=True) for k, v in (("means", s.means), ("scales", s.scales),
+                                               ("quats", s.quats), ("colors", s.colors),
+                                               ("opac", s.opacities))}
+        vm = _t(vm_np, grad=pose)
+        bg = _t(s.background)
+        if fused:
+            loss, img = splax_amd.render_loss(*p.values(), target=tgt, loss=kind, viewmat=vm,
+                                              background=bg, **cam)
+            assert not img.requires_grad and loss.shape == ()
+        else:
+            img, _ = splax_amd.render(*p.values(), viewmat=vm, background=bg, **cam)
+            loss = (l1_loss if kind == "l1" else mse_loss)(img, tgt)
+        (loss * g).backward()
+        torch.cuda.synchronize()
+        grads = {k: _np(v.grad) for k, v in p.items()}
+        if pose:
+            grads["viewmat"] = _np(vm.grad)
+        outs.append((_np(img), float(loss.item()), grads))
+    (fi, fl, fg), (ui, ul, ug) = outs
+    assert fi.shape == ((B,) if B > 1 else ()) + (*s.img_shape, 3)
+    assert_bit_exact(fi, ui, f"{name}/img")
+    d = fi.astype(np.float32) - _np(tgt)
+    ref = np.float32((np.abs(d) if kind == "l1" else d.astype(np.float64) ** 2)
+                     .astype(np.float64).sum() / d.size)
+    ulp = float(np.spacing(ref))
+    assert abs(fl - ul) <= ulp and abs(fl - float(ref)) <= ulp, (fl, ul, float(ref))
+    for k in ug:
+        _grad_compare(fg[k], ug[k], f"{name}/{k}")
+    # without autograd the fused forward gives the same value
+    with torch.no_grad():
+        p = [_t(v) for v in (s.means, s.scales, s.quats, s.colors, s.opacities)]
+        loss2, img2 = splax_amd.render_loss(*p, target=tgt, loss=kind, viewmat=_t(vm_np),
+                                            background=_t(s.background), **cam)
+    assert float(loss2.item()) == fl
+    assert_bit_exact(_np(img2), fi, f"{name}/img (no grad)")
+
+
+def test_render_loss_validates_its_target():
+    s = make_scene(0, n=500)
+    p = [_t(v) for v in (s.means, s.scales, s.quats, s.colors, s.opacities)]
+    cam = dict(viewmat=_t(s.viewmats[0]), background=_t(s.background), img_shape=s.img_shape,
+               f=s.f)
+    with pytest.raises(ValueError, match="target must be float32 of the image's shape"):
+        splax_amd.render_loss(*p, target=_t(s.targets), **cam)  # (1, H, W, 3) for one image
+    with pytest.raises(ValueError, match="loss must be one of"):
+        splax_amd.render_loss(*p, target=_t(s.targets[0]), loss="huber", **cam)

@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(handle, name), f"{name} declared in include/splat_hip.h but not exported"
     assert set(names) == set(_lib._SIGS), "Python binding and header disagree"
     lib = _lib.lib()
-    assert lib.splat_abi_version() == 14
+    assert lib.splat_abi_version() == 15
     assert isinstance(lib.splat_last_error(), bytes)
 
 
@@ -262,6 +262,40 @@ def test_forward_requires_the_image_output():
     rc = lib.splat_rasterize_fwd(None, buf, n, buf, n, buf, n, buf, 1, buf, buf, buf, buf, buf, n,
                                  1, 16, 16, buf, buf, None, ctypes.byref(m))
     assert rc == _lib.ERR_ARGS and b"missing image output" in lib.splat_last_error()
+
+
+def test_fused_loss_arguments_are_checked():
+    """splat_render_fwd / splat_render_bwd reject an unknown loss kind, and a fused loss without
+    its target, value, image or cotangent, with status 1 before touching the device."""
+    import ctypes
+
+    lib = _lib.lib()
+    lib.splat_last_error.restype = ctypes.c_char_p
+    n, buf = 10, 256
+    m = ctypes.c_int64(0)
+
+    def fwd(kind, target, loss):
+        return lib.splat_render_fwd(None, *([buf, n] * 8), buf, n, 1, 0, 1, 16, 16, 100.0, 100.0,
+                                    8.0, 8.0, 1.0, 0.01, 1, 0, *([buf] * 6), 0, *([buf] * 9),
+                                    ctypes.byref(m), target, kind, loss)
+
+    def bwd(kind, target, img, v_loss):
+        return lib.splat_render_bwd(None, buf, n, buf, n, buf, n, buf, 4, buf, n, buf, n, buf, 1,
+                                    buf, 1, buf, n, 1, 0, 1, 16, 16, 100.0, 100.0, 1.0, 1, 0,
+                                    *([buf] * 10), 0, buf, buf, None, 16, None, 0, *([buf] * 7),
+                                    0, target, kind, img, v_loss)
+
+    for rc in (fwd(3, buf, buf), bwd(3, buf, buf, buf), fwd(-1, buf, buf)):
+        assert rc == _lib.ERR_ARGS and b"loss_kind must be" in lib.splat_last_error()
+    for args in ((None, buf), (buf, None)):
+        assert fwd(2, *args) == _lib.ERR_ARGS, args
+        assert b"fused loss needs" in lib.splat_last_error()
+    for args in ((None, buf, buf), (buf, None, buf), (buf, buf, None)):
+        assert bwd(1, *args) == _lib.ERR_ARGS, args
+        assert b"fused loss needs" in lib.splat_last_error()
+    # without a fused loss the image cotangent is required as before
+    assert bwd(0, None, None, None) == _lib.ERR_ARGS
+    assert b"image cotangent are required" in lib.splat_last_error()
 
 
 def test_opacity_compensation_backward_follows_the_reference_rules():
