@@ -1,7 +1,8 @@
 """Benchmark of the gfx950 render path: fwd and fwd+bwd frames/s on the BASELINE workload.
 
 A step is one forward + backward render of the workload (project -> rasterize -> MSE loss ->
-backward through rasterize and project), with all inputs resident in HBM. The default workload is
+backward through rasterize and project, the loss fused into the blends by
+splax_amd.render_loss), with all inputs resident in HBM. The default workload is
 config 2 (1,000,000 gaussians on 64 planes, one 1920x1080 camera).
 
 The JSON line carries:
