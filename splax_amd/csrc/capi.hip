@@ -100,6 +100,10 @@ int DeviceScratch::ensure_base() {
     if (hipHostMalloc(&h, sizeof(int32_t), hipHostMallocDefault) != hipSuccess)
         return fail(kErrAlloc, "pinned readback allocation failed");
     pinned_count = static_cast<int32_t*>(h);
+    void* hd = nullptr;
+    if (hipHostGetDevicePointer(&hd, h, 0) != hipSuccess || !hd)
+        return fail(kErrAlloc, "pinned readback mapping failed");
+    pinned_count_dev = static_cast<int32_t*>(hd);
     if (hipEventCreateWithFlags(&count_event, hipEventDisableTiming) != hipSuccess)
         return fail(kErrRuntime, "event creation failed");
     int cus = 0;
@@ -330,6 +334,7 @@ void DeviceScratch::release() {
     dev_free(&hist);
     if (pinned_count) (void)hipHostFree(pinned_count);
     pinned_count = nullptr;
+    pinned_count_dev = nullptr;
     if (count_event) (void)hipEventDestroy(count_event);
     count_event = nullptr;
     has_last = false;
@@ -1138,6 +1143,7 @@ int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_m
     // several chunks: the chunk scan writes the count and the emission finalizes cum_tiles_hit
     int32_t* count_word = reinterpret_cast<int32_t*>(sc.tickets + kCountWord);
     f.count_word = chunks > 1 ? count_word : nullptr;
+    f.count_host = chunks > 1 ? sc.pinned_count_dev : nullptr;
     g_last_error.clear();
     {
         StageTimer tm(s, kStageProject);
@@ -1154,6 +1160,7 @@ int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_m
         tgt.chunk_prefix = sc.chunk_sums;
         tgt.num_tiles_hit = num_tiles_hit;
         tgt.count_src = count_word;
+        tgt.count_on_host = true;
     }
     PixelLoss lp;
     lp.kind = loss_kind;

@@ -313,14 +313,16 @@ constexpr int kChunkScanThreads = 1024;
 // Two independent single-workgroup passes between the projection and the sort, in one launch:
 // (1) block 0 (when chunks > 1) turns the chunk totals into exclusive prefixes, which
 //     chunk_offset_kernel (or, on the render path, the emission) then adds to the chunks' items,
-//     and with total_out non-null writes the grand total (the intersection count) there;
+//     and with total_out non-null writes the grand total (the intersection count) there, and
+//     with total_host non-null also into that host-visible word (a system-scope store, so the
+//     host reads it once the kernel's completion is signalled, with no copy launch);
 // (2) with mm non-null, block b < images folds the fused projection's per-chunk depth-range
 //     partials of image b into the image's range of visible items (what minmax_partial_kernel /
 //     minmax_final_kernel give): chunk c holds items [1024 c, 1024 c + 1024), its slot 0 the
 //     image of its first item, slot 1 the next.
 __global__ void __launch_bounds__(kChunkScanThreads)
 chunk_scan_kernel(uint32_t* sums, int64_t chunks, const uint32_t* partial, int32_t n, float* mm,
-                  int64_t images, int32_t* total_out) {
+                  int64_t images, int32_t* total_out, int32_t* total_host) {
     __shared__ uint32_t s_wave[kChunkScanThreads / 64];
     __shared__ uint32_t s_lo[kChunkScanThreads / 64], s_hi[kChunkScanThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -364,6 +366,9 @@ chunk_scan_kernel(uint32_t* sums, int64_t chunks, const uint32_t* partial, int32
         // the last thread's run ends at the grand total (runs past the chunks are empty); int32
         // wrap-around on overflow is kept, as in cum_tiles_hit
         if (total_out && tid == kChunkScanThreads - 1) *total_out = (int32_t)run;
+        if (total_host && tid == kChunkScanThreads - 1)
+            __hip_atomic_store(total_host, (int32_t)run, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
     }
     if (mm != nullptr && (int64_t)blockIdx.x < images) {
         const int64_t image = blockIdx.x;
@@ -829,7 +834,8 @@ int launch_project_fwd_impl(const ProjectArgs& a, uint32_t* chunk_sums, const Fu
         hipLaunchKernelGGL(chunk_scan_kernel, dim3((unsigned)(images > 1 ? images : 1)),
                            dim3(kChunkScanThreads), 0, stream, P.chunk_sums, blocks,
                            f ? f->mm_partial : nullptr, a.n, images > 0 ? f->depth_mm : nullptr,
-                           images, offsets_later ? f->count_word : nullptr);
+                           images, offsets_later ? f->count_word : nullptr,
+                           offsets_later ? f->count_host : nullptr);
     if (blocks > 1 && !offsets_later)
         return launch_chunk_offsets(P.cum_tiles_hit, a.total, P.chunk_sums, stream);
     return hipGetLastError() == hipSuccess ? 0 : kErrLaunch;

@@ -649,8 +649,9 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
     // (settle_count), so the host never stalls the stream between the projection and the blend.
     const bool deferred = !known && tgt && tgt->capacity >= 0;
     const int32_t* count_src = tgt && tgt->count_src ? tgt->count_src : in.cum + (total - 1);
-    if (!known && (hipMemcpyAsync(sc.pinned_count, count_src, sizeof(int32_t),
-                                  hipMemcpyDeviceToHost, stream) != hipSuccess ||
+    const bool on_host = tgt && tgt->count_on_host;  // already stored by its kernel
+    if (!known && ((!on_host && hipMemcpyAsync(sc.pinned_count, count_src, sizeof(int32_t),
+                                               hipMemcpyDeviceToHost, stream) != hipSuccess) ||
                    hipEventRecord(sc.count_event, stream) != hipSuccess))
         return fail(kErrRuntime, "count readback enqueue failed");
     const float* depth_mm = sc.depth_mm;

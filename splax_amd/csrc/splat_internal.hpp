@@ -137,6 +137,7 @@ struct DeviceScratch {
     float* depth_mm = nullptr; int64_t mm_cap = 0;                  // 2 * B
     uint32_t* mm_partial = nullptr; int64_t mm_partial_cap = 0;     // 2 * blocks
     int32_t* pinned_count = nullptr;
+    int32_t* pinned_count_dev = nullptr;  // the device's address of pinned_count
     hipEvent_t count_event = nullptr;
     int64_t last_count = -1;  // the last settled deferred count: the sort's partition shape
     // Calls on one device share these buffers: a call on another stream than the last user's
@@ -228,6 +229,9 @@ struct FusedRecords {
     // projection leaves cum_tiles_hit chunk-local (chunk_sums then hold the chunks' exclusive
     // prefixes): the emission adds them (SortTargets::chunk_prefix)
     int32_t* count_word = nullptr;
+    // non-null (with count_word): the chunk scan also stores the count into this host-visible
+    // word (DeviceScratch::pinned_count_dev), so the readback needs no copy
+    int32_t* count_host = nullptr;
 };
 int launch_project_fwd_fused(const ProjectArgs& a, const FusedRecords& f, DeviceScratch& sc,
                              hipStream_t stream);
@@ -265,6 +269,9 @@ struct SortTargets {
     const uint32_t* chunk_prefix = nullptr;
     const int32_t* num_tiles_hit = nullptr;
     const int32_t* count_src = nullptr;
+    // the kernel that forms count_src also stores it into the pinned readback word
+    // (FusedRecords::count_host): only the readback event is recorded
+    bool count_on_host = false;
 };
 
 // Where sort_and_bin left its results: sorted keys (int32 when packed, uint64 when wide), ids,
