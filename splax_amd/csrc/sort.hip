@@ -642,7 +642,9 @@ int run_sort_and_bin(const RasterInputs& in, DeviceScratch& sc, hipStream_t stre
         return fill_zero_i32(bins, 2 * nbins, stream);
     }
     // The one device-to-host read: the intersection count (skipped when the caller supplies it).
-    // The copy is enqueued first; the depth range launches run while the host waits
+    // The copy is enqueued first (on the render path the chunk scan has already stored the count
+    // into the pinned word, so only the event is recorded); the depth range launches run while
+    // the host waits
     // (splax/_rasterize/_sort/_sort.py:71-96). With a capacity-bounded target the host does not
     // wait here at all: every launch below is sized by the capacity and bounded on the device by
     // the count itself (live_count), and the caller settles the count after its last launch
