@@ -282,9 +282,14 @@ def render_loss(means3d: torch.Tensor, scales: torch.Tensor, quats: torch.Tensor
     if tuple(target.shape) != (*S, H, W, 3) or target.dtype != torch.float32:
         raise ValueError(f"target must be float32 of the image's shape {(*S, H, W, 3)}, got "
                          f"{tuple(target.shape)} {target.dtype}")
-    value, img = _RenderLossFn.apply(*ops[:7], ops[7], tf_ids,
-                                     target.detach().reshape(-1, W, 3).contiguous(), statics,
-                                     _LOSS_KINDS[loss])
+    tgt = target.detach().reshape(-1, W, 3).contiguous()
+    if torch.is_grad_enabled() and any(t.requires_grad for t in ops):
+        value, img = _RenderLossFn.apply(*ops[:7], ops[7], tf_ids, tgt, statics,
+                                         _LOSS_KINDS[loss])
+    else:  # no backward can follow: the forward alone, keeping no emission positions
+        value = torch.empty((), device=means3d.device, dtype=torch.float32)
+        img = _fused_forward(*ops, tf_ids, statics, backward=False,
+                             loss=(_LOSS_KINDS[loss], tgt, value))[0]
     return value, img.reshape(*S, H, W, 3)
 
 

@@ -919,6 +919,13 @@ static int rasterize_bwd_core(hipStream_t s, DeviceScratch& sc, const RasterInpu
         recs = sc.recs;
     }
     a.recs = recs;
+    if (M == 1) {
+        // a lone intersection's bin stays [0, 0) (the reference's bin-edge rule): no blend
+        // workgroup visits it, so its partial sums are zero rather than what the slot last held
+        rc = fill_zero_i32(reinterpret_cast<int32_t*>(a.rgrad), images * (a.v_depths ? 10 : 9),
+                           s);
+        if (rc) return rc;
+    }
     rc = launch_blend_bwd(in, L, M > 0 ? ids : nullptr, bins, a, sc.tile_order,
                           kept ? kept->order : nullptr, s);
     if (rc) return fail(rc, "blend_bwd launch failed");

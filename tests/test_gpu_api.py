@@ -338,12 +338,24 @@ def test_empty_and_single_intersection():
     np.testing.assert_array_equal(_np(img), np.broadcast_to(bg, (H, W, 3)))
     img.sum().backward()
     assert (_np(mt.grad) == 0).all() and (_np(p["colors"].grad) == 0).all()
-    # one small gaussian in one tile: the lone bin stays [0, 0) and nothing is drawn
-    img1, _ = splax_amd.render(_t(np.array([[0.0, 0.0, 4.0]], np.float32)), p["scales"],
-                               p["quats"], p["colors"], p["opac"],
+    # one small gaussian in one tile: the lone bin stays [0, 0), nothing is drawn and no
+    # gradient flows (the blend never visits the intersection, whose partial sums are zeroed
+    # rather than read from whatever the scratch held); a large render first leaves the
+    # gradient scratch non-zero
+    big = random_scene(3000, 64, 64, seed=12)
+    bp = [_t(big[k], grad=True) for k in ("means", "scales", "quats", "colors", "opac")]
+    splax_amd.render(*bp, viewmat=_t(big["vm"]), background=_t(big["bg"]), img_shape=(64, 64),
+                     f=big["f"], c=big["c"])[0].sum().backward()
+    for k in p:
+        p[k].grad = None
+    m1 = _t(np.array([[0.0, 0.0, 4.0]], np.float32), grad=True)
+    img1, _ = splax_amd.render(m1, p["scales"], p["quats"], p["colors"], p["opac"],
                                viewmat=_t(np.eye(4, dtype=np.float32)), background=_t(bg),
                                img_shape=(H, W), f=(40.0, 40.0), c=(40.0, 40.0))
     np.testing.assert_array_equal(_np(img1), np.broadcast_to(bg, (H, W, 3)))
+    img1.sum().backward()
+    for g in (m1.grad, *(v.grad for v in p.values())):
+        assert g is not None and (_np(g) == 0).all()
 
 
 def test_render_depth_and_grads_match_oracle():

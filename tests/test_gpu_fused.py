@@ -532,3 +532,32 @@ def test_render_loss_validates_its_target():
         splax_amd.render_loss(*p, target=_t(s.targets), **cam)  # (1, H, W, 3) for one image
     with pytest.raises(ValueError, match="loss must be one of"):
         splax_amd.render_loss(*p, target=_t(s.targets[0]), loss="huber", **cam)
+
+
+def test_render_loss_with_no_intersections():
+    """M == 0 (the only gaussian behind the camera; and, second, one small gaussian whose lone
+    tile bin stays empty): every pixel is the background, so the fused loss is the mean of
+    |bg - target| or (bg - target)^2 over the image, and every gradient is exactly zero."""
+    _case("render_loss M == 0")
+    H = W = 48
+    bg = np.array([0.2, 0.4, 0.6], np.float32)
+    tgt = np.random.default_rng(4).uniform(size=(H, W, 3)).astype(np.float32)
+    ones = dict(scales=np.full((1, 3), 0.02, np.float32),
+                quats=np.array([[1.0, 0, 0, 0]], np.float32),
+                colors=np.array([[1.0, 0, 0]], np.float32), opac=np.array([[0.9]], np.float32))
+    for means, c in ((np.array([[0.0, 0.0, -3.0]], np.float32), None),
+                     (np.array([[0.0, 0.0, 4.0]], np.float32), (40.0, 40.0))):
+        for kind in ("mse", "l1"):
+            p = {k: _t(v, grad=True) for k, v in ones.items()}
+            mt = _t(means, grad=True)
+            loss, img = splax_amd.render_loss(
+                mt, p["scales"], p["quats"], p["colors"], p["opac"], target=_t(tgt), loss=kind,
+                viewmat=_t(np.eye(4, dtype=np.float32)), background=_t(bg), img_shape=(H, W),
+                f=(40.0, 40.0), c=c)
+            np.testing.assert_array_equal(_np(img), np.broadcast_to(bg, (H, W, 3)))
+            d = (np.broadcast_to(bg, (H, W, 3)) - tgt).astype(np.float64)
+            ref = np.float32((d * d if kind == "mse" else np.abs(d)).sum() / d.size)
+            assert abs(float(loss.item()) - float(ref)) <= float(np.spacing(ref))
+            loss.backward()
+            for g in (mt.grad, *(v.grad for v in p.values())):
+                assert g is not None and (_np(g) == 0).all()
