@@ -453,3 +453,21 @@ def test_wide_keys_batch_equals_stack_bit_exact():
         _lib.set_wide_keys(False)
     for b in range(3):
         assert_bit_exact(_np(bimg[b]), _np(singles[b]), f"wide batch/img[{b}]")
+
+
+def test_principal_point_defaults_to_center():
+    """Omitting c equals passing the image centre (W / 2, H / 2) bit for bit, through render and
+    render_loss (the reference's tests/test_warp_rasterize.py:198-205)."""
+    _case("principal point default")
+    sc = random_scene(10_000, 256, 192, seed=42)
+    H, W = sc["img_shape"]
+    args = [_t(sc[k]) for k in ("means", "scales", "quats", "colors", "opac")]
+    kw = dict(viewmat=_t(sc["vm"]), background=_t(sc["bg"]), img_shape=(H, W), f=sc["f"])
+    explicit = _np(splax_amd.render(*args, c=(W / 2, H / 2), **kw)[0])
+    defaulted = _np(splax_amd.render(*args, **kw)[0])
+    assert_bit_exact(defaulted, explicit, "render image")
+    tgt = _t(np.zeros((H, W, 3), np.float32))
+    le, ie = splax_amd.render_loss(*args, target=tgt, c=(W / 2, H / 2), **kw)
+    ld, idf = splax_amd.render_loss(*args, target=tgt, **kw)
+    assert_bit_exact(_np(idf), _np(ie), "render_loss image")
+    assert float(ld.item()) == float(le.item())
