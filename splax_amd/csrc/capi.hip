@@ -813,13 +813,15 @@ static int rasterize_fwd_core(hipStream_t s, DeviceScratch& sc, const RasterInpu
         lp = *loss;
         lp.partials = sc.loss_partials;
     }
-    StageTimer tm(s, kStageBlendFwd);
-    if (M > 0 && !packed) rc = launch_pack_records(in, recs, s);
-    if (!rc)
-        rc = launch_blend_fwd(in, L, M > 0 ? ids : nullptr, bins, final_Ts, final_idx, out_img,
-                              out_depth, recs, order, loss ? &lp : nullptr, s);
-    if (!rc && loss)
-        rc = launch_loss_final(lp.partials, blocks, loss->count, loss_out, s);
+    {
+        StageTimer tm(s, kStageBlendFwd);
+        if (M > 0 && !packed) rc = launch_pack_records(in, recs, s);
+        if (!rc)
+            rc = launch_blend_fwd(in, L, M > 0 ? ids : nullptr, bins, final_Ts, final_idx,
+                                  out_img, out_depth, recs, order, loss ? &lp : nullptr, s);
+    }
+    // the loss's final sum is not part of the blend stage's timing
+    if (!rc && loss) rc = launch_loss_final(lp.partials, blocks, loss->count, loss_out, s);
     if (rc) return fail(rc, "blend_fwd launch failed");
     if (deferred) {
         int64_t count = 0;
