@@ -220,8 +220,8 @@ def render_fwd(means, scales, quats_wxyz, colors, opac, viewmat, background, tra
     H, W = img_shape
     total = B * n
     if loss_kind:
-        loss_target = _f32(loss_target)
         _check_loss_operands(loss_kind, loss_target, B, H, W, dev, loss_out)
+        loss_target = _f32(loss_target)
     tiles = ((W + 15) // 16) * ((H + 15) // 16)
     e = lambda *shape, dt=torch.float32: torch.empty(shape, device=dev, dtype=dt)  # noqa: E731
     xys, depths, conics = e(total, 2), e(total), e(total, 3)
@@ -275,11 +275,11 @@ def render_bwd(means, scales, quats_wxyz, colors, opac, viewmat, background, tra
         _f32, (means, scales, quats_wxyz, colors, opac, viewmat, background, transforms))
     H, W = img_shape
     if loss_kind:
-        loss_target, out_img = _f32(loss_target), _f32(out_img)
-        v_loss = _f32(v_loss.reshape(()))
         _check_loss_operands(loss_kind, loss_target, B, H, W, means.device, v_loss)
-        if out_img.shape != loss_target.shape:
-            raise ValueError("render_bwd: the forward's image and the loss target differ in shape")
+        if out_img is None or out_img.shape != loss_target.shape:
+            raise ValueError("render_bwd: a fused loss needs the forward's image, of the "
+                             "target's shape")
+        loss_target, out_img, v_loss = _f32(loss_target), _f32(out_img), _f32(v_loss.reshape(()))
         v_out = None
     else:
         v_out = _f32(v_out)
@@ -317,8 +317,9 @@ LOSS_L1, LOSS_MSE = 1, 2  # loss_kind of the fused render loss
 def _check_loss_operands(kind, target, B, H, W, dev, scalar):
     if kind not in (LOSS_L1, LOSS_MSE):
         raise ValueError(f"loss_kind must be {LOSS_L1} (L1) or {LOSS_MSE} (MSE), got {kind}")
-    if target is None or target.numel() != B * H * W * 3 or target.device != dev:
-        raise ValueError(f"the loss target must hold {B} x {H} x {W} x 3 values on {dev}")
+    if target is None or target.numel() != B * H * W * 3 or target.device != dev or \
+            target.dtype != torch.float32:
+        raise ValueError(f"the loss target must hold {B} x {H} x {W} x 3 float32 values on {dev}")
     if scalar is None or scalar.numel() != 1 or scalar.dtype != torch.float32 or \
             scalar.device != dev:
         raise ValueError(f"the loss value / cotangent must be one float32 on {dev}")

@@ -329,3 +329,29 @@ def test_opacity_compensation_backward_follows_the_reference_rules():
     np.testing.assert_allclose(o_t.grad.numpy(), v_o, rtol=1e-6, atol=0)
     fin = ~np.isnan(v_c)
     np.testing.assert_allclose(g_c[fin], v_c[fin], rtol=1e-5, atol=1e-7)
+
+
+def test_fused_loss_operands_are_validated_on_the_host():
+    """The fused render loss's operands are checked before any library call: the loss kind, the
+    target's size, dtype and device, and the loss value / cotangent scalar."""
+    from splax_amd import _ops
+
+    cpu = torch.device("cpu")
+    ok = dict(target=torch.zeros(48), scalar=torch.zeros(()))
+    _ops._check_loss_operands(_ops.LOSS_MSE, ok["target"], 1, 4, 4, cpu, ok["scalar"])
+    bad = [
+        (3, ok["target"], ok["scalar"], "loss_kind must be"),
+        (_ops.LOSS_L1, None, ok["scalar"], "loss target must hold"),
+        (_ops.LOSS_L1, torch.zeros(47), ok["scalar"], "loss target must hold"),
+        (_ops.LOSS_L1, torch.zeros(48, dtype=torch.float64), ok["scalar"], "loss target"),
+        (_ops.LOSS_MSE, ok["target"], None, "one float32"),
+        (_ops.LOSS_MSE, ok["target"], torch.zeros(2), "one float32"),
+    ]
+    for kind, target, scalar, msg in bad:
+        with pytest.raises(ValueError, match=msg):
+            _ops._check_loss_operands(kind, target, 1, 4, 4, cpu, scalar)
+    with pytest.raises(ValueError, match="loss must be one of"):
+        x = torch.zeros((4, 3))
+        splax_amd.render_loss(x, x, torch.zeros(4, 4), x, torch.ones(4, 1), target=x,
+                              loss="l2", viewmat=torch.eye(4), background=torch.zeros(3),
+                              img_shape=(16, 16), f=(10.0, 10.0))
