@@ -561,3 +561,34 @@ def test_render_loss_with_no_intersections():
             loss.backward()
             for g in (mt.grad, *(v.grad for v in p.values())):
                 assert g is not None and (_np(g) == 0).all()
+
+
+def test_render_log_loss_equals_render_log_then_l1():
+    """render_log_loss (the training step's call: parameter map, antialiased render and L1 fused
+    into the blends) against render_log followed by the library's L1 loss, over a batch of two
+    cameras: image bit for bit, loss within one float ulp, gradients of the log / logit
+    parameters within the bar."""
+    from splax_amd.train import l1_loss, params_from_scene
+
+    _case("render_log_loss")
+    s = make_scene(4, n=20_000)
+    B = 2
+    tgt = _t(s.targets[:B])
+    kw = dict(viewmat=_t(s.viewmats[:B]), background=_t(s.background), img_shape=s.img_shape,
+              f=s.f, c=s.c, antialiased=True)
+    outs = []
+    for fused in (True, False):
+        params = {k: v.clone().requires_grad_(True) for k, v in params_from_scene(s).items()}
+        if fused:
+            loss, img = splax_amd.render_log_loss(*params.values(), target=tgt, loss="l1", **kw)
+        else:
+            img, _ = splax_amd.render_log(*params.values(), **kw)
+            loss = l1_loss(img, tgt)
+        loss.backward()
+        torch.cuda.synchronize()
+        outs.append((_np(img), float(loss.item()), {k: _np(v.grad) for k, v in params.items()}))
+    (fi, fl, fg), (ui, ul, ug) = outs
+    assert_bit_exact(fi, ui, "img")
+    assert abs(fl - ul) <= float(np.spacing(np.float32(ul))), (fl, ul)
+    for k in ug:
+        _grad_compare(fg[k], ug[k], f"log/{k}")
