@@ -143,3 +143,36 @@ def test_partly_batched_geometry_is_tiled():
                           rep(radii, 1), rep(conics, 3), np.cumsum(nth_t).astype(np.int32),
                           n=N, B=2 * B, img_shape=KW["img_shape"])[0]
     assert_bit_exact(_np(out).reshape(ref.shape), ref, "tiled geometry vs oracle")
+
+
+def test_nested_render_loss_equals_render_then_loss():
+    """render_loss over a nested batch (A splats on the outer axis x B viewmats on the inner one,
+    folded into one launch) against render over the same batch followed by the library's MSE:
+    the target's (A, B) images line up with the folded images, so the image, the loss and the
+    gradients agree (image bit for bit, loss within one ulp, gradients within the bar)."""
+    from splax_amd.train import mse_loss
+
+    _case("nested render_loss 3 x 3")
+    scenes = [_splat(s) for s in (7, 8, 9)]
+    A, B = len(scenes), VIEWS.shape[0]
+    tgt = _t(np.random.default_rng(11).uniform(size=(A, B, H, W, 3)).astype(np.float32))
+    outs = []
+    for fused in (True, False):
+        stacked = [torch.stack([sc[i] for sc in scenes])[:, None].clone().requires_grad_(True)
+                   for i in range(5)]  # (A, 1, N, .)
+        kw = dict(viewmat=_t(VIEWS), background=_t(BG), **KW)
+        if fused:
+            loss, img = splax_amd.render_loss(*stacked, target=tgt, loss="mse", **kw)
+        else:
+            img = splax_amd.render(*stacked, **kw)[0]
+            loss = mse_loss(img, tgt)
+        loss.backward()
+        torch.cuda.synchronize()
+        outs.append((_np(img), float(loss.item()), [_np(t.grad) for t in stacked]))
+    (fi, fl, fg), (ui, ul, ug) = outs
+    assert fi.shape == (A, B, H, W, 3)
+    assert_bit_exact(fi, ui, "nested image")
+    assert abs(fl - ul) <= float(np.spacing(np.float32(ul))), (fl, ul)
+    for k, (a, b) in enumerate(zip(fg, ug)):
+        r = rel_fro(a.astype(np.float64), b.astype(np.float64))
+        assert r < 1e-5, f"gradient {k}: {r:.2e}"
