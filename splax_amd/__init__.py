@@ -10,7 +10,7 @@ loaded by ``splax_amd._lib``).
 __version__ = "0.1.0"
 
 from splax_amd import utils
-from splax_amd._lib import clear_cache
+from splax_amd._ops import clear_cache
 from splax_amd._project import opacity_compensation, project, transform_ids
 from splax_amd._rasterize import rasterize, rasterize_depth
 from splax_amd._render import render, render_log, render_log_loss, render_loss

@@ -36,6 +36,16 @@ def batch_shape(named: dict[str, tuple[torch.Tensor | None, int]]) -> tuple[int,
                          ", ".join(f"{n}{lead}" for n, lead in leads)) from e
 
 
+def shared_background(background: torch.Tensor) -> torch.Tensor:
+    """A background whose leading dims are all of size 1 as one shared (3,) colour: the
+    reference reshapes its background to (1, 3) inside rasterize
+    (splax/_rasterize/_rasterize.py:131), so a (1, 3) background renders an unbatched image, and
+    such size-1 dims are no batch axes."""
+    if background.ndim > 1 and math.prod(background.shape[:-1]) == 1:
+        return background.reshape(background.shape[-1])
+    return background
+
+
 def fold(t: torch.Tensor | None, base: int, shape: tuple[int, ...],
          expand_shared: bool = False) -> torch.Tensor | None:
     """``t`` with its leading dims folded into one flat axis of prod(shape) rows, outer axis

@@ -78,6 +78,9 @@ _SIGS = {
 STAGES = ("project", "minmax", "emit", "sort", "bins", "blend_fwd", "blend_bwd", "project_bwd",
           "blend_fwd_kernel", "blend_bwd_kernel")
 
+# splat_abi_version() of the library this binding was written for (include/splat_hip.h)
+ABI_VERSION = 15
+
 # status codes (splax_amd/csrc/splat_internal.hpp)
 ERR_ARGS, ERR_KEY_OVERFLOW, ERR_TOO_MANY = 1, 2, 6
 
@@ -104,6 +107,11 @@ def lib() -> ctypes.CDLL:
                 fn.restype = ctypes.c_int
             handle.splat_last_error.restype = ctypes.c_char_p
             handle.splat_clear_cache.restype = None
+            version = handle.splat_abi_version()
+            if version != ABI_VERSION:
+                raise ImportError(
+                    f"{LIB_PATH} has ABI version {version}, this binding expects "
+                    f"{ABI_VERSION}: rebuild it with `python -m splax_amd._build`")
             _lib = handle
     return _lib
 

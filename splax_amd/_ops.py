@@ -127,7 +127,27 @@ def rasterize_fwd(colors, opac, map_opac, background, xys, depths, radii, conics
     return img, Ts, fidx, int(m.value)
 
 
-_KEEP_CAPACITY: dict = {}  # per device: capacity estimate for the kept sorted lists
+# Per device: the capacity estimate for the kept sorted lists (1.25x the largest count seen) and
+# the workload signature (B, n, tiles per image) it was seen on. A call with another signature
+# starts again from no estimate, as the library drops its own scratch then (the reference drops
+# its scratch entry on a signature change, splax/_cache.py:61-75); clear_cache() forgets both.
+_KEEP_CAPACITY: dict = {}
+_KEEP_SIG: dict = {}
+
+
+def _keep_capacity(key: str, sig: tuple) -> int:
+    if _KEEP_SIG.get(key) != sig:
+        _KEEP_SIG[key] = sig
+        _KEEP_CAPACITY[key] = 0
+    return _KEEP_CAPACITY.get(key, 0)
+
+
+def clear_cache() -> None:
+    """Release the library's persistent per-device scratch and forget the kept-list capacity
+    estimates (splax/_cache.py:158-164)."""
+    _KEEP_CAPACITY.clear()
+    _KEEP_SIG.clear()
+    _lib.clear_cache()
 
 
 class KeptSort(NamedTuple):
@@ -167,7 +187,7 @@ def rasterize_fwd_keep(colors, opac, map_opac, background, xys, depths, radii, c
     recs = torch.empty((xys.shape[0], 16), device=dev, dtype=torch.float32)
     order = torch.empty((B * tiles,), device=dev, dtype=torch.int32)
     key = str(dev)
-    cap = _KEEP_CAPACITY.get(key, 0)
+    cap = _keep_capacity(key, (B, n, tiles))
     m = ctypes.c_int64(0)
     p = _lib.ptr
     for _ in range(2):
@@ -231,7 +251,7 @@ def render_fwd(means, scales, quats_wxyz, colors, opac, viewmat, background, tra
     depth = e(B * H, W) if render_depth else None
     bins, recs, order = e(B * tiles, 2, dt=torch.int32), e(total, 16), e(B * tiles, dt=torch.int32)
     key = str(dev)
-    cap = _KEEP_CAPACITY.get(key, 0)
+    cap = _keep_capacity(key, (B, n, tiles))
     m = ctypes.c_int64(0)
     p = _lib.ptr
     for _ in range(2):

@@ -14,7 +14,7 @@ import math
 import torch
 
 from splax_amd import _ops
-from splax_amd._batching import batch_shape, fold
+from splax_amd._batching import batch_shape, fold, shared_background
 
 
 def key_layout(B: int, H: int, W: int) -> dict:
@@ -112,6 +112,7 @@ def _rasterize_checked(colors, opacities, background, xys, depths, radii, conics
     per_g = lambda t: t.reshape(*t.shape[:-2], n) if t.ndim >= 2 and t.shape[-1] == 1 \
         and t.shape[-2] == n else t  # noqa: E731 ((..., N, 1) -> (..., N))
     opacities, map_opacities = per_g(opacities), per_g(map_opacities)
+    background = shared_background(background)
     glead = tuple(xys.shape[:-2])
     G = math.prod(glead)
     if (depths.numel() != G * n or radii.numel() != G * n or cum_tiles_hit.numel() != G * n

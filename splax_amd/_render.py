@@ -14,7 +14,7 @@ import torch
 import math
 
 from splax_amd import _lib, _ops
-from splax_amd._batching import batch_shape, fold
+from splax_amd._batching import batch_shape, fold, shared_background
 from splax_amd._project import _no_transforms, transform_ids
 from splax_amd._rasterize import check_key_fits
 
@@ -217,6 +217,7 @@ def _prepare(means3d, scales, quats, colors, opacities, viewmat, background, img
     per_g = lambda t: t.reshape(*t.shape[:-2], n) if t.ndim >= 2 and t.shape[-1] == 1 \
         and t.shape[-2] == n else t  # noqa: E731 ((..., N, 1) -> (..., N))
     opacities = per_g(opacities)
+    background = shared_background(background)
     # every operand's leading axes broadcast to one batch shape, folded into one flat batch
     # (the nested vmap of splax/_batching.py); the batch folds into one launch
     S = batch_shape(dict(means=(means3d, 2), scales=(scales, 2), quats=(quats, 2),

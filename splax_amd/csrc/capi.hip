@@ -297,8 +297,18 @@ static int ensure_minmax_partials(DeviceScratch& sc, int64_t count) {
     return 0;
 }
 
-void DeviceScratch::release() {
-    if (!tickets && !keys[0] && !tile_bins) return;
+// A new workload signature drops every workload-sized buffer before the call grows what it
+// needs, so a large render's buffers do not outlive it (the reference drops its whole scratch
+// entry on a signature change, splax/_cache.py:61-75). The base buffers stay.
+void DeviceScratch::workload(int32_t B, int32_t n, int32_t num_tiles) {
+    if (B == sig_B && n == sig_n && num_tiles == sig_tiles) return;
+    if (sig_B >= 0) release_sized();
+    sig_B = B;
+    sig_n = n;
+    sig_tiles = num_tiles;
+}
+
+void DeviceScratch::release_sized() {
     (void)hipDeviceSynchronize();
     for (int k = 0; k < 2; ++k) {
         dev_free(&keys[k]);
@@ -330,6 +340,13 @@ void DeviceScratch::release() {
     mm_partial_cap = 0;
     dev_free(&chunk_sums);
     chunk_sums_cap = 0;
+    last_count = -1;
+}
+
+void DeviceScratch::release() {
+    if (!tickets && !keys[0] && !tile_bins) return;
+    release_sized();
+    sig_B = sig_n = sig_tiles = -1;
     dev_free(&tickets);
     dev_free(&hist);
     if (pinned_count) (void)hipHostFree(pinned_count);
@@ -501,6 +518,9 @@ static int project_fwd_args(const float* means3d, int64_t rows_means, const floa
                               "num_transforms / B * num_transforms)");
     if (total >= ((int64_t)1 << 31))
         return fail(kErrArgs, "project_fwd: more than 2^31 items");
+    if (total > 0 && (!means3d || !scales || !quats || !viewmat || !opacities || !xys ||
+                      !depths || !radii || !conics || !num_tiles_hit || !cum_tiles_hit))
+        return fail(kErrArgs, "project_fwd: missing input or output buffer");
     // xys rows are stored as one 8-byte vector each
     if ((uintptr_t)xys & 7) return fail(kErrArgs, "project_fwd: xys must be 8-byte aligned");
     ProjectArgs& a = *out;
@@ -611,6 +631,9 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
         return fail(kErrArgs, "project_bwd: transforms requested but not given");
     if ((int64_t)B * num_gaussians >= ((int64_t)1 << 31))
         return fail(kErrArgs, "project_bwd: more than 2^31 items");
+    if (!means3d || !scales || !quats || !viewmat || !radii || !conics || !v_xy || !v_conic ||
+        !v_mean3d || !v_scale || !v_quat)
+        return fail(kErrArgs, "project_bwd: missing input or output buffer");
     if (fold_shared && (rows_means != num_gaussians || rows_scales != num_gaussians ||
                         rows_quats != num_gaussians))
         return fail(kErrArgs, "project_bwd: folding needs shared means, scales and quats");
@@ -649,7 +672,8 @@ int splat_project_bwd(splat_stream_t stream, const float* means3d, int64_t rows_
     return rc;
 }
 
-static int check_raster(const RasterInputs& in, int32_t B_out) {
+// blend: the call blends (colours, opacities and background are read), not only sorts.
+static int check_raster(const RasterInputs& in, int32_t B_out, bool blend = true) {
     if (in.n <= 0 || in.B_geom <= 0 || in.img_h <= 0 || in.img_w <= 0)
         return fail(kErrArgs, "rasterize: invalid sizes");
     // xys rows are read as one 8-byte vector each
@@ -662,6 +686,9 @@ static int check_raster(const RasterInputs& in, int32_t B_out) {
         return fail(kErrArgs, "rasterize: background needs 1 or B rows");
     if ((int64_t)in.B_geom * in.n >= ((int64_t)1 << 31))
         return fail(kErrArgs, "rasterize: more than 2^31 items");
+    if (!in.map_opac || !in.xys || !in.conics || !in.cum ||
+        (blend && (!in.colors || !in.opac || !in.background)))
+        return fail(kErrArgs, "rasterize: missing input buffer");
     return 0;
 }
 
@@ -684,13 +711,16 @@ int splat_sort_and_bin(splat_stream_t stream, const float* xys, const float* dep
     in.xys = xys; in.depths = depths; in.radii = radii; in.conics = conics;
     in.cum = cum_tiles_hit; in.n = num_gaussians; in.B_geom = B;
     in.img_h = img_h; in.img_w = img_w;
-    int rc = check_raster(in, B);
+    int rc = check_raster(in, B, false);
     if (rc) return rc;
+    if (!depths || !radii || !tile_bins || (capacity > 0 && (!sorted_keys || !sorted_ids)))
+        return fail(kErrArgs, "sort_and_bin: missing input or output buffer");
     hipStream_t s = static_cast<hipStream_t>(stream);
     DeviceScratch& sc = scratch_for_current_device();
     ScratchUse use(sc, s);
     rc = use.rc;
     if (!rc) {
+        sc.workload(B, num_gaussians, key_layout(B, img_h, img_w).num_tiles);
         const int32_t bpi = (num_gaussians + 4095) / 4096;
         rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * B);
     }
@@ -758,7 +788,7 @@ static int rasterize_fwd_impl(hipStream_t s, const RasterInputs& in, const SortT
     int rc = check_raster(in, in.B_geom);
     if (rc) return rc;
     if (!out_img) return fail(kErrArgs, "rasterize: missing image output");
-    if (out_depth && !in.depths) return fail(kErrArgs, "rasterize: depth channel needs depths");
+    if (!in.depths || !in.radii) return fail(kErrArgs, "rasterize: missing input buffer");
     DeviceScratch& sc = scratch_for_current_device();
     ScratchUse use(sc, s);
     rc = use.rc;
@@ -778,6 +808,7 @@ static int rasterize_fwd_core(hipStream_t s, DeviceScratch& sc, const RasterInpu
                               int64_t* num_intersects, bool packed, const PixelLoss* loss,
                               float* loss_out) {
     int rc = 0;
+    sc.workload(in.B_geom, in.n, key_layout(in.B_geom, in.img_h, in.img_w).num_tiles);
     {
         const int32_t bpi = (in.n + 4095) / 4096;
         rc = ensure_minmax_partials(sc, 2 * (int64_t)bpi * in.B_geom);
@@ -859,6 +890,8 @@ static int check_raster_bwd(const RasterInputs& in, const BlendBwdArgs& args) {
         return fail(kErrArgs, "rasterize_bwd: depth channel needs depths and v_out_depth");
     if ((int64_t)args.B_out * in.n >= ((int64_t)1 << 31))
         return fail(kErrArgs, "rasterize_bwd: more than 2^31 gradient rows");
+    if (!args.v_colors || !args.v_opacity)
+        return fail(kErrArgs, "rasterize_bwd: missing gradient output");
     return 0;
 }
 
@@ -869,6 +902,8 @@ static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptL
                               const BlendBwdArgs& args) {
     int rc = check_raster_bwd(in, args);
     if (rc) return rc;
+    if (!args.v_xy || !args.v_conic)
+        return fail(kErrArgs, "rasterize_bwd: missing gradient output");
     DeviceScratch& sc = scratch_for_current_device();
     ScratchUse use(sc, s);
     rc = use.rc;
@@ -880,6 +915,7 @@ static int rasterize_bwd_impl(hipStream_t s, const RasterInputs& in, const KeptL
 static int rasterize_bwd_core(hipStream_t s, DeviceScratch& sc, const RasterInputs& in,
                               const KeptLists* kept, const BlendBwdArgs& args) {
     int rc = 0;
+    sc.workload(in.B_geom, in.n, key_layout(in.B_geom, in.img_h, in.img_w).num_tiles);
     KeyLayout L;
     const int32_t* ids = nullptr;
     const int32_t* pos = nullptr;
@@ -1134,6 +1170,7 @@ int splat_render_fwd(splat_stream_t stream, const float* means3d, int64_t rows_m
     if (rc) return rc;
     const KeyLayout L = key_layout(B, img_h, img_w);
     if (L.overflow) return fail(kErrKeyOverflow, "render_fwd: intersection key overflow");
+    sc.workload(B, num_gaussians, L.num_tiles);
     // the depth range from the projection: packed key, chunks meeting at most two images
     const bool fuse_range = L.packed && num_gaussians >= 1024;
     const int64_t chunks = project_fwd_chunks(total);
@@ -1224,6 +1261,9 @@ int splat_render_bwd(splat_stream_t stream, const float* means3d, int64_t rows_m
         return fail(kErrArgs, "render_bwd: v_quats and records must be 16-byte aligned");
     if (num_intersects < 0 || !tile_bins || (num_intersects > 0 && (!sorted_ids || !sorted_pos)))
         return fail(kErrArgs, "render_bwd: invalid sorted lists");
+    if (!means3d || !scales || !quats || !viewmat || !radii || !v_means || !v_scales ||
+        !v_quats)
+        return fail(kErrArgs, "render_bwd: missing input or output buffer");
     RasterInputs in = raster_inputs(colors, rows_colors, opacities, rows_opac, opacities,
                                     rows_opac, background, rows_bg, xys, depths, nullptr, conics,
                                     cum_tiles_hit, n, B, img_h, img_w);
@@ -1248,6 +1288,7 @@ int splat_render_bwd(splat_stream_t stream, const float* means3d, int64_t rows_m
     ScratchUse use(sc, s);
     rc = use.rc;
     if (rc) return rc;
+    sc.workload(B, n, key_layout(B, img_h, img_w).num_tiles);
     rc = sc.ensure_item_grads(items);
     if (rc) return rc;
     ba.v_xy = sc.item_grads;

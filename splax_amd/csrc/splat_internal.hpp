@@ -145,8 +145,13 @@ struct DeviceScratch {
     // after the other.
     hipStream_t last_stream = nullptr;
     bool has_last = false;
+    // workload signature (B_geom, n, num_tiles) of the last sort or blend call: a call with
+    // another one drops every workload-sized buffer first (splax/_cache.py:61-75)
+    int32_t sig_B = -1, sig_n = -1, sig_tiles = -1;
 
     int ensure_base();
+    void workload(int32_t B, int32_t n, int32_t num_tiles);
+    void release_sized();
     int order_after_last(hipStream_t s);
     void mark_done(hipStream_t s);
     int grow_chunk_sums(int64_t blocks);

@@ -41,8 +41,18 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(handle, name), f"{name} declared in include/splat_hip.h but not exported"
     assert set(names) == set(_lib._SIGS), "Python binding and header disagree"
     lib = _lib.lib()
-    assert lib.splat_abi_version() == 15
+    assert lib.splat_abi_version() == _lib.ABI_VERSION
     assert isinstance(lib.splat_last_error(), bytes)
+
+
+def test_binding_refuses_a_library_of_another_abi(monkeypatch):
+    """lib() compares splat_abi_version() with the version the binding was written for, so a
+    stale library exporting the same symbols raises instead of running under a changed
+    contract."""
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "ABI_VERSION", _lib.ABI_VERSION + 1)
+    with pytest.raises(ImportError, match="ABI version"):
+        _lib.lib()
 
 
 def test_no_cpu_fallback():
@@ -227,6 +237,95 @@ def test_nested_batch_shapes_and_errors():
     assert fold(x, 2, ()).shape == x.shape
     with pytest.raises(ValueError, match="inconsistent batch shapes"):
         batch_shape({"x": (torch.zeros((2, 7, 3)), 2), "v": (torch.zeros((3, 4, 4)), 2)})
+
+
+def test_size_one_background_is_shared():
+    """A background of shape (1, 3) (or any size-1 leading dims) is one shared colour, not a
+    batch axis: the reference reshapes it to (1, 3) inside rasterize
+    (splax/_rasterize/_rasterize.py:131), so an unbatched render stays (H, W, 3)."""
+    from splax_amd._batching import batch_shape, shared_background
+
+    means, vm = torch.zeros((7, 3)), torch.eye(4)
+    for bg in (torch.ones(3), torch.ones((1, 3)), torch.ones((1, 1, 3))):
+        b = shared_background(bg)
+        assert b.shape == (3,)
+        assert batch_shape({"means": (means, 2), "viewmat": (vm, 2), "bg": (b, 1)}) == ()
+    # a per-image background stays a batch axis
+    assert shared_background(torch.ones((2, 3))).shape == (2, 3)
+    assert batch_shape({"viewmat": (torch.zeros((2, 4, 4)), 2),
+                        "bg": (shared_background(torch.ones((1, 3))), 1)}) == (2,)
+
+
+_BUF = 256  # a stand-in device address (16-byte aligned; only the host checks run)
+
+
+def test_missing_required_buffers_are_rejected():
+    """A NULL required input or output of project_fwd / project_bwd / render_fwd /
+    render_bwd is status 1 before any device work (the placeholder addresses are never
+    dereferenced)."""
+    lib = _lib.lib()
+    lib.splat_last_error.restype = ctypes.c_char_p
+    n, buf, f = 10, _BUF, ctypes.c_float
+    m = ctypes.c_int64(0)
+
+    def project_fwd(**null):
+        a = dict(means=buf, scales=buf, quats=buf, viewmat=buf, opac=buf, xys=buf, depths=buf,
+                 radii=buf, conics=buf, nth=buf, cum=buf)
+        a.update(null)
+        return lib.splat_project_fwd(None, a["means"], n, a["scales"], n, a["quats"], n,
+                                     a["viewmat"], 4, a["opac"], n, None, 1, None, n, 1, 0, n,
+                                     16, 16, f(10.0), f(10.0), f(8.0), f(8.0), f(1.0), f(0.01),
+                                     a["xys"], a["depths"], a["radii"], a["conics"], a["nth"],
+                                     a["cum"], 1)
+
+    for k in ("means", "scales", "quats", "viewmat", "opac", "xys", "depths", "radii", "conics",
+              "nth", "cum"):
+        assert project_fwd(**{k: None}) == _lib.ERR_ARGS, k
+        assert b"missing input or output buffer" in lib.splat_last_error(), k
+
+    def project_bwd(**null):
+        a = dict(means=buf, scales=buf, quats=buf, viewmat=buf, radii=buf, conics=buf, v_xy=buf,
+                 v_conic=buf, v_mean=buf, v_scale=buf, v_quat=buf)
+        a.update(null)
+        return lib.splat_project_bwd(None, a["means"], n, a["scales"], n, a["quats"], n,
+                                     a["viewmat"], 4, a["radii"], n, a["conics"], n, a["v_xy"],
+                                     n, None, n, a["v_conic"], n, None, 1, None, n, 1, 0, 1,
+                                     f(10.0), f(10.0), f(1.0), a["v_mean"], a["v_scale"],
+                                     a["v_quat"], None, None, 1, 0)
+
+    for k in ("means", "scales", "quats", "viewmat", "radii", "conics", "v_xy", "v_conic",
+              "v_mean", "v_scale", "v_quat"):
+        assert project_bwd(**{k: None}) == _lib.ERR_ARGS, k
+        assert b"missing input or output buffer" in lib.splat_last_error(), k
+
+    def render_fwd(colors=buf, background=buf, xys=buf, radii=buf):
+        return lib.splat_render_fwd(None, buf, n, buf, n, buf, n, buf, 4, buf, n, colors, n,
+                                    background, 1, None, 1, None, n, 1, 0, 1, 16, 16, 100.0,
+                                    100.0, 8.0, 8.0, 1.0, 0.01, 1, 0, xys, buf, radii, buf, buf,
+                                    buf, 0, buf, buf, buf, buf, buf, buf, buf, buf, None,
+                                    ctypes.byref(m), None, 0, None)
+
+    for k in ("xys", "radii"):
+        assert render_fwd(**{k: None}) == _lib.ERR_ARGS, k
+        assert b"missing input or output buffer" in lib.splat_last_error(), k
+    for k in ("colors", "background"):
+        assert render_fwd(**{k: None}) == _lib.ERR_ARGS, k
+        assert b"missing input buffer" in lib.splat_last_error(), k
+
+    def render_bwd(**null):
+        a = dict(means=buf, radii=buf, v_means=buf, v_scales=buf, v_quats=buf, v_colors=buf,
+                 v_opac=buf)
+        a.update(null)
+        return lib.splat_render_bwd(None, a["means"], n, buf, n, buf, n, buf, 4, buf, n, buf, n,
+                                    buf, 1, None, 1, None, n, 1, 0, 1, 16, 16, 100.0, 100.0, 1.0,
+                                    1, 0, buf, buf, a["radii"], buf, buf, buf, buf, buf, buf, buf,
+                                    0, buf, buf, buf, 16, None, 0, a["v_means"], a["v_scales"],
+                                    a["v_quats"], a["v_colors"], a["v_opac"], None, None, 0,
+                                    None, 0, None, None)
+
+    for k in ("means", "radii", "v_means", "v_scales", "v_quats", "v_colors", "v_opac"):
+        assert render_bwd(**{k: None}) == _lib.ERR_ARGS, k
+        assert b"missing" in lib.splat_last_error(), k
 
 
 def test_backward_requires_the_final_buffers():
