@@ -267,6 +267,33 @@ def rasterize_bwd(colors, opacities, map_opac, background, xys, depths, radii, c
     return v_colors, v_opac, v_xy, v_conic, stats, v_depths
 
 
+def rasterize_bwd_f64(colors, opacities, map_opac, background, xys, depths, radii, conics, cum,
+                      final_Ts, final_idx, v_out, *, n, B_out, B_geom, img_shape,
+                      v_out_depth=None):
+    """The float64 truth of rasterize_bwd: the float walk's pairs and accept decisions, every
+    value after them in double (oracle_rasterize_bwd_f64). Returns float64 (v_colors,
+    v_opacity, v_xy, v_conic) sized B_out*n, and v_depths last when v_out_depth is given."""
+    colors, opac, mopac, bg, xys, depths, conics, Ts, vout = map(
+        _c32, (colors, opacities, map_opac, background, xys, depths, conics, final_Ts, v_out))
+    radii, cum, fidx = _ci32(radii).ravel(), _ci32(cum).ravel(), _ci32(final_idx)
+    H, W = img_shape
+    vd = None if v_out_depth is None else _c32(v_out_depth)
+    NG = 9 if vd is None else 10
+    out = np.empty((B_out * n, NG), np.float64)
+    fn = lib().oracle_rasterize_bwd_f64
+    fn.restype = ctypes.c_int64
+    m = fn(_f(colors), _i64(_rows(colors, 3)), _f(opac), _i64(opac.size), _f(mopac),
+           _i64(mopac.size), _f(bg), _i64(_rows(bg, 3)), _f(xys), _f(depths), _i(radii),
+           _f(conics), _i(cum), _f(Ts), _i(fidx), _f(vout), _i64(vout.size // (3 * W)), _i32(n),
+           _i32(B_out), _i32(B_geom), _i32(H), _i32(W), None if vd is None else _f(vd),
+           _i64(0 if vd is None else vd.size // W),
+           out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    if m < 0:
+        raise ValueError(f"oracle rasterize_bwd_f64 failed with code {m}")
+    res = (out[:, 0:3], out[:, 8].copy(), out[:, 6:8], out[:, 3:6])
+    return res if vd is None else res + (out[:, 9].copy(),)
+
+
 def project_bwd(means, scales, quats_xyzw, viewmat, radii, conics, v_xy, v_depth, v_conic, *, n,
                 B, f, glob_scale=1.0, transforms=None, transform_ids=None, num_transforms=None):
     """Returns (v_mean3d, v_scale, v_quat (xyzw), v_viewmat (B*4, 4), v_transforms)."""

@@ -912,7 +912,172 @@ int64_t oracle_rasterize_fwd(const float* colors, int64_t rows_colors, const flo
  * accumulated in double here (the reference's float atomics have no fixed order). With v_depths,
  * the depth-channel backward _rasterize_bwd_depth_warp / _kernel (:797-1080) with
  * _blend_depth_vjp (:1257-1302): the depth term joins v_alpha after the colour terms, its own
- * accumulator dbuffer, and v_depth = v_out_depth * fac per pair. */
+ * accumulator dbuffer, and v_depth = v_out_depth * fac per pair.
+ *
+ * truth != 0 evaluates the same walk in double: the pairs and their accept decisions (sigma
+ * range, alpha threshold, the 0.999 clamp) are the float walk's, and every value after them
+ * (sigma, e^-sigma, alpha, T, the colour buffer, v_alpha and the gradient terms) is formed in
+ * double from the float32 inputs. That is the float64 truth of the reference's backward formulas
+ * at the float forward's decisions, against which float32 evaluations are measured. */
+
+static int64_t rasterize_bwd_walk(const float* colors, int64_t rows_colors,
+                                  const float* opacities, int64_t rows_opac,
+                                  const float* map_opac, int64_t rows_map_opac,
+                                  const float* background, int64_t rows_bg, const float* xys,
+                                  const float* depths, const int32_t* radii, const float* conics,
+                                  const int32_t* cum, const float* final_Ts,
+                                  const int32_t* final_idx, const float* v_out_img,
+                                  int64_t vout_rows, int32_t n, int32_t B_out, int32_t B_geom,
+                                  int32_t img_h, int32_t img_w, int64_t* stats,
+                                  const float* v_out_depth, int64_t vdepth_rows, int with_depth,
+                                  int truth, double* acc) {
+    const int NG = with_depth ? 10 : 9;
+    int32_t L[6];
+    oracle_key_layout(B_geom, img_h, img_w, L);
+    const int32_t tbx = L[0], num_tiles = L[2];
+    const int64_t total = (int64_t)B_geom * n;
+    const int64_t M = total > 0 ? cum[total - 1] : 0;
+    int32_t* ids = (int32_t*)malloc(sizeof(int32_t) * (size_t)(M > 0 ? M : 1));
+    int32_t* bins = (int32_t*)malloc(sizeof(int32_t) * 2 * (size_t)B_geom * (size_t)num_tiles);
+    int64_t m = sort_ids_and_bins(xys, depths, radii, conics, map_opac, rows_map_opac, cum, n,
+                                  B_geom, img_h, img_w, ids, M, bins);
+    const int sel_geom = B_geom > 1, sel_bg = rows_bg > 1;
+    int64_t qc = 0, qr = 0;
+    if (m > 0) {
+        const int64_t rows_total = (int64_t)B_out * img_h;
+#pragma omp parallel for schedule(dynamic, 4) reduction(+ : qc, qr)
+        for (int64_t row = 0; row < rows_total; ++row) {
+            const int32_t image = (int32_t)(row / img_h), i = (int32_t)(row % img_h);
+            const int32_t geom_image = sel_geom ? image : 0;
+            const int64_t og_base = sel_geom ? 0 : (int64_t)image * n;
+            const float* bg = background + 3 * (sel_bg ? image : 0);
+            for (int32_t j = 0; j < img_w; ++j) {
+                int32_t tile_local = (i / BLOCK_WIDTH) * tbx + j / BLOCK_WIDTH;
+                int32_t tile = geom_image * num_tiles + tile_local;
+                int32_t start = bins[2 * tile], end = bins[2 * tile + 1];
+                if (end <= start) continue;
+                int64_t frow = (int64_t)geom_image * img_h + i;
+                int32_t bin_final = final_idx[frow * img_w + j];
+                float t_final = final_Ts[frow * img_w + j];
+                float T = t_final;
+                const float* vo =
+                    v_out_img + 3 * ((((int64_t)image * img_h + i) % vout_rows) * img_w + j);
+                const float vd =
+                    with_depth
+                        ? v_out_depth[(((int64_t)image * img_h + i) % vdepth_rows) * img_w + j]
+                        : 0.0f;
+                float px = (float)j + 0.5f, py = (float)i + 0.5f;
+                float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, db = 0.0f;
+                /* truth: the same state in double */
+                double Td = (double)t_final, b0d = 0.0, b1d = 0.0, b2d = 0.0, dbd = 0.0;
+                for (int32_t k = bin_final; k >= start; --k) {
+                    int64_t g = ids[k];
+                    float dx = xys[2 * g] - px, dy = xys[2 * g + 1] - py;
+                    const float* cn = conics + 3 * g;
+                    float a = cn[0], b = cn[1], c = cn[2];
+                    float sigma = blend_sigma(cn, dx, dy);
+                    if (sigma < 0.0f || sigma > BLEND_SIGMA_CAP) {
+                        ++qr;
+                        continue;
+                    }
+                    float vis = oracle_blend_expf(-sigma);
+                    float op = opacities[g % rows_opac];
+                    float alpha = fminw(ALPHA_MAX, op * vis);
+                    if (!(alpha >= ALPHA_THRESHOLD)) {
+                        ++qr;
+                        continue;
+                    }
+                    ++qc;
+                    const float* col = colors + 3 * (g % rows_colors);
+                    const int geo = op * vis <= ALPHA_MAX;
+                    const float dep = with_depth ? depths[g] : 0.0f;
+                    double* o = acc + NG * (og_base + g);
+                    double gr[10] = {0};
+                    if (truth) {
+                        const double dxd = (double)xys[2 * g] - ((double)j + 0.5);
+                        const double dyd = (double)xys[2 * g + 1] - ((double)i + 0.5);
+                        const double sd = 0.5 * ((double)a * dxd * dxd + (double)c * dyd * dyd) +
+                                          (double)b * dxd * dyd;
+                        const double visd = exp(-sd);
+                        const double ad = geo ? (double)op * visd : (double)ALPHA_MAX;
+                        const double rad = 1.0 / (1.0 - ad);
+                        Td = Td * rad;
+                        const double facd = ad * Td;
+                        double va = ((double)col[0] * Td - b0d * rad) * (double)vo[0] +
+                                    ((double)col[1] * Td - b1d * rad) * (double)vo[1] +
+                                    ((double)col[2] * Td - b2d * rad) * (double)vo[2];
+                        if (with_depth) va += ((double)dep * Td - dbd * rad) * (double)vd;
+                        va -= (double)t_final * rad *
+                              ((double)bg[0] * vo[0] + (double)bg[1] * vo[1] +
+                               (double)bg[2] * vo[2]);
+                        b0d += (double)col[0] * facd;
+                        b1d += (double)col[1] * facd;
+                        b2d += (double)col[2] * facd;
+                        if (with_depth) dbd += (double)dep * facd;
+                        gr[0] = vo[0] * facd;
+                        gr[1] = vo[1] * facd;
+                        gr[2] = vo[2] * facd;
+                        if (geo) {
+                            const double vs = -(double)op * visd * va;
+                            gr[3] = 0.5 * vs * dxd * dxd;
+                            gr[4] = vs * dxd * dyd;
+                            gr[5] = 0.5 * vs * dyd * dyd;
+                            gr[6] = vs * ((double)a * dxd + (double)b * dyd);
+                            gr[7] = vs * ((double)b * dxd + (double)c * dyd);
+                            gr[8] = visd * va;
+                        }
+                        gr[9] = (double)vd * facd;
+                    } else {
+                        /* _blend_color_vjp */
+                        float ra = 1.0f / (1.0f - alpha);
+                        T = T * ra;
+                        float fac = alpha * T;
+                        float v_alpha = (col[0] * T - b0 * ra) * vo[0];
+                        v_alpha += (col[1] * T - b1 * ra) * vo[1];
+                        v_alpha += (col[2] * T - b2 * ra) * vo[2];
+                        if (with_depth) v_alpha += (dep * T - db * ra) * vd;
+                        v_alpha += -t_final * ra * bg[0] * vo[0];
+                        v_alpha += -t_final * ra * bg[1] * vo[1];
+                        v_alpha += -t_final * ra * bg[2] * vo[2];
+                        b0 = b0 + col[0] * fac;
+                        b1 = b1 + col[1] * fac;
+                        b2 = b2 + col[2] * fac;
+                        if (with_depth) db = db + dep * fac;
+                        gr[0] = (double)(vo[0] * fac);
+                        gr[1] = (double)(vo[1] * fac);
+                        gr[2] = (double)(vo[2] * fac);
+                        if (geo) {
+                            float v_sigma = -op * vis * v_alpha;
+                            gr[3] = (double)(0.5f * v_sigma * dx * dx);
+                            gr[4] = (double)(v_sigma * dx * dy);
+                            gr[5] = (double)(0.5f * v_sigma * dy * dy);
+                            gr[6] = (double)(v_sigma * (a * dx + b * dy));
+                            gr[7] = (double)(v_sigma * (b * dx + c * dy));
+                            gr[8] = (double)(vis * v_alpha);
+                        }
+                        gr[9] = (double)(vd * fac);
+                    }
+                    const int ng = geo ? 9 : 3;
+                    if (with_depth) {
+#pragma omp atomic
+                        o[9] += gr[9];
+                    }
+                    for (int q = 0; q < ng; ++q) {
+#pragma omp atomic
+                        o[q] += gr[q];
+                    }
+                }
+            }
+        }
+    }
+    if (stats) {
+        stats[0] = qc;
+        stats[1] = qr;
+    }
+    free(ids);
+    free(bins);
+    return m;
+}
 
 int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const float* opacities,
                              int64_t rows_opac, const float* map_opac, int64_t rows_map_opac,
@@ -925,109 +1090,13 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
                              const float* v_out_depth, int64_t vdepth_rows, float* v_depths) {
     const int with_depth = v_depths != NULL;
     const int NG = with_depth ? 10 : 9;
-    int32_t L[6];
-    oracle_key_layout(B_geom, img_h, img_w, L);
-    const int32_t tbx = L[0], num_tiles = L[2];
-    const int64_t total = (int64_t)B_geom * n;
-    const int64_t M = total > 0 ? cum[total - 1] : 0;
-    int32_t* ids = (int32_t*)malloc(sizeof(int32_t) * (size_t)(M > 0 ? M : 1));
-    int32_t* bins = (int32_t*)malloc(sizeof(int32_t) * 2 * (size_t)B_geom * (size_t)num_tiles);
-    int64_t m = sort_ids_and_bins(xys, depths, radii, conics, map_opac, rows_map_opac, cum, n,
-                                  B_geom, img_h, img_w, ids, M, bins);
     const int64_t nout = (int64_t)B_out * n;
     double* acc = (double*)calloc((size_t)(nout > 0 ? nout : 1) * NG, sizeof(double));
-    const int sel_geom = B_geom > 1, sel_bg = rows_bg > 1;
-    int64_t qc = 0, qr = 0;
-    if (m > 0) {
-        const int64_t rows_total = (int64_t)B_out * img_h;
-#pragma omp parallel for schedule(dynamic, 4) reduction(+ : qc, qr)
-        for (int64_t row = 0; row < rows_total; ++row) {
-            const int32_t image = (int32_t)(row / img_h), i = (int32_t)(row % img_h);
-            const int32_t geom_image = sel_geom ? image : 0;
-            const int64_t og_base = sel_geom ? 0 : (int64_t)image * n;
-            const float* bg = background + 3 * (sel_bg ? image : 0);
-            {
-                for (int32_t j = 0; j < img_w; ++j) {
-                    int32_t tile_local = (i / BLOCK_WIDTH) * tbx + j / BLOCK_WIDTH;
-                    int32_t tile = geom_image * num_tiles + tile_local;
-                    int32_t start = bins[2 * tile], end = bins[2 * tile + 1];
-                    if (end <= start) continue;
-                    int64_t frow = (int64_t)geom_image * img_h + i;
-                    int32_t bin_final = final_idx[frow * img_w + j];
-                    float t_final = final_Ts[frow * img_w + j];
-                    float T = t_final;
-                    const float* vo = v_out_img + 3 * ((((int64_t)image * img_h + i) % vout_rows) *
-                                                           img_w + j);
-                    const float vd =
-                        with_depth ? v_out_depth[(((int64_t)image * img_h + i) % vdepth_rows) *
-                                                     img_w + j]
-                                   : 0.0f;
-                    float px = (float)j + 0.5f, py = (float)i + 0.5f;
-                    float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, db = 0.0f;
-                    for (int32_t k = bin_final; k >= start; --k) {
-                        int64_t g = ids[k];
-                        float dx = xys[2 * g] - px, dy = xys[2 * g + 1] - py;
-                        const float* cn = conics + 3 * g;
-                        float a = cn[0], b = cn[1], c = cn[2];
-                        float sigma = blend_sigma(cn, dx, dy);
-                        if (sigma < 0.0f || sigma > BLEND_SIGMA_CAP) {
-                            ++qr;
-                            continue;
-                        }
-                        float vis = oracle_blend_expf(-sigma);
-                        float op = opacities[g % rows_opac];
-                        float alpha = fminw(ALPHA_MAX, op * vis);
-                        if (!(alpha >= ALPHA_THRESHOLD)) {
-                            ++qr;
-                            continue;
-                        }
-                        ++qc;
-                        const float* col = colors + 3 * (g % rows_colors);
-                        /* _blend_color_vjp */
-                        float ra = 1.0f / (1.0f - alpha);
-                        T = T * ra;
-                        float fac = alpha * T;
-                        float v_alpha = (col[0] * T - b0 * ra) * vo[0];
-                        v_alpha += (col[1] * T - b1 * ra) * vo[1];
-                        v_alpha += (col[2] * T - b2 * ra) * vo[2];
-                        float dep = 0.0f;
-                        if (with_depth) {
-                            dep = depths[g];
-                            v_alpha += (dep * T - db * ra) * vd;
-                        }
-                        v_alpha += -t_final * ra * bg[0] * vo[0];
-                        v_alpha += -t_final * ra * bg[1] * vo[1];
-                        v_alpha += -t_final * ra * bg[2] * vo[2];
-                        b0 = b0 + col[0] * fac;
-                        b1 = b1 + col[1] * fac;
-                        b2 = b2 + col[2] * fac;
-                        if (with_depth) db = db + dep * fac;
-                        double* o = acc + NG * (og_base + g);
-                        float gr[9] = {vo[0] * fac, vo[1] * fac, vo[2] * fac, 0, 0, 0, 0, 0, 0};
-                        int ng = 3;
-                        if (with_depth) {
-#pragma omp atomic
-                            o[9] += (double)(vd * fac);
-                        }
-                        if (op * vis <= ALPHA_MAX) {
-                            float v_sigma = -op * vis * v_alpha;
-                            gr[3] = 0.5f * v_sigma * dx * dx;
-                            gr[4] = v_sigma * dx * dy;
-                            gr[5] = 0.5f * v_sigma * dy * dy;
-                            gr[6] = v_sigma * (a * dx + b * dy);
-                            gr[7] = v_sigma * (b * dx + c * dy);
-                            gr[8] = vis * v_alpha;
-                            ng = 9;
-                        }
-                        for (int k = 0; k < ng; ++k) {
-#pragma omp atomic
-                            o[k] += (double)gr[k];
-                        }
-                    }
-                }
-            }
-        }
-    }
+    int64_t m = rasterize_bwd_walk(colors, rows_colors, opacities, rows_opac, map_opac,
+                                   rows_map_opac, background, rows_bg, xys, depths, radii, conics,
+                                   cum, final_Ts, final_idx, v_out_img, vout_rows, n, B_out,
+                                   B_geom, img_h, img_w, stats, v_out_depth, vdepth_rows,
+                                   with_depth, 0, acc);
     for (int64_t g = 0; g < nout; ++g) {
         const double* o = acc + NG * g;
         if (with_depth) v_depths[g] = (float)o[9];
@@ -1041,14 +1110,30 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
         v_xy[2 * g + 1] = (float)o[7];
         v_opacity[g] = (float)o[8];
     }
-    if (stats) {
-        stats[0] = qc;
-        stats[1] = qr;
-    }
     free(acc);
-    free(ids);
-    free(bins);
     return m;
+}
+
+/* The float64 truth of oracle_rasterize_bwd (the walk above with truth set): the per-item sums
+ * [nout, 9] (or 10 with v_out_depth) in the order v_colour (3), v_conic (3), v_xy (2),
+ * v_opacity, v_depth, in double. */
+int64_t oracle_rasterize_bwd_f64(const float* colors, int64_t rows_colors, const float* opacities,
+                                 int64_t rows_opac, const float* map_opac, int64_t rows_map_opac,
+                                 const float* background, int64_t rows_bg, const float* xys,
+                                 const float* depths, const int32_t* radii, const float* conics,
+                                 const int32_t* cum, const float* final_Ts,
+                                 const int32_t* final_idx, const float* v_out_img,
+                                 int64_t vout_rows, int32_t n, int32_t B_out, int32_t B_geom,
+                                 int32_t img_h, int32_t img_w, const float* v_out_depth,
+                                 int64_t vdepth_rows, double* out) {
+    const int with_depth = v_out_depth != NULL;
+    const int NG = with_depth ? 10 : 9;
+    const int64_t nout = (int64_t)B_out * n;
+    memset(out, 0, sizeof(double) * (size_t)(nout > 0 ? nout : 0) * NG);
+    return rasterize_bwd_walk(colors, rows_colors, opacities, rows_opac, map_opac, rows_map_opac,
+                              background, rows_bg, xys, depths, radii, conics, cum, final_Ts,
+                              final_idx, v_out_img, vout_rows, n, B_out, B_geom, img_h, img_w,
+                              NULL, v_out_depth, vdepth_rows, with_depth, 1, out);
 }
 
 /* ---------------------------------------------------------------- projection backward

@@ -102,6 +102,19 @@ int64_t oracle_rasterize_bwd(const float* colors, int64_t rows_colors, const flo
                              float* v_opacity, float* v_xy, float* v_conic, int64_t* stats,
                              const float* v_out_depth, int64_t vdepth_rows, float* v_depths);
 
+/* The float64 truth of oracle_rasterize_bwd: the same pairs and accept decisions, every value
+ * after them in double; out holds [B_out * n, NG] sums (v_colour 3, v_conic 3, v_xy 2,
+ * v_opacity, and v_depth when v_out_depth is given). */
+int64_t oracle_rasterize_bwd_f64(const float* colors, int64_t rows_colors, const float* opacities,
+                                 int64_t rows_opac, const float* map_opac, int64_t rows_map_opac,
+                                 const float* background, int64_t rows_bg, const float* xys,
+                                 const float* depths, const int32_t* radii, const float* conics,
+                                 const int32_t* cum, const float* final_Ts,
+                                 const int32_t* final_idx, const float* v_out_img,
+                                 int64_t vout_rows, int32_t n, int32_t B_out, int32_t B_geom,
+                                 int32_t img_h, int32_t img_w, const float* v_out_depth,
+                                 int64_t vdepth_rows, double* out);
+
 int oracle_project_bwd(const float* means3d, int64_t rows_means, const float* scales,
                        int64_t rows_scales, const float* quats_xyzw, int64_t rows_quats,
                        const float* viewmat, int64_t rows_viewmat, const int32_t* radii,

@@ -24,8 +24,9 @@
 // values) and add the totals into the record's LDS accumulator. After each batch every record
 // stores its nine sums (plain stores, no global atomics) at its emission position, where all
 // intersections of one item are contiguous; grad_gather_kernel then adds them per item in a
-// fixed order and writes the four gradient outputs. Only the LDS sums of one record over the
-// tile's four quadrant waves depend on the order in which the waves arrive.
+// fixed order and writes the four gradient outputs. The LDS sums of one record over the tile's
+// four quadrant waves take two accumulator copies, each added into by two waves, so no sum depends
+// on the order in which the waves arrive: the backward is deterministic.
 #include <hip/hip_ext.h>
 
 #include <type_traits>
@@ -201,10 +202,9 @@ struct BatchLds {
     // a backward wave reads its whole list row as one dword per lane: rows of kTile bytes
     typename std::conditional<kRows, uint16_t, uint8_t>::type list[kRows ? 16 : 4][kTile];
 };
-// Records per batch of the backward: 192 keeps its LDS at 20 KB, so with at most 64 VGPRs eight
-// workgroups share a CU (eight waves per SIMD: 0.43 ms at config 2 against 0.44 with 224 records
-// and seven, 0.46 with 256 and six).
-constexpr int kBwdBatch = 192;
+// Records per batch of the backward: 128 keeps its LDS (records, lists and two accumulator
+// copies) at 19.3 KB, so with at most 64 VGPRs eight workgroups share a CU (eight waves per SIMD).
+constexpr int kBwdBatch = 128;
 
 // Stages record `src` of the sorted range into slot `tid` (one barrier), then each wave builds
 // its own record lists from the staged masks, in slot order: with kRows the lists of its four
@@ -640,21 +640,26 @@ __device__ __forceinline__ float row_reduce_scatter3(float a, float b, float c, 
     return s;
 }
 
-// Record accumulator slot k of batch record t ([t][kAccSlots] layout: the lanes that add at once
-// hit different banks). Slots 0-7 hold g0..g7; slots 8-11 hold per-row partials of the last
-// sums, which the batch readout adds: g8 from each of the four rows, or with the depth channel
-// g8 from rows 0-1 and g9 from rows 2-3.
+// Record accumulator slot k of batch record t, copy c ([t][c][kAccSlots] layout: the lanes that
+// add at once hit different banks). Slots 0-7 hold g0..g7; slots 8-11 hold per-row partials of
+// the last sums, which the batch readout adds: g8 from each of the four rows, or with the depth
+// channel g8 from rows 0-1 and g9 from rows 2-3. Waves 0 and 1 add into copy 0, waves 2 and 3
+// into copy 1, so a slot receives at most two adds into its zero: 0 + a + b rounds as 0 + b + a
+// (float addition commutes), whatever order the waves arrive in, and the readout adds copy 0 and
+// copy 1 in that order. Every sum is therefore the same from run to run.
 constexpr int kAccSlots = 12;
-#define ACC(t, k) acc[(t) * kAccSlots + (k)]
+constexpr int kAccCopies = 2;
+constexpr int kAccStride = kAccSlots * kAccCopies;
+#define ACC(t, k) acc[(t) * kAccStride + (k)]
 
 // kDepth adds the depth channel of _rasterize_bwd_depth_kernel / _blend_depth_vjp
 // (splax/_rasterize/_kernels.py:935-1080,1257-1302): the record's depth joins the colour dot
 // product (v_alpha and the accumulator), and v_depth = v_out_depth * fac is a tenth sum.
 template <bool kDepth>
-__global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
+__global__ void __launch_bounds__(kTile, 8) blend_bwd_kernel(BlendBwdParams P) {
     constexpr int NG = kDepth ? 10 : 9;
     __shared__ BatchLds<false, kBwdBatch> L;
-    __shared__ float acc[kBwdBatch * kAccSlots];
+    __shared__ float acc[kBwdBatch * kAccStride];
     __shared__ int32_t s_max;
 
     const BlendCommon& C = P.c;
@@ -723,7 +728,7 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     // running sum
     float acc_v = tfbg;
     if (tid == 0) s_max = range_start - 1;
-    for (int k = tid; k < kBwdBatch * kAccSlots; k += kTile) acc[k] = 0.0f;
+    for (int k = tid; k < kBwdBatch * kAccStride; k += kTile) acc[k] = 0.0f;
     __syncthreads();
     atomicMax(&s_max, bin_final);
     // wave-wide largest final index: a record above it has no contributing lane in this wave
@@ -754,7 +759,7 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
     const bool hi8 = (l16 & 8) != 0, hi4 = (l16 & 4) != 0;
     const int ka = (row == 0) ? 0 : (row == 1) ? 2 : (row == 2) ? 1 : 3;
     const bool adds = l16 == 0 || l16 == 4 || l16 == 8;
-    const int kslot = l16 == 0 ? ka : l16 == 8 ? 4 + ka : 8 + row;
+    const int kslot = (l16 == 0 ? ka : l16 == 8 ? 4 + ka : 8 + row) + kAccSlots * (wave >> 1);
     for (int32_t bt = 0; bt < num_batches; ++bt) {
         const int32_t batch_end = start_idx - bt * kBwdBatch;
         const int32_t src = imaxw(batch_end - tid, range_start);
@@ -819,7 +824,7 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
             // An empty use keeps the last DPP add in this block: sunk into the branch below it
             // would no longer fuse with its DPP move.
             asm volatile("" ::"v"(sum));
-            if (adds) atomicAdd(&acc[t * kAccSlots + kslot], sum);
+            if (adds) atomicAdd(&acc[t * kAccStride + kslot], sum);
         }
         __syncthreads();
         if (tid < kBwdBatch) {
@@ -827,13 +832,16 @@ __global__ void __launch_bounds__(kTile) blend_bwd_kernel(BlendBwdParams P) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 // the halved sums doubled (the conic's a and c terms, slots 3 and 5, are whole)
-                s[k] = (k == 3 || k == 5) ? ACC(tid, k) : 2.0f * ACC(tid, k);
+                const float v = ACC(tid, k) + ACC(tid, kAccSlots + k);
+                s[k] = (k == 3 || k == 5) ? v : 2.0f * v;
                 ACC(tid, k) = 0.0f;
+                ACC(tid, kAccSlots + k) = 0.0f;
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                part[r] = ACC(tid, 8 + r);
+                part[r] = ACC(tid, 8 + r) + ACC(tid, kAccSlots + 8 + r);
                 ACC(tid, 8 + r) = 0.0f;
+                ACC(tid, kAccSlots + 8 + r) = 0.0f;
             }
             if constexpr (kDepth) {
                 s[8] = 2.0f * (part[0] + part[1]);

@@ -6,6 +6,7 @@ CPU oracle; all other tests run on the CPU and pin the oracle itself.
 
 from __future__ import annotations
 
+import functools
 import sys
 from pathlib import Path
 
@@ -30,6 +31,15 @@ def _oracle_built():
 
         build()
     yield
+
+
+@functools.lru_cache(maxsize=2)
+def cached_scene(config: int, n: int | None = None):
+    """splax_amd.scenes.make_scene, kept for the session (the config-4 scene takes seconds to
+    draw); callers must not modify its arrays."""
+    from splax_amd.scenes import make_scene
+
+    return make_scene(config, n=n)
 
 
 def random_scene(n: int, H: int, W: int, seed: int = 0, scale_range=(0.005, 0.05),

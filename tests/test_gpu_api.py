@@ -90,6 +90,32 @@ def test_render_and_grads_match_oracle():
     assert (_np(vm.grad)[3] == 0).all()
 
 
+def test_size_one_background_renders_one_image():
+    """A background of shape (1, 3) is one shared colour (the reference reshapes it to (1, 3)
+    inside rasterize, splax/_rasterize/_rasterize.py:131): the image stays (H, W, 3) and equals
+    the render with a (3,) background bit for bit, loss and gradients included."""
+    _case("background (1, 3)")
+    n, H, W = 3000, 64, 80
+    sc = random_scene(n, H, W, seed=12)
+    outs = []
+    for bg in (sc["bg"], sc["bg"].reshape(1, 3), sc["bg"].reshape(1, 1, 3)):
+        p = [_t(sc[k], grad=True) for k in ("means", "scales", "quats", "colors", "opac")]
+        img, _ = splax_amd.render(*p, viewmat=_t(sc["vm"]), background=_t(bg),
+                                  img_shape=(H, W), f=sc["f"], c=sc["c"])
+        assert img.shape == (H, W, 3), bg.shape
+        img.sum().backward()
+        loss, img2 = splax_amd.render_loss(*[_t(sc[k]) for k in ("means", "scales", "quats",
+                                                                  "colors", "opac")],
+                                           target=torch.zeros((H, W, 3), device="cuda"),
+                                           viewmat=_t(sc["vm"]), background=_t(bg),
+                                           img_shape=(H, W), f=sc["f"], c=sc["c"])
+        assert img2.shape == (H, W, 3)
+        outs.append([_np(img), _np(loss)] + [_np(t.grad) for t in p])
+    for other in outs[1:]:
+        for k, (a, b) in enumerate(zip(other, outs[0])):
+            assert_bit_exact(a, b, f"output {k}")
+
+
 def _stress_scene():
     """test_gpu_parity's extremes scene (huge, needle-thin and near-plane gaussians, opacities at
     the clamp and the threshold), in random_scene's dictionary form."""

@@ -4,9 +4,11 @@ the two-call path (project then rasterize, each with its own backward) on the GP
 The fused forward's projection also packs the blend records and forms the per-image depth range
 (the sort's depth-range pass and the record pack do not run); the fused backward keeps the
 per-item 2D cotangents in library scratch. Bars: projection outputs, kept lists, records
-and the image bit-exact; gradients within relative Frobenius 1e-5 plus allclose(rtol=1e-4,
-atol=1e-5 * max|ref|) (the viewmat and transform gradients, and the blend's per-record sums over
-a tile's waves, add in an order the GPU's scheduling decides).
+and the image bit-exact. The backward is deterministic (no sum depends on the GPU's scheduling),
+so one camera's gradients are bit-exact as well, and two runs of one render agree bit for bit;
+batched renders, whose two-call path sums the shared gaussians' per-camera gradients in torch
+rather than in the library, are held to relative Frobenius 1e-5 plus allclose(rtol=1e-4,
+atol=1e-5 * max|ref|).
 """
 
 from __future__ import annotations
@@ -152,6 +154,12 @@ def test_fused_render_equals_two_call_path(name):
     assert_bit_exact(fi, ui, f"{name}/img")
     if rd:
         assert_bit_exact(fd, ud, f"{name}/depth")
+    if B == 1:
+        # one camera: the same records, lists, order and kernels on both paths, and no sum
+        # whose order the GPU's scheduling decides
+        for k in ug:
+            assert_bit_exact(fg[k], ug[k], f"{name}/{k}")
+        return
     if not cfg.get("cond_split"):
         for k in ug:
             _grad_compare(fg[k], ug[k], f"{name}/{k}")
@@ -173,6 +181,42 @@ def test_fused_render_equals_two_call_path(name):
             _grad_compare(fg[k], ug[k], f"{name}/{k}", rel_tol=1e-3, elementwise=False)
         else:
             _grad_compare(fg[k], ug[k], f"{name}/{k}")
+
+
+@pytest.mark.parametrize("name", ["cfg2_60k", "cfg3_20k_B4", "stress_aa_depth"])
+def test_backward_is_deterministic(name):
+    """Two runs of one render and its backward give every gradient bit for bit: the blend
+    backward's per-record sums over a tile's four waves use two accumulator copies with at most
+    two adds each (float addition commutes), the gather adds each item's intersections in
+    emission order and the viewmat gradient is reduced in a fixed order."""
+    _case(f"deterministic backward {name}")
+    cfg = CASES[name]
+    s = cfg["scene"]()
+    B = cfg["B"]
+    aa, rd = cfg.get("antialiased", False), cfg.get("depth", False)
+    cam = dict(img_shape=s.img_shape, f=s.f, c=s.c)
+    vms = s.viewmats[:B] if s.B >= B else np.stack([s.viewmats[0]] * B)
+    runs = []
+    for _ in range(2):
+        p = {k: _t(v, grad=True) for k, v in (("means", s.means), ("scales", s.scales),
+                                               ("quats", s.quats), ("colors", s.colors),
+                                               ("opac", s.opacities))}
+        vm = _t(vms if B > 1 else vms[0], grad=True)
+        img, depth = splax_amd.render(p["means"], p["scales"], p["quats"], p["colors"],
+                                      p["opac"], viewmat=vm, background=_t(s.background),
+                                      antialiased=aa, render_depth=rd, **cam)
+        w = torch.from_numpy(np.random.default_rng(7).uniform(-1, 1, img.shape)
+                             .astype(np.float32)).cuda()
+        loss = (img * w).sum()
+        if rd:
+            loss = loss + depth.sum()
+        loss.backward()
+        torch.cuda.synchronize()
+        g = {k: _np(v.grad) for k, v in p.items()}
+        g["viewmat"] = _np(vm.grad)
+        runs.append(g)
+    for k in runs[0]:
+        assert_bit_exact(runs[1][k], runs[0][k], f"{name}/{k} run 2 vs run 1")
 
 
 def test_fused_render_with_transforms_and_nested_batch():

@@ -264,6 +264,50 @@ def test_batched_full_size_matches_oracle(config):
         _grad_compare(_np(g).reshape(r.shape), r, f"config{config}/{label}")
 
 
+@pytest.mark.parametrize("H,W", [(1600, 2560), (2160, 3840)])
+def test_images_above_8192_tiles_match_oracle(H, W):
+    """Images past 8,192 tiles (2560x1600: 16,000; 3840x2160: 32,400) take the tile order's
+    strided two-pass path, which no other test reaches: a wrong permutation there would drop or
+    repeat tiles. Image, final_Ts and final_idx bit for bit against the oracle, through the
+    rasterize call and through splax_amd.render (the fused path), and the blend backward within
+    the gradient bar."""
+    import splax_amd
+
+    _case(f"above 8192 tiles {W}x{H}")
+    O.set_threads(16)
+    n = 150_000
+    s = random_scene(n, H, W, seed=H)
+    assert ((W + 15) // 16) * ((H + 15) // 16) > 8192
+    q = np.roll(s["quats"], -1, axis=-1)
+    xys, depths, radii, conics, nth, cum = O.project_fwd(
+        s["means"], s["scales"], q, s["vm"], s["opac"], n=n, total=n, img_shape=(H, W),
+        f=s["f"], c=s["c"])
+    rimg, rT, ridx, _, M = O.rasterize_fwd(s["colors"], s["opac"], s["opac"], s["bg"], xys,
+                                           depths, radii, conics, cum, n=n, B=1,
+                                           img_shape=(H, W))
+    o = _t(s["opac"]).reshape(-1)
+    geo = (_t(xys), _t(depths), _t(radii), _t(conics), _t(cum))
+    gimg, gT, gidx, gM = _ops.rasterize_fwd(_t(s["colors"]), o, o, _t(s["bg"]), *geo, n=n, B=1,
+                                            img_shape=(H, W))
+    torch.cuda.synchronize()
+    assert gM == M > 100_000
+    assert_bit_exact(_np(gT), rT, "final_Ts")
+    assert_bit_exact(_np(gidx), ridx, "final_idx")
+    assert_bit_exact(_np(gimg), rimg, "img")
+    img, _ = splax_amd.render(_t(s["means"]), _t(s["scales"]), _t(s["quats"]), _t(s["colors"]),
+                              _t(s["opac"]), viewmat=_t(s["vm"]), background=_t(s["bg"]),
+                              img_shape=(H, W), f=s["f"], c=s["c"])
+    assert_bit_exact(_np(img), rimg.reshape(H, W, 3), "render/img")
+    vout = np.random.default_rng(1).uniform(-1, 1, (H * W, 3)).astype(np.float32)
+    rg = O.rasterize_bwd(s["colors"], s["opac"], s["opac"], s["bg"], xys, depths, radii, conics,
+                         cum, rT, ridx, vout, n=n, B_out=1, B_geom=1, img_shape=(H, W))
+    gg = _ops.rasterize_bwd(_t(s["colors"]), o, o, _t(s["bg"]), *geo, _t(rT), _t(ridx),
+                            _t(vout), n=n, B_out=1, B_geom=1, img_shape=(H, W))
+    torch.cuda.synchronize()
+    for label, g, r in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), gg, rg[:4]):
+        _grad_compare(_np(g).reshape(r.shape), r, f"{W}x{H}/{label}")
+
+
 @pytest.mark.parametrize("name", list(CASES))
 def test_rasterize_bwd_matches_oracle(name):
     _case(f"rasterize_bwd {name}")

@@ -1,9 +1,9 @@
-"""The library's grow-only device scratch on the GPU (the counterpart of splax/_cache.py): renders
-on warm scratch, left by differently sized calls, equal renders on freshly cleared scratch, and
-clear_cache() returns the scratch's device memory. Mirrors the reference's scratch invariants
-(tests/test_warp_rasterize.py:208-242) through the fused render with its loss and gradients. The
-reference's second invariant, that a smaller call releases a larger call's buffers, does not
-carry over: this scratch only grows until clear_cache() (sized for one GPU's 288 GB)."""
+"""The library's device scratch on the GPU (the counterpart of splax/_cache.py): renders on warm
+scratch, left by differently sized calls, equal renders on freshly cleared scratch; a call with
+a new workload signature (B, n, tiles) releases the previous workload's buffers, as the
+reference drops its scratch entry (splax/_cache.py:61-75); clear_cache() returns the rest and
+forgets the kept-list capacity estimate. Mirrors the reference's scratch invariants
+(tests/test_warp_rasterize.py:208-242) through the fused render with its loss and gradients."""
 
 from __future__ import annotations
 
@@ -12,8 +12,8 @@ import pytest
 import torch
 
 import splax_amd
-from conftest import assert_bit_exact, random_scene, rel_fro
-from splax_amd import _lib
+from conftest import assert_bit_exact, cached_scene, random_scene, rel_fro
+from splax_amd import _lib, _ops
 
 pytestmark = pytest.mark.gpu
 
@@ -80,3 +80,44 @@ def test_clear_cache_returns_the_scratch():
     img, loss, _ = _render(random_scene(5_000, 128, 128, seed=2),
                            np.zeros((128, 128, 3), np.float32))
     assert np.isfinite(loss) and img.shape == (128, 128, 3)
+
+
+def _free_after_release() -> int:
+    """Free device memory once torch's cached blocks are returned."""
+    import gc
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return torch.cuda.mem_get_info()[0]
+
+
+def test_new_workload_signature_releases_the_scratch():
+    """After a config-4-size training render (3M gaussians, four 1600x1060 cameras, 31M
+    intersections) the library holds gigabytes of sort and gradient scratch; the next call with
+    another workload signature (a config-0 render) drops it first, and its kept-list capacity
+    estimate starts again from that call's count. clear_cache() then returns the small
+    workload's scratch and forgets the estimate."""
+    _case("scratch dropped on a new workload signature")
+    s = cached_scene(4)
+    p = [_t(a, grad=True) for a in (s.means, s.scales, s.quats, s.colors, s.opacities)]
+    loss, _ = splax_amd.render_loss(*p, target=_t(s.targets), loss="l1",
+                                    viewmat=_t(s.viewmats), background=_t(s.background),
+                                    img_shape=s.img_shape, f=s.f, c=s.c, antialiased=True)
+    loss.backward()
+    key = str(p[0].device)
+    big_cap = _ops._KEEP_CAPACITY[key]
+    assert big_cap > 30_000_000
+    del p, loss
+    free_big = _free_after_release()
+    small = random_scene(10_000, 256, 256, seed=4)
+    img, _, _ = _render(small, np.zeros((256, 256, 3), np.float32))
+    assert img.shape == (256, 256, 3)
+    small_cap = _ops._KEEP_CAPACITY[key]
+    assert 0 < small_cap < big_cap // 100, (small_cap, big_cap)
+    free_small = _free_after_release()
+    # the intersection-sized sort buffers and per-intersection sums alone are several GB
+    assert free_small - free_big > 2 << 30, (free_big, free_small)
+    splax_amd.clear_cache()
+    assert key not in _ops._KEEP_CAPACITY
+    assert _free_after_release() >= free_small
