@@ -858,9 +858,12 @@ __global__ void __launch_bounds__(kTile, 8) blend_bwd_kernel(BlendBwdParams P) {
 #undef ACC
 
 // Per output item: sum of its intersections' partial gradients in emission order (fixed, so
-// deterministic), then v_xy = (a Sx + b Sy, b Sx + c Sy) with the item's conic (a, b, c), which
-// equals the reference's per-pair sum of v_sigma (a dx + b dy, b dx + c dy)
-// (splax/_rasterize/_kernels.py:1246-1250) up to rounding. Every output is written.
+// deterministic) in double, then v_xy = (a Sx + b Sy, b Sx + c Sy) with the item's conic
+// (a, b, c), in double, which equals the reference's per-pair sum of
+// v_sigma (a dx + b dy, b dx + c dy) (splax/_rasterize/_kernels.py:1246-1250) up to rounding; each
+// output is rounded to float once. Every output is written. The double sums keep the gather's
+// rounding out of the gradients of needle-thin items, whose projection VJP multiplies it by up
+// to cond(conic)^2.
 struct GatherParams {
     const int32_t* cum; const float* conics; const float* rgrad;
     int64_t M; int64_t nout; int32_t n; int32_t sel_geom;
@@ -884,7 +887,7 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
     const int64_t t_last = (t_first + 255 < limit ? t_first + 255 : limit - 1);
     const bool valid = t < limit;
     const int32_t images = P.fold ? (int32_t)(P.nout / P.n) : 1;
-    float fc0 = 0.f, fc1 = 0.f, fc2 = 0.f, fo = 0.f;
+    double fc0 = 0.0, fc1 = 0.0, fc2 = 0.0, fo = 0.0;
     for (int32_t image = 0; image < images; ++image) {
     const int64_t og = P.fold ? (int64_t)image * P.n + t : t;
     int64_t gi = og, off = 0;
@@ -905,7 +908,7 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
     const int64_t og_first = P.fold ? (int64_t)image * P.n + t_first : t_first;
     const int64_t og_last = P.fold ? (int64_t)image * P.n + t_last : t_last;
     const bool one_range = P.sel_geom || og_first / P.n == og_last / P.n;
-    float s[NG];
+    double s[NG];
     if (one_range) {
         int64_t gf = og_first, gl = og_last, woff = 0;
         if (!P.sel_geom) {
@@ -920,21 +923,21 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
         block_gather<NG, 256>(P.rgrad, woff, wlo, whi, lo, hi, s_buf, s);
     } else {
 #pragma unroll
-        for (int k = 0; k < NG; ++k) s[k] = 0.0f;
+        for (int k = 0; k < NG; ++k) s[k] = 0.0;
         for (int64_t e = lo; e < hi; ++e) {
             const float* r = P.rgrad + (off + e) * NG;
 #pragma unroll
-            for (int k = 0; k < NG; ++k) s[k] += r[k];
+            for (int k = 0; k < NG; ++k) s[k] += (double)r[k];
         }
     }
     if (!valid) continue;
-    float vc[3] = {s[3], s[4], s[5]};
-    float vo = s[8];
+    float vc[3] = {(float)s[3], (float)s[4], (float)s[5]};
+    float vo = (float)s[8];
     float vx = 0.f, vy = 0.f;
-    if (s[6] != 0.f || s[7] != 0.f || P.compensate) {
+    if (s[6] != 0.0 || s[7] != 0.0 || P.compensate) {
         const float a = P.conics[3 * gi], b = P.conics[3 * gi + 1], c = P.conics[3 * gi + 2];
-        vx = a * s[6] + b * s[7];
-        vy = b * s[6] + c * s[7];
+        vx = (float)((double)a * s[6] + (double)b * s[7]);
+        vy = (float)((double)b * s[6] + (double)c * s[7]);
         if (P.compensate) vo = compensation_vjp(vo, P.opac[gi % P.rows_opac], a, b, c, vc);
     }
     P.v_conic[3 * og] = vc[0];
@@ -942,24 +945,24 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
     P.v_conic[3 * og + 2] = vc[2];
     P.v_xy[2 * og] = vx;
     P.v_xy[2 * og + 1] = vy;
-    if constexpr (NG == 10) P.v_depths[og] = s[9];
+    if constexpr (NG == 10) P.v_depths[og] = (float)s[9];
     if (P.fold) {
         fc0 = fc0 + s[0];
         fc1 = fc1 + s[1];
         fc2 = fc2 + s[2];
-        fo = fo + vo;
+        fo = fo + (double)vo;
     } else {
-        P.v_colors[3 * og] = s[0];
-        P.v_colors[3 * og + 1] = s[1];
-        P.v_colors[3 * og + 2] = s[2];
+        P.v_colors[3 * og] = (float)s[0];
+        P.v_colors[3 * og + 1] = (float)s[1];
+        P.v_colors[3 * og + 2] = (float)s[2];
         P.v_opacity[og] = vo;
     }
     }
     if (P.fold && valid) {
-        P.v_colors[3 * t] = fc0;
-        P.v_colors[3 * t + 1] = fc1;
-        P.v_colors[3 * t + 2] = fc2;
-        P.v_opacity[t] = fo;
+        P.v_colors[3 * t] = (float)fc0;
+        P.v_colors[3 * t + 1] = (float)fc1;
+        P.v_colors[3 * t + 2] = (float)fc2;
+        P.v_opacity[t] = (float)fo;
     }
 }
 

@@ -361,7 +361,7 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
 constexpr int kGatherChunk = 512;
 
 // Per-item sums of NG floats over the item's emission range [my_lo, my_hi) of rgrad rows
-// (row e at rgrad + (off + e) * NG), added in emission order. The workgroup's items cover one
+// (row e at rgrad + (off + e) * NG), added in emission order in double. The workgroup's items cover one
 // contiguous range [wg_lo, wg_hi) of rows (uniform over the workgroup), which is read with
 // coalesced loads into s_buf (kGatherChunk * NG floats of LDS) a round at a time; each thread then
 // adds its own rows from LDS. Every thread of the workgroup calls it (an item outside the
@@ -369,9 +369,9 @@ constexpr int kGatherChunk = 512;
 template <int NG, int kThreads>
 __device__ __forceinline__ void block_gather(const float* __restrict__ rgrad, int64_t off,
                                              int64_t wg_lo, int64_t wg_hi, int64_t my_lo,
-                                             int64_t my_hi, float* s_buf, float* s) {
+                                             int64_t my_hi, float* s_buf, double* s) {
 #pragma unroll
-    for (int k = 0; k < NG; ++k) s[k] = 0.0f;
+    for (int k = 0; k < NG; ++k) s[k] = 0.0;
     for (int64_t cs = wg_lo; cs < wg_hi; cs += kGatherChunk) {
         const int64_t ce = cs + kGatherChunk < wg_hi ? cs + kGatherChunk : wg_hi;
         const int nf = (int)((ce - cs) * NG);
@@ -395,7 +395,7 @@ __device__ __forceinline__ void block_gather(const float* __restrict__ rgrad, in
         for (int64_t e = a; e < b; ++e) {
             const float* r = s_buf + (e - cs) * NG;
 #pragma unroll
-            for (int k = 0; k < NG; ++k) s[k] += r[k];
+            for (int k = 0; k < NG; ++k) s[k] += (double)r[k];
         }
     }
 }

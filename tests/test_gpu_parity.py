@@ -940,6 +940,17 @@ def test_stress_scene_matches_oracle():
     r_all = rel_fro(gx.astype(np.float64), rx.astype(np.float64))
     assert r_all < 1e-4, f"stress/v_xy: relative Frobenius error {r_all:.3e}"
     np.testing.assert_array_equal(gx[radii <= 0], 0.0)  # culled items get exact zeros
+    # against the float64 truth of the same walk, per condition band: at most timed_path.FACTOR
+    # times the float32 oracle's error, or 1e-5
+    import timed_path as TP
+
+    tb = O.rasterize_bwd_f64(s["colors"], s["opac"], s["opac"], s["bg"], xys, depths, radii,
+                             conics, cum, rT, ridx, vout, n=n, B_out=1, B_geom=1,
+                             img_shape=s["img_shape"])
+    cond_v = np.where(radii.ravel() > 0, cond, 0.0)
+    for label, g, r, t in zip(("v_colors", "v_opacity", "v_xy", "v_conic"), gb, rb[:4], tb):
+        TP.assert_bands(_np(g).reshape(r.shape), r, np.asarray(t).reshape(r.shape), cond_v,
+                        f"stress/{label}")
     q = np.roll(s["quats"], -1, axis=-1)
     rp = O.project_bwd(s["means"], s["scales"], q, s["vm"], radii, conics, rb[2],
                        np.zeros(n, np.float32), rb[3], n=n, B=1, f=s["f"])
