@@ -312,6 +312,15 @@ __device__ __forceinline__ float blend_sigma(const float4& r0, const float4& r1,
     return fmaf(dx, fmaf(r0.z, dx, r0.w * dy), (r1.x * dy) * dy);
 }
 
+// 0 <= sigma <= sigma_max as one unsigned compare of the float bits (one VALU where two float
+// compares take two). Equal for every record a list holds: its sigma_max is >= 0 and not NaN
+// (a record with sigma_max < 0 or NaN is kCullNone and reaches no sub-block); sigma is never
+// -0.0 (with c > 0 the term (c/2 dy) dy is +0 or positive, and a rounded sum is -0.0 only when
+// both addends are), so a negative sigma has its sign bit set and fails, as a NaN does.
+__device__ __forceinline__ bool sigma_in_range(float sigma, float sigma_max) {
+    return __float_as_uint(sigma) <= __float_as_uint(sigma_max);
+}
+
 // ------------------------------------------------------------------ forward
 // _rasterize_kernel, splax/_rasterize/_kernels.py:102-205
 
@@ -379,9 +388,8 @@ __global__ void __launch_bounds__(kTile, 7) blend_fwd_kernel(BlendFwdParams P) {
             const float dx = r0.x - px, dy = r0.y - py;
             const float sigma = blend_sigma(r0, r1, dx, dy);
             // Nested conditions and the one exit above: every other path falls through to the
-            // next step, which keeps the loop's control flow in the exec mask. Bitwise: no
-            // short-circuit branch around the sigma_max read (NaN sigma fails both).
-            if ((sigma >= 0.0f) & (sigma <= r1.z)) {
+            // next step, which keeps the loop's control flow in the exec mask.
+            if (sigma_in_range(sigma, r1.z)) {
                 // v_min: no accepted record has a NaN opacity (the pack culls those), so it
                 // equals the reference's compare-and-select minimum here
                 const float alpha = fminf(kAlphaMax, r1.y * blend_exp(-sigma, exp_round, exp_c5));
@@ -624,17 +632,49 @@ __device__ __forceinline__ float dpp_pair_add(float keep, float send) {
     return keep + __int_as_float(r);
 }
 
+// x + x[row_mirror] (lane l of each 16-lane row with lane 15 - l) written only into the lanes
+// of the 4-lane banks kBanks of each row, d kept in the others: one v_add_f32_dpp with a bank
+// mask, where a select of what to keep and what to send plus the add take three VALU. The
+// compiler does not form the bank-masked add from the DPP builtins, so it is written here, with
+// the two wait states a DPP read of a VGPR written by the previous VALU instruction needs.
+template <int kBanks>
+__device__ __forceinline__ float dpp_add_mirror_banks(float d, float x) {
+    static_assert(kBanks == 0x3 || kBanks == 0xc, "banks 0-1 or 2-3");
+    if constexpr (kBanks == 0x3)
+        asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_mirror row_mask:0xf bank_mask:0x3"
+            : "+v"(d) : "v"(x));
+    else
+        asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_mirror row_mask:0xf bank_mask:0xc"
+            : "+v"(d) : "v"(x));
+    return d;
+}
+// The same with row_half_mirror (lane j of each 8-lane half with lane 7 - j): banks 0 and 2
+// (kBanks 0x5) or 1 and 3 (0xa).
+template <int kBanks>
+__device__ __forceinline__ float dpp_add_half_mirror_banks(float d, float x) {
+    static_assert(kBanks == 0x5 || kBanks == 0xa, "banks 0 and 2 or 1 and 3");
+    if constexpr (kBanks == 0x5)
+        asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0x5"
+            : "+v"(d) : "v"(x));
+    else
+        asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0xa"
+            : "+v"(d) : "v"(x));
+    return d;
+}
+
 // Reduce-scatter of three values over each 16-lane row. Lane l pairs with 15 - l (row_mirror):
-// the lower half keeps a and sends b, the upper half the reverse, and c is summed on its own;
-// then lane j of each 8-lane half pairs with 7 - j (row_half_mirror), the lower quad keeping the
-// a/b partial and the upper one c; two quad butterflies finish. Lanes 0-3 of the row then hold
-// the row sum of a, lanes 8-11 that of b, lanes 4-7 and 12-15 that of c: nine VALU, where
-// four DPP steps per value take twelve and leave three values to add into LDS.
-__device__ __forceinline__ float row_reduce_scatter3(float a, float b, float c, bool hi8,
-                                                     bool hi4) {
-    const float r = dpp_pair_add<0x140>(hi8 ? b : a, hi8 ? a : b);  // row_mirror
-    c = dpp_pair_add<0x140>(c, c);
-    float s = dpp_pair_add<0x141>(hi4 ? c : r, hi4 ? r : c);  // row_half_mirror
+// the lower half sums a and the upper half b, and c is summed on its own; then lane j of each
+// 8-lane half pairs with 7 - j (row_half_mirror), the lower quad summing the a/b partial and the
+// upper one c; two quad butterflies finish. Lanes 0-3 of the row then hold the row sum of a,
+// lanes 8-11 that of b, lanes 4-7 and 12-15 that of c: seven VALU (the halves' different sums
+// are bank-masked DPP adds), where four DPP steps per value take twelve and leave three values to
+// add into LDS.
+__device__ __forceinline__ float row_reduce_scatter3(float a, float b, float c) {
+    float r = dpp_add_mirror_banks<0x3>(a, a);  // lanes 0-7: a + a[15 - l]
+    r = dpp_add_mirror_banks<0xc>(r, b);        // lanes 8-15: b + b[15 - l]
+    c = dpp_pair_add<0x140>(c, c);              // row_mirror
+    float s = dpp_add_half_mirror_banks<0x5>(r, r);  // lanes 0-3, 8-11: the a / b partials
+    s = dpp_add_half_mirror_banks<0xa>(s, c);        // lanes 4-7, 12-15: the c partials
     s = dpp_pair_add<0xb1>(s, s);  // quad_perm [1, 0, 3, 2]
     s = dpp_pair_add<0x4e>(s, s);  // quad_perm [2, 3, 0, 1]
     return s;
@@ -756,7 +796,6 @@ __global__ void __launch_bounds__(kTile, 8) blend_bwd_kernel(BlendBwdParams P) {
     const int row = lane >> 4, l16 = lane & 15;
     // After the wave reduction below, lane 0 of row r holds the sum of g[ka], lane 8 that of
     // g[4 + ka] and lane 4 the row's partial for slot 8 + r; they alone add into LDS.
-    const bool hi8 = (l16 & 8) != 0, hi4 = (l16 & 4) != 0;
     const int ka = (row == 0) ? 0 : (row == 1) ? 2 : (row == 2) ? 1 : 3;
     const bool adds = l16 == 0 || l16 == 4 || l16 == 8;
     const int kslot = (l16 == 0 ? ka : l16 == 8 ? 4 + ka : 8 + row) + kAccSlots * (wave >> 1);
@@ -780,7 +819,7 @@ __global__ void __launch_bounds__(kTile, 8) blend_bwd_kernel(BlendBwdParams P) {
             const float dx = r0.x - px, dy = r0.y - py;
             const float sigma = blend_sigma(r0, r1, dx, dy);
             // bitwise: no short-circuit branch around the sigma_max read
-            const bool in_range = (idx <= bin_final) & (sigma >= 0.0f) & (sigma <= r1.z);
+            const bool in_range = (idx <= bin_final) & sigma_in_range(sigma, r1.z);
             if (__builtin_amdgcn_ballot_w64(in_range) == 0ull) continue;
             // Every lane computes and the lanes outside the accepted set are masked by selects
             // (an exec-masked instruction costs the same issue slot), so the wave reduction
@@ -810,7 +849,9 @@ __global__ void __launch_bounds__(kTile, 8) blend_bwd_kernel(BlendBwdParams P) {
             const float g0 = v0 * fac, g1 = v1 * fac, g2 = v2 * fac;
             const float g3 = hx * dx, g4 = hx * dy, g5 = hy * dy;  // g3, g5 whole
             const float g6 = hx, g7 = hy;
-            const float g8 = geo ? vis * v_alpha : 0.0f;
+            // the opacity term vis v_alpha is -v_sigma / o with the record's o, so the sum of
+            // v_sigma is carried and the readout divides by -o once per record
+            const float g8 = vs;
             const float g9 = kDepth ? vd * fac : 0.0f;
             // reduce-scatter over the wave: after the swaps, row r of qa holds g0/g2/g1/g3 and
             // of qb g4/g6/g5/g7 (rows 0..3); qc is g8 unswapped (each row reduces its own lanes)
@@ -820,7 +861,7 @@ __global__ void __launch_bounds__(kTile, 8) blend_bwd_kernel(BlendBwdParams P) {
             const float p45 = swap32_add(g4, g5), p67 = swap32_add(g6, g7);
             const float qa = swap16_add(p01, p23), qb = swap16_add(p45, p67);
             const float qc = kDepth ? swap32_add(g8, g9) : g8;
-            const float sum = row_reduce_scatter3(qa, qb, qc, hi8, hi4);
+            const float sum = row_reduce_scatter3(qa, qb, qc);
             // An empty use keeps the last DPP add in this block: sunk into the branch below it
             // would no longer fuse with its DPP move.
             asm volatile("" ::"v"(sum));
@@ -843,12 +884,16 @@ __global__ void __launch_bounds__(kTile, 8) blend_bwd_kernel(BlendBwdParams P) {
                 ACC(tid, 8 + r) = 0.0f;
                 ACC(tid, kAccSlots + 8 + r) = 0.0f;
             }
+            // v_opacity = sum vis v_alpha = -(sum v_sigma) / o (o >= 1/255 for every accepted
+            // pair; a record with none sums to zero, which stays zero)
+            float vsig;
             if constexpr (kDepth) {
-                s[8] = 2.0f * (part[0] + part[1]);
+                vsig = 2.0f * (part[0] + part[1]);
                 s[9] = 2.0f * (part[2] + part[3]);
             } else {
-                s[8] = 2.0f * ((part[0] + part[1]) + (part[2] + part[3]));
+                vsig = 2.0f * ((part[0] + part[1]) + (part[2] + part[3]));
             }
+            s[8] = vsig != 0.0f ? -vsig / L.r1[tid].y : 0.0f;
             if (my_pos >= 0 && my_pos < P.M) store_rgrad<NG>(P.rgrad, rg_off + my_pos, s);
         }
         __syncthreads();
