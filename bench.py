@@ -19,7 +19,15 @@ The JSON line carries:
 - stages: every stage's average duration per call (HIP events around each stage, in an untimed
   pass) with its algorithmic bytes or FLOPs per call and the achieved rate against MI355X's peak
   (HBM 8 TB/s for projection, depth range, emission, sort, bins and the projection backward;
-  FP32 157.3 TFLOP/s for the two blends).
+  FP32 157.3 TFLOP/s for the two blends). `work_per_call` / `frac` price the stage on the
+  path's algorithmic bytes (projection 44 N + 40 G, depth range 8 G, emission 4 G + 32 V + 8 M,
+  sort 64 M, bins 4 M + 16 T, projection backward 40 N + 80 G); `moved_per_call` /
+  `frac_moved` on the bytes this build's kernels move (the fused projection's colour reads and
+  record writes, the sort's positions and 16-bit key halves, the bins' 16-bit halves).
+- resort_path_frames_per_s: forward+backward frames/s through the reference's own call shape,
+  one library call per custom_vjp rule: project, rasterize (its own sort), the loss cotangent,
+  a rasterize backward that sorts again (splat_rasterize_bwd), the projection backward; the
+  value line's step keeps the forward's sorted lists and records instead.
 - cpu_baseline: the CPU oracle (the C restatement of the reference kernels, "port") timed on the
   host on one full forward+backward frame of the same workload, OpenMP over `cores` threads
   (the host's share, at most 16), and again on one thread (`single_thread`), with the CPU model.
@@ -114,29 +122,31 @@ def cpu_model() -> str:
     return "unknown"
 
 
-# Algorithmic work per call of each library stage: (bound, work, unit) from the workload counts
-# (G items, N gaussians, V visible items, M intersections, T tiles, Pc/Pr and Qc/Qr the
-# contributing / rejected pixel-gaussian pairs of the forward / backward walk). The step renders
+# Work per call of each library stage: (bound, algorithmic work, work this build moves, unit)
+# from the workload counts (G items, N gaussians, V visible items, M intersections, T tiles,
+# Pc/Pr and Qc/Qr the contributing / rejected pixel-gaussian pairs of the forward / backward
+# walk). Algorithmic bytes are the path's own (projection 44 N + 40 G, sort 64 M: four passes
+# reading and writing 8-byte pairs, bins 4 M + 16 T). What this build moves: the step renders
 # through splat_render_fwd, whose projection also reads the colours (12 B/gaussian) and writes the
-# packed blend records (64 B/item): 56 N + 104 G for the "project" stage.
+# packed blend records (64 B/item), 56 N + 104 G; its sort reads 4 + 4 + 2 + 2 B per key for the
+# digit counts and its scatters move 20 + 22 + 20 + 20 B per key (key, emission position, id; the
+# pass over bits 8-15 writes the keys' 16-bit high halves, which the last two passes and the bin
+# edges read), 94 M; the bins read those 16-bit halves, 2 M + 16 T.
 def stage_work(counts, N, T):
     G, V, M = counts["G"], counts["V"], counts["M"]
     fwd_flops = 26 * counts["Pc"] + 16 * counts["Pr"]
     bwd_flops = 65 * counts["Qc"] + 16 * counts["Qr"]
     return {
-        "project": ("hbm", 56 * N + 104 * G, "GB/s"),
-        "minmax": ("hbm", 8 * G, "GB/s"),
-        "emit": ("hbm", 4 * G + 32 * V + 8 * M, "GB/s"),
-        # four passes: counts read 4 + 4 + 2 + 2 B, scatters move 20 + 22 + 20 + 20 B per key
-        # (key, emission position, id; the pass over bits 8-15 writes the keys' 16-bit high
-        # halves, which the last two passes and the bin edges read)
-        "sort": ("hbm", 94 * M, "GB/s"),
-        "bins": ("hbm", 2 * M + 16 * T, "GB/s"),
-        "blend_fwd": ("valu", fwd_flops, "TFLOP/s"),
-        "blend_fwd_kernel": ("valu", fwd_flops, "TFLOP/s"),
-        "blend_bwd": ("valu", bwd_flops, "TFLOP/s"),
-        "blend_bwd_kernel": ("valu", bwd_flops, "TFLOP/s"),
-        "project_bwd": ("hbm", 40 * N + 80 * G, "GB/s"),
+        "project": ("hbm", 44 * N + 40 * G, 56 * N + 104 * G, "GB/s"),
+        "minmax": ("hbm", 8 * G, 8 * G, "GB/s"),
+        "emit": ("hbm", 4 * G + 32 * V + 8 * M, 4 * G + 32 * V + 8 * M, "GB/s"),
+        "sort": ("hbm", 64 * M, 94 * M, "GB/s"),
+        "bins": ("hbm", 4 * M + 16 * T, 2 * M + 16 * T, "GB/s"),
+        "blend_fwd": ("valu", fwd_flops, fwd_flops, "TFLOP/s"),
+        "blend_fwd_kernel": ("valu", fwd_flops, fwd_flops, "TFLOP/s"),
+        "blend_bwd": ("valu", bwd_flops, bwd_flops, "TFLOP/s"),
+        "blend_bwd_kernel": ("valu", bwd_flops, bwd_flops, "TFLOP/s"),
+        "project_bwd": ("hbm", 40 * N + 80 * G, 40 * N + 80 * G, "GB/s"),
     }
 
 
@@ -151,14 +161,70 @@ def stage_rates(cal, cal_steps, counts, N, T):
         per_call = ms / calls
         row = {"ms_per_call": round(per_call, 4), "calls_per_step": round(calls / cal_steps, 2)}
         if name in work:
-            bound, w, unit = work[name]
+            bound, w, moved, unit = work[name]
             scale = 1e12 if unit == "TFLOP/s" else 1e9
             rate = w / (per_call / 1e3) / scale
             peak = FP32_PEAK_TFLOPS if unit == "TFLOP/s" else HBM_PEAK_GBS
             row.update(bound=bound, work_per_call=int(w), achieved=round(rate, 2), unit=unit,
                        frac=round(rate / peak, 4))
+            if moved != w:
+                mrate = moved / (per_call / 1e3) / scale
+                row.update(moved_per_call=int(moved), achieved_moved=round(mrate, 2),
+                           frac_moved=round(mrate / peak, 4))
         out[name] = row
     return out
+
+
+def resort_path_ms(scene, params, vm, bg, target, steps, warmup=2):
+    """ms per fwd+bwd step through the reference's call shape (splax/_render.py:94-115 with the
+    custom_vjp rules of splax/_project/_project.py and splax/_rasterize/_rasterize.py): one
+    library call per rule, the rasterize backward sorting again (splat_rasterize_bwd, as the
+    reference's _rasterize_bwd_warp does at splax/_rasterize/_kernels.py:422), the MSE and its
+    image cotangent in torch (the caller's loss), per-camera colour / opacity rows summed in
+    torch for a batch."""
+    import torch
+
+    from splax_amd import _ops
+
+    B, n = scene.B, scene.n
+    H, W = scene.img_shape
+    dev = params[0].device
+    means, scales, quats, colors, opac = (p.detach() for p in params)
+    opac = opac.reshape(-1)
+    vmf = vm.detach().reshape(-1, 4)
+    tgt = target.reshape(B * H, W, 3)
+    tf = torch.zeros((1, 4, 4), device=dev)
+    tids = torch.full((1,), -1, device=dev, dtype=torch.int32)
+    want_vm = vm.requires_grad
+
+    def step():
+        xys, depths, radii, conics, _, cum = _ops.project_fwd(
+            means, scales, quats, vmf, opac, tf, tids, n=n, total=B * n, num_transforms=1,
+            has_transforms=False, img_shape=(H, W), f=scene.f, c=scene.c, glob_scale=1.0,
+            clip_thresh=0.01, quats_wxyz=True)
+        img, Ts, fidx, _ = _ops.rasterize_fwd(colors, opac, opac, bg, xys, depths, radii,
+                                              conics, cum, n=n, B=B, img_shape=(H, W))
+        d = img - tgt
+        loss = (d * d).mean()
+        v_out = d * (2.0 / d.numel())
+        vc, vo, vxy, vcon = _ops.rasterize_bwd(colors, opac, opac, bg, xys, depths, radii,
+                                               conics, cum, Ts, fidx, v_out.reshape(-1, 3), n=n,
+                                               B_out=B, B_geom=B, img_shape=(H, W))
+        if B > 1:
+            vc, vo = vc.reshape(B, n, 3).sum(0), vo.reshape(B, n).sum(0)
+        _ops.project_bwd(means, scales, quats, vmf, radii, conics, vxy, None, vcon, tf, tids,
+                         n=n, B=B, num_transforms=1, has_transforms=False, f=scene.f,
+                         glob_scale=1.0, quats_wxyz=True, fold=B > 1, want_viewmat=want_vm)
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
 
 
 def bench_train(args):
@@ -353,6 +419,7 @@ def main():
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     _lib.set_stage_timing(False)
     stages = _lib.stage_times()
+    resort_ms = resort_path_ms(scene, params, vm, bg, target, args.steps)
 
     counts = None
     cpu = None
@@ -384,7 +451,7 @@ def main():
             "blend_fwd": ("valu", (26 * counts["Pc"] + 16 * counts["Pr"]) / 1e12, "TFLOP/s",
                           FP32_PEAK_TFLOPS),
             "sort": ("hbm", 64 * M / 1e9, "GB/s", HBM_PEAK_GBS),
-            "project": ("hbm", (56 * scene.n + 104 * G) / 1e9, "GB/s", HBM_PEAK_GBS),
+            "project": ("hbm", (44 * scene.n + 40 * G) / 1e9, "GB/s", HBM_PEAK_GBS),
         }
         bound, work, unit, peak = cands[dom]
         dur_s = per_stage[timed] / 1e3
@@ -410,6 +477,8 @@ def main():
         "ms_per_step": round(ms, 4),
         "fwd_frames_per_s": round(B * 1e3 / fwd_ms, 3),
         "fwd_ms": round(fwd_ms, 4),
+        "resort_path_frames_per_s": round(B * 1e3 / resort_ms, 3),
+        "resort_path_ms": round(resort_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
