@@ -349,6 +349,17 @@ int splat_mcmc_relocate(splat_stream_t stream, float* means3d, float* log_scales
                         int32_t n_max, float min_opacity, uint64_t seed, int32_t* source,
                         uint8_t* reset);
 
+/* Replaces splax.mcmc.inject_noise (splax/mcmc.py:134-169): out_means [n,3] = means3d +
+ * Sigma (z sigmoid(100 (min_opacity - o)) scaler) with Sigma = R diag(exp(log_scales))^2 R^T
+ * (R of the normalized wxyz quats [n,4]), o = sigmoid(logit_opacities [n]) and z three standard
+ * normals per gaussian, read from noise [n,3] when it is not NULL, else drawn by Box-Muller from
+ * Philox4x32-10 keyed by seed (the reference draws with a JAX PRNG key). out_means may be
+ * means3d (in place). */
+int splat_mcmc_inject_noise(splat_stream_t stream, const float* means3d, const float* log_scales,
+                            const float* quats, const float* logit_opacities,
+                            int64_t num_gaussians, float scaler, float min_opacity,
+                            uint64_t seed, const float* noise, float* out_means);
+
 /* Replaces splax.mcmc.compute_relocation (splax/mcmc.py:44-71): opacities [n], scales [n,3],
  * ratios [n] (rounded, clipped to [1, n_max]) -> new_opacities [n], new_scales [n,3]. Evaluated
  * in double with exact binomial coefficients. */

@@ -15,6 +15,12 @@ the GPU library; the product package never does.
 - ``relocate``: splax/mcmc.py:74-131 with the library's exact draw (integer weights
   opacity * 2^32, inclusive uint64 prefix, u = floor(r * total / 2^64) from a Philox draw at
   counter (i, 0, tag, 0), first index whose prefix exceeds u).
+- ``noise_normals``: the library's standard normals for ``inject_noise``: Philox at counter
+  (i_lo, i_hi, NOISE_TAG, 0), each word's top 23 bits as u = (k + 1/2) 2^-23, and Box-Muller
+  (z0, z1) = sqrt(-2 ln u0) (cos, sin)(2 pi u1), z2 = sqrt(-2 ln u2) cos(2 pi u3), in double.
+- ``inject_noise``: splax/mcmc.py:134-169 in double: means + R diag(s)^2 R^T (z gate scaler)
+  with s = exp(log_scales), R the rotation of the normalized wxyz quaternion and
+  gate = sigmoid(100 (min_opacity - sigmoid(logit))).
 """
 
 from __future__ import annotations
@@ -28,6 +34,7 @@ from oracle import oracle as O
 PHILOX_M = (0xD2511F53, 0xCD9E8D57)
 PHILOX_W = (0x9E3779B9, 0xBB67AE85)
 RELOCATE_TAG = 0x4D434D43
+NOISE_TAG = 0x4E4F4953
 _M32 = np.uint64(0xFFFFFFFF)
 
 
@@ -168,6 +175,48 @@ def relocate(seed: int, means, log_scales, quats, logit_colors, logit_opacities,
             out_means[i], out_q[i], out_c[i] = means[s], quats[s], colors[s]
         out_l[i], out_ls[i] = newv[s]
     return out_means, out_ls, out_q, out_c, out_l, src.astype(np.int32), reset
+
+
+# ---------------------------------------------------------------- noise on the means
+
+def noise_uniforms(seed: int, n: int) -> np.ndarray:
+    """(n, 4) uniforms (k + 1/2) 2^-23 from the top 23 bits of each Philox word."""
+    i = np.arange(n, dtype=np.uint64)
+    c = philox4x32_10((i & _M32, i >> np.uint64(32), np.full(n, NOISE_TAG, np.uint64),
+                       np.zeros(n, np.uint64)), (seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF))
+    return np.stack([((np.asarray(w, np.uint64) >> np.uint64(9)).astype(np.float64) + 0.5)
+                     * 2.0**-23 for w in c], axis=1)
+
+
+def noise_normals(seed: int, n: int) -> np.ndarray:
+    """(n, 3) standard normals by Box-Muller on noise_uniforms, in double."""
+    u = noise_uniforms(seed, n)
+    r0, r1 = np.sqrt(-2.0 * np.log(u[:, 0])), np.sqrt(-2.0 * np.log(u[:, 2]))
+    t0, t1 = 2.0 * np.pi * u[:, 1], 2.0 * np.pi * u[:, 3]
+    return np.stack([r0 * np.cos(t0), r0 * np.sin(t0), r1 * np.cos(t1)], axis=1)
+
+
+def quat_wxyz_to_rot(q) -> np.ndarray:
+    """Rotation matrices (n, 3, 3) of the normalized wxyz quaternions, in double."""
+    q = np.asarray(q, np.float64).reshape(-1, 4)
+    w, x, y, z = (q / np.linalg.norm(q, axis=1, keepdims=True)).T
+    return np.stack([
+        np.stack([1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y)], -1),
+        np.stack([2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x)], -1),
+        np.stack([2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)], -1),
+    ], axis=1)
+
+
+def inject_noise(means, log_scales, quats, logit_opacities, scaler: float, noise,
+                 min_opacity: float = 0.005) -> np.ndarray:
+    """splax/mcmc.py:134-169 in double with the given standard normals noise (n, 3)."""
+    means = np.asarray(means, np.float64).reshape(-1, 3)
+    s = np.exp(np.asarray(log_scales, np.float64).reshape(-1, 3))
+    o = 1.0 / (1.0 + np.exp(-np.asarray(logit_opacities, np.float64).reshape(-1)))
+    gate = 1.0 / (1.0 + np.exp(-100.0 * (float(min_opacity) - o)))
+    w = np.asarray(noise, np.float64).reshape(-1, 3) * (gate * float(scaler))[:, None]
+    m = quat_wxyz_to_rot(quats) * s[:, None, :]  # R diag(s), Sigma = m m^T
+    return means + np.einsum("nij,nkj,nk->ni", m, m, w)
 
 
 # ---------------------------------------------------------------- render_log map and L1 loss

@@ -61,6 +61,7 @@ _SIGS = {
     "splat_adam_reset_rows": [_vp, _vp, _i32, _vp, _i64],
     "splat_mcmc_relocate": [_vp] + [_vp] * 5 + [_i64, _i32, _f32, _u64, _vp, _vp],
     "splat_mcmc_compute_relocation": [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp],
+    "splat_mcmc_inject_noise": [_vp] + [_vp] * 4 + [_i64, _f32, _f32, _u64, _vp, _vp],
     "splat_log_params_fwd": [_vp] + [_vp] * 4 + [_i64] + [_vp] * 4,
     "splat_log_params_bwd": [_vp] + [_vp] * 4 + [_i64] + [_vp] * 8,
     "splat_l1_loss_fwd": [_vp, _vp, _vp, _i64, _vp, _vp],
@@ -79,7 +80,7 @@ STAGES = ("project", "minmax", "emit", "sort", "bins", "blend_fwd", "blend_bwd",
           "blend_fwd_kernel", "blend_bwd_kernel")
 
 # splat_abi_version() of the library this binding was written for (include/splat_hip.h)
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 # status codes (splax_amd/csrc/splat_internal.hpp)
 ERR_ARGS, ERR_KEY_OVERFLOW, ERR_TOO_MANY = 1, 2, 6

@@ -3,7 +3,8 @@
 //     scale_by_learning_rate, then apply_updates) as the trainers configure it per parameter
 //     group (scripts/train_lego.py:203-211), and the moment reset of relocated rows
 //     (scripts/train_lego.py:136-146);
-//   - the fixed-budget MCMC relocation, splax/mcmc.py:29-131.
+//   - the fixed-budget MCMC relocation, splax/mcmc.py:29-131, and the trainers' noise on the
+//     means, splax/mcmc.py:134-169.
 //
 // Adam arithmetic per element (float32, no contraction): mu = c1 g + b1 mu; nu = c2 (g g) + b2 nu;
 // u = (mu / bc1) / (sqrt(nu / bc2 + eps_root) + eps); p = p + (-lr) u, with c1 = f32(1 - b1),
@@ -112,6 +113,73 @@ __device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32
         const uint32_t n3 = (uint32_t)p0;
         c[0] = n0; c[1] = n1; c[2] = n2; c[3] = n3;
     }
+}
+
+// ------------------------------------------------------------------ noise injection
+// inject_noise, splax/mcmc.py:134-169: means + Sigma (z sigmoid(100 (min_opacity - o)) scaler),
+// Sigma = M M^T with M = R diag(exp(log_scales)), R the rotation of the normalized wxyz
+// quaternion (scipy's from_quat normalizes), o = sigmoid(logit) and z three standard normals
+// per gaussian: from the caller (noise) or drawn here by Box-Muller on the four words of
+// Philox4x32-10 at counter (i, tag) under the caller's seed, each word's top 23 bits giving a
+// uniform (k + 1/2) 2^-23 in [2^-24, 1 - 2^-24] (k + 1/2 fits float32's 24-bit significand, so u
+// is exact and |z| <= sqrt(48 ln 2) < 5.8). Float32 throughout; the reference draws its normals with
+// jax.random.normal, so the distribution is the reference's and the stream the library's.
+constexpr uint32_t kNoiseTag = 0x4e4f4953u;  // counter word 2 of the noise draws
+
+struct NoiseParams {
+    const float* means; const float* log_scales; const float* quats; const float* logit_opac;
+    const float* noise;  // [n, 3] standard normals, or null to draw them
+    float* out;
+    int64_t n;
+    float scaler, min_opacity;
+    uint32_t seed_lo, seed_hi;
+};
+
+__global__ void __launch_bounds__(256) inject_noise_kernel(NoiseParams P) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= P.n) return;
+    float z[3];
+    if (P.noise) {
+        z[0] = P.noise[3 * i];
+        z[1] = P.noise[3 * i + 1];
+        z[2] = P.noise[3 * i + 2];
+    } else {
+        uint32_t c[4] = {(uint32_t)i, (uint32_t)((uint64_t)i >> 32), kNoiseTag, 0u};
+        philox4x32_10(c, P.seed_lo, P.seed_hi);
+        float u[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) u[k] = ((float)(c[k] >> 9) + 0.5f) * 0x1p-23f;
+        const float r0 = sqrtf(-2.0f * logf(u[0])), r1 = sqrtf(-2.0f * logf(u[2]));
+        const float t0 = 6.28318530717958647692f * u[1], t1 = 6.28318530717958647692f * u[3];
+        z[0] = r0 * cosf(t0);
+        z[1] = r0 * sinf(t0);
+        z[2] = r1 * cosf(t1);
+    }
+    const float o = 1.0f / (1.0f + expf(-P.logit_opac[i]));
+    const float gate = 1.0f / (1.0f + expf(-(100.0f * (P.min_opacity - o))));
+    const float a = gate * P.scaler;
+    const float w[3] = {z[0] * a, z[1] * a, z[2] * a};
+    const float* q = P.quats + 4 * i;
+    const float qn = sqrtf(((q[0] * q[0] + q[1] * q[1]) + q[2] * q[2]) + q[3] * q[3]);
+    const float qw = q[0] / qn, qx = q[1] / qn, qy = q[2] / qn, qz = q[3] / qn;
+    const float R[9] = {1.0f - 2.0f * (qy * qy + qz * qz), 2.0f * (qx * qy - qw * qz),
+                        2.0f * (qx * qz + qw * qy),        2.0f * (qx * qy + qw * qz),
+                        1.0f - 2.0f * (qx * qx + qz * qz), 2.0f * (qy * qz - qw * qx),
+                        2.0f * (qx * qz - qw * qy),        2.0f * (qy * qz + qw * qx),
+                        1.0f - 2.0f * (qx * qx + qy * qy)};
+    float s[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) s[k] = expf(P.log_scales[3 * i + k]);
+    // Sigma w = M (M^T w): t = diag(s) R^T w, then R diag(s) t
+    float t[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) t[k] = s[k] * ((R[k] * w[0] + R[3 + k] * w[1]) + R[6 + k] * w[2]);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) t[k] = s[k] * t[k];
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+        P.out[3 * i + r] = P.means[3 * i + r] + ((R[3 * r] * t[0] + R[3 * r + 1] * t[1]) +
+                                                 R[3 * r + 2] * t[2]);
 }
 
 // ------------------------------------------------------------------ relocation
@@ -504,6 +572,21 @@ int splat_mcmc_relocate(splat_stream_t stream, float* means3d, float* log_scales
     if ((rc = launched("relocate values"))) return rc;
     hipLaunchKernelGGL(reloc_apply_kernel, dim3(rows), dim3(256), 0, s, P);
     return launched("relocate apply");
+}
+
+int splat_mcmc_inject_noise(splat_stream_t stream, const float* means3d, const float* log_scales,
+                            const float* quats, const float* logit_opacities,
+                            int64_t num_gaussians, float scaler, float min_opacity,
+                            uint64_t seed, const float* noise, float* out_means) {
+    if (num_gaussians < 0) return fail(kErrArgs, "inject_noise: negative count");
+    if (num_gaussians == 0) return 0;
+    if (!means3d || !log_scales || !quats || !logit_opacities || !out_means)
+        return fail(kErrArgs, "inject_noise: missing arrays");
+    NoiseParams P{means3d, log_scales, quats, logit_opacities, noise, out_means,
+                  num_gaussians, scaler, min_opacity, (uint32_t)seed, (uint32_t)(seed >> 32)};
+    hipLaunchKernelGGL(inject_noise_kernel, dim3(grid_for(num_gaussians, 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), P);
+    return launched("inject_noise");
 }
 
 int splat_mcmc_compute_relocation(splat_stream_t stream, const float* opacities,

@@ -3,11 +3,14 @@
 ``relocate`` teleports dead gaussians (opacity at or below ``min_opacity``) onto alive ones drawn
 in proportion to opacity, and corrects opacity and scale so that gaussians sharing a location keep
 the source's contribution (the relocation of gsplat's MCMC strategy, splax/mcmc.py:44-131).
+``inject_noise`` perturbs the means with noise shaped by each gaussian's covariance and gated by
+its opacity (splax/mcmc.py:134-169).
 
 Differences of substance from the reference, all in ``include/splat_hip.h``:
 - ``key`` is an integer seed of the library's Philox4x32-10 draw instead of a JAX PRNG key; the
   draw's distribution is the reference's (categorical over log-opacities of the alive gaussians,
-  i.e. probability proportional to opacity) and exact, but its random stream is the library's.
+  i.e. probability proportional to opacity; standard normals for the noise) and exact, but its
+  random stream is the library's.
 - ``compute_relocation`` is evaluated in double with exact binomial coefficients, so it agrees
   with gsplat's double loop to float32 rounding; the table argument fixes only its size.
 """
@@ -98,3 +101,45 @@ def relocate(key: int, means3d: torch.Tensor, log_scales: torch.Tensor, quats: t
                                                          logit_colors, logit_opacities))
     reset = relocate_(key, *new, binoms, min_opacity)
     return new, reset
+
+
+def inject_noise(key: int, means3d: torch.Tensor, log_scales: torch.Tensor, quats: torch.Tensor,
+                 logit_opacities: torch.Tensor, scaler: float, min_opacity: float = 0.005,
+                 noise: torch.Tensor | None = None, *,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Means perturbed by covariance- and opacity-weighted noise (splax/mcmc.py:134-169).
+
+    Returns ``means3d + Sigma (z * sigmoid(100 (min_opacity - o)) * scaler)`` of shape (N, 3),
+    with ``Sigma = R diag(exp(log_scales))^2 R^T`` (R from the normalized wxyz ``quats``),
+    ``o = sigmoid(logit_opacities)`` and ``z`` standard normals: ``noise`` (N, 3) when given,
+    else drawn on the device from Philox4x32-10 under ``key`` (the reference draws with
+    ``jax.random.normal``; same distribution, another stream). ``out`` (a contiguous float32
+    (N, 3) tensor on the means' device, ``means3d`` itself for an in-place update) receives the
+    result when given.
+    """
+    m = _f32c(means3d, "means3d").reshape(-1, 3)
+    n = m.shape[0]
+    ls = _f32c(log_scales, "log_scales").reshape(-1)
+    q = _f32c(quats, "quats").reshape(-1)
+    lo = _f32c(logit_opacities, "logit_opacities").reshape(-1)
+    if ls.numel() != 3 * n or q.numel() != 4 * n or lo.numel() != n:
+        raise ValueError("log_scales, quats and logit_opacities must have 3, 4 and 1 values per "
+                         f"gaussian for {n} gaussians")
+    if out is not None and (out.dtype != torch.float32 or not out.is_contiguous()
+                            or out.numel() != 3 * n or out.device != m.device):
+        raise ValueError("out must be a contiguous float32 (N, 3) tensor on the means' device")
+    z = None
+    if noise is not None:
+        z = _f32c(noise, "noise").reshape(-1)
+        if z.numel() != 3 * n:
+            raise ValueError(f"noise must have shape ({n}, 3), got {tuple(noise.shape)}")
+    dev = _lib.require_gpu(m, ls, q, lo, *(() if z is None else (z,)))
+    if out is None:
+        out = torch.empty_like(m)
+    with torch.cuda.device(dev):
+        st = _lib.lib().splat_mcmc_inject_noise(
+            _lib.stream_handle(dev), _lib.ptr(m), _lib.ptr(ls), _lib.ptr(q), _lib.ptr(lo), n,
+            float(scaler), float(min_opacity), int(key) & 0xFFFFFFFFFFFFFFFF,
+            _lib.ptr(z), _lib.ptr(out))
+    _lib.check(st, "inject_noise")
+    return out.reshape(means3d.shape)

@@ -9,7 +9,10 @@ gaussian budget with the loss reduced to L1:
   3. one fused Adam update of the five parameter groups (optax.adam per group,
      scripts/train_lego.py:203-211, exponential decay on the means' learning rate);
   4. one MCMC relocation (splax/mcmc.py:74-131) and the moment reset of the relocated rows
-     (scripts/train_lego.py:136-146, 217-222).
+     (scripts/train_lego.py:136-146, 217-222);
+  5. with ``noise_lr > 0`` (off by default, as config 4 times it), the means' noise of the
+     reference trainer (scripts/train_lego.py:224-229,277-284): ``inject_noise`` at strength
+     means-learning-rate(step) * noise_lr.
 """
 
 from __future__ import annotations
@@ -103,7 +106,8 @@ class TrainStep:
                  f: tuple[float, float], c: tuple[float, float] | None = None,
                  antialiased: bool = True, steps: int = 30_000,
                  lrs: Mapping[str, float] | None = None, min_opacity: float = 0.005,
-                 n_max: int = 51, relocate_every: int = 1, seed: int = 0):
+                 n_max: int = 51, relocate_every: int = 1, seed: int = 0,
+                 noise_lr: float = 0.0):
         if tuple(params) != SPLAT_KEYS:
             raise ValueError(f"params must hold {SPLAT_KEYS} in this order")
         self.params = {k: p.detach().contiguous() for k, p in params.items()}
@@ -111,6 +115,8 @@ class TrainStep:
         sched = dict(lr)
         sched["means"] = exponential_decay(lr["means"], steps, 0.01)  # train_lego.py:203
         self.opt = Adam(self.params, sched)
+        self.means_lr = sched["means"]
+        self.noise_lr = float(noise_lr)
         self.viewmats = viewmats
         self.targets = targets
         self.background = background
@@ -142,4 +148,10 @@ class TrainStep:
             key = (self.seed << 32) ^ self.step_idx
             reset = mcmc.relocate_(key, *self.params.values(), self.binoms, self.min_opacity)
             self.opt.reset_rows(reset)
+        if self.noise_lr > 0:
+            key = (self.seed << 32) ^ self.step_idx
+            p = self.params
+            mcmc.inject_noise(key, p["means"], p["log_scales"], p["quats"], p["opac_logit"],
+                              self.means_lr(self.step_idx) * self.noise_lr, self.min_opacity,
+                              out=p["means"])
         return loss

@@ -9,6 +9,13 @@
   size (3M gaussians) through size-independent properties: determinism, alive sources, rows
   sharing a source carry identical values, r copies of the new opacity compose to the old one,
   and the draw frequencies follow opacity.
+- inject_noise: with the caller's normals, the displacement within 1e-5 relative Frobenius (and
+  per element within 1e-5 of the largest) of the oracle's float64 transform (float32 exp,
+  sigmoid and rotation on the device, double in the oracle); with the device's own Philox draw,
+  the same bar against the oracle's float64 Box-Muller of the same Philox words (the stream
+  itself is pinned); at 1M gaussians the normals' moments, correlations and Kolmogorov-Smirnov
+  distance; determinism per key; in place equal to out of place; the reference's opacity check
+  (tests/test_mcmc.py:102-114); and the trainer's noise equal to the call on its parameters.
 """
 
 from __future__ import annotations
@@ -224,6 +231,122 @@ def test_relocate_config4_size_properties():
     exp = mass / mass.sum() * d.size
     chi2 = float(((hist - exp) ** 2 / exp).sum())
     assert chi2 < 27.9, (hist, exp, chi2)  # p = 0.001 at 9 degrees of freedom
+    assert _lib.check_device() == 0
+
+
+def _noise_inputs(n, seed):
+    rng = np.random.default_rng(seed)
+    means = rng.normal(scale=2.0, size=(n, 3)).astype(np.float32)
+    ls = rng.normal(loc=-2.0, scale=0.8, size=(n, 3)).astype(np.float32)
+    q = (rng.normal(size=(n, 4)) * rng.uniform(0.3, 2.0, size=(n, 1))).astype(np.float32)
+    logit = rng.normal(loc=-3.0, scale=3.0, size=(n, 1)).astype(np.float32)
+    return means, ls, q, logit
+
+
+def _assert_displacement(got, ref, means, label):
+    """got = fl32(means + d) against ref = means + d_ref in double: the final rounding costs at
+    most half an ulp of the sum (2^-24 |ref| up to the ulp's own rounding); what exceeds it is
+    the displacement's error, held to 1e-5 relative Frobenius and per element to 1e-5 of the
+    largest displacement."""
+    got = np.asarray(got, np.float64)
+    d_ref = np.asarray(ref, np.float64) - means
+    excess = np.maximum(np.abs(got - ref) - 2.0**-24 * (1.0 + 2.0**-20) * np.abs(ref), 0.0)
+    err = np.linalg.norm(excess) / max(np.linalg.norm(d_ref), 1e-30)
+    assert err < 1e-5, (label, err)
+    assert (excess <= 1e-5 * np.abs(d_ref).max()).all(), label
+
+
+@pytest.mark.parametrize("n,seed", [(1, 0), (1000, 1), (65_537, 2)])
+def test_inject_noise_given_normals(n, seed):
+    _case(f"inject_noise given normals n={n} seed={seed}")
+    means, ls, q, logit = _noise_inputs(n, seed)
+    z = np.random.default_rng(seed + 100).normal(size=(n, 3)).astype(np.float32)
+    got = _np(mcmc.inject_noise(0, _t(means), _t(ls), _t(q), _t(logit), 0.05, 0.01,
+                                noise=_t(z)))
+    ref = T.inject_noise(means, ls, q, logit, 0.05, z, 0.01)
+    assert got.shape == (n, 3)
+    _assert_displacement(got, ref, means.astype(np.float64), f"n={n}")
+    assert _lib.check_device() == 0
+
+
+@pytest.mark.parametrize("n,key", [(1, 5), (4099, 0x0123_4567_89AB_CDEF)])
+def test_inject_noise_drawn_normals_follow_the_philox_stream(n, key):
+    _case(f"inject_noise drawn normals n={n} key={key:#x}")
+    means, ls, q, logit = _noise_inputs(n, 7)
+    got = _np(mcmc.inject_noise(key, _t(means), _t(ls), _t(q), _t(logit), 0.5))
+    ref = T.inject_noise(means, ls, q, logit, 0.5, T.noise_normals(key, n))
+    _assert_displacement(got, ref, means.astype(np.float64), f"n={n}")
+
+
+def test_inject_noise_normals_law_at_1m():
+    """Identity rotation and unit scales: the displacement is z * gate * scaler exactly up to
+    float32 rounding, so z is recovered and tested against the standard normal law."""
+    from scipy import stats
+
+    _case("inject_noise normal law n=1M")
+    n = 1 << 20
+    means = torch.zeros((n, 3), device="cuda")
+    ls = torch.zeros((n, 3), device="cuda")
+    q = torch.tensor([1.0, 0.0, 0.0, 0.0], device="cuda").repeat(n, 1)
+    logit = torch.full((n, 1), -40.0, device="cuda")
+    out = _np(mcmc.inject_noise(11, means, ls, q, logit, 1.0, min_opacity=0.5))
+    gate = 1.0 / (1.0 + math.exp(-100.0 * (0.5 - 1.0 / (1.0 + math.exp(40.0)))))
+    z = out.astype(np.float64) / gate
+    # float32 log / sqrt / cos / sin of the same exact uniforms: 1.7e-6 at most, measured
+    np.testing.assert_allclose(z, T.noise_normals(11, n), rtol=1e-5, atol=5e-6)
+    assert np.abs(z.mean(axis=0)).max() < 5 * n ** -0.5
+    assert np.abs(z.var(axis=0) - 1.0).max() < 5 * (2.0 / n) ** 0.5
+    assert np.abs(np.corrcoef(z.T) - np.eye(3)).max() < 5 * n ** -0.5
+    for k in range(3):
+        assert stats.kstest(z[:, k], "norm").pvalue > 1e-3, k
+    assert np.isfinite(z).all() and np.abs(z).max() < 5.8  # u >= 2^-24 bounds |z| by 5.77
+
+
+def test_inject_noise_determinism_in_place_and_opacity():
+    _case("inject_noise determinism / in place / opacity")
+    n = 400
+    means = torch.zeros((n, 3), device="cuda")
+    ls = torch.full((n, 3), math.log(0.1), device="cuda")
+    q = torch.tensor([1.0, 0.0, 0.0, 0.0], device="cuda").repeat(n, 1)
+    logit = torch.cat([torch.full((200, 1), -5.0), torch.full((200, 1), 8.0)]).cuda()
+    a = mcmc.inject_noise(2, means, ls, q, logit, scaler=100.0)
+    b = mcmc.inject_noise(2, means, ls, q, logit, scaler=100.0)
+    c = mcmc.inject_noise(3, means, ls, q, logit, scaler=100.0)
+    assert torch.equal(a, b) and not torch.equal(a, c)
+    disp = np.linalg.norm(_np(a), axis=1)
+    assert disp[:200].mean() > 10 * disp[200:].mean() + 1e-6  # tests/test_mcmc.py:102-114
+    m2 = means.clone()
+    r = mcmc.inject_noise(2, m2, ls, q, logit, scaler=100.0, out=m2)
+    assert r.data_ptr() == m2.data_ptr() and torch.equal(m2, a)
+    empty = torch.zeros((0, 3), device="cuda")
+    assert mcmc.inject_noise(0, empty, empty, torch.zeros((0, 4), device="cuda"),
+                             torch.zeros((0, 1), device="cuda"), 1.0).shape == (0, 3)
+    assert _lib.check_device() == 0
+
+
+def test_train_step_noise_equals_the_call():
+    """TrainStep(noise_lr > 0) adds inject_noise at means-lr(step) * noise_lr after the Adam
+    update and relocation (scripts/train_lego.py:277-284): one step with noise equals one step
+    without, followed by the call with the trainer's key."""
+    from splax_amd.scenes import make_scene
+    from splax_amd.train import TrainStep, params_from_scene
+
+    _case("train step with noise n=20000")
+    scene = make_scene(4, n=20_000)
+    kw = dict(viewmats=_t(scene.viewmats), targets=_t(scene.targets),
+              background=_t(scene.background), img_shape=scene.img_shape, f=scene.f, seed=9)
+    noisy = TrainStep(params_from_scene(scene), noise_lr=5e5, **kw)
+    plain = TrainStep(params_from_scene(scene), **kw)
+    noisy()
+    plain()
+    p = plain.params
+    want = mcmc.inject_noise((9 << 32) ^ 1, p["means"], p["log_scales"], p["quats"],
+                             p["opac_logit"], plain.means_lr(1) * 5e5, plain.min_opacity)
+    for k in p:
+        if k != "means":
+            assert torch.equal(noisy.params[k], p[k]), k
+    assert torch.equal(noisy.params["means"], want)
+    assert not torch.equal(want, p["means"])
     assert _lib.check_device() == 0
 
 

@@ -327,6 +327,33 @@ def test_missing_required_buffers_are_rejected():
         assert render_bwd(**{k: None}) == _lib.ERR_ARGS, k
         assert b"missing" in lib.splat_last_error(), k
 
+    def noise(**null):
+        a = dict(means=buf, ls=buf, quats=buf, logit=buf, out=buf)
+        a.update(null)
+        return lib.splat_mcmc_inject_noise(None, a["means"], a["ls"], a["quats"], a["logit"], n,
+                                           1.0, 0.005, 0, None, a["out"])
+
+    for k in ("means", "ls", "quats", "logit", "out"):
+        assert noise(**{k: None}) == _lib.ERR_ARGS, k
+        assert b"inject_noise: missing arrays" in lib.splat_last_error(), k
+    assert lib.splat_mcmc_inject_noise(None, buf, buf, buf, buf, -1, 1.0, 0.005, 0, None,
+                                       buf) == _lib.ERR_ARGS
+    assert b"negative count" in lib.splat_last_error()
+
+
+def test_inject_noise_validates_shapes_before_the_device():
+    from splax_amd import mcmc
+
+    m, ls, q, lo = torch.zeros(4, 3), torch.zeros(4, 3), torch.zeros(4, 4), torch.zeros(4, 1)
+    with pytest.raises(ValueError, match="values per"):
+        mcmc.inject_noise(0, m, ls, q[:3], lo, 1.0)
+    with pytest.raises(ValueError, match="noise must have shape"):
+        mcmc.inject_noise(0, m, ls, q, lo, 1.0, noise=torch.zeros(4, 2))
+    with pytest.raises(ValueError, match="out must be"):
+        mcmc.inject_noise(0, m, ls, q, lo, 1.0, out=torch.zeros(4, 3, dtype=torch.float64))
+    with pytest.raises(ValueError, match="float32"):
+        mcmc.inject_noise(0, m.double(), ls, q, lo, 1.0)
+
 
 def test_backward_requires_the_final_buffers():
     """A forward-only render may leave final_Ts / final_idx out; the backward entry points

@@ -12,6 +12,13 @@
 - relocate: the reference's invariants (tests/test_mcmc.py:63-99: dead rows reset, new opacity
   above the threshold, relocated means on alive sources), a draw brute-forced with Python
   integers, and a chi-square test of the draw frequencies against opacity.
+- noise_normals: the uniforms brute-forced with Python integers, the Box-Muller identity
+  z0^2 + z1^2 = -2 ln u0, and the moments, cross-correlations and Kolmogorov-Smirnov distance of
+  the normals against the standard normal law.
+- inject_noise: the covariance against scipy's Rotation (an independent quaternion routine),
+  the closed forms of the identity rotation and of the opacity gate (1/2 at the threshold), the
+  symmetry of Sigma, and the reference's own check that transparent gaussians move at least ten
+  times as far as opaque ones (tests/test_mcmc.py:102-114).
 """
 
 from __future__ import annotations
@@ -267,3 +274,92 @@ def test_mse_loss_closed_form_and_torch():
     (2.0 * ref).backward()
     assert abs(float(loss) - ref.item()) <= 1e-6 * ref.item()
     np.testing.assert_allclose(v, x.grad.numpy(), rtol=1e-6, atol=0)
+
+
+def test_noise_uniforms_brute_force():
+    seed = 0x1234_5678_9ABC_DEF0
+    u = T.noise_uniforms(seed, 5)
+    for i in range(5):
+        c = T.philox4x32_10((i, 0, T.NOISE_TAG, 0), (seed & 0xFFFFFFFF, seed >> 32))
+        want = [((int(w) >> 9) + 0.5) / 2**23 for w in c]
+        assert list(u[i]) == want
+    assert (u > 0).all() and (u < 1).all()
+    assert (u.astype(np.float32).astype(np.float64) == u).all()  # exact in float32
+
+
+def test_noise_normals_box_muller_identity_and_law():
+    from scipy import stats
+
+    n = 400_000
+    z = T.noise_normals(7, n)
+    u = T.noise_uniforms(7, n)
+    np.testing.assert_allclose(z[:, 0] ** 2 + z[:, 1] ** 2, -2.0 * np.log(u[:, 0]), rtol=1e-12)
+    assert np.abs(z.mean(axis=0)).max() < 5 * n ** -0.5
+    assert np.abs(z.var(axis=0) - 1.0).max() < 5 * (2.0 / n) ** 0.5
+    c = np.corrcoef(z.T)
+    assert np.abs(c - np.eye(3)).max() < 5 * n ** -0.5
+    for k in range(3):
+        assert stats.kstest(z[:, k], "norm").pvalue > 1e-3, k
+    # a planted mistake: the same uniform for radius and angle is visibly not normal
+    bad = np.sqrt(-2.0 * np.log(u[:, 0])) * np.cos(2.0 * np.pi * u[:, 0])
+    assert stats.kstest(bad, "norm").pvalue < 1e-6
+
+
+def test_inject_noise_covariance_matches_scipy():
+    from scipy.spatial.transform import Rotation
+
+    rng = np.random.default_rng(3)
+    n = 64
+    means = rng.normal(size=(n, 3))
+    ls = rng.normal(scale=0.7, size=(n, 3))
+    q = rng.normal(size=(n, 4)) * rng.uniform(0.2, 3.0, size=(n, 1))  # not unit on purpose
+    logit = rng.normal(scale=4.0, size=(n, 1))
+    z = rng.normal(size=(n, 3))
+    scaler, mo = 0.37, 0.01
+    got = T.inject_noise(means, ls, q, logit, scaler, z, mo)
+    R = Rotation.from_quat(q, scalar_first=True).as_matrix()
+    s2 = np.exp(2.0 * ls)
+    o = 1.0 / (1.0 + np.exp(-logit[:, 0]))
+    gate = 1.0 / (1.0 + np.exp(-100.0 * (mo - o)))
+    want = np.empty_like(means)
+    for i in range(n):
+        sigma = R[i] @ np.diag(s2[i]) @ R[i].T
+        assert np.allclose(sigma, sigma.T)
+        want[i] = means[i] + sigma @ (z[i] * gate[i] * scaler)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    # planted mistakes: m^T m in place of m m^T, and the conjugate rotation, both differ
+    m = T.quat_wxyz_to_rot(q) * np.exp(ls)[:, None, :]
+    wrong = means + np.einsum("nji,njk,nk->ni", m, m, z * (gate * scaler)[:, None])
+    assert np.abs(wrong - want).max() > 1e-3
+    qc = q * np.array([1.0, -1.0, -1.0, -1.0])
+    assert np.abs(T.inject_noise(means, ls, qc, logit, scaler, z, mo) - want).max() > 1e-3
+
+
+def test_inject_noise_closed_forms():
+    n = 6
+    means = np.arange(3 * n, dtype=np.float64).reshape(n, 3)
+    ls = np.log(np.array([[0.5, 2.0, 3.0]] * n))
+    q = np.tile([2.0, 0.0, 0.0, 0.0], (n, 1))  # identity after normalization
+    mo = 0.2
+    logit = np.full((n, 1), np.log(mo / (1.0 - mo)))  # opacity exactly at the threshold
+    z = np.ones((n, 3))
+    got = T.inject_noise(means, ls, q, logit, 4.0, z, mo)
+    np.testing.assert_allclose(got - means, np.tile([0.25 * 2.0, 4.0 * 2.0, 9.0 * 2.0], (n, 1)),
+                               rtol=1e-12)
+    # a rotation by 90 degrees about z swaps the x and y variances
+    q90 = np.tile([np.cos(np.pi / 4), 0.0, 0.0, np.sin(np.pi / 4)], (n, 1))
+    got = T.inject_noise(means, ls, q90, logit, 4.0, z, mo)
+    np.testing.assert_allclose(got - means, np.tile([4.0 * 2.0, 0.25 * 2.0, 9.0 * 2.0], (n, 1)),
+                               rtol=1e-12)
+
+
+def test_inject_noise_respects_opacity():
+    """The reference's check (tests/test_mcmc.py:102-114) on the oracle with its own normals."""
+    n = 400
+    means = np.zeros((n, 3))
+    ls = np.full((n, 3), np.log(0.1))
+    q = np.tile([1.0, 0.0, 0.0, 0.0], (n, 1))
+    logit = np.concatenate([np.full((200, 1), -5.0), np.full((200, 1), 8.0)])
+    moved = T.inject_noise(means, ls, q, logit, 100.0, T.noise_normals(2, n))
+    disp = np.linalg.norm(moved, axis=1)
+    assert disp[:200].mean() > 10 * disp[200:].mean() + 1e-6
