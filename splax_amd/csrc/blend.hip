@@ -903,8 +903,9 @@ __global__ void __launch_bounds__(kTile, 8) blend_bwd_kernel(BlendBwdParams P) {
 #undef ACC
 
 // Per output item: sum of its intersections' partial gradients in emission order (fixed, so
-// deterministic) in double, then v_xy = (a Sx + b Sy, b Sx + c Sy) with the item's conic
-// (a, b, c), in double, which equals the reference's per-pair sum of
+// deterministic; the conic and xy sums in double, the others in float), then
+// v_xy = (a Sx + b Sy, b Sx + c Sy) with the item's conic (a, b, c), in double, which equals the
+// reference's per-pair sum of
 // v_sigma (a dx + b dy, b dx + c dy) (splax/_rasterize/_kernels.py:1246-1250) up to rounding; each
 // output is rounded to float once. Every output is written. The double sums keep the gather's
 // rounding out of the gradients of needle-thin items, whose projection VJP multiplies it by up
@@ -967,13 +968,10 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
         whi = whi > P.M ? P.M : whi;
         block_gather<NG, 256>(P.rgrad, woff, wlo, whi, lo, hi, s_buf, s);
     } else {
-#pragma unroll
-        for (int k = 0; k < NG; ++k) s[k] = 0.0;
-        for (int64_t e = lo; e < hi; ++e) {
-            const float* r = P.rgrad + (off + e) * NG;
-#pragma unroll
-            for (int k = 0; k < NG; ++k) s[k] += (double)r[k];
-        }
+        GatherSums<NG> acc;
+        acc.clear();
+        for (int64_t e = lo; e < hi; ++e) acc.add_row(P.rgrad + (off + e) * NG);
+        acc.out(s);
     }
     if (!valid) continue;
     float vc[3] = {(float)s[3], (float)s[4], (float)s[5]};

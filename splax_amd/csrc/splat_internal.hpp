@@ -360,18 +360,51 @@ int launch_blend_bwd(const RasterInputs& in, const KeyLayout& lay, const int32_t
 // keeps a workgroup's LDS at 18 KB, eight per CU (config 4's gather 0.39 -> 0.33 ms against 768).
 constexpr int kGatherChunk = 512;
 
+// Sums of the per-item gather kept in double: the conic and xy sums (slots 3..7), whose rounding
+// the projection VJP multiplies by up to cond(conic)^2 on needle-thin items. The colour, opacity
+// and depth sums (slots 0..2, 8, 9) add a few float rows each and stay in float.
+__host__ __device__ constexpr bool gather_in_double(int k) { return k >= 3 && k <= 7; }
+
+// Running per-item sums of rgrad rows: five in double, the others in float (gather_in_double).
+template <int NG>
+struct GatherSums {
+    static constexpr int dslot(int k) { return k >= 3 && k <= 7 ? k - 3 : 0; }
+    static constexpr int fslot(int k) { return k < 3 ? k : (k >= 8 ? k - 5 : 0); }
+    double d[5];
+    float f[NG - 5];
+    __device__ __forceinline__ void clear() {
+#pragma unroll
+        for (int k = 0; k < 5; ++k) d[k] = 0.0;
+#pragma unroll
+        for (int k = 0; k < NG - 5; ++k) f[k] = 0.0f;
+    }
+    __device__ __forceinline__ void add_row(const float* r) {
+#pragma unroll
+        for (int k = 0; k < NG; ++k) {
+            if (gather_in_double(k))
+                d[dslot(k)] += (double)r[k];
+            else
+                f[fslot(k)] += r[k];
+        }
+    }
+    __device__ __forceinline__ void out(double* s) const {
+#pragma unroll
+        for (int k = 0; k < NG; ++k) s[k] = gather_in_double(k) ? d[dslot(k)] : (double)f[fslot(k)];
+    }
+};
+
 // Per-item sums of NG floats over the item's emission range [my_lo, my_hi) of rgrad rows
-// (row e at rgrad + (off + e) * NG), added in emission order in double. The workgroup's items cover one
-// contiguous range [wg_lo, wg_hi) of rows (uniform over the workgroup), which is read with
-// coalesced loads into s_buf (kGatherChunk * NG floats of LDS) a round at a time; each thread then
-// adds its own rows from LDS. Every thread of the workgroup calls it (an item outside the
-// workgroup's range passes my_lo = my_hi).
+// (row e at rgrad + (off + e) * NG), added in emission order (GatherSums). The workgroup's items
+// cover one contiguous range [wg_lo, wg_hi) of rows (uniform over the workgroup), which is read
+// with coalesced loads into s_buf (kGatherChunk * NG floats of LDS) a round at a time; each
+// thread then adds its own rows from LDS. Every thread of the workgroup calls it (an item outside
+// the workgroup's range passes my_lo = my_hi).
 template <int NG, int kThreads>
 __device__ __forceinline__ void block_gather(const float* __restrict__ rgrad, int64_t off,
                                              int64_t wg_lo, int64_t wg_hi, int64_t my_lo,
                                              int64_t my_hi, float* s_buf, double* s) {
-#pragma unroll
-    for (int k = 0; k < NG; ++k) s[k] = 0.0;
+    GatherSums<NG> acc;
+    acc.clear();
     for (int64_t cs = wg_lo; cs < wg_hi; cs += kGatherChunk) {
         const int64_t ce = cs + kGatherChunk < wg_hi ? cs + kGatherChunk : wg_hi;
         const int nf = (int)((ce - cs) * NG);
@@ -392,12 +425,9 @@ __device__ __forceinline__ void block_gather(const float* __restrict__ rgrad, in
         }
         __syncthreads();
         const int64_t a = my_lo > cs ? my_lo : cs, b = my_hi < ce ? my_hi : ce;
-        for (int64_t e = a; e < b; ++e) {
-            const float* r = s_buf + (e - cs) * NG;
-#pragma unroll
-            for (int k = 0; k < NG; ++k) s[k] += (double)r[k];
-        }
+        for (int64_t e = a; e < b; ++e) acc.add_row(s_buf + (e - cs) * NG);
     }
+    acc.out(s);
 }
 
 // Inclusive prefix sum over the 64 lanes (every lane active): DPP row shifts scan each row of 16,
