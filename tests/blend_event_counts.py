@@ -7,7 +7,15 @@ entry whose ballot of "in range" lanes (idx <= final_idx, 0 <= sigma <= sigma_ma
 the sigma evaluation only; every other entry is an event that pays the full per-pair arithmetic
 and the wave reduction. This script counts those entries and the lanes that contribute
 (alpha >= 1/255) per event over every tile (or a seeded sample scaled to the whole image) of the
-workload's first camera.
+workload's first camera, and the lanes an event's ellipse reaches before the final-index test.
+
+It also counts the forward blend's row walks: each 16-lane row of a wave walks the list of the
+records that reach its 4x4 sub-block (the ellipse {sigma <= sigma_max} meets a pixel centre of
+it), and a pixel stops at the record that brings its transmittance to 1e-4 or below, so in each
+batch of 256 staged records a row takes as many steps as its slowest pixel and a wave as many as
+its slowest row. Printed: the wave steps
+as built, the steps if the four rows of each wave were balanced (every row a quarter of the
+wave's total), and the steps if every pixel's own steps were packed 64 to a wave step.
 
 The geometry evaluates in float64 (a pair at a threshold edge may count differently from the
 float32 kernel; that moves the totals far below their printed precision). Run from the repository
@@ -73,7 +81,10 @@ def main() -> None:
     rng = np.random.default_rng(0)
     sample = live if args.tiles is None else rng.choice(live, size=min(args.tiles, len(live)),
                                                          replace=False)
-    tot = dict(entries=0, past_wmax=0, reach=0, events=0, lanes=0, pairs_in_range=0)
+    tot = dict(entries=0, past_wmax=0, reach=0, events=0, lanes=0, pairs_in_range=0,
+               reach_lanes=0, fwd_wave_steps=0, fwd_row_balanced=0.0, fwd_packed=0.0)
+    # sub-block (row-major over the tile's 4x4 grid of 4x4 pixel blocks) of each pixel
+    sub = (np.arange(16)[:, None] // 4) * 4 + np.arange(16)[None, :] // 4
     hist = np.zeros(65, np.int64)
     t0 = time.time()
     for tile in sample:
@@ -97,6 +108,34 @@ def main() -> None:
         reach = (sig >= 0) & (sig <= smax[g][:, None, None]) & inside[None]
         in_range = reach & (idx[:, None, None] <= bf[None])
         contrib = in_range & (alpha >= ALPHA_MIN)
+        # forward row walks: the tile's whole range in sorted order
+        gf = sid[rs:re]
+        fdx = xys[gf, 0][:, None, None] - (jj + 0.5)[None]
+        fdy = xys[gf, 1][:, None, None] - (ii + 0.5)[None]
+        fsig = 0.5 * (ca[gf][:, None, None] * fdx * fdx + cc[gf][:, None, None] * fdy * fdy) + \
+            cb[gf][:, None, None] * fdx * fdy
+        with np.errstate(over="ignore", invalid="ignore"):
+            falpha = np.minimum(ALPHA_MAX, opac[gf][:, None, None] * np.exp(-fsig))
+        fr = (fsig >= 0) & (fsig <= smax[gf][:, None, None]) & inside[None]
+        fa = np.where(fr & (falpha >= ALPHA_MIN), falpha, 0.0)
+        below = np.cumprod(1.0 - fa, axis=0) <= 1e-4
+        nf = len(gf)
+        stop = np.where(below.any(0), below.argmax(0), nf)  # the record where a pixel stops
+        on_list = np.stack([fr[:, sub == b].any(1) for b in range(16)], 1)  # [records, 16]
+        pos = np.cumsum(on_list, axis=0)
+        pos = np.vstack([np.zeros((1, 16), pos.dtype), pos])  # pos[k + 1]: entries in [0, k]
+        last = np.minimum(stop, nf - 1)
+        for a in range(0, nf, 256):  # the kernel's batches of 256 staged records
+            e = min(a + 256, nf)
+            # a pixel's steps in this batch: its list's entries from a to its stop (inclusive)
+            upto = np.minimum(last, e - 1)
+            steps = np.where(inside & (stop >= a), pos[upto + 1, sub] - pos[a, sub], 0)
+            row_task = np.array([steps[sub == b].max() for b in range(16)])
+            for w in range(4):
+                rows = [(2 * (w >> 1) + (r >> 1)) * 4 + 2 * (w & 1) + (r & 1) for r in range(4)]
+                tot["fwd_wave_steps"] += int(row_task[rows].max())
+                tot["fwd_row_balanced"] += float(row_task[rows].mean())
+            tot["fwd_packed"] += float(steps.sum()) / 64.0
         x0 = tx * 16 + np.arange(4) * 4 + 0.5
         y0 = ty * 16 + np.arange(4) * 4 + 0.5
         xm = (xys[g, 0][:, None] + ex[g][:, None] >= x0) & (xys[g, 0][:, None] - ex[g][:, None]
@@ -119,6 +158,7 @@ def main() -> None:
                 tot["events"] += int(ev.sum())
                 tot["lanes"] += int(lanes[ev].sum())
                 tot["pairs_in_range"] += int(ir[ev].sum())
+                tot["reach_lanes"] += int(reach[:, rows, cols].reshape(len(idx), 64)[ev].sum())
                 hist += np.bincount(lanes[ev], minlength=65)
     scale = len(live) / len(sample)
     print(f"config {args.config}, first of {s.B} camera(s): {H}x{W}, M = {M}, "
@@ -132,9 +172,16 @@ def main() -> None:
     print(f"contributing pairs           {tot['lanes'] * scale:.4g}")
     print(f"contributing lanes per event {tot['lanes'] / max(tot['events'], 1):.2f} of 64")
     print(f"in-range lanes per event     {tot['pairs_in_range'] / max(tot['events'], 1):.2f}")
+    print(f"lanes the ellipse reaches per event (before the final-index test) "
+          f"{tot['reach_lanes'] / max(tot['events'], 1):.2f}")
     cdf = np.cumsum(hist) / max(hist.sum(), 1)
     print("events with <= k contributing lanes: " +
           ", ".join(f"k={k}: {cdf[k]:.2f}" for k in (1, 4, 8, 16, 32, 48)))
+    ws = tot["fwd_wave_steps"]
+    print(f"forward row walks: wave steps {ws * scale:.4g}; rows balanced within each wave "
+          f"{tot['fwd_row_balanced'] * scale:.4g} ({tot['fwd_row_balanced'] / max(ws, 1):.3f}); "
+          f"every pixel's steps packed 64 per wave step {tot['fwd_packed'] * scale:.4g} "
+          f"({tot['fwd_packed'] / max(ws, 1):.3f})")
 
 
 if __name__ == "__main__":
