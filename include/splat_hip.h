@@ -332,6 +332,24 @@ typedef struct splat_adam_group {
 int splat_adam_step(splat_stream_t stream, const splat_adam_group* groups, int32_t num_groups,
                     double b1, double b2, double eps, double eps_root, int64_t count);
 
+/* Parameter maps of splat_adam_step_mapped: the group's gradient is the cotangent of the
+ * group's value under render_log's map (splax/_render.py:161-164) and the update first applies
+ * the map's reverse-mode rule at the parameter before the update, with the float operations of
+ * splat_log_params_bwd. */
+#define SPLAT_MAP_NONE 0    /* the gradient is the parameter's own */
+#define SPLAT_MAP_EXP 1     /* scales = exp(log_scales) */
+#define SPLAT_MAP_SIGMOID 2 /* colours / opacities = sigmoid(logits) */
+#define SPLAT_MAP_QUAT 3    /* quats / (|quats| + 1e-8), rows of 4 (16-byte aligned) */
+
+/* splat_adam_step with a parameter map per group (maps[num_groups], SPLAT_MAP_*; NULL = none):
+ * the reference's render_log backward (splax/_render.py:161-164, here splat_log_params_bwd)
+ * followed by the update, in one launch. No counterpart entry point in the reference, whose
+ * optax update takes the gradients jax.grad returns for the log / logit parameters; bit for bit
+ * equal to splat_log_params_bwd then splat_adam_step. */
+int splat_adam_step_mapped(splat_stream_t stream, const splat_adam_group* groups,
+                           int32_t num_groups, const int32_t* maps, double b1, double b2,
+                           double eps, double eps_root, int64_t count);
+
 /* Replaces _reset_opt_state (scripts/train_lego.py:136-146): zeroes mu and nu of every row
  * whose reset[row] != 0; each group's size must be a multiple of num_rows (its row width). */
 int splat_adam_reset_rows(splat_stream_t stream, const splat_adam_group* groups,

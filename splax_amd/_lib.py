@@ -58,6 +58,7 @@ _SIGS = {
     + [_i32, _i32] + [_vp] * 10 + [_i64] + [_vp] * 3 + [_i64, _vp, _i64] + [_vp] * 7 + [_i32]
     + [_vp, _i32, _vp, _vp],
     "splat_adam_step": [_vp, _vp, _i32, _f64, _f64, _f64, _f64, _i64],
+    "splat_adam_step_mapped": [_vp, _vp, _i32, _vp, _f64, _f64, _f64, _f64, _i64],
     "splat_adam_reset_rows": [_vp, _vp, _i32, _vp, _i64],
     "splat_mcmc_relocate": [_vp] + [_vp] * 5 + [_i64, _i32, _f32, _u64, _vp, _vp],
     "splat_mcmc_compute_relocation": [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp],
@@ -80,7 +81,7 @@ STAGES = ("project", "minmax", "emit", "sort", "bins", "blend_fwd", "blend_bwd",
           "blend_fwd_kernel", "blend_bwd_kernel")
 
 # splat_abi_version() of the library this binding was written for (include/splat_hip.h)
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 # status codes (splax_amd/csrc/splat_internal.hpp)
 ERR_ARGS, ERR_KEY_OVERFLOW, ERR_TOO_MANY = 1, 2, 6

@@ -435,7 +435,7 @@ static int64_t g_stage_calls[kNumStages];
 
 extern "C" {
 
-int splat_abi_version(void) { return 16; }
+int splat_abi_version(void) { return 17; }
 
 int splat_check_device(void) {
     DeviceScratch& sc = scratch_for_current_device();

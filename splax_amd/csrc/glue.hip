@@ -5,10 +5,8 @@
 //   - the L1 loss mean |img - target| of the trainers (scripts/train_lego.py:111) and its
 //     cotangent sign(img - target) * g / count.
 //
-// exp is det_expf and sigmoid(x) = 1 / (1 + det_expf(-x)), so the CPU oracle reproduces every
-// bit. |q| = sqrt(((q0^2 + q1^2) + q2^2) + q3^2). Reverse-mode rules follow the reference's
-// primitives: exp' = exp, logistic' = s (1 - s), sqrt' = 0.5 / sqrt, x / s gives g / s and
-// -(g x) / s^2 to the divisor, and the square's two uses add 2 q v.
+// The map and its reverse-mode rules are the device functions of splat_common.hpp (map_sigmoid,
+// quat_norm, map_*_vjp): exp is det_expf, so the CPU oracle reproduces every bit.
 #include <string>
 
 #include "../../include/splat_hip.h"
@@ -16,14 +14,6 @@
 #include "splat_internal.hpp"
 
 namespace splat {
-
-constexpr float kQuatEps = 0x1.5798eep-27f;  // float32(1e-8), splax/_render.py:162
-
-__device__ __forceinline__ float glue_sigmoid(float x) { return 1.0f / (1.0f + det_expf(-x)); }
-
-__device__ __forceinline__ float quat_norm(const float q[4]) {
-    return sqrtf(((q[0] * q[0] + q[1] * q[1]) + q[2] * q[2]) + q[3] * q[3]);
-}
 
 struct LogParams {
     const float* log_scales; const float* quats; const float* logit_colors;
@@ -41,14 +31,14 @@ __global__ void __launch_bounds__(256) log_params_fwd_kernel(LogParams P) {
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         P.scales[3 * i + k] = det_expf(P.log_scales[3 * i + k]);
-        P.colors[3 * i + k] = glue_sigmoid(P.logit_colors[3 * i + k]);
+        P.colors[3 * i + k] = map_sigmoid(P.logit_colors[3 * i + k]);
     }
     const float4 q4 = reinterpret_cast<const float4*>(P.quats)[i];
     const float q[4] = {q4.x, q4.y, q4.z, q4.w};
     const float s = quat_norm(q) + kQuatEps;
     reinterpret_cast<float4*>(P.quats_out)[i] =
         make_float4(q[0] / s, q[1] / s, q[2] / s, q[3] / s);
-    P.opac[i] = glue_sigmoid(P.logit_opac[i]);
+    P.opac[i] = map_sigmoid(P.logit_opac[i]);
 }
 
 // A null cotangent is a zero one.
@@ -60,27 +50,17 @@ __global__ void __launch_bounds__(256) log_params_bwd_kernel(LogParams P) {
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         const int64_t j = 3 * i + k;
-        P.v_log_scales[j] = cot(P.v_scales, j) * det_expf(P.log_scales[j]);
-        const float sc = glue_sigmoid(P.logit_colors[j]);
-        P.v_logit_colors[j] = cot(P.v_colors, j) * (sc * (1.0f - sc));
+        P.v_log_scales[j] = map_exp_vjp(cot(P.v_scales, j), P.log_scales[j]);
+        P.v_logit_colors[j] = map_sigmoid_vjp(cot(P.v_colors, j), P.logit_colors[j]);
     }
-    const float so = glue_sigmoid(P.logit_opac[i]);
-    P.v_logit_opac[i] = cot(P.v_opac, i) * (so * (1.0f - so));
+    P.v_logit_opac[i] = map_sigmoid_vjp(cot(P.v_opac, i), P.logit_opac[i]);
     const float4 q4 = reinterpret_cast<const float4*>(P.quats)[i];
     const float q[4] = {q4.x, q4.y, q4.z, q4.w};
-    const float nrm = quat_norm(q);
-    const float s = nrm + kQuatEps;
     float vy[4], vq[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) vy[k] = cot(P.v_quats, 4 * i + k);
-    // y = q / s: the divisor's cotangent sums -(g q) / s^2 over the four components
-    const float inv_s2 = 1.0f / (s * s);
-    float v_s = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) v_s = v_s + (-(vy[k] * q[k])) * inv_s2;
-    const float v_ss = v_s * (0.5f / nrm);  // s = sqrt(sum q^2) + eps
-#pragma unroll
-    for (int k = 0; k < 4; ++k) vq[k] = vy[k] / s + (v_ss * q[k] + v_ss * q[k]);
+    for (int k = 0; k < 4; ++k) vq[k] = map_quat_vjp(q, vy, k);
     reinterpret_cast<float4*>(P.v_quats_in)[i] = make_float4(vq[0], vq[1], vq[2], vq[3]);
 }
 

@@ -134,6 +134,42 @@ __device__ __forceinline__ float det_expf(float x) {
     return ldexpf(p, (int)kf);
 }
 
+// ------------------------------------------------------------------ render_log's parameter map
+// splax/_render.py:161-164: scales = exp(log_scales), quats / (|quats| + 1e-8), sigmoid of the
+// colour and opacity logits, with sigmoid(x) = 1 / (1 + det_expf(-x)) and
+// |q| = sqrt(((q0^2 + q1^2) + q2^2) + q3^2). The reverse-mode rules follow the reference's
+// primitives: exp' = exp, logistic' = s (1 - s), sqrt' = 0.5 / sqrt, x / s gives g / s and
+// -(g x) / s^2 to the divisor, and the square's two uses add 2 q v.
+constexpr float kQuatEps = 0x1.5798eep-27f;  // float32(1e-8), splax/_render.py:162
+
+__device__ __forceinline__ float map_sigmoid(float x) { return 1.0f / (1.0f + det_expf(-x)); }
+
+__device__ __forceinline__ float quat_norm(const float q[4]) {
+    return sqrtf(((q[0] * q[0] + q[1] * q[1]) + q[2] * q[2]) + q[3] * q[3]);
+}
+
+// Cotangent of a log-scale from its scale's cotangent g.
+__device__ __forceinline__ float map_exp_vjp(float g, float log_scale) {
+    return g * det_expf(log_scale);
+}
+// Cotangent of a logit from its sigmoid's cotangent g.
+__device__ __forceinline__ float map_sigmoid_vjp(float g, float logit) {
+    const float s = map_sigmoid(logit);
+    return g * (s * (1.0f - s));
+}
+// Cotangent of the raw quaternion component k from the normalized quaternion's cotangents vy.
+__device__ __forceinline__ float map_quat_vjp(const float q[4], const float vy[4], int k) {
+    const float nrm = quat_norm(q);
+    const float s = nrm + kQuatEps;
+    // y = q / s: the divisor's cotangent sums -(g q) / s^2 over the four components
+    const float inv_s2 = 1.0f / (s * s);
+    float v_s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v_s = v_s + (-(vy[j] * q[j])) * inv_s2;
+    const float v_ss = v_s * (0.5f / nrm);  // s = sqrt(sum q^2) + eps
+    return vy[k] / s + (v_ss * q[k] + v_ss * q[k]);
+}
+
 // Opacity-aware isocontour level, splax/_project/_kernels.py:227.
 __device__ __forceinline__ float iso_level(float opac) {
     return minw(kExtendSq, 2.0f * det_logf(opac / kAlphaThresh));

@@ -38,6 +38,7 @@ struct AdamGroupDev {
     float* p; const float* g; float* mu; float* nu;
     int64_t size;
     float neg_lr;
+    int32_t map;  // SPLAT_MAP_*: g is the cotangent of the group's mapped value
 };
 
 struct AdamParams {
@@ -57,7 +58,22 @@ __global__ void __launch_bounds__(256) adam_step_kernel(AdamParams P) {
     for (int j = 0; j < kAdamChunk / 256; ++j) {
         const int64_t i = base + j * 256 + threadIdx.x;
         if (i >= G.size) break;
-        const float g = G.g[i];
+        // the gradient of the stored parameter: the reverse-mode rule of render_log's map
+        // applied to the mapped value's cotangent (log_params_bwd_kernel's float operations),
+        // with the parameter before this update
+        float g = G.g[i];
+        if (G.map == SPLAT_MAP_EXP) {
+            g = map_exp_vjp(g, G.p[i]);
+        } else if (G.map == SPLAT_MAP_SIGMOID) {
+            g = map_sigmoid_vjp(g, G.p[i]);
+        } else if (G.map == SPLAT_MAP_QUAT) {
+            const int64_t row = i >> 2;  // the group is [rows, 4], 16-byte aligned
+            const float4 q4 = reinterpret_cast<const float4*>(G.p)[row];
+            const float4 v4 = reinterpret_cast<const float4*>(G.g)[row];
+            const float q[4] = {q4.x, q4.y, q4.z, q4.w};
+            const float vy[4] = {v4.x, v4.y, v4.z, v4.w};
+            g = map_quat_vjp(q, vy, (int)(i & 3));
+        }
         float m = G.mu[i], v = G.nu[i];
         m = P.c1 * g + P.b1 * m;
         v = P.c2 * (g * g) + P.b2 * v;
@@ -471,6 +487,13 @@ extern "C" {
 
 int splat_adam_step(splat_stream_t stream, const splat_adam_group* groups, int32_t num_groups,
                     double b1, double b2, double eps, double eps_root, int64_t count) {
+    return splat_adam_step_mapped(stream, groups, num_groups, nullptr, b1, b2, eps, eps_root,
+                                  count);
+}
+
+int splat_adam_step_mapped(splat_stream_t stream, const splat_adam_group* groups,
+                           int32_t num_groups, const int32_t* maps, double b1, double b2,
+                           double eps, double eps_root, int64_t count) {
     if (num_groups < 0 || num_groups > kAdamMaxGroups || (num_groups > 0 && !groups))
         return fail(kErrArgs, "adam_step: between 0 and 8 parameter groups");
     if (count < 1) return fail(kErrArgs, "adam_step: count (the incremented step) must be >= 1");
@@ -481,7 +504,15 @@ int splat_adam_step(splat_stream_t stream, const splat_adam_group* groups, int32
         const splat_adam_group& s = groups[g];
         if (s.size < 0 || (s.size > 0 && (!s.params || !s.grads || !s.mu || !s.nu)))
             return fail(kErrArgs, "adam_step: group " + std::to_string(g) + " has no buffers");
-        P.grp[g] = AdamGroupDev{s.params, s.grads, s.mu, s.nu, s.size, (float)(-s.lr)};
+        const int32_t map = maps ? maps[g] : SPLAT_MAP_NONE;
+        if (map < SPLAT_MAP_NONE || map > SPLAT_MAP_QUAT)
+            return fail(kErrArgs, "adam_step: group " + std::to_string(g) +
+                                      " has an unknown parameter map");
+        if (map == SPLAT_MAP_QUAT &&
+            (s.size % 4 != 0 || (((uintptr_t)s.params | (uintptr_t)s.grads) & 15)))
+            return fail(kErrArgs, "adam_step: a quaternion group holds rows of 4 floats, "
+                                  "16-byte aligned");
+        P.grp[g] = AdamGroupDev{s.params, s.grads, s.mu, s.nu, s.size, (float)(-s.lr), map};
         P.block_start[g] = blocks;
         blocks += (s.size + kAdamChunk - 1) / kAdamChunk;
     }

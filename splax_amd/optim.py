@@ -18,6 +18,11 @@ from splax_amd import _lib
 
 Schedule = Callable[[int], float]
 
+# Parameter maps of Adam.step (include/splat_hip.h SPLAT_MAP_*): the gradient given for the group
+# is the cotangent of the mapped value of render_log (splax/_render.py:161-164), and the update
+# applies the map's reverse-mode rule first.
+MAP_NONE, MAP_EXP, MAP_SIGMOID, MAP_QUAT = 0, 1, 2, 3
+
 
 def exponential_decay(init_value: float, transition_steps: int,
                       decay_rate: float) -> Schedule:
@@ -69,13 +74,27 @@ class Adam:
                                     float(lr))
         return arr, keep
 
-    def step(self, grads: Mapping[str, torch.Tensor]) -> None:
-        """One update of every group (learning-rate schedules see the pre-increment count)."""
+    def step(self, grads: Mapping[str, torch.Tensor],
+             maps: Mapping[str, int] | None = None) -> None:
+        """One update of every group (learning-rate schedules see the pre-increment count).
+
+        ``maps`` names, per group, the parameter map whose output ``grads`` differentiates
+        (MAP_EXP, MAP_SIGMOID, MAP_QUAT; groups not named take MAP_NONE): the update then applies
+        the map's reverse-mode rule at the parameters before the update, bit for bit as
+        render_log's own backward does, in the same launch."""
         arr, keep = self._groups(grads, self.count)
         self.count += 1
+        map_arr = None
+        if maps is not None:
+            unknown = set(maps) - set(self.params)
+            if unknown:
+                raise ValueError(f"maps name groups {sorted(unknown)} that do not exist")
+            map_arr = (ctypes.c_int32 * len(arr))(*[int(maps.get(k, MAP_NONE))
+                                                    for k in self.params])
         with torch.cuda.device(self._dev):
-            st = _lib.lib().splat_adam_step(
-                _lib.stream_handle(self._dev), ctypes.addressof(arr), len(arr), self.b1, self.b2,
+            st = _lib.lib().splat_adam_step_mapped(
+                _lib.stream_handle(self._dev), ctypes.addressof(arr), len(arr),
+                None if map_arr is None else ctypes.addressof(map_arr), self.b1, self.b2,
                 self.eps, self.eps_root, self.count)
         _lib.check(st, "adam_step")
         del keep

@@ -23,11 +23,16 @@ import numpy as np
 import torch
 
 from splax_amd import _lib, mcmc
-from splax_amd._render import render_log_loss
-from splax_amd.optim import Adam, exponential_decay
+from splax_amd._render import _LogParamsFn, render_log_loss, render_loss
+from splax_amd.optim import MAP_EXP, MAP_QUAT, MAP_SIGMOID, Adam, exponential_decay
 from splax_amd.scenes import Scene
 
 SPLAT_KEYS = ("means", "log_scales", "quats", "colors_logit", "opac_logit")
+
+# render_log's map of each parameter group (splax/_render.py:161-164), applied in reverse by the
+# fused Adam update
+PARAM_MAPS = {"log_scales": MAP_EXP, "quats": MAP_QUAT, "colors_logit": MAP_SIGMOID,
+              "opac_logit": MAP_SIGMOID}
 
 # scripts/train_lego.py:407-411 (defaults of the reference trainer)
 DEFAULT_LRS = {"means": 1.5e-3, "log_scales": 5e-3, "quats": 1e-3, "colors_logit": 1e-2,
@@ -139,10 +144,26 @@ class TrainStep:
             p.requires_grad_(False)
         return loss.detach(), dict(zip(SPLAT_KEYS, grads))
 
+    def mapped_loss_and_grads(self) -> tuple[torch.Tensor, dict[str, torch.Tensor]]:
+        """The loss and its gradients with respect to the means and the mapped values (scales,
+        normalized quaternions, colours, opacities) of render_log's map, which the fused Adam
+        update (PARAM_MAPS) turns into the log / logit parameters' gradients."""
+        p = self.params
+        with torch.no_grad():
+            mapped = _LogParamsFn.apply(p["log_scales"], p["quats"], p["colors_logit"],
+                                        p["opac_logit"])
+        leaves = [p["means"].requires_grad_(True), *(t.requires_grad_(True) for t in mapped)]
+        loss, _ = render_loss(*leaves, target=self.targets, loss="l1", viewmat=self.viewmats,
+                              background=self.background, **self.camera)
+        grads = torch.autograd.grad(loss, leaves)
+        p["means"].requires_grad_(False)
+        return loss.detach(), dict(zip(SPLAT_KEYS, grads))
+
     def __call__(self) -> torch.Tensor:
-        """One step; returns the L1 loss before the update (a device scalar)."""
-        loss, grads = self.loss_and_grads()
-        self.opt.step(grads)
+        """One step; returns the L1 loss before the update (a device scalar). The map's backward
+        runs inside the Adam launch (bit for bit loss_and_grads followed by opt.step)."""
+        loss, grads = self.mapped_loss_and_grads()
+        self.opt.step(grads, maps=PARAM_MAPS)
         self.step_idx += 1
         if self.relocate_every and self.step_idx % self.relocate_every == 0:
             key = (self.seed << 32) ^ self.step_idx

@@ -376,6 +376,82 @@ def test_train_step_config4_small():
     assert _lib.check_device() == 0
 
 
+@pytest.mark.parametrize("n", [1, 333, 20000])
+def test_mapped_adam_equals_log_params_bwd_then_adam(n):
+    """splat_adam_step_mapped (render_log's map applied in reverse inside the update) equals
+    splat_log_params_bwd followed by splat_adam_step bit for bit: parameters, mu and nu over
+    three steps of mapped-space gradients of mixed scales, with an unmapped group beside."""
+    _case(f"mapped adam n={n}")
+    rng = np.random.default_rng(n)
+    raw = {"means": rng.normal(size=(n, 3)), "log_scales": rng.normal(-4, 1, size=(n, 3)),
+           "quats": rng.normal(size=(n, 4)), "colors_logit": rng.normal(0, 2, size=(n, 3)),
+           "opac_logit": rng.normal(0, 3, size=(n, 1))}
+    raw["quats"][0] = 0.0  # a zero quaternion: the rule's 0.5 / |q| gives inf / NaN in both
+    mk = lambda: {k: _t(v.astype(np.float32)) for k, v in raw.items()}  # noqa: E731
+    pa, pb = mk(), mk()
+    lrs = {"means": 1e-3, "log_scales": 5e-3, "quats": 1e-3, "colors_logit": 1e-2,
+           "opac_logit": 5e-2}
+    adam_a, adam_b = optim.Adam(pa, lrs), optim.Adam(pb, lrs)
+    maps = {"log_scales": optim.MAP_EXP, "quats": optim.MAP_QUAT,
+            "colors_logit": optim.MAP_SIGMOID, "opac_logit": optim.MAP_SIGMOID}
+    for step in range(3):
+        g = {k: _t((rng.normal(size=v.shape) * 10.0 ** rng.integers(-6, 2, size=v.shape))
+                   .astype(np.float32)) for k, v in raw.items()}
+        # path A: the map's backward as its own launch, then the plain update
+        ins = [pa[k].contiguous() for k in ("log_scales", "quats", "colors_logit", "opac_logit")]
+        outs = [torch.empty_like(t) for t in ins]
+        vs = [g[k] for k in ("log_scales", "quats", "colors_logit", "opac_logit")]
+        st = _lib.lib().splat_log_params_bwd(_lib.stream_handle(ins[0].device),
+                                             *map(_lib.ptr, ins), n, *map(_lib.ptr, vs),
+                                             *map(_lib.ptr, outs))
+        _lib.check(st, "log_params_bwd")
+        ga = {"means": g["means"], **dict(zip(("log_scales", "quats", "colors_logit",
+                                                "opac_logit"), outs))}
+        adam_a.step(ga)
+        # path B: one launch
+        adam_b.step(g, maps=maps)
+        torch.cuda.synchronize()
+        for k in raw:
+            assert_bit_exact(_np(pb[k]), _np(pa[k]), f"step {step} {k}")
+            assert_bit_exact(_np(adam_b.mu[k]), _np(adam_a.mu[k]), f"step {step} mu {k}")
+            assert_bit_exact(_np(adam_b.nu[k]), _np(adam_a.nu[k]), f"step {step} nu {k}")
+    assert not bool(torch.isfinite(pb["quats"][0]).all())  # the zero quaternion, as in path A
+    with pytest.raises(ValueError):
+        adam_b.step(g, maps={"nope": optim.MAP_EXP})
+    assert _lib.check_device() == 0
+
+
+def test_train_step_fused_map_equals_unfused():
+    """TrainStep's step (the render on the mapped values, the map's backward inside Adam) equals
+    the autograd chain through render_log (loss_and_grads) followed by the plain update, bit for
+    bit over three steps with relocation."""
+    from splax_amd.scenes import make_scene
+    from splax_amd.train import TrainStep, params_from_scene
+
+    _case("train step fused map vs unfused n=20000")
+    scene = make_scene(4, n=20_000)
+    kw = dict(viewmats=_t(scene.viewmats), targets=_t(scene.targets),
+              background=_t(scene.background), img_shape=scene.img_shape, f=scene.f, seed=3)
+    p0 = params_from_scene(scene)
+    p0["opac_logit"][:300] = -12.0  # dead rows to relocate
+    fused = TrainStep({k: v.clone() for k, v in p0.items()}, **kw)
+    plain = TrainStep({k: v.clone() for k, v in p0.items()}, **kw)
+    for _ in range(3):
+        lf = fused()
+        lp, grads = plain.loss_and_grads()
+        plain.opt.step(grads)
+        plain.step_idx += 1
+        key = (plain.seed << 32) ^ plain.step_idx
+        reset = mcmc.relocate_(key, *plain.params.values(), plain.binoms, plain.min_opacity)
+        plain.opt.reset_rows(reset)
+        torch.cuda.synchronize()
+        assert_bit_exact(_np(lf), _np(lp), "loss")
+        for k in fused.params:
+            assert_bit_exact(_np(fused.params[k]), _np(plain.params[k]), k)
+            assert_bit_exact(_np(fused.opt.mu[k]), _np(plain.opt.mu[k]), f"mu {k}")
+    assert _lib.check_device() == 0
+
+
 @pytest.mark.parametrize("n", [1, 777, 20000])
 def test_log_params_bit_exact(n):
     """render_log's parameter map and its reverse mode, one library pass each, against the

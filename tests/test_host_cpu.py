@@ -175,6 +175,22 @@ def test_training_entry_points_validate_before_touching_the_device():
     assert lib.splat_adam_step(None, addr, 9, 0.9, 0.999, 1e-8, 0.0, 1) == _lib.ERR_ARGS
     assert lib.splat_adam_step(None, addr, 1, 0.9, 0.999, 1e-8, 0.0, 0) == _lib.ERR_ARGS
     assert lib.splat_adam_reset_rows(None, addr, 9, None, 4) == _lib.ERR_ARGS
+    # the mapped update: an unknown map, and a quaternion group that is not rows of 4 floats or
+    # not 16-byte aligned (fake device addresses: the checks precede any device call)
+    one = (_lib.AdamGroup * 1)()
+    one[0] = _lib.AdamGroup(1 << 20, 2 << 20, 3 << 20, 4 << 20, 8, 1e-3)
+    bad_map = (ctypes.c_int32 * 1)(4)
+    assert lib.splat_adam_step_mapped(None, ctypes.addressof(one), 1, ctypes.addressof(bad_map),
+                                      0.9, 0.999, 1e-8, 0.0, 1) == _lib.ERR_ARGS
+    assert b"unknown parameter map" in lib.splat_last_error()
+    quat_map = (ctypes.c_int32 * 1)(3)
+    one[0] = _lib.AdamGroup(1 << 20, 2 << 20, 3 << 20, 4 << 20, 6, 1e-3)
+    assert lib.splat_adam_step_mapped(None, ctypes.addressof(one), 1, ctypes.addressof(quat_map),
+                                      0.9, 0.999, 1e-8, 0.0, 1) == _lib.ERR_ARGS
+    one[0] = _lib.AdamGroup((1 << 20) + 4, 2 << 20, 3 << 20, 4 << 20, 8, 1e-3)
+    assert lib.splat_adam_step_mapped(None, ctypes.addressof(one), 1, ctypes.addressof(quat_map),
+                                      0.9, 0.999, 1e-8, 0.0, 1) == _lib.ERR_ARGS
+    assert b"16-byte aligned" in lib.splat_last_error()
     assert lib.splat_mcmc_relocate(None, None, None, None, None, None, 10, 63, 0.005, 1, None,
                                    None) == _lib.ERR_ARGS
     assert lib.splat_mcmc_relocate(None, None, None, None, None, None, 10, 51, 0.005, 1, None,
