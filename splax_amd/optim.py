@@ -102,8 +102,9 @@ class Adam:
     def reset_rows(self, reset: torch.Tensor) -> None:
         """Zero mu and nu of the rows flagged in ``reset`` (bool or uint8, one per row)."""
         rows = reset.numel()
-        mask = reset.to(torch.uint8).contiguous() if reset.dtype != torch.uint8 else \
-            reset.contiguous()
+        # a bool tensor holds one byte per row, 0 or 1: read as uint8 without a cast kernel
+        mask = reset.contiguous()
+        mask = mask.view(torch.uint8) if mask.dtype == torch.bool else mask.to(torch.uint8)
         arr, _ = self._groups(None, self.count)
         with torch.cuda.device(self._dev):
             st = _lib.lib().splat_adam_reset_rows(
