@@ -3,11 +3,14 @@
 // One workgroup of 256 threads (four wave64s) per (image, 16x16 tile), as in the reference
 // (splax/_rasterize/_kernels.py:63-87,469-500). Each wave owns one 8x8 quadrant of the tile and
 // each 16-lane row of a wave one 4x4 sub-block of it. The tile's sorted range is staged in LDS in
-// batches of 256 records (three float4 per record). While staging, each record gets
+// batches of records (three float4 per record; 256 per forward batch, 128 per backward batch).
+// Each packed record carries
 //   - sigma_max: a conservative bound (log(255 o) + 1e-3) above which o e^-sigma < 1/255, so a
-//     lane skips the exponential for pairs the reference rejects anyway, and
+//     lane skips the exponential for pairs the reference rejects anyway,
+// and while staging each record gets
 //   - a 16-bit sub-block mask: the 4x4 sub-blocks whose pixel centres can reach
-//     sigma <= sigma_max, from the ellipse's bounding box;
+//     sigma <= sigma_max (the forward from the ellipse's exact extent per band of rows, the
+//     backward from its bounding box);
 // and each row then walks only the compacted, order-preserving list of records that reach its
 // sub-block (the four rows of a wave walk their own lists in lockstep, each row reading its own
 // record, an LDS broadcast within the row). A wave takes as many steps as its longest row list,
@@ -20,8 +23,8 @@
 // wave over the list of its whole quadrant (per-row walks there cost more in LDS bank conflicts
 // and same-record accumulator collisions than they save in steps). A pixel's contribution to a
 // record is nine floats; per record the contributing lanes of a wave reduce them with a
-// reduce-scatter (v_permlane32_swap, v_permlane16_swap, then DPP row shifts: 28 VALU for nine
-// values) and add the totals into the record's LDS accumulator. After each batch every record
+// reduce-scatter (v_permlane32_swap, v_permlane16_swap, then bank-masked DPP adds within rows:
+// 19 VALU for nine values) and add the totals into the record's LDS accumulator. After each batch every record
 // stores its nine sums (plain stores, no global atomics) at its emission position, where all
 // intersections of one item are contiguous; grad_gather_kernel then adds them per item in a
 // fixed order and writes the four gradient outputs. The LDS sums of one record over the tile's
@@ -192,7 +195,7 @@ __device__ __forceinline__ uint32_t subblock_mask_tight(const float4& r0, const 
 // blue, depth), each record's sub-block mask, and compacted record lists: with kRows (the
 // forward) one per sub-block, of record byte offsets (16 t for slot t: the address needs no
 // shift), otherwise (the backward) one per quadrant wave, of slot indices. The backward's four
-// lists keep its LDS at 26 KB, six workgroups per CU (sixteen lists: five).
+// lists (with 128-record batches and two accumulator copies) keep its LDS at 19.7 KB.
 template <bool kRows, int kBatch>
 struct BatchLds {
     float4 r0[kBatch];
@@ -203,7 +206,7 @@ struct BatchLds {
     typename std::conditional<kRows, uint16_t, uint8_t>::type list[kRows ? 16 : 4][kTile];
 };
 // Records per batch of the backward: 128 keeps its LDS (records, lists and two accumulator
-// copies) at 19.3 KB, so with at most 64 VGPRs eight workgroups share a CU (eight waves per SIMD).
+// copies) at 19.7 KB, so with at most 64 VGPRs eight workgroups share a CU (eight waves per SIMD).
 constexpr int kBwdBatch = 128;
 
 // Stages record `src` of the sorted range into slot `tid` (one barrier), then each wave builds
