@@ -436,18 +436,22 @@ struct ProjectBwdParams {
     int32_t fold;  // gaussian gradients summed over the images into n rows
 };
 
-// One workgroup per (image, block of gaussians); with P.fold one workgroup per block of
+// One workgroup per (image, block of gaussians); with kFold one workgroup per block of
 // gaussians walks every image in order and sums the gaussian gradients in registers, so the
 // shared parameters are read once per gaussian and the per-image rows are never written.
+// kTf (rigid transforms given), kView (the viewmat gradient asked for) and kFold are template
+// parameters: without them the kernel holds 64 VGPRs (eight waves per SIMD) where the general
+// form holds 130 (three).
+template <bool kTf, bool kView, bool kFold>
 __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdParams P) {
     __shared__ float s_red[kProjThreads / 64][12];
     __shared__ int32_t s_tf[2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int32_t n = P.n;
-    const int32_t first_image = P.fold ? 0 : blockIdx.x / P.blocks_per_image;
+    const int32_t first_image = kFold ? 0 : blockIdx.x / P.blocks_per_image;
     const int32_t local_block =
-        P.fold ? (int32_t)blockIdx.x : (int32_t)blockIdx.x - first_image * P.blocks_per_image;
-    const int32_t end_image = P.fold ? P.B : first_image + 1;
+        kFold ? (int32_t)blockIdx.x : (int32_t)blockIdx.x - first_image * P.blocks_per_image;
+    const int32_t end_image = kFold ? P.B : first_image + 1;
     const int32_t gid = local_block * kProjThreads + tid;
     float fm[3] = {0.f, 0.f, 0.f}, fs[3] = {0.f, 0.f, 0.f}, fq[4] = {0.f, 0.f, 0.f, 0.f};
     for (int32_t image_id = first_image; image_id < end_image; ++image_id) {
@@ -459,7 +463,7 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
     bool moved = false;
     int32_t tf_id = -1;
     const bool in_range = gid < n;
-    if (in_range && P.has_transforms) tf_id = P.transform_ids[gid];
+    if (in_range && kTf) tf_id = P.transform_ids[gid];
     if (in_range) {
         float zero3[3] = {0.f, 0.f, 0.f};
         float vmean_out[3] = {0.f, 0.f, 0.f}, vscale[3] = {0.f, 0.f, 0.f};
@@ -644,7 +648,7 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
 #pragma unroll
             for (int k = 0; k < 4; ++k) vq[k] = 0.0f;
         }
-        if (P.fold) {
+        if (kFold) {
 #pragma unroll
             for (int k = 0; k < 3; ++k) {
                 fm[k] = fm[k] + vmean_out[k];
@@ -667,7 +671,7 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
     // viewmat gradient (when asked for): wave DPP reduction, then across the 4 waves in LDS, one
     // partial per (image, workgroup) that viewmat_reduce_kernel sums in a fixed order (atomics
     // from thousands of workgroups into the same 12 words serialize in the L2)
-    if (P.view_partials) {
+    if (kView) {
         float red[12];
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
@@ -688,7 +692,7 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
     }
     // Transform gradient: uniform block -> block reduction; mixed -> per-thread atomics
     // (splax/_project/_kernels.py:461-484).
-    if (P.has_transforms) {
+    if (kTf) {
         int32_t id = in_range ? tf_id : -1;
         int32_t tmin = block_min_i32(in_range ? tf_id : 2147483647, s_tf);
         int32_t tmax = block_max_i32(in_range ? tf_id : (-2147483647 - 1), s_tf);
@@ -727,7 +731,7 @@ __global__ void __launch_bounds__(kProjThreads) project_bwd_kernel(ProjectBwdPar
     }
     __syncthreads();  // s_red / s_tf are reused by the next image
     }
-    if (P.fold && gid < n) {
+    if (kFold && gid < n) {
         P.v_mean3d[3 * gid] = fm[0];
         P.v_mean3d[3 * gid + 1] = fm[1];
         P.v_mean3d[3 * gid + 2] = fm[2];
@@ -887,8 +891,18 @@ int launch_project_bwd(const ProjectBwdArgs& a, DeviceScratch& sc, hipStream_t s
     P.wxyz = a.quats_wxyz;
     P.fold = a.fold;
     int64_t blocks = (a.fold ? 1 : (int64_t)a.B) * blocks_per_image;
-    hipLaunchKernelGGL(project_bwd_kernel, dim3((unsigned)blocks), dim3(kProjThreads), 0, stream,
-                       P);
+    const int variant = (a.has_transforms ? 4 : 0) | (a.v_viewmat ? 2 : 0) | (a.fold ? 1 : 0);
+    const dim3 grid((unsigned)blocks), block(kProjThreads);
+    switch (variant) {
+        case 0: hipLaunchKernelGGL((project_bwd_kernel<false, false, false>), grid, block, 0, stream, P); break;
+        case 1: hipLaunchKernelGGL((project_bwd_kernel<false, false, true>), grid, block, 0, stream, P); break;
+        case 2: hipLaunchKernelGGL((project_bwd_kernel<false, true, false>), grid, block, 0, stream, P); break;
+        case 3: hipLaunchKernelGGL((project_bwd_kernel<false, true, true>), grid, block, 0, stream, P); break;
+        case 4: hipLaunchKernelGGL((project_bwd_kernel<true, false, false>), grid, block, 0, stream, P); break;
+        case 5: hipLaunchKernelGGL((project_bwd_kernel<true, false, true>), grid, block, 0, stream, P); break;
+        case 6: hipLaunchKernelGGL((project_bwd_kernel<true, true, false>), grid, block, 0, stream, P); break;
+        default: hipLaunchKernelGGL((project_bwd_kernel<true, true, true>), grid, block, 0, stream, P); break;
+    }
     if (a.v_viewmat)
         hipLaunchKernelGGL(viewmat_reduce_kernel, dim3((unsigned)a.B), dim3(kProjThreads), 0,
                            stream, sc.view_partials, blocks_per_image, a.v_viewmat);
