@@ -134,14 +134,16 @@ class TrainStep:
 
     def loss_and_grads(self) -> tuple[torch.Tensor, dict[str, torch.Tensor]]:
         leaves = [p.requires_grad_(True) for p in self.params.values()]
-        # the L1 loss fused into the blends (render_log then l1_loss, without the loss's own
-        # passes over the images)
-        loss, _ = render_log_loss(*leaves, target=self.targets, loss="l1",
-                                  viewmat=self.viewmats, background=self.background,
-                                  **self.camera)
-        grads = torch.autograd.grad(loss, leaves)
-        for p in leaves:
-            p.requires_grad_(False)
+        try:
+            # the L1 loss fused into the blends (render_log then l1_loss, without the loss's own
+            # passes over the images)
+            loss, _ = render_log_loss(*leaves, target=self.targets, loss="l1",
+                                      viewmat=self.viewmats, background=self.background,
+                                      **self.camera)
+            grads = torch.autograd.grad(loss, leaves)
+        finally:
+            for p in leaves:
+                p.requires_grad_(False)
         return loss.detach(), dict(zip(SPLAT_KEYS, grads))
 
     def mapped_loss_and_grads(self) -> tuple[torch.Tensor, dict[str, torch.Tensor]]:
@@ -153,10 +155,13 @@ class TrainStep:
             mapped = _LogParamsFn.apply(p["log_scales"], p["quats"], p["colors_logit"],
                                         p["opac_logit"])
         leaves = [p["means"].requires_grad_(True), *(t.requires_grad_(True) for t in mapped)]
-        loss, _ = render_loss(*leaves, target=self.targets, loss="l1", viewmat=self.viewmats,
-                              background=self.background, **self.camera)
-        grads = torch.autograd.grad(loss, leaves)
-        p["means"].requires_grad_(False)
+        try:
+            loss, _ = render_loss(*leaves, target=self.targets, loss="l1",
+                                  viewmat=self.viewmats, background=self.background,
+                                  **self.camera)
+            grads = torch.autograd.grad(loss, leaves)
+        finally:
+            p["means"].requires_grad_(False)
         return loss.detach(), dict(zip(SPLAT_KEYS, grads))
 
     def __call__(self) -> torch.Tensor:
