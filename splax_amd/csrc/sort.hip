@@ -7,7 +7,9 @@
 // partition counts its digits, (2) one workgroup per digit scans that digit's counts over the
 // partitions and writes the digit's total, (3) every partition ranks its keys stably with
 // ballot-based digit matching per wave and scatters keys and values through LDS so that each
-// digit's run (about 32 keys) leaves as a contiguous write. No partition waits on another: on MI355X the eight XCDs have separate
+// digit's run (about 32 keys) leaves as a contiguous write; each XCD scatters one contiguous
+// segment of the partitions, so the runs that neighbouring partitions write side by side merge
+// in one L2. No partition waits on another: on MI355X the eight XCDs have separate
 // L2s, so the per-digit status polling of a single-pass (look-back) sort costs device-scope
 // round trips and partial-line writes that the extra count read does not. Ranking follows
 // position order (wave-striped items, lanes in order, waves in order, partitions in index
@@ -345,9 +347,21 @@ rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ va
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t M = live_count(m_dev, M_bound);
-    const int64_t part = blockIdx.x;
+    // Workgroup b runs on XCD b mod 8 (the dispatcher deals workgroups to the eight XCDs in
+    // turn). Each XCD takes one contiguous segment of the live partitions, in order: the digit
+    // runs that consecutive partitions write side by side then meet in that XCD's L2, where
+    // their partial lines merge before they leave it (dealt in turn, neighbouring partitions
+    // sit on different XCDs and every run end leaves its L2 as a partial-line write). The
+    // segments split the live count, not the grid, which a capacity-bounded caller sizes above
+    // it, so every XCD gets an equal share. Workgroups past the segments exit (uniform, before
+    // any barrier); the grid holds at least eight segments' worth.
+    const int64_t live_parts = (M + kTile - 1) / kTile;
+    const int64_t per_xcd = (live_parts + 7) >> 3;
+    const int64_t seg_pos = blockIdx.x >> 3;
+    if (seg_pos >= per_xcd) return;
+    const int64_t part = (int64_t)(blockIdx.x & 7u) * per_xcd + seg_pos;
+    if (part >= live_parts) return;
     const int64_t base = part * kTile;
-    if (base >= M) return;  // a partition past the count (uniform, before any barrier)
     for (int i = tid; i < kSortWaves * 256; i += kSortThreads) (&s_cnt[0][0])[i] = 0u;
     __syncthreads();
     const int64_t wbase = base + (int64_t)wave * (kItems * 64);
@@ -482,7 +496,9 @@ static void launch_pass(const K* keys_in, const int32_t* vals_in, const int32_t*
                        0, stream, keys_in, M, m_dev, shift, counts, parts, bins, nbins2);
     hipLaunchKernelGGL(rts_scan_kernel, dim3(256), dim3(kScanThreads), 0, stream, counts, parts,
                        totals);
-    hipLaunchKernelGGL((rts_scatter_kernel<K, kItems, KO>), dim3((unsigned)parts),
+    // the scatter's grid: whole groups of eight workgroups, one per XCD (the kernel deals the
+    // live partitions to XCD segments)
+    hipLaunchKernelGGL((rts_scatter_kernel<K, kItems, KO>), dim3((unsigned)((parts + 7) / 8 * 8)),
                        dim3(kSortThreads), 0, stream, keys_in, vals_in, ids_in, keys_out,
                        vals_out, ids_out, M, m_dev, shift, counts, totals, parts);
 }
