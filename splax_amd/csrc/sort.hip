@@ -7,9 +7,9 @@
 // partition counts its digits, (2) one workgroup per digit scans that digit's counts over the
 // partitions and writes the digit's total, (3) every partition ranks its keys stably with
 // ballot-based digit matching per wave and scatters keys and values through LDS so that each
-// digit's run (about 32 keys) leaves as a contiguous write; each XCD scatters one contiguous
-// segment of the partitions, so the runs that neighbouring partitions write side by side merge
-// in one L2. No partition waits on another: on MI355X the eight XCDs have separate
+// digit's run (about 32 keys) leaves as a contiguous write; each XCD counts and scatters one
+// contiguous segment of the partitions, so the runs and counts that neighbouring partitions
+// write side by side merge in one L2. No partition waits on another: on MI355X the eight XCDs have separate
 // L2s, so the per-digit status polling of a single-pass (look-back) sort costs device-scope
 // round trips and partial-line writes that the extra count read does not. Ranking follows
 // position order (wave-striped items, lanes in order, waves in order, partitions in index
@@ -217,14 +217,35 @@ constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
 static_assert(kSortThreads * 4 == kSortTileMin, "smallest partition");
 
+// The partition that workgroup blockIdx.x of a count or scatter launch takes, or -1 for none.
+// Workgroup b runs on XCD b mod 8 (the dispatcher deals workgroups to the eight XCDs in turn).
+// Each XCD takes one contiguous segment of the live partitions, in order, so neighbouring
+// partitions share an L2: the runs of one digit that they scatter side by side, and the counts
+// they store side by side in a digit's row, merge there into whole lines before they leave it
+// (dealt in turn, neighbouring partitions sit on different XCDs and every run end or count
+// leaves its L2 as a partial-line write). The segments split the live partitions, not the grid,
+// which a capacity-bounded caller sizes above the count, so every XCD gets an equal share. The
+// grid must hold at least 8 * ceil(live_parts / 8) workgroups.
+__device__ __forceinline__ int64_t xcd_segment_part(int64_t live_parts) {
+    const int64_t per_xcd = (live_parts + 7) >> 3;
+    const int64_t seg_pos = blockIdx.x >> 3;
+    if (seg_pos >= per_xcd) return -1;
+    const int64_t part = (int64_t)(blockIdx.x & 7u) * per_xcd + seg_pos;
+    return part < live_parts ? part : -1;
+}
+
+// Workgroups of a count or scatter launch over `parts` partitions: whole groups of eight, one
+// workgroup per XCD (the kernels deal the live partitions to XCD segments).
+static unsigned segment_grid(int64_t parts) { return (unsigned)((parts + 7) / 8 * 8); }
+
 // (1) digit counts of one partition of kItems * kSortThreads keys, stored digit-major:
-// counts[d * parts + p]. The first pass also clears the tile bins (nbins2 > 0).
+// counts[d * parts + p]. The first pass also clears the tile bins (nbins2 > 0). Only the live
+// partitions store counts; the digit scan reads the columns past them as zero.
 template <typename K, int kItems>
 __global__ void __launch_bounds__(kSortThreads)
 rts_count_kernel(const K* __restrict__ keys, int64_t M_bound, const int32_t* __restrict__ m_dev,
                  int shift, uint32_t* __restrict__ counts, int64_t parts,
                  int32_t* __restrict__ bins, int64_t nbins2) {
-    // partitions past the count (a grid sized by capacity) count nothing: zero columns
     __shared__ uint32_t s_h[kSortWaves][256];
     const int tid = threadIdx.x, wave = tid >> 6;
     for (int i = tid; i < kSortWaves * 256; i += kSortThreads) (&s_h[0][0])[i] = 0u;
@@ -234,7 +255,10 @@ rts_count_kernel(const K* __restrict__ keys, int64_t M_bound, const int32_t* __r
         bins[i] = 0;
     __syncthreads();
     const int64_t M = live_count(m_dev, M_bound);
-    const int64_t base = (int64_t)blockIdx.x * (kItems * kSortThreads);
+    constexpr int64_t kPart = (int64_t)kItems * kSortThreads;
+    const int64_t part = xcd_segment_part((M + kPart - 1) / kPart);
+    if (part < 0) return;  // uniform, after the workgroup's share of the bin clearing
+    const int64_t base = part * kPart;
     K key[kItems];
 #pragma unroll
     for (int i = 0; i < kItems; ++i) {
@@ -251,7 +275,7 @@ rts_count_kernel(const K* __restrict__ keys, int64_t M_bound, const int32_t* __r
         uint32_t c = 0;
 #pragma unroll
         for (int w = 0; w < kSortWaves; ++w) c += s_h[w][tid];
-        counts[(int64_t)tid * parts + blockIdx.x] = c;
+        counts[(int64_t)tid * parts + part] = c;
     }
 }
 
@@ -276,20 +300,22 @@ __device__ __forceinline__ uint32_t scan_256(uint32_t v, uint32_t* s_tmp, uint32
 
 // (2) one workgroup per digit d: counts[d][p] <- sum_{q < p} counts[d][q], and totals[d]. 1024
 // threads, four counts each: up to 4096 partitions (16M keys at 4 keys per thread, 32M at 8) in
-// one pass over the row.
+// one pass over the row. Columns past the live partitions (of part_keys keys each) count as zero.
 constexpr int kScanThreads = 1024;
 __global__ void __launch_bounds__(kScanThreads)
-rts_scan_kernel(uint32_t* __restrict__ counts, int64_t parts, uint32_t* __restrict__ totals) {
+rts_scan_kernel(uint32_t* __restrict__ counts, int64_t parts, uint32_t* __restrict__ totals,
+                int64_t M_bound, const int32_t* __restrict__ m_dev, int64_t part_keys) {
     __shared__ uint32_t s_wave[kScanThreads / 64];
     const int d = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint32_t carry = 0;
     uint32_t* row = counts + (int64_t)d * parts;
+    const int64_t live = (live_count(m_dev, M_bound) + part_keys - 1) / part_keys;
     for (int64_t p0 = 0; p0 < parts; p0 += 4 * kScanThreads) {
         // four consecutive counts per thread
         const int64_t p = p0 + 4 * (int64_t)tid;
         uint32_t v[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) v[k] = p + k < parts ? row[p + k] : 0u;
+        for (int k = 0; k < 4; ++k) v[k] = p + k < live ? row[p + k] : 0u;
         const uint32_t mine = (v[0] + v[1]) + (v[2] + v[3]);
         const uint32_t incl = (uint32_t)wave_inclusive_scan_i32((int32_t)mine, lane);
         if (lane == 63) s_wave[wave] = incl;
@@ -347,20 +373,8 @@ rts_scatter_kernel(const K* __restrict__ keys_in, const int32_t* __restrict__ va
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t M = live_count(m_dev, M_bound);
-    // Workgroup b runs on XCD b mod 8 (the dispatcher deals workgroups to the eight XCDs in
-    // turn). Each XCD takes one contiguous segment of the live partitions, in order: the digit
-    // runs that consecutive partitions write side by side then meet in that XCD's L2, where
-    // their partial lines merge before they leave it (dealt in turn, neighbouring partitions
-    // sit on different XCDs and every run end leaves its L2 as a partial-line write). The
-    // segments split the live count, not the grid, which a capacity-bounded caller sizes above
-    // it, so every XCD gets an equal share. Workgroups past the segments exit (uniform, before
-    // any barrier); the grid holds at least eight segments' worth.
-    const int64_t live_parts = (M + kTile - 1) / kTile;
-    const int64_t per_xcd = (live_parts + 7) >> 3;
-    const int64_t seg_pos = blockIdx.x >> 3;
-    if (seg_pos >= per_xcd) return;
-    const int64_t part = (int64_t)(blockIdx.x & 7u) * per_xcd + seg_pos;
-    if (part >= live_parts) return;
+    const int64_t part = xcd_segment_part((M + kTile - 1) / kTile);
+    if (part < 0) return;  // uniform, before any barrier
     const int64_t base = part * kTile;
     for (int i = tid; i < kSortWaves * 256; i += kSortThreads) (&s_cnt[0][0])[i] = 0u;
     __syncthreads();
@@ -492,13 +506,12 @@ static void launch_pass(const K* keys_in, const int32_t* vals_in, const int32_t*
                         int32_t* bins, int64_t nbins2, hipStream_t stream) {
     // M bounds the count (live_count): the grid covers M keys
     const int64_t parts = (M + (int64_t)kItems * kSortThreads - 1) / ((int64_t)kItems * kSortThreads);
-    hipLaunchKernelGGL((rts_count_kernel<K, kItems>), dim3((unsigned)parts), dim3(kSortThreads),
-                       0, stream, keys_in, M, m_dev, shift, counts, parts, bins, nbins2);
+    hipLaunchKernelGGL((rts_count_kernel<K, kItems>), dim3(segment_grid(parts)),
+                       dim3(kSortThreads), 0, stream, keys_in, M, m_dev, shift, counts, parts,
+                       bins, nbins2);
     hipLaunchKernelGGL(rts_scan_kernel, dim3(256), dim3(kScanThreads), 0, stream, counts, parts,
-                       totals);
-    // the scatter's grid: whole groups of eight workgroups, one per XCD (the kernel deals the
-    // live partitions to XCD segments)
-    hipLaunchKernelGGL((rts_scatter_kernel<K, kItems, KO>), dim3((unsigned)((parts + 7) / 8 * 8)),
+                       totals, M, m_dev, (int64_t)kItems * kSortThreads);
+    hipLaunchKernelGGL((rts_scatter_kernel<K, kItems, KO>), dim3(segment_grid(parts)),
                        dim3(kSortThreads), 0, stream, keys_in, vals_in, ids_in, keys_out,
                        vals_out, ids_out, M, m_dev, shift, counts, totals, parts);
 }
