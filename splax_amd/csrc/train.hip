@@ -32,7 +32,7 @@ namespace splat {
 // ------------------------------------------------------------------ Adam
 
 constexpr int kAdamMaxGroups = 8;
-constexpr int kAdamChunk = 2048;  // elements per workgroup (8 per thread)
+constexpr int kAdamChunk = 1024;  // elements per workgroup (4 per thread)
 
 struct AdamGroupDev {
     float* p; const float* g; float* mu; float* nu;
@@ -48,41 +48,86 @@ struct AdamParams {
     float b1, c1, b2, c2, eps, eps_root, bc1, bc2;
 };
 
+// The update of one workgroup's chunk of group G, with kMap the group's parameter map. Every
+// load of the chunk is issued before any update (restrict-qualified pointers: the compiler
+// would otherwise keep each element's loads behind the previous element's stores), so a thread
+// has its four elements' reads in flight together. The gradient of the stored parameter is the
+// reverse-mode rule of render_log's map applied to the mapped value's cotangent
+// (log_params_bwd_kernel's float operations), at the parameter before this update.
+template <int kMap>
+__device__ __forceinline__ void adam_chunk(const AdamParams& P, const AdamGroupDev& G,
+                                           int64_t base) {
+    constexpr int K = kAdamChunk / 256;
+    float* __restrict__ pp = G.p;
+    const float* __restrict__ gp = G.g;
+    float* __restrict__ mp = G.mu;
+    float* __restrict__ np = G.nu;
+    const int64_t i0 = base + threadIdx.x;
+    float g[K], pv[K], m[K], v[K];
+    float q[K][4], vy[K][4];  // kMap == SPLAT_MAP_QUAT: the element's row of the group [rows, 4]
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        const int64_t i = i0 + j * 256;
+        if (i < G.size) {
+            if constexpr (kMap == SPLAT_MAP_QUAT) {
+                const int64_t row = i >> 2;  // the group is 16-byte aligned
+                const float4 q4 = reinterpret_cast<const float4*>(pp)[row];
+                const float4 v4 = reinterpret_cast<const float4*>(gp)[row];
+                q[j][0] = q4.x; q[j][1] = q4.y; q[j][2] = q4.z; q[j][3] = q4.w;
+                vy[j][0] = v4.x; vy[j][1] = v4.y; vy[j][2] = v4.z; vy[j][3] = v4.w;
+            } else {
+                g[j] = gp[i];
+                pv[j] = pp[i];
+            }
+            m[j] = mp[i];
+            v[j] = np[i];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        const int64_t i = i0 + j * 256;
+        if (i >= G.size) break;
+        float gg, p0;
+        if constexpr (kMap == SPLAT_MAP_QUAT) {
+            const int c = (int)(i & 3);
+            // whole-row copies, indexed by the component (a dynamic index into q[j] itself
+            // would put the arrays in scratch memory)
+            const float qa[4] = {q[j][0], q[j][1], q[j][2], q[j][3]};
+            const float va[4] = {vy[j][0], vy[j][1], vy[j][2], vy[j][3]};
+            gg = map_quat_vjp(qa, va, c);
+            p0 = c == 0 ? qa[0] : c == 1 ? qa[1] : c == 2 ? qa[2] : qa[3];
+        } else if constexpr (kMap == SPLAT_MAP_EXP) {
+            gg = map_exp_vjp(g[j], pv[j]);
+            p0 = pv[j];
+        } else if constexpr (kMap == SPLAT_MAP_SIGMOID) {
+            gg = map_sigmoid_vjp(g[j], pv[j]);
+            p0 = pv[j];
+        } else {
+            gg = g[j];
+            p0 = pv[j];
+        }
+        const float mm = P.c1 * gg + P.b1 * m[j];
+        const float vv = P.c2 * (gg * gg) + P.b2 * v[j];
+        const float mh = mm / P.bc1;
+        const float vh = vv / P.bc2;
+        const float u = mh / (sqrtf(vh + P.eps_root) + P.eps);
+        mp[i] = mm;
+        np[i] = vv;
+        pp[i] = p0 + G.neg_lr * u;
+    }
+}
+
 __global__ void __launch_bounds__(256) adam_step_kernel(AdamParams P) {
     const int64_t b = blockIdx.x;
     int gi = 0;
     while (gi + 1 < P.n_groups && b >= P.block_start[gi + 1]) ++gi;  // uniform per workgroup
     const AdamGroupDev G = P.grp[gi];
     const int64_t base = (b - P.block_start[gi]) * kAdamChunk;
-#pragma unroll
-    for (int j = 0; j < kAdamChunk / 256; ++j) {
-        const int64_t i = base + j * 256 + threadIdx.x;
-        if (i >= G.size) break;
-        // the gradient of the stored parameter: the reverse-mode rule of render_log's map
-        // applied to the mapped value's cotangent (log_params_bwd_kernel's float operations),
-        // with the parameter before this update
-        float g = G.g[i];
-        if (G.map == SPLAT_MAP_EXP) {
-            g = map_exp_vjp(g, G.p[i]);
-        } else if (G.map == SPLAT_MAP_SIGMOID) {
-            g = map_sigmoid_vjp(g, G.p[i]);
-        } else if (G.map == SPLAT_MAP_QUAT) {
-            const int64_t row = i >> 2;  // the group is [rows, 4], 16-byte aligned
-            const float4 q4 = reinterpret_cast<const float4*>(G.p)[row];
-            const float4 v4 = reinterpret_cast<const float4*>(G.g)[row];
-            const float q[4] = {q4.x, q4.y, q4.z, q4.w};
-            const float vy[4] = {v4.x, v4.y, v4.z, v4.w};
-            g = map_quat_vjp(q, vy, (int)(i & 3));
-        }
-        float m = G.mu[i], v = G.nu[i];
-        m = P.c1 * g + P.b1 * m;
-        v = P.c2 * (g * g) + P.b2 * v;
-        const float mh = m / P.bc1;
-        const float vh = v / P.bc2;
-        const float u = mh / (sqrtf(vh + P.eps_root) + P.eps);
-        G.mu[i] = m;
-        G.nu[i] = v;
-        G.p[i] = G.p[i] + G.neg_lr * u;
+    switch (G.map) {  // uniform per workgroup
+    case SPLAT_MAP_EXP: adam_chunk<SPLAT_MAP_EXP>(P, G, base); break;
+    case SPLAT_MAP_SIGMOID: adam_chunk<SPLAT_MAP_SIGMOID>(P, G, base); break;
+    case SPLAT_MAP_QUAT: adam_chunk<SPLAT_MAP_QUAT>(P, G, base); break;
+    default: adam_chunk<SPLAT_MAP_NONE>(P, G, base); break;
     }
 }
 
