@@ -25,20 +25,30 @@ struct LogParams {
     float* v_log_scales; float* v_quats_in; float* v_logit_colors; float* v_logit_opac;
 };
 
+// Both map kernels read every input of their item before they store anything: a load placed
+// after a store to another array stays behind it (the compiler cannot rule out aliasing), and the
+// interleaved form made each item several dependent memory round trips.
 __global__ void __launch_bounds__(256) log_params_fwd_kernel(LogParams P) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= P.n) return;
+    float ls[3], lc[3];
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-        P.scales[3 * i + k] = det_expf(P.log_scales[3 * i + k]);
-        P.colors[3 * i + k] = map_sigmoid(P.logit_colors[3 * i + k]);
+        ls[k] = P.log_scales[3 * i + k];
+        lc[k] = P.logit_colors[3 * i + k];
     }
     const float4 q4 = reinterpret_cast<const float4*>(P.quats)[i];
+    const float lo = P.logit_opac[i];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        P.scales[3 * i + k] = det_expf(ls[k]);
+        P.colors[3 * i + k] = map_sigmoid(lc[k]);
+    }
     const float q[4] = {q4.x, q4.y, q4.z, q4.w};
     const float s = quat_norm(q) + kQuatEps;
     reinterpret_cast<float4*>(P.quats_out)[i] =
         make_float4(q[0] / s, q[1] / s, q[2] / s, q[3] / s);
-    P.opac[i] = map_sigmoid(P.logit_opac[i]);
+    P.opac[i] = map_sigmoid(lo);
 }
 
 // A null cotangent is a zero one.
@@ -47,18 +57,28 @@ __device__ __forceinline__ float cot(const float* v, int64_t j) { return v ? v[j
 __global__ void __launch_bounds__(256) log_params_bwd_kernel(LogParams P) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= P.n) return;
+    float vs[3], ls[3], vc[3], lc[3], vy[4];
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         const int64_t j = 3 * i + k;
-        P.v_log_scales[j] = map_exp_vjp(cot(P.v_scales, j), P.log_scales[j]);
-        P.v_logit_colors[j] = map_sigmoid_vjp(cot(P.v_colors, j), P.logit_colors[j]);
+        vs[k] = cot(P.v_scales, j);
+        ls[k] = P.log_scales[j];
+        vc[k] = cot(P.v_colors, j);
+        lc[k] = P.logit_colors[j];
     }
-    P.v_logit_opac[i] = map_sigmoid_vjp(cot(P.v_opac, i), P.logit_opac[i]);
+    const float vo = cot(P.v_opac, i), lo = P.logit_opac[i];
     const float4 q4 = reinterpret_cast<const float4*>(P.quats)[i];
-    const float q[4] = {q4.x, q4.y, q4.z, q4.w};
-    float vy[4], vq[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) vy[k] = cot(P.v_quats, 4 * i + k);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int64_t j = 3 * i + k;
+        P.v_log_scales[j] = map_exp_vjp(vs[k], ls[k]);
+        P.v_logit_colors[j] = map_sigmoid_vjp(vc[k], lc[k]);
+    }
+    P.v_logit_opac[i] = map_sigmoid_vjp(vo, lo);
+    const float q[4] = {q4.x, q4.y, q4.z, q4.w};
+    float vq[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) vq[k] = map_quat_vjp(q, vy, k);
     reinterpret_cast<float4*>(P.v_quats_in)[i] = make_float4(vq[0], vq[1], vq[2], vq[3]);
