@@ -946,7 +946,14 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
         off = b * P.M;
     }
     int64_t lo = 0, hi = 0;
+    // the item's conic (and with compensation its opacity) load with its range, ahead of the
+    // row sums rather than behind them
+    float ca = 0.f, cb = 0.f, cc = 0.f, op = 0.f;
     if (valid) {
+        ca = P.conics[3 * gi];
+        cb = P.conics[3 * gi + 1];
+        cc = P.conics[3 * gi + 2];
+        if (P.compensate) op = P.opac[gi % P.rows_opac];
         lo = gi > 0 ? (int64_t)P.cum[gi - 1] : 0;
         hi = P.cum[gi];
         lo = lo < 0 ? 0 : lo;
@@ -981,10 +988,9 @@ __global__ void __launch_bounds__(256) grad_gather_kernel(GatherParams P) {
     float vo = (float)s[8];
     float vx = 0.f, vy = 0.f;
     if (s[6] != 0.0 || s[7] != 0.0 || P.compensate) {
-        const float a = P.conics[3 * gi], b = P.conics[3 * gi + 1], c = P.conics[3 * gi + 2];
-        vx = (float)((double)a * s[6] + (double)b * s[7]);
-        vy = (float)((double)b * s[6] + (double)c * s[7]);
-        if (P.compensate) vo = compensation_vjp(vo, P.opac[gi % P.rows_opac], a, b, c, vc);
+        vx = (float)((double)ca * s[6] + (double)cb * s[7]);
+        vy = (float)((double)cb * s[6] + (double)cc * s[7]);
+        if (P.compensate) vo = compensation_vjp(vo, op, ca, cb, cc, vc);
     }
     P.v_conic[3 * og] = vc[0];
     P.v_conic[3 * og + 1] = vc[1];
