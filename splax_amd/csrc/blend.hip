@@ -210,12 +210,12 @@ struct BatchLds {
 constexpr int kBwdBatch = 128;
 
 // Stages the record of item `id` (the sorted range's entry for slot `tid`) into slot `tid` (one
-// barrier), then each wave builds
-// its own record lists from the staged masks, in slot order: with kRows the lists of its four
-// sub-blocks (one per 16-lane row), otherwise the list of its whole quadrant (a record reaches a
-// quadrant when it reaches one of its sub-blocks, which is the 8x8 box test). `live` is false
-// for the clamped tail slots of the last batch (they reach no sub-block). Returns the length of
-// the wave's longest list, with kRows plus 65536 times the calling lane's row list length.
+// barrier), then each wave builds its own record lists from the staged masks, in slot order:
+// with kRows the lists of its four sub-blocks (one per 16-lane row), otherwise the list of its
+// whole quadrant (a record reaches a quadrant when it reaches one of its sub-blocks, which is the
+// 8x8 box test). `live` is false for the clamped tail slots of the last batch (they reach no
+// sub-block). Returns the length of the wave's longest list, with kRows plus 65536 times the
+// calling lane's row list length.
 template <bool kRows, int kBatch>
 __device__ __forceinline__ int stage_batch(const BlendCommon& C, BatchLds<kRows, kBatch>& L,
                                            int32_t id, bool live, int tile_x, int tile_y) {
