@@ -277,15 +277,63 @@ rts_count_kernel(const K* __restrict__ keys, int64_t M_bound, const int32_t* __r
     if (part < 0) return;  // uniform, after the workgroup's share of the bin clearing
     const int64_t base = part * kPart;
     K key[kItems];
+    constexpr int kBytes = kItems * (int)sizeof(K);
+    const int64_t my0 = base + (int64_t)tid * kItems;
+    if constexpr (sizeof(K) <= 4 && kBytes % 4 == 0) {
+        // a digit count does not depend on the keys' order: each thread takes kItems
+        // consecutive keys, read as whole 32-bit words (the run starts kBytes * tid bytes into
+        // the partition, so the widest load that divides kBytes is aligned), where one load per
+        // key took more load instructions than the bytes need (the sort 0.106 -> 0.103 ms at
+        // config 2, 0.715 -> 0.692 ms at config 4); 64-bit keys and odd 16-bit runs keep the
+        // wave-striped scalar loads
+        if (my0 + kItems <= M) {
+            constexpr int kW = kBytes / 4;
+            uint32_t w[kW];
+            const char* src = reinterpret_cast<const char*>(keys + my0);
+            if constexpr (kBytes % 16 == 0) {
 #pragma unroll
-    for (int i = 0; i < kItems; ++i) {
-        const int64_t pos = base + i * kSortThreads + tid;
-        key[i] = pos < M ? keys[pos] : (K)0;
-    }
+                for (int q = 0; q < kW / 4; ++q) {
+                    const uint4 v = reinterpret_cast<const uint4*>(src)[q];
+                    w[4 * q] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
+                }
+            } else if constexpr (kBytes % 8 == 0) {
 #pragma unroll
-    for (int i = 0; i < kItems; ++i) {
-        const int64_t pos = base + i * kSortThreads + tid;
-        if (pos < M) atomicAdd(&s_h[wave][(uint32_t)(key[i] >> shift) & 255u], 1u);
+                for (int q = 0; q < kW / 2; ++q) {
+                    const uint2 v = reinterpret_cast<const uint2*>(src)[q];
+                    w[2 * q] = v.x; w[2 * q + 1] = v.y;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < kW; ++q) w[q] = reinterpret_cast<const uint32_t*>(src)[q];
+            }
+#pragma unroll
+            for (int i = 0; i < kItems; ++i) {
+                if constexpr (sizeof(K) == 4)
+                    key[i] = (K)w[i];
+                else
+                    key[i] = (K)((w[i / 2] >> (16 * (i & 1))) & 0xffffu);
+            }
+#pragma unroll
+            for (int i = 0; i < kItems; ++i)
+                atomicAdd(&s_h[wave][(uint32_t)(key[i] >> shift) & 255u], 1u);
+        } else {
+#pragma unroll
+            for (int i = 0; i < kItems; ++i) key[i] = my0 + i < M ? keys[my0 + i] : (K)0;
+#pragma unroll
+            for (int i = 0; i < kItems; ++i)
+                if (my0 + i < M) atomicAdd(&s_h[wave][(uint32_t)(key[i] >> shift) & 255u], 1u);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            const int64_t pos = base + i * kSortThreads + tid;
+            key[i] = pos < M ? keys[pos] : (K)0;
+        }
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            const int64_t pos = base + i * kSortThreads + tid;
+            if (pos < M) atomicAdd(&s_h[wave][(uint32_t)(key[i] >> shift) & 255u], 1u);
+        }
     }
     __syncthreads();
     if (tid < 256) {
