@@ -9,11 +9,11 @@
 // ballot-based digit matching per wave and scatters keys and values through LDS so that each
 // digit's run (about 32 keys) leaves as a contiguous write; each XCD counts and scatters one
 // contiguous segment of the partitions, so the runs and counts that neighbouring partitions
-// write side by side merge in one L2. No partition waits on another: on MI355X the eight XCDs have separate
-// L2s, so the per-digit status polling of a single-pass (look-back) sort costs device-scope
-// round trips and partial-line writes that the extra count read does not. Ranking follows
-// position order (wave-striped items, lanes in order, waves in order, partitions in index
-// order), so the sort is stable: ties keep emission order, which is the reference's
+// write side by side merge in one L2. No partition waits on another: on MI355X the eight XCDs
+// have separate L2s, so the per-digit status polling of a single-pass (look-back) sort costs
+// device-scope round trips and partial-line writes that the extra count read does not. Ranking
+// follows position order (wave-striped items, lanes in order, waves in order, partitions in
+// index order), so the sort is stable: ties keep emission order, which is the reference's
 // (key, position) order.
 //
 // Each key carries two values: the reference's value (the flat item id) and the key's emission
