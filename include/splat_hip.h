@@ -315,7 +315,7 @@ int splat_render_bwd(splat_stream_t stream, const float* means3d, int64_t rows_m
 
 /* One Adam parameter group: params, grads, first and second moments (size elements each) and
  * its learning rate at this step (schedules are evaluated by the caller at the pre-increment
- * count, as optax's scale_by_schedule does). */
+ * count, as optax's scale_by_schedule does). The four buffers of a group must not overlap. */
 typedef struct splat_adam_group {
     float* params;
     const float* grads;
