@@ -1,5 +1,7 @@
 """Seeded parity sweep: small random scenes through ``splax_amd.render`` against the oracle.
 
+Three groups: the plain render, render_loss (MSE and L1) and the antialiased render.
+
 Each case draws a scene in the style of the reference's random tests
 (tests/test_warp_rasterize.py:91-104, conftest.random_scene) with its sizes and shapes varied:
 1 to 20000 gaussians (log-uniform), image sides of 8 to 200 pixels (mostly not multiples of the
@@ -38,6 +40,7 @@ pytestmark = pytest.mark.gpu
 
 CASES = 24
 LOSS_CASES = 8
+AA_CASES = 8
 BAND_MIN = 32
 
 
@@ -165,4 +168,30 @@ def test_random_scene_loss_matches_oracle(seed):
     assert_bit_exact(got_img, rimg.reshape(shape), f"seed {seed}/img")
     ulps = abs(int(np.float32(got_loss).view(np.int32)) - int(np.float32(ref_loss).view(np.int32)))
     assert ulps <= 1, (got_loss, float(ref_loss))
+    _check_grads(grads, rg, tg, cond, seed)
+
+
+@pytest.mark.parametrize("seed", range(300, 300 + AA_CASES))
+def test_random_scene_antialiased_matches_oracle(seed):
+    """render(antialiased=True) (the compensation fused into the blends, config 4's render) on
+    swept scenes, held like the plain render to the oracle's chain with the compensation
+    (splax/_render.py:105-110) and its float64 truth."""
+    sc, vms, w, desc = draw_case(seed)
+    print(f"[case] sweep antialiased seed {seed}: {desc}", flush=True)
+    H, W = sc["img_shape"]
+    B = vms.shape[0]
+    p = {k: _t(sc[k], grad=True) for k in ("means", "scales", "quats", "colors", "opac")}
+    vm = _t(vms if B > 1 else vms[0], grad=True)
+    img, _ = splax_amd.render(*p.values(), viewmat=vm, background=_t(sc["bg"]),
+                              img_shape=(H, W), f=sc["f"], c=sc["c"], antialiased=True)
+    wt = w if B > 1 else w[0]
+    (img * _t(wt)).sum().backward()
+    torch.cuda.synchronize()
+    got_img = img.detach().cpu().numpy()
+    grads = {k: v.grad.detach().cpu().numpy() for k, v in p.items()}
+    grads["viewmat"] = vm.grad.detach().cpu().numpy()
+
+    rimg, rg, cond = TP.weighted_chain(sc, wt, vm=vms, antialiased=True)
+    _, tg, _ = TP.weighted_chain(sc, wt, vm=vms, truth=True, antialiased=True)
+    assert_bit_exact(got_img, rimg.reshape(got_img.shape), f"seed {seed}/img")
     _check_grads(grads, rg, tg, cond, seed)

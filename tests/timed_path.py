@@ -214,11 +214,14 @@ def band_errors(got, ref, truth, cond):
     return rows
 
 
-def weighted_chain(sc, w, vm=None, truth=False):
+def weighted_chain(sc, w, vm=None, truth=False, antialiased=False):
     """The oracle's forward and chained backward of sum(img * w) for a random_scene-style
     dictionary (conftest.random_scene), float32 or the float64 truth; with B stacked viewmats
     (vm of shape (B, 4, 4), w of shape (B, H, W, 3)) the per-camera item gradients are summed.
-    Returns (image, grads keyed means / scales / quats (wxyz) / colors / opac / viewmat, cond)."""
+    With antialiased, the blend takes the compensated opacities o * rho(conic) of the visible
+    items and the tile intersection the raw ones, and the backward adds the compensation's VJP
+    (splax/_render.py:105-110, as oracle_chain does). Returns (image, grads keyed means / scales /
+    quats (wxyz) / colors / opac / viewmat, cond)."""
     H, W = sc["img_shape"]
     n = len(sc["means"])
     vm = sc["vm"] if vm is None else vm
@@ -227,26 +230,41 @@ def weighted_chain(sc, w, vm=None, truth=False):
     xys, depths, radii, conics, nth, cum = O.project_fwd(
         sc["means"], sc["scales"], q, vm.reshape(-1, 4), sc["opac"], n=n, total=B * n,
         img_shape=(H, W), f=sc["f"], c=sc["c"])
-    img, Ts, fidx, _, _ = O.rasterize_fwd(sc["colors"], sc["opac"], sc["opac"], sc["bg"], xys,
-                                          depths, radii, conics, cum, n=n, B=B, img_shape=(H, W))
-    args = (sc["colors"], sc["opac"], sc["opac"], sc["bg"], xys, depths, radii, conics, cum, Ts,
-            fidx, np.asarray(w, np.float32).reshape(-1, 3))
+    vis = radii.reshape(-1) > 0
+    opac_b = np.tile(np.asarray(sc["opac"], np.float32).reshape(-1), B)
+    ob = sc["opac"]
+    if antialiased:
+        rho, _ = O.compensation_rho(conics)
+        ob = (opac_b * np.where(vis, rho, np.float32(1))).astype(np.float32).reshape(-1, 1)
+    img, Ts, fidx, _, _ = O.rasterize_fwd(sc["colors"], ob, sc["opac"], sc["bg"], xys, depths,
+                                          radii, conics, cum, n=n, B=B, img_shape=(H, W))
+    args = (sc["colors"], ob, sc["opac"], sc["bg"], xys, depths, radii, conics, cum, Ts, fidx,
+            np.asarray(w, np.float32).reshape(-1, 3))
     kw = dict(n=n, B_out=B, B_geom=B, img_shape=(H, W))
     if truth:
         vc, vo, vxy, vcon = O.rasterize_bwd_f64(*args, **kw)
+    else:
+        vc, vo, vxy, vcon, _ = O.rasterize_bwd(*args, **kw)
+    if antialiased:
+        if truth:
+            v_op, v_c = truth64.compensation_vjp_f64(vo, opac_b, conics)
+        else:
+            v_op, v_c = O.compensation_vjp(vo, opac_b, conics)
+        vo = np.where(vis, v_op, 0)  # culled items: rho = 1 in the reference, no blend terms
+        vcon = vcon + np.where(vis[:, None], v_c, 0)
+    if truth:
         vm_, vs_, vq_, vv_ = truth64.project_bwd_f64(
             sc["means"], sc["scales"], q, vm.reshape(B, 4, 4), radii, conics, vxy,
             np.zeros(B * n), vcon, n=n, B=B, f=sc["f"])
     else:
-        vc, vo, vxy, vcon, _ = O.rasterize_bwd(*args, **kw)
         vm_, vs_, vq_, vv_, _ = O.project_bwd(sc["means"], sc["scales"], q, vm.reshape(-1, 4),
                                               radii, conics, vxy, np.zeros(B * n, np.float32),
-                                              vcon, n=n, B=B, f=sc["f"])
+                                              np.asarray(vcon, np.float32), n=n, B=B,
+                                              f=sc["f"])
     g = dict(means=_fold(vm_, B, n), scales=_fold(vs_, B, n),
              quats=np.roll(_fold(vq_, B, n), 1, axis=-1), colors=_fold(vc, B, n),
              opac=_fold(np.asarray(vo).reshape(-1, 1), B, n),
              viewmat=np.asarray(vv_, np.float64).reshape(B, 4, 4))
-    vis = radii.reshape(-1) > 0
     ca, cb, cc = (conics[:, k].astype(np.float64) for k in range(3))
     cond = np.where(vis, (ca + cc) ** 2 / np.maximum(ca * cc - cb * cb, 1e-300), 0.0)
     return img, g, cond.reshape(B, n).max(0)
