@@ -1,6 +1,7 @@
 """Seeded parity sweep: small random scenes through ``splax_amd.render`` against the oracle.
 
-Three groups: the plain render, render_loss (MSE and L1) and the antialiased render.
+Four groups: the plain render, render_loss (MSE and L1), the antialiased render and the
+render with the expected-depth channel.
 
 Each case draws a scene in the style of the reference's random tests
 (tests/test_warp_rasterize.py:91-104, conftest.random_scene) with its sizes and shapes varied:
@@ -41,6 +42,7 @@ pytestmark = pytest.mark.gpu
 CASES = 24
 LOSS_CASES = 8
 AA_CASES = 8
+DEPTH_CASES = 8
 BAND_MIN = 32
 
 
@@ -194,4 +196,32 @@ def test_random_scene_antialiased_matches_oracle(seed):
     rimg, rg, cond = TP.weighted_chain(sc, wt, vm=vms, antialiased=True)
     _, tg, _ = TP.weighted_chain(sc, wt, vm=vms, truth=True, antialiased=True)
     assert_bit_exact(got_img, rimg.reshape(got_img.shape), f"seed {seed}/img")
+    _check_grads(grads, rg, tg, cond, seed)
+
+
+@pytest.mark.parametrize("seed", range(400, 400 + DEPTH_CASES))
+def test_random_scene_depth_matches_oracle(seed):
+    """render(render_depth=True) on swept scenes: the image and the expected depth bit for bit,
+    and the gradients of sum(img * w) + sum(depth * wd) (the depth's cotangent reaching the
+    projection's depth input, splax/_render.py:112-114) held as above."""
+    sc, vms, w, desc = draw_case(seed)
+    print(f"[case] sweep depth seed {seed}: {desc}", flush=True)
+    H, W = sc["img_shape"]
+    B = vms.shape[0]
+    wd = np.random.default_rng(seed).uniform(-1, 1, (B, H, W)).astype(np.float32)
+    p = {k: _t(sc[k], grad=True) for k in ("means", "scales", "quats", "colors", "opac")}
+    vm = _t(vms if B > 1 else vms[0], grad=True)
+    img, depth = splax_amd.render(*p.values(), viewmat=vm, background=_t(sc["bg"]),
+                                  img_shape=(H, W), f=sc["f"], c=sc["c"], render_depth=True)
+    wt, wdt = (w, wd) if B > 1 else (w[0], wd[0])
+    ((img * _t(wt)).sum() + (depth * _t(wdt)).sum()).backward()
+    torch.cuda.synchronize()
+    got_img, got_depth = img.detach().cpu().numpy(), depth.detach().cpu().numpy()
+    grads = {k: v.grad.detach().cpu().numpy() for k, v in p.items()}
+    grads["viewmat"] = vm.grad.detach().cpu().numpy()
+
+    (rimg, rdepth), rg, cond = TP.weighted_chain(sc, wt, vm=vms, wd=wdt)
+    _, tg, _ = TP.weighted_chain(sc, wt, vm=vms, truth=True, wd=wdt)
+    assert_bit_exact(got_img, rimg.reshape(got_img.shape), f"seed {seed}/img")
+    assert_bit_exact(got_depth, rdepth.reshape(got_depth.shape), f"seed {seed}/depth")
     _check_grads(grads, rg, tg, cond, seed)

@@ -214,14 +214,17 @@ def band_errors(got, ref, truth, cond):
     return rows
 
 
-def weighted_chain(sc, w, vm=None, truth=False, antialiased=False):
+def weighted_chain(sc, w, vm=None, truth=False, antialiased=False, wd=None):
     """The oracle's forward and chained backward of sum(img * w) for a random_scene-style
     dictionary (conftest.random_scene), float32 or the float64 truth; with B stacked viewmats
     (vm of shape (B, 4, 4), w of shape (B, H, W, 3)) the per-camera item gradients are summed.
     With antialiased, the blend takes the compensated opacities o * rho(conic) of the visible
     items and the tile intersection the raw ones, and the backward adds the compensation's VJP
-    (splax/_render.py:105-110, as oracle_chain does). Returns (image, grads keyed means / scales /
-    quats (wxyz) / colors / opac / viewmat, cond)."""
+    (splax/_render.py:105-110, as oracle_chain does). With wd (shaped like the image without its
+    channel axis) the objective adds sum(depth * wd) over the expected-depth channel, whose
+    cotangent reaches the projection's depth input (splax/_render.py:112-114). Returns (image,
+    grads keyed means / scales / quats (wxyz) / colors / opac / viewmat, cond), the image being
+    (image, depth image) with wd."""
     H, W = sc["img_shape"]
     n = len(sc["means"])
     vm = sc["vm"] if vm is None else vm
@@ -236,15 +239,22 @@ def weighted_chain(sc, w, vm=None, truth=False, antialiased=False):
     if antialiased:
         rho, _ = O.compensation_rho(conics)
         ob = (opac_b * np.where(vis, rho, np.float32(1))).astype(np.float32).reshape(-1, 1)
-    img, Ts, fidx, _, _ = O.rasterize_fwd(sc["colors"], ob, sc["opac"], sc["bg"], xys, depths,
-                                          radii, conics, cum, n=n, B=B, img_shape=(H, W))
+    fw = O.rasterize_fwd(sc["colors"], ob, sc["opac"], sc["bg"], xys, depths, radii, conics, cum,
+                         n=n, B=B, img_shape=(H, W), render_depth=wd is not None)
+    img, Ts, fidx = fw[0], fw[1], fw[2]
+    dkw = {} if wd is None else dict(v_out_depth=np.asarray(wd, np.float32).reshape(-1))
     args = (sc["colors"], ob, sc["opac"], sc["bg"], xys, depths, radii, conics, cum, Ts, fidx,
             np.asarray(w, np.float32).reshape(-1, 3))
-    kw = dict(n=n, B_out=B, B_geom=B, img_shape=(H, W))
+    kw = dict(n=n, B_out=B, B_geom=B, img_shape=(H, W), **dkw)
+    vdep = np.zeros(B * n, np.float64 if truth else np.float32)
     if truth:
-        vc, vo, vxy, vcon = O.rasterize_bwd_f64(*args, **kw)
+        out = O.rasterize_bwd_f64(*args, **kw)
+        vc, vo, vxy, vcon = out[:4]
     else:
-        vc, vo, vxy, vcon, _ = O.rasterize_bwd(*args, **kw)
+        out = O.rasterize_bwd(*args, **kw)
+        vc, vo, vxy, vcon = out[:4]
+    if wd is not None:
+        vdep = out[-1]
     if antialiased:
         if truth:
             v_op, v_c = truth64.compensation_vjp_f64(vo, opac_b, conics)
@@ -255,10 +265,11 @@ def weighted_chain(sc, w, vm=None, truth=False, antialiased=False):
     if truth:
         vm_, vs_, vq_, vv_ = truth64.project_bwd_f64(
             sc["means"], sc["scales"], q, vm.reshape(B, 4, 4), radii, conics, vxy,
-            np.zeros(B * n), vcon, n=n, B=B, f=sc["f"])
+            np.asarray(vdep, np.float64).reshape(-1), vcon, n=n, B=B, f=sc["f"])
     else:
         vm_, vs_, vq_, vv_, _ = O.project_bwd(sc["means"], sc["scales"], q, vm.reshape(-1, 4),
-                                              radii, conics, vxy, np.zeros(B * n, np.float32),
+                                              radii, conics, vxy,
+                                              np.asarray(vdep, np.float32).reshape(-1),
                                               np.asarray(vcon, np.float32), n=n, B=B,
                                               f=sc["f"])
     g = dict(means=_fold(vm_, B, n), scales=_fold(vs_, B, n),
@@ -267,7 +278,7 @@ def weighted_chain(sc, w, vm=None, truth=False, antialiased=False):
              viewmat=np.asarray(vv_, np.float64).reshape(B, 4, 4))
     ca, cb, cc = (conics[:, k].astype(np.float64) for k in range(3))
     cond = np.where(vis, (ca + cc) ** 2 / np.maximum(ca * cc - cb * cb, 1e-300), 0.0)
-    return img, g, cond.reshape(B, n).max(0)
+    return (img if wd is None else (img, fw[-1])), g, cond.reshape(B, n).max(0)
 
 
 # The bar's factor. The float32 oracle rounds each per-pixel term once and sums the terms in
