@@ -492,8 +492,7 @@ __device__ __forceinline__ int order_bucket(int32_t c) {
     return e < 3 ? c : e * 8 + ((c >> (e - 3)) & 7);
 }
 
-// Exclusive scan of the 256 bucket counts in s_cnt, in place (all threads call it).
-// Exclusive scan of the 256 bucket counts in place: waves 0-3 (threads 0-255, whole waves) scan
+// Exclusive scan of the 256 bucket counts in s_cnt, in place: waves 0-3 (threads 0-255) scan
 // by DPP, then add the totals of the waves before them. Every thread of the workgroup calls it.
 __device__ __forceinline__ void order_scan(uint32_t* s_cnt, uint32_t* s_tot, int tid) {
     const int lane = tid & 63, wave = tid >> 6;
