@@ -278,6 +278,19 @@ def weighted_chain(sc, w, vm=None, truth=False, antialiased=False, wd=None):
              viewmat=np.asarray(vv_, np.float64).reshape(B, 4, 4))
     ca, cb, cc = (conics[:, k].astype(np.float64) for k in range(3))
     cond = np.where(vis, (ca + cc) ** 2 / np.maximum(ca * cc - cb * cb, 1e-300), 0.0)
+    if antialiased:
+        # The compensation's own condition. rho2 = 1 - eps (a + c) + eps^2 (a c - b^2) cancels
+        # to nearly zero for a gaussian far below a pixel (the 0.3 px^2 dilation then dominates
+        # its covariance), keeping rho2 / (1 + eps (a + c) + eps^2 (|a c| + b^2)) of its terms'
+        # magnitude, and sqrt's VJP divides by rho: the conic's rounding reaches the gradients
+        # amplified by the inverse ratio. Where the float32 rho2 is <= 0 the reference's VJP is
+        # NaN (0.5 / sqrt(0) times clip's zero slope) and the condition infinite.
+        eps = 0.3
+        r2 = 1.0 - eps * (ca + cc) + eps * eps * (ca * cc - cb * cb)
+        mag = 1.0 + eps * (ca + cc) + eps * eps * (np.abs(ca * cc) + cb * cb)
+        _, r2f = O.compensation_rho(conics)
+        cond_rho = np.where(r2f > 0, mag / np.maximum(r2, 1e-300), np.inf)
+        cond = np.where(vis, np.maximum(cond, cond_rho), cond)
     return (img if wd is None else (img, fw[-1])), g, cond.reshape(B, n).max(0)
 
 
