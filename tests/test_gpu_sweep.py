@@ -14,7 +14,12 @@ random w. Each case holds:
 - the image bit for bit to the oracle's forward (batched cases to the batched oracle, whose key
   layout they share);
 - every gradient within north_star's 1e-4 (relative Frobenius) of the oracle's chain, and on
-  the items below condition 1e2 in every camera within 1e-5;
+  the items below condition 1e2 in every camera, when at least BAND_MIN of them, within 1e-5.
+  A set of a few items is left to the 1e-4 bar: a gradient summed over many pixels whose terms
+  cancel (random-sign weights, an L1 cotangent of one sign per pixel) keeps only float32's
+  precision of the terms' magnitude in either computation. Of 4000 further seeds, the three
+  that a 1e-5 bar on every such set failed had 1, 2 and 8 gaussians: the GPU 4.1e-5, 1.3e-6
+  and 1.8e-5 from the float64 truth, the oracle 2.5e-5, 4.1e-5 and 5.2e-7;
 - against the float64 truth of the same chain, per conic-condition band holding at least
   BAND_MIN items: the GPU's relative error at most timed_path.FACTOR times the float32 oracle's,
   or below 1e-5 (timed_path.assert_bands' bar). A band of a few items is left to the bars
@@ -121,7 +126,7 @@ def _check_grads(grads, rg, tg, cond, seed):
             continue
         c = cond[fin]
         well = c < 1e2
-        if well.any():
+        if well.sum() >= BAND_MIN:
             r = rel_fro(g[well], ref[well])
             assert r < 1e-5, f"{label} (cond < 1e2) vs the oracle: {r:.2e}"
         for (lo, hi), (cnt, eg, eo) in zip(TP.BANDS, TP.band_errors(g, ref, truth, c)):
