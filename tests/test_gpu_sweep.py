@@ -1,7 +1,7 @@
 """Seeded parity sweep: small random scenes through ``splax_amd.render`` against the oracle.
 
-Four groups: the plain render, render_loss (MSE and L1), the antialiased render and the
-render with the expected-depth channel.
+Five groups: the plain render, the same with the 64-bit intersection key forced, render_loss
+(MSE and L1), the antialiased render and the render with the expected-depth channel.
 
 Each case draws a scene in the style of the reference's random tests
 (tests/test_warp_rasterize.py:91-104, conftest.random_scene) with its sizes and shapes varied:
@@ -54,6 +54,7 @@ CASES = 24
 LOSS_CASES = 8
 AA_CASES = 8
 DEPTH_CASES = 8
+WIDE_CASES = 8
 BAND_MIN = 32
 
 
@@ -134,10 +135,9 @@ def _check_grads(grads, rg, tg, cond, seed):
                 assert eg <= max(TP.FACTOR * eo, 1e-5), (label, (lo, hi), cnt, eg, eo)
 
 
-@pytest.mark.parametrize("seed", range(CASES))
-def test_random_scene_matches_oracle(seed):
+def _plain_case(seed, tag=""):
     sc, vms, w, desc = draw_case(seed)
-    print(f"[case] sweep seed {seed}: {desc}", flush=True)
+    print(f"[case] sweep{tag} seed {seed}: {desc}", flush=True)
     H, W = sc["img_shape"]
     B = vms.shape[0]
     p = {k: _t(sc[k], grad=True) for k in ("means", "scales", "quats", "colors", "opac")}
@@ -155,6 +155,32 @@ def test_random_scene_matches_oracle(seed):
     _, tg, _ = TP.weighted_chain(sc, wt, vm=vms, truth=True)
     assert_bit_exact(got_img, rimg.reshape(got_img.shape), f"seed {seed}/img")
     _check_grads(grads, rg, tg, cond, seed)
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_random_scene_matches_oracle(seed):
+    _plain_case(seed)
+
+
+@pytest.fixture
+def _wide_keys():
+    """The 64-bit intersection key forced in the library and the oracle (the reference's
+    fallback when fewer than 16 depth bits remain, splax/_rasterize/_sort/_sort.py:23-26)."""
+    from oracle import oracle as O
+    from splax_amd import _lib
+
+    _lib.set_wide_keys(True)
+    O.set_wide_keys(True)
+    yield
+    _lib.set_wide_keys(False)
+    O.set_wide_keys(False)
+
+
+@pytest.mark.parametrize("seed", range(500, 500 + WIDE_CASES))
+def test_random_scene_wide_keys_matches_oracle(_wide_keys, seed):
+    """The plain render's checks with the 64-bit key: the 32 depth bits' four 8-bit passes,
+    one or two more for these scenes' image and tile bits, and the 64-bit bin edges."""
+    _plain_case(seed, " wide keys")
 
 
 @pytest.mark.parametrize("seed", range(100, 100 + LOSS_CASES))
